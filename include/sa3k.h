@@ -1,0 +1,148 @@
+/* sa3k — C ABI of the MI355X (gfx950) kernels behind sa3.cpp's DiT LoRA/DoRA training update.
+ *
+ * The reference runs this path as ggml graphs (src/train_ckpt.h:143-474 builds them,
+ * src/train_loop.h:309-441 executes them, src/train_loop.h:147-211 + src/train_optimizer.h:42-66
+ * apply the clip and AdamW on the host). There is no training entry in the reference's own C ABI
+ * (src/libsa3.h:163-191 is inference only), so this header is a new thin layer that follows
+ * libsa3's conventions:
+ *
+ *   Lifecycle:  sa3k_create() -> sa3k_* calls -> sa3k_destroy().
+ *   Ownership:  device buffers come from sa3k_malloc() and are released with sa3k_free(); opaque
+ *               objects (weights, linears) have their own *_destroy().
+ *   Threading:  a context owns one HIP device and one stream. It is NOT reentrant: serialise calls
+ *               per context (libsa3 contract, src/libsa3.h:8).
+ *   Ordering:   every compute call is enqueued on the context stream and returns before the GPU is
+ *               done, except calls that hand a host scalar back (documented per call), which
+ *               synchronise the stream.
+ *   Errors:     no C++ exception crosses this boundary. Every call returns SA3K_OK (0) or a non-zero
+ *               code; sa3k_last_error() returns the message of the last failure on that context
+ *               (libsa3 copies messages into `err`, src/libsa3.cpp:25-27; sa3k_create() does the same
+ *               since there is no context yet).
+ *
+ * Layout conventions (PyTorch order; ggml `ne` is the reverse):
+ *   weight W   [out][in]  row-major (ggml ne=[in,out], src/train_lora.h:149-151)
+ *   activation X [N][in] token-major (ggml ne=[in,N])
+ *   lora_A     [rank][in] row-major (src/train_lora.h:26)
+ *   lora_B     [out][rank] row-major (src/train_lora.h:27)
+ *   magnitude  [out]     (dora-rows, src/train_lora.h:31)
+ */
+#ifndef SA3K_H
+#define SA3K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA3K_API __attribute__((visibility("default")))
+
+enum {
+    SA3K_OK = 0,
+    SA3K_ERR_INVALID = 1,     /* bad argument (shape, null pointer, size mismatch, step <= 0 ...) */
+    SA3K_ERR_DEVICE = 2,      /* HIP runtime failure */
+    SA3K_ERR_NOMEM = 3,       /* device allocation failed */
+    SA3K_ERR_UNSUPPORTED = 4  /* shape/type combination the kernels do not implement */
+};
+
+/* Element / block types of a frozen base weight (the GGUF tensor types the path reads). */
+enum {
+    SA3K_TYPE_F32 = 0,
+    SA3K_TYPE_F16 = 1,
+    SA3K_TYPE_Q8_0 = 8,   /* 32-element blocks {f16 d; int8 qs[32]} = 34 bytes, ggml block_q8_0 */
+    SA3K_TYPE_BF16 = 30
+};
+
+/* Arithmetic of the contractions. */
+enum {
+    SA3K_PREC_F32 = 0,    /* fp32 MFMA, fp32 operands (1e-4 gradient tolerance) */
+    SA3K_PREC_BF16 = 1    /* bf16 MFMA operands, fp32 accumulation */
+};
+
+typedef struct sa3k_ctx sa3k_ctx;
+
+/* ---------------------------------------------------------------- context / memory */
+
+/* Create a context on HIP device `device` with its own stream. Returns NULL on failure and copies
+ * the message into err (err_len bytes, NUL-terminated), like sa3_init (src/libsa3.h:163). */
+SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len);
+SA3K_API void sa3k_destroy(sa3k_ctx* ctx);
+SA3K_API const char* sa3k_last_error(const sa3k_ctx* ctx);
+SA3K_API const char* sa3k_version(void);
+
+SA3K_API int sa3k_malloc(sa3k_ctx* ctx, size_t bytes, void** out);
+SA3K_API int sa3k_free(sa3k_ctx* ctx, void* ptr);
+/* Stream-ordered copies; host memory may be pageable. Both return once the copy is enqueued
+ * (upload) or complete (download: synchronises the stream). */
+SA3K_API int sa3k_upload(sa3k_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+SA3K_API int sa3k_download(sa3k_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+SA3K_API int sa3k_copy_d2d(sa3k_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes);
+SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst_dev, int value, size_t bytes);
+SA3K_API int sa3k_sync(sa3k_ctx* ctx);
+
+/* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a
+ * second one, synchronises and returns the elapsed milliseconds between them. */
+SA3K_API int sa3k_timer_start(sa3k_ctx* ctx);
+SA3K_API int sa3k_timer_stop(sa3k_ctx* ctx, float* ms);
+
+/* Per-kernel timing with HIP events on the context stream (off by default; the reference's
+ * SA3_TRAIN_PROFILE wall-clock phases, src/train_loop.h:314-437, have no per-kernel counterpart).
+ * While enabled every kernel launch is bracketed by an event pair; sa3k_profile_report writes one
+ * line per kernel name, "name launches total_ms\n", into buf (synchronises the stream). */
+SA3K_API int sa3k_profile_enable(sa3k_ctx* ctx, int on);
+SA3K_API int sa3k_profile_reset(sa3k_ctx* ctx);
+SA3K_API int sa3k_profile_report(sa3k_ctx* ctx, char* buf, int buf_len);
+
+/* ---------------------------------------------------------------- K6: AdamW + global clip */
+
+/* Mirrors TrainAdamWParams (src/train_optimizer.h:28-35). */
+typedef struct {
+    float learning_rate;
+    float beta1;
+    float beta2;
+    float eps;
+    float weight_decay;
+    float grad_clip;      /* global L2 clip; <= 0 disables (reference default 1.0 in training) */
+} sa3k_adamw_params;
+
+/* One fused update of a flat arena of n f32 adapter parameters (every A, B and magnitude of every
+ * target laid end to end). Replaces, on device, the host pair
+ *   train_average_and_clip   (src/train_loop.h:147-171)  and
+ *   adamw_update_vector      (src/train_optimizer.h:42-66) over every tensor
+ * as called by train_apply_accumulated_adamw (src/train_loop.h:173-211):
+ *   g := g * (1/count)                 if count > 1            (float)
+ *   norm := sqrt(sum (double)g^2)      over the whole arena    (double)
+ *   g := g * (float)(clip/(norm+1e-6)) if clip > 0 && norm > clip
+ *   m := b1*m + (1-b1)*g ; v := b2*v + (1-b2)*g*g
+ *   p := p - lr*((m/b1c)/(sqrt(v/b2c)+eps) + wd*p), b1c = 1-powf(b1,step), b2c = 1-powf(b2,step)
+ * evaluated with the same float operation order (no contraction), so param/m/v are bit-identical
+ * to the reference whenever the float clip scale is (the double sum is reduced in a different
+ * order; see sa3k_adamw_clip_scale). `grad` is not modified. step must be >= 1 (the reference
+ * rejects step <= 0, src/train_optimizer.h:49-52) and count >= 1 (src/train_loop.h:176-179).
+ * grad_norm_out (nullable) receives the pre-clip global norm; passing it synchronises the stream. */
+SA3K_API int sa3k_adamw_clip(sa3k_ctx* ctx, float* param, const float* grad, float* m, float* v,
+                             int64_t n, const sa3k_adamw_params* hp, int step, int count,
+                             double* grad_norm_out);
+
+/* The float clip scale and pre-clip norm the last sa3k_adamw_clip on this context used
+ * (scale = 1 when no clipping happened). Synchronises the stream. */
+SA3K_API int sa3k_adamw_clip_scale(sa3k_ctx* ctx, double* norm_out, float* scale_out);
+
+/* ---------------------------------------------------------------- a5: Q8_0 weight blocks */
+
+/* Decode n_elems (multiple of 32) Q8_0 elements from raw GGUF blocks (34 bytes each, 2-byte
+ * aligned) into f32: y = f32(d) * qs[i] — exact, so bit-identical to ggml's dequantize_row_q8_0
+ * (called at tools/sa3-quant-check.cpp:43, used by mul_mat over a Q8_0 base in src/lora.h:239-251). */
+SA3K_API int sa3k_q8_0_dequant(sa3k_ctx* ctx, const void* blocks, float* out, int64_t n_elems);
+
+/* Encode n_elems (multiple of 32) f32 values into Q8_0 blocks with ggml's reference quantizer
+ * (per block: d = amax/127, q = roundf(x * (1/d)), d stored as f16), the re-encode the reference's
+ * quantizer tool applies to 2D weights (tools/sa3-quantize.cpp:43-56, 79-85). */
+SA3K_API int sa3k_q8_0_quantize(sa3k_ctx* ctx, const float* x, void* blocks, int64_t n_elems);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA3K_H */

@@ -1,0 +1,80 @@
+/* oracle — CPU restatement of sa3.cpp's DiT LoRA/DoRA training-update math.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load this library, and only as the checker (or the timed CPU baseline), never as part of
+ * the product path. The product (sa3.cpp_amd/libsa3k.so) never links or calls it.
+ *
+ * Each function names the reference file:line it restates. The reference's own implementation
+ * (header-only C++ over the un-vendored ggml fork betweentwomidnights/ggml tag
+ * sa3-training-v1-metal, commit 922875a6) cannot be compiled here, so this is a from-scratch
+ * restatement: float loops where the reference is a host float loop (optimizer, clip, quantizer),
+ * double accumulation where the reference is a ggml graph (dit_lin, attention, block), so that the
+ * oracle is closer to the exact value than any single-precision implementation.
+ *
+ * Pinning (how each part is checked beyond restating it) is listed per function in the test
+ * files; parts without an independent check say "parity unpinned".
+ */
+#ifndef SA3_ORACLE_H
+#define SA3_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- optimizer (src/train_optimizer.h, src/train_loop.h) ---- */
+float orc_inverse_lr(float base_lr, int step0, float inv_gamma, float power, float warmup, float final_lr);
+/* adamw_update_vector on one tensor; returns 0 ok, 1 size/step error (src/train_optimizer.h:42-66) */
+int orc_adamw_update_vector(float* param, const float* grad, float* m, float* v, int64_t n,
+                            float lr, float b1, float b2, float eps, float wd, int step);
+/* train_average_and_clip over tensors laid end to end in the order the reference visits them
+ * (A, B, mxs, mag, mag_r, mag_c per target): grad is modified in place like accum is.
+ * (src/train_loop.h:147-171) */
+void orc_average_and_clip(float* grad, int64_t n, int count, float grad_clip, double* norm_out,
+                          float* scale_out);
+/* train_apply_accumulated_adamw on a flat arena (src/train_loop.h:173-211). grad is modified
+ * (averaged/clipped) like the reference modifies its accumulator. */
+int orc_apply_accumulated_adamw(float* param, float* grad, float* m, float* v, int64_t n,
+                                float lr, float b1, float b2, float eps, float wd, float clip,
+                                int step, int count, double* norm_out, float* scale_out);
+
+/* ---- Q8_0 / f16 (ggml block_q8_0, quantize_row_q8_0_ref, dequantize_row_q8_0) ---- */
+uint16_t orc_f32_to_f16(float x);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_f16_row(const float* x, uint16_t* y, int64_t n);
+void orc_f16_to_f32_row(const uint16_t* x, float* y, int64_t n);
+void orc_q8_0_quantize(const float* x, void* blocks, int64_t n);
+void orc_q8_0_dequant(const void* blocks, float* y, int64_t n);
+
+/* ---- adapter state (src/train_lora.h) ---- */
+/* W [out][in] f32 (an f16 or Q8_0 base is decoded first). */
+void orc_row_norm_sq(const float* W, int64_t in, int64_t out, float eps, float* nsq);  /* :160-174 */
+void orc_row_norms(const float* W, int64_t in, int64_t out, float* norms);               /* :141-155 */
+/* materialised effective weight (train_lora_effective_weight, :301-329) for lora / dora-rows */
+void orc_effective_weight(const float* W, int64_t in, int64_t out, const float* A, const float* B,
+                          const float* mag, int rank, float alpha, int dora, float* Weff);
+
+/* ---- dit_lin (src/dit.h:92-149) forward and closed-form backward, double accumulation ----
+ * X [N][in], W [out][in], A [r][in], B [out][r], mag/bnsq [out], bias [out] or NULL, s = alpha/r.
+ * fwd writes Y [N][out] and (nullable) U [N][out] (pre-row-scale) and dscale [out] (m/sqrt(nsq),
+ * or 1 for lora) and nsq [out]. */
+void orc_dit_lin_fwd(const float* X, int64_t N, const float* W, int64_t in, int64_t out,
+                     const float* A, const float* B, int rank, float s, int dora, const float* mag,
+                     const float* bnsq, const float* bias, float* Y, float* U, float* dscale,
+                     float* nsq_out);
+/* bwd from dY [N][out]: dX [N][in], dA [r][in], dB [out][r], dm [out] (dora; nullable otherwise).
+ * Any output pointer may be NULL to skip it. */
+void orc_dit_lin_bwd(const float* X, int64_t N, const float* W, int64_t in, int64_t out,
+                     const float* A, const float* B, int rank, float s, int dora, const float* mag,
+                     const float* bnsq, const float* dY, float* dX, float* dA, float* dB, float* dm);
+/* plain double-accumulated products used by tests: C[M][N] = A[M][K] * B[N][K]^T */
+void orc_gemm_nt(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
+
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

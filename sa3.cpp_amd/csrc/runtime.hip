@@ -1,0 +1,204 @@
+// Context, device memory and stream timing for the sa3k C ABI.
+#include "sa3k_internal.h"
+
+#include <cstring>
+
+namespace {
+constexpr int kAdamwMaxBlocks = 2048;
+
+void copy_err(char* err, int n, const std::string& m) {
+    if (err && n > 0) {
+        std::strncpy(err, m.c_str(), (size_t)n - 1);
+        err[n - 1] = '\0';
+    }
+}
+}  // namespace
+
+hipEvent_t prof_event(sa3k_ctx* ctx) {
+    if (!ctx->prof_pool.empty()) {
+        hipEvent_t e = ctx->prof_pool.back();
+        ctx->prof_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    SA3K_HIP(hipEventCreate(&e));
+    return e;
+}
+
+void prof_collect(sa3k_ctx* ctx) {
+    if (ctx->prof_pending.empty()) return;
+    SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    for (const ProfRecord& r : ctx->prof_pending) {
+        float ms = 0.0f;
+        SA3K_HIP(hipEventElapsedTime(&ms, r.start, r.stop));
+        ProfTotal& t = ctx->prof_totals[r.name];
+        t.count += 1;
+        t.ms += ms;
+        ctx->prof_pool.push_back(r.start);
+        ctx->prof_pool.push_back(r.stop);
+    }
+    ctx->prof_pending.clear();
+}
+
+extern "C" {
+
+SA3K_API const char* sa3k_version(void) { return "sa3k 0.1 gfx950"; }
+
+SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
+    sa3k_ctx* ctx = new (std::nothrow) sa3k_ctx();
+    if (!ctx) {
+        copy_err(err, err_len, "sa3k_create: out of host memory");
+        return nullptr;
+    }
+    int rc = sa3k_guard(ctx, "sa3k_create", [&] {
+        int n = 0;
+        SA3K_HIP(hipGetDeviceCount(&n));
+        SA3K_REQUIRE(device >= 0 && device < n, "device ordinal out of range");
+        ctx->device = device;
+        SA3K_HIP(hipSetDevice(device));
+        hipDeviceProp_t prop;
+        SA3K_HIP(hipGetDeviceProperties(&prop, device));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            sa3k_throw(SA3K_ERR_UNSUPPORTED,
+                       std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+        // Default-priority stream (non-blocking w.r.t. the null stream).
+        SA3K_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        SA3K_HIP(hipEventCreate(&ctx->ev_start));
+        SA3K_HIP(hipEventCreate(&ctx->ev_stop));
+        SA3K_HIP(hipMalloc(&ctx->adamw_partials, sizeof(double) * kAdamwMaxBlocks));
+        SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
+        SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    });
+    if (rc != SA3K_OK) {
+        copy_err(err, err_len, ctx->last_error);
+        sa3k_destroy(ctx);
+        return nullptr;
+    }
+    return ctx;
+}
+
+SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->adamw_partials) (void)hipFree(ctx->adamw_partials);
+    if (ctx->adamw_result) (void)hipFree(ctx->adamw_result);
+    for (const ProfRecord& r : ctx->prof_pending) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    for (hipEvent_t e : ctx->prof_pool) (void)hipEventDestroy(e);
+    if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+SA3K_API const char* sa3k_last_error(const sa3k_ctx* ctx) {
+    return ctx ? ctx->last_error.c_str() : "null context";
+}
+
+SA3K_API int sa3k_malloc(sa3k_ctx* ctx, size_t bytes, void** out) {
+    return sa3k_guard(ctx, "sa3k_malloc", [&] {
+        SA3K_REQUIRE(out != nullptr, "out is null");
+        *out = nullptr;
+        SA3K_HIP(hipSetDevice(ctx->device));
+        SA3K_HIP(hipMalloc(out, bytes ? bytes : 1));
+    });
+}
+
+SA3K_API int sa3k_free(sa3k_ctx* ctx, void* ptr) {
+    return sa3k_guard(ctx, "sa3k_free", [&] {
+        if (!ptr) return;
+        SA3K_HIP(hipSetDevice(ctx->device));
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        SA3K_HIP(hipFree(ptr));
+    });
+}
+
+SA3K_API int sa3k_upload(sa3k_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return sa3k_guard(ctx, "sa3k_upload", [&] {
+        if (!bytes) return;
+        SA3K_REQUIRE(dst && src, "null pointer");
+        SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+        // pageable source: the runtime stages it, but keep the contract simple for callers that
+        // reuse the host buffer right away
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+SA3K_API int sa3k_download(sa3k_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return sa3k_guard(ctx, "sa3k_download", [&] {
+        if (!bytes) return;
+        SA3K_REQUIRE(dst && src, "null pointer");
+        SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+SA3K_API int sa3k_copy_d2d(sa3k_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return sa3k_guard(ctx, "sa3k_copy_d2d", [&] {
+        if (!bytes) return;
+        SA3K_REQUIRE(dst && src, "null pointer");
+        SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    });
+}
+
+SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
+    return sa3k_guard(ctx, "sa3k_memset", [&] {
+        if (!bytes) return;
+        SA3K_REQUIRE(dst, "null pointer");
+        SA3K_HIP(hipMemsetAsync(dst, value, bytes, ctx->stream));
+    });
+}
+
+SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
+    return sa3k_guard(ctx, "sa3k_sync", [&] { SA3K_HIP(hipStreamSynchronize(ctx->stream)); });
+}
+
+SA3K_API int sa3k_timer_start(sa3k_ctx* ctx) {
+    return sa3k_guard(ctx, "sa3k_timer_start",
+                      [&] { SA3K_HIP(hipEventRecord(ctx->ev_start, ctx->stream)); });
+}
+
+SA3K_API int sa3k_timer_stop(sa3k_ctx* ctx, float* ms) {
+    return sa3k_guard(ctx, "sa3k_timer_stop", [&] {
+        SA3K_REQUIRE(ms != nullptr, "ms is null");
+        SA3K_HIP(hipEventRecord(ctx->ev_stop, ctx->stream));
+        SA3K_HIP(hipEventSynchronize(ctx->ev_stop));
+        SA3K_HIP(hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+    });
+}
+
+SA3K_API int sa3k_profile_enable(sa3k_ctx* ctx, int on) {
+    return sa3k_guard(ctx, "sa3k_profile_enable", [&] {
+        prof_collect(ctx);
+        ctx->prof_on = on != 0;
+    });
+}
+
+SA3K_API int sa3k_profile_reset(sa3k_ctx* ctx) {
+    return sa3k_guard(ctx, "sa3k_profile_reset", [&] {
+        prof_collect(ctx);
+        ctx->prof_totals.clear();
+    });
+}
+
+SA3K_API int sa3k_profile_report(sa3k_ctx* ctx, char* buf, int buf_len) {
+    return sa3k_guard(ctx, "sa3k_profile_report", [&] {
+        SA3K_REQUIRE(buf && buf_len > 0, "null buffer");
+        prof_collect(ctx);
+        std::string out;
+        char line[256];
+        for (const auto& kv : ctx->prof_totals) {
+            std::snprintf(line, sizeof line, "%s %lld %.6f\n", kv.first.c_str(),
+                          (long long)kv.second.count, kv.second.ms);
+            out += line;
+        }
+        SA3K_REQUIRE((int)out.size() < buf_len, "report buffer too small");
+        std::memcpy(buf, out.c_str(), out.size() + 1);
+    });
+}
+
+}  // extern "C"

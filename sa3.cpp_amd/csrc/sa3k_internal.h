@@ -1,0 +1,109 @@
+// Internal helpers shared by the sa3k translation units: the context object, error plumbing and
+// small device utilities. Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "sa3k.h"
+
+// Per-kernel event timing (off by default): every launch site wraps its launch in a KernelScope,
+// which records a start/stop event pair on the context stream while profiling is on.
+struct ProfRecord {
+    const char* name;
+    hipEvent_t start, stop;
+};
+struct ProfTotal {
+    int64_t count = 0;
+    double ms = 0.0;
+};
+
+struct sa3k_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string last_error;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    bool prof_on = false;
+    std::vector<ProfRecord> prof_pending;
+    std::vector<hipEvent_t> prof_pool;
+    std::map<std::string, ProfTotal> prof_totals;
+    // AdamW: per-block partial sums of squares and the {norm, scale} pair of the last update.
+    double* adamw_partials = nullptr;     // [kAdamwMaxBlocks]
+    double* adamw_result = nullptr;       // [0] = norm, [1] = scale (as double)
+};
+
+// An error that carries an sa3k status code across the internal call chain; every C entry point
+// converts it into a return code + ctx->last_error.
+struct Sa3kError : std::runtime_error {
+    int code;
+    Sa3kError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+inline void sa3k_throw(int code, const std::string& msg) { throw Sa3kError(code, msg); }
+
+#define SA3K_HIP(call)                                                                            \
+    do {                                                                                          \
+        hipError_t e_ = (call);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            sa3k_throw(e_ == hipErrorOutOfMemory ? SA3K_ERR_NOMEM : SA3K_ERR_DEVICE,              \
+                       std::string(#call) + ": " + hipGetErrorString(e_));                        \
+    } while (0)
+
+#define SA3K_REQUIRE(cond, msg)                                                                   \
+    do {                                                                                          \
+        if (!(cond)) sa3k_throw(SA3K_ERR_INVALID, (msg));                                         \
+    } while (0)
+
+// Wrap an entry point body: returns SA3K_OK or the code of the first failure, recording the message.
+template <class F>
+inline int sa3k_guard(sa3k_ctx* ctx, const char* fn, F&& body) {
+    if (!ctx) return SA3K_ERR_INVALID;
+    try {
+        body();
+        return SA3K_OK;
+    } catch (const Sa3kError& e) {
+        ctx->last_error = std::string(fn) + ": " + e.what();
+        return e.code;
+    } catch (const std::exception& e) {
+        ctx->last_error = std::string(fn) + ": " + e.what();
+        return SA3K_ERR_DEVICE;
+    } catch (...) {
+        ctx->last_error = std::string(fn) + ": unknown failure";
+        return SA3K_ERR_DEVICE;
+    }
+}
+
+// Launch-error check after a kernel launch on the context stream.
+#define SA3K_LAUNCHED() SA3K_HIP(hipGetLastError())
+
+hipEvent_t prof_event(sa3k_ctx* ctx);
+void prof_collect(sa3k_ctx* ctx);
+
+class KernelScope {
+public:
+    KernelScope(sa3k_ctx* ctx, const char* name) : ctx_(ctx) {
+        if (!ctx_->prof_on) return;
+        rec_.name = name;
+        rec_.start = prof_event(ctx_);
+        rec_.stop = prof_event(ctx_);
+        (void)hipEventRecord(rec_.start, ctx_->stream);
+    }
+    ~KernelScope() {
+        if (!ctx_->prof_on) return;
+        (void)hipEventRecord(rec_.stop, ctx_->stream);
+        ctx_->prof_pending.push_back(rec_);
+        if (ctx_->prof_pending.size() >= 4096) prof_collect(ctx_);
+    }
+private:
+    sa3k_ctx* ctx_;
+    ProfRecord rec_{};
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1,0 +1,218 @@
+"""Python binding of the sa3k C ABI (include/sa3k.h) over ctypes.
+
+This is plumbing for the test and benchmark harnesses: it loads the in-tree libsa3k.so (built by
+sa3.cpp_amd/build.py), owns device buffers and converts numpy arrays. It never falls back to
+another implementation: when the library or a GPU is missing it raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsa3k.so")
+
+SA3K_OK = 0
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
+PREC_F32, PREC_BF16 = 0, 1
+
+_lib = None
+
+
+class Sa3kError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"sa3k error {code}: {msg}")
+        self.code = code
+
+
+class AdamWParams(C.Structure):
+    _fields_ = [("learning_rate", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("eps", C.c_float), ("weight_decay", C.c_float), ("grad_clip", C.c_float)]
+
+
+def _declare(lib):
+    P, I64, I, F, D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
+    sig = {
+        "sa3k_create": (P, [I, C.c_char_p, I]),
+        "sa3k_destroy": (None, [P]),
+        "sa3k_last_error": (C.c_char_p, [P]),
+        "sa3k_version": (C.c_char_p, []),
+        "sa3k_malloc": (I, [P, C.c_size_t, C.POINTER(P)]),
+        "sa3k_free": (I, [P, P]),
+        "sa3k_upload": (I, [P, P, P, C.c_size_t]),
+        "sa3k_download": (I, [P, P, P, C.c_size_t]),
+        "sa3k_copy_d2d": (I, [P, P, P, C.c_size_t]),
+        "sa3k_memset": (I, [P, P, I, C.c_size_t]),
+        "sa3k_sync": (I, [P]),
+        "sa3k_timer_start": (I, [P]),
+        "sa3k_timer_stop": (I, [P, C.POINTER(F)]),
+        "sa3k_profile_enable": (I, [P, I]),
+        "sa3k_profile_reset": (I, [P]),
+        "sa3k_profile_report": (I, [P, C.c_char_p, I]),
+        "sa3k_adamw_clip": (I, [P, P, P, P, P, I64, C.POINTER(AdamWParams), I, I, C.POINTER(D)]),
+        "sa3k_adamw_clip_scale": (I, [P, C.POINTER(D), C.POINTER(F)]),
+        "sa3k_q8_0_dequant": (I, [P, P, P, I64]),
+        "sa3k_q8_0_quantize": (I, [P, P, P, I64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return sig
+
+
+def load_library(path=None):
+    """Load libsa3k.so (cached). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: run python sa3.cpp_amd/build.py first")
+    lib = C.CDLL(path)
+    _declare(lib)
+    _lib = lib
+    return lib
+
+
+def declared_symbols(header=None):
+    """Every sa3k_* function name declared in include/sa3k.h."""
+    import re
+    header = header or os.path.join(os.path.dirname(HERE), "include", "sa3k.h")
+    text = open(header).read()
+    return sorted(set(re.findall(r"SA3K_API\s+[^;(]*?\b(sa3k_\w+)\s*\(", text)))
+
+
+class DeviceArray:
+    """A device allocation with a numpy shape/dtype, owned by a Context."""
+
+    def __init__(self, ctx, ptr, shape, dtype, owner=True):
+        self.ctx, self.ptr = ctx, ptr
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+        self.owner = owner
+
+    @property
+    def nbytes(self):
+        return int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+
+    @property
+    def size(self):
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        self.ctx.check(self.ctx.lib.sa3k_download(self.ctx.h, out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def view(self, offset_elems, shape, dtype=None):
+        dtype = np.dtype(dtype or self.dtype)
+        return DeviceArray(self.ctx, self.ptr + offset_elems * self.dtype.itemsize, shape, dtype, owner=False)
+
+    def free(self):
+        if self.owner and self.ptr:
+            self.ctx.lib.sa3k_free(self.ctx.h, self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.owner and self.ptr and self.ctx.h:
+                self.ctx.lib.sa3k_free(self.ctx.h, self.ptr)
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device=0, lib_path=None):
+        self.lib = load_library(lib_path)
+        err = C.create_string_buffer(512)
+        self.h = self.lib.sa3k_create(device, err, 512)
+        if not self.h:
+            raise Sa3kError(-1, err.value.decode(errors="replace"))
+
+    def check(self, rc):
+        if rc != SA3K_OK:
+            raise Sa3kError(rc, self.lib.sa3k_last_error(self.h).decode(errors="replace"))
+
+    def close(self):
+        if self.h:
+            self.lib.sa3k_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- memory
+    def empty(self, shape, dtype=np.float32):
+        shape = (shape,) if np.isscalar(shape) else tuple(shape)
+        nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize
+        p = C.c_void_p()
+        self.check(self.lib.sa3k_malloc(self.h, nbytes, C.byref(p)))
+        return DeviceArray(self, p.value, shape, dtype)
+
+    def zeros(self, shape, dtype=np.float32):
+        a = self.empty(shape, dtype)
+        self.check(self.lib.sa3k_memset(self.h, a.ptr, 0, a.nbytes))
+        return a
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        a = self.empty(arr.shape, arr.dtype)
+        self.check(self.lib.sa3k_upload(self.h, a.ptr, arr.ctypes.data, arr.nbytes))
+        return a
+
+    def copy_into(self, dst, arr):
+        arr = np.ascontiguousarray(arr, dtype=dst.dtype)
+        assert arr.nbytes == dst.nbytes
+        self.check(self.lib.sa3k_upload(self.h, dst.ptr, arr.ctypes.data, arr.nbytes))
+
+    def sync(self):
+        self.check(self.lib.sa3k_sync(self.h))
+
+    def timer_start(self):
+        self.check(self.lib.sa3k_timer_start(self.h))
+
+    def timer_stop(self):
+        ms = C.c_float()
+        self.check(self.lib.sa3k_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
+    # -- per-kernel event timing
+    def profile(self, on=True):
+        self.check(self.lib.sa3k_profile_enable(self.h, 1 if on else 0))
+
+    def profile_reset(self):
+        self.check(self.lib.sa3k_profile_reset(self.h))
+
+    def profile_report(self):
+        """{kernel name: (launches, total_ms)}"""
+        buf = C.create_string_buffer(1 << 16)
+        self.check(self.lib.sa3k_profile_report(self.h, buf, 1 << 16))
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, cnt, ms = line.rsplit(" ", 2)
+            out[name] = (int(cnt), float(ms))
+        return out
+
+    # -- K6
+    def adamw_clip(self, p, g, m, v, hp, step, count=1, want_norm=False):
+        hpv = AdamWParams(*hp) if not isinstance(hp, AdamWParams) else hp
+        norm = C.c_double()
+        self.check(self.lib.sa3k_adamw_clip(self.h, p.ptr, g.ptr, m.ptr, v.ptr, p.size, C.byref(hpv),
+                                            int(step), int(count), C.byref(norm) if want_norm else None))
+        return norm.value if want_norm else None
+
+    def adamw_clip_scale(self):
+        n, s = C.c_double(), C.c_float()
+        self.check(self.lib.sa3k_adamw_clip_scale(self.h, C.byref(n), C.byref(s)))
+        return n.value, s.value
+
+    # -- Q8_0
+    def q8_0_dequant(self, blocks, out, n):
+        self.check(self.lib.sa3k_q8_0_dequant(self.h, blocks.ptr, out.ptr, int(n)))
+
+    def q8_0_quantize(self, x, blocks, n):
+        self.check(self.lib.sa3k_q8_0_quantize(self.h, x.ptr, blocks.ptr, int(n)))

@@ -1,0 +1,61 @@
+import importlib.util
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "sa3.cpp_amd")
+
+
+def _load(name, path):
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+sa3k = _load("sa3k", os.path.join(PKG, "sa3k.py"))
+oracle = _load("sa3_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built libsa3k.so")
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    c = sa3k.Context(0)
+    yield c
+    c.close()
+
+
+def rng(seed):
+    """Counter-based generator shared by tests and the bench (Philox4x32-10, numpy)."""
+    return np.random.Generator(np.random.Philox(seed))
+
+
+def rel_err(a, b):
+    """normwise relative error ||a-b|| / ||b||"""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    nb = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (nb if nb > 0 else 1.0))
+
+
+def max_rel_err(a, b, floor_frac=1e-3):
+    """max_i |a_i-b_i| / (|b_i| + floor), floor = floor_frac * max|b| (elementwise, guarded near 0)"""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    floor = floor_frac * float(np.max(np.abs(b))) if b.size else 0.0
+    return float(np.max(np.abs(a - b) / (np.abs(b) + floor + 1e-300))) if b.size else 0.0
+
+
+def cosine(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
