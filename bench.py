@@ -96,8 +96,129 @@ class AdamWWorkload:
                 "kind": "port", "sample": f"{len(times)} updates of an {n}-param slice of the arena, scaled to 48M"}
 
 
-WORKLOADS = {"adamw": AdamWWorkload}
-DEFAULT = "adamw"
+class LinearWorkload:
+    """One full adapter update of a single functional LoRA/DoRA linear (dit_lin, src/dit.h:92-149):
+    prepare (DoRA norms) + forward + backward + fused clip/AdamW over its adapter arena [A | B | m].
+
+    dora_q8: DoRA rank 32 (alpha 32), 1536 -> 6144, Q8_0 base quantised from N(0, 0.02),
+             X [2048 x 1536] ~ N(0,1), dY ~ N(0, 1e-2), bf16 MFMA.
+    lora_f32: LoRA rank 16 (alpha 16), 1536 -> 1536, f32 base N(0, 0.02), fp32 MFMA."""
+
+    def __init__(self, ctx, kind):
+        sa3k = sys.modules["sa3k"]
+        self.ctx, self.kind = ctx, kind
+        if kind == "dora_q8":
+            self.N, self.in_, self.out_, self.r, alpha = 2048, 1536, 6144, 32, 32.0
+            self.dora, self.prec, self.dtype = True, sa3k.PREC_BF16, "bf16"
+            self.name = "dora_linear_q8_0_2048x1536x6144_r32"
+            self.peak = BF16_PEAK_TFLOPS
+        else:
+            self.N, self.in_, self.out_, self.r, alpha = 2048, 1536, 1536, 16, 16.0
+            self.dora, self.prec, self.dtype = False, sa3k.PREC_F32, "f32"
+            self.name = "lora_linear_f32_2048x1536x1536_r16"
+            self.peak = FP32_MFMA_PEAK_TFLOPS
+        self.s = alpha / self.r
+        N, in_, out_, r = self.N, self.in_, self.out_, self.r
+        g = rng(1 if kind == "dora_q8" else 0)
+        self.X_host = g.normal(0, 1, (N, in_)).astype(np.float32)
+        self.dY_host = g.normal(0, 1e-2, (N, out_)).astype(np.float32)
+        self.W_host = g.normal(0, 0.02, (out_, in_)).astype(np.float32)
+        bound = 1.0 / np.sqrt(in_)
+        self.A_host = g.uniform(-bound, bound, (r, in_)).astype(np.float32)
+        self.B_host = g.normal(0, 0.01, (out_, r)).astype(np.float32)
+        if kind == "dora_q8":
+            wf = ctx.upload(self.W_host)
+            blocks = ctx.zeros(out_ * in_ // 32 * 34, np.uint8)
+            ctx.q8_0_quantize(wf, blocks, out_ * in_)
+            self.blocks_host = blocks.numpy()
+            self.w = ctx.weight((self.blocks_host, in_, out_), sa3k.TYPE_Q8_0)
+        else:
+            self.w = ctx.weight(self.W_host, sa3k.TYPE_F32)
+        self.lin = ctx.lin(self.w, r, self.prec, N)
+        # adapter arena [A | B | m] (the reference's visit order A, B, magnitude per target)
+        nA, nB, nm = r * in_, out_ * r, out_ if self.dora else 0
+        self.n = nA + nB + nm
+        self.p = ctx.zeros(self.n)
+        ctx.copy_into(self.p.view(0, (nA,)), self.A_host.ravel())
+        ctx.copy_into(self.p.view(nA, (nB,)), self.B_host.ravel())
+        self.A, self.B = self.p.view(0, (r, in_)), self.p.view(nA, (out_, r))
+        self.grad = ctx.zeros(self.n)
+        self.gA, self.gB = self.grad.view(0, (r, in_)), self.grad.view(nA, (out_, r))
+        self.m, self.v = ctx.zeros(self.n), ctx.zeros(self.n)
+        if self.dora:
+            self.bnsq = self.w.row_norm_sq(1e-12)
+            norms = self.w.row_norms()
+            ctx.check(ctx.lib.sa3k_copy_d2d(ctx.h, self.p.ptr + 4 * (nA + nB), norms.ptr, 4 * nm))
+            self.mag, self.gm = self.p.view(nA + nB, (nm,)), self.grad.view(nA + nB, (nm,))
+        else:
+            self.bnsq = self.mag = self.gm = None
+        self.X, self.dY = ctx.upload(self.X_host), ctx.upload(self.dY_host)
+        self.Y, self.dX = ctx.empty((N, out_)), ctx.empty((N, in_))
+        self.hp = (1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0)
+        self.k = 0
+
+    def step(self):
+        self.k += 1
+        c = self.ctx
+        self.lin.prepare(self.A, self.B, self.s, self.dora, self.mag, self.bnsq)
+        c.check(c.lib.sa3k_memset(c.h, self.grad.ptr, 0, self.grad.nbytes))
+        self.lin.forward(self.X, self.N, self.Y)
+        self.lin.backward(self.X, self.N, self.dY, self.dX, self.gA, self.gB, self.gm)
+        c.adamw_clip(self.p, self.grad, self.m, self.v, self.hp, self.k, 1)
+
+    def flops(self):
+        N, i, o, r = self.N, self.in_, self.out_, self.r
+        main = 2.0 * N * i * o
+        fwd = main + 2.0 * N * i * r + 2.0 * N * r * o + (2.0 * r * i * o if self.dora else 0.0)
+        bwd = main + 2.0 * N * o * r + 2.0 * N * r * i + 2.0 * N * o * r + 2.0 * N * r * i + \
+            (2.0 * r * i * o if self.dora else 0.0)
+        return fwd, bwd
+
+    def config(self):
+        return {"workload": self.name, "tokens": self.N, "in": self.in_, "out": self.out_, "rank": self.r,
+                "adapter": "dora-rows" if self.dora else "lora",
+                "base": "q8_0" if self.kind == "dora_q8" else "f32"}
+
+    def roofline(self, prof, steps):
+        # dominant kernel: the largest of the two base GEMMs (forward X W^T and backward dU W)
+        N, i, o = self.N, self.in_, self.out_
+        cands = {"lin_fwd_main": 2.0 * N * i * o + 2.0 * N * self.r * o,
+                 "lin_bwd_dx": 2.0 * N * i * o + 2.0 * N * self.r * i + (2.0 * self.r * i * o if self.dora else 0)}
+        k = max(cands, key=lambda n: prof.get(n, (1, 0.0))[1])
+        cnt, ms = prof[k]
+        avg = ms / cnt
+        ach = cands[k] / (avg * 1e-3) / 1e12
+        return {"kernel": k, "bound": "mfma", "achieved": round(ach, 1), "peak": self.peak, "unit": "TFLOP/s",
+                "frac": round(ach / self.peak, 4), "traffic": None, "avg_launch_ms": round(avg, 5),
+                "algorithmic_flops_per_launch": cands[k]}
+
+    def extra(self, ms_per_step):
+        fwd, bwd = self.flops()
+        return {"algorithmic_gflop_per_update": round((fwd + bwd) / 1e9, 2),
+                "tflops_whole_update": round((fwd + bwd) / (ms_per_step * 1e-3) / 1e12, 1)}
+
+    def cpu_baseline(self):
+        oracle = _load("sa3_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        Wd = oracle.q8_0_dequant(self.blocks_host, self.out_ * self.in_).reshape(self.out_, self.in_) \
+            if self.kind == "dora_q8" else self.W_host
+        mag = oracle.row_norms(Wd) if self.dora else None
+        bnsq = oracle.row_norm_sq(Wd) if self.dora else None
+        times = []
+        t_end = time.time() + 10.0
+        while time.time() < t_end or not times:
+            t0 = time.perf_counter()
+            oracle.dit_lin_fwd(self.X_host, Wd, self.A_host, self.B_host, self.s, self.dora, mag, bnsq)
+            oracle.dit_lin_bwd(self.X_host, Wd, self.dY_host, self.A_host, self.B_host, self.s, self.dora, mag, bnsq)
+            times.append(time.perf_counter() - t0)
+        return {"value": round(float(np.median(times)) * 1e3, 1), "unit": "ms/update (fwd+bwd, same shapes)",
+                "cores": oracle.lib().orc_num_threads(), "kind": "port",
+                "sample": f"{len(times)} full-size fwd+bwd of the oracle restatement (double accumulation, OpenMP)"}
+
+
+WORKLOADS = {"adamw": AdamWWorkload,
+             "dora_linear": lambda ctx: LinearWorkload(ctx, "dora_q8"),
+             "lora_linear": lambda ctx: LinearWorkload(ctx, "lora_f32")}
+DEFAULT = "dora_linear"
 
 
 def main():

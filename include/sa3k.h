@@ -141,6 +141,76 @@ SA3K_API int sa3k_q8_0_dequant(sa3k_ctx* ctx, const void* blocks, float* out, in
  * quantizer tool applies to 2D weights (tools/sa3-quantize.cpp:43-56, 79-85). */
 SA3K_API int sa3k_q8_0_quantize(sa3k_ctx* ctx, const float* x, void* blocks, int64_t n_elems);
 
+/* ---------------------------------------------------------------- K1/K2: the MFMA GEMM */
+
+/* C[M][N] = alpha * A[M][K] . B[N][K]^T, then *colscale[n] (nullable), +bias[n] (nullable),
+ * written (accumulate = 0) or added (accumulate = 1) to f32 C [M][ldc]. Both operands are
+ * K-contiguous. prec: SA3K_PREC_BF16 (A: f32 or bf16; B: f32, f16, bf16 or Q8_0 decoded in the
+ * kernel) or SA3K_PREC_F32 (A f32; B f32 or f16). For b_type SA3K_TYPE_Q8_0, B holds int8 quants
+ * [N][ldb] and B_scales the f16 block scales [N][ldbs] (one per 32 K); b_type -8 selects the
+ * transposed Q8_0 layout (quants [N][K], scales [N/32][ldbs] per 32 rows). This is the kernel under
+ * the reference's ggml_mul_mat(W, x) (src/dit.h:107) and its autodiff out_prod, exposed for tests
+ * and measurement; dit_lin itself is sa3k_lin_*. K must be a multiple of 64 (bf16) / 32 (f32). */
+SA3K_API int sa3k_gemm_nt(sa3k_ctx* ctx, int prec, int a_type, const void* A, int64_t lda,
+                          int b_type, const void* B, int64_t ldb, const void* B_scales, int64_t ldbs,
+                          int64_t M, int64_t N, int64_t K, float alpha, const float* colscale,
+                          const float* bias, float* C, int64_t ldc, int accumulate);
+
+/* ---------------------------------------------------------------- frozen base weights */
+
+typedef struct sa3k_weight sa3k_weight;
+
+/* Load a frozen base weight W [out][in] of GGUF type `type` (f32 / f16 / bf16 elements, or raw
+ * Q8_0 blocks) from host memory (data_on_device = 0) or device memory. The library keeps the
+ * forward layout and a transposed copy for the backward; Q8_0 blocks are split into int8 quants
+ * and f16 scales (the same bytes, not re-encoded) in both layouts, so every contraction decodes
+ * the stored blocks exactly. in must be a multiple of 64; out a multiple of 8 (32 for Q8_0).
+ * The reference reads weights through GgufModel::get (src/gguf_model.h:200-276). */
+SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out, const void* data,
+                                int data_on_device, sa3k_weight** out_w);
+SA3K_API int sa3k_weight_destroy(sa3k_ctx* ctx, sa3k_weight* w);
+/* nsq[o] = (float)(sum_i (double)W[o][i]^2 + in*eps)   (train_row_norm_sq, src/train_lora.h:160-174)
+ * norms[o] = (float)sqrt(sum_i (double)W[o][i]^2)       (train_row_norms,   src/train_lora.h:141-155)
+ * over the decoded weight; outputs are device [out] f32. */
+SA3K_API int sa3k_weight_row_norm_sq(sa3k_ctx* ctx, const sa3k_weight* w, float eps, float* nsq);
+SA3K_API int sa3k_weight_row_norms(sa3k_ctx* ctx, const sa3k_weight* w, float* norms);
+
+/* ---------------------------------------------------------------- K1-K4: dit_lin (lora / dora-rows) */
+
+/* One adapted linear: the functional dit_lin of src/dit.h:92-149 over a frozen sa3k_weight, with
+ * its own device scratch for up to max_tokens rows (saved activations and backward workspace).
+ * rank: 0 (plain mul_mat) or 8/16/24/32; prec: SA3K_PREC_F32 (f32/f16 weights) or SA3K_PREC_BF16. */
+typedef struct sa3k_lin sa3k_lin;
+SA3K_API int sa3k_lin_create(sa3k_ctx* ctx, const sa3k_weight* W, int rank, int prec, int64_t max_tokens,
+                             sa3k_lin** out_l);
+SA3K_API int sa3k_lin_destroy(sa3k_ctx* ctx, sa3k_lin* l);
+
+/* Refresh the adapter-derived terms after A/B/magnitude change (once per optimizer step):
+ * A [rank][in], B [out][rank], scale = alpha/rank (src/train_dit.h:151); dora = 1 adds the
+ * dora-rows row scale d = m / sqrt(bnsq + 2s.t2 + s^2.t3) with t2 = rowsum((W A^T) * B) and
+ * t3 = rowsum(B * (B A A^T)) (src/dit.h:123-145), base_norm_sq from sa3k_weight_row_norm_sq with
+ * eps 1e-12 (src/train_dit.h:159). All pointers are device memory and must stay valid and
+ * unchanged until the next prepare (the backward reads B and magnitude). */
+SA3K_API int sa3k_lin_prepare(sa3k_ctx* ctx, sa3k_lin* l, const float* A, const float* B, float scale,
+                              int dora, const float* magnitude, const float* base_norm_sq);
+
+/* Y [N][out] f32 = (X W^T + s (X A^T) B^T) * d + bias  (bias nullable; d = 1 for lora).
+ * X [N][in] is f32 (x_type SA3K_TYPE_F32) or, with bf16 precision, bf16. Saves what the
+ * backward needs (s X A^T and, for dora, the pre-scale output) in the linear's scratch. */
+SA3K_API int sa3k_lin_forward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const void* X, int64_t N,
+                              const float* bias, float* Y);
+
+/* Backward of the last forward (same X and N), the closed form of ggml's autodiff of dit_lin:
+ *   dX  = dU W + s (dU B) A                 (dU = dY * d)      -> written, or added if dx_accumulate
+ *   dA += s (dU B)^T X + 2s B^T diag(gn) W + 2s^2 (B^T diag(gn) B) A
+ *   dB += s dU^T (X A^T) + 2s diag(gn) W A^T + 2s^2 diag(gn) B A A^T
+ *   dm += gd / sqrt(nsq)                    (gd = sum_n dY * U, gn = -gd m nsq^-3/2 / 2; dora only)
+ * dA [rank][in], dB [out][rank], dm [out] are f32 accumulators (the micro-batch sum of
+ * train_accum_add, src/train_loop.h:75-78). dX may be NULL (no input gradient). */
+SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const void* X, int64_t N,
+                               const float* dY, float* dX, int dx_accumulate, float* dA, float* dB,
+                               float* dm);
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,10 +147,10 @@ void orc_gemm_nt(const float* A, const float* B, float* C, int64_t M, int64_t N,
 }
 
 // src/dit.h:92-149: y = W x (+ s B A x), dora: y *= m / sqrt(bnsq + 2s t2 + s^2 t3), then + bias
-void orc_dit_lin_fwd(const float* Xf, int64_t N, const float* Wf, int64_t in, int64_t out,
-                     const float* Af, const float* Bf, int r, float sf, int dora, const float* mag,
-                     const float* bnsq, const float* bias, float* Y, float* U, float* dscale,
-                     float* nsq_out) {
+static void dit_lin_fwd_impl(const float* Xf, int64_t N, const float* Wf, int64_t in, int64_t out,
+                             const float* Af, const float* Bf, int r, float sf, int dora, const float* mag,
+                             const float* bnsq, const float* bias, float* Y, float* U, float* dscale,
+                             float* nsq_out, std::vector<double>* Yd) {
     const double s = sf;
     dvec X = to_d(Xf, N * in), W = to_d(Wf, out * in);
     dvec A = r ? to_d(Af, (int64_t)r * in) : dvec(), B = r ? to_d(Bf, out * r) : dvec();
@@ -160,7 +160,7 @@ void orc_dit_lin_fwd(const float* Xf, int64_t N, const float* Wf, int64_t in, in
         dvec H((size_t)(N * r));
         mm_nt(X.data(), A.data(), H.data(), N, r, in);
         dvec BAX((size_t)(N * out));
-        mm_nt(H.data(), transpose(B.data(), out, r).data(), BAX.data(), N, out, r);
+        mm_nt(H.data(), B.data(), BAX.data(), N, out, r);   // (X A^T) B^T: B [out][r] is K-contiguous
         for (size_t i = 0; i < Y0.size(); ++i) Y0[i] += s * BAX[i];
     }
     DoraTerms t = dora_terms(W, A, B, in, out, r, s, dora && r > 0, mag, bnsq);
@@ -170,12 +170,32 @@ void orc_dit_lin_fwd(const float* Xf, int64_t N, const float* Wf, int64_t in, in
             if (U) U[n * out + o] = (float)u;
             double y = u * t.d[(size_t)o];
             if (bias) y += bias[o];
-            Y[n * out + o] = (float)y;
+            if (Y) Y[n * out + o] = (float)y;
+            if (Yd) (*Yd)[(size_t)(n * out + o)] = y;
         }
     if (dscale)
         for (int64_t o = 0; o < out; ++o) dscale[o] = (float)t.d[(size_t)o];
     if (nsq_out)
         for (int64_t o = 0; o < out; ++o) nsq_out[o] = (float)t.nsq[(size_t)o];
+}
+
+void orc_dit_lin_fwd(const float* Xf, int64_t N, const float* Wf, int64_t in, int64_t out,
+                     const float* Af, const float* Bf, int r, float sf, int dora, const float* mag,
+                     const float* bnsq, const float* bias, float* Y, float* U, float* dscale,
+                     float* nsq_out) {
+    dit_lin_fwd_impl(Xf, N, Wf, in, out, Af, Bf, r, sf, dora, mag, bnsq, bias, Y, U, dscale, nsq_out, nullptr);
+}
+
+// sum (Y - tgt)^2 with Y kept in double (for finite-difference checks of the backward)
+double orc_dit_lin_sqloss(const float* Xf, int64_t N, const float* Wf, int64_t in, int64_t out,
+                          const float* Af, const float* Bf, int r, float sf, int dora, const float* mag,
+                          const float* bnsq, const float* bias, const float* tgt) {
+    std::vector<double> Yd((size_t)(N * out));
+    dit_lin_fwd_impl(Xf, N, Wf, in, out, Af, Bf, r, sf, dora, mag, bnsq, bias, nullptr, nullptr, nullptr,
+                     nullptr, &Yd);
+    double l = 0.0;
+    for (size_t i = 0; i < Yd.size(); ++i) l += (Yd[i] - tgt[i]) * (Yd[i] - tgt[i]);
+    return l;
 }
 
 void orc_dit_lin_bwd(const float* Xf, int64_t N, const float* Wf, int64_t in, int64_t out,
@@ -197,7 +217,7 @@ void orc_dit_lin_bwd(const float* Xf, int64_t N, const float* Wf, int64_t in, in
         dvec U((size_t)(N * out));
         mm_nt(X.data(), W.data(), U.data(), N, out, in);
         dvec BAX((size_t)(N * out));
-        mm_nt(H.data(), transpose(B.data(), out, r).data(), BAX.data(), N, out, r);
+        mm_nt(H.data(), B.data(), BAX.data(), N, out, r);   // (X A^T) B^T: B [out][r] is K-contiguous
         dvec gd((size_t)out, 0.0);
         for (int64_t n = 0; n < N; ++n)
             for (int64_t o = 0; o < out; ++o) {

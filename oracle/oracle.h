@@ -63,6 +63,10 @@ void orc_dit_lin_fwd(const float* X, int64_t N, const float* W, int64_t in, int6
                      const float* A, const float* B, int rank, float s, int dora, const float* mag,
                      const float* bnsq, const float* bias, float* Y, float* U, float* dscale,
                      float* nsq_out);
+/* sum (Y - tgt)^2 with Y in double (finite-difference checks) */
+double orc_dit_lin_sqloss(const float* X, int64_t N, const float* W, int64_t in, int64_t out,
+                          const float* A, const float* B, int rank, float s, int dora, const float* mag,
+                          const float* bnsq, const float* bias, const float* tgt);
 /* bwd from dY [N][out]: dX [N][in], dA [r][in], dB [out][r], dm [out] (dora; nullable otherwise).
  * Any output pointer may be NULL to skip it. */
 void orc_dit_lin_bwd(const float* X, int64_t N, const float* W, int64_t in, int64_t out,

@@ -48,6 +48,7 @@ def lib():
         "orc_effective_weight": (None, [f32p, I64, I64, f32p, f32p, optf, I, F, I, f32p]),
         "orc_dit_lin_fwd": (None, [f32p, I64, f32p, I64, I64, optf, optf, I, F, I, optf, optf, optf,
                                    f32p, optf, optf, optf]),
+        "orc_dit_lin_sqloss": (D, [f32p, I64, f32p, I64, I64, optf, optf, I, F, I, optf, optf, optf, f32p]),
         "orc_dit_lin_bwd": (None, [f32p, I64, f32p, I64, I64, optf, optf, I, F, I, optf, optf, f32p,
                                    optf, optf, optf, optf]),
         "orc_gemm_nt": (None, [f32p, f32p, f32p, I64, I64, I64]),
@@ -166,6 +167,20 @@ def dit_lin_fwd(X, W, A=None, B=None, s=1.0, dora=False, mag=None, bnsq=None, bi
     lib().orc_dit_lin_fwd(X, N, W, in_, out_, _p(A), _p(B), r, s, int(dora), _p(mag), _p(bnsq), _p(bias),
                           Y, _p(U), _p(d), _p(nsq))
     return dict(Y=Y, U=U, d=d, nsq=nsq)
+
+
+def dit_lin_sqloss(X, W, tgt, A=None, B=None, s=1.0, dora=False, mag=None, bnsq=None, bias=None):
+    X, W, tgt = f32(X), f32(W), f32(tgt)
+    N, in_ = X.shape
+    out_ = W.shape[0]
+    r = 0 if A is None else A.shape[0]
+    A = None if A is None else f32(A)
+    B = None if B is None else f32(B)
+    mag = None if mag is None else f32(mag)
+    bnsq = None if bnsq is None else f32(bnsq)
+    bias = None if bias is None else f32(bias)
+    return lib().orc_dit_lin_sqloss(X, N, W, in_, out_, _p(A), _p(B), r, s, int(dora), _p(mag), _p(bnsq),
+                                    _p(bias), tgt)
 
 
 def dit_lin_bwd(X, W, dY, A=None, B=None, s=1.0, dora=False, mag=None, bnsq=None):

@@ -1,0 +1,78 @@
+// K1/K2: LDS-tiled MFMA GEMM for gfx950, C[M][N] = alpha * (A[M][K] . B[N][K]^T (+ A2 . B2^T)).
+//
+// Both operands are K-contiguous ("NT"): the frozen base weight W [out][in] is the B operand of
+// the forward product X W^T, and its transposed copy W^T [in][out] (laid out once when the weight
+// is loaded) is the B operand of dX = dU W. The B operand is decoded in the global->LDS path from
+// its stored type (bf16, f16, f32, or Q8_0 quants + f16 scales) into the compute type, so a Q8_0 or
+// f16 base is never expanded in HBM.
+//
+// Compute types: bf16 (v_mfma_f32_16x16x32_bf16, fp32 accumulation) and f32
+// (v_mfma_f32_16x16x4_f32). Tiles: 256 threads = 4 wave64s; BK = 128 bytes of the compute type
+// per row (64 bf16 or 32 f32); every LDS row is padded to 144 bytes; double-buffered LDS with one
+// barrier per K step; each lane feeds the MFMAs from 16-byte LDS reads.
+//
+// The optional second segment (A2 [M][K2], B2 [N][K2], K2 <= one K tile, stored in the compute
+// type) appends a rank-K2 product to the same accumulators: the LoRA term s.(X A^T) B^T of the
+// forward and the (dU B) A term of dX ride on the base GEMM this way.
+//
+// Extra rows (Mx) let a rank-sized product that contracts the same B operand ride on the same
+// GEMM: the DoRA term 2s B^T diag(gn) W of dA shares the W^T tiles of dX.
+//
+// Epilogue per column n: v = alpha*acc; U = v (optional pre-scale copy); v *= colscale[n];
+// v += bias[n]; C = v (or C += v); Cb = bf16(v).
+#pragma once
+
+#include "sa3k_internal.h"
+
+namespace sa3k {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+enum SrcType { SRC_BF16 = 0, SRC_F16 = 1, SRC_F32 = 2, SRC_Q8 = 3, SRC_Q8T = 4 };
+
+struct GemmDesc {
+    int prec = SA3K_PREC_BF16;   // compute type
+    int a_src = SRC_BF16;        // SRC_BF16 or SRC_F32
+    int b_src = SRC_BF16;        // any SrcType
+    const void* A = nullptr;     // [M][lda]
+    int64_t lda = 0;
+    const void* B = nullptr;     // [N][ldb] (Q8/Q8T: int8 quants)
+    int64_t ldb = 0;
+    const void* Bs = nullptr;    // Q8: f16 scales [N][ldbs] per 32 K; Q8T: [N/32][ldbs] per 32 N
+    int64_t ldbs = 0;
+    const void* A2 = nullptr;    // [M][lda2] compute type
+    int64_t lda2 = 0;
+    const void* B2 = nullptr;    // [N][ldb2] compute type
+    int64_t ldb2 = 0;
+    int K2 = 0;
+    int64_t M = 0, N = 0, K = 0;
+    float alpha = 1.0f;
+    const float* colscale = nullptr;  // [N]
+    const float* bias = nullptr;      // [N]
+    float* C = nullptr;               // [M][ldc]
+    int64_t ldc = 0;
+    int accumulate = 0;               // C += v
+    bf16* Cb = nullptr;               // [M][ldcb]
+    int64_t ldcb = 0;
+    float* U = nullptr;               // [M][ldu] pre-colscale copy (f32)
+    bf16* Ub = nullptr;               // [M][ldu] pre-colscale copy (bf16)
+    int64_t ldu = 0;
+    // Mx extra rows appended below A (compute type, [Mx][ldax]), with their own second-segment rows
+    // A2x [Mx][lda2x]; their results go to Cx [Mx][ldcx] (+= when accumulate_x) without the
+    // epilogue's colscale/bias. They share every B tile with the main rows.
+    int64_t Mx = 0;
+    const void* Ax = nullptr;
+    int64_t ldax = 0;
+    const void* A2x = nullptr;
+    int64_t lda2x = 0;
+    float* Cx = nullptr;
+    int64_t ldcx = 0;
+    int accumulate_x = 0;
+};
+
+// Enqueue one GEMM on the context stream (validates shapes, picks the tile configuration).
+void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name);
+
+}  // namespace sa3k

@@ -1,0 +1,716 @@
+// K1-K4: the functional LoRA / DoRA-rows linear of the DiT (dit_lin, src/dit.h:92-149), forward
+// and backward, on top of the MFMA GEMM (gemm.h) and three small families of kernels:
+//   * frozen weights:   layout once at load (forward [out][in] + transposed [in][out]; Q8_0 blocks
+//                       split into int8 quants and f16 scales, bit-for-bit), row norms
+//                       (train_row_norm_sq / train_row_norms, src/train_lora.h:141-174)
+//   * adapter prepare:  once per optimizer step: P^T = A W^T (W-streaming GEMM), G = A A^T,
+//                       t2, t3, nsq = bnsq + 2s t2 + s^2 t3, d = m / sqrt(nsq)  (src/dit.h:123-145)
+//   * column reductions over the token axis (K3): gd = sum_n dY*U, dU^T H, (s dU B)^T X
+//
+// Forward (per call):   Hc = s X A^T                      (skinny GEMM)
+//                       Y  = (X W^T + Hc B^T) * d + bias  (one GEMM: K-extension + epilogue)
+// Backward (per call):  dU = dY*d, gd, dU^T Hc             (column reduction, writes dU)
+//                       dm += gd/sqrt(nsq), gn = -gd m nsq^-3/2 / 2,
+//                       dB += dU^T Hc + 2s gn P + 2s^2 gn B G
+//                       sdUB = s dU B                      (skinny GEMM)
+//                       dX = dU W + sdUB A  and, as r extra GEMM rows sharing the W^T tiles,
+//                       dA += 2s B^T diag(gn) W + 2s^2 (B^T diag(gn) B) A
+//                       dA += sdUB^T X                     (column reduction)
+#include "gemm.h"
+
+#include <cmath>
+#include <vector>
+
+using namespace sa3k;
+
+struct sa3k_weight {
+    int type = SA3K_TYPE_F32;
+    int64_t in = 0, out = 0;
+    void* w = nullptr;      // forward layout [out][in] (Q8_0: int8 quants)
+    void* ws = nullptr;     // Q8_0: f16 scales [out][in/32]
+    void* wt = nullptr;     // transposed [in][out] (Q8_0: int8 quants)
+    void* wts = nullptr;    // Q8_0: f16 scales [in/32][out]
+};
+
+struct sa3k_lin {
+    const sa3k_weight* W = nullptr;
+    int rank = 0, prec = SA3K_PREC_BF16, dora = 0;
+    float s = 1.0f;
+    int64_t max_tokens = 0;
+    size_t ct = 2;                      // bytes of the compute type
+    // adapter-derived, refreshed by prepare
+    void* Ac = nullptr;                 // [r][in]   compute type
+    void* At = nullptr;                 // [in][r]
+    void* Bc = nullptr;                 // [out][r]
+    void* Bt = nullptr;                 // [r][out]
+    float* Pt = nullptr;                // [r][out]  (A W^T)
+    float* G = nullptr;                 // [r][r]
+    float* BG = nullptr;                // [out][r]  B G
+    float* nsq = nullptr;               // [out]
+    float* d = nullptr;                 // [out]
+    const float* B = nullptr;           // adapter pointers of the last prepare (device)
+    const float* mag = nullptr;
+    // saved by forward for backward
+    void* Hc = nullptr;                 // [max_tokens][r] compute type: s X A^T
+    void* U = nullptr;                  // [max_tokens][out] compute type: pre-scale output
+    int64_t saved_tokens = -1;
+    // backward scratch
+    void* dU = nullptr;                 // [max_tokens][out] compute type
+    void* sdUB = nullptr;               // [max_tokens][r] compute type
+    float* gd = nullptr;                // [out]
+    float* gn = nullptr;                // [out]
+    void* Ax = nullptr;                 // [r][out] compute type: 2s (B*gn)^T
+    void* A2x = nullptr;                // [r][r]   compute type: 2s^2 B^T diag(gn) B
+    float* part = nullptr;              // column-reduction partial sums
+    size_t part_elems = 0;
+    float* red = nullptr;               // [out][r] reduced dU^T Hc
+};
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <class T>
+T* dev_alloc(size_t n) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    SA3K_HIP(hipMalloc(&p, n * sizeof(T)));
+    return static_cast<T*>(p);
+}
+
+// ---------------------------------------------------------------- weight layout
+// transpose a [rows][cols] matrix of T into [cols][rows] through a 32x32 LDS tile
+template <class T>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                              int64_t rows, int64_t cols) {
+    __shared__ T tile[32][33];
+    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8
+    for (int k = ty; k < 32; k += 8) {
+        const int64_t r = r0 + k, c = c0 + tx;
+        if (r < rows && c < cols) tile[k][tx] = src[r * cols + c];
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += 8) {
+        const int64_t c = c0 + k, r = r0 + tx;
+        if (r < rows && c < cols) dst[c * rows + r] = tile[tx][k];
+    }
+}
+
+template <class T>
+void transpose(sa3k_ctx* ctx, const T* src, T* dst, int64_t rows, int64_t cols) {
+    dim3 grid((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32));
+    transpose_kernel<T><<<grid, kThreads, 0, ctx->stream>>>(src, dst, rows, cols);
+    SA3K_LAUNCHED();
+}
+
+// Q8_0 blocks -> int8 quants [out][in] + f16 scales [out][in/32] (bytes copied, not re-encoded)
+__global__ __launch_bounds__(kThreads) void q8_split_kernel(const uint16_t* __restrict__ blocks,
+                                                            int8_t* __restrict__ qs, uint16_t* __restrict__ sc,
+                                                            int64_t nb) {
+    const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (b >= nb) return;
+    const uint16_t* src = blocks + b * 17;
+    sc[b] = src[0];
+    uint16_t* dq = reinterpret_cast<uint16_t*>(qs + b * 32);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dq[j] = src[1 + j];
+}
+
+__device__ inline float load_w(const sa3k_weight& w, const void* p, const void* ps, int64_t idx, int64_t in) {
+    switch (w.type) {
+        case SA3K_TYPE_F32: return static_cast<const float*>(p)[idx];
+        case SA3K_TYPE_F16: return (float)static_cast<const _Float16*>(p)[idx];
+        case SA3K_TYPE_BF16: return (float)static_cast<const bf16*>(p)[idx];
+        default: {  // Q8_0 split: value = scale[row][col/32] * q
+            const int64_t row = idx / in, col = idx - row * in;
+            return (float)static_cast<const _Float16*>(ps)[row * (in / 32) + (col >> 5)] *
+                   (float)static_cast<const int8_t*>(p)[idx];
+        }
+    }
+}
+
+// sum_i W[o][i]^2 in double per row; mode 0: + in*eps (nsq), mode 1: sqrt (norms)
+__global__ __launch_bounds__(kThreads) void row_norm_kernel(sa3k_weight w, float eps, int mode,
+                                                            float* __restrict__ out) {
+    __shared__ double sh[kThreads / 64];
+    const int64_t o = blockIdx.x;
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < w.in; i += kThreads) {
+        const float v = load_w(w, w.w, w.ws, o * w.in + i, w.in);
+        acc += (double)v * v;
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int k = 0; k < kThreads / 64; ++k) s += sh[k];
+        out[o] = mode == 0 ? (float)(s + (double)w.in * eps) : (float)sqrt(s);
+    }
+}
+
+// ---------------------------------------------------------------- adapter prepare
+template <class CT>
+__global__ __launch_bounds__(kThreads) void cvt_kernel(const float* __restrict__ src, CT* __restrict__ dst,
+                                                       int64_t n, float scale) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) dst[i] = (CT)(src[i] * scale);
+}
+
+template <class CT>
+__global__ __launch_bounds__(kThreads) void cvt_t_kernel(const float* __restrict__ src, CT* __restrict__ dst,
+                                                         int64_t rows, int64_t cols) {
+    // dst[c][r] = src[r][c] (small adapter matrices)
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols, c = i - r * cols;
+    dst[c * rows + r] = (CT)src[i];
+}
+
+// G[a][b] = sum_i A[a][i] A[b][i] (one block per (a,b), double accumulation)
+__global__ __launch_bounds__(kThreads) void gram_kernel(const float* __restrict__ A, int64_t in, int r,
+                                                        float* __restrict__ G) {
+    __shared__ double sh[kThreads / 64];
+    const int a = blockIdx.x / r, b = blockIdx.x % r;
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < in; i += kThreads) acc += (double)A[a * in + i] * A[b * in + i];
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) G[a * r + b] = (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+}
+
+// per output row o: t2 = sum_a P[o][a] B[o][a]; BG[o] = B[o] G; t3 = B[o] . BG[o];
+// nsq = bnsq + 2s t2 + s^2 t3; d = m / sqrt(nsq)
+__global__ __launch_bounds__(kThreads) void dora_terms_kernel(const float* __restrict__ Pt, const float* __restrict__ B,
+                                                              const float* __restrict__ G, const float* __restrict__ bnsq,
+                                                              const float* __restrict__ mag, int64_t out, int r, float s,
+                                                              float* __restrict__ BG, float* __restrict__ nsq,
+                                                              float* __restrict__ d) {
+    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (o >= out) return;
+    float b[32];
+    for (int a = 0; a < r; ++a) b[a] = B[o * r + a];
+    float t2 = 0.f, t3 = 0.f;
+    for (int a = 0; a < r; ++a) {
+        t2 += Pt[(int64_t)a * out + o] * b[a];
+        float g = 0.f;
+        for (int c = 0; c < r; ++c) g += b[c] * G[c * r + a];
+        BG[o * r + a] = g;
+        t3 += b[a] * g;
+    }
+    const float n2 = bnsq[o] + 2.0f * s * t2 + s * s * t3;
+    nsq[o] = n2;
+    d[o] = mag[o] / sqrtf(n2);
+}
+
+// ---------------------------------------------------------------- K3 column reductions
+template <class CT>
+__device__ inline float ld_ct(const CT* p, int64_t i) { return (float)p[i]; }
+
+// Rows [r0, r1) of dY: dU = dY*d (stored, compute type), partial gd = sum dY*U and
+// partial (dU^T Hc)[o][a] = sum_n dU[n][o] Hc[n][a]. One thread per column o.
+template <class CT, int R>
+__global__ __launch_bounds__(kThreads) void colred_dy_kernel(const float* __restrict__ dY, const CT* __restrict__ U,
+                                                             const float* __restrict__ d, const CT* __restrict__ Hc,
+                                                             CT* __restrict__ dU, float* __restrict__ part,
+                                                             int64_t N, int64_t out, int r, int64_t rows_per) {
+    __shared__ float hs[64][R];
+    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(N, r0 + rows_per);
+    const float dd = (d && o < out) ? d[o] : 1.0f;
+    float gd = 0.f, acc[R];
+#pragma unroll
+    for (int a = 0; a < R; ++a) acc[a] = 0.f;
+    for (int64_t nb = r0; nb < r1; nb += 64) {
+        const int cnt = (int)min((int64_t)64, r1 - nb);
+        __syncthreads();
+        for (int k = threadIdx.x; k < cnt * R; k += kThreads) {
+            const int row = k / R, a = k - row * R;
+            hs[row][a] = a < r ? ld_ct(Hc, (nb + row) * r + a) : 0.f;
+        }
+        __syncthreads();
+        if (o < out) {
+            for (int row = 0; row < cnt; ++row) {
+                const int64_t n = nb + row;
+                const float y = dY[n * out + o];
+                const float du = y * dd;
+                if (U) gd += y * ld_ct(U, n * out + o);
+                dU[n * out + o] = (CT)du;
+#pragma unroll
+                for (int a = 0; a < R; ++a) acc[a] += du * hs[row][a];
+            }
+        }
+    }
+    if (o >= out) return;
+    // partial layout: [split][R+1][out] (coalesced over o)
+    float* p = part + (int64_t)blockIdx.y * (R + 1) * out;
+    p[o] = gd;
+#pragma unroll
+    for (int a = 0; a < R; ++a) p[(int64_t)(a + 1) * out + o] = acc[a];
+}
+
+// partial (G^T X)[a][i] = sum_n G[n][a] X[n][i] over rows [r0, r1). One thread per column i.
+template <class XT, class CT, int R>
+__global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict__ X, const CT* __restrict__ Gm,
+                                                            float* __restrict__ part, int64_t N, int64_t in, int r,
+                                                            int64_t rows_per) {
+    __shared__ float gs[64][R];
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(N, r0 + rows_per);
+    float acc[R];
+#pragma unroll
+    for (int a = 0; a < R; ++a) acc[a] = 0.f;
+    for (int64_t nb = r0; nb < r1; nb += 64) {
+        const int cnt = (int)min((int64_t)64, r1 - nb);
+        __syncthreads();
+        for (int k = threadIdx.x; k < cnt * R; k += kThreads) {
+            const int row = k / R, a = k - row * R;
+            gs[row][a] = a < r ? ld_ct(Gm, (nb + row) * r + a) : 0.f;
+        }
+        __syncthreads();
+        if (i < in) {
+            for (int row = 0; row < cnt; ++row) {
+                const float x = (float)X[(nb + row) * in + i];
+#pragma unroll
+                for (int a = 0; a < R; ++a) acc[a] += x * gs[row][a];
+            }
+        }
+    }
+    if (i >= in) return;
+    float* p = part + (int64_t)blockIdx.y * R * in;
+#pragma unroll
+    for (int a = 0; a < R; ++a) p[(int64_t)a * in + i] = acc[a];
+}
+
+// y[j] (+)= sum_s part[s][j], j < n (fixed summation order: deterministic)
+__global__ __launch_bounds__(kThreads) void sum_splits_kernel(const float* __restrict__ part, int64_t stride, int S,
+                                                              int64_t n, float* __restrict__ y, int accumulate) {
+    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (j >= n) return;
+    float s = 0.f;
+    for (int k = 0; k < S; ++k) s += part[(int64_t)k * stride + j];
+    y[j] = accumulate ? y[j] + s : s;
+}
+
+// after gd: dm += gd/sqrt(nsq); gn = -gd m nsq^-3/2 / 2; dB[o][a] += dUtH[a][o] + 2s gn P[o][a] + 2s^2 gn BG[o][a];
+// Ax[a][o] = 2s B[o][a] gn[o]  (lora: dB += dUtH only)
+template <class CT>
+__global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __restrict__ gd, const float* __restrict__ redT,
+                                                                 const float* __restrict__ nsq, const float* __restrict__ mag,
+                                                                 const float* __restrict__ Pt, const float* __restrict__ BG,
+                                                                 const float* __restrict__ B, int64_t out, int r, float s,
+                                                                 int dora, float* __restrict__ dB, float* __restrict__ dm,
+                                                                 float* __restrict__ gn_out, CT* __restrict__ Ax) {
+    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (o >= out) return;
+    float gn = 0.f;
+    if (dora) {
+        const float n2 = nsq[o], sq = sqrtf(n2);
+        const float g = gd[o];
+        if (dm) dm[o] += g / sq;
+        gn = -0.5f * g * mag[o] / (n2 * sq);
+        gn_out[o] = gn;
+    }
+    for (int a = 0; a < r; ++a) {
+        float v = redT[(int64_t)a * out + o];
+        if (dora) {
+            v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
+            Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
+        }
+        dB[o * r + a] += v;
+    }
+}
+
+// A2x[a][b] = 2 s^2 sum_o B[o][a] gn[o] B[o][b]  (one block per (a,b))
+template <class CT>
+__global__ __launch_bounds__(kThreads) void btgb_kernel(const float* __restrict__ B, const float* __restrict__ gn,
+                                                        int64_t out, int r, float s, CT* __restrict__ A2x) {
+    __shared__ float sh[kThreads / 64];
+    const int a = blockIdx.x / r, b = blockIdx.x % r;
+    float acc = 0.f;
+    for (int64_t o = threadIdx.x; o < out; o += kThreads) acc += B[o * r + a] * gn[o] * B[o * r + b];
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) A2x[a * r + b] = (CT)(2.0f * s * s * (sh[0] + sh[1] + sh[2] + sh[3]));
+}
+
+int src_of_weight(int type, bool transposed) {
+    switch (type) {
+        case SA3K_TYPE_F32: return SRC_F32;
+        case SA3K_TYPE_F16: return SRC_F16;
+        case SA3K_TYPE_BF16: return SRC_BF16;
+        case SA3K_TYPE_Q8_0: return transposed ? SRC_Q8T : SRC_Q8;
+    }
+    sa3k_throw(SA3K_ERR_UNSUPPORTED, "weight type");
+    return 0;
+}
+
+size_t type_size(int type) {
+    switch (type) {
+        case SA3K_TYPE_F32: return 4;
+        case SA3K_TYPE_F16: case SA3K_TYPE_BF16: return 2;
+        case SA3K_TYPE_Q8_0: return 1;
+    }
+    sa3k_throw(SA3K_ERR_UNSUPPORTED, "weight type");
+    return 0;
+}
+
+void free_weight(sa3k_weight* w) {
+    if (!w) return;
+    for (void* p : {w->w, w->ws, w->wt, w->wts}) if (p) (void)hipFree(p);
+    delete w;
+}
+
+void free_lin(sa3k_lin* L) {
+    if (!L) return;
+    for (void* p : {L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
+                    (void*)L->d, L->Hc, L->U, L->dU, L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x,
+                    (void*)L->part, (void*)L->red})
+        if (p) (void)hipFree(p);
+    delete L;
+}
+
+// row split count for the column reductions: enough blocks to cover the chip
+int choose_splits(int64_t cols, int64_t N) {
+    const int64_t col_blocks = ceil_div(cols, kThreads);
+    int64_t S = ceil_div(1024, col_blocks);
+    S = std::max<int64_t>(1, std::min<int64_t>(S, ceil_div(N, 16)));
+    return (int)std::min<int64_t>(S, 128);
+}
+
+template <class CT>
+void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* bias, float* Y) {
+    const sa3k_weight* W = L->W;
+    const bool bf = L->prec == SA3K_PREC_BF16;
+    // Hc = s X A^T
+    if (L->rank > 0) {
+        GemmDesc h;
+        h.prec = L->prec; h.a_src = x_src; h.b_src = bf ? SRC_BF16 : SRC_F32;
+        h.A = X; h.lda = W->in; h.B = L->Ac; h.ldb = W->in;
+        h.M = N; h.N = L->rank; h.K = W->in; h.alpha = L->s;
+        if (bf) { h.Cb = static_cast<bf16*>(L->Hc); h.ldcb = L->rank; }
+        else { h.C = static_cast<float*>(L->Hc); h.ldc = L->rank; }
+        gemm_run(ctx, h, "lin_fwd_h");
+    }
+    GemmDesc g;
+    g.prec = L->prec; g.a_src = x_src; g.b_src = src_of_weight(W->type, false);
+    g.A = X; g.lda = W->in; g.B = W->w; g.ldb = W->in; g.Bs = W->ws; g.ldbs = W->in / 32;
+    if (L->rank > 0) { g.A2 = L->Hc; g.lda2 = L->rank; g.B2 = L->Bc; g.ldb2 = L->rank; g.K2 = L->rank; }
+    g.M = N; g.N = W->out; g.K = W->in; g.alpha = 1.0f;
+    g.colscale = L->dora ? L->d : nullptr;
+    g.bias = bias;
+    g.C = Y; g.ldc = W->out;
+    g.ldu = W->out;
+    if (L->dora) { if (bf) g.Ub = static_cast<bf16*>(L->U); else g.U = static_cast<float*>(L->U); }
+    gemm_run(ctx, g, "lin_fwd_main");
+    L->saved_tokens = N;
+}
+
+template <class CT, int R>
+void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* dY, float* dX,
+                    int dx_acc, float* dA, float* dB, float* dm) {
+    const sa3k_weight* W = L->W;
+    const bool bf = L->prec == SA3K_PREC_BF16;
+    const int64_t in = W->in, out = W->out;
+    const int r = L->rank;
+    // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens)
+    {
+        const int S = choose_splits(out, N);
+        const int64_t rows_per = ceil_div(N, S);
+        SA3K_REQUIRE((size_t)S * (R + 1) * out <= L->part_elems, "column-reduction scratch too small");
+        dim3 grid((unsigned)ceil_div(out, kThreads), (unsigned)S);
+        {
+            KernelScope ks(ctx, "lin_bwd_colred_dy");
+            colred_dy_kernel<CT, R><<<grid, kThreads, 0, ctx->stream>>>(
+                dY, static_cast<const CT*>(L->dora ? L->U : nullptr), L->dora ? L->d : nullptr,
+                static_cast<const CT*>(L->Hc), static_cast<CT*>(L->dU), L->part, N, out, r, rows_per);
+            SA3K_LAUNCHED();
+        }
+        KernelScope ks(ctx, "lin_bwd_reduce");
+        // gd -> L->gd ; rows a+1 -> red[a][out]
+        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(R + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
+            L->part, (int64_t)(R + 1) * out, S, (int64_t)(R + 1) * out, L->red, 0);
+        SA3K_LAUNCHED();
+    }
+    // L->red holds [gd | dUtH rows]: gd = red[0..out), dUtH[a] = red[(a+1)*out ...]
+    const float* gd = L->red;
+    const float* redT = L->red + out;
+    {
+        KernelScope ks(ctx, "lin_bwd_rows");
+        dora_bwd_rows_kernel<CT><<<(unsigned)ceil_div(out, kThreads), kThreads, 0, ctx->stream>>>(
+            gd, redT, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
+            static_cast<CT*>(L->Ax));
+        SA3K_LAUNCHED();
+        if (L->dora) {
+            btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
+                                                                             static_cast<CT*>(L->A2x));
+            SA3K_LAUNCHED();
+        }
+    }
+    // 2. sdUB = s dU B
+    {
+        GemmDesc g;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = bf ? SRC_BF16 : SRC_F32;
+        g.A = L->dU; g.lda = out; g.B = L->Bt; g.ldb = out;
+        g.M = N; g.N = r; g.K = out; g.alpha = L->s;
+        if (bf) { g.Cb = static_cast<bf16*>(L->sdUB); g.ldcb = r; }
+        else { g.C = static_cast<float*>(L->sdUB); g.ldc = r; }
+        gemm_run(ctx, g, "lin_bwd_dub");
+    }
+    // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
+    //    of the same GEMM (they share the W^T tiles)
+    if (dX) {
+        GemmDesc g;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(W->type, true);
+        g.A = L->dU; g.lda = out; g.B = W->wt; g.ldb = out; g.Bs = W->wts; g.ldbs = out;
+        g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
+        g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
+        g.C = dX; g.ldc = in; g.accumulate = dx_acc;
+        if (L->dora) {
+            g.Mx = r; g.Ax = L->Ax; g.ldax = out; g.A2x = L->A2x; g.lda2x = r;
+            g.Cx = dA; g.ldcx = in; g.accumulate_x = 1;
+        }
+        gemm_run(ctx, g, "lin_bwd_dx");
+    } else if (L->dora) {
+        GemmDesc g;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(W->type, true);
+        g.A = L->Ax; g.lda = out; g.B = W->wt; g.ldb = out; g.Bs = W->wts; g.ldbs = out;
+        g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
+        g.M = r; g.N = in; g.K = out; g.alpha = 1.0f;
+        g.C = dA; g.ldc = in; g.accumulate = 1;
+        gemm_run(ctx, g, "lin_bwd_dora_da");
+    }
+    // 4. dA += sdUB^T X
+    {
+        const int S = choose_splits(in, N);
+        const int64_t rows_per = ceil_div(N, S);
+        SA3K_REQUIRE((size_t)S * R * in <= L->part_elems, "column-reduction scratch too small");
+        dim3 grid((unsigned)ceil_div(in, kThreads), (unsigned)S);
+        {
+            KernelScope ks(ctx, "lin_bwd_colred_x");
+            if (x_src == SRC_F32)
+                colred_x_kernel<float, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), L->part, N, in, r, rows_per);
+            else
+                colred_x_kernel<bf16, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const bf16*>(X), static_cast<const CT*>(L->sdUB), L->part, N, in, r, rows_per);
+            SA3K_LAUNCHED();
+        }
+        KernelScope ks(ctx, "lin_bwd_reduce");
+        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
+            L->part, (int64_t)R * in, S, (int64_t)r * in, dA, 1);
+        SA3K_LAUNCHED();
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------ C ABI
+extern "C" {
+
+SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out, const void* data,
+                                int data_on_device, sa3k_weight** out_w) {
+    return sa3k_guard(ctx, "sa3k_weight_create", [&] {
+        SA3K_REQUIRE(out_w && data, "null pointer");
+        *out_w = nullptr;
+        SA3K_REQUIRE(in > 0 && out > 0, "weight extents must be positive");
+        SA3K_REQUIRE(type == SA3K_TYPE_F32 || type == SA3K_TYPE_F16 || type == SA3K_TYPE_BF16 ||
+                     type == SA3K_TYPE_Q8_0, "unsupported weight type");
+        SA3K_REQUIRE(in % 64 == 0, "weight input dimension must be a multiple of 64");
+        SA3K_REQUIRE(type != SA3K_TYPE_Q8_0 || out % 32 == 0, "Q8_0 output dimension must be a multiple of 32");
+        SA3K_REQUIRE(out % 8 == 0, "weight output dimension must be a multiple of 8");
+        sa3k_weight* w = new sa3k_weight();
+        w->type = type; w->in = in; w->out = out;
+        try {
+            const int64_t n = in * out;
+            const size_t raw_bytes = type == SA3K_TYPE_Q8_0 ? (size_t)(n / 32) * 34 : (size_t)n * type_size(type);
+            const void* src = data;
+            void* staging = nullptr;
+            if (!data_on_device) {
+                SA3K_HIP(hipMalloc(&staging, raw_bytes));
+                SA3K_HIP(hipMemcpyAsync(staging, data, raw_bytes, hipMemcpyHostToDevice, ctx->stream));
+                src = staging;
+            }
+            if (type == SA3K_TYPE_Q8_0) {
+                w->w = dev_alloc<int8_t>(n);
+                w->ws = dev_alloc<uint16_t>(n / 32);
+                w->wt = dev_alloc<int8_t>(n);
+                w->wts = dev_alloc<uint16_t>(n / 32);
+                q8_split_kernel<<<(unsigned)ceil_div(n / 32, kThreads), kThreads, 0, ctx->stream>>>(
+                    static_cast<const uint16_t*>(src), static_cast<int8_t*>(w->w), static_cast<uint16_t*>(w->ws), n / 32);
+                SA3K_LAUNCHED();
+                transpose<int8_t>(ctx, static_cast<int8_t*>(w->w), static_cast<int8_t*>(w->wt), out, in);
+                transpose<uint16_t>(ctx, static_cast<uint16_t*>(w->ws), static_cast<uint16_t*>(w->wts), out, in / 32);
+            } else {
+                const size_t es = type_size(type);
+                SA3K_HIP(hipMalloc(&w->w, (size_t)n * es));
+                SA3K_HIP(hipMalloc(&w->wt, (size_t)n * es));
+                SA3K_HIP(hipMemcpyAsync(w->w, src, (size_t)n * es, hipMemcpyDeviceToDevice, ctx->stream));
+                if (es == 4) transpose<uint32_t>(ctx, static_cast<uint32_t*>(w->w), static_cast<uint32_t*>(w->wt), out, in);
+                else transpose<uint16_t>(ctx, static_cast<uint16_t*>(w->w), static_cast<uint16_t*>(w->wt), out, in);
+            }
+            SA3K_HIP(hipStreamSynchronize(ctx->stream));
+            if (staging) SA3K_HIP(hipFree(staging));
+        } catch (...) {
+            free_weight(w);
+            throw;
+        }
+        *out_w = w;
+    });
+}
+
+SA3K_API int sa3k_weight_destroy(sa3k_ctx* ctx, sa3k_weight* w) {
+    return sa3k_guard(ctx, "sa3k_weight_destroy", [&] {
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        free_weight(w);
+    });
+}
+
+SA3K_API int sa3k_weight_row_norm_sq(sa3k_ctx* ctx, const sa3k_weight* w, float eps, float* nsq) {
+    return sa3k_guard(ctx, "sa3k_weight_row_norm_sq", [&] {
+        SA3K_REQUIRE(w && nsq, "null pointer");
+        KernelScope ks(ctx, "weight_row_norm");
+        row_norm_kernel<<<(unsigned)w->out, kThreads, 0, ctx->stream>>>(*w, eps, 0, nsq);
+        SA3K_LAUNCHED();
+    });
+}
+
+SA3K_API int sa3k_weight_row_norms(sa3k_ctx* ctx, const sa3k_weight* w, float* norms) {
+    return sa3k_guard(ctx, "sa3k_weight_row_norms", [&] {
+        SA3K_REQUIRE(w && norms, "null pointer");
+        KernelScope ks(ctx, "weight_row_norm");
+        row_norm_kernel<<<(unsigned)w->out, kThreads, 0, ctx->stream>>>(*w, 0.0f, 1, norms);
+        SA3K_LAUNCHED();
+    });
+}
+
+SA3K_API int sa3k_lin_create(sa3k_ctx* ctx, const sa3k_weight* W, int rank, int prec, int64_t max_tokens,
+                             sa3k_lin** out_l) {
+    return sa3k_guard(ctx, "sa3k_lin_create", [&] {
+        SA3K_REQUIRE(W && out_l, "null pointer");
+        *out_l = nullptr;
+        SA3K_REQUIRE(rank >= 0 && rank <= 32 && rank % 8 == 0, "rank must be 0, 8, 16, 24 or 32");
+        SA3K_REQUIRE(prec == SA3K_PREC_BF16 || prec == SA3K_PREC_F32, "unknown precision");
+        SA3K_REQUIRE(prec == SA3K_PREC_BF16 || W->type == SA3K_TYPE_F32 || W->type == SA3K_TYPE_F16,
+                     "f32 precision needs an f32 or f16 weight");
+        SA3K_REQUIRE(prec == SA3K_PREC_BF16 || rank % 4 == 0, "rank");
+        SA3K_REQUIRE(max_tokens > 0, "max_tokens must be positive");
+        sa3k_lin* L = new sa3k_lin();
+        L->W = W; L->rank = rank; L->prec = prec; L->max_tokens = max_tokens;
+        L->ct = prec == SA3K_PREC_BF16 ? 2 : 4;
+        try {
+            const int64_t in = W->in, out = W->out, r = std::max(rank, 1);
+            auto ct_alloc = [&](int64_t n) { void* p = nullptr; SA3K_HIP(hipMalloc(&p, (size_t)std::max<int64_t>(n, 1) * L->ct)); return p; };
+            L->Ac = ct_alloc(r * in); L->At = ct_alloc(r * in);
+            L->Bc = ct_alloc(r * out); L->Bt = ct_alloc(r * out);
+            L->Pt = dev_alloc<float>(r * out); L->G = dev_alloc<float>(r * r); L->BG = dev_alloc<float>(r * out);
+            L->nsq = dev_alloc<float>(out); L->d = dev_alloc<float>(out);
+            L->Hc = ct_alloc(max_tokens * r); L->U = ct_alloc(max_tokens * out);
+            L->dU = ct_alloc(max_tokens * out); L->sdUB = ct_alloc(max_tokens * r);
+            L->gd = dev_alloc<float>(out); L->gn = dev_alloc<float>(out);
+            L->Ax = ct_alloc(r * out); L->A2x = ct_alloc(r * r);
+            L->part_elems = std::max((size_t)choose_splits(out, max_tokens) * 33 * out,
+                                     (size_t)choose_splits(in, max_tokens) * 32 * in);
+            L->part = dev_alloc<float>(L->part_elems);
+            L->red = dev_alloc<float>(33 * out);
+        } catch (...) {
+            free_lin(L);
+            throw;
+        }
+        *out_l = L;
+    });
+}
+
+SA3K_API int sa3k_lin_destroy(sa3k_ctx* ctx, sa3k_lin* L) {
+    return sa3k_guard(ctx, "sa3k_lin_destroy", [&] {
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        free_lin(L);
+    });
+}
+
+SA3K_API int sa3k_lin_prepare(sa3k_ctx* ctx, sa3k_lin* L, const float* A, const float* B, float scale, int dora,
+                              const float* magnitude, const float* base_norm_sq) {
+    return sa3k_guard(ctx, "sa3k_lin_prepare", [&] {
+        SA3K_REQUIRE(L != nullptr, "null linear");
+        const int64_t in = L->W->in, out = L->W->out;
+        const int r = L->rank;
+        L->s = scale;
+        L->dora = dora ? 1 : 0;
+        L->B = B;
+        L->mag = magnitude;
+        if (r == 0) {
+            SA3K_REQUIRE(!dora, "dora needs a rank > 0 adapter");
+            return;
+        }
+        SA3K_REQUIRE(A && B, "adapter A/B are null");
+        SA3K_REQUIRE(!dora || (magnitude && base_norm_sq), "dora needs magnitude and base_norm_sq");
+        const bool bf = L->prec == SA3K_PREC_BF16;
+        KernelScope ks(ctx, "lin_prepare");
+        auto cvt = [&](const float* src, void* dst, int64_t n) {
+            if (bf) cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(src, static_cast<bf16*>(dst), n, 1.0f);
+            else cvt_kernel<float><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(src, static_cast<float*>(dst), n, 1.0f);
+            SA3K_LAUNCHED();
+        };
+        auto cvt_t = [&](const float* src, void* dst, int64_t rows, int64_t cols) {
+            const int64_t n = rows * cols;
+            if (bf) cvt_t_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(src, static_cast<bf16*>(dst), rows, cols);
+            else cvt_t_kernel<float><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(src, static_cast<float*>(dst), rows, cols);
+            SA3K_LAUNCHED();
+        };
+        cvt(A, L->Ac, (int64_t)r * in);
+        cvt_t(A, L->At, r, in);
+        cvt(B, L->Bc, (int64_t)out * r);
+        cvt_t(B, L->Bt, out, r);
+        if (!dora) return;
+        // P^T = A W^T  [r][out]: streams W once through the forward weight loader
+        GemmDesc g;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(L->W->type, false);
+        g.A = L->Ac; g.lda = in; g.B = L->W->w; g.ldb = in; g.Bs = L->W->ws; g.ldbs = in / 32;
+        g.M = r; g.N = out; g.K = in; g.C = L->Pt; g.ldc = out;
+        gemm_run(ctx, g, "lin_prepare_p");
+        gram_kernel<<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(A, in, r, L->G);
+        SA3K_LAUNCHED();
+        dora_terms_kernel<<<(unsigned)ceil_div(out, kThreads), kThreads, 0, ctx->stream>>>(
+            L->Pt, B, L->G, base_norm_sq, magnitude, out, r, scale, L->BG, L->nsq, L->d);
+        SA3K_LAUNCHED();
+    });
+}
+
+SA3K_API int sa3k_lin_forward(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, const float* bias,
+                              float* Y) {
+    return sa3k_guard(ctx, "sa3k_lin_forward", [&] {
+        SA3K_REQUIRE(L && X && Y, "null pointer");
+        SA3K_REQUIRE(N > 0 && N <= L->max_tokens, "token count exceeds the linear's max_tokens");
+        SA3K_REQUIRE(x_type == SA3K_TYPE_F32 || (x_type == SA3K_TYPE_BF16 && L->prec == SA3K_PREC_BF16),
+                     "activation type must be f32 (or bf16 with bf16 precision)");
+        const int xs = x_type == SA3K_TYPE_F32 ? SRC_F32 : SRC_BF16;
+        if (L->prec == SA3K_PREC_BF16) lin_forward_t<bf16>(ctx, L, xs, X, N, bias, Y);
+        else lin_forward_t<float>(ctx, L, xs, X, N, bias, Y);
+    });
+}
+
+SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, const float* dY,
+                               float* dX, int dx_accumulate, float* dA, float* dB, float* dm) {
+    return sa3k_guard(ctx, "sa3k_lin_backward", [&] {
+        SA3K_REQUIRE(L && X && dY, "null pointer");
+        SA3K_REQUIRE(N == L->saved_tokens, "backward must follow a forward over the same tokens");
+        SA3K_REQUIRE(L->rank > 0 && dA && dB, "adapter gradients need a rank > 0 adapter and dA/dB buffers");
+        SA3K_REQUIRE(!L->dora || dm, "dora needs a magnitude gradient buffer");
+        SA3K_REQUIRE(x_type == SA3K_TYPE_F32 || (x_type == SA3K_TYPE_BF16 && L->prec == SA3K_PREC_BF16),
+                     "activation type must be f32 (or bf16 with bf16 precision)");
+        const int xs = x_type == SA3K_TYPE_F32 ? SRC_F32 : SRC_BF16;
+        const int r = L->rank;
+        if (L->prec == SA3K_PREC_BF16) {
+            if (r <= 16) lin_backward_t<bf16, 16>(ctx, L, xs, X, N, dY, dX, dx_accumulate, dA, dB, dm);
+            else lin_backward_t<bf16, 32>(ctx, L, xs, X, N, dY, dX, dx_accumulate, dA, dB, dm);
+        } else {
+            if (r <= 16) lin_backward_t<float, 16>(ctx, L, xs, X, N, dY, dX, dx_accumulate, dA, dB, dm);
+            else lin_backward_t<float, 32>(ctx, L, xs, X, N, dY, dX, dx_accumulate, dA, dB, dm);
+        }
+    });
+}
+
+}  // extern "C"

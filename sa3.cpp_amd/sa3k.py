@@ -53,6 +53,16 @@ def _declare(lib):
         "sa3k_adamw_clip_scale": (I, [P, C.POINTER(D), C.POINTER(F)]),
         "sa3k_q8_0_dequant": (I, [P, P, P, I64]),
         "sa3k_q8_0_quantize": (I, [P, P, P, I64]),
+        "sa3k_gemm_nt": (I, [P, I, I, P, I64, I, P, I64, P, I64, I64, I64, I64, F, P, P, P, I64, I]),
+        "sa3k_weight_create": (I, [P, I, I64, I64, P, I, C.POINTER(P)]),
+        "sa3k_weight_destroy": (I, [P, P]),
+        "sa3k_weight_row_norm_sq": (I, [P, P, F, P]),
+        "sa3k_weight_row_norms": (I, [P, P, P]),
+        "sa3k_lin_create": (I, [P, P, I, I, I64, C.POINTER(P)]),
+        "sa3k_lin_destroy": (I, [P, P]),
+        "sa3k_lin_prepare": (I, [P, P, P, P, F, I, P, P]),
+        "sa3k_lin_forward": (I, [P, P, I, P, I64, P, P]),
+        "sa3k_lin_backward": (I, [P, P, I, P, I64, P, P, I, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -216,3 +226,75 @@ class Context:
 
     def q8_0_quantize(self, x, blocks, n):
         self.check(self.lib.sa3k_q8_0_quantize(self.h, x.ptr, blocks.ptr, int(n)))
+
+    # -- GEMM
+    def gemm_nt(self, A, B, M, N, K, prec=PREC_BF16, a_type=TYPE_F32, b_type=TYPE_F32, lda=None, ldb=None,
+                B_scales=None, ldbs=0, alpha=1.0, colscale=None, bias=None, C=None, ldc=None, accumulate=False):
+        self.check(self.lib.sa3k_gemm_nt(
+            self.h, prec, a_type, A.ptr, lda if lda is not None else K, b_type, B.ptr,
+            ldb if ldb is not None else K, B_scales.ptr if B_scales is not None else None, ldbs,
+            M, N, K, alpha, colscale.ptr if colscale is not None else None,
+            bias.ptr if bias is not None else None, C.ptr, ldc if ldc is not None else N, int(accumulate)))
+
+    # -- weights and adapted linears
+    def weight(self, W, wtype=TYPE_F32):
+        """W: numpy [out][in] f32 / f16 / bf16-as-uint16 array, or (blocks uint8, in, out) for Q8_0"""
+        if wtype == TYPE_Q8_0:
+            blocks, in_, out_ = W
+            data = np.ascontiguousarray(blocks, np.uint8)
+        else:
+            data = np.ascontiguousarray(W)
+            out_, in_ = data.shape
+        h = C.c_void_p()
+        self.check(self.lib.sa3k_weight_create(self.h, wtype, in_, out_, data.ctypes.data, 0, C.byref(h)))
+        return Weight(self, h.value, in_, out_, wtype)
+
+    def lin(self, weight, rank, prec, max_tokens):
+        h = C.c_void_p()
+        self.check(self.lib.sa3k_lin_create(self.h, weight.h, rank, prec, max_tokens, C.byref(h)))
+        return Lin(self, h.value, weight, rank, prec)
+
+
+class Weight:
+    def __init__(self, ctx, h, in_, out_, wtype):
+        self.ctx, self.h, self.in_, self.out_, self.wtype = ctx, h, in_, out_, wtype
+
+    def row_norm_sq(self, eps=1e-12):
+        y = self.ctx.empty(self.out_)
+        self.ctx.check(self.ctx.lib.sa3k_weight_row_norm_sq(self.ctx.h, self.h, eps, y.ptr))
+        return y
+
+    def row_norms(self):
+        y = self.ctx.empty(self.out_)
+        self.ctx.check(self.ctx.lib.sa3k_weight_row_norms(self.ctx.h, self.h, y.ptr))
+        return y
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_weight_destroy(self.ctx.h, self.h))
+            self.h = None
+
+
+class Lin:
+    def __init__(self, ctx, h, weight, rank, prec):
+        self.ctx, self.h, self.weight, self.rank, self.prec = ctx, h, weight, rank, prec
+
+    def prepare(self, A, B, scale, dora=False, mag=None, bnsq=None):
+        self.ctx.check(self.ctx.lib.sa3k_lin_prepare(self.ctx.h, self.h, A.ptr if A is not None else None,
+                                                     B.ptr if B is not None else None, scale, int(dora),
+                                                     mag.ptr if mag is not None else None,
+                                                     bnsq.ptr if bnsq is not None else None))
+
+    def forward(self, X, N, Y, bias=None, x_type=TYPE_F32):
+        self.ctx.check(self.ctx.lib.sa3k_lin_forward(self.ctx.h, self.h, x_type, X.ptr, N,
+                                                     bias.ptr if bias is not None else None, Y.ptr))
+
+    def backward(self, X, N, dY, dX, dA, dB, dm=None, dx_accumulate=False, x_type=TYPE_F32):
+        self.ctx.check(self.ctx.lib.sa3k_lin_backward(self.ctx.h, self.h, x_type, X.ptr, N, dY.ptr,
+                                                      dX.ptr if dX is not None else None, int(dx_accumulate),
+                                                      dA.ptr, dB.ptr, dm.ptr if dm is not None else None))
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_lin_destroy(self.ctx.h, self.h))
+            self.h = None

@@ -55,6 +55,26 @@ def max_rel_err(a, b, floor_frac=1e-3):
     return float(np.max(np.abs(a - b) / (np.abs(b) + floor + 1e-300))) if b.size else 0.0
 
 
+def bf16_round(x):
+    """float32 -> nearest-even bfloat16, returned as float32 (finite inputs)"""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u >> 16) & 1) + 0x7FFF
+    return ((u + r) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+def bf16_bits(x):
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def q8_0_split(blocks, out_, in_):
+    """raw Q8_0 blocks of W [out][in] -> (quants int8 [out][in], f16 scale bits [out][in/32], decoded f32)"""
+    b = np.asarray(blocks, np.uint8).reshape(out_, in_ // 32, 34)
+    sc = b[:, :, 0:2].copy().view(np.uint16).reshape(out_, in_ // 32)
+    q = b[:, :, 2:].copy().view(np.int8).reshape(out_, in_)
+    dec = (sc.view(np.float16).astype(np.float32).repeat(32, axis=1) * q.astype(np.float32)).astype(np.float32)
+    return q, sc, dec
+
+
 def cosine(a, b):
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

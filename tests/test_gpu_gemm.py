@@ -1,0 +1,105 @@
+"""K1/K2 MFMA GEMM on the GPU vs float64 products of the same (rounded) operands.
+
+bf16 compute: operands are rounded to bf16 by the kernel's loader, so the reference multiplies the
+bf16-rounded values in float64; what remains is fp32 accumulation error (<= 1e-5 normwise).
+f32 compute (v_mfma_f32_16x16x4_f32): reference is the float64 product of the f32 operands.
+"""
+import numpy as np
+import pytest
+
+from conftest import bf16_bits, bf16_round, oracle, q8_0_split, rel_err, rng, sa3k
+
+pytestmark = pytest.mark.gpu
+
+
+def run(ctx, A, Bop, M, N, K, prec, a_type, b_type, B_scales=None, ldbs=0, **kw):
+    dA = ctx.upload(A)
+    dB = ctx.upload(Bop)
+    dS = ctx.upload(B_scales) if B_scales is not None else None
+    colscale = kw.pop("colscale", None)
+    bias = kw.pop("bias", None)
+    c0 = kw.pop("c0", None)
+    dC = ctx.upload(c0) if c0 is not None else ctx.zeros((M, N))
+    ctx.gemm_nt(dA, dB, M, N, K, prec=prec, a_type=a_type, b_type=b_type, B_scales=dS, ldbs=ldbs,
+                colscale=ctx.upload(colscale) if colscale is not None else None,
+                bias=ctx.upload(bias) if bias is not None else None, C=dC, **kw)
+    return dC.numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 96, 192), (2048, 1536, 1536), (37, 20, 128),
+                                   (16, 640, 256), (300, 64, 1024)])
+@pytest.mark.parametrize("btype", ["f32", "f16", "bf16"])
+def test_gemm_bf16(ctx, M, N, K, btype):
+    r = rng(M * 7 + N)
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    if btype == "f32":
+        Bop, bt, Wd = W, sa3k.TYPE_F32, W
+    elif btype == "f16":
+        Bop = W.astype(np.float16)
+        bt, Wd = sa3k.TYPE_F16, Bop.astype(np.float32)
+    else:
+        Bop, bt, Wd = bf16_bits(W), sa3k.TYPE_BF16, bf16_round(W)
+    got = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_F32, bt)
+    ref = bf16_round(A).astype(np.float64) @ bf16_round(Wd).astype(np.float64).T
+    assert rel_err(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 384, 1536), (100, 6144, 1536), (2048, 1536, 6144)])
+def test_gemm_q8_0(ctx, M, N, K):
+    r = rng(N)
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    q, sc, dec = q8_0_split(oracle.q8_0_quantize(W), N, K)
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    got = run(ctx, A, q, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_F32, sa3k.TYPE_Q8_0, B_scales=sc, ldbs=K // 32)
+    ref = bf16_round(A).astype(np.float64) @ bf16_round(dec).astype(np.float64).T
+    assert rel_err(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,out_,in_", [(128, 256, 128), (2048, 6144, 1536), (77, 1536, 512)])
+def test_gemm_q8_0_transposed(ctx, M, out_, in_):
+    # dX = dU . W with W Q8_0 [out][in]: B operand rows are the `in` index, K is `out`
+    r = rng(in_)
+    W = r.normal(0, 0.02, (out_, in_)).astype(np.float32)
+    q, sc, dec = q8_0_split(oracle.q8_0_quantize(W), out_, in_)
+    qT = np.ascontiguousarray(q.T)                      # [in][out]
+    scT = np.ascontiguousarray(sc.T)                    # [in/32][out]
+    dU = r.normal(0, 1e-2, (M, out_)).astype(np.float32)
+    got = run(ctx, dU, qT, M, in_, out_, sa3k.PREC_BF16, sa3k.TYPE_F32, -8, B_scales=scT, ldbs=out_)
+    ref = bf16_round(dU).astype(np.float64) @ bf16_round(dec).astype(np.float64)
+    assert rel_err(got, ref) < 1e-5
+
+
+def test_gemm_epilogue(ctx):
+    r = rng(11)
+    M, N, K = 300, 200, 256
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    W = r.normal(0, 0.05, (N, K)).astype(np.float32)
+    cs = r.uniform(0.5, 2, N).astype(np.float32)
+    b = r.normal(0, 1, N).astype(np.float32)
+    c0 = r.normal(0, 1, (M, N)).astype(np.float32)
+    got = run(ctx, A, W, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_F32, sa3k.TYPE_F32, alpha=0.5, colscale=cs,
+              bias=b, c0=c0, accumulate=True)
+    ref = c0 + (0.5 * (bf16_round(A).astype(np.float64) @ bf16_round(W).astype(np.float64).T)) * cs + b
+    assert rel_err(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 1536, 1536), (130, 40, 96), (64, 16, 1536)])
+@pytest.mark.parametrize("btype", ["f32", "f16"])
+def test_gemm_f32(ctx, M, N, K, btype):
+    r = rng(M + N + K)
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    if btype == "f16":
+        Bop, bt, Wd = W.astype(np.float16), sa3k.TYPE_F16, W.astype(np.float16).astype(np.float32)
+    else:
+        Bop, bt, Wd = W, sa3k.TYPE_F32, W
+    got = run(ctx, A, Bop, M, N, K, sa3k.PREC_F32, sa3k.TYPE_F32, bt)
+    ref = A.astype(np.float64) @ Wd.astype(np.float64).T
+    assert rel_err(got, ref) < 2e-6
+
+
+def test_gemm_rejects_bad_shapes(ctx):
+    a = ctx.zeros((64, 100))
+    with pytest.raises(sa3k.Sa3kError):
+        ctx.gemm_nt(a, a, 64, 64, 100, C=ctx.zeros((64, 64)))   # K not a multiple of 64

@@ -1,0 +1,143 @@
+"""K1-K4: the functional LoRA/DoRA linear (dit_lin, src/dit.h:92-149) on the GPU vs the oracle.
+
+Configurations:
+  * f32 LoRA linear 2048x1536 -> 1536, rank 16, alpha 16: fp32 MFMA, every output within 1e-4
+    max relative error of the oracle (elementwise, floor 1e-3 * max|ref|);
+  * DoRA linear 1536 -> 6144 over a Q8_0 base, rank 32: bf16 MFMA, outputs within 2e-2 normwise
+    relative error and cosine >= 0.9999 of the oracle run on the exactly decoded Q8_0 weight;
+  * smaller and ragged shapes, f16 and f32 bases, lora and dora, both precisions.
+The oracle is the double-precision restatement in oracle/dit_lin.cpp (pinned in
+tests/test_oracle_dit_lin.py).
+"""
+import numpy as np
+import pytest
+
+from conftest import cosine, max_rel_err, oracle, q8_0_split, rel_err, rng, sa3k
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(seed, N, in_, out_, r, w_sd=0.02, b_sd=0.01):
+    g = rng(seed)
+    X = g.normal(0, 1, (N, in_)).astype(np.float32)
+    dY = g.normal(0, 1e-2, (N, out_)).astype(np.float32)
+    W = g.normal(0, w_sd, (out_, in_)).astype(np.float32)
+    bound = 1.0 / np.sqrt(in_)
+    A = g.uniform(-bound, bound, (r, in_)).astype(np.float32)    # Kaiming-uniform (src/train_lora.h:252-260)
+    B = g.normal(0, b_sd, (out_, r)).astype(np.float32)
+    return X, dY, W, A, B
+
+
+def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1):
+    N, in_ = X.shape
+    out_ = dY.shape[1]
+    r = A.shape[0]
+    w = ctx.weight(Wop, wtype)
+    lin = ctx.lin(w, r, prec, N)
+    dA_, dB_ = ctx.upload(A), ctx.upload(B)
+    dmag = ctx.upload(mag) if dora else None
+    bnsq = w.row_norm_sq(1e-12) if dora else None
+    lin.prepare(dA_, dB_, s, dora, dmag, bnsq)
+    dX_, dY_ = ctx.upload(X), ctx.upload(dY)
+    Y = ctx.empty((N, out_))
+    gX, gA, gB, gm = ctx.empty((N, in_)), ctx.zeros((r, in_)), ctx.zeros((out_, r)), ctx.zeros(out_)
+    for _ in range(reps):
+        lin.forward(dX_, N, Y, bias=ctx.upload(bias) if bias is not None else None)
+        lin.backward(dX_, N, dY_, gX, gA, gB, gm if dora else None)
+    out = dict(Y=Y.numpy(), dX=gX.numpy(), dA=gA.numpy() / reps, dB=gB.numpy() / reps, dm=gm.numpy() / reps,
+               bnsq=bnsq.numpy() if dora else None)
+    lin.destroy()
+    w.destroy()
+    return out
+
+
+def run_oracle(X, dY, Wdec, A, B, s, dora, mag, bias=None):
+    bnsq = oracle.row_norm_sq(Wdec, 1e-12) if dora else None
+    f = oracle.dit_lin_fwd(X, Wdec, A, B, s, dora, mag, bnsq, bias)
+    g = oracle.dit_lin_bwd(X, Wdec, dY, A, B, s, dora, mag, bnsq)
+    return dict(Y=f["Y"], dX=g["dX"], dA=g["dA"], dB=g["dB"], dm=g["dm"], bnsq=bnsq)
+
+
+@pytest.mark.parametrize("N", [256, 2048])
+def test_lora_f32_linear(ctx, N):
+    # single LoRA linear 2048x1536 -> 1536, rank 16, alpha 16 (s = 1), seed 0, f32
+    X, dY, W, A, B = make_inputs(0, N, 1536, 1536, 16)
+    got = run_gpu(ctx, X, dY, W, sa3k.TYPE_F32, A, B, 1.0, False, None, sa3k.PREC_F32)
+    ref = run_oracle(X, dY, W, A, B, 1.0, False, None)
+    for k in ("Y", "dX", "dA", "dB"):
+        assert max_rel_err(got[k], ref[k]) < 1e-4, k
+
+
+@pytest.mark.parametrize("N", [256, 2048])
+def test_dora_q8_0_linear(ctx, N):
+    # DoRA linear 1536 -> 6144, Q8_0 base quantised from N(0, 0.02), rank 32, alpha 32, m = row norms
+    in_, out_, r = 1536, 6144, 32
+    X, dY, W, A, B = make_inputs(1, N, in_, out_, r)
+    blocks = oracle.q8_0_quantize(W)
+    _, _, Wdec = q8_0_split(blocks, out_, in_)
+    mag = oracle.row_norms(Wdec)
+    got = run_gpu(ctx, X, dY, (blocks, in_, out_), sa3k.TYPE_Q8_0, A, B, 1.0, True, mag, sa3k.PREC_BF16)
+    ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
+    np.testing.assert_allclose(got["bnsq"], ref["bnsq"], rtol=1e-6)
+    for k in ("Y", "dX", "dA", "dB", "dm"):
+        assert rel_err(got[k], ref[k]) < 2e-2, k
+        assert cosine(got[k], ref[k]) >= 0.9999, k
+
+
+@pytest.mark.parametrize("prec", [sa3k.PREC_F32, sa3k.PREC_BF16])
+@pytest.mark.parametrize("wt", ["f32", "f16"])
+@pytest.mark.parametrize("dora", [False, True])
+def test_linear_small_shapes(ctx, prec, wt, dora):
+    # ragged token count, non-square, bias on the output
+    N, in_, out_, r = 77, 192, 320, 8
+    X, dY, W, A, B = make_inputs(2, N, in_, out_, r, w_sd=0.1, b_sd=0.05)
+    if wt == "f16":
+        Wop, wtype = W.astype(np.float16), sa3k.TYPE_F16
+        Wdec = Wop.astype(np.float32)
+    else:
+        Wop, wtype, Wdec = W, sa3k.TYPE_F32, W
+    mag = (oracle.row_norms(Wdec) * 1.1 + 0.05).astype(np.float32)
+    bias = rng(3).normal(0, 1, out_).astype(np.float32)
+    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 2.0, dora, mag, prec, bias=bias)
+    ref = run_oracle(X, dY, Wdec, A, B, 2.0, dora, mag, bias)
+    keys = ("Y", "dX", "dA", "dB") + (("dm",) if dora else ())
+    for k in keys:
+        if prec == sa3k.PREC_F32:
+            assert max_rel_err(got[k], ref[k]) < 1e-4, k
+        else:
+            assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
+
+
+def test_gradients_accumulate(ctx):
+    # dA/dB/dm are accumulators: two identical micro-batches give twice the gradient
+    N, in_, out_, r = 64, 128, 256, 16
+    X, dY, W, A, B = make_inputs(4, N, in_, out_, r, w_sd=0.1, b_sd=0.05)
+    mag = oracle.row_norms(W)
+    one = run_gpu(ctx, X, dY, W, sa3k.TYPE_F32, A, B, 1.0, True, mag, sa3k.PREC_F32, reps=1)
+    two = run_gpu(ctx, X, dY, W, sa3k.TYPE_F32, A, B, 1.0, True, mag, sa3k.PREC_F32, reps=2)
+    for k in ("dA", "dB", "dm"):
+        assert max_rel_err(two[k], one[k]) < 1e-5, k
+
+
+def test_row_norms_match_oracle(ctx):
+    g = rng(7)
+    W = g.normal(0, 0.02, (384, 1536)).astype(np.float32)
+    for Wop, wt, Wdec in ((W, sa3k.TYPE_F32, W),
+                          (W.astype(np.float16), sa3k.TYPE_F16, W.astype(np.float16).astype(np.float32))):
+        w = ctx.weight(Wop, wt)
+        np.testing.assert_allclose(w.row_norm_sq(1e-12).numpy(), oracle.row_norm_sq(Wdec, 1e-12), rtol=1e-6)
+        np.testing.assert_allclose(w.row_norms().numpy(), oracle.row_norms(Wdec), rtol=1e-6)
+        w.destroy()
+
+
+def test_lin_rejects_bad_calls(ctx):
+    W = np.zeros((64, 128), np.float32)
+    w = ctx.weight(W, sa3k.TYPE_F32)
+    with pytest.raises(sa3k.Sa3kError):
+        ctx.lin(w, 12, sa3k.PREC_BF16, 16)          # rank must be a multiple of 8
+    lin = ctx.lin(w, 8, sa3k.PREC_BF16, 16)
+    X = ctx.zeros((32, 128))
+    with pytest.raises(sa3k.Sa3kError):
+        lin.forward(X, 32, ctx.empty((32, 64)))     # more tokens than max_tokens
+    lin.destroy()
+    w.destroy()
