@@ -169,6 +169,11 @@ typedef struct sa3k_weight sa3k_weight;
 SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out, const void* data,
                                 int data_on_device, sa3k_weight** out_w);
 SA3K_API int sa3k_weight_destroy(sa3k_ctx* ctx, sa3k_weight* w);
+/* Free the bf16 working copies (forward and transposed) that sa3k_weight_create decodes from an
+ * f16 / f32 / Q8_0 base for the bf16-precision contractions; afterwards those contractions decode
+ * the stored elements or Q8_0 blocks inside the GEMM on their way into LDS (same results, less
+ * memory, slower). No reference counterpart (ggml decodes inside mul_mat, src/dit.h:100-107). */
+SA3K_API int sa3k_weight_drop_working_copy(sa3k_ctx* ctx, sa3k_weight* w);
 /* nsq[o] = (float)(sum_i (double)W[o][i]^2 + in*eps)   (train_row_norm_sq, src/train_lora.h:160-174)
  * norms[o] = (float)sqrt(sum_i (double)W[o][i]^2)       (train_row_norms,   src/train_lora.h:141-155)
  * over the decoded weight; outputs are device [out] f32. */

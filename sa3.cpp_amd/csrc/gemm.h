@@ -72,7 +72,12 @@ struct GemmDesc {
     int accumulate_x = 0;
 };
 
-// Enqueue one GEMM on the context stream (validates shapes, picks the tile configuration).
+// Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile
+// configuration): operands already in the compute type take the DMA-fed kernel (gemm_dma.hip),
+// any other source type the kernel that decodes it on its way into LDS (gemm.hip).
 void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name);
+void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d);
+// split-K partial-sum workspace owned by the context (grows on demand)
+float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);
 
 }  // namespace sa3k

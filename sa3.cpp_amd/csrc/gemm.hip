@@ -30,7 +30,28 @@ struct KParams {
     const void* Ax; int64_t ldax;
     const void* A2x; int64_t lda2x;
     float* Cx; int64_t ldcx; int accumulate_x;
+    float* ws;   // split-K partials [splits][M+Mx][N] (null: no split)
+    int kps;     // K tiles per split
 };
+
+}  // namespace
+
+// split-K workspace owned by the context (grows on demand; kernels on one stream use it in turn)
+float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes) {
+    if (bytes > ctx->gemm_ws_bytes) {
+        if (ctx->gemm_ws) {
+            SA3K_HIP(hipStreamSynchronize(ctx->stream));
+            SA3K_HIP(hipFree(ctx->gemm_ws));
+            ctx->gemm_ws = nullptr;
+            ctx->gemm_ws_bytes = 0;
+        }
+        SA3K_HIP(hipMalloc(&ctx->gemm_ws, bytes));
+        ctx->gemm_ws_bytes = bytes;
+    }
+    return static_cast<float*>(ctx->gemm_ws);
+}
+
+namespace {
 
 __device__ inline uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
@@ -41,28 +62,30 @@ __device__ inline uint4 pack8(const float (&f)[8]) {
     return __builtin_bit_cast(uint4, v);
 }
 
-// 16 bytes of the compute type for row `row`, elements k .. k+CE-1 of a K-contiguous source.
+template <int SRC>
+constexpr int src_bytes() { return SRC == SRC_F32 ? 4 : (SRC == SRC_BF16 || SRC == SRC_F16) ? 2 : 1; }
+
+// 16 bytes of the compute type from element pointer p (CE consecutive K elements of one row) and,
+// for Q8_0 sources, scale pointer s (Q8: the row's f16 scale of this 32-block; Q8T: 8 f16 scales).
 template <int SRC, bool BF16>
-__device__ inline uint4 load_chunk(const void* base, int64_t ld, const void* sc, int64_t lds,
-                                   int64_t row, int64_t k) {
+__device__ inline uint4 load_src(const char* p, const char* s) {
     if constexpr (BF16) {
         if constexpr (SRC == SRC_BF16) {
-            return *reinterpret_cast<const uint4*>(static_cast<const bf16*>(base) + row * ld + k);
+            return *reinterpret_cast<const uint4*>(p);
         } else if constexpr (SRC == SRC_F32) {
-            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + row * ld + k);
-            const float4 a = p[0], b = p[1];
+            const float4* q = reinterpret_cast<const float4*>(p);
+            const float4 a = q[0], b = q[1];
             const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
             return pack8(f);
         } else if constexpr (SRC == SRC_F16) {
-            const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(base) + row * ld + k);
+            const f16x8 h = *reinterpret_cast<const f16x8*>(p);
             float f[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = (float)h[e];
             return pack8(f);
         } else if constexpr (SRC == SRC_Q8) {
-            // quants [row][k], scales [row][k/32]
-            const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(base) + row * ld + k);
-            const float d = (float)static_cast<const _Float16*>(sc)[row * lds + (k >> 5)];
+            const uint2 q = *reinterpret_cast<const uint2*>(p);
+            const float d = (float)*reinterpret_cast<const _Float16*>(s);
             float f[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -70,9 +93,9 @@ __device__ inline uint4 load_chunk(const void* base, int64_t ld, const void* sc,
                 f[4 + e] = d * (float)(int8_t)((q.y >> (8 * e)) & 0xff);
             }
             return pack8(f);
-        } else {  // SRC_Q8T: quants [row][k], scales [row/32][k]
-            const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(base) + row * ld + k);
-            const f16x8 d = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(sc) + (row >> 5) * lds + k);
+        } else {  // SRC_Q8T
+            const uint2 q = *reinterpret_cast<const uint2*>(p);
+            const f16x8 d = *reinterpret_cast<const f16x8*>(s);
             float f[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -83,9 +106,9 @@ __device__ inline uint4 load_chunk(const void* base, int64_t ld, const void* sc,
         }
     } else {
         if constexpr (SRC == SRC_F32) {
-            return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + row * ld + k);
+            return *reinterpret_cast<const uint4*>(p);
         } else {  // SRC_F16
-            const f16x4 h = *reinterpret_cast<const f16x4*>(static_cast<const _Float16*>(base) + row * ld + k);
+            const f16x4 h = *reinterpret_cast<const f16x4*>(p);
             const float4 f = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
             return __builtin_bit_cast(uint4, f);
         }
@@ -132,14 +155,41 @@ __device__ inline void mma_tile(const char* As, const char* Bs, int wm0, int wn0
     }
 }
 
-template <int BM, int BN, int WMW, int ASRC, int BSRC, bool BF16>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(KParams p) {
+// Epilogue of one output element (see gemm.h): rows >= M are the extra rows, stored to Cx.
+__device__ inline void epilogue_elem(const KParams& p, int64_t m, int64_t n, float acc) {
+    float x = p.alpha * acc;
+    if (m >= p.M) {
+        float* cx = p.Cx + (m - p.M) * p.ldcx + n;
+        *cx = p.accumulate_x ? *cx + x : x;
+        return;
+    }
+    if (p.U) p.U[m * p.ldu + n] = x;
+    if (p.Ub) p.Ub[m * p.ldu + n] = (bf16)x;
+    if (p.colscale) x = x * p.colscale[n];
+    if (p.bias) x = x + p.bias[n];
+    if (p.C) {
+        if (p.accumulate) p.C[m * p.ldc + n] += x;
+        else p.C[m * p.ldc + n] = x;
+    }
+    if (p.Cb) p.Cb[m * p.ldcb + n] = (bf16)x;
+}
+
+// Main kernel. Grid: x = output tiles (padded to a multiple of 8, XCD-remapped), y = K splits.
+// Pipeline: K tiles stream through two LDS buffers; global loads run two tiles ahead of the MFMAs
+// in two register staging sets (the loop is unrolled by two so the sets stay in registers).
+template <int BM, int BN, int WMW, int ASRC, int BSRC, bool BF16, int PD>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(KParams p) {
     constexpr int WNW = 4 / WMW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int FM = WTM / 16, FN = WTN / 16;
     constexpr int NA = BM * 8 / kThreads, NB = BN * 8 / kThreads;
     constexpr int BKE = BF16 ? 64 : 32;   // elements per K tile
     constexpr int CE = BF16 ? 8 : 4;      // elements per 16-byte chunk
+    constexpr int CTSRC = BF16 ? SRC_BF16 : SRC_F32;
+    constexpr int CTB = BF16 ? 2 : 4;
+    constexpr int AEB = src_bytes<ASRC>(), BEB = src_bytes<BSRC>();
+    // per-tile byte advance of the B scale pointer: Q8 one f16 per 32 K; Q8T 8 f16 per chunk row
+    constexpr int BSSTR = BSRC == SRC_Q8 ? (BKE / 32) * 2 : BSRC == SRC_Q8T ? BKE * 2 : 0;
     static_assert(NA >= 1 && NB >= 1 && FM >= 1 && FN >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) char lds[2 * (BM + BN) * kRowBytes];
 
@@ -163,43 +213,94 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(KParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave % WMW) * WTM, wn0 = (wave / WMW) * WTN;
 
+    // K range of this split; the second segment (K2) belongs to the last split
+    const int KT = (int)(p.K / BKE);
+    const int z = blockIdx.y;
+    const int kt0 = z * p.kps;
+    const int Tm = max(0, min(KT, kt0 + p.kps) - kt0);
+    const bool ext = p.K2 > 0 && z == (int)gridDim.y - 1;
+    const int T = Tm + (ext ? 1 : 0);
+    const int64_t k0 = (int64_t)kt0 * BKE;
+
+    // per-chunk 32-bit byte offsets at the split's first K tile (kNone = zero chunk); main rows
+    // index A, extra rows (flag bit) index Ax. Scalar bases + vector offsets keep the address
+    // arithmetic out of the loop and the register budget at two waves per SIMD.
+    constexpr uint32_t kNone = 0xffffffffu;
+    uint32_t aoff[NA];
+    uint32_t axmask = 0;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+        const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
+        const int64_t gm = m0 + row;
+        aoff[q] = kNone;
+        if (gm < p.M) {
+            aoff[q] = (uint32_t)((gm * p.lda + k0 + part * CE) * AEB);
+        } else if (gm < Mt) {
+            aoff[q] = (uint32_t)(((gm - p.M) * p.ldax + k0 + part * CE) * CTB);
+            axmask |= 1u << q;
+        }
+    }
+    uint32_t boff[NB], bsoff[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
+        const int64_t gn = n0 + row;
+        boff[q] = kNone;
+        bsoff[q] = 0;
+        if (gn < p.N) {
+            const int64_t k = k0 + part * CE;
+            boff[q] = (uint32_t)((gn * p.ldb + k) * BEB);
+            if constexpr (BSRC == SRC_Q8) bsoff[q] = (uint32_t)((gn * p.ldbs + (k >> 5)) * 2);
+            if constexpr (BSRC == SRC_Q8T) bsoff[q] = (uint32_t)(((gn >> 5) * p.ldbs + k) * 2);
+        }
+    }
+    const char* Ab = static_cast<const char*>(p.A);
+    const char* Axb = static_cast<const char*>(p.Ax);
+    const char* Bb = static_cast<const char*>(p.B);
+    const char* Bsb = static_cast<const char*>(p.Bs);
+
     f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 ra[NA], rb[NB];
-    const int KT = (int)(p.K / BKE);
-    const int T = KT + (p.K2 > 0 ? 1 : 0);
-
-    auto load = [&](int t) {
+    auto load = [&](int t, uint4 (&ra)[NA], uint4 (&rb)[NB]) {
+        if (t < Tm) {
 #pragma unroll
-        for (int q = 0; q < NA; ++q) {
-            const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
-            const int64_t gm = m0 + row;
-            constexpr int CTSRC = BF16 ? SRC_BF16 : SRC_F32;
-            if (gm < p.M) {
-                if (t < KT) ra[q] = load_chunk<ASRC, BF16>(p.A, p.lda, nullptr, 0, gm, (int64_t)t * BKE + part * CE);
-                else ra[q] = (part * CE < p.K2) ? load_chunk<CTSRC, BF16>(p.A2, p.lda2, nullptr, 0, gm, part * CE) : zero4();
-            } else if (gm < Mt) {
-                const int64_t xr = gm - p.M;
-                if (t < KT) ra[q] = load_chunk<CTSRC, BF16>(p.Ax, p.ldax, nullptr, 0, xr, (int64_t)t * BKE + part * CE);
-                else ra[q] = (part * CE < p.K2) ? load_chunk<CTSRC, BF16>(p.A2x, p.lda2x, nullptr, 0, xr, part * CE) : zero4();
-            } else {
+            for (int q = 0; q < NA; ++q) {
+                if (aoff[q] == kNone) ra[q] = zero4();
+                else if (axmask & (1u << q)) ra[q] = load_src<CTSRC, BF16>(Axb + aoff[q] + t * (BKE * CTB), nullptr);
+                else ra[q] = load_src<ASRC, BF16>(Ab + aoff[q] + t * (BKE * AEB), nullptr);
+            }
+#pragma unroll
+            for (int q = 0; q < NB; ++q)
+                rb[q] = boff[q] != kNone ? load_src<BSRC, BF16>(Bb + boff[q] + t * (BKE * BEB), Bsb + bsoff[q] + t * BSSTR)
+                                         : zero4();
+        } else {  // the second segment: one tile of K2 <= BKE elements
+#pragma unroll
+            for (int q = 0; q < NA; ++q) {
+                const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
+                const int64_t gm = m0 + row;
                 ra[q] = zero4();
+                if (part * CE < p.K2) {
+                    if (gm < p.M)
+                        ra[q] = load_src<CTSRC, BF16>(static_cast<const char*>(p.A2) + (gm * p.lda2 + part * CE) * CTB, nullptr);
+                    else if (gm < Mt)
+                        ra[q] = load_src<CTSRC, BF16>(static_cast<const char*>(p.A2x) + ((gm - p.M) * p.lda2x + part * CE) * CTB, nullptr);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < NB; ++q) {
+                const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
+                const int64_t gn = n0 + row;
+                rb[q] = (gn < p.N && part * CE < p.K2)
+                            ? load_src<CTSRC, BF16>(static_cast<const char*>(p.B2) + (gn * p.ldb2 + part * CE) * CTB, nullptr)
+                            : zero4();
             }
         }
-#pragma unroll
-        for (int q = 0; q < NB; ++q) {
-            const int c = tid + q * kThreads, row = c >> 3, part = c & 7;
-            const int64_t gn = n0 + row;
-            if (gn >= p.N) rb[q] = zero4();
-            else if (t < KT) rb[q] = load_chunk<BSRC, BF16>(p.B, p.ldb, p.Bs, p.ldbs, gn, (int64_t)t * BKE + part * CE);
-            else rb[q] = (part * CE < p.K2) ? load_chunk<BF16 ? SRC_BF16 : SRC_F32, BF16>(p.B2, p.ldb2, nullptr, 0, gn, part * CE) : zero4();
-        }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, const uint4 (&ra)[NA], const uint4 (&rb)[NB]) {
         char* base = lds + buf * (BM + BN) * kRowBytes;
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
@@ -212,60 +313,111 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(KParams p) {
             *reinterpret_cast<uint4*>(base + (BM + (c >> 3)) * kRowBytes + (c & 7) * 16) = rb[q];
         }
     };
-
-    if (T > 0) {
-        load(0);
-        store(0);
-    }
-    __syncthreads();
-    for (int t = 0; t < T; ++t) {
-        if (t + 1 < T) load(t + 1);
-        const char* base = lds + (t & 1) * (BM + BN) * kRowBytes;
+    auto compute = [&](int buf) {
+        const char* base = lds + buf * (BM + BN) * kRowBytes;
         mma_tile<FM, FN, BF16>(base, base + BM * kRowBytes, wm0, wn0, lane, acc);
-        if (t + 1 < T) store((t + 1) & 1);
+    };
+
+    if constexpr (PD == 2) {
+        uint4 ra0[NA], rb0[NB], ra1[NA], rb1[NB];
+        if (T > 0) load(0, ra0, rb0);
+        if (T > 1) load(1, ra1, rb1);
+        if (T > 0) store(0, ra0, rb0);
         __syncthreads();
+        if (T > 2) load(2, ra0, rb0);
+        for (int t = 0; t < T; t += 2) {
+            // tile t in LDS buffer 0; tile t+1 in ra1/rb1; tile t+2 in flight into ra0/rb0
+            compute(0);
+            if (t + 1 < T) store(1, ra1, rb1);
+            __syncthreads();
+            if (t + 3 < T) load(t + 3, ra1, rb1);
+            if (t + 1 >= T) break;
+            compute(1);
+            if (t + 2 < T) store(0, ra0, rb0);
+            __syncthreads();
+            if (t + 4 < T) load(t + 4, ra0, rb0);
+        }
+    } else {
+        // one tile of register prefetch: load t+1 while the MFMAs consume tile t
+        uint4 ra[NA], rb[NB];
+        if (T > 0) {
+            load(0, ra, rb);
+            store(0, ra, rb);
+        }
+        __syncthreads();
+        for (int t = 0; t < T; ++t) {
+            if (t + 1 < T) load(t + 1, ra, rb);
+            compute(t & 1);
+            if (t + 1 < T) store((t + 1) & 1, ra, rb);
+            __syncthreads();
+        }
     }
 
-    // epilogue: lane holds rows 4*(lane/16)+v, column lane%16 of each 16x16 block
+    // lane holds rows 4*(lane/16)+v, column lane%16 of each 16x16 block
+    if (p.ws) {  // split-K partial sums, reduced (and epilogued) by gemm_splitk_reduce
+        float* w = p.ws + (int64_t)z * Mt * p.N;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t n = n0 + wn0 + 16 * j + (lane & 15);
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int64_t m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + v;
+                    if (m < Mt) w[m * p.N + n] = acc[i][j][v];
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int64_t n = n0 + wn0 + 16 * j + (lane & 15);
         if (n >= p.N) continue;
-        const float cs = p.colscale ? p.colscale[n] : 1.0f;
-        const float bi = p.bias ? p.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int64_t m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + v;
-                if (m >= p.M) {
-                    if (m < Mt) {
-                        float* cx = p.Cx + (m - p.M) * p.ldcx + n;
-                        const float x = p.alpha * acc[i][j][v];
-                        *cx = p.accumulate_x ? *cx + x : x;
-                    }
-                    continue;
-                }
-                float x = p.alpha * acc[i][j][v];
-                if (p.U) p.U[m * p.ldu + n] = x;
-                if (p.Ub) p.Ub[m * p.ldu + n] = (bf16)x;
-                if (p.colscale) x = x * cs;
-                if (p.bias) x = x + bi;
-                if (p.C) {
-                    if (p.accumulate) p.C[m * p.ldc + n] += x;
-                    else p.C[m * p.ldc + n] = x;
-                }
-                if (p.Cb) p.Cb[m * p.ldcb + n] = (bf16)x;
+                if (m < Mt) epilogue_elem(p, m, n, acc[i][j][v]);
             }
-        }
     }
 }
 
+// sum of the split partials in split order (deterministic), then the epilogue
+__global__ __launch_bounds__(kThreads) void gemm_splitk_reduce(KParams p, int splits) {
+    const int64_t Mt = p.M + p.Mx;
+    const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= Mt * p.N) return;
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += p.ws[(int64_t)z * Mt * p.N + idx];
+    const int64_t m = idx / p.N, n = idx - m * p.N;
+    epilogue_elem(p, m, n, s);
+}
+
 template <int BM, int BN, int WMW, int ASRC, int BSRC, bool BF16>
-void launch(sa3k_ctx* ctx, const KParams& p) {
+void launch(sa3k_ctx* ctx, KParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.N, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
-    gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16><<<(unsigned)grid, kThreads, 0, ctx->stream>>>(p);
+    const int KT = (int)(p.K / (BF16 ? 64 : 32));
+    // split K when the output tiles cannot fill the chip twice over (2 workgroups per CU resident)
+    int splits = 1;
+    if (ctx->gemm_split && tiles < 512 && KT >= 8) splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, 512 / tiles)});
+    p.kps = (KT + splits - 1) / std::max(splits, 1);
+    if (p.kps == 0) p.kps = 1;
+    splits = std::max(1, (KT + p.kps - 1) / p.kps);
+    p.ws = nullptr;
+    if (splits > 1) {
+        const size_t need = (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float);
+        p.ws = gemm_workspace_bytes(ctx, need);
+    }
+    dim3 g((unsigned)grid, (unsigned)splits);
+    if (ctx->gemm_pd == 2) gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 2><<<g, kThreads, 0, ctx->stream>>>(p);
+    else gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 1><<<g, kThreads, 0, ctx->stream>>>(p);
+    if (splits > 1) {
+        SA3K_LAUNCHED();
+        gemm_splitk_reduce<<<(unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
+    }
 }
 
 template <int ASRC, int BSRC, bool BF16>
@@ -322,9 +474,18 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     SA3K_REQUIRE(d.Mx >= 0, "negative extra rows");
     SA3K_REQUIRE(d.Mx == 0 || (d.Ax && d.Cx && al16(d.Ax) && (d.K2 == 0 || (d.A2x && al16(d.A2x)))),
                  "GEMM extra rows need Ax, Cx (and A2x with a second segment)");
+    const int ct_src = bf ? SRC_BF16 : SRC_F32;
+    if (d.a_src == ct_src && d.b_src == ct_src && ctx->gemm_dma) {
+        SA3K_REQUIRE((d.ldb * (bf ? 2 : 4)) % 16 == 0 && (d.Mx == 0 || (d.ldax * (bf ? 2 : 4)) % 16 == 0),
+                     "GEMM operand rows must be 16-byte aligned");
+        KernelScope ks(ctx, prof_name);
+        gemm_run_dma(ctx, d);
+        SA3K_LAUNCHED();
+        return;
+    }
     KParams p{d.A, d.lda, d.B, d.ldb, d.Bs, d.ldbs, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K,
               d.alpha, d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
-              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x};
+              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, nullptr, 0};
     KernelScope ks(ctx, prof_name);
     if (bf) {
         if (d.a_src == SRC_BF16) launch_b<SRC_BF16, true>(ctx, p, d.b_src);

@@ -30,6 +30,14 @@ struct sa3k_weight {
     void* ws = nullptr;     // Q8_0: f16 scales [out][in/32]
     void* wt = nullptr;     // transposed [in][out] (Q8_0: int8 quants)
     void* wts = nullptr;    // Q8_0: f16 scales [in/32][out]
+    // bf16 working copies of the decoded weight, [out][in] and [in][out], built at load for every
+    // non-bf16 type: the frozen base is contracted three times per training step (forward,
+    // checkpoint recompute, dX), and the bf16-MFMA kernels round every decoded element to bf16
+    // anyway, so decoding once keeps bit-identical results and takes the per-element decode off
+    // the GEMM's inner loop. sa3k_weight_drop_working_copy frees them; the GEMMs then decode the
+    // stored blocks in the global->LDS path instead.
+    void* wb = nullptr;
+    void* wbt = nullptr;
 };
 
 struct sa3k_lin {
@@ -57,6 +65,7 @@ struct sa3k_lin {
     // backward scratch
     void* dU = nullptr;                 // [max_tokens][out] compute type
     void* sdUB = nullptr;               // [max_tokens][r] compute type
+    void* Xb = nullptr;                 // [max_tokens][in] bf16 copy of an f32 input (bf16 precision)
     float* gd = nullptr;                // [out]
     float* gn = nullptr;                // [out]
     void* Ax = nullptr;                 // [r][out] compute type: 2s (B*gn)^T
@@ -130,6 +139,13 @@ __device__ inline float load_w(const sa3k_weight& w, const void* p, const void* 
     }
 }
 
+// decoded bf16 copy of the forward layout (RNE of the exact decoded value)
+__global__ __launch_bounds__(kThreads) void decode_bf16_kernel(sa3k_weight w, bf16* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= w.in * w.out) return;
+    dst[i] = (bf16)load_w(w, w.w, w.ws, i, w.in);
+}
+
 // sum_i W[o][i]^2 in double per row; mode 0: + in*eps (nsq), mode 1: sqrt (norms)
 __global__ __launch_bounds__(kThreads) void row_norm_kernel(sa3k_weight w, float eps, int mode,
                                                             float* __restrict__ out) {
@@ -183,26 +199,41 @@ __global__ __launch_bounds__(kThreads) void gram_kernel(const float* __restrict_
 
 // per output row o: t2 = sum_a P[o][a] B[o][a]; BG[o] = B[o] G; t3 = B[o] . BG[o];
 // nsq = bnsq + 2s t2 + s^2 t3; d = m / sqrt(nsq)
+// One block = 8 output rows; thread (row, a) with a < 32 the rank index; the rank sums are
+// 32-lane shuffles. G and the block's B rows are staged in LDS.
 __global__ __launch_bounds__(kThreads) void dora_terms_kernel(const float* __restrict__ Pt, const float* __restrict__ B,
                                                               const float* __restrict__ G, const float* __restrict__ bnsq,
                                                               const float* __restrict__ mag, int64_t out, int r, float s,
                                                               float* __restrict__ BG, float* __restrict__ nsq,
                                                               float* __restrict__ d) {
-    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (o >= out) return;
-    float b[32];
-    for (int a = 0; a < r; ++a) b[a] = B[o * r + a];
-    float t2 = 0.f, t3 = 0.f;
-    for (int a = 0; a < r; ++a) {
-        t2 += Pt[(int64_t)a * out + o] * b[a];
-        float g = 0.f;
-        for (int c = 0; c < r; ++c) g += b[c] * G[c * r + a];
-        BG[o * r + a] = g;
-        t3 += b[a] * g;
+    __shared__ float gs[32][33];
+    __shared__ float bs[8][32];
+    const int ol = threadIdx.x >> 5, a = threadIdx.x & 31;
+    const int64_t o = (int64_t)blockIdx.x * 8 + ol;
+    for (int k = threadIdx.x; k < 32 * 32; k += kThreads) {
+        const int i = k >> 5, j = k & 31;
+        gs[i][j] = (i < r && j < r) ? G[i * r + j] : 0.f;
     }
-    const float n2 = bnsq[o] + 2.0f * s * t2 + s * s * t3;
-    nsq[o] = n2;
-    d[o] = mag[o] / sqrtf(n2);
+    bs[ol][a] = (o < out && a < r) ? B[o * r + a] : 0.f;
+    __syncthreads();
+    float g = 0.f;
+#pragma unroll 8
+    for (int c = 0; c < 32; ++c) g += bs[ol][c] * gs[c][a];
+    float t2 = 0.f, t3 = 0.f;
+    if (o < out && a < r) {
+        BG[o * r + a] = g;
+        t2 = Pt[(int64_t)a * out + o] * bs[ol][a];
+        t3 = bs[ol][a] * g;
+    }
+    for (int off = 16; off > 0; off >>= 1) {
+        t2 += __shfl_xor(t2, off, 32);
+        t3 += __shfl_xor(t3, off, 32);
+    }
+    if (a == 0 && o < out) {
+        const float n2 = bnsq[o] + 2.0f * s * t2 + s * s * t3;
+        nsq[o] = n2;
+        d[o] = mag[o] / sqrtf(n2);
+    }
 }
 
 // ---------------------------------------------------------------- K3 column reductions
@@ -303,24 +334,27 @@ __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __
                                                                  const float* __restrict__ B, int64_t out, int r, float s,
                                                                  int dora, float* __restrict__ dB, float* __restrict__ dm,
                                                                  float* __restrict__ gn_out, CT* __restrict__ Ax) {
-    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    // thread (row, a): 8 output rows per block, a < 32 the rank index
+    const int ol = threadIdx.x >> 5, a = threadIdx.x & 31;
+    const int64_t o = (int64_t)blockIdx.x * 8 + ol;
     if (o >= out) return;
     float gn = 0.f;
     if (dora) {
         const float n2 = nsq[o], sq = sqrtf(n2);
         const float g = gd[o];
-        if (dm) dm[o] += g / sq;
         gn = -0.5f * g * mag[o] / (n2 * sq);
-        gn_out[o] = gn;
-    }
-    for (int a = 0; a < r; ++a) {
-        float v = redT[(int64_t)a * out + o];
-        if (dora) {
-            v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
-            Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
+        if (a == 0) {
+            if (dm) dm[o] += g / sq;
+            gn_out[o] = gn;
         }
-        dB[o * r + a] += v;
     }
+    if (a >= r) return;
+    float v = redT[(int64_t)a * out + o];
+    if (dora) {
+        v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
+        Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
+    }
+    dB[o * r + a] += v;
 }
 
 // A2x[a][b] = 2 s^2 sum_o B[o][a] gn[o] B[o][b]  (one block per (a,b))
@@ -360,13 +394,13 @@ size_t type_size(int type) {
 
 void free_weight(sa3k_weight* w) {
     if (!w) return;
-    for (void* p : {w->w, w->ws, w->wt, w->wts}) if (p) (void)hipFree(p);
+    for (void* p : {w->w, w->ws, w->wt, w->wts, w->wb, w->wbt}) if (p) (void)hipFree(p);
     delete w;
 }
 
 void free_lin(sa3k_lin* L) {
     if (!L) return;
-    for (void* p : {L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
+    for (void* p : {L->Xb, L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
                     (void*)L->d, L->Hc, L->U, L->dU, L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x,
                     (void*)L->part, (void*)L->red})
         if (p) (void)hipFree(p);
@@ -375,16 +409,40 @@ void free_lin(sa3k_lin* L) {
 
 // row split count for the column reductions: enough blocks to cover the chip
 int choose_splits(int64_t cols, int64_t N) {
+    // about 512 blocks in total, at least 64 rows per split (fewer partial sums to reduce)
     const int64_t col_blocks = ceil_div(cols, kThreads);
-    int64_t S = ceil_div(1024, col_blocks);
-    S = std::max<int64_t>(1, std::min<int64_t>(S, ceil_div(N, 16)));
-    return (int)std::min<int64_t>(S, 128);
+    int64_t S = ceil_div(512, col_blocks);
+    S = std::max<int64_t>(1, std::min<int64_t>(S, ceil_div(N, 64)));
+    return (int)std::min<int64_t>(S, 64);
+}
+
+struct WOp {
+    int src;
+    const void* p;
+    const void* s;
+    int64_t ld, lds;
+};
+
+// B operand of X W^T (transposed = false) or of dU W (transposed = true)
+WOp weight_operand(const sa3k_weight* W, bool bf, bool transposed) {
+    if (bf && W->wb) return transposed ? WOp{SRC_BF16, W->wbt, nullptr, W->out, 0} : WOp{SRC_BF16, W->wb, nullptr, W->in, 0};
+    if (transposed) return WOp{src_of_weight(W->type, true), W->wt, W->wts, W->out, W->out};
+    return WOp{src_of_weight(W->type, false), W->w, W->ws, W->in, W->in / 32};
 }
 
 template <class CT>
 void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* bias, float* Y) {
     const sa3k_weight* W = L->W;
     const bool bf = L->prec == SA3K_PREC_BF16;
+    if (bf && x_src == SRC_F32) {   // one pass to bf16 so both GEMMs stream compute-type operands
+        const int64_t n = N * W->in;
+        KernelScope ks(ctx, "lin_fwd_cvt_x");
+        cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(
+            static_cast<const float*>(X), static_cast<bf16*>(L->Xb), n, 1.0f);
+        SA3K_LAUNCHED();
+        X = L->Xb;
+        x_src = SRC_BF16;
+    }
     // Hc = s X A^T
     if (L->rank > 0) {
         GemmDesc h;
@@ -395,9 +453,10 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
         else { h.C = static_cast<float*>(L->Hc); h.ldc = L->rank; }
         gemm_run(ctx, h, "lin_fwd_h");
     }
+    const WOp wo = weight_operand(W, bf, false);
     GemmDesc g;
-    g.prec = L->prec; g.a_src = x_src; g.b_src = src_of_weight(W->type, false);
-    g.A = X; g.lda = W->in; g.B = W->w; g.ldb = W->in; g.Bs = W->ws; g.ldbs = W->in / 32;
+    g.prec = L->prec; g.a_src = x_src; g.b_src = wo.src;
+    g.A = X; g.lda = W->in; g.B = wo.p; g.ldb = wo.ld; g.Bs = wo.s; g.ldbs = wo.lds;
     if (L->rank > 0) { g.A2 = L->Hc; g.lda2 = L->rank; g.B2 = L->Bc; g.ldb2 = L->rank; g.K2 = L->rank; }
     g.M = N; g.N = W->out; g.K = W->in; g.alpha = 1.0f;
     g.colscale = L->dora ? L->d : nullptr;
@@ -440,11 +499,23 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     const float* redT = L->red + out;
     {
         KernelScope ks(ctx, "lin_bwd_rows");
-        dora_bwd_rows_kernel<CT><<<(unsigned)ceil_div(out, kThreads), kThreads, 0, ctx->stream>>>(
+        dora_bwd_rows_kernel<CT><<<(unsigned)ceil_div(out, 8), kThreads, 0, ctx->stream>>>(
             gd, redT, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
             static_cast<CT*>(L->Ax));
         SA3K_LAUNCHED();
-        if (L->dora) {
+    }
+    if (L->dora) {
+        // A2x = 2 s^2 B^T diag(gn) B = s * (Ax . Bt^T), K = out (a rank x rank GEMM, split over K)
+        if (out % (bf ? 64 : 32) == 0) {
+            GemmDesc g;
+            g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = g.a_src;
+            g.A = L->Ax; g.lda = out; g.B = L->Bt; g.ldb = out;
+            g.M = r; g.N = r; g.K = out; g.alpha = L->s;
+            if (bf) { g.Cb = static_cast<bf16*>(L->A2x); g.ldcb = r; }
+            else { g.C = static_cast<float*>(L->A2x); g.ldc = r; }
+            gemm_run(ctx, g, "lin_bwd_btgb");
+        } else {
+            KernelScope ks(ctx, "lin_bwd_btgb");
             btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
                                                                              static_cast<CT*>(L->A2x));
             SA3K_LAUNCHED();
@@ -462,10 +533,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
     //    of the same GEMM (they share the W^T tiles)
+    const WOp wt = weight_operand(W, bf, true);
     if (dX) {
         GemmDesc g;
-        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(W->type, true);
-        g.A = L->dU; g.lda = out; g.B = W->wt; g.ldb = out; g.Bs = W->wts; g.ldbs = out;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
+        g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
         g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
@@ -476,8 +548,8 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, "lin_bwd_dx");
     } else if (L->dora) {
         GemmDesc g;
-        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(W->type, true);
-        g.A = L->Ax; g.lda = out; g.B = W->wt; g.ldb = out; g.Bs = W->wts; g.ldbs = out;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
+        g.A = L->Ax; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
         g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
         g.M = r; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dA; g.ldc = in; g.accumulate = 1;
@@ -552,6 +624,13 @@ SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out
                 if (es == 4) transpose<uint32_t>(ctx, static_cast<uint32_t*>(w->w), static_cast<uint32_t*>(w->wt), out, in);
                 else transpose<uint16_t>(ctx, static_cast<uint16_t*>(w->w), static_cast<uint16_t*>(w->wt), out, in);
             }
+            if (type != SA3K_TYPE_BF16) {
+                w->wb = dev_alloc<bf16>(n);
+                w->wbt = dev_alloc<bf16>(n);
+                decode_bf16_kernel<<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(*w, static_cast<bf16*>(w->wb));
+                SA3K_LAUNCHED();
+                transpose<uint16_t>(ctx, static_cast<uint16_t*>(w->wb), static_cast<uint16_t*>(w->wbt), out, in);
+            }
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
             if (staging) SA3K_HIP(hipFree(staging));
         } catch (...) {
@@ -559,6 +638,16 @@ SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out
             throw;
         }
         *out_w = w;
+    });
+}
+
+SA3K_API int sa3k_weight_drop_working_copy(sa3k_ctx* ctx, sa3k_weight* w) {
+    return sa3k_guard(ctx, "sa3k_weight_drop_working_copy", [&] {
+        SA3K_REQUIRE(w != nullptr, "null weight");
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        if (w->wb) SA3K_HIP(hipFree(w->wb));
+        if (w->wbt) SA3K_HIP(hipFree(w->wbt));
+        w->wb = w->wbt = nullptr;
     });
 }
 
@@ -610,6 +699,7 @@ SA3K_API int sa3k_lin_create(sa3k_ctx* ctx, const sa3k_weight* W, int rank, int 
             L->nsq = dev_alloc<float>(out); L->d = dev_alloc<float>(out);
             L->Hc = ct_alloc(max_tokens * r); L->U = ct_alloc(max_tokens * out);
             L->dU = ct_alloc(max_tokens * out); L->sdUB = ct_alloc(max_tokens * r);
+            if (prec == SA3K_PREC_BF16) L->Xb = dev_alloc<bf16>(max_tokens * in);
             L->gd = dev_alloc<float>(out); L->gn = dev_alloc<float>(out);
             L->Ax = ct_alloc(r * out); L->A2x = ct_alloc(r * r);
             L->part_elems = std::max((size_t)choose_splits(out, max_tokens) * 33 * out,
@@ -666,14 +756,15 @@ SA3K_API int sa3k_lin_prepare(sa3k_ctx* ctx, sa3k_lin* L, const float* A, const 
         cvt_t(B, L->Bt, out, r);
         if (!dora) return;
         // P^T = A W^T  [r][out]: streams W once through the forward weight loader
+        const WOp wo = weight_operand(L->W, bf, false);
         GemmDesc g;
-        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = src_of_weight(L->W->type, false);
-        g.A = L->Ac; g.lda = in; g.B = L->W->w; g.ldb = in; g.Bs = L->W->ws; g.ldbs = in / 32;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wo.src;
+        g.A = L->Ac; g.lda = in; g.B = wo.p; g.ldb = wo.ld; g.Bs = wo.s; g.ldbs = wo.lds;
         g.M = r; g.N = out; g.K = in; g.C = L->Pt; g.ldc = out;
         gemm_run(ctx, g, "lin_prepare_p");
         gram_kernel<<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(A, in, r, L->G);
         SA3K_LAUNCHED();
-        dora_terms_kernel<<<(unsigned)ceil_div(out, kThreads), kThreads, 0, ctx->stream>>>(
+        dora_terms_kernel<<<(unsigned)ceil_div(out, 8), kThreads, 0, ctx->stream>>>(
             L->Pt, B, L->G, base_norm_sq, magnitude, out, r, scale, L->BG, L->nsq, L->d);
         SA3K_LAUNCHED();
     });

@@ -1,6 +1,8 @@
 // Context, device memory and stream timing for the sa3k C ABI.
 #include "sa3k_internal.h"
 
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 namespace {
@@ -65,6 +67,13 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
+        if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
+        if (const char* e = std::getenv("SA3K_GEMM_SPLIT")) ctx->gemm_split = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_DMA")) ctx->gemm_dma = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
+        if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
+        SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
+        SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
         SA3K_HIP(hipMalloc(&ctx->adamw_partials, sizeof(double) * kAdamwMaxBlocks));
         SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
         SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
@@ -84,6 +93,8 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->adamw_partials) (void)hipFree(ctx->adamw_partials);
     if (ctx->adamw_result) (void)hipFree(ctx->adamw_result);
+    if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     for (const ProfRecord& r : ctx->prof_pending) {
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);

@@ -37,6 +37,14 @@ struct sa3k_ctx {
     // AdamW: per-block partial sums of squares and the {norm, scale} pair of the last update.
     double* adamw_partials = nullptr;     // [kAdamwMaxBlocks]
     double* adamw_result = nullptr;       // [0] = norm, [1] = scale (as double)
+    void* gemm_ws = nullptr;              // split-K partial sums (grown on demand)
+    size_t gemm_ws_bytes = 0;
+    int gemm_pd = 1;                      // GEMM global-load prefetch depth (1 or 2 K tiles)
+    int gemm_split = 1;                   // allow split-K
+    int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
+    int gemm_cfg = 0;                     // DMA kernel tile configuration
+    int gemm_wg_per_cu = 2;               // resident workgroups per CU assumed by the split choice
+    void* zero_page = nullptr;            // 256 zero bytes
 };
 
 // An error that carries an sa3k status code across the internal call chain; every C entry point

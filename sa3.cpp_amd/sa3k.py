@@ -56,6 +56,7 @@ def _declare(lib):
         "sa3k_gemm_nt": (I, [P, I, I, P, I64, I, P, I64, P, I64, I64, I64, I64, F, P, P, P, I64, I]),
         "sa3k_weight_create": (I, [P, I, I64, I64, P, I, C.POINTER(P)]),
         "sa3k_weight_destroy": (I, [P, P]),
+        "sa3k_weight_drop_working_copy": (I, [P, P]),
         "sa3k_weight_row_norm_sq": (I, [P, P, F, P]),
         "sa3k_weight_row_norms": (I, [P, P, P]),
         "sa3k_lin_create": (I, [P, P, I, I, I64, C.POINTER(P)]),
@@ -268,6 +269,9 @@ class Weight:
         y = self.ctx.empty(self.out_)
         self.ctx.check(self.ctx.lib.sa3k_weight_row_norms(self.ctx.h, self.h, y.ptr))
         return y
+
+    def drop_working_copy(self):
+        self.ctx.check(self.ctx.lib.sa3k_weight_drop_working_copy(self.ctx.h, self.h))
 
     def destroy(self):
         if self.h:

@@ -27,12 +27,15 @@ def run(ctx, A, Bop, M, N, K, prec, a_type, b_type, B_scales=None, ldbs=0, **kw)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 96, 192), (2048, 1536, 1536), (37, 20, 128),
-                                   (16, 640, 256), (300, 64, 1024)])
-@pytest.mark.parametrize("btype", ["f32", "f16", "bf16"])
+                                   (16, 640, 256), (300, 64, 1024), (2176, 7680, 1536), (2176, 1536, 6144),
+                                   (2048, 32, 6144)])
+@pytest.mark.parametrize("btype", ["f32", "f16", "bf16", "bf16-dma"])
 def test_gemm_bf16(ctx, M, N, K, btype):
+    # "bf16-dma": both operands bf16, the DMA-fed kernel; the others decode on the way into LDS
     r = rng(M * 7 + N)
     A = r.normal(0, 1, (M, K)).astype(np.float32)
     W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    a_op, a_type = A, sa3k.TYPE_F32
     if btype == "f32":
         Bop, bt, Wd = W, sa3k.TYPE_F32, W
     elif btype == "f16":
@@ -40,7 +43,9 @@ def test_gemm_bf16(ctx, M, N, K, btype):
         bt, Wd = sa3k.TYPE_F16, Bop.astype(np.float32)
     else:
         Bop, bt, Wd = bf16_bits(W), sa3k.TYPE_BF16, bf16_round(W)
-    got = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_F32, bt)
+        if btype == "bf16-dma":
+            a_op, a_type = bf16_bits(A), sa3k.TYPE_BF16
+    got = run(ctx, a_op, Bop, M, N, K, sa3k.PREC_BF16, a_type, bt)
     ref = bf16_round(A).astype(np.float64) @ bf16_round(Wd).astype(np.float64).T
     assert rel_err(got, ref) < 1e-5
 

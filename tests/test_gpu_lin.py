@@ -28,11 +28,13 @@ def make_inputs(seed, N, in_, out_, r, w_sd=0.02, b_sd=0.01):
     return X, dY, W, A, B
 
 
-def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1):
+def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1, decode_in_gemm=False):
     N, in_ = X.shape
     out_ = dY.shape[1]
     r = A.shape[0]
     w = ctx.weight(Wop, wtype)
+    if decode_in_gemm:
+        w.drop_working_copy()
     lin = ctx.lin(w, r, prec, N)
     dA_, dB_ = ctx.upload(A), ctx.upload(B)
     dmag = ctx.upload(mag) if dora else None
@@ -68,15 +70,16 @@ def test_lora_f32_linear(ctx, N):
         assert max_rel_err(got[k], ref[k]) < 1e-4, k
 
 
-@pytest.mark.parametrize("N", [256, 2048])
-def test_dora_q8_0_linear(ctx, N):
+@pytest.mark.parametrize("N,decode", [(256, False), (2048, False), (2048, True)])
+def test_dora_q8_0_linear(ctx, N, decode):
     # DoRA linear 1536 -> 6144, Q8_0 base quantised from N(0, 0.02), rank 32, alpha 32, m = row norms
     in_, out_, r = 1536, 6144, 32
     X, dY, W, A, B = make_inputs(1, N, in_, out_, r)
     blocks = oracle.q8_0_quantize(W)
     _, _, Wdec = q8_0_split(blocks, out_, in_)
     mag = oracle.row_norms(Wdec)
-    got = run_gpu(ctx, X, dY, (blocks, in_, out_), sa3k.TYPE_Q8_0, A, B, 1.0, True, mag, sa3k.PREC_BF16)
+    got = run_gpu(ctx, X, dY, (blocks, in_, out_), sa3k.TYPE_Q8_0, A, B, 1.0, True, mag, sa3k.PREC_BF16,
+                  decode_in_gemm=decode)
     ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
     np.testing.assert_allclose(got["bnsq"], ref["bnsq"], rtol=1e-6)
     for k in ("Y", "dX", "dA", "dB", "dm"):
@@ -87,7 +90,8 @@ def test_dora_q8_0_linear(ctx, N):
 @pytest.mark.parametrize("prec", [sa3k.PREC_F32, sa3k.PREC_BF16])
 @pytest.mark.parametrize("wt", ["f32", "f16"])
 @pytest.mark.parametrize("dora", [False, True])
-def test_linear_small_shapes(ctx, prec, wt, dora):
+@pytest.mark.parametrize("decode", [False, True])
+def test_linear_small_shapes(ctx, prec, wt, dora, decode):
     # ragged token count, non-square, bias on the output
     N, in_, out_, r = 77, 192, 320, 8
     X, dY, W, A, B = make_inputs(2, N, in_, out_, r, w_sd=0.1, b_sd=0.05)
@@ -98,7 +102,7 @@ def test_linear_small_shapes(ctx, prec, wt, dora):
         Wop, wtype, Wdec = W, sa3k.TYPE_F32, W
     mag = (oracle.row_norms(Wdec) * 1.1 + 0.05).astype(np.float32)
     bias = rng(3).normal(0, 1, out_).astype(np.float32)
-    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 2.0, dora, mag, prec, bias=bias)
+    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 2.0, dora, mag, prec, bias=bias, decode_in_gemm=decode)
     ref = run_oracle(X, dY, Wdec, A, B, 2.0, dora, mag, bias)
     keys = ("Y", "dX", "dA", "dB") + (("dm",) if dora else ())
     for k in keys:
