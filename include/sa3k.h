@@ -216,6 +216,29 @@ SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const voi
                                const float* dY, float* dX, int dx_accumulate, float* dA, float* dB,
                                float* dm);
 
+/* ---------------------------------------------------------------- K5: differential attention */
+
+/* Flash-style differential attention (dit_diff_attn, src/dit.h:151-158, over nn::sdpa,
+ * src/nn.h:135-144): per (batch, head) O = softmax(Q1 K1^T scale) V - softmax(Q2 K2^T scale) V,
+ * without materialising the scores. q1, q2 [B*H][Sq][64] and k1, k2, v [B*H][Sk][64] are bf16
+ * (head-major); window 0 is dense (the reference), window > 0 keeps |q - k| <= window/2 and needs
+ * Sq == Sk. Outputs: o bf16 [B][Sq][H*64] (token-major, the out-projection input), o1, o2 bf16
+ * [B*H][Sq][64] (the normalised branch outputs) and lse1, lse2 f32 [B*H][Sq] (base-2 log-sum-exp
+ * of scale*log2(e)*scores), which the backward consumes. */
+SA3K_API int sa3k_diff_attn_fwd(sa3k_ctx* ctx, const void* q1, const void* k1, const void* q2, const void* k2,
+                                const void* v, int B, int H, int Sq, int Sk, int head_dim, int window, float scale,
+                                void* o, void* o1, void* o2, float* lse1, float* lse2);
+
+/* Backward of sa3k_diff_attn_fwd from dO f32 [B][Sq][H*64] (token-major): writes dq1, dq2
+ * [B*H][Sq][64], dk1, dk2, dv [B*H][Sk][64] (f32). The scores are recomputed from lse (ggml's
+ * soft_max_back over stored scores in the reference). Scratch: dOh bf16 [B*H][Sq][64] and dn
+ * f32 [2][B*H][Sq], caller-provided. */
+SA3K_API int sa3k_diff_attn_bwd(sa3k_ctx* ctx, const void* q1, const void* k1, const void* q2, const void* k2,
+                                const void* v, const void* o1, const void* o2, const float* lse1, const float* lse2,
+                                const float* dO, int B, int H, int Sq, int Sk, int head_dim, int window, float scale,
+                                void* scratch_dOh, float* scratch_dn, float* dq1, float* dk1, float* dq2, float* dk2,
+                                float* dv);
+
 #ifdef __cplusplus
 }
 #endif

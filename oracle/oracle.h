@@ -75,6 +75,17 @@ void orc_dit_lin_bwd(const float* X, int64_t N, const float* W, int64_t in, int6
 /* plain double-accumulated products used by tests: C[M][N] = A[M][K] * B[N][K]^T */
 void orc_gemm_nt(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
 
+/* ---- differential attention (src/dit.h:151-158, src/nn.h:135-144), double accumulation ----
+ * Q1, Q2 [BH][Sq][D]; K1, K2, V [BH][Sk][D]; window 0 = dense, else |i-j| <= window/2.
+ * fwd: O = O1 - O2 [BH][Sq][D] (O1, O2, lse1, lse2 [BH][Sq] nullable; lse natural log of the
+ * scaled-score softmax denominator). bwd from dO: dQ1, dK1, dQ2, dK2, dV. */
+void orc_diff_attn_fwd(const float* Q1, const float* K1, const float* Q2, const float* K2, const float* V,
+                       int BH, int Sq, int Sk, int D, float scale, int window, float* O, float* O1, float* O2,
+                       float* lse1, float* lse2);
+void orc_diff_attn_bwd(const float* Q1, const float* K1, const float* Q2, const float* K2, const float* V,
+                       const float* dO, int BH, int Sq, int Sk, int D, float scale, int window, float* dQ1,
+                       float* dK1, float* dQ2, float* dK2, float* dV);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -209,3 +209,40 @@ def gemm_nt(A, B):
     Cm = np.empty((M, N), np.float32)
     lib().orc_gemm_nt(A, B, Cm, M, N, K)
     return Cm
+
+
+# ---------------------------------------------------------------- differential attention
+def _attn_sig():
+    L = lib()
+    if getattr(L, "_attn_declared", False):
+        return L
+    I, F = C.c_int, C.c_float
+    optf = C.c_void_p
+    L.orc_diff_attn_fwd.restype = None
+    L.orc_diff_attn_fwd.argtypes = [f32p, f32p, f32p, f32p, f32p, I, I, I, I, F, I, f32p, optf, optf, optf, optf]
+    L.orc_diff_attn_bwd.restype = None
+    L.orc_diff_attn_bwd.argtypes = [f32p, f32p, f32p, f32p, f32p, f32p, I, I, I, I, F, I, f32p, f32p, f32p, f32p, f32p]
+    L._attn_declared = True
+    return L
+
+
+def diff_attn_fwd(Q1, K1, Q2, K2, V, scale=0.125, window=0):
+    """arrays [BH][S][D]; returns dict O, O1, O2, lse1, lse2"""
+    Q1, K1, Q2, K2, V = (f32(x) for x in (Q1, K1, Q2, K2, V))
+    BH, Sq, D = Q1.shape
+    Sk = K1.shape[1]
+    O, O1, O2 = (np.empty((BH, Sq, D), np.float32) for _ in range(3))
+    l1, l2 = np.empty((BH, Sq), np.float32), np.empty((BH, Sq), np.float32)
+    _attn_sig().orc_diff_attn_fwd(Q1, K1, Q2, K2, V, BH, Sq, Sk, D, scale, window, O, O1.ctypes.data,
+                                  O2.ctypes.data, l1.ctypes.data, l2.ctypes.data)
+    return dict(O=O, O1=O1, O2=O2, lse1=l1, lse2=l2)
+
+
+def diff_attn_bwd(Q1, K1, Q2, K2, V, dO, scale=0.125, window=0):
+    Q1, K1, Q2, K2, V, dO = (f32(x) for x in (Q1, K1, Q2, K2, V, dO))
+    BH, Sq, D = Q1.shape
+    Sk = K1.shape[1]
+    dQ1, dQ2 = np.empty_like(Q1), np.empty_like(Q2)
+    dK1, dK2, dV = np.empty_like(K1), np.empty_like(K2), np.empty_like(V)
+    _attn_sig().orc_diff_attn_bwd(Q1, K1, Q2, K2, V, dO, BH, Sq, Sk, D, scale, window, dQ1, dK1, dQ2, dK2, dV)
+    return dict(dQ1=dQ1, dK1=dK1, dQ2=dQ2, dK2=dK2, dV=dV)

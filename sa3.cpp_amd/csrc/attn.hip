@@ -1,0 +1,525 @@
+// K5: differential attention, flash-style, on bf16 MFMA (head_dim 64).
+//
+// Reference: dit_diff_attn (src/dit.h:151-158) over nn::sdpa (src/nn.h:135-144): per (batch,
+// head) O = softmax(Q1 K1^T s) V - softmax(Q2 K2^T s) V, materialised [S x S] scores in ggml.
+// Here nothing of size S x S ever leaves the CU:
+//   forward   one pass over key blocks keeps both branches' online-softmax state and shares the
+//             V tile; writes O (token-major bf16, the out-projection's input), the normalised
+//             branch outputs O1, O2 and the per-query log2-sum-exp of each branch;
+//   backward  Dn_i = rowsum(dO * O_i) first (also re-lays dO head-major in bf16), then two
+//             recompute kernels: one per key block (dK1, dK2, dV; loops over queries) and one
+//             per query block (dQ1, dQ2; loops over keys) -- no atomics, deterministic.
+// With dO_2 = -dO: dS_1 = P1 (dP - Dn1), dS_2 = -P2 (dP - Dn2), dP = dO V^T, dV = (P1 - P2)^T dO.
+//
+// MFMA layout (v_mfma_f32_16x16x32_bf16): scores are computed transposed, S^T = K Q^T, so that a
+// lane holds one query (lane % 16) and 4 keys per 16-key tile; two adjacent key tiles give the 8
+// key-values that lane feeds as the A operand of P V. The B operand for that product is read from
+// a transposed V tile (dims x keys) with the same key pattern, so both operands agree on K order.
+// The dK/dV kernel computes S = Q K^T instead (lane = one key) for the same reason.
+//
+// window > 0 keeps keys with |q - k| <= window/2 (self-attention only); 0 is dense.
+#include "sa3k_internal.h"
+
+namespace {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+constexpr int kThreads = 256;
+constexpr int HD = 64;          // head dim
+constexpr int BLK = 64;         // queries / keys per block
+constexpr int ROW = 128;        // bytes per [row][64] bf16 LDS row (swizzled, unpadded)
+constexpr int TROW = 136;       // bytes per transposed [64][64] LDS row (padded by 4 bf16)
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte chunk c (8 dims) of row r in a swizzled [64][64] tile
+__device__ __forceinline__ bf16x8 ld_row(const char* t, int r, int c) {
+    return *reinterpret_cast<const bf16x8*>(t + r * ROW + ((c ^ swz(r)) << 4));
+}
+__device__ __forceinline__ void st_row(char* t, int r, int c, uint4 v) {
+    *reinterpret_cast<uint4*>(t + r * ROW + ((c ^ swz(r)) << 4)) = v;
+}
+// 4 consecutive columns (8 bytes) of row r in a transposed [64][64] tile
+__device__ __forceinline__ bf16x4 ld_t4(const char* t, int r, int col) {
+    return *reinterpret_cast<const bf16x4*>(t + r * TROW + col * 2);
+}
+__device__ __forceinline__ bf16x8 cat44(bf16x4 a, bf16x4 b) {
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Load a [64 rows][64] bf16 tile (rows r0.., row stride 64 elems, rows >= nrows zero) into LDS as
+// a swizzled row tile and/or a transposed (dims x rows) tile.
+__device__ __forceinline__ void load_tile(const bf16* __restrict__ src, int r0, int nrows, char* row_t,
+                                          char* tr_t) {
+    for (int k = threadIdx.x; k < BLK * 8; k += kThreads) {
+        const int r = k >> 3, c = k & 7;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (r0 + r < nrows) v = *reinterpret_cast<const uint4*>(src + (int64_t)(r0 + r) * HD + c * 8);
+        if (row_t) st_row(row_t, r, c, v);
+        if (tr_t) {
+            const bf16x8 e = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) *reinterpret_cast<bf16*>(tr_t + (c * 8 + j) * TROW + r * 2) = e[j];
+        }
+    }
+}
+
+__device__ __forceinline__ bool vis(int q, int k, int nk, int window) {
+    if (k >= nk) return false;
+    if (window <= 0) return true;
+    const int d = q > k ? q - k : k - q;
+    return 2 * d <= window;
+}
+
+// key/query block range [lo, hi) that can interact with block b under the window
+__device__ __forceinline__ void band_range(int b, int n_other, int window, int& lo, int& hi) {
+    const int nb = (n_other + BLK - 1) / BLK;
+    lo = 0;
+    hi = nb;
+    if (window > 0) {
+        const int half = window / 2;
+        lo = max(0, (b * BLK - half) / BLK);
+        hi = min(nb, (b * BLK + BLK - 1 + half) / BLK + 1);
+    }
+}
+
+// ------------------------------------------------------------------------------------ forward
+struct FwdArgs {
+    const bf16 *q1, *k1, *q2, *k2, *v;   // [BH][S][64]
+    int H, Sq, Sk, window;
+    float scale;
+    bf16* o;             // [B][Sq][H*64] token-major
+    bf16 *o1, *o2;       // [BH][Sq][64] normalised branch outputs
+    float *lse1, *lse2;  // [BH][Sq] log2-sum-exp of scale*log2e*scores
+};
+
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char k1s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char k2s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char vts[HD * TROW];
+    const int bh = blockIdx.y, qb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
+    const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
+    const int qrow = qb * BLK + w * 16 + r;        // this lane's query for the S^T layout
+    const float c = a.scale * kLog2e;
+
+    bf16x8 q1f[2], q2f[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        uint4 z = make_uint4(0, 0, 0, 0), u1 = z, u2 = z;
+        if (qrow < a.Sq) {
+            u1 = *reinterpret_cast<const uint4*>(a.q1 + qoff + (int64_t)qrow * HD + ks * 32 + g * 8);
+            u2 = *reinterpret_cast<const uint4*>(a.q2 + qoff + (int64_t)qrow * HD + ks * 32 + g * 8);
+        }
+        q1f[ks] = __builtin_bit_cast(bf16x8, u1);
+        q2f[ks] = __builtin_bit_cast(bf16x8, u2);
+    }
+    f32x4 o1[4], o2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o1[i] = o2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m1 = -INFINITY, m2 = -INFINITY, l1 = 0.f, l2 = 0.f;   // per lane: query qrow (l partial)
+
+    int kb_lo, kb_hi;
+    band_range(qb, a.Sk, a.window, kb_lo, kb_hi);
+    for (int kb = kb_lo; kb < kb_hi; ++kb) {
+        __syncthreads();
+        load_tile(a.k1 + koff, kb * BLK, a.Sk, k1s, nullptr);
+        load_tile(a.k2 + koff, kb * BLK, a.Sk, k2s, nullptr);
+        load_tile(a.v + koff, kb * BLK, a.Sk, nullptr, vts);
+        __syncthreads();
+        // S^T tiles: keys kt*16 + 4g + v, query qrow
+        f32x4 s1[4], s2[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            s1[kt] = s2[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                s1[kt] = mfma(ld_row(k1s, kt * 16 + r, ks * 4 + g), q1f[ks], s1[kt]);
+                s2[kt] = mfma(ld_row(k2s, kt * 16 + r, ks * 4 + g), q2f[ks], s2[kt]);
+            }
+        }
+        // wait: the MFMA output layout is rows = 4*(lane/16)+v of the A operand (keys), col = lane%16
+        // (queries); the A rows fed above were keys kt*16 + r, so output row index 4g+v is key
+        // kt*16 + 4g + v and the column is query w*16 + r.
+        float mx1 = -INFINITY, mx2 = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int key = kb * BLK + kt * 16 + 4 * g + v;
+                const bool ok = vis(qrow, key, a.Sk, a.window);
+                s1[kt][v] = ok ? s1[kt][v] * c : -INFINITY;
+                s2[kt][v] = ok ? s2[kt][v] * c : -INFINITY;
+                mx1 = fmaxf(mx1, s1[kt][v]);
+                mx2 = fmaxf(mx2, s2[kt][v]);
+            }
+        mx1 = fmaxf(mx1, __shfl_xor(mx1, 16, 64));
+        mx1 = fmaxf(mx1, __shfl_xor(mx1, 32, 64));
+        mx2 = fmaxf(mx2, __shfl_xor(mx2, 16, 64));
+        mx2 = fmaxf(mx2, __shfl_xor(mx2, 32, 64));
+        const float mn1 = fmaxf(m1, mx1), mn2 = fmaxf(m2, mx2);
+        const float base1 = mn1 == -INFINITY ? 0.f : mn1, base2 = mn2 == -INFINITY ? 0.f : mn2;
+        const float al1 = exp2f(m1 - base1), al2 = exp2f(m2 - base2);   // 0 when m was -inf
+        m1 = mn1;
+        m2 = mn2;
+        float ps1 = 0.f, ps2 = 0.f;
+        bf16x8 p1[2], p2[2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float e1 = exp2f(s1[kt][v] - base1), e2 = exp2f(s2[kt][v] - base2);
+                ps1 += e1;
+                ps2 += e2;
+                p1[kt >> 1][(kt & 1) * 4 + v] = (bf16)e1;
+                p2[kt >> 1][(kt & 1) * 4 + v] = (bf16)e2;
+            }
+        l1 = l1 * al1 + ps1;
+        l2 = l2 * al2 + ps2;
+        // rescale O rows (queries w*16 + 4g + v) by their alpha (held by lane 4g+v)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float a1 = __shfl(al1, 4 * g + v, 64), a2 = __shfl(al2, 4 * g + v, 64);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                o1[dt][v] *= a1;
+                o2[dt][v] *= a2;
+            }
+        }
+        // O += P V over two 32-key chunks: key(e) = 32c + (e < 4 ? 4g + e : 16 + 4g + e - 4)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const bf16x8 vb = cat44(ld_t4(vts, dt * 16 + r, 32 * ch + 4 * g), ld_t4(vts, dt * 16 + r, 32 * ch + 16 + 4 * g));
+                o1[dt] = mfma(p1[ch], vb, o1[dt]);
+                o2[dt] = mfma(p2[ch], vb, o2[dt]);
+            }
+    }
+    // l: sum the four lane groups' partials (per query qrow)
+    l1 += __shfl_xor(l1, 16, 64);
+    l1 += __shfl_xor(l1, 32, 64);
+    l2 += __shfl_xor(l2, 16, 64);
+    l2 += __shfl_xor(l2, 32, 64);
+    if (g == 0 && qrow < a.Sq) {
+        a.lse1[(int64_t)bh * a.Sq + qrow] = m1 + log2f(l1);
+        a.lse2[(int64_t)bh * a.Sq + qrow] = m2 + log2f(l2);
+    }
+    const int b = bh / a.H, h = bh % a.H;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const float i1 = 1.0f / __shfl(l1, 4 * g + v, 64), i2 = 1.0f / __shfl(l2, 4 * g + v, 64);
+        const int q = qb * BLK + w * 16 + 4 * g + v;
+        if (q >= a.Sq) continue;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d = dt * 16 + r;
+            const float x1 = o1[dt][v] * i1, x2 = o2[dt][v] * i2;
+            a.o1[qoff + (int64_t)q * HD + d] = (bf16)x1;
+            a.o2[qoff + (int64_t)q * HD + d] = (bf16)x2;
+            a.o[((int64_t)b * a.Sq + q) * (a.H * HD) + h * HD + d] = (bf16)(x1 - x2);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------ backward
+// Dn_i[bh][q] = sum_d dO[b][q][h][d] * O_i[bh][q][d]; dOh[bh][q][d] = bf16(dO) (head-major)
+__global__ __launch_bounds__(kThreads) void attn_bwd_dot_kernel(const float* __restrict__ dO, const bf16* __restrict__ o1,
+                                                                const bf16* __restrict__ o2, int BH, int H, int Sq,
+                                                                bf16* __restrict__ dOh, float* __restrict__ dn1,
+                                                                float* __restrict__ dn2) {
+    // one wave per (bh, q): 64 lanes = 64 dims
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int d = threadIdx.x & 63;
+    if (item >= (int64_t)BH * Sq) return;
+    const int bh = (int)(item / Sq), q = (int)(item % Sq);
+    const int b = bh / H, h = bh % H;
+    const float x = dO[((int64_t)b * Sq + q) * (H * HD) + h * HD + d];
+    const int64_t idx = item * HD + d;
+    dOh[idx] = (bf16)x;
+    float s1 = x * (float)o1[idx], s2 = x * (float)o2[idx];
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off, 64);
+        s2 += __shfl_xor(s2, off, 64);
+    }
+    if (d == 0) {
+        dn1[item] = s1;
+        dn2[item] = s2;
+    }
+}
+
+struct BwdArgs {
+    const bf16 *q1, *k1, *q2, *k2, *v, *dO;   // [BH][S][64]
+    const float *lse1, *lse2, *dn1, *dn2;     // [BH][Sq]
+    int Sq, Sk, window;
+    float scale;
+    float *dq1, *dq2, *dk1, *dk2, *dv;        // [BH][S][64] f32
+};
+
+// Per key block: dK1, dK2, dV. S = Q K^T with lane = key (lane%16), queries 4g+v per 16-query tile.
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char q1s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char q2s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char dos[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char q1t[HD * TROW];
+    __shared__ __attribute__((aligned(16))) char q2t[HD * TROW];
+    __shared__ __attribute__((aligned(16))) char dot[HD * TROW];
+    __shared__ float sl1[BLK], sl2[BLK], sd1[BLK], sd2[BLK];
+    const int bh = blockIdx.y, kb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
+    const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
+    const int key = kb * BLK + w * 16 + r;     // this lane's key
+    const float c = a.scale * kLog2e;
+
+    bf16x8 k1f[2], k2f[2], vf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        uint4 z = make_uint4(0, 0, 0, 0), u1 = z, u2 = z, u3 = z;
+        if (key < a.Sk) {
+            u1 = *reinterpret_cast<const uint4*>(a.k1 + koff + (int64_t)key * HD + ks * 32 + g * 8);
+            u2 = *reinterpret_cast<const uint4*>(a.k2 + koff + (int64_t)key * HD + ks * 32 + g * 8);
+            u3 = *reinterpret_cast<const uint4*>(a.v + koff + (int64_t)key * HD + ks * 32 + g * 8);
+        }
+        k1f[ks] = __builtin_bit_cast(bf16x8, u1);
+        k2f[ks] = __builtin_bit_cast(bf16x8, u2);
+        vf[ks] = __builtin_bit_cast(bf16x8, u3);
+    }
+    f32x4 dvt[4], dk1t[4], dk2t[4];   // transposed accumulators: rows dims dt*16 + 4g + v, col = key
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dvt[i] = dk1t[i] = dk2t[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int qb_lo, qb_hi;
+    band_range(kb, a.Sq, a.window, qb_lo, qb_hi);
+    for (int qb = qb_lo; qb < qb_hi; ++qb) {
+        __syncthreads();
+        load_tile(a.q1 + qoff, qb * BLK, a.Sq, q1s, q1t);
+        load_tile(a.q2 + qoff, qb * BLK, a.Sq, q2s, q2t);
+        load_tile(a.dO + qoff, qb * BLK, a.Sq, dos, dot);
+        if (threadIdx.x < BLK) {
+            const int q = qb * BLK + threadIdx.x;
+            const bool ok = q < a.Sq;
+            sl1[threadIdx.x] = ok ? a.lse1[(int64_t)bh * a.Sq + q] : 0.f;
+            sl2[threadIdx.x] = ok ? a.lse2[(int64_t)bh * a.Sq + q] : 0.f;
+            sd1[threadIdx.x] = ok ? a.dn1[(int64_t)bh * a.Sq + q] : 0.f;
+            sd2[threadIdx.x] = ok ? a.dn2[(int64_t)bh * a.Sq + q] : 0.f;
+        }
+        __syncthreads();
+        // per 16-query tile qt: S1, S2, dP with rows = queries qt*16 + 4g + v, col = key
+        bf16x8 pd[2], ds1[2], ds2[2];    // (P1 - P2), dS1, dS2 as B operands over query pairs
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+            f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                s1 = mfma(ld_row(q1s, qt * 16 + r, ks * 4 + g), k1f[ks], s1);
+                s2 = mfma(ld_row(q2s, qt * 16 + r, ks * 4 + g), k2f[ks], s2);
+                dp = mfma(ld_row(dos, qt * 16 + r, ks * 4 + g), vf[ks], dp);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int ql = qt * 16 + 4 * g + v, q = qb * BLK + ql;
+                const bool ok = q < a.Sq && vis(q, key, a.Sk, a.window);
+                const float p1 = ok ? exp2f(s1[v] * c - sl1[ql]) : 0.f;
+                const float p2 = ok ? exp2f(s2[v] * c - sl2[ql]) : 0.f;
+                const int e = (qt & 1) * 4 + v;
+                pd[qt >> 1][e] = (bf16)(p1 - p2);
+                ds1[qt >> 1][e] = (bf16)(p1 * (dp[v] - sd1[ql]));
+                ds2[qt >> 1][e] = (bf16)(-p2 * (dp[v] - sd2[ql]));
+            }
+        }
+        // dV^T += dO^T (P1 - P2); dK_i^T += Q_i^T dS_i  (A: transposed tiles, 8 queries per lane group)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int row = dt * 16 + r, c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
+                dvt[dt] = mfma(cat44(ld_t4(dot, row, c0), ld_t4(dot, row, c1)), pd[ch], dvt[dt]);
+                dk1t[dt] = mfma(cat44(ld_t4(q1t, row, c0), ld_t4(q1t, row, c1)), ds1[ch], dk1t[dt]);
+                dk2t[dt] = mfma(cat44(ld_t4(q2t, row, c0), ld_t4(q2t, row, c1)), ds2[ch], dk2t[dt]);
+            }
+    }
+    if (key >= a.Sk) return;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t idx = koff + (int64_t)key * HD + dt * 16 + 4 * g + v;
+            a.dv[idx] = dvt[dt][v];
+            a.dk1[idx] = a.scale * dk1t[dt][v];
+            a.dk2[idx] = a.scale * dk2t[dt][v];
+        }
+}
+
+// Per query block: dQ1, dQ2. S^T = K Q^T (lane = query), dP^T = V dO^T.
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char k1s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char k2s[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char vs[BLK * ROW];
+    __shared__ __attribute__((aligned(16))) char k1t[HD * TROW];
+    __shared__ __attribute__((aligned(16))) char k2t[HD * TROW];
+    const int bh = blockIdx.y, qb = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
+    const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
+    const int qrow = qb * BLK + w * 16 + r;
+    const float c = a.scale * kLog2e;
+
+    bf16x8 q1f[2], q2f[2], dof[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        uint4 z = make_uint4(0, 0, 0, 0), u1 = z, u2 = z, u3 = z;
+        if (qrow < a.Sq) {
+            u1 = *reinterpret_cast<const uint4*>(a.q1 + qoff + (int64_t)qrow * HD + ks * 32 + g * 8);
+            u2 = *reinterpret_cast<const uint4*>(a.q2 + qoff + (int64_t)qrow * HD + ks * 32 + g * 8);
+            u3 = *reinterpret_cast<const uint4*>(a.dO + qoff + (int64_t)qrow * HD + ks * 32 + g * 8);
+        }
+        q1f[ks] = __builtin_bit_cast(bf16x8, u1);
+        q2f[ks] = __builtin_bit_cast(bf16x8, u2);
+        dof[ks] = __builtin_bit_cast(bf16x8, u3);
+    }
+    const bool qok = qrow < a.Sq;
+    const float L1 = qok ? a.lse1[(int64_t)bh * a.Sq + qrow] : 0.f;
+    const float L2 = qok ? a.lse2[(int64_t)bh * a.Sq + qrow] : 0.f;
+    const float D1 = qok ? a.dn1[(int64_t)bh * a.Sq + qrow] : 0.f;
+    const float D2 = qok ? a.dn2[(int64_t)bh * a.Sq + qrow] : 0.f;
+    f32x4 dq1[4], dq2[4];   // rows queries 4g+v, col dims dt*16 + r
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dq1[i] = dq2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int kb_lo, kb_hi;
+    band_range(qb, a.Sk, a.window, kb_lo, kb_hi);
+    for (int kb = kb_lo; kb < kb_hi; ++kb) {
+        __syncthreads();
+        load_tile(a.k1 + koff, kb * BLK, a.Sk, k1s, k1t);
+        load_tile(a.k2 + koff, kb * BLK, a.Sk, k2s, k2t);
+        load_tile(a.v + koff, kb * BLK, a.Sk, vs, nullptr);
+        __syncthreads();
+        bf16x8 ds1[2], ds2[2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                s1 = mfma(ld_row(k1s, kt * 16 + r, ks * 4 + g), q1f[ks], s1);
+                s2 = mfma(ld_row(k2s, kt * 16 + r, ks * 4 + g), q2f[ks], s2);
+                dp = mfma(ld_row(vs, kt * 16 + r, ks * 4 + g), dof[ks], dp);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int k = kb * BLK + kt * 16 + 4 * g + v;
+                const bool ok = qok && vis(qrow, k, a.Sk, a.window);
+                const float p1 = ok ? exp2f(s1[v] * c - L1) : 0.f;
+                const float p2 = ok ? exp2f(s2[v] * c - L2) : 0.f;
+                const int e = (kt & 1) * 4 + v;
+                ds1[kt >> 1][e] = (bf16)(p1 * (dp[v] - D1));
+                ds2[kt >> 1][e] = (bf16)(-p2 * (dp[v] - D2));
+            }
+        }
+        // dQ_i += dS_i K_i: B = K^T tile rows = dims, 8 keys per lane group
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int row = dt * 16 + r, c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
+                dq1[dt] = mfma(ds1[ch], cat44(ld_t4(k1t, row, c0), ld_t4(k1t, row, c1)), dq1[dt]);
+                dq2[dt] = mfma(ds2[ch], cat44(ld_t4(k2t, row, c0), ld_t4(k2t, row, c1)), dq2[dt]);
+            }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int q = qb * BLK + w * 16 + 4 * g + v;
+        if (q >= a.Sq) continue;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int64_t idx = qoff + (int64_t)q * HD + dt * 16 + r;
+            a.dq1[idx] = a.scale * dq1[dt][v];
+            a.dq2[idx] = a.scale * dq2[dt][v];
+        }
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------ host
+namespace sa3k {
+
+void attn_forward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2, const bf16* k2, const bf16* v,
+                  int B, int H, int Sq, int Sk, int window, float scale, bf16* o, bf16* o1, bf16* o2,
+                  float* lse1, float* lse2) {
+    SA3K_REQUIRE(B > 0 && H > 0 && Sq > 0 && Sk > 0, "attention extents must be positive");
+    SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
+    FwdArgs a{q1, k1, q2, k2, v, H, Sq, Sk, window, scale, o, o1, o2, lse1, lse2};
+    dim3 grid((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H));
+    KernelScope ks(ctx, "attn_fwd");
+    attn_fwd_kernel<<<grid, kThreads, 0, ctx->stream>>>(a);
+    SA3K_LAUNCHED();
+}
+
+// dO: f32 [B][Sq][H*64] token-major; scratch dOh bf16 [BH][Sq][64], dn1/dn2 f32 [BH][Sq]
+void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2, const bf16* k2, const bf16* v,
+                   const bf16* o1, const bf16* o2, const float* lse1, const float* lse2, const float* dO,
+                   int B, int H, int Sq, int Sk, int window, float scale, bf16* dOh, float* dn1, float* dn2,
+                   float* dq1, float* dk1, float* dq2, float* dk2, float* dv) {
+    SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
+    const int BH = B * H;
+    {
+        KernelScope ks(ctx, "attn_bwd_dot");
+        const int64_t items = (int64_t)BH * Sq;
+        attn_bwd_dot_kernel<<<(unsigned)ceil_div(items, kThreads / 64), kThreads, 0, ctx->stream>>>(
+            dO, o1, o2, BH, H, Sq, dOh, dn1, dn2);
+        SA3K_LAUNCHED();
+    }
+    BwdArgs a{q1, k1, q2, k2, v, dOh, lse1, lse2, dn1, dn2, Sq, Sk, window, scale, dq1, dq2, dk1, dk2, dv};
+    {
+        KernelScope ks(ctx, "attn_bwd_dkdv");
+        attn_bwd_dkdv_kernel<<<dim3((unsigned)ceil_div(Sk, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
+        SA3K_LAUNCHED();
+    }
+    {
+        KernelScope ks(ctx, "attn_bwd_dq");
+        attn_bwd_dq_kernel<<<dim3((unsigned)ceil_div(Sq, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
+        SA3K_LAUNCHED();
+    }
+}
+
+}  // namespace sa3k
+
+// ------------------------------------------------------------------------------------ C ABI
+extern "C" {
+
+SA3K_API int sa3k_diff_attn_fwd(sa3k_ctx* ctx, const void* q1, const void* k1, const void* q2, const void* k2,
+                                const void* v, int B, int H, int Sq, int Sk, int head_dim, int window, float scale,
+                                void* o, void* o1, void* o2, float* lse1, float* lse2) {
+    return sa3k_guard(ctx, "sa3k_diff_attn_fwd", [&] {
+        SA3K_REQUIRE(head_dim == HD, "head_dim must be 64");
+        SA3K_REQUIRE(q1 && k1 && q2 && k2 && v && o && o1 && o2 && lse1 && lse2, "null pointer");
+        sa3k::attn_forward(ctx, (const bf16*)q1, (const bf16*)k1, (const bf16*)q2, (const bf16*)k2, (const bf16*)v,
+                           B, H, Sq, Sk, window, scale, (bf16*)o, (bf16*)o1, (bf16*)o2, lse1, lse2);
+    });
+}
+
+SA3K_API int sa3k_diff_attn_bwd(sa3k_ctx* ctx, const void* q1, const void* k1, const void* q2, const void* k2,
+                                const void* v, const void* o1, const void* o2, const float* lse1, const float* lse2,
+                                const float* dO, int B, int H, int Sq, int Sk, int head_dim, int window, float scale,
+                                void* scratch_dOh, float* scratch_dn, float* dq1, float* dk1, float* dq2, float* dk2,
+                                float* dv) {
+    return sa3k_guard(ctx, "sa3k_diff_attn_bwd", [&] {
+        SA3K_REQUIRE(head_dim == HD, "head_dim must be 64");
+        SA3K_REQUIRE(q1 && k1 && q2 && k2 && v && o1 && o2 && lse1 && lse2 && dO && scratch_dOh && scratch_dn,
+                     "null pointer");
+        SA3K_REQUIRE(dq1 && dk1 && dq2 && dk2 && dv, "null gradient pointer");
+        const int64_t n = (int64_t)B * H * Sq;
+        sa3k::attn_backward(ctx, (const bf16*)q1, (const bf16*)k1, (const bf16*)q2, (const bf16*)k2, (const bf16*)v,
+                            (const bf16*)o1, (const bf16*)o2, lse1, lse2, dO, B, H, Sq, Sk, window, scale,
+                            (bf16*)scratch_dOh, scratch_dn, scratch_dn + n, dq1, dk1, dq2, dk2, dv);
+    });
+}
+
+}  // extern "C"

@@ -64,6 +64,8 @@ def _declare(lib):
         "sa3k_lin_prepare": (I, [P, P, P, P, F, I, P, P]),
         "sa3k_lin_forward": (I, [P, P, I, P, I64, P, P]),
         "sa3k_lin_backward": (I, [P, P, I, P, I64, P, P, I, P, P, P]),
+        "sa3k_diff_attn_fwd": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P]),
+        "sa3k_diff_attn_bwd": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -302,3 +304,24 @@ class Lin:
         if self.h:
             self.ctx.check(self.ctx.lib.sa3k_lin_destroy(self.ctx.h, self.h))
             self.h = None
+
+
+def attn_fwd(ctx, q1, k1, q2, k2, v, B, H, Sq, Sk, window=0, scale=0.125):
+    """device bf16 inputs [B*H][S][64]; returns (o, o1, o2, lse1, lse2) device arrays"""
+    o = ctx.empty((B, Sq, H * 64), np.uint16)
+    o1, o2 = ctx.empty((B * H, Sq, 64), np.uint16), ctx.empty((B * H, Sq, 64), np.uint16)
+    l1, l2 = ctx.empty((B * H, Sq)), ctx.empty((B * H, Sq))
+    ctx.check(ctx.lib.sa3k_diff_attn_fwd(ctx.h, q1.ptr, k1.ptr, q2.ptr, k2.ptr, v.ptr, B, H, Sq, Sk, 64, window,
+                                         scale, o.ptr, o1.ptr, o2.ptr, l1.ptr, l2.ptr))
+    return o, o1, o2, l1, l2
+
+
+def attn_bwd(ctx, q1, k1, q2, k2, v, o1, o2, l1, l2, dO, B, H, Sq, Sk, window=0, scale=0.125):
+    """dO f32 device [B][Sq][H*64]; returns dict of f32 device gradients"""
+    BH = B * H
+    dOh, dn = ctx.empty((BH, Sq, 64), np.uint16), ctx.empty((2, BH, Sq))
+    g = {k: ctx.empty((BH, Sq if k in ("dq1", "dq2") else Sk, 64)) for k in ("dq1", "dk1", "dq2", "dk2", "dv")}
+    ctx.check(ctx.lib.sa3k_diff_attn_bwd(ctx.h, q1.ptr, k1.ptr, q2.ptr, k2.ptr, v.ptr, o1.ptr, o2.ptr, l1.ptr, l2.ptr,
+                                         dO.ptr, B, H, Sq, Sk, 64, window, scale, dOh.ptr, dn.ptr, g["dq1"].ptr,
+                                         g["dk1"].ptr, g["dq2"].ptr, g["dk2"].ptr, g["dv"].ptr))
+    return g

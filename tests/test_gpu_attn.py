@@ -1,0 +1,61 @@
+"""K5: flash differential attention on the GPU vs the oracle (bf16 operands, fp32 accumulation).
+
+Inputs are rounded to bf16 before the oracle sees them, so the comparison measures the kernel's
+arithmetic (bf16 P in the PV / dS products, fp32 accumulation) against a double-precision
+restatement: outputs within 2e-2 normwise relative error and cosine >= 0.9999. Shapes cover the
+DiT block's self-attention (64 memory + T tokens), its cross-attention to the conditioning tokens,
+ragged lengths, the banded window and a single-key window (closed form: O = 0)."""
+import numpy as np
+import pytest
+
+from conftest import bf16_bits, bf16_round, cosine, oracle, rel_err, rng, sa3k
+
+pytestmark = pytest.mark.gpu
+
+
+def run(ctx, B, H, Sq, Sk, window, seed=0, check_bwd=True):
+    r = rng(seed)
+    X = {k: bf16_round(r.normal(0, 1, (B * H, Sq if k in ("q1", "q2") else Sk, 64)).astype(np.float32))
+         for k in ("q1", "k1", "q2", "k2", "v")}
+    dO = r.normal(0, 1, (B, Sq, H * 64)).astype(np.float32)
+    dev = {k: ctx.upload(bf16_bits(v)) for k, v in X.items()}
+    o, o1, o2, l1, l2 = sa3k.attn_fwd(ctx, dev["q1"], dev["k1"], dev["q2"], dev["k2"], dev["v"], B, H, Sq, Sk, window)
+    ref = oracle.diff_attn_fwd(X["q1"], X["k1"], X["q2"], X["k2"], X["v"], 0.125, window)
+    got_o = (o.numpy().astype(np.uint32) << 16).view(np.float32).reshape(B, Sq, H, 64).transpose(0, 2, 1, 3)
+    ref_o = ref["O"].reshape(B, H, Sq, 64)
+    assert rel_err(got_o, ref_o) < 2e-2 and cosine(got_o, ref_o) >= 0.9999
+    np.testing.assert_allclose(l1.numpy() / np.log2(np.e), ref["lse1"], rtol=0, atol=2e-2)
+    if not check_bwd:
+        return
+    dOd = ctx.upload(dO)
+    g = sa3k.attn_bwd(ctx, dev["q1"], dev["k1"], dev["q2"], dev["k2"], dev["v"], o1, o2, l1, l2, dOd, B, H, Sq, Sk,
+                      window)
+    dOh = dO.reshape(B, Sq, H, 64).transpose(0, 2, 1, 3).reshape(B * H, Sq, 64)
+    rb = oracle.diff_attn_bwd(X["q1"], X["k1"], X["q2"], X["k2"], X["v"], bf16_round(dOh), 0.125, window)
+    for k in ("dq1", "dk1", "dq2", "dk2", "dv"):
+        got, want = g[k].numpy(), rb["d" + k[1:].upper()[:1] + k[2:]] if False else rb[{"dq1": "dQ1", "dk1": "dK1", "dq2": "dQ2", "dk2": "dK2", "dv": "dV"}[k]]
+        assert rel_err(got, want) < 2e-2 and cosine(got, want) >= 0.9999, (k, rel_err(got, want), cosine(got, want))
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,window", [
+    (1, 2, 64, 64, 0), (1, 3, 100, 100, 0), (2, 2, 200, 37, 0), (1, 2, 256, 256, 64), (1, 1, 130, 130, 16),
+    (2, 24, 1088, 128, 0), (1, 4, 1088, 1088, 256),
+])
+def test_attention_matches_oracle(ctx, B, H, Sq, Sk, window):
+    run(ctx, B, H, Sq, Sk, window, seed=Sq + Sk + window)
+
+
+def test_attention_single_key_window(ctx):
+    # window 1: every query sees only its own key, so both branches return V and O = 0
+    B, H, S = 1, 2, 96
+    r = rng(5)
+    X = [ctx.upload(bf16_bits(r.normal(0, 1, (B * H, S, 64)).astype(np.float32))) for _ in range(5)]
+    o, o1, o2, l1, l2 = sa3k.attn_fwd(ctx, *X, B, H, S, S, window=1)
+    assert np.max(np.abs((o.numpy().astype(np.uint32) << 16).view(np.float32))) == 0.0
+    assert np.array_equal(o1.numpy(), X[4].numpy())
+
+
+@pytest.mark.parametrize("B,H,S", [(2, 24, 1088)])
+def test_attention_full_block_forward(ctx, B, H, S):
+    # the block's dense self-attention at full size (64 memory + 1024 latent tokens, batch 2)
+    run(ctx, B, H, S, S, 0, seed=9, check_bwd=False)
