@@ -186,21 +186,6 @@ dvec headmajor(const dvec& tm, int B, int H, int Sx) {
 
 extern "C" {
 
-struct orc_block {
-    int B, S, Ctx, dim, heads, inner, rope_dims, window;
-    float rope_base, norm_eps, qk_eps;
-    const float *ssg, *pre_g, *cross_g, *ff_g, *sq_g, *sk_g, *cq_g, *ck_g;
-    // 7 targets: 0 self.qkv, 1 self.out, 2 cross.q, 3 cross.kv, 4 cross.out, 5 ff.proj, 6 ff.out
-    const float* W[7];
-    const float* bias[7];
-    const float* A[7];
-    const float* Bm[7];
-    const float* mag[7];
-    const float* bnsq[7];
-    int rank, dora;
-    float scale;
-};
-
 static Lin mk(const orc_block* p, int t) {
     const int dim = p->dim;
     const int ins[7] = {dim, dim, dim, dim, dim, dim, p->inner};

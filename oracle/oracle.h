@@ -86,6 +86,25 @@ void orc_diff_attn_bwd(const float* Q1, const float* K1, const float* Q2, const 
                        const float* dO, int BH, int Sq, int Sk, int D, float scale, int window, float* dQ1,
                        float* dK1, float* dQ2, float* dK2, float* dV);
 
+/* ---- one DiT block (src/dit.h:164-266), batch-major tokens [B][S][dim] ---- */
+typedef struct orc_block {
+    int B, S, Ctx, dim, heads, inner, rope_dims, window;
+    float rope_base, norm_eps, qk_eps;
+    const float *ssg, *pre_g, *cross_g, *ff_g, *sq_g, *sk_g, *cq_g, *ck_g;
+    /* 7 targets: 0 self.qkv, 1 self.out, 2 cross.q, 3 cross.kv, 4 cross.out, 5 ff.proj, 6 ff.out */
+    const float* W[7];
+    const float* bias[7];
+    const float* A[7];
+    const float* Bm[7];
+    const float* mag[7];
+    const float* bnsq[7];
+    int rank, dora;
+    float scale;
+} orc_block;
+void orc_block_fwd(const orc_block* p, const float* x, const float* ctx, const float* gcond, float* out);
+void orc_block_bwd(const orc_block* p, const float* x, const float* ctx, const float* gcond, const float* dout,
+                   float* dx, float* dctx, float* dgcond, float* const* dA, float* const* dB, float* const* dm);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus
