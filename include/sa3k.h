@@ -239,6 +239,64 @@ SA3K_API int sa3k_diff_attn_bwd(sa3k_ctx* ctx, const void* q1, const void* k1, c
                                 void* scratch_dOh, float* scratch_dn, float* dq1, float* dk1, float* dq2, float* dk2,
                                 float* dv);
 
+/* ---------------------------------------------------------------- C3: one DiT block */
+
+/* Shape of a (differential) DiT block, the DitConfig fields dit_block reads (src/dit.h:20-46). */
+typedef struct {
+    int dim;          /* model width = heads * head_dim */
+    int heads;
+    int head_dim;     /* 64 */
+    int inner;        /* feed-forward inner width (ff.proj has 2*inner outputs: value | gate) */
+    int rope_dims;    /* DitConfig::rot, rotary dims per head (NEOX pairs i, i + rope_dims/2) */
+    int window;       /* self-attention window (0 dense, the reference); see sa3k_diff_attn_fwd */
+    float rope_base;
+    float norm_eps;
+    float qk_eps;
+} sa3k_block_config;
+
+/* Frozen block tensors in host memory. Targets: 0 self.qkv [5*dim][dim], 1 self.out [dim][dim],
+ * 2 cross.q [2*dim][dim], 3 cross.kv [3*dim][dim], 4 cross.out [dim][dim], 5 ff.proj
+ * [2*inner][dim], 6 ff.out [dim][inner]; W[t] of GGUF type weight_type, bias[t] f32 or NULL.
+ * ssg [6][dim] = the scale/shift/gate table (sc_a, sh_a, g_a, sc_f, sh_f, g_f); *_g are the
+ * norm gammas (pre/cross/ff [dim], self q/k and cross q/k per-head [64]). */
+typedef struct {
+    int weight_type;
+    const void* W[7];
+    const float* bias[7];
+    const float *ssg, *pre_g, *cross_g, *ff_g, *sq_g, *sk_g, *cq_g, *ck_g;
+} sa3k_block_weights;
+
+typedef struct sa3k_block sa3k_block;        /* frozen weights + 7 adapted linears */
+typedef struct sa3k_block_ws sa3k_block_ws;  /* activations of one forward, backward scratch */
+
+/* Upload a block's frozen tensors, build its 7 bf16-precision adapted linears (rank 0 = plain
+ * mul_mat) with scratch for max_tokens latent rows (max_ctx_tokens rows for cross.kv), and compute
+ * every target's base_norm_sq (eps 1e-12) for dora. */
+SA3K_API int sa3k_block_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, const sa3k_block_weights* w,
+                               int rank, int64_t max_tokens, int64_t max_ctx_tokens, sa3k_block** out);
+SA3K_API int sa3k_block_destroy(sa3k_ctx* ctx, sa3k_block* b);
+/* Device pointer to target t's base_norm_sq [out] (owned by the block). */
+SA3K_API int sa3k_block_base_norm_sq(sa3k_ctx* ctx, const sa3k_block* b, int target, const float** nsq);
+/* Workspace for a batch of B samples of S latent tokens (memory tokens included) and Ctx context
+ * tokens; one workspace can serve every block of a stack (it holds one block's activations). */
+SA3K_API int sa3k_block_ws_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, int B, int S, int Ctx,
+                                  sa3k_block_ws** out);
+SA3K_API int sa3k_block_ws_destroy(sa3k_ctx* ctx, sa3k_block_ws* ws);
+/* Bind the adapters: A[t] [rank][in], B[t] [out][rank], mag[t] [out] (dora) device f32, same
+ * contract as sa3k_lin_prepare. */
+SA3K_API int sa3k_block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* B,
+                                const float* const* mag, float scale, int dora);
+/* dit_block (src/dit.h:164-266) forward: x, out [B][S][dim], context [B][Ctx][dim], gcond
+ * [B][6*dim], all f32 device. x and context must stay unchanged until the matching backward. */
+SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* ws, const float* x,
+                                const float* context, const float* gcond, float* out);
+/* Backward of the last sa3k_block_forward on ws: dx [B][S][dim] is written; dcontext
+ * [B][Ctx][dim] and dgcond [B][6*dim] are ADDED to (they are shared by every block of a stack);
+ * dA/dB/dm[t] accumulate as in sa3k_lin_backward (dm may be NULL for lora). */
+SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* ws, const float* dout, float* dx,
+                                 float* dcontext, float* dgcond, float* const* dA, float* const* dB,
+                                 float* const* dm);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,615 @@
+// One DiT block forward and backward on the GPU (dit_block, src/dit.h:164-266, autodiff_safe).
+//
+// The block is the seven adapted linears (lora.hip), the two differential attentions (attn.hip)
+// and the element-wise / row-wise ops between them, which are the kernels of this file:
+//   norm_fwd/bwd     rms_norm * gamma (+ adaLN modulation h*(1+sc)+sh)       (src/nn.h:40-42, dit.h:177-185)
+//   prep_fwd/bwd     per-head rms q/k-norm + partial NEOX RoPE, head-major re-layout
+//                                                                            (src/dit.h:194-217, nn.h:53-59)
+//   gate_res         x + y * sigmoid(1 - g)                                  (src/dit.h:186-193, 223, 265)
+//   swiglu           val * silu(glu)                                         (src/dit.h:259-263)
+//   colred           per-sample column sums of the modulation/gate gradients (d gcond)
+// Batch-major tokens: x is [B][S][dim], S = memory tokens + latent frames, RoPE position = index
+// in S (src/train_loop.h:229-230). The backward of a block consumes the activations its own most
+// recent forward left in the workspace, which is how the gradient-checkpointed runner uses it
+// (recompute block l, then backprop it; src/train_ckpt.h:386-431).
+#include "gemm.h"
+
+#include <cmath>
+#include <vector>
+
+using namespace sa3k;
+
+// attn.hip
+namespace sa3k {
+void attn_forward(sa3k_ctx*, const bf16*, const bf16*, const bf16*, const bf16*, const bf16*, int, int, int, int, int,
+                  float, bf16*, bf16*, bf16*, float*, float*);
+void attn_backward(sa3k_ctx*, const bf16*, const bf16*, const bf16*, const bf16*, const bf16*, const bf16*,
+                   const bf16*, const float*, const float*, const float*, int, int, int, int, int, float, bf16*,
+                   float*, float*, float*, float*, float*, float*, float*);
+}
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int HD = 64;
+constexpr int NT = 7;   // adapted linears per block
+
+// call a C-ABI entry from inside another entry point: rethrow its failure
+void chk(sa3k_ctx* ctx, int rc) {
+    if (rc != SA3K_OK) sa3k_throw(rc, ctx->last_error);
+}
+
+template <class T>
+T* dalloc(size_t n) {
+    void* p = nullptr;
+    SA3K_HIP(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)));
+    return static_cast<T*>(p);
+}
+
+__device__ inline float block_sum(float v, float* sh) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = sh[0] + sh[1] + sh[2] + sh[3];
+    __syncthreads();
+    return t;
+}
+
+__device__ inline float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// ---------------------------------------------------------------- modulation vector
+// modv[b][k][c] = ssg[k*dim + c] + gcond[b][k*dim + c]   (src/dit.h:174)
+__global__ void modv_kernel(const float* __restrict__ ssg, const float* __restrict__ gcond, int64_t n, int per,
+                            float* __restrict__ modv) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) modv[i] = ssg[i % per] + gcond[i];
+}
+
+// ---------------------------------------------------------------- rms norm (+ modulation)
+// h = x * rstd * gamma [* (1 + sc) + sh]; one block per token row
+__global__ __launch_bounds__(kThreads) void norm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                            const float* __restrict__ modv, int sc_part, int S,
+                                                            int dim, float eps, bf16* __restrict__ h,
+                                                            float* __restrict__ rstd) {
+    __shared__ float sh[4];
+    const int64_t n = blockIdx.x;
+    const float* xr = x + n * dim;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < dim; c += kThreads) ss += xr[c] * xr[c];
+    ss = block_sum(ss, sh);
+    const float r = 1.0f / sqrtf(ss / dim + eps);
+    if (threadIdx.x == 0) rstd[n] = r;
+    const float* mv = modv ? modv + (n / S) * 6 * dim : nullptr;
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        float v = xr[c] * r * gamma[c];
+        if (mv) v = v * (1.0f + mv[sc_part * dim + c]) + mv[(sc_part + 1) * dim + c];
+        h[n * dim + c] = (bf16)v;
+    }
+}
+
+// dx = dres + rstd * dn * gamma - rstd^3 * x * <dn gamma, x> / dim, dn = dh * (1 + sc) (or dh);
+// dres is the residual branch's gradient
+__global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ x,
+                                                            const float* __restrict__ rstd, const float* __restrict__ gamma,
+                                                            const float* __restrict__ modv, int sc_part, int S, int dim,
+                                                            const float* __restrict__ dres, float* __restrict__ dx) {
+    __shared__ float sh[4];
+    const int64_t n = blockIdx.x;
+    const float* xr = x + n * dim;
+    const float* dr = dh + n * dim;
+    const float* mv = modv ? modv + (n / S) * 6 * dim + sc_part * dim : nullptr;
+    const float r = rstd[n];
+    float dot = 0.f;
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        const float dn = mv ? dr[c] * (1.0f + mv[c]) : dr[c];
+        dot += dn * gamma[c] * xr[c];
+    }
+    dot = block_sum(dot, sh);
+    const float k3 = r * r * r * dot / dim;
+    for (int c = threadIdx.x; c < dim; c += kThreads) {
+        const float dn = mv ? dr[c] * (1.0f + mv[c]) : dr[c];
+        dx[n * dim + c] = dres[n * dim + c] + (r * dn * gamma[c] - k3 * xr[c]);
+    }
+}
+
+// Column partial sums per sample over a chunk of rows. mode 0 (norm modulation):
+//   p0 = sum dh * x * rstd * gamma (d sc),  p1 = sum dh (d sh)
+// mode 1 (gate g, s = sigmoid(1 - g)):  p0 = -sum dout * y * s (1 - s)
+// part layout [B][nchunk][2][dim]
+__global__ __launch_bounds__(kThreads) void colred_kernel(int mode, const float* __restrict__ a,
+                                                          const float* __restrict__ x, const float* __restrict__ rstd,
+                                                          const float* __restrict__ gamma, const float* __restrict__ modv,
+                                                          int g_part, int S, int dim, int chunk, float* __restrict__ part) {
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    const int ch = blockIdx.y, b = blockIdx.z, nch = gridDim.y;
+    if (c >= dim) return;
+    const int t0 = ch * chunk, t1 = min(S, t0 + chunk);
+    float p0 = 0.f, p1 = 0.f;
+    float s = 0.f;
+    if (mode == 1) s = sigmoidf_(1.0f - modv[((int64_t)b * 6 + g_part) * dim + c]);
+    for (int t = t0; t < t1; ++t) {
+        const int64_t n = (int64_t)b * S + t;
+        const float av = a[n * dim + c];
+        if (mode == 0) {
+            p0 += av * x[n * dim + c] * rstd[n] * gamma[c];
+            p1 += av;
+        } else {
+            p0 += av * x[n * dim + c];
+        }
+    }
+    if (mode == 1) p0 *= -s * (1.0f - s);
+    float* o = part + (((int64_t)b * nch + ch) * 2) * dim;
+    o[c] = p0;
+    o[dim + c] = p1;
+}
+
+// dssg[b][part0][c] += sum_ch part[b][ch][0][c]; (mode 0) dssg[b][part0+1][c] += sum part[..][1][c]
+__global__ __launch_bounds__(kThreads) void colred_sum_kernel(const float* __restrict__ part, int nch, int dim, int B,
+                                                              int part0, int two, float* __restrict__ dssg) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= (int64_t)B * dim) return;
+    const int b = (int)(i / dim), c = (int)(i % dim);
+    float s0 = 0.f, s1 = 0.f;
+    for (int ch = 0; ch < nch; ++ch) {
+        const float* o = part + (((int64_t)b * nch + ch) * 2) * dim;
+        s0 += o[c];
+        s1 += o[dim + c];
+    }
+    dssg[((int64_t)b * 6 + part0) * dim + c] += s0;
+    if (two) dssg[((int64_t)b * 6 + part0 + 1) * dim + c] += s1;
+}
+
+// ---------------------------------------------------------------- gate + residual, add, swiglu
+// out = x + y * sigmoid(1 - g_b)
+__global__ void gate_res_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ modv,
+                                int g_part, int S, int dim, int64_t n, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / dim;
+    const int c = (int)(i - row * dim);
+    const float g = modv[((row / S) * 6 + g_part) * dim + c];
+    out[i] = x[i] + y[i] * sigmoidf_(1.0f - g);
+}
+
+// dy = dout * sigmoid(1 - g_b)
+__global__ void gate_bwd_kernel(const float* __restrict__ dout, const float* __restrict__ modv, int g_part, int S, int dim,
+                                int64_t n, float* __restrict__ dy) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / dim;
+    const int c = (int)(i - row * dim);
+    dy[i] = dout[i] * sigmoidf_(1.0f - modv[((row / S) * 6 + g_part) * dim + c]);
+}
+
+__global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t n, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+// g[n][c] = F[n][c] * silu(F[n][I + c])
+__global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int64_t n, bf16* __restrict__ g) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / I;
+    const int c = (int)(i - row * I);
+    const float val = F[row * 2 * I + c], glu = F[row * 2 * I + I + c];
+    g[i] = (bf16)(val * glu * sigmoidf_(glu));
+}
+
+__global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __restrict__ F, int I, int64_t n,
+                                  float* __restrict__ dF) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / I;
+    const int c = (int)(i - row * I);
+    const float val = F[row * 2 * I + c], glu = F[row * 2 * I + I + c];
+    const float sg = sigmoidf_(glu), d = dg[i];
+    dF[row * 2 * I + c] = d * glu * sg;
+    dF[row * 2 * I + I + c] = d * val * (sg + glu * sg * (1.0f - sg));
+}
+
+// ---------------------------------------------------------------- q/k-norm + RoPE prep
+struct PrepPart {
+    bf16* out;            // [B*H][Sx][64]
+    const float* gamma;   // [64]; null: plain copy (v)
+    int rope;
+};
+struct PrepArgs {
+    const float* in;      // [B*Sx][parts*dim]
+    int parts, Sx, H, dim, rope_dims;
+    float base, eps;
+    PrepPart p[5];
+    float* rstd;          // [B*Sx][H][parts]
+};
+
+// rotate pairs (i, i + rope/2), i < rope/2, by theta_i = pos * base^(-2i/rope); lanes = dims
+__device__ inline float rope_lane(float y, int d, int rope, float pos, float base, bool inverse) {
+    const int half = rope >> 1;
+    const int i = d < half ? d : d - half;
+    const float partner = __shfl(y, d < half ? d + half : d - half, 64);
+    if (d >= rope) return y;
+    const float th = pos * powf(base, -2.0f * (float)i / (float)rope);
+    float sn, cs;
+    sincosf(th, &sn, &cs);
+    if (inverse) sn = -sn;
+    return d < half ? y * cs - partner * sn : partner * sn + y * cs;
+}
+
+// one wave per (row, head)
+__global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int64_t rows) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int d = threadIdx.x & 63;
+    if (item >= rows * a.H) return;
+    const int64_t row = item / a.H;
+    const int h = (int)(item % a.H);
+    const int b = (int)(row / a.Sx), t = (int)(row % a.Sx);
+    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d;
+    for (int k = 0; k < a.parts; ++k) {
+        const float x = a.in[row * a.parts * a.dim + (int64_t)k * a.dim + h * HD + d];
+        float y = x;
+        if (a.p[k].gamma) {
+            float ss = x * x;
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+            const float r = 1.0f / sqrtf(ss / HD + a.eps);
+            if (d == 0) a.rstd[(row * a.H + h) * a.parts + k] = r;
+            y = x * r * a.p[k].gamma[d];
+            if (a.p[k].rope) y = rope_lane(y, d, a.rope_dims, (float)t, a.base, false);
+        }
+        a.p[k].out[ho] = (bf16)y;
+    }
+}
+
+struct PrepBwdPart {
+    const float* dy;      // [B*H][Sx][64] f32
+    const float* gamma;
+    int rope;
+};
+struct PrepBwdArgs {
+    const float* in;      // forward input [B*Sx][parts*dim] (pre-norm values)
+    int parts, Sx, H, dim, rope_dims;
+    float base;
+    PrepBwdPart p[5];
+    const float* rstd;
+    float* din;           // [B*Sx][parts*dim]
+};
+
+__global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int64_t rows) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int d = threadIdx.x & 63;
+    if (item >= rows * a.H) return;
+    const int64_t row = item / a.H;
+    const int h = (int)(item % a.H);
+    const int b = (int)(row / a.Sx), t = (int)(row % a.Sx);
+    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d;
+    for (int k = 0; k < a.parts; ++k) {
+        float g = a.p[k].dy[ho];
+        const int64_t xi = row * a.parts * a.dim + (int64_t)k * a.dim + h * HD + d;
+        if (a.p[k].gamma) {
+            if (a.p[k].rope) g = rope_lane(g, d, a.rope_dims, (float)t, a.base, true);
+            const float x = a.in[xi], gm = a.p[k].gamma[d];
+            const float r = a.rstd[(row * a.H + h) * a.parts + k];
+            float dot = g * gm * x;
+            for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+            g = r * g * gm - r * r * r * x * dot / HD;
+        }
+        a.din[xi] = g;
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------ objects
+struct sa3k_block {
+    sa3k_block_config cfg{};
+    int rank = 0;
+    int64_t max_tokens = 0, max_ctx = 0;
+    sa3k_weight* W[NT] = {};
+    sa3k_lin* L[NT] = {};
+    float* bias[NT] = {};
+    float* bnsq[NT] = {};
+    float *ssg = nullptr, *pre_g = nullptr, *cross_g = nullptr, *ff_g = nullptr;
+    float *sq_g = nullptr, *sk_g = nullptr, *cq_g = nullptr, *ck_g = nullptr;
+};
+
+struct sa3k_block_ws {
+    int B = 0, S = 0, Ctx = 0, dim = 0, H = 0, inner = 0;
+    // forward activations
+    float* modv; float* x; float* rs_a; bf16* h; float* qkv; bf16 *q1, *k1, *q2, *k2, *v; float* rq;
+    bf16* o; bf16 *o1, *o2; float *l1, *l2; float* y; float* x1; float* rs_c; bf16* hc; float* qf; float* kv;
+    float* ctxf; bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck; bf16* oc; bf16 *co1, *co2; float *cl1, *cl2;
+    float* yc; float* x2; float* rs_f; bf16* fin; float* F; bf16* g; float* yf;
+    // backward
+    float *d3, *dyf, *dg, *dF, *dfin, *dx2, *doc, *dqf, *dkv, *dhc, *dx1, *dy, *dob, *dqkv, *dh;
+    bf16* dOh; float* dn; float *dq1, *dk1, *dq2, *dk2, *dv;
+    float* dssg; float* part; int part_chunks;
+    std::vector<void*> allocs;
+};
+
+namespace {
+
+void free_ws(sa3k_block_ws* w) {
+    if (!w) return;
+    for (void* p : w->allocs) (void)hipFree(p);
+    delete w;
+}
+
+void free_block(sa3k_ctx* ctx, sa3k_block* b) {
+    if (!b) return;
+    for (int t = 0; t < NT; ++t) {
+        if (b->L[t]) sa3k_lin_destroy(ctx, b->L[t]);
+        if (b->W[t]) sa3k_weight_destroy(ctx, b->W[t]);
+        if (b->bias[t]) (void)hipFree(b->bias[t]);
+        if (b->bnsq[t]) (void)hipFree(b->bnsq[t]);
+    }
+    for (float* p : {b->ssg, b->pre_g, b->cross_g, b->ff_g, b->sq_g, b->sk_g, b->cq_g, b->ck_g})
+        if (p) (void)hipFree(p);
+    delete b;
+}
+
+void target_dims(const sa3k_block_config& c, int t, int64_t& in, int64_t& out) {
+    const int64_t d = c.dim, I = c.inner;
+    const int64_t ins[NT] = {d, d, d, d, d, d, I};
+    const int64_t outs[NT] = {5 * d, d, 2 * d, 3 * d, d, 2 * I, d};
+    in = ins[t];
+    out = outs[t];
+}
+
+inline unsigned nblk(int64_t n) { return (unsigned)ceil_div(n, kThreads); }
+inline unsigned nwave_blk(int64_t items) { return (unsigned)ceil_div(items, kThreads / 64); }
+
+// launch a kernel of this file on the context stream under a profiler scope
+template <class... KArgs, class... Args>
+void launch(sa3k_ctx* ctx, const char* name, void (*kernel)(KArgs...), dim3 grid, Args&&... args) {
+    KernelScope ks(ctx, name);
+    kernel<<<grid, kThreads, 0, ctx->stream>>>(std::forward<Args>(args)...);
+    SA3K_LAUNCHED();
+}
+
+// per-sample column reductions into dssg (deterministic: fixed chunking and summation order)
+void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const float* x, const float* rstd,
+            const float* gamma, int g_part, int part0) {
+    const int chunk = (int)ceil_div(w->S, w->part_chunks);
+    launch(ctx, "blk_colred", colred_kernel, dim3(nblk(w->dim), (unsigned)w->part_chunks, (unsigned)w->B), mode, a, x,
+           rstd, gamma, (const float*)w->modv, g_part, w->S, w->dim, chunk, w->part);
+    launch(ctx, "blk_colred", colred_sum_kernel, dim3(nblk((int64_t)w->B * w->dim)), (const float*)w->part,
+           w->part_chunks, w->dim, w->B, part0, (int)(mode == 0), w->dssg);
+}
+
+}  // namespace
+
+extern "C" {
+
+SA3K_API int sa3k_block_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, const sa3k_block_weights* wts, int rank,
+                               int64_t max_tokens, int64_t max_ctx_tokens, sa3k_block** out) {
+    return sa3k_guard(ctx, "sa3k_block_create", [&] {
+        SA3K_REQUIRE(cfg && wts && out, "null pointer");
+        *out = nullptr;
+        SA3K_REQUIRE(cfg->head_dim == HD && cfg->dim == cfg->heads * HD, "dim must be heads * 64");
+        SA3K_REQUIRE(cfg->rope_dims > 0 && cfg->rope_dims <= HD && cfg->rope_dims % 2 == 0, "rope_dims");
+        SA3K_REQUIRE(max_tokens > 0 && max_ctx_tokens > 0, "token budgets must be positive");
+        sa3k_block* b = new sa3k_block();
+        b->cfg = *cfg;
+        b->rank = rank;
+        b->max_tokens = max_tokens;
+        b->max_ctx = max_ctx_tokens;
+        try {
+            for (int t = 0; t < NT; ++t) {
+                int64_t in, o;
+                target_dims(*cfg, t, in, o);
+                SA3K_REQUIRE(wts->W[t] != nullptr, "missing block weight");
+                chk(ctx, sa3k_weight_create(ctx, wts->weight_type, in, o, wts->W[t], 0, &b->W[t]));
+                chk(ctx, sa3k_lin_create(ctx, b->W[t], rank, SA3K_PREC_BF16, t == 3 ? max_ctx_tokens : max_tokens,
+                                         &b->L[t]));
+                b->bnsq[t] = dalloc<float>((size_t)o);
+                chk(ctx, sa3k_weight_row_norm_sq(ctx, b->W[t], 1e-12f, b->bnsq[t]));
+                if (wts->bias[t]) {
+                    b->bias[t] = dalloc<float>((size_t)o);
+                    SA3K_HIP(hipMemcpyAsync(b->bias[t], wts->bias[t], o * 4, hipMemcpyHostToDevice, ctx->stream));
+                }
+            }
+            auto up = [&](const float* src, size_t n) {
+                SA3K_REQUIRE(src != nullptr, "missing block vector");
+                float* d = dalloc<float>(n);
+                SA3K_HIP(hipMemcpyAsync(d, src, n * 4, hipMemcpyHostToDevice, ctx->stream));
+                return d;
+            };
+            const size_t dim = cfg->dim;
+            b->ssg = up(wts->ssg, 6 * dim);
+            b->pre_g = up(wts->pre_g, dim);
+            b->cross_g = up(wts->cross_g, dim);
+            b->ff_g = up(wts->ff_g, dim);
+            b->sq_g = up(wts->sq_g, HD);
+            b->sk_g = up(wts->sk_g, HD);
+            b->cq_g = up(wts->cq_g, HD);
+            b->ck_g = up(wts->ck_g, HD);
+            SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        } catch (...) {
+            free_block(ctx, b);
+            throw;
+        }
+        *out = b;
+    });
+}
+
+SA3K_API int sa3k_block_destroy(sa3k_ctx* ctx, sa3k_block* b) {
+    return sa3k_guard(ctx, "sa3k_block_destroy", [&] {
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        free_block(ctx, b);
+    });
+}
+
+SA3K_API int sa3k_block_base_norm_sq(sa3k_ctx* ctx, const sa3k_block* b, int target, const float** nsq) {
+    return sa3k_guard(ctx, "sa3k_block_base_norm_sq", [&] {
+        SA3K_REQUIRE(b && nsq && target >= 0 && target < NT, "bad target");
+        *nsq = b->bnsq[target];
+    });
+}
+
+SA3K_API int sa3k_block_ws_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, int B, int S, int Ctx,
+                                  sa3k_block_ws** out) {
+    return sa3k_guard(ctx, "sa3k_block_ws_create", [&] {
+        SA3K_REQUIRE(cfg && out && B > 0 && S > 0 && Ctx > 0, "bad workspace shape");
+        *out = nullptr;
+        sa3k_block_ws* w = new sa3k_block_ws();
+        w->B = B; w->S = S; w->Ctx = Ctx; w->dim = cfg->dim; w->H = cfg->heads; w->inner = cfg->inner;
+        try {
+            const size_t N = (size_t)B * S, NC = (size_t)B * Ctx, D = cfg->dim, I = cfg->inner, H = cfg->heads;
+            const size_t BHS = (size_t)B * H * S * HD, BHC = (size_t)B * H * Ctx * HD;
+            auto F32 = [&](size_t n) { float* p = dalloc<float>(n); w->allocs.push_back(p); return p; };
+            auto B16 = [&](size_t n) { bf16* p = dalloc<bf16>(n); w->allocs.push_back(p); return p; };
+            w->modv = F32((size_t)B * 6 * D); w->x = nullptr;
+            w->rs_a = F32(N); w->h = B16(N * D); w->qkv = F32(N * 5 * D);
+            w->q1 = B16(BHS); w->k1 = B16(BHS); w->q2 = B16(BHS); w->k2 = B16(BHS); w->v = B16(BHS);
+            w->rq = F32(N * H * 5);
+            w->o = B16(N * D); w->o1 = B16(BHS); w->o2 = B16(BHS); w->l1 = F32((size_t)B * H * S); w->l2 = F32((size_t)B * H * S);
+            w->y = F32(N * D); w->x1 = F32(N * D); w->rs_c = F32(N); w->hc = B16(N * D); w->qf = F32(N * 2 * D);
+            w->kv = F32(NC * 3 * D); w->ctxf = nullptr;
+            w->cq1 = B16(BHS); w->cq2 = B16(BHS); w->ck1 = B16(BHC); w->ck2 = B16(BHC); w->cv = B16(BHC);
+            w->rcq = F32(N * H * 2); w->rck = F32(NC * H * 3);
+            w->oc = B16(N * D); w->co1 = B16(BHS); w->co2 = B16(BHS); w->cl1 = F32((size_t)B * H * S); w->cl2 = F32((size_t)B * H * S);
+            w->yc = F32(N * D); w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D); w->F = F32(N * 2 * I);
+            w->g = B16(N * I); w->yf = F32(N * D);
+            w->d3 = nullptr;
+            w->dyf = F32(N * D); w->dg = F32(N * I); w->dF = F32(N * 2 * I); w->dfin = F32(N * D); w->dx2 = F32(N * D);
+            w->doc = F32(N * D); w->dqf = F32(N * 2 * D); w->dkv = F32(NC * 3 * D); w->dhc = F32(N * D); w->dx1 = F32(N * D);
+            w->dy = F32(N * D); w->dob = F32(N * D); w->dqkv = F32(N * 5 * D); w->dh = F32(N * D);
+            w->dOh = B16(BHS); w->dn = F32((size_t)2 * B * H * S);
+            const size_t BHK = std::max(BHS, BHC);   // dK/dV of self (S keys) and cross (Ctx keys)
+            w->dq1 = F32(BHS); w->dk1 = F32(BHK); w->dq2 = F32(BHS); w->dk2 = F32(BHK); w->dv = F32(BHK);
+            w->dssg = nullptr;
+            w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
+            w->part = F32((size_t)B * w->part_chunks * 2 * D);
+        } catch (...) {
+            free_ws(w);
+            throw;
+        }
+        *out = w;
+    });
+}
+
+SA3K_API int sa3k_block_ws_destroy(sa3k_ctx* ctx, sa3k_block_ws* w) {
+    return sa3k_guard(ctx, "sa3k_block_ws_destroy", [&] {
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+        free_ws(w);
+    });
+}
+
+SA3K_API int sa3k_block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
+                                const float* const* mag, float scale, int dora) {
+    return sa3k_guard(ctx, "sa3k_block_prepare", [&] {
+        SA3K_REQUIRE(b && A && Bm && (!dora || mag), "null adapter arrays");
+        for (int t = 0; t < NT; ++t)
+            chk(ctx, sa3k_lin_prepare(ctx, b->L[t], A[t], Bm[t], scale, dora, dora ? mag[t] : nullptr,
+                                      dora ? b->bnsq[t] : nullptr));
+    });
+}
+
+SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
+                                const float* gcond, float* out) {
+    return sa3k_guard(ctx, "sa3k_block_forward", [&] {
+        SA3K_REQUIRE(b && w && x && context && gcond && out, "null pointer");
+        SA3K_REQUIRE(w->dim == b->cfg.dim && w->inner == b->cfg.inner, "workspace shape differs from the block");
+        const sa3k_block_config& c = b->cfg;
+        const int B = w->B, S = w->S, Ctx = w->Ctx, D = c.dim, H = c.heads, I = c.inner;
+        const int64_t N = (int64_t)B * S, NC = (int64_t)B * Ctx;
+        SA3K_REQUIRE(N <= b->max_tokens && NC <= b->max_ctx, "workspace exceeds the block's token budget");
+        const float scale = 1.0f / sqrtf((float)HD);
+        w->x = const_cast<float*>(x);
+        w->ctxf = const_cast<float*>(context);
+        const float* mv = w->modv;
+        launch(ctx, "blk_modv", modv_kernel, dim3(nblk((int64_t)B * 6 * D)), (const float*)b->ssg, gcond,
+               (int64_t)B * 6 * D, 6 * D, w->modv);
+        // self attention
+        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), x, (const float*)b->pre_g, mv, 0, S, D,
+               c.norm_eps, w->h, w->rs_a);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, nullptr, w->qkv));
+        PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+                    {{w->q1, b->sq_g, 1}, {w->k1, b->sk_g, 1}, {w->v, nullptr, 0}, {w->q2, b->sq_g, 1}, {w->k2, b->sk_g, 1}},
+                    w->rq};
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(N * H)), ps, N);
+        attn_forward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, B, H, S, S, c.window, scale, w->o, w->o1, w->o2, w->l1, w->l2);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, nullptr, w->y));
+        launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D)), x, (const float*)w->y, mv, 2, S, D, N * D, w->x1);
+        // cross attention
+        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), (const float*)w->x1, (const float*)b->cross_g,
+               (const float*)nullptr, 0, S, D, c.norm_eps, w->hc, w->rs_c);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, nullptr, w->qf));
+        chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
+        PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+                    {{w->cq1, b->cq_g, 0}, {w->cq2, b->cq_g, 0}, {}, {}, {}}, w->rcq};
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(N * H)), pq, N);
+        PrepArgs pk{w->kv, 3, Ctx, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+                    {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck};
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(NC * H)), pk, NC);
+        attn_forward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, B, H, S, Ctx, 0, scale, w->oc, w->co1, w->co2, w->cl1, w->cl2);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, nullptr, w->yc));
+        launch(ctx, "blk_add", add_kernel, dim3(nblk(N * D)), (const float*)w->x1, (const float*)w->yc, N * D, w->x2);
+        // feed-forward
+        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), (const float*)w->x2, (const float*)b->ff_g, mv, 3,
+               S, D, c.norm_eps, w->fin, w->rs_f);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, b->bias[5], w->F));
+        launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I)), (const float*)w->F, I, N * I, w->g);
+        chk(ctx, sa3k_lin_forward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, b->bias[6], w->yf));
+        launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D)), (const float*)w->x2, (const float*)w->yf, mv, 5, S, D,
+               N * D, out);
+    });
+}
+
+SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx,
+                                 float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm) {
+    return sa3k_guard(ctx, "sa3k_block_backward", [&] {
+        SA3K_REQUIRE(b && w && dout && dx && dcontext && dgcond && dA && dB, "null pointer");
+        SA3K_REQUIRE(w->x != nullptr, "backward needs a preceding forward on this workspace");
+        const sa3k_block_config& c = b->cfg;
+        const int B = w->B, S = w->S, Ctx = w->Ctx, D = c.dim, H = c.heads, I = c.inner;
+        const int64_t N = (int64_t)B * S, NC = (int64_t)B * Ctx;
+        const float scale = 1.0f / sqrtf((float)HD);
+        float* dmt[NT];
+        for (int t = 0; t < NT; ++t) dmt[t] = dm ? dm[t] : nullptr;
+        const float* mv = w->modv;
+        w->dssg = dgcond;   // the column reductions add each of the 6 modulation parts once
+        const int64_t nq = (int64_t)B * H * S;
+        // out = x2 + yf * s_f
+        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D)), dout, mv, 5, S, D, N * D, w->dyf);
+        colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
+        chk(ctx, sa3k_lin_backward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dyf, w->dg, 0, dA[6], dB[6], dmt[6]));
+        launch(ctx, "blk_swiglu", swiglu_bwd_kernel, dim3(nblk(N * I)), (const float*)w->dg, (const float*)w->F, I,
+               N * I, w->dF);
+        chk(ctx, sa3k_lin_backward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dF, w->dfin, 0, dA[5], dB[5], dmt[5]));
+        colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
+        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dfin, (const float*)w->x2,
+               (const float*)w->rs_f, (const float*)b->ff_g, mv, 3, S, D, dout, w->dx2);
+        // x2 = x1 + yc
+        chk(ctx, sa3k_lin_backward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->dx2, w->doc, 0, dA[4], dB[4], dmt[4]));
+        attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,
+                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
+        PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, c.rope_base,
+                       {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, w->dqf};
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(N * H)), bq, N);
+        PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, c.rope_base,
+                       {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, w->dkv};
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(NC * H)), bk, NC);
+        chk(ctx, sa3k_lin_backward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dqf, w->dhc, 0, dA[2], dB[2], dmt[2]));
+        chk(ctx, sa3k_lin_backward(ctx, b->L[3], SA3K_TYPE_F32, w->ctxf, NC, w->dkv, dcontext, 1, dA[3], dB[3], dmt[3]));
+        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dhc, (const float*)w->x1,
+               (const float*)w->rs_c, (const float*)b->cross_g, (const float*)nullptr, 0, S, D, (const float*)w->dx2,
+               w->dx1);
+        // x1 = x + y * s_a
+        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D)), (const float*)w->dx1, mv, 2, S, D, N * D, w->dy);
+        colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
+        chk(ctx, sa3k_lin_backward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dy, w->dob, 0, dA[1], dB[1], dmt[1]));
+        attn_backward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, w->o1, w->o2, w->l1, w->l2, w->dob, B, H, S, S, c.window,
+                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
+        PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, c.rope_base,
+                       {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
+                       w->rq, w->dqkv};
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(N * H)), bs, N);
+        chk(ctx, sa3k_lin_backward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, w->dqkv, w->dh, 0, dA[0], dB[0], dmt[0]));
+        colred(ctx, w, 0, w->dh, w->x, w->rs_a, b->pre_g, 0, 0);
+        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dh, (const float*)w->x,
+               (const float*)w->rs_a, (const float*)b->pre_g, mv, 0, S, D, (const float*)w->dx1, dx);
+        w->dssg = nullptr;
+    });
+}
+
+}  // extern "C"

@@ -30,6 +30,25 @@ class AdamWParams(C.Structure):
                 ("eps", C.c_float), ("weight_decay", C.c_float), ("grad_clip", C.c_float)]
 
 
+class BlockConfig(C.Structure):
+    _fields_ = [("dim", C.c_int), ("heads", C.c_int), ("head_dim", C.c_int), ("inner", C.c_int),
+                ("rope_dims", C.c_int), ("window", C.c_int), ("rope_base", C.c_float), ("norm_eps", C.c_float),
+                ("qk_eps", C.c_float)]
+
+
+class BlockWeights(C.Structure):
+    _fields_ = [("weight_type", C.c_int), ("W", C.c_void_p * 7), ("bias", C.c_void_p * 7)] + \
+               [(n, C.c_void_p) for n in ("ssg", "pre_g", "cross_g", "ff_g", "sq_g", "sk_g", "cq_g", "ck_g")]
+
+
+BLOCK_VECTORS = ("ssg", "pre_g", "cross_g", "ff_g", "sq_g", "sk_g", "cq_g", "ck_g")
+
+
+def block_target_dims(dim, inner):
+    """(in, out) of the 7 adapted linears of a block, in target order"""
+    return [(dim, 5 * dim), (dim, dim), (dim, 2 * dim), (dim, 3 * dim), (dim, dim), (dim, 2 * inner), (inner, dim)]
+
+
 def _declare(lib):
     P, I64, I, F, D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
     sig = {
@@ -66,6 +85,14 @@ def _declare(lib):
         "sa3k_lin_backward": (I, [P, P, I, P, I64, P, P, I, P, P, P]),
         "sa3k_diff_attn_fwd": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P]),
         "sa3k_diff_attn_bwd": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P, P, P]),
+        "sa3k_block_create": (I, [P, C.POINTER(BlockConfig), C.POINTER(BlockWeights), I, I64, I64, C.POINTER(P)]),
+        "sa3k_block_destroy": (I, [P, P]),
+        "sa3k_block_base_norm_sq": (I, [P, P, I, C.POINTER(P)]),
+        "sa3k_block_ws_create": (I, [P, C.POINTER(BlockConfig), I, I, I, C.POINTER(P)]),
+        "sa3k_block_ws_destroy": (I, [P, P]),
+        "sa3k_block_prepare": (I, [P, P, P, P, P, F, I]),
+        "sa3k_block_forward": (I, [P, P, P, P, P, P, P]),
+        "sa3k_block_backward": (I, [P, P, P, P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -304,6 +331,77 @@ class Lin:
         if self.h:
             self.ctx.check(self.ctx.lib.sa3k_lin_destroy(self.ctx.h, self.h))
             self.h = None
+
+
+def _ptr_array(arrs):
+    return (C.c_void_p * len(arrs))(*[a.ptr if a is not None else None for a in arrs])
+
+
+class Block:
+    """One DiT block (sa3k_block_*). W: list of 7 host arrays as accepted by Context.weight
+    (numpy [out][in], or (blocks, in, out) for Q8_0), bias: 7 host f32 arrays or None, vecs: dict
+    of the 8 block vectors (ssg, pre_g, ...)."""
+
+    def __init__(self, ctx, cfg, W, bias, vecs, rank, max_tokens, max_ctx, wtype=TYPE_F32):
+        self.ctx, self.cfg = ctx, cfg
+        self.keep = []
+        bw = BlockWeights()
+        bw.weight_type = wtype
+        for t in range(7):
+            data = np.ascontiguousarray(W[t][0] if wtype == TYPE_Q8_0 else W[t])
+            self.keep.append(data)
+            bw.W[t] = data.ctypes.data
+            if bias[t] is not None:
+                b = np.ascontiguousarray(bias[t], np.float32)
+                self.keep.append(b)
+                bw.bias[t] = b.ctypes.data
+        for n in BLOCK_VECTORS:
+            v = np.ascontiguousarray(vecs[n], np.float32)
+            self.keep.append(v)
+            setattr(bw, n, v.ctypes.data)
+        h = C.c_void_p()
+        ctx.check(ctx.lib.sa3k_block_create(ctx.h, C.byref(cfg), C.byref(bw), rank, max_tokens, max_ctx, C.byref(h)))
+        self.h = h.value
+        self.keep = []
+
+    def base_norm_sq(self, t):
+        p = C.c_void_p()
+        self.ctx.check(self.ctx.lib.sa3k_block_base_norm_sq(self.ctx.h, self.h, t, C.byref(p)))
+        return p.value
+
+    def prepare(self, A, B, scale, dora=False, mag=None):
+        self.ctx.check(self.ctx.lib.sa3k_block_prepare(self.ctx.h, self.h, _ptr_array(A), _ptr_array(B),
+                                                       _ptr_array(mag) if dora else None, scale, int(dora)))
+
+    def forward(self, ws, x, context, gcond, out):
+        # the backward reads x and context again: the workspace keeps them alive until then
+        ws.inputs = (x, context, gcond)
+        self.ctx.check(self.ctx.lib.sa3k_block_forward(self.ctx.h, self.h, ws.h, x.ptr, context.ptr, gcond.ptr, out.ptr))
+
+    def backward(self, ws, dout, dx, dcontext, dgcond, dA, dB, dm=None):
+        self.ctx.check(self.ctx.lib.sa3k_block_backward(self.ctx.h, self.h, ws.h, dout.ptr, dx.ptr, dcontext.ptr,
+                                                        dgcond.ptr, _ptr_array(dA), _ptr_array(dB),
+                                                        _ptr_array(dm) if dm is not None else None))
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_block_destroy(self.ctx.h, self.h))
+            self.h = None
+
+
+class BlockWorkspace:
+    def __init__(self, ctx, cfg, B, S, Ctx):
+        self.ctx = ctx
+        h = C.c_void_p()
+        ctx.check(ctx.lib.sa3k_block_ws_create(ctx.h, C.byref(cfg), B, S, Ctx, C.byref(h)))
+        self.h = h.value
+        self.inputs = None
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_block_ws_destroy(self.ctx.h, self.h))
+            self.h = None
+        self.inputs = None
 
 
 def attn_fwd(ctx, q1, k1, q2, k2, v, B, H, Sq, Sk, window=0, scale=0.125):

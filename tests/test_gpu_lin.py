@@ -2,7 +2,7 @@
 
 Configurations:
   * f32 LoRA linear 2048x1536 -> 1536, rank 16, alpha 16: fp32 MFMA, every output within 1e-4
-    max relative error of the oracle (elementwise, floor 1e-3 * max|ref|);
+    max relative error of the oracle (infinity-norm reading, conftest.max_rel_err);
   * DoRA linear 1536 -> 6144 over a Q8_0 base, rank 32: bf16 MFMA, outputs within 2e-2 normwise
     relative error and cosine >= 0.9999 of the oracle run on the exactly decoded Q8_0 weight;
   * smaller and ragged shapes, f16 and f32 bases, lora and dora, both precisions.
