@@ -215,9 +215,162 @@ class LinearWorkload:
                 "sample": f"{len(times)} full-size fwd+bwd of the oracle restatement (double accumulation, OpenMP)"}
 
 
+def block_flops(B, S, Ctx, dim, inner, r, window, dora=True, heads=None):
+    """Algorithmic flops of one DiT block forward and backward (dit_block, src/dit.h:164-266).
+
+    Linears: forward X W^T + the rank terms; backward dX only for the frozen base (no dW) + the
+    rank terms (dU B, (dU B) A, dU^T H, (s dU B)^T X); dora adds W A^T (forward) and B^T gn W
+    (backward). Attention: QK^T and PV per branch per kept (query, key) pair, 2 x 2 x 2 x 64
+    flops; its backward counted as twice the forward. Recompute is not counted."""
+    heads = heads or dim // 64
+    N, NC = B * S, B * Ctx
+    tg = [(dim, 5 * dim, N), (dim, dim, N), (dim, 2 * dim, N), (dim, 3 * dim, NC), (dim, dim, N),
+          (dim, 2 * inner, N), (inner, dim, N)]
+    fwd = bwd = 0.0
+    for i, o, n in tg:
+        fwd += 2.0 * n * i * o + 2.0 * n * i * r + 2.0 * n * r * o + (2.0 * r * i * o if dora else 0.0)
+        bwd += 2.0 * n * o * i + 2.0 * n * r * i + 2.0 * n * o * r * 2 + 2.0 * n * r * i + \
+            (2.0 * r * i * o if dora else 0.0)
+    q = np.arange(S)
+    if window > 0:
+        h = window // 2
+        pairs = float(np.sum(np.minimum(q + h, S - 1) - np.maximum(q - h, 0) + 1))
+    else:
+        pairs = float(S) * S
+    attn = B * heads * (pairs + S * Ctx) * 2 * 2 * 2 * 64
+    return fwd + attn, bwd + 2 * attn
+
+
+class BlockWorkload:
+    """One DiT block fwd+bwd + clip/AdamW over its adapter arena: dim 1536, 24 heads x 64, FFN
+    1536 -> 2x6144 -> 1536 (SwiGLU), batch 2 x (64 memory + 1024 latent) tokens, self-attention
+    window 256, cross-attention to 128 context tokens (already projected to 1536, N(0,1)), DoRA rank
+    32 (alpha 32) on all 7 projections, f16 base ~ N(0, 0.02); gcond ~ N(0, 0.1), dout ~ N(0, 1e-2)."""
+    name = "dit_block_1536_s1088_b2_w256_dora_r32"
+    dtype = "bf16"
+
+    def __init__(self, ctx, B=2, S=1088, Ctx=128, dim=1536, heads=24, inner=6144, r=32, window=256, seed=7):
+        sa3k = sys.modules["sa3k"]
+        self.ctx = ctx
+        self.B, self.S, self.Ctx, self.dim, self.heads, self.inner, self.r, self.window = \
+            B, S, Ctx, dim, heads, inner, r, window
+        g = rng(seed)
+        nd = lambda shape, sd: g.normal(0, sd, shape).astype(np.float32)
+        dims = sa3k.block_target_dims(dim, inner)
+        self.W_host = [nd((o, i), 0.02).astype(np.float16) for i, o in dims]
+        self.bias_host = [None] * 5 + [nd(dims[5][1], 0.02), nd(dims[6][1], 0.02)]
+        self.vecs = dict(ssg=nd(6 * dim, 0.1), pre_g=1 + nd(dim, 0.1), cross_g=1 + nd(dim, 0.1),
+                         ff_g=1 + nd(dim, 0.1), sq_g=1 + nd(64, 0.1), sk_g=1 + nd(64, 0.1), cq_g=1 + nd(64, 0.1),
+                         ck_g=1 + nd(64, 0.1))
+        self.cfg = sa3k.BlockConfig(dim, heads, 64, inner, 32, window, 1e4, 1e-5, 1e-6)
+        self.blk = sa3k.Block(ctx, self.cfg, self.W_host, self.bias_host, self.vecs, r, B * S, B * Ctx,
+                              sa3k.TYPE_F16)
+        # adapter arena: per target [A | B | m] (A Kaiming-uniform, B ~ N(0, 0.01), m = row norms)
+        sizes = [(r * i, o * r, o) for i, o in dims]
+        self.n = sum(a + b + m for a, b, m in sizes)
+        self.p, self.grad = ctx.zeros(self.n), ctx.zeros(self.n)
+        self.m, self.v = ctx.zeros(self.n), ctx.zeros(self.n)
+        self.A, self.Bm, self.mag, self.gA, self.gB, self.gm = [], [], [], [], [], []
+        self.A_host, self.B_host, self.mag_host = [], [], []
+        off = 0
+        for (i, o), (na, nb, nm), W in zip(dims, sizes, self.W_host):
+            a = g.uniform(-1 / np.sqrt(i), 1 / np.sqrt(i), (r, i)).astype(np.float32)
+            b = nd((o, r), 0.01)
+            mg = np.sqrt((W.astype(np.float64) ** 2).sum(1)).astype(np.float32)
+            for host, lst, glst, n_, shape in ((a, self.A, self.gA, na, (r, i)), (b, self.Bm, self.gB, nb, (o, r)),
+                                                (mg, self.mag, self.gm, nm, (o,))):
+                ctx.copy_into(self.p.view(off, (n_,)), host.ravel())
+                lst.append(self.p.view(off, shape))
+                glst.append(self.grad.view(off, shape))
+                off += n_
+            self.A_host.append(a)
+            self.B_host.append(b)
+            self.mag_host.append(mg)
+        self.x_host = nd((B, S, dim), 1.0)
+        self.ctx_host = nd((B, Ctx, dim), 1.0)
+        self.gc_host = nd((B, 6 * dim), 0.1)
+        self.dout_host = nd((B, S, dim), 1e-2)
+        self.x, self.cx, self.gc = ctx.upload(self.x_host), ctx.upload(self.ctx_host), ctx.upload(self.gc_host)
+        self.dout = ctx.upload(self.dout_host)
+        self.out, self.dx = ctx.empty((B, S, dim)), ctx.empty((B, S, dim))
+        self.dctx, self.dgc = ctx.zeros((B, Ctx, dim)), ctx.zeros((B, 6 * dim))
+        self.ws = sa3k.BlockWorkspace(ctx, self.cfg, B, S, Ctx)
+        self.hp = (1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0)
+        self.k = 0
+
+    def step(self):
+        self.k += 1
+        c = self.ctx
+        self.blk.prepare(self.A, self.Bm, 1.0, True, self.mag)
+        c.check(c.lib.sa3k_memset(c.h, self.grad.ptr, 0, self.grad.nbytes))
+        self.blk.forward(self.ws, self.x, self.cx, self.gc, self.out)
+        self.blk.backward(self.ws, self.dout, self.dx, self.dctx, self.dgc, self.gA, self.gB, self.gm)
+        c.adamw_clip(self.p, self.grad, self.m, self.v, self.hp, self.k, 1)
+
+    def flops(self):
+        return block_flops(self.B, self.S, self.Ctx, self.dim, self.inner, self.r, self.window)
+
+    def config(self):
+        return {"workload": self.name, "batch": self.B, "tokens_per_sample": self.S, "memory_tokens": 64,
+                "context_tokens": self.Ctx, "dim": self.dim, "heads": self.heads, "ffn_inner": self.inner,
+                "window": self.window, "rank": self.r, "adapter": "dora-rows", "base": "f16"}
+
+    def roofline(self, prof, steps):
+        return gemm_roofline(prof, steps, self.lin_flops())
+
+    def lin_flops(self):
+        """per kernel name: algorithmic flops summed over one step's launches"""
+        B, S, Ctx, dim, inner, r = self.B, self.S, self.Ctx, self.dim, self.inner, self.r
+        N, NC = B * S, B * Ctx
+        tg = [(dim, 5 * dim, N), (dim, dim, N), (dim, 2 * dim, N), (dim, 3 * dim, NC), (dim, dim, N),
+              (dim, 2 * inner, N), (inner, dim, N)]
+        return {"lin_fwd_main": sum(2.0 * n * i * o + 2.0 * n * r * o for i, o, n in tg),
+                "lin_bwd_dx": sum(2.0 * n * o * i + 2.0 * n * r * i + 2.0 * r * i * o for i, o, n in tg)}
+
+    def extra(self, ms_per_step):
+        fwd, bwd = self.flops()
+        return {"algorithmic_gflop_per_update": round((fwd + bwd) / 1e9, 2),
+                "tflops_whole_update": round((fwd + bwd) / (ms_per_step * 1e-3) / 1e12, 1)}
+
+    def cpu_baseline(self):
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        bb = _load("block_binding", os.path.join(ROOT, "oracle", "block_binding.py"))
+        S_s = 136   # bounded sample: 64 memory + 72 latent tokens per sample, same weights
+        cfg = dict(B=self.B, S=S_s, Ctx=self.Ctx, dim=self.dim, heads=self.heads, inner=self.inner,
+                   window=self.window, rank=self.r, alpha=32.0, dora=True)
+        W = [w.astype(np.float32) for w in self.W_host]
+        w = dict(self.vecs, W=W, bias=self.bias_host, A=self.A_host, B=self.B_host, mag=self.mag_host,
+                 bnsq=[((x.astype(np.float64) ** 2).sum(1) + x.shape[1] * 1e-12).astype(np.float32) for x in W])
+        x, dout = self.x_host[:, :S_s], self.dout_host[:, :S_s]
+        t0 = time.perf_counter()
+        bb.block_bwd(cfg, w, x, self.ctx_host, self.gc_host, dout)   # forward + backward
+        dt = time.perf_counter() - t0
+        f_s = sum(block_flops(self.B, S_s, self.Ctx, self.dim, self.inner, self.r, self.window))
+        f_full = sum(self.flops())
+        return {"value": round(dt * f_full / f_s * 1e3, 1), "unit": "ms/update (fwd+bwd, scaled by algorithmic flops)",
+                "cores": bb.lib().orc_num_threads(), "kind": "port",
+                "sample": f"one fwd+bwd of the oracle block at S={S_s} (batch {self.B}) in {dt:.1f} s, scaled "
+                          f"by the algorithmic flop ratio {f_full / f_s:.2f}"}
+
+
+def gemm_roofline(prof, steps, flops_per_step):
+    """roofline of the GEMM kernel with the largest total time: its algorithmic flops per step
+    over its measured time per step (= flops per launch / average launch duration)"""
+    k = max(flops_per_step, key=lambda n: prof.get(n, (1, 0.0))[1])
+    cnt, ms = prof[k]
+    per_step_ms = ms / steps
+    ach = flops_per_step[k] / (per_step_ms * 1e-3) / 1e12
+    return {"kernel": k, "bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "avg_launch_ms": round(ms / cnt, 5), "launches_per_step": cnt // steps,
+            "algorithmic_flops_per_launch": flops_per_step[k] / max(cnt // steps, 1)}
+
+
 WORKLOADS = {"adamw": AdamWWorkload,
              "dora_linear": lambda ctx: LinearWorkload(ctx, "dora_q8"),
-             "lora_linear": lambda ctx: LinearWorkload(ctx, "lora_f32")}
+             "lora_linear": lambda ctx: LinearWorkload(ctx, "lora_f32"),
+             "block": BlockWorkload}
 DEFAULT = "dora_linear"
 
 

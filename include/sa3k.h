@@ -211,7 +211,8 @@ SA3K_API int sa3k_lin_forward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const void
  *   dB += s dU^T (X A^T) + 2s diag(gn) W A^T + 2s^2 diag(gn) B A A^T
  *   dm += gd / sqrt(nsq)                    (gd = sum_n dY * U, gn = -gd m nsq^-3/2 / 2; dora only)
  * dA [rank][in], dB [out][rank], dm [out] are f32 accumulators (the micro-batch sum of
- * train_accum_add, src/train_loop.h:75-78). dX may be NULL (no input gradient). */
+ * train_accum_add, src/train_loop.h:75-78). dX may be NULL (no input gradient). With rank 0 the
+ * linear is a plain mul_mat and only dX = dY W is computed (dA/dB/dm may be NULL). */
 SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const void* X, int64_t N,
                                const float* dY, float* dX, int dx_accumulate, float* dA, float* dB,
                                float* dm);

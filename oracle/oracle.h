@@ -105,6 +105,35 @@ void orc_block_fwd(const orc_block* p, const float* x, const float* ctx, const f
 void orc_block_bwd(const orc_block* p, const float* x, const float* ctx, const float* gcond, const float* dout,
                    float* dx, float* dctx, float* dgcond, float* const* dA, float* const* dB, float* const* dm);
 
+/* ---- the whole DiT training loss (dit_head / dit_block x depth / dit_tail, src/dit.h:269-338,
+ * loss src/train_dit.h:174-184), batch-major ---- */
+typedef struct orc_lin {
+    const float *W, *bias, *A, *B, *mag, *bnsq;   /* A/B NULL: no adapter (plain mul_mat) */
+    int in, out;
+} orc_lin;
+/* head/tail linears, in this order */
+enum { ORC_PRE_CONV, ORC_PROJ_IN, ORC_TIME0, ORC_TIME2, ORC_GLOBAL0, ORC_GLOBAL2, ORC_GCE0, ORC_GCE2,
+       ORC_COND0, ORC_COND2, ORC_PROJ_OUT, ORC_POST_CONV, ORC_NHEAD };
+typedef struct orc_dit {
+    int B, T, Ctx, io, dim, heads, inner, depth, mem, cond_dim, time_dim, rope_dims, window;
+    float rope_base, norm_eps, qk_eps, time_min_freq, time_max_freq;
+    const orc_block* blocks;     /* depth blocks: W/bias/vectors/adapters (their B/S/Ctx are ignored) */
+    orc_lin head[ORC_NHEAD];
+    const float* memory_tokens;  /* [mem][dim] */
+    int rank, dora;
+    float scale;
+} orc_dit;
+/* Forward to the per-sample losses (loss [B]) and, if dA_* is non-NULL, the backward: adapter
+ * gradients of sum_b loss_b ADDED to dA/dB/dm (blocks: [depth*7], head: [ORC_NHEAD], entries of
+ * un-adapted linears ignored). x_t, target [B][T][io]; t [B]; cross [B][Ctx][cond_dim]; glob
+ * [B][cond_dim]; loss_weight [B][T] or NULL (uniform 1/(io*T)); velocity [B][T][io] nullable. */
+void orc_dit_loss(const orc_dit* p, const float* x_t, const float* target, const float* t, const float* cross,
+                  const float* glob, const float* loss_weight, float* velocity, double* loss,
+                  float* const* dA_blocks, float* const* dB_blocks, float* const* dm_blocks,
+                  float* const* dA_head, float* const* dB_head, float* const* dm_head);
+/* ExpoFourierFeatures of t into out[dim] (expo_features, src/sa3_pipeline.h:57-67) */
+void orc_expo_features(float t, float* out, int dim, float min_f, float max_f);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

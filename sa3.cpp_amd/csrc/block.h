@@ -1,0 +1,58 @@
+// One DiT block (block.hip): frozen weights + 7 adapted linears, and the workspace holding one
+// forward's activations. Shared by the C ABI in block.hip and the stack runner in dit.hip.
+#pragma once
+
+#include "gemm.h"
+
+#include <vector>
+
+struct sa3k_block {
+    static constexpr int NT = 7;   // 0 self.qkv, 1 self.out, 2 cross.q, 3 cross.kv, 4 cross.out, 5 ff.proj, 6 ff.out
+    sa3k_block_config cfg{};
+    int rank = 0;
+    int64_t max_tokens = 0, max_ctx = 0;
+    sa3k_weight* W[NT] = {};
+    sa3k_lin* L[NT] = {};
+    float* bias[NT] = {};
+    float* bnsq[NT] = {};
+    float *ssg = nullptr, *pre_g = nullptr, *cross_g = nullptr, *ff_g = nullptr;
+    float *sq_g = nullptr, *sk_g = nullptr, *cq_g = nullptr, *ck_g = nullptr;
+};
+
+struct sa3k_block_ws {
+    int B = 0, S = 0, Ctx = 0, dim = 0, H = 0, inner = 0;
+    // forward activations (read again by the backward)
+    float* modv; const float* x; float* rs_a; sa3k::bf16* h; float* qkv;
+    sa3k::bf16 *q1, *k1, *q2, *k2, *v; float* rq;
+    sa3k::bf16* o; sa3k::bf16 *o1, *o2; float *l1, *l2; float* y; float* x1; float* rs_c; sa3k::bf16* hc;
+    float* qf; float* kv; const float* ctxf; sa3k::bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck;
+    sa3k::bf16* oc; sa3k::bf16 *co1, *co2; float *cl1, *cl2; float* x2; float* rs_f; sa3k::bf16* fin; float* F;
+    sa3k::bf16* g; float* yf;
+    // scratch of the forward (yc) and the backward: may be shared by several workspaces that are
+    // used one at a time on the same stream
+    float* yc;
+    float *dyf, *dg, *dF, *dfin, *dx2, *doc, *dqf, *dkv, *dhc, *dx1, *dy, *dob, *dqkv, *dh;
+    sa3k::bf16* dOh; float* dn; float *dq1, *dk1, *dq2, *dk2, *dv;
+    float* dssg; float* part; int part_chunks;
+    std::vector<void*> allocs;
+};
+
+namespace sa3k {
+
+// W[t] (type weight_type), bias[t] (f32 or null) and vecs = {ssg, pre_g, cross_g, ff_g, sq_g, sk_g,
+// cq_g, ck_g} in host (on_device = 0) or device memory.
+sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_type, const void* const* W,
+                        const float* const* bias, const float* const* vecs, int on_device, int rank,
+                        int64_t max_tokens, int64_t max_ctx);
+void block_free(sa3k_ctx* ctx, sa3k_block* b);
+// share_scratch: take the forward/backward scratch of another workspace of the same shape
+sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share_scratch);
+void block_ws_free(sa3k_block_ws* w);
+void block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
+                   const float* const* mag, float scale, int dora);
+void block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
+                   const float* gcond, float* out);
+void block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx, float* dcontext,
+                    float* dgcond, float* const* dA, float* const* dB, float* const* dm);
+
+}  // namespace sa3k

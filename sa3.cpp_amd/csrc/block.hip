@@ -10,9 +10,10 @@
 //   colred           per-sample column sums of the modulation/gate gradients (d gcond)
 // Batch-major tokens: x is [B][S][dim], S = memory tokens + latent frames, RoPE position = index
 // in S (src/train_loop.h:229-230). The backward of a block consumes the activations its own most
-// recent forward left in the workspace, which is how the gradient-checkpointed runner uses it
-// (recompute block l, then backprop it; src/train_ckpt.h:386-431).
-#include "gemm.h"
+// recent forward left in the workspace: the stack runner either keeps one workspace per block, or
+// recomputes block l into a shared one right before its backward (the gradient-checkpointed
+// schedule of src/train_ckpt.h:386-431).
+#include "block.h"
 
 #include <cmath>
 #include <vector>
@@ -299,52 +300,7 @@ __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int64
 }  // namespace
 
 // ------------------------------------------------------------------------------------ objects
-struct sa3k_block {
-    sa3k_block_config cfg{};
-    int rank = 0;
-    int64_t max_tokens = 0, max_ctx = 0;
-    sa3k_weight* W[NT] = {};
-    sa3k_lin* L[NT] = {};
-    float* bias[NT] = {};
-    float* bnsq[NT] = {};
-    float *ssg = nullptr, *pre_g = nullptr, *cross_g = nullptr, *ff_g = nullptr;
-    float *sq_g = nullptr, *sk_g = nullptr, *cq_g = nullptr, *ck_g = nullptr;
-};
-
-struct sa3k_block_ws {
-    int B = 0, S = 0, Ctx = 0, dim = 0, H = 0, inner = 0;
-    // forward activations
-    float* modv; float* x; float* rs_a; bf16* h; float* qkv; bf16 *q1, *k1, *q2, *k2, *v; float* rq;
-    bf16* o; bf16 *o1, *o2; float *l1, *l2; float* y; float* x1; float* rs_c; bf16* hc; float* qf; float* kv;
-    float* ctxf; bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck; bf16* oc; bf16 *co1, *co2; float *cl1, *cl2;
-    float* yc; float* x2; float* rs_f; bf16* fin; float* F; bf16* g; float* yf;
-    // backward
-    float *d3, *dyf, *dg, *dF, *dfin, *dx2, *doc, *dqf, *dkv, *dhc, *dx1, *dy, *dob, *dqkv, *dh;
-    bf16* dOh; float* dn; float *dq1, *dk1, *dq2, *dk2, *dv;
-    float* dssg; float* part; int part_chunks;
-    std::vector<void*> allocs;
-};
-
 namespace {
-
-void free_ws(sa3k_block_ws* w) {
-    if (!w) return;
-    for (void* p : w->allocs) (void)hipFree(p);
-    delete w;
-}
-
-void free_block(sa3k_ctx* ctx, sa3k_block* b) {
-    if (!b) return;
-    for (int t = 0; t < NT; ++t) {
-        if (b->L[t]) sa3k_lin_destroy(ctx, b->L[t]);
-        if (b->W[t]) sa3k_weight_destroy(ctx, b->W[t]);
-        if (b->bias[t]) (void)hipFree(b->bias[t]);
-        if (b->bnsq[t]) (void)hipFree(b->bnsq[t]);
-    }
-    for (float* p : {b->ssg, b->pre_g, b->cross_g, b->ff_g, b->sq_g, b->sk_g, b->cq_g, b->ck_g})
-        if (p) (void)hipFree(p);
-    delete b;
-}
 
 void target_dims(const sa3k_block_config& c, int t, int64_t& in, int64_t& out) {
     const int64_t d = c.dim, I = c.inner;
@@ -377,6 +333,130 @@ void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const flo
 
 }  // namespace
 
+namespace sa3k {
+
+void block_free(sa3k_ctx* ctx, sa3k_block* b) {
+    if (!b) return;
+    for (int t = 0; t < NT; ++t) {
+        if (b->L[t]) sa3k_lin_destroy(ctx, b->L[t]);
+        if (b->W[t]) sa3k_weight_destroy(ctx, b->W[t]);
+        if (b->bias[t]) (void)hipFree(b->bias[t]);
+        if (b->bnsq[t]) (void)hipFree(b->bnsq[t]);
+    }
+    for (float* p : {b->ssg, b->pre_g, b->cross_g, b->ff_g, b->sq_g, b->sk_g, b->cq_g, b->ck_g})
+        if (p) (void)hipFree(p);
+    delete b;
+}
+
+sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_type, const void* const* W,
+                        const float* const* bias, const float* const* vecs, int on_device, int rank,
+                        int64_t max_tokens, int64_t max_ctx) {
+    SA3K_REQUIRE(cfg.head_dim == HD && cfg.dim == cfg.heads * HD, "dim must be heads * 64");
+    SA3K_REQUIRE(cfg.rope_dims > 0 && cfg.rope_dims <= HD && cfg.rope_dims % 2 == 0, "rope_dims");
+    SA3K_REQUIRE(cfg.inner > 0 && cfg.window >= 0, "inner / window");
+    SA3K_REQUIRE(max_tokens > 0 && max_ctx > 0, "token budgets must be positive");
+    sa3k_block* b = new sa3k_block();
+    b->cfg = cfg;
+    b->rank = rank;
+    b->max_tokens = max_tokens;
+    b->max_ctx = max_ctx;
+    try {
+        for (int t = 0; t < NT; ++t) {
+            int64_t in, o;
+            target_dims(cfg, t, in, o);
+            SA3K_REQUIRE(W[t] != nullptr, "missing block weight");
+            chk(ctx, sa3k_weight_create(ctx, weight_type, in, o, W[t], on_device, &b->W[t]));
+            chk(ctx, sa3k_lin_create(ctx, b->W[t], rank, SA3K_PREC_BF16, t == 3 ? max_ctx : max_tokens, &b->L[t]));
+            b->bnsq[t] = dalloc<float>((size_t)o);
+            chk(ctx, sa3k_weight_row_norm_sq(ctx, b->W[t], 1e-12f, b->bnsq[t]));
+            if (bias && bias[t]) {
+                b->bias[t] = dalloc<float>((size_t)o);
+                SA3K_HIP(hipMemcpyAsync(b->bias[t], bias[t], o * 4, hipMemcpyDefault, ctx->stream));
+            }
+        }
+        const size_t dim = cfg.dim;
+        const size_t len[8] = {6 * dim, dim, dim, dim, HD, HD, HD, HD};
+        float** dst[8] = {&b->ssg, &b->pre_g, &b->cross_g, &b->ff_g, &b->sq_g, &b->sk_g, &b->cq_g, &b->ck_g};
+        for (int i = 0; i < 8; ++i) {
+            SA3K_REQUIRE(vecs[i] != nullptr, "missing block vector");
+            *dst[i] = dalloc<float>(len[i]);
+            SA3K_HIP(hipMemcpyAsync(*dst[i], vecs[i], len[i] * 4, hipMemcpyDefault, ctx->stream));
+        }
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    } catch (...) {
+        block_free(ctx, b);
+        throw;
+    }
+    return b;
+}
+
+void block_ws_free(sa3k_block_ws* w) {
+    if (!w) return;
+    for (void* p : w->allocs) (void)hipFree(p);
+    delete w;
+}
+
+sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share) {
+    SA3K_REQUIRE(B > 0 && S > 0 && Ctx > 0, "bad workspace shape");
+    SA3K_REQUIRE(!share || (share->B == B && share->S == S && share->Ctx == Ctx && share->dim == cfg.dim &&
+                            share->inner == cfg.inner && share->H == cfg.heads),
+                 "shared scratch comes from a workspace of another shape");
+    sa3k_block_ws* w = new sa3k_block_ws();
+    w->B = B; w->S = S; w->Ctx = Ctx; w->dim = cfg.dim; w->H = cfg.heads; w->inner = cfg.inner;
+    try {
+        const size_t N = (size_t)B * S, NC = (size_t)B * Ctx, D = cfg.dim, I = cfg.inner, H = cfg.heads;
+        const size_t BHS = (size_t)B * H * S * HD, BHC = (size_t)B * H * Ctx * HD, BHq = (size_t)B * H * S;
+        auto F32 = [&](size_t n) { float* p = dalloc<float>(n); w->allocs.push_back(p); return p; };
+        auto B16 = [&](size_t n) { bf16* p = dalloc<bf16>(n); w->allocs.push_back(p); return p; };
+        w->x = nullptr; w->ctxf = nullptr; w->dssg = nullptr;
+        w->modv = F32((size_t)B * 6 * D);
+        w->rs_a = F32(N); w->h = B16(N * D); w->qkv = F32(N * 5 * D);
+        w->q1 = B16(BHS); w->k1 = B16(BHS); w->q2 = B16(BHS); w->k2 = B16(BHS); w->v = B16(BHS);
+        w->rq = F32(N * H * 5);
+        w->o = B16(N * D); w->o1 = B16(BHS); w->o2 = B16(BHS); w->l1 = F32(BHq); w->l2 = F32(BHq);
+        w->y = F32(N * D); w->x1 = F32(N * D); w->rs_c = F32(N); w->hc = B16(N * D); w->qf = F32(N * 2 * D);
+        w->kv = F32(NC * 3 * D);
+        w->cq1 = B16(BHS); w->cq2 = B16(BHS); w->ck1 = B16(BHC); w->ck2 = B16(BHC); w->cv = B16(BHC);
+        w->rcq = F32(N * H * 2); w->rck = F32(NC * H * 3);
+        w->oc = B16(N * D); w->co1 = B16(BHS); w->co2 = B16(BHS); w->cl1 = F32(BHq); w->cl2 = F32(BHq);
+        w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D); w->F = F32(N * 2 * I);
+        w->g = B16(N * I); w->yf = F32(N * D);
+        w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
+        if (share) {
+            w->yc = share->yc;
+            w->dyf = share->dyf; w->dg = share->dg; w->dF = share->dF; w->dfin = share->dfin; w->dx2 = share->dx2;
+            w->doc = share->doc; w->dqf = share->dqf; w->dkv = share->dkv; w->dhc = share->dhc; w->dx1 = share->dx1;
+            w->dy = share->dy; w->dob = share->dob; w->dqkv = share->dqkv; w->dh = share->dh;
+            w->dOh = share->dOh; w->dn = share->dn;
+            w->dq1 = share->dq1; w->dk1 = share->dk1; w->dq2 = share->dq2; w->dk2 = share->dk2; w->dv = share->dv;
+            w->part = share->part;
+        } else {
+            w->yc = F32(N * D);
+            w->dyf = F32(N * D); w->dg = F32(N * I); w->dF = F32(N * 2 * I); w->dfin = F32(N * D); w->dx2 = F32(N * D);
+            w->doc = F32(N * D); w->dqf = F32(N * 2 * D); w->dkv = F32(NC * 3 * D); w->dhc = F32(N * D);
+            w->dx1 = F32(N * D); w->dy = F32(N * D); w->dob = F32(N * D); w->dqkv = F32(N * 5 * D); w->dh = F32(N * D);
+            w->dOh = B16(BHS); w->dn = F32(2 * BHq);
+            const size_t BHK = std::max(BHS, BHC);   // dK/dV of self (S keys) and cross (Ctx keys)
+            w->dq1 = F32(BHS); w->dk1 = F32(BHK); w->dq2 = F32(BHS); w->dk2 = F32(BHK); w->dv = F32(BHK);
+            w->part = F32((size_t)B * w->part_chunks * 2 * D);
+        }
+    } catch (...) {
+        block_ws_free(w);
+        throw;
+    }
+    return w;
+}
+
+void block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
+                   const float* const* mag, float scale, int dora) {
+    SA3K_REQUIRE(b && A && Bm && (!dora || mag), "null adapter arrays");
+    for (int t = 0; t < NT; ++t)
+        chk(ctx, sa3k_lin_prepare(ctx, b->L[t], A[t], Bm[t], scale, dora, dora ? mag[t] : nullptr,
+                                  dora ? b->bnsq[t] : nullptr));
+}
+
+}  // namespace sa3k
+
 extern "C" {
 
 SA3K_API int sa3k_block_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, const sa3k_block_weights* wts, int rank,
@@ -384,57 +464,15 @@ SA3K_API int sa3k_block_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, cons
     return sa3k_guard(ctx, "sa3k_block_create", [&] {
         SA3K_REQUIRE(cfg && wts && out, "null pointer");
         *out = nullptr;
-        SA3K_REQUIRE(cfg->head_dim == HD && cfg->dim == cfg->heads * HD, "dim must be heads * 64");
-        SA3K_REQUIRE(cfg->rope_dims > 0 && cfg->rope_dims <= HD && cfg->rope_dims % 2 == 0, "rope_dims");
-        SA3K_REQUIRE(max_tokens > 0 && max_ctx_tokens > 0, "token budgets must be positive");
-        sa3k_block* b = new sa3k_block();
-        b->cfg = *cfg;
-        b->rank = rank;
-        b->max_tokens = max_tokens;
-        b->max_ctx = max_ctx_tokens;
-        try {
-            for (int t = 0; t < NT; ++t) {
-                int64_t in, o;
-                target_dims(*cfg, t, in, o);
-                SA3K_REQUIRE(wts->W[t] != nullptr, "missing block weight");
-                chk(ctx, sa3k_weight_create(ctx, wts->weight_type, in, o, wts->W[t], 0, &b->W[t]));
-                chk(ctx, sa3k_lin_create(ctx, b->W[t], rank, SA3K_PREC_BF16, t == 3 ? max_ctx_tokens : max_tokens,
-                                         &b->L[t]));
-                b->bnsq[t] = dalloc<float>((size_t)o);
-                chk(ctx, sa3k_weight_row_norm_sq(ctx, b->W[t], 1e-12f, b->bnsq[t]));
-                if (wts->bias[t]) {
-                    b->bias[t] = dalloc<float>((size_t)o);
-                    SA3K_HIP(hipMemcpyAsync(b->bias[t], wts->bias[t], o * 4, hipMemcpyHostToDevice, ctx->stream));
-                }
-            }
-            auto up = [&](const float* src, size_t n) {
-                SA3K_REQUIRE(src != nullptr, "missing block vector");
-                float* d = dalloc<float>(n);
-                SA3K_HIP(hipMemcpyAsync(d, src, n * 4, hipMemcpyHostToDevice, ctx->stream));
-                return d;
-            };
-            const size_t dim = cfg->dim;
-            b->ssg = up(wts->ssg, 6 * dim);
-            b->pre_g = up(wts->pre_g, dim);
-            b->cross_g = up(wts->cross_g, dim);
-            b->ff_g = up(wts->ff_g, dim);
-            b->sq_g = up(wts->sq_g, HD);
-            b->sk_g = up(wts->sk_g, HD);
-            b->cq_g = up(wts->cq_g, HD);
-            b->ck_g = up(wts->ck_g, HD);
-            SA3K_HIP(hipStreamSynchronize(ctx->stream));
-        } catch (...) {
-            free_block(ctx, b);
-            throw;
-        }
-        *out = b;
+        const float* vecs[8] = {wts->ssg, wts->pre_g, wts->cross_g, wts->ff_g, wts->sq_g, wts->sk_g, wts->cq_g, wts->ck_g};
+        *out = block_build(ctx, *cfg, wts->weight_type, wts->W, wts->bias, vecs, 0, rank, max_tokens, max_ctx_tokens);
     });
 }
 
 SA3K_API int sa3k_block_destroy(sa3k_ctx* ctx, sa3k_block* b) {
     return sa3k_guard(ctx, "sa3k_block_destroy", [&] {
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
-        free_block(ctx, b);
+        block_free(ctx, b);
     });
 }
 
@@ -448,65 +486,28 @@ SA3K_API int sa3k_block_base_norm_sq(sa3k_ctx* ctx, const sa3k_block* b, int tar
 SA3K_API int sa3k_block_ws_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, int B, int S, int Ctx,
                                   sa3k_block_ws** out) {
     return sa3k_guard(ctx, "sa3k_block_ws_create", [&] {
-        SA3K_REQUIRE(cfg && out && B > 0 && S > 0 && Ctx > 0, "bad workspace shape");
-        *out = nullptr;
-        sa3k_block_ws* w = new sa3k_block_ws();
-        w->B = B; w->S = S; w->Ctx = Ctx; w->dim = cfg->dim; w->H = cfg->heads; w->inner = cfg->inner;
-        try {
-            const size_t N = (size_t)B * S, NC = (size_t)B * Ctx, D = cfg->dim, I = cfg->inner, H = cfg->heads;
-            const size_t BHS = (size_t)B * H * S * HD, BHC = (size_t)B * H * Ctx * HD;
-            auto F32 = [&](size_t n) { float* p = dalloc<float>(n); w->allocs.push_back(p); return p; };
-            auto B16 = [&](size_t n) { bf16* p = dalloc<bf16>(n); w->allocs.push_back(p); return p; };
-            w->modv = F32((size_t)B * 6 * D); w->x = nullptr;
-            w->rs_a = F32(N); w->h = B16(N * D); w->qkv = F32(N * 5 * D);
-            w->q1 = B16(BHS); w->k1 = B16(BHS); w->q2 = B16(BHS); w->k2 = B16(BHS); w->v = B16(BHS);
-            w->rq = F32(N * H * 5);
-            w->o = B16(N * D); w->o1 = B16(BHS); w->o2 = B16(BHS); w->l1 = F32((size_t)B * H * S); w->l2 = F32((size_t)B * H * S);
-            w->y = F32(N * D); w->x1 = F32(N * D); w->rs_c = F32(N); w->hc = B16(N * D); w->qf = F32(N * 2 * D);
-            w->kv = F32(NC * 3 * D); w->ctxf = nullptr;
-            w->cq1 = B16(BHS); w->cq2 = B16(BHS); w->ck1 = B16(BHC); w->ck2 = B16(BHC); w->cv = B16(BHC);
-            w->rcq = F32(N * H * 2); w->rck = F32(NC * H * 3);
-            w->oc = B16(N * D); w->co1 = B16(BHS); w->co2 = B16(BHS); w->cl1 = F32((size_t)B * H * S); w->cl2 = F32((size_t)B * H * S);
-            w->yc = F32(N * D); w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D); w->F = F32(N * 2 * I);
-            w->g = B16(N * I); w->yf = F32(N * D);
-            w->d3 = nullptr;
-            w->dyf = F32(N * D); w->dg = F32(N * I); w->dF = F32(N * 2 * I); w->dfin = F32(N * D); w->dx2 = F32(N * D);
-            w->doc = F32(N * D); w->dqf = F32(N * 2 * D); w->dkv = F32(NC * 3 * D); w->dhc = F32(N * D); w->dx1 = F32(N * D);
-            w->dy = F32(N * D); w->dob = F32(N * D); w->dqkv = F32(N * 5 * D); w->dh = F32(N * D);
-            w->dOh = B16(BHS); w->dn = F32((size_t)2 * B * H * S);
-            const size_t BHK = std::max(BHS, BHC);   // dK/dV of self (S keys) and cross (Ctx keys)
-            w->dq1 = F32(BHS); w->dk1 = F32(BHK); w->dq2 = F32(BHS); w->dk2 = F32(BHK); w->dv = F32(BHK);
-            w->dssg = nullptr;
-            w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
-            w->part = F32((size_t)B * w->part_chunks * 2 * D);
-        } catch (...) {
-            free_ws(w);
-            throw;
-        }
-        *out = w;
+        SA3K_REQUIRE(cfg && out, "null pointer");
+        *out = block_ws_build(*cfg, B, S, Ctx, nullptr);
     });
 }
 
 SA3K_API int sa3k_block_ws_destroy(sa3k_ctx* ctx, sa3k_block_ws* w) {
     return sa3k_guard(ctx, "sa3k_block_ws_destroy", [&] {
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
-        free_ws(w);
+        block_ws_free(w);
     });
 }
 
 SA3K_API int sa3k_block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
                                 const float* const* mag, float scale, int dora) {
-    return sa3k_guard(ctx, "sa3k_block_prepare", [&] {
-        SA3K_REQUIRE(b && A && Bm && (!dora || mag), "null adapter arrays");
-        for (int t = 0; t < NT; ++t)
-            chk(ctx, sa3k_lin_prepare(ctx, b->L[t], A[t], Bm[t], scale, dora, dora ? mag[t] : nullptr,
-                                      dora ? b->bnsq[t] : nullptr));
-    });
+    return sa3k_guard(ctx, "sa3k_block_prepare", [&] { block_prepare(ctx, b, A, Bm, mag, scale, dora); });
 }
 
-SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
-                                const float* gcond, float* out) {
-    return sa3k_guard(ctx, "sa3k_block_forward", [&] {
+}  // extern "C"
+
+void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
+                         const float* gcond, float* out) {
+    {
         SA3K_REQUIRE(b && w && x && context && gcond && out, "null pointer");
         SA3K_REQUIRE(w->dim == b->cfg.dim && w->inner == b->cfg.inner, "workspace shape differs from the block");
         const sa3k_block_config& c = b->cfg;
@@ -514,8 +515,8 @@ SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, 
         const int64_t N = (int64_t)B * S, NC = (int64_t)B * Ctx;
         SA3K_REQUIRE(N <= b->max_tokens && NC <= b->max_ctx, "workspace exceeds the block's token budget");
         const float scale = 1.0f / sqrtf((float)HD);
-        w->x = const_cast<float*>(x);
-        w->ctxf = const_cast<float*>(context);
+        w->x = x;
+        w->ctxf = context;
         const float* mv = w->modv;
         launch(ctx, "blk_modv", modv_kernel, dim3(nblk((int64_t)B * 6 * D)), (const float*)b->ssg, gcond,
                (int64_t)B * 6 * D, 6 * D, w->modv);
@@ -552,12 +553,12 @@ SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, 
         chk(ctx, sa3k_lin_forward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, b->bias[6], w->yf));
         launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D)), (const float*)w->x2, (const float*)w->yf, mv, 5, S, D,
                N * D, out);
-    });
+    }
 }
 
-SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx,
-                                 float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm) {
-    return sa3k_guard(ctx, "sa3k_block_backward", [&] {
+void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx,
+                          float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm) {
+    {
         SA3K_REQUIRE(b && w && dout && dx && dcontext && dgcond && dA && dB, "null pointer");
         SA3K_REQUIRE(w->x != nullptr, "backward needs a preceding forward on this workspace");
         const sa3k_block_config& c = b->cfg;
@@ -609,7 +610,20 @@ SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w,
         launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dh, (const float*)w->x,
                (const float*)w->rs_a, (const float*)b->pre_g, mv, 0, S, D, (const float*)w->dx1, dx);
         w->dssg = nullptr;
-    });
+    }
+}
+
+extern "C" {
+
+SA3K_API int sa3k_block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
+                                const float* gcond, float* out) {
+    return sa3k_guard(ctx, "sa3k_block_forward", [&] { block_forward(ctx, b, w, x, context, gcond, out); });
+}
+
+SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx,
+                                 float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm) {
+    return sa3k_guard(ctx, "sa3k_block_backward",
+                      [&] { block_backward(ctx, b, w, dout, dx, dcontext, dgcond, dA, dB, dm); });
 }
 
 }  // extern "C"

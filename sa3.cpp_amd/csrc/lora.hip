@@ -475,6 +475,26 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     const bool bf = L->prec == SA3K_PREC_BF16;
     const int64_t in = W->in, out = W->out;
     const int r = L->rank;
+    if (r == 0) {   // plain mul_mat: dX = dY W only
+        if (!dX) return;
+        const void* dyc = dY;
+        if (bf) {
+            const int64_t n = N * out;
+            KernelScope ks(ctx, "lin_bwd_cvt_dy");
+            cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(dY, static_cast<bf16*>(L->dU),
+                                                                                        n, 1.0f);
+            SA3K_LAUNCHED();
+            dyc = L->dU;
+        }
+        const WOp wt = weight_operand(W, bf, true);
+        GemmDesc g;
+        g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
+        g.A = dyc; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
+        g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
+        g.C = dX; g.ldc = in; g.accumulate = dx_acc;
+        gemm_run(ctx, g, "lin_bwd_dx");
+        return;
+    }
     // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens)
     {
         const int S = choose_splits(out, N);
@@ -788,7 +808,7 @@ SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const voi
     return sa3k_guard(ctx, "sa3k_lin_backward", [&] {
         SA3K_REQUIRE(L && X && dY, "null pointer");
         SA3K_REQUIRE(N == L->saved_tokens, "backward must follow a forward over the same tokens");
-        SA3K_REQUIRE(L->rank > 0 && dA && dB, "adapter gradients need a rank > 0 adapter and dA/dB buffers");
+        SA3K_REQUIRE(L->rank == 0 || (dA && dB), "adapter gradients need dA/dB buffers");
         SA3K_REQUIRE(!L->dora || dm, "dora needs a magnitude gradient buffer");
         SA3K_REQUIRE(x_type == SA3K_TYPE_F32 || (x_type == SA3K_TYPE_BF16 && L->prec == SA3K_PREC_BF16),
                      "activation type must be f32 (or bf16 with bf16 precision)");
