@@ -298,6 +298,88 @@ SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* ws
                                  float* dcontext, float* dgcond, float* const* dA, float* const* dB,
                                  float* const* dm);
 
+/* ---------------------------------------------------------------- C4: the DiT training step */
+
+/* DitConfig (src/dit.h:20-46) of a differential DiT, plus the feed-forward inner width and the
+ * self-attention window of this build (0 = dense, the reference). */
+typedef struct {
+    int io, dim, depth, heads, head_dim, cond_dim, mem_tokens, rope_dims, time_dim, inner, window;
+    float rope_base, norm_eps, qk_eps, time_min_freq, time_max_freq;
+} sa3k_dit_config;
+
+/* The training setup: adapter family and scope (TrainLoraScope, src/train_lora.h:53-97), the
+ * micro-batch shape, and the activation schedule. */
+typedef struct {
+    int rank;          /* 8 / 16 / 24 / 32 */
+    float alpha;       /* scale = alpha / rank (src/train_dit.h:151) */
+    int dora;          /* 1: dora-rows, 0: lora */
+    int scope;         /* SA3K_SCOPE_CORE (the 7 block projections) or SA3K_SCOPE_FULL (+ 12 head/tail) */
+    int batch;         /* samples per accumulate call */
+    int frames;        /* latent frames T per sample (tokens = mem_tokens + T) */
+    int ctx_tokens;    /* cross-attention conditioning tokens per sample */
+    int recompute;     /* 1: gradient-checkpointed schedule of src/train_ckpt.h (one block of
+                          activations, every block but the last recomputed before its backward);
+                          0: every block keeps its forward activations (no recompute) */
+} sa3k_dit_train;
+#define SA3K_SCOPE_CORE 0
+#define SA3K_SCOPE_FULL 1
+
+typedef struct sa3k_dit sa3k_dit;
+
+/* A DiT whose 2-D weights are stored as weight_type (f32 / f16 / bf16) and every other tensor
+ * (biases, norm gammas, ssg tables, memory tokens) as f32. Tensors are named as in the DiT GGUF
+ * (dit.memory_tokens, dit.pre_conv.weight, dit.<l>.self.qkv.weight, dit.<l>.ssg, ...,
+ * GgufModel::get, src/gguf_model.h:200-276) and are filled by sa3k_dit_set_tensor or
+ * sa3k_dit_init_random before sa3k_dit_setup. */
+SA3K_API int sa3k_dit_create(sa3k_ctx* ctx, const sa3k_dit_config* cfg, int weight_type, sa3k_dit** out);
+SA3K_API int sa3k_dit_destroy(sa3k_ctx* ctx, sa3k_dit* dit);
+/* Number of named tensors and the name / element count / stored type of tensor i. */
+SA3K_API int sa3k_dit_tensor_count(sa3k_ctx* ctx, const sa3k_dit* dit, int* count);
+SA3K_API int sa3k_dit_tensor_info(sa3k_ctx* ctx, const sa3k_dit* dit, int i, char* name, int name_len,
+                                  int64_t* rows, int64_t* cols, int* type);
+/* Copy a tensor's elements (host, in its stored type) into the model. */
+SA3K_API int sa3k_dit_set_tensor(sa3k_ctx* ctx, sa3k_dit* dit, const char* name, const void* data, int64_t bytes);
+/* Synthetic model on the device (counter-based Philox4x32-10 + Box-Muller): 2-D weights
+ * N(0, w_sd), biases N(0, 0.02), ssg tables N(0, 0.1), gammas 1 + N(0, 0.1), memory tokens N(0, 1). */
+SA3K_API int sa3k_dit_init_random(sa3k_ctx* ctx, sa3k_dit* dit, uint64_t seed, float w_sd);
+/* Build the frozen weights (decoded bf16 working copies, base_norm_sq), the adapted linears, the
+ * flat adapter arena and the activation workspaces for one micro-batch shape. */
+SA3K_API int sa3k_dit_setup(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_dit_train* train);
+
+/* The adapter arena: every selected target, in the reference's order (weight names sorted,
+ * src/train_lora.h:99-121), holds A [rank][in], B [out][rank] and (dora) magnitude [out], laid
+ * end to end (the order train_apply_accumulated_adamw visits them, src/train_loop.h:181-207).
+ * which: 0 parameters, 1 accumulated gradients, 2 AdamW first moments, 3 second moments. */
+SA3K_API int sa3k_dit_arena(sa3k_ctx* ctx, sa3k_dit* dit, int which, float** ptr, int64_t* n);
+SA3K_API int sa3k_dit_target_count(sa3k_ctx* ctx, const sa3k_dit* dit, int* count);
+SA3K_API int sa3k_dit_target_info(sa3k_ctx* ctx, const sa3k_dit* dit, int i, char* name, int name_len,
+                                  int64_t* in, int64_t* out, int64_t* off_a, int64_t* off_b, int64_t* off_m);
+/* Initialise the adapters on the device: A Kaiming-uniform U(+-1/sqrt(in)), B ~ N(0, b_sd) (0 =
+ * zeros, the reference's init), magnitude = row norms of the decoded base (train_row_norms,
+ * src/train_lora.h:141-155, init_train_lora_state :205-273). Moments and gradients are zeroed. */
+SA3K_API int sa3k_dit_adapters_init(sa3k_ctx* ctx, sa3k_dit* dit, uint64_t seed, float b_sd);
+/* Mark the adapter arena as changed outside the library (e.g. uploaded): the derived terms are
+ * refreshed before the next forward. */
+SA3K_API int sa3k_dit_adapters_changed(sa3k_ctx* ctx, sa3k_dit* dit);
+
+/* One micro-batch of the rectified-flow step (run_train_dit_accumulate[_ckpt], src/train_loop.h:
+ * 212-441, over build_train_dit_forward_graph, src/train_dit.h:30-218): forward, velocity MSE, and
+ * the gradients of sum_b loss_b ADDED to the gradient arena (the accumulator adds one sample per
+ * graph run in the reference; here the batch runs at once and counts batch samples). Device
+ * inputs: x_t, target [B][T][io]; t [B]; cross [B][Ctx][cond_dim]; glob [B][cond_dim]; loss_weight
+ * [B][T] (per-frame weights of the inpaint loss, src/train_dit.h:175-182) or NULL for the uniform
+ * mean 1/(io*T). loss_out (host, nullable) receives the B per-sample losses and synchronises. */
+SA3K_API int sa3k_dit_accumulate(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* target,
+                                 const float* t, const float* cross, const float* glob,
+                                 const float* loss_weight, double* loss_out);
+/* train_apply_accumulated_adamw (src/train_loop.h:173-211) over the arena: average over the
+ * accumulated sample count, global clip, AdamW (sa3k_adamw_clip), then clear the accumulator. */
+SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw_params* hp, int step,
+                                  double* grad_norm_out);
+/* Forward only: velocity [B][T][io] (dit_forward, src/dit.h:327-338). */
+SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* t, const float* cross,
+                              const float* glob, float* velocity);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,25 @@ class BlockWeights(C.Structure):
 BLOCK_VECTORS = ("ssg", "pre_g", "cross_g", "ff_g", "sq_g", "sk_g", "cq_g", "ck_g")
 
 
+class DitConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("io", "dim", "depth", "heads", "head_dim", "cond_dim", "mem_tokens", "rope_dims",
+                                       "time_dim", "inner", "window")] + \
+               [(n, C.c_float) for n in ("rope_base", "norm_eps", "qk_eps", "time_min_freq", "time_max_freq")]
+
+
+class DitTrain(C.Structure):
+    _fields_ = [("rank", C.c_int), ("alpha", C.c_float), ("dora", C.c_int), ("scope", C.c_int), ("batch", C.c_int),
+                ("frames", C.c_int), ("ctx_tokens", C.c_int), ("recompute", C.c_int)]
+
+
+SCOPE_CORE, SCOPE_FULL = 0, 1
+
+
+def dit_config(io, dim, depth, heads, cond_dim, mem_tokens, time_dim, inner, window=0, rope_dims=32):
+    return DitConfig(io, dim, depth, heads, 64, cond_dim, mem_tokens, rope_dims, time_dim, inner, window,
+                     1e4, 1e-5, 1e-6, 0.5, 1e4)
+
+
 def block_target_dims(dim, inner):
     """(in, out) of the 7 adapted linears of a block, in target order"""
     return [(dim, 5 * dim), (dim, dim), (dim, 2 * dim), (dim, 3 * dim), (dim, dim), (dim, 2 * inner), (inner, dim)]
@@ -93,6 +112,22 @@ def _declare(lib):
         "sa3k_block_prepare": (I, [P, P, P, P, P, F, I]),
         "sa3k_block_forward": (I, [P, P, P, P, P, P, P]),
         "sa3k_block_backward": (I, [P, P, P, P, P, P, P, P, P, P]),
+        "sa3k_dit_create": (I, [P, C.POINTER(DitConfig), I, C.POINTER(P)]),
+        "sa3k_dit_destroy": (I, [P, P]),
+        "sa3k_dit_tensor_count": (I, [P, P, C.POINTER(I)]),
+        "sa3k_dit_tensor_info": (I, [P, P, I, C.c_char_p, I, C.POINTER(I64), C.POINTER(I64), C.POINTER(I)]),
+        "sa3k_dit_set_tensor": (I, [P, P, C.c_char_p, P, I64]),
+        "sa3k_dit_init_random": (I, [P, P, C.c_uint64, F]),
+        "sa3k_dit_setup": (I, [P, P, C.POINTER(DitTrain)]),
+        "sa3k_dit_arena": (I, [P, P, I, C.POINTER(P), C.POINTER(I64)]),
+        "sa3k_dit_target_count": (I, [P, P, C.POINTER(I)]),
+        "sa3k_dit_target_info": (I, [P, P, I, C.c_char_p, I, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64),
+                                     C.POINTER(I64), C.POINTER(I64)]),
+        "sa3k_dit_adapters_init": (I, [P, P, C.c_uint64, F]),
+        "sa3k_dit_adapters_changed": (I, [P, P]),
+        "sa3k_dit_accumulate": (I, [P, P, P, P, P, P, P, P, P]),
+        "sa3k_dit_apply_adamw": (I, [P, P, C.POINTER(AdamWParams), I, C.POINTER(D)]),
+        "sa3k_dit_forward": (I, [P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -402,6 +437,88 @@ class BlockWorkspace:
             self.ctx.check(self.ctx.lib.sa3k_block_ws_destroy(self.ctx.h, self.h))
             self.h = None
         self.inputs = None
+
+
+class Dit:
+    """The DiT training step (sa3k_dit_*): named tensors, setup, adapter arena, accumulate / AdamW."""
+
+    def __init__(self, ctx, cfg, wtype=TYPE_F16):
+        self.ctx, self.cfg, self.wtype = ctx, cfg, wtype
+        h = C.c_void_p()
+        ctx.check(ctx.lib.sa3k_dit_create(ctx.h, C.byref(cfg), wtype, C.byref(h)))
+        self.h = h.value
+        self.train = None
+
+    def tensors(self):
+        """[(name, rows, cols, type)]"""
+        L, out = self.ctx.lib, []
+        n = C.c_int()
+        self.ctx.check(L.sa3k_dit_tensor_count(self.ctx.h, self.h, C.byref(n)))
+        buf = C.create_string_buffer(256)
+        r, c, t = C.c_int64(), C.c_int64(), C.c_int()
+        for i in range(n.value):
+            self.ctx.check(L.sa3k_dit_tensor_info(self.ctx.h, self.h, i, buf, 256, C.byref(r), C.byref(c), C.byref(t)))
+            out.append((buf.value.decode(), r.value, c.value, t.value))
+        return out
+
+    def set_tensor(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        self.ctx.check(self.ctx.lib.sa3k_dit_set_tensor(self.ctx.h, self.h, name.encode(), a.ctypes.data, a.nbytes))
+
+    def init_random(self, seed, w_sd=0.02):
+        self.ctx.check(self.ctx.lib.sa3k_dit_init_random(self.ctx.h, self.h, seed, w_sd))
+
+    def setup(self, rank, alpha, dora, scope, batch, frames, ctx_tokens, recompute=False):
+        self.train = DitTrain(rank, alpha, int(dora), scope, batch, frames, ctx_tokens, int(recompute))
+        self.ctx.check(self.ctx.lib.sa3k_dit_setup(self.ctx.h, self.h, C.byref(self.train)))
+
+    def arena(self, which=0):
+        """0 params, 1 grads, 2 m, 3 v: a non-owning DeviceArray view"""
+        p, n = C.c_void_p(), C.c_int64()
+        self.ctx.check(self.ctx.lib.sa3k_dit_arena(self.ctx.h, self.h, which, C.byref(p), C.byref(n)))
+        return DeviceArray(self.ctx, p.value, (n.value,), np.float32, owner=False)
+
+    def targets(self):
+        """[(name, in, out, off_a, off_b, off_m)] in arena order"""
+        L, out = self.ctx.lib, []
+        n = C.c_int()
+        self.ctx.check(L.sa3k_dit_target_count(self.ctx.h, self.h, C.byref(n)))
+        buf = C.create_string_buffer(256)
+        v = [C.c_int64() for _ in range(5)]
+        for i in range(n.value):
+            self.ctx.check(L.sa3k_dit_target_info(self.ctx.h, self.h, i, buf, 256, *[C.byref(x) for x in v]))
+            out.append((buf.value.decode(),) + tuple(x.value for x in v))
+        return out
+
+    def adapters_init(self, seed, b_sd=0.0):
+        self.ctx.check(self.ctx.lib.sa3k_dit_adapters_init(self.ctx.h, self.h, seed, b_sd))
+
+    def adapters_changed(self):
+        self.ctx.check(self.ctx.lib.sa3k_dit_adapters_changed(self.ctx.h, self.h))
+
+    def accumulate(self, x_t, target, t, cross, glob, loss_weight=None, want_loss=True):
+        B = self.train.batch
+        loss = (C.c_double * B)()
+        self.ctx.check(self.ctx.lib.sa3k_dit_accumulate(self.ctx.h, self.h, x_t.ptr, target.ptr, t.ptr, cross.ptr,
+                                                        glob.ptr, loss_weight.ptr if loss_weight is not None else None,
+                                                        loss if want_loss else None))
+        return np.array(loss[:]) if want_loss else None
+
+    def apply_adamw(self, hp, step, want_norm=False):
+        p = AdamWParams(*hp)
+        nrm = C.c_double(0.0)
+        self.ctx.check(self.ctx.lib.sa3k_dit_apply_adamw(self.ctx.h, self.h, C.byref(p), step,
+                                                         C.byref(nrm) if want_norm else None))
+        return nrm.value if want_norm else None
+
+    def forward(self, x_t, t, cross, glob, velocity):
+        self.ctx.check(self.ctx.lib.sa3k_dit_forward(self.ctx.h, self.h, x_t.ptr, t.ptr, cross.ptr, glob.ptr,
+                                                     velocity.ptr))
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_dit_destroy(self.ctx.h, self.h))
+            self.h = None
 
 
 def attn_fwd(ctx, q1, k1, q2, k2, v, B, H, Sq, Sk, window=0, scale=0.125):

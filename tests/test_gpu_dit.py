@@ -1,0 +1,171 @@
+"""C4: the DiT training step (run_train_dit_accumulate_ckpt + train_apply_accumulated_adamw,
+src/train_loop.h:173-441) on the GPU vs the whole-DiT oracle (oracle/dit.cpp, pinned against
+torch float64 autograd in tests/test_oracle_dit.py).
+
+* depth-2 model, full scope (12 head/tail targets + blocks, DoRA, dense attention) and core scope
+  (blocks only, LoRA, banded attention, per-frame loss weights), f32 and f16 bases: per-sample
+  losses, the velocity and every adapter gradient to the bf16 bar (normwise relative error
+  <= 2e-2 and cosine >= 0.9999; the loss to 1e-3);
+* the arena layout is the reference's: targets in sorted weight-name order, [A | B | m] each;
+* the checkpointed (recompute) and resident schedules give bitwise-identical losses and gradients;
+* two accumulate calls give exactly twice the gradients; apply_adamw equals the oracle's
+  train_apply_accumulated_adamw on the same arena (bit-exact parameters and moments);
+* the full-size step (24 blocks, batch 2 x (64 + 1024) tokens, io 64, window 256, DoRA r32):
+  finite, deterministic, and the loss falls over a few updates on a fixed batch.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, cosine, oracle, rel_err, sa3k
+
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+import dit_binding as db  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(B=2, T=12, Ctx=5, io=64, dim=128, heads=2, inner=128, depth=2, mem=4, cond_dim=64, time_dim=64,
+           rope_dims=32, window=0, rank=8, alpha=16.0, dora=True)
+HP = (1e-3, 0.9, 0.999, 1e-8, 0.01, 1.0)
+
+
+def make_gpu(ctx, cfg, tensors, adapters, scope, wtype, recompute=False):
+    c = sa3k.dit_config(cfg["io"], cfg["dim"], cfg["depth"], cfg["heads"], cfg["cond_dim"], cfg["mem"],
+                        cfg["time_dim"], cfg["inner"], cfg["window"])
+    d = sa3k.Dit(ctx, c, wtype)
+    for name, rows, cols, typ in d.tensors():
+        a = tensors[name]
+        if typ == sa3k.TYPE_F16:
+            a = a.astype(np.float16)
+        d.set_tensor(name, a)
+    d.setup(cfg["rank"], cfg["alpha"], cfg["dora"], sa3k.SCOPE_FULL if scope == "full" else sa3k.SCOPE_CORE,
+            cfg["B"], cfg["T"], cfg["Ctx"], recompute)
+    p = np.zeros(d.arena(0).shape, np.float32)
+    for name, i, o, oa, ob, om in d.targets():
+        A, Bm, mag = adapters[name]
+        p[oa:oa + A.size] = A.ravel()
+        p[ob:ob + Bm.size] = Bm.ravel()
+        if om >= 0:
+            p[om:om + o] = mag
+    ctx.copy_into(d.arena(0), p)
+    d.adapters_changed()
+    return d
+
+
+def upload_inputs(ctx, inputs, lw=None):
+    up = {k: ctx.upload(np.ascontiguousarray(v, np.float32)) for k, v in inputs.items()}
+    return up, (ctx.upload(lw) if lw is not None else None)
+
+
+def grads_by_target(d, g):
+    out = {}
+    for name, i, o, oa, ob, om in d.targets():
+        r = (ob - oa) // i
+        out[name] = (g[oa:oa + r * i].reshape(r, i), g[ob:ob + o * r].reshape(o, r),
+                     g[om:om + o] if om >= 0 else None)
+    return out
+
+
+def check(got, ref, what):
+    e, c = rel_err(got, ref), cosine(got, ref)
+    assert e <= 2e-2 and c >= 0.9999, f"{what}: rel {e:.3e} cos {c:.6f}"
+
+
+CASES = {"full_dora_dense_f32": (41, "full", True, 0, False, sa3k.TYPE_F32),
+         "full_dora_dense_f16": (41, "full", True, 0, False, sa3k.TYPE_F16),
+         "core_lora_band_weighted_f16": (42, "core", False, 6, True, sa3k.TYPE_F16)}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_dit_step_vs_oracle(ctx, name):
+    seed, scope, dora, window, weighted, wtype = CASES[name]
+    cfg = dict(CFG, dora=dora, window=window)
+    tensors, adapters, inputs = db.random_dit(seed, cfg, scope)
+    if wtype == sa3k.TYPE_F16:   # the oracle sees the f16 values the GPU decodes
+        tensors = {k: (v.astype(np.float16).astype(np.float32) if (k.endswith(".weight")) else v)
+                   for k, v in tensors.items()}
+    lw = None
+    if weighted:
+        lw = np.random.Generator(np.random.Philox(seed + 7)).uniform(
+            0, 2.0 / (cfg["io"] * cfg["T"]), (cfg["B"], cfg["T"])).astype(np.float32)
+    d = make_gpu(ctx, cfg, tensors, adapters, scope, wtype)
+    try:
+        assert [t[0] for t in d.targets()] == db.target_names(cfg, scope)
+        up, lw_d = upload_inputs(ctx, inputs, lw)
+        loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"], lw_d)
+        vel = ctx.empty((cfg["B"], cfg["T"], cfg["io"]))
+        d.forward(up["x_t"], up["t"], up["cross"], up["glob"], vel)
+        got = grads_by_target(d, d.arena(1).numpy())
+        ref_loss, ref_vel, ref = db.dit_loss(cfg, tensors, adapters, inputs, loss_weight=lw)
+        assert np.allclose(loss, ref_loss, rtol=1e-3), (loss, ref_loss)
+        check(vel.numpy(), ref_vel, "velocity")
+        for n, (dA, dB, dm) in ref.items():
+            check(got[n][0], dA, f"dA {n}")
+            check(got[n][1], dB, f"dB {n}")
+            if dora:
+                check(got[n][2], dm, f"dm {n}")
+    finally:
+        d.destroy()
+
+
+def test_dit_schedules_accumulation_and_adamw(ctx):
+    cfg = dict(CFG, window=4)
+    tensors, adapters, inputs = db.random_dit(43, cfg, "full")
+    runs = []
+    for recompute in (False, True):
+        d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16, recompute)
+        up, _ = upload_inputs(ctx, inputs)
+        l1 = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+        g1 = d.arena(1).numpy()
+        l2 = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+        g2 = d.arena(1).numpy()
+        assert np.array_equal(l1, l2)
+        # each target's gradient is added in several terms, so the sum is 2 g1 up to f32 rounding
+        assert rel_err(g2, 2 * g1) < 1e-6, "two identical micro-batches must add"
+        p0, m0, v0 = d.arena(0).numpy(), d.arena(2).numpy(), d.arena(3).numpy()
+        nrm = d.apply_adamw(HP, 1, want_norm=True)
+        _, gscale = ctx.adamw_clip_scale()
+        # oracle: train_apply_accumulated_adamw on the same arena, count = 2 micro-batches x 2 samples
+        pr, _, mr, vr, onorm, oscale = oracle.apply_accumulated_adamw(p0, g2, m0, v0, *HP, 1, 4)
+        assert abs(nrm - onorm) <= 1e-12 * max(1.0, onorm)
+        assert np.float32(gscale) == np.float32(oscale)
+        assert np.array_equal(d.arena(0).numpy(), pr)
+        assert np.array_equal(d.arena(2).numpy(), mr) and np.array_equal(d.arena(3).numpy(), vr)
+        assert not np.any(d.arena(1).numpy()), "the accumulator is cleared"
+        runs.append((l1, g1))
+        d.destroy()
+    assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1]), \
+        "resident and recompute schedules must agree bitwise"
+
+
+def test_dit_full_size_step(ctx):
+    # 24 blocks, dim 1536, 24 heads, FFN 6144, io 64, batch 2 x (64 + 1024), 128 context tokens of 768
+    c = sa3k.dit_config(64, 1536, 24, 24, 768, 64, 256, 6144, window=256)
+    d = sa3k.Dit(ctx, c, sa3k.TYPE_F16)
+    try:
+        d.init_random(1234, 0.02)
+        d.setup(32, 32.0, True, sa3k.SCOPE_FULL, 2, 1024, 128, recompute=False)
+        d.adapters_init(99, 0.01)
+        g = np.random.Generator(np.random.Philox(5))
+        x = ctx.upload(g.normal(0, 1, (2, 1024, 64)).astype(np.float32))
+        tg = ctx.upload(g.normal(0, 1, (2, 1024, 64)).astype(np.float32))
+        t = ctx.upload(g.uniform(0, 1, 2).astype(np.float32))
+        cr = ctx.upload(g.normal(0, 1, (2, 128, 768)).astype(np.float32))
+        gl = ctx.upload(g.normal(0, 1, (2, 768)).astype(np.float32))
+        l0 = d.accumulate(x, tg, t, cr, gl)
+        g0 = d.arena(1).numpy()
+        assert np.all(np.isfinite(l0)) and np.all(np.isfinite(g0)) and np.any(g0)
+        # the same micro-batch again, on a cleared accumulator, gives the same loss and gradients
+        ctx.check(ctx.lib.sa3k_memset(ctx.h, d.arena(1).ptr, 0, d.arena(1).nbytes))
+        assert np.array_equal(d.accumulate(x, tg, t, cr, gl), l0)
+        assert np.array_equal(d.arena(1).numpy(), g0)
+        losses = [float(np.mean(l0))]
+        hp = (1e-3, 0.9, 0.999, 1e-8, 0.01, 1.0)
+        for step in range(1, 4):
+            d.apply_adamw(hp, step)
+            losses.append(float(np.mean(d.accumulate(x, tg, t, cr, gl))))
+        assert losses[-1] < losses[0], losses
+    finally:
+        d.destroy()
