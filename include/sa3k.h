@@ -89,7 +89,9 @@ SA3K_API int sa3k_timer_stop(sa3k_ctx* ctx, float* ms);
 /* Per-kernel timing with HIP events on the context stream (off by default; the reference's
  * SA3_TRAIN_PROFILE wall-clock phases, src/train_loop.h:314-437, have no per-kernel counterpart).
  * While enabled every kernel launch is bracketed by an event pair; sa3k_profile_report writes one
- * line per kernel name, "name launches total_ms\n", into buf (synchronises the stream). */
+ * line per scope name, "name launches total_ms work\n", into buf (synchronises the stream); work is
+ * the algorithmic flop count of the launches where the library counts it (the GEMMs: 2 (M + extra
+ * rows) N (K + rank extension) per launch), else 0. */
 SA3K_API int sa3k_profile_enable(sa3k_ctx* ctx, int on);
 SA3K_API int sa3k_profile_reset(sa3k_ctx* ctx);
 SA3K_API int sa3k_profile_report(sa3k_ctx* ctx, char* buf, int buf_len);
@@ -376,6 +378,11 @@ SA3K_API int sa3k_dit_accumulate(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t,
  * accumulated sample count, global clip, AdamW (sa3k_adamw_clip), then clear the accumulator. */
 SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw_params* hp, int step,
                                   double* grad_norm_out);
+/* Replay the accumulate step as a captured HIP graph (default on; environment SA3K_DIT_GRAPH=0
+ * turns it off): the first call runs eagerly, the next captures the step for its input pointers
+ * (with and without the adapter refresh), later calls with the same pointers replay it. Results
+ * are identical to the eager path. While profiling is on the step always runs eagerly. */
+SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
 /* Forward only: velocity [B][T][io] (dit_forward, src/dit.h:327-338). */
 SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* t, const float* cross,
                               const float* glob, float* velocity);

@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -135,6 +136,11 @@ __global__ void silu_bwd_kernel(const float* __restrict__ da, const float* __res
     if (i >= n) return;
     const float z = h[i], s = 1.0f / (1.0f + expf(-z));
     dh[i] = da[i] * s * (1.0f + z * (1.0f - s));
+}
+
+__global__ void copy_kernel(const float* __restrict__ a, int64_t n, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) out[i] = a[i];
 }
 
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t n, float* __restrict__ out) {
@@ -271,6 +277,11 @@ struct sa3k_dit {
     float *xp, *xi, *xt, *v0, *vel, *dv, *dv0, *dxt, *dxa, *dxb, *dctx, *dgcond, *dxi, *dxp, *da, *dh, *dg, *dca, *dch;
     double *loss_part, *loss;
     int loss_chunks = 1;
+    // HIP graphs of the accumulate step (index 1: with the adapter prepare, 0: without), keyed by
+    // the input pointers they were captured with
+    bool use_graph = true, warm = false;
+    hipGraphExec_t gexec[2] = {nullptr, nullptr};
+    const void* gkey[2][6] = {};
 };
 
 namespace {
@@ -336,6 +347,8 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
     for (Tensor& t : d->tensors)
         if (t.raw) (void)hipFree(t.raw);
     for (void* p : d->bufs) (void)hipFree(p);
+    for (hipGraphExec_t e : d->gexec)
+        if (e) (void)hipGraphExecDestroy(e);
     for (float* p : {d->p, d->g, d->m, d->v})
         if (p) (void)hipFree(p);
     delete d;
@@ -560,8 +573,8 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
            d->vel);
 }
 
-void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* target, const float* t, const float* cross,
-                const float* glob, const float* lw, double* loss_out) {
+void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* target, const float* t,
+                     const float* cross, const float* glob, const float* lw) {
     const sa3k_dit_config& c = d->cfg;
     const int B = d->tr.batch, T = d->tr.frames, S = d->S;
     const int64_t NT = (int64_t)B * T, NC = (int64_t)B * d->tr.ctx_tokens, D = c.dim;
@@ -573,7 +586,7 @@ void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* targe
            c.io, chunk, d->loss_part, d->dv);
     launch(ctx, "dit_loss", mse_sum_kernel, dim3(1), (const double*)d->loss_part, d->loss_chunks, B, d->loss);
     // tail backward: v = post_conv(v0) + v0, v0 = proj_out(x_depth[mem:])
-    SA3K_HIP(hipMemcpyAsync(d->dv0, d->dv, sizeof(float) * NT * c.io, hipMemcpyDeviceToDevice, ctx->stream));
+    launch(ctx, "dit_tail", copy_kernel, dim3(nblk(NT * c.io)), (const float*)d->dv, NT * c.io, d->dv0);
     lin_bwd(ctx, d, H_POST_CONV, d->v0, NT, d->dv, d->dv0, 1);
     lin_bwd(ctx, d, H_PROJ_OUT, d->xt, NT, d->dv0, d->dxt, 0);
     launch(ctx, "dit_tail", scatter_frames_kernel, dim3(nblk((int64_t)B * S * D)), (const float*)d->dxt, B, T,
@@ -614,9 +627,64 @@ void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* targe
         mlp_bwd(ctx, d, H_TIME0, d->tf, B, d->te_h, d->te_a, d->dg, nullptr);
         mlp_bwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->dctx, nullptr);
     }
+}
+
+// Capture the accumulate step into a graph (prepare included when the adapters changed). On a
+// capture failure the graphs are switched off and the step runs eagerly.
+bool capture(sa3k_ctx* ctx, sa3k_dit* d, int gi, const void* const* key, const float* x_t, const float* target,
+             const float* t, const float* cross, const float* glob, const float* lw) {
+    if (d->gexec[gi]) {
+        SA3K_HIP(hipGraphExecDestroy(d->gexec[gi]));
+        d->gexec[gi] = nullptr;
+    }
+    hipGraph_t g = nullptr;
+    SA3K_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    try {
+        accumulate_body(ctx, d, x_t, target, t, cross, glob, lw);
+    } catch (...) {
+        ctx->capturing = false;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        d->use_graph = false;
+        return false;
+    }
+    ctx->capturing = false;
+    SA3K_HIP(hipStreamEndCapture(ctx->stream, &g));
+    const hipError_t e = hipGraphInstantiate(&d->gexec[gi], g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    SA3K_HIP(e);
+    for (int k = 0; k < 6; ++k) d->gkey[gi][k] = key[k];
+    return true;
+}
+
+void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* target, const float* t, const float* cross,
+                const float* glob, const float* lw, double* loss_out) {
+    const int B = d->tr.batch;
+    const bool graph = d->use_graph && d->warm && !ctx->prof_on;
+    bool launched = false;
+    if (graph) {
+        const int gi = d->dirty ? 1 : 0;
+        const void* key[6] = {x_t, target, t, cross, glob, lw};
+        bool have = d->gexec[gi] != nullptr;
+        for (int k = 0; k < 6 && have; ++k) have = d->gkey[gi][k] == key[k];
+        if (!have) have = capture(ctx, d, gi, key, x_t, target, t, cross, glob, lw);
+        if (have) {
+            SA3K_HIP(hipGraphLaunch(d->gexec[gi], ctx->stream));
+            d->dirty = false;
+            launched = true;
+        }
+    }
+    if (!launched) {
+        accumulate_body(ctx, d, x_t, target, t, cross, glob, lw);
+        d->warm = true;   // the split-K workspace has its final size: later steps can be captured
+    }
     d->count += B;
-    if (loss_out) SA3K_HIP(hipMemcpyAsync(loss_out, d->loss, sizeof(double) * B, hipMemcpyDeviceToHost, ctx->stream));
-    if (loss_out) SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    if (loss_out) {
+        SA3K_HIP(hipMemcpyAsync(loss_out, d->loss, sizeof(double) * B, hipMemcpyDeviceToHost, ctx->stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    }
 }
 
 }  // namespace
@@ -637,6 +705,7 @@ SA3K_API int sa3k_dit_create(sa3k_ctx* ctx, const sa3k_dit_config* cfg, int weig
         sa3k_dit* d = new sa3k_dit();
         d->cfg = *cfg;
         d->wtype = weight_type;
+        if (const char* e = std::getenv("SA3K_DIT_GRAPH")) d->use_graph = std::atoi(e) != 0;
         try {
             describe(d);
             for (Tensor& t : d->tensors) SA3K_HIP(hipMalloc(&t.raw, t.bytes()));
@@ -810,6 +879,18 @@ SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw
         fill(ctx, dit->g, dit->n_params, 0.0f);
         dit->count = 0;
         dit->dirty = true;
+    });
+}
+
+SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on) {
+    return sa3k_guard(ctx, "sa3k_dit_set_graphs", [&] {
+        SA3K_REQUIRE(dit, "null pointer");
+        dit->use_graph = on != 0;
+        for (hipGraphExec_t& e : dit->gexec)
+            if (e) {
+                SA3K_HIP(hipGraphExecDestroy(e));
+                e = nullptr;
+            }
     });
 }
 

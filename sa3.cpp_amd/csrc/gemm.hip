@@ -39,6 +39,7 @@ struct KParams {
 // split-K workspace owned by the context (grows on demand; kernels on one stream use it in turn)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes) {
     if (bytes > ctx->gemm_ws_bytes) {
+        SA3K_REQUIRE(!ctx->capturing, "the split-K workspace cannot grow while a graph is being captured");
         if (ctx->gemm_ws) {
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
             SA3K_HIP(hipFree(ctx->gemm_ws));
@@ -412,10 +413,17 @@ void launch(sa3k_ctx* ctx, KParams p) {
         p.ws = gemm_workspace_bytes(ctx, need);
     }
     dim3 g((unsigned)grid, (unsigned)splits);
-    if (ctx->gemm_pd == 2) gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 2><<<g, kThreads, 0, ctx->stream>>>(p);
-    else gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 1><<<g, kThreads, 0, ctx->stream>>>(p);
-    if (splits > 1) {
+    {
+        static const std::string name = std::string("gemm_decode<") + std::to_string(BM) + "," + std::to_string(BN) +
+                                        "," + std::to_string(WMW) + ",a" + std::to_string(ASRC) + ",b" +
+                                        std::to_string(BSRC) + (BF16 ? ",bf16>" : ",f32>");
+        KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
+        if (ctx->gemm_pd == 2) gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 2><<<g, kThreads, 0, ctx->stream>>>(p);
+        else gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 1><<<g, kThreads, 0, ctx->stream>>>(p);
         SA3K_LAUNCHED();
+    }
+    if (splits > 1) {
+        KernelScope ks(ctx, "gemm_splitk_reduce");
         gemm_splitk_reduce<<<(unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
     }
 }

@@ -294,9 +294,16 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     if (splits > 1)
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
     dim3 g((unsigned)grid, (unsigned)splits);
-    gemm_dma_kernel<BM, BN, WMW, STAGES, BF16><<<g, kThreads, 0, ctx->stream>>>(p);
-    if (splits > 1) {
+    {
+        // profiled per kernel instantiation, with its algorithmic flops (padding excluded)
+        static const std::string name = std::string("gemm_dma<") + std::to_string(BM) + "," + std::to_string(BN) + "," +
+                                        std::to_string(WMW) + "," + std::to_string(STAGES) + (BF16 ? ",bf16>" : ",f32>");
+        KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
+        gemm_dma_kernel<BM, BN, WMW, STAGES, BF16><<<g, kThreads, 0, ctx->stream>>>(p);
         SA3K_LAUNCHED();
+    }
+    if (splits > 1) {
+        KernelScope ks(ctx, "gemm_splitk_reduce");
         gemm_dma_splitk_reduce<<<(unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
     }
 }

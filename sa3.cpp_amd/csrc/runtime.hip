@@ -36,6 +36,7 @@ void prof_collect(sa3k_ctx* ctx) {
         ProfTotal& t = ctx->prof_totals[r.name];
         t.count += 1;
         t.ms += ms;
+        t.work += r.work;
         ctx->prof_pool.push_back(r.start);
         ctx->prof_pool.push_back(r.stop);
     }
@@ -203,8 +204,8 @@ SA3K_API int sa3k_profile_report(sa3k_ctx* ctx, char* buf, int buf_len) {
         std::string out;
         char line[256];
         for (const auto& kv : ctx->prof_totals) {
-            std::snprintf(line, sizeof line, "%s %lld %.6f\n", kv.first.c_str(),
-                          (long long)kv.second.count, kv.second.ms);
+            std::snprintf(line, sizeof line, "%s %lld %.6f %.6e\n", kv.first.c_str(),
+                          (long long)kv.second.count, kv.second.ms, kv.second.work);
             out += line;
         }
         SA3K_REQUIRE((int)out.size() < buf_len, "report buffer too small");

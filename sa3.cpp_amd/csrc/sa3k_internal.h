@@ -19,10 +19,12 @@
 struct ProfRecord {
     const char* name;
     hipEvent_t start, stop;
+    double work;   // algorithmic flops (or bytes) of the launch, 0 when not counted
 };
 struct ProfTotal {
     int64_t count = 0;
     double ms = 0.0;
+    double work = 0.0;
 };
 
 struct sa3k_ctx {
@@ -44,6 +46,7 @@ struct sa3k_ctx {
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
     int gemm_wg_per_cu = 2;               // resident workgroups per CU assumed by the split choice
+    bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
 };
 
@@ -96,9 +99,10 @@ void prof_collect(sa3k_ctx* ctx);
 
 class KernelScope {
 public:
-    KernelScope(sa3k_ctx* ctx, const char* name) : ctx_(ctx) {
+    KernelScope(sa3k_ctx* ctx, const char* name, double work = 0.0) : ctx_(ctx) {
         if (!ctx_->prof_on) return;
         rec_.name = name;
+        rec_.work = work;
         rec_.start = prof_event(ctx_);
         rec_.stop = prof_event(ctx_);
         (void)hipEventRecord(rec_.start, ctx_->stream);

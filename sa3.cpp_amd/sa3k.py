@@ -128,6 +128,7 @@ def _declare(lib):
         "sa3k_dit_accumulate": (I, [P, P, P, P, P, P, P, P, P]),
         "sa3k_dit_apply_adamw": (I, [P, P, C.POINTER(AdamWParams), I, C.POINTER(D)]),
         "sa3k_dit_forward": (I, [P, P, P, P, P, P, P]),
+        "sa3k_dit_set_graphs": (I, [P, P, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -262,14 +263,14 @@ class Context:
     def profile_reset(self):
         self.check(self.lib.sa3k_profile_reset(self.h))
 
-    def profile_report(self):
-        """{kernel name: (launches, total_ms)}"""
+    def profile_report(self, with_work=False):
+        """{scope name: (launches, total_ms)} or, with_work, (launches, total_ms, algorithmic work)"""
         buf = C.create_string_buffer(1 << 16)
         self.check(self.lib.sa3k_profile_report(self.h, buf, 1 << 16))
         out = {}
         for line in buf.value.decode().splitlines():
-            name, cnt, ms = line.rsplit(" ", 2)
-            out[name] = (int(cnt), float(ms))
+            name, cnt, ms, work = line.rsplit(" ", 3)
+            out[name] = (int(cnt), float(ms), float(work)) if with_work else (int(cnt), float(ms))
         return out
 
     # -- K6
@@ -510,6 +511,9 @@ class Dit:
         self.ctx.check(self.ctx.lib.sa3k_dit_apply_adamw(self.ctx.h, self.h, C.byref(p), step,
                                                          C.byref(nrm) if want_norm else None))
         return nrm.value if want_norm else None
+
+    def set_graphs(self, on):
+        self.ctx.check(self.ctx.lib.sa3k_dit_set_graphs(self.ctx.h, self.h, int(on)))
 
     def forward(self, x_t, t, cross, glob, velocity):
         self.ctx.check(self.ctx.lib.sa3k_dit_forward(self.ctx.h, self.h, x_t.ptr, t.ptr, cross.ptr, glob.ptr,

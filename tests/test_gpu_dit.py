@@ -140,6 +140,33 @@ def test_dit_schedules_accumulation_and_adamw(ctx):
         "resident and recompute schedules must agree bitwise"
 
 
+def test_dit_graph_replays_match_eager(ctx):
+    # the captured step (with and without the adapter refresh) replayed over several updates, with
+    # eager work and host round trips in between, gives the eager path's results bit for bit
+    cfg = dict(CFG, window=6)
+    tensors, adapters, inputs = db.random_dit(44, cfg, "full")
+    models = []
+    for graphs in (False, True):
+        d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
+        d.set_graphs(graphs)
+        models.append(d)
+    up, _ = upload_inputs(ctx, inputs)
+    try:
+        for step in range(1, 6):
+            res = []
+            for d in models:
+                l1 = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+                l2 = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])   # no refresh
+                g = d.arena(1).numpy()
+                d.apply_adamw(HP, step)
+                res.append((l1, l2, g, d.arena(0).numpy(), d.arena(3).numpy()))
+            for a, b in zip(res[0], res[1]):
+                assert np.array_equal(a, b), f"graph replay differs from eager at step {step}"
+    finally:
+        for d in models:
+            d.destroy()
+
+
 def test_dit_full_size_step(ctx):
     # 24 blocks, dim 1536, 24 heads, FFN 6144, io 64, batch 2 x (64 + 1024), 128 context tokens of 768
     c = sa3k.dit_config(64, 1536, 24, 24, 768, 64, 256, 6144, window=256)
