@@ -17,6 +17,7 @@
 // Head (dit_head, src/dit.h:286-312) and tail (dit_tail, src/dit.h:316-325) run as adapted linears
 // plus the small kernels below; tokens are batch-major ([B][S][dim], S = mem_tokens + T).
 #include "block.h"
+#include "lora.h"
 
 #include <algorithm>
 #include <cmath>
@@ -269,6 +270,7 @@ struct sa3k_dit {
     int64_t n_params = 0;
     bool dirty = true;
     int count = 0;
+    LinGroup* group = nullptr;      // every adapted linear, refreshed together
     // activations
     std::vector<sa3k_block_ws*> ws;
     std::vector<float*> xs;
@@ -349,6 +351,7 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
     for (void* p : d->bufs) (void)hipFree(p);
     for (hipGraphExec_t e : d->gexec)
         if (e) (void)hipGraphExecDestroy(e);
+    lin_group_free(d->group);
     for (float* p : {d->p, d->g, d->m, d->v})
         if (p) (void)hipFree(p);
     delete d;
@@ -467,6 +470,22 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     double* ls = dalloc<double>((size_t)B);
     d->bufs.push_back(ls);
     d->loss = ls;
+    {
+        std::vector<sa3k_lin*> lins;
+        std::vector<const float*> A, Bm, mag, bnsq;
+        for (const Target& t : d->targets) {
+            lins.push_back(t.lin);
+            A.push_back(d->p + t.off_a);
+            Bm.push_back(d->p + t.off_b);
+            mag.push_back(tr.dora ? d->p + t.off_m : nullptr);
+            bnsq.push_back(tr.dora ? t.bnsq : nullptr);
+        }
+        d->group = lin_group_create(ctx, lins.data(), (int)lins.size(), A.data(), Bm.data(), mag.data(), bnsq.data(),
+                                    d->scale, tr.dora);
+        for (int i = 0; i < H_N; ++i)
+            if (d->head_target[i] < 0)
+                chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
+    }
     const int nws = tr.recompute ? 1 : c.depth;
     for (int l = 0; l < nws; ++l) d->ws.push_back(block_ws_build(bc, B, S, Ctx, l == 0 ? nullptr : d->ws[0]));
     SA3K_HIP(hipStreamSynchronize(ctx->stream));
@@ -477,29 +496,7 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
 void prepare(sa3k_ctx* ctx, sa3k_dit* d) {
     if (!d->dirty) return;
     KernelScope ks(ctx, "dit_prepare");
-    const int dora = d->tr.dora;
-    for (int l = 0; l < d->cfg.depth; ++l) {
-        const float* A[7];
-        const float* Bm[7];
-        const float* mag[7];
-        for (int t = 0; t < 7; ++t) {
-            const Target& tg = d->targets[d->block_target[(size_t)l * 7 + t]];
-            A[t] = d->p + tg.off_a;
-            Bm[t] = d->p + tg.off_b;
-            mag[t] = dora ? d->p + tg.off_m : nullptr;
-        }
-        block_prepare(ctx, d->blocks[l], A, Bm, mag, d->scale, dora);
-    }
-    for (int i = 0; i < H_N; ++i) {
-        const int ti = d->head_target[i];
-        if (ti < 0) {
-            chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
-            continue;
-        }
-        const Target& tg = d->targets[ti];
-        chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], d->p + tg.off_a, d->p + tg.off_b, d->scale, dora,
-                                  dora ? d->p + tg.off_m : nullptr, dora ? tg.bnsq : nullptr));
-    }
+    lin_group_prepare(ctx, d->group);
     d->dirty = false;
 }
 

@@ -70,8 +70,6 @@ struct sa3k_lin {
     float* gn = nullptr;                // [out]
     void* Ax = nullptr;                 // [r][out] compute type: 2s (B*gn)^T
     void* A2x = nullptr;                // [r][r]   compute type: 2s^2 B^T diag(gn) B
-    float* part = nullptr;              // column-reduction partial sums
-    size_t part_elems = 0;
     float* red = nullptr;               // [out][r] reduced dU^T Hc
 };
 
@@ -315,6 +313,140 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
     for (int a = 0; a < R; ++a) p[(int64_t)a * in + i] = acc[a];
 }
 
+// ---- the same column reductions on bf16 MFMA (bf16 precision): skinny "TN" products over tokens
+//   TN_DY: Q = dU = dY * d (written out as bf16), part[z][0][c] = sum_n dY*U, part[z][1+a][c] =
+//          sum_n Hc[n][a] dU[n][c]                                   (dU^T Hc, stride 33 rows)
+//   TN_X:  part[z][a][c] = sum_n G[n][a] X[n][c]                      ((s dU B)^T X, stride 32 rows)
+// over the token rows of split z. A workgroup owns 64 columns; per 32-token step the Q tile (dU or
+// X) and the P tile (Hc or G, rank padded to 32) are stored transposed in LDS so that each MFMA
+// operand is one 16-byte read of 8 consecutive tokens; each wave owns 16 columns x 32 ranks (two
+// v_mfma_f32_16x16x32_bf16 per step). The kernel is bound by streaming Q once.
+constexpr int TN_DY = 0, TN_X = 1;
+constexpr int TN_COLS = 64, TN_ROWS = 32, TN_LD = 40;   // LDS row: 32 tokens + 8 pad (80 bytes)
+
+template <int MODE, class QT>
+__global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restrict__ Q, const bf16* __restrict__ P, int r,
+                                                             const bf16* __restrict__ U, const float* __restrict__ d,
+                                                             bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
+                                                             int64_t cols, int64_t rows_per) {
+    __shared__ __attribute__((aligned(16))) bf16 qt[TN_COLS * TN_LD];
+    __shared__ __attribute__((aligned(16))) bf16 pt[32 * TN_LD];
+    __shared__ float red[TN_ROWS][TN_COLS + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t c0 = (int64_t)blockIdx.x * TN_COLS;
+    const int z = blockIdx.y;
+    const int64_t r0 = (int64_t)z * rows_per, r1 = min(N, r0 + rows_per);
+    const int lrow = tid >> 3;            // token row of this thread's loads within a step
+    const int c8 = (tid & 7) * 8;         // its 8 columns
+    const int a4 = (tid & 7) * 4;         // its 4 ranks of the P tile
+    const int64_t col = c0 + c8;
+    const bool col_ok = col < cols;       // cols is a multiple of 8
+    float dd[8], gd[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        gd[j] = 0.f;
+        dd[j] = (MODE == TN_DY && d && col_ok) ? d[col + j] : 1.0f;
+    }
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const int r16 = lane & 15, g = lane >> 4;
+    for (int64_t n0 = r0; n0 < r1; n0 += TN_ROWS) {
+        const int64_t n = n0 + lrow;
+        const bool row_ok = n < r1;
+        float q[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = 0.f;
+        if (row_ok && col_ok) {
+            if constexpr (MODE == TN_DY) {
+                const float4* y4 = reinterpret_cast<const float4*>(Q + n * cols + col);
+                const float4 ya = y4[0], yb = y4[1];
+                const float y[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+                bf16x8 ub;
+                if (U) ub = *reinterpret_cast<const bf16x8*>(U + n * cols + col);
+                bf16x8 du;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    q[j] = y[j] * dd[j];
+                    du[j] = (bf16)q[j];
+                    if (U) gd[j] += y[j] * (float)ub[j];
+                }
+                *reinterpret_cast<bf16x8*>(dU + n * cols + col) = du;
+            } else if constexpr (sizeof(QT) == 4) {
+                const float4* x4 = reinterpret_cast<const float4*>(Q + n * cols + col);
+                const float4 xa = x4[0], xb = x4[1];
+                q[0] = xa.x; q[1] = xa.y; q[2] = xa.z; q[3] = xa.w; q[4] = xb.x; q[5] = xb.y; q[6] = xb.z; q[7] = xb.w;
+            } else {
+                const bf16x8 xv = *reinterpret_cast<const bf16x8*>(Q + n * cols + col);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = (float)xv[j];
+            }
+        }
+        float pv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (row_ok && a4 < r) {
+            const bf16* pp = P + n * r + a4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pv[j] = (float)pp[j];
+        }
+        __syncthreads();   // the previous step's MFMAs are done with the LDS tiles
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qt[(c8 + j) * TN_LD + lrow] = (bf16)q[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pt[(a4 + j) * TN_LD + lrow] = (bf16)pv[j];
+        __syncthreads();
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(qt + (wave * 16 + r16) * TN_LD + 8 * g);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(pt + (t * 16 + r16) * TN_LD + 8 * g);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[t], 0, 0, 0);
+        }
+    }
+    // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + r16
+    constexpr int RS = MODE == TN_DY ? 33 : 32;
+    const int row0 = MODE == TN_DY ? 1 : 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int a = t * 16 + r16;
+        if (a >= r) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t c = c0 + wave * 16 + 4 * g + v;
+            if (c < cols) part[((int64_t)z * RS + row0 + a) * cols + c] = acc[t][v];
+        }
+    }
+    if constexpr (MODE == TN_DY) {   // gd: sum the 32 token-row slots of each column
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[lrow][c8 + j] = gd[j];
+        __syncthreads();
+        if (tid < TN_COLS) {
+            float s = 0.f;
+            for (int k = 0; k < TN_ROWS; ++k) s += red[k][tid];
+            if (c0 + tid < cols) part[((int64_t)z * RS) * cols + c0 + tid] = s;
+        }
+    }
+}
+
+// token rows per split of a skinny TN reduction over `cols` columns: about 1024 workgroups
+int64_t tn_rows_per(int64_t cols, int64_t N) {
+    const int64_t tiles = ceil_div(cols, TN_COLS);
+    return std::max<int64_t>(TN_ROWS, ceil_div(ceil_div(N * tiles, 1024), TN_ROWS) * TN_ROWS);
+}
+
+// partial sums of the column reductions: one buffer per context, shared by every linear (used
+// in turn on the context stream); it grows outside graph capture only
+float* reduce_workspace(sa3k_ctx* ctx, size_t bytes) {
+    if (bytes > ctx->red_ws_bytes) {
+        SA3K_REQUIRE(!ctx->capturing, "the reduction workspace cannot grow while a graph is being captured");
+        if (ctx->red_ws) {
+            SA3K_HIP(hipStreamSynchronize(ctx->stream));
+            SA3K_HIP(hipFree(ctx->red_ws));
+            ctx->red_ws = nullptr;
+            ctx->red_ws_bytes = 0;
+        }
+        SA3K_HIP(hipMalloc(&ctx->red_ws, bytes));
+        ctx->red_ws_bytes = bytes;
+    }
+    return static_cast<float*>(ctx->red_ws);
+}
+
 // y[j] (+)= sum_s part[s][j], j < n (fixed summation order: deterministic)
 __global__ __launch_bounds__(kThreads) void sum_splits_kernel(const float* __restrict__ part, int64_t stride, int S,
                                                               int64_t n, float* __restrict__ y, int accumulate) {
@@ -402,7 +534,7 @@ void free_lin(sa3k_lin* L) {
     if (!L) return;
     for (void* p : {L->Xb, L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
                     (void*)L->d, L->Hc, L->U, L->dU, L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x,
-                    (void*)L->part, (void*)L->red})
+                    (void*)L->red})
         if (p) (void)hipFree(p);
     delete L;
 }
@@ -496,22 +628,38 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         return;
     }
     // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens)
-    {
+    if constexpr (sizeof(CT) == 2) {
+        const int64_t rows_per = tn_rows_per(out, N);
+        const int S = (int)ceil_div(N, rows_per);
+        float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
+        {
+            KernelScope ks(ctx, "lin_bwd_colred_dy", 2.0 * N * out * r);
+            skinny_tn_kernel<TN_DY, float><<<dim3((unsigned)ceil_div(out, TN_COLS), (unsigned)S), kThreads, 0,
+                                               ctx->stream>>>(
+                dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
+                L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per);
+            SA3K_LAUNCHED();
+        }
+        KernelScope ks(ctx, "lin_bwd_reduce");
+        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(r + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
+            part, (int64_t)33 * out, S, (int64_t)(r + 1) * out, L->red, 0);
+        SA3K_LAUNCHED();
+    } else {
         const int S = choose_splits(out, N);
         const int64_t rows_per = ceil_div(N, S);
-        SA3K_REQUIRE((size_t)S * (R + 1) * out <= L->part_elems, "column-reduction scratch too small");
+        float* part = reduce_workspace(ctx, (size_t)S * (R + 1) * out * sizeof(float));
         dim3 grid((unsigned)ceil_div(out, kThreads), (unsigned)S);
         {
             KernelScope ks(ctx, "lin_bwd_colred_dy");
             colred_dy_kernel<CT, R><<<grid, kThreads, 0, ctx->stream>>>(
                 dY, static_cast<const CT*>(L->dora ? L->U : nullptr), L->dora ? L->d : nullptr,
-                static_cast<const CT*>(L->Hc), static_cast<CT*>(L->dU), L->part, N, out, r, rows_per);
+                static_cast<const CT*>(L->Hc), static_cast<CT*>(L->dU), part, N, out, r, rows_per);
             SA3K_LAUNCHED();
         }
         KernelScope ks(ctx, "lin_bwd_reduce");
         // gd -> L->gd ; rows a+1 -> red[a][out]
         sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(R + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
-            L->part, (int64_t)(R + 1) * out, S, (int64_t)(R + 1) * out, L->red, 0);
+            part, (int64_t)(R + 1) * out, S, (int64_t)(R + 1) * out, L->red, 0);
         SA3K_LAUNCHED();
     }
     // L->red holds [gd | dUtH rows]: gd = red[0..out), dUtH[a] = red[(a+1)*out ...]
@@ -576,29 +724,271 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, "lin_bwd_dora_da");
     }
     // 4. dA += sdUB^T X
-    {
+    if constexpr (sizeof(CT) == 2) {
+        const int64_t rows_per = tn_rows_per(in, N);
+        const int S = (int)ceil_div(N, rows_per);
+        float* part = reduce_workspace(ctx, (size_t)S * 32 * in * sizeof(float));
+        const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)S);
+        {
+            KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);
+            if (x_src == SRC_F32)
+                skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
+                    N, in, rows_per);
+            else
+                skinny_tn_kernel<TN_X, bf16><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const bf16*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
+                    N, in, rows_per);
+            SA3K_LAUNCHED();
+        }
+        KernelScope ks(ctx, "lin_bwd_reduce");
+        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
+            part, (int64_t)32 * in, S, (int64_t)r * in, dA, 1);
+        SA3K_LAUNCHED();
+    } else {
         const int S = choose_splits(in, N);
         const int64_t rows_per = ceil_div(N, S);
-        SA3K_REQUIRE((size_t)S * R * in <= L->part_elems, "column-reduction scratch too small");
+        float* part = reduce_workspace(ctx, (size_t)S * R * in * sizeof(float));
         dim3 grid((unsigned)ceil_div(in, kThreads), (unsigned)S);
         {
             KernelScope ks(ctx, "lin_bwd_colred_x");
             if (x_src == SRC_F32)
                 colred_x_kernel<float, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), L->part, N, in, r, rows_per);
+                    static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), part, N, in, r, rows_per);
             else
                 colred_x_kernel<bf16, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const bf16*>(X), static_cast<const CT*>(L->sdUB), L->part, N, in, r, rows_per);
+                    static_cast<const bf16*>(X), static_cast<const CT*>(L->sdUB), part, N, in, r, rows_per);
             SA3K_LAUNCHED();
         }
         KernelScope ks(ctx, "lin_bwd_reduce");
         sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
-            L->part, (int64_t)R * in, S, (int64_t)r * in, dA, 1);
+            part, (int64_t)R * in, S, (int64_t)r * in, dA, 1);
         SA3K_LAUNCHED();
     }
 }
 
+// ---------------------------------------------------------------- grouped adapter refresh
+// One descriptor per member linear; every stage is one launch over the whole group.
+struct PrepDesc {
+    const float *A, *B, *mag, *bnsq;   // adapter (device) [r][in], [out][r], [out], [out]
+    bf16 *Ac, *At, *Bc, *Bt;           // compute-type copies [r][in], [in][r], [out][r], [r][out]
+    const bf16* W;                     // bf16 working copy of the base [out][in]
+    float *Pt, *G, *BG, *nsq, *d;
+    int in, out, tile0;                // tile0: first 64-row tile of this member in the P stage
+};
+
+// Ac/At/Bc/Bt from A and B (grid.y = member)
+__global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc* __restrict__ ds, int r) {
+    const PrepDesc& q = ds[blockIdx.y];
+    const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t na = (int64_t)r * q.in, nb = (int64_t)q.out * r;
+    if (e < na) {
+        const int64_t a = e / q.in, i = e - a * q.in;
+        const bf16 v = (bf16)q.A[e];
+        q.Ac[e] = v;
+        q.At[i * r + a] = v;
+    } else if (e < na + nb) {
+        const int64_t f = e - na, o = f / r, a = f - o * r;
+        const bf16 v = (bf16)q.B[f];
+        q.Bc[f] = v;
+        q.Bt[a * q.out + o] = v;
+    }
+}
+
+// P^T[a][o] = sum_i A[a][i] W[o][i] for every member: one workgroup per 64 rows o of one member,
+// each wave 16 rows o x 32 ranks on v_mfma_f32_16x16x32_bf16. Both operands are read straight from
+// global memory (a lane's 8 consecutive K elements are 16 contiguous bytes of a row of W / Ac),
+// so W streams once with no LDS; 4 K-steps are issued ahead of their MFMAs.
+__global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __restrict__ ds,
+                                                            const int* __restrict__ tile_member, int r) {
+    const int m = tile_member[blockIdx.x];
+    const PrepDesc& q = ds[m];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int64_t o0 = (int64_t)(blockIdx.x - q.tile0) * 64 + wave * 16;
+    if (o0 >= q.out) return;
+    const bf16* wrow = q.W + (o0 + r16) * (int64_t)q.in + 8 * g;
+    const bf16* a0row = q.Ac + (int64_t)r16 * q.in + 8 * g;
+    const bf16* a1row = q.Ac + (int64_t)(16 + r16) * q.in + 8 * g;
+    const bool hi = r > 16;   // the second 16-rank tile exists
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    constexpr int U = 4;
+    for (int k0 = 0; k0 < q.in; k0 += 32 * U) {
+        bf16x8 w[U], a0[U], a1[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = k0 + 32 * u;
+            if (k < q.in) {
+                w[u] = *reinterpret_cast<const bf16x8*>(wrow + k);
+                a0[u] = r16 < r ? *reinterpret_cast<const bf16x8*>(a0row + k) : bf16x8{};
+                a1[u] = (hi && 16 + r16 < r) ? *reinterpret_cast<const bf16x8*>(a1row + k) : bf16x8{};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (k0 + 32 * u < q.in) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], a0[u], acc0, 0, 0, 0);
+                if (hi) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], a1[u], acc1, 0, 0, 0);
+            }
+        }
+    }
+    // D[i][j]: o = o0 + 4g + v, rank j = r16 (+16)
+    if (r16 < r)
+        *reinterpret_cast<float4*>(q.Pt + (int64_t)r16 * q.out + o0 + 4 * g) = make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
+    if (hi && 16 + r16 < r)
+        *reinterpret_cast<float4*>(q.Pt + (int64_t)(16 + r16) * q.out + o0 + 4 * g) =
+            make_float4(acc1[0], acc1[1], acc1[2], acc1[3]);
+}
+
+// G = A A^T (double accumulation), grid (r*r, members)
+__global__ __launch_bounds__(kThreads) void group_gram_kernel(const PrepDesc* __restrict__ ds, int r) {
+    const PrepDesc& q = ds[blockIdx.y];
+    __shared__ double sh[kThreads / 64];
+    const int a = blockIdx.x / r, b = blockIdx.x % r;
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < q.in; i += kThreads) acc += (double)q.A[a * q.in + i] * q.A[b * q.in + i];
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) q.G[a * r + b] = (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+}
+
+// dora_terms_kernel for every member, grid (ceil(max out / 8), members)
+__global__ __launch_bounds__(kThreads) void group_dora_terms_kernel(const PrepDesc* __restrict__ ds, int r, float s) {
+    const PrepDesc& q = ds[blockIdx.y];
+    __shared__ float gs[32][33];
+    __shared__ float bs[8][32];
+    const int ol = threadIdx.x >> 5, a = threadIdx.x & 31;
+    if ((int64_t)blockIdx.x * 8 >= q.out) return;   // uniform per block
+    const int64_t o = (int64_t)blockIdx.x * 8 + ol;
+    for (int k = threadIdx.x; k < 32 * 32; k += kThreads) {
+        const int i = k >> 5, j = k & 31;
+        gs[i][j] = (i < r && j < r) ? q.G[i * r + j] : 0.f;
+    }
+    bs[ol][a] = (o < q.out && a < r) ? q.B[o * r + a] : 0.f;
+    __syncthreads();
+    float gv = 0.f;
+#pragma unroll 8
+    for (int c = 0; c < 32; ++c) gv += bs[ol][c] * gs[c][a];
+    float t2 = 0.f, t3 = 0.f;
+    if (o < q.out && a < r) {
+        q.BG[o * r + a] = gv;
+        t2 = q.Pt[(int64_t)a * q.out + o] * bs[ol][a];
+        t3 = bs[ol][a] * gv;
+    }
+    for (int off = 16; off > 0; off >>= 1) {
+        t2 += __shfl_xor(t2, off, 32);
+        t3 += __shfl_xor(t3, off, 32);
+    }
+    if (a == 0 && o < q.out) {
+        const float n2 = q.bnsq[o] + 2.0f * s * t2 + s * s * t3;
+        q.nsq[o] = n2;
+        q.d[o] = q.mag[o] / sqrtf(n2);
+    }
+}
+
 }  // namespace
+
+namespace sa3k {
+
+struct LinGroup {
+    std::vector<sa3k_lin*> lins;
+    std::vector<const float*> B, mag;
+    PrepDesc* dev = nullptr;
+    int* tile_member = nullptr;
+    int n = 0, r = 0, dora = 0, tiles = 0;
+    int64_t max_conv = 0, max_out = 0;
+    float s = 1.0f;
+};
+
+void lin_group_free(LinGroup* g) {
+    if (!g) return;
+    if (g->dev) (void)hipFree(g->dev);
+    if (g->tile_member) (void)hipFree(g->tile_member);
+    delete g;
+}
+
+LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const float* const* A, const float* const* B,
+                           const float* const* mag, const float* const* bnsq, float scale, int dora) {
+    SA3K_REQUIRE(n > 0 && lins && A && B && (!dora || (mag && bnsq)), "bad linear group");
+    LinGroup* g = new LinGroup();
+    try {
+        g->n = n;
+        g->r = lins[0]->rank;
+        g->dora = dora ? 1 : 0;
+        g->s = scale;
+        std::vector<PrepDesc> h(n);
+        std::vector<int> tm;
+        for (int i = 0; i < n; ++i) {
+            sa3k_lin* L = lins[i];
+            SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && L->W->wb && L->rank == g->r && g->r > 0,
+                         "a linear group needs bf16 linears of one rank with bf16 working copies");
+            SA3K_REQUIRE(A[i] && B[i] && (!dora || (mag[i] && bnsq[i])), "missing adapter pointer");
+            const int64_t in = L->W->in, out = L->W->out;
+            SA3K_REQUIRE(out % 64 == 0 || out % 16 == 0, "group output dimension must be a multiple of 16");
+            PrepDesc& q = h[i];
+            q.A = A[i]; q.B = B[i]; q.mag = dora ? mag[i] : nullptr; q.bnsq = dora ? bnsq[i] : nullptr;
+            q.Ac = static_cast<bf16*>(L->Ac); q.At = static_cast<bf16*>(L->At);
+            q.Bc = static_cast<bf16*>(L->Bc); q.Bt = static_cast<bf16*>(L->Bt);
+            q.W = static_cast<const bf16*>(L->W->wb);
+            q.Pt = L->Pt; q.G = L->G; q.BG = L->BG; q.nsq = L->nsq; q.d = L->d;
+            q.in = (int)in; q.out = (int)out;
+            q.tile0 = (int)tm.size();
+            for (int64_t t = 0; t < ceil_div(out, 64); ++t) tm.push_back(i);
+            g->max_conv = std::max(g->max_conv, (int64_t)g->r * (in + out));
+            g->max_out = std::max(g->max_out, out);
+            g->lins.push_back(L);
+            g->B.push_back(B[i]);
+            g->mag.push_back(dora ? mag[i] : nullptr);
+        }
+        g->tiles = (int)tm.size();
+        SA3K_HIP(hipMalloc(&g->dev, sizeof(PrepDesc) * n));
+        SA3K_HIP(hipMalloc(&g->tile_member, sizeof(int) * tm.size()));
+        SA3K_HIP(hipMemcpyAsync(g->dev, h.data(), sizeof(PrepDesc) * n, hipMemcpyHostToDevice, ctx->stream));
+        SA3K_HIP(hipMemcpyAsync(g->tile_member, tm.data(), sizeof(int) * tm.size(), hipMemcpyHostToDevice, ctx->stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
+    } catch (...) {
+        lin_group_free(g);
+        throw;
+    }
+    return g;
+}
+
+void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
+    for (int i = 0; i < g->n; ++i) {   // the per-linear state sa3k_lin_prepare sets
+        sa3k_lin* L = g->lins[i];
+        L->s = g->s;
+        L->dora = g->dora;
+        L->B = g->B[i];
+        L->mag = g->mag[i];
+    }
+    {
+        KernelScope ks(ctx, "group_convert");
+        group_convert_kernel<<<dim3((unsigned)ceil_div(g->max_conv, kThreads), (unsigned)g->n), kThreads, 0,
+                               ctx->stream>>>(g->dev, g->r);
+        SA3K_LAUNCHED();
+    }
+    if (!g->dora) return;
+    {
+        double flops = 0.0;
+        for (sa3k_lin* L : g->lins) flops += 2.0 * g->r * (double)L->W->in * (double)L->W->out;
+        KernelScope ks(ctx, "group_pt", flops);
+        group_pt_kernel<<<(unsigned)g->tiles, kThreads, 0, ctx->stream>>>(g->dev, g->tile_member, g->r);
+        SA3K_LAUNCHED();
+    }
+    {
+        KernelScope ks(ctx, "group_gram");
+        group_gram_kernel<<<dim3((unsigned)(g->r * g->r), (unsigned)g->n), kThreads, 0, ctx->stream>>>(g->dev, g->r);
+        SA3K_LAUNCHED();
+    }
+    {
+        KernelScope ks(ctx, "group_dora_terms");
+        group_dora_terms_kernel<<<dim3((unsigned)ceil_div(g->max_out, 8), (unsigned)g->n), kThreads, 0, ctx->stream>>>(
+            g->dev, g->r, g->s);
+        SA3K_LAUNCHED();
+    }
+}
+
+}  // namespace sa3k
 
 // ------------------------------------------------------------------------------------ C ABI
 extern "C" {
@@ -722,9 +1112,6 @@ SA3K_API int sa3k_lin_create(sa3k_ctx* ctx, const sa3k_weight* W, int rank, int 
             if (prec == SA3K_PREC_BF16) L->Xb = dev_alloc<bf16>(max_tokens * in);
             L->gd = dev_alloc<float>(out); L->gn = dev_alloc<float>(out);
             L->Ax = ct_alloc(r * out); L->A2x = ct_alloc(r * r);
-            L->part_elems = std::max((size_t)choose_splits(out, max_tokens) * 33 * out,
-                                     (size_t)choose_splits(in, max_tokens) * 32 * in);
-            L->part = dev_alloc<float>(L->part_elems);
             L->red = dev_alloc<float>(33 * out);
         } catch (...) {
             free_lin(L);

@@ -95,6 +95,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->adamw_partials) (void)hipFree(ctx->adamw_partials);
     if (ctx->adamw_result) (void)hipFree(ctx->adamw_result);
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    if (ctx->red_ws) (void)hipFree(ctx->red_ws);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     for (const ProfRecord& r : ctx->prof_pending) {
         (void)hipEventDestroy(r.start);

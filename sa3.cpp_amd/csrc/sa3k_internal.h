@@ -46,6 +46,8 @@ struct sa3k_ctx {
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
     int gemm_wg_per_cu = 2;               // resident workgroups per CU assumed by the split choice
+    void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
+    size_t red_ws_bytes = 0;
     bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
 };
