@@ -116,32 +116,72 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
 // Column partial sums per sample over a chunk of rows. mode 0 (norm modulation):
 //   p0 = sum dh * x * rstd * gamma (d sc),  p1 = sum dh (d sh)
 // mode 1 (gate g, s = sigmoid(1 - g)):  p0 = -sum dout * y * s (1 - s)
-// part layout [B][nchunk][2][dim]
+// part layout [B][nchunk][2][dim]. With counters, the last chunk of a (column block, sample) to
+// arrive adds the chunk sums, in chunk order, into dssg (see colred_sum_kernel); else that kernel
+// does it.
 __global__ __launch_bounds__(kThreads) void colred_kernel(int mode, const float* __restrict__ a,
                                                           const float* __restrict__ x, const float* __restrict__ rstd,
                                                           const float* __restrict__ gamma, const float* __restrict__ modv,
-                                                          int g_part, int S, int dim, int chunk, float* __restrict__ part) {
+                                                          int g_part, int S, int dim, int chunk, float* __restrict__ part,
+                                                          int part0, float* __restrict__ dssg, int* __restrict__ counters) {
     const int c = blockIdx.x * kThreads + threadIdx.x;
     const int ch = blockIdx.y, b = blockIdx.z, nch = gridDim.y;
-    if (c >= dim) return;
+    const bool ok = c < dim;
     const int t0 = ch * chunk, t1 = min(S, t0 + chunk);
     float p0 = 0.f, p1 = 0.f;
-    float s = 0.f;
-    if (mode == 1) s = sigmoidf_(1.0f - modv[((int64_t)b * 6 + g_part) * dim + c]);
-    for (int t = t0; t < t1; ++t) {
-        const int64_t n = (int64_t)b * S + t;
-        const float av = a[n * dim + c];
-        if (mode == 0) {
-            p0 += av * x[n * dim + c] * rstd[n] * gamma[c];
-            p1 += av;
-        } else {
-            p0 += av * x[n * dim + c];
+    if (ok) {
+        const float gm = mode == 0 ? gamma[c] : 0.f;
+        int t = t0;
+        for (; t + 4 <= t1; t += 4) {   // four independent rows in flight
+            float av[4], xv[4], rs[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t n = (int64_t)b * S + t + u;
+                av[u] = a[n * dim + c];
+                xv[u] = x[n * dim + c];
+                rs[u] = mode == 0 ? rstd[n] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (mode == 0) {
+                    p0 += av[u] * xv[u] * rs[u] * gm;
+                    p1 += av[u];
+                } else {
+                    p0 += av[u] * xv[u];
+                }
+            }
         }
+        for (; t < t1; ++t) {
+            const int64_t n = (int64_t)b * S + t;
+            const float av = a[n * dim + c];
+            if (mode == 0) {
+                p0 += av * x[n * dim + c] * rstd[n] * gm;
+                p1 += av;
+            } else {
+                p0 += av * x[n * dim + c];
+            }
+        }
+        if (mode == 1) {
+            const float s = sigmoidf_(1.0f - modv[((int64_t)b * 6 + g_part) * dim + c]);
+            p0 *= -s * (1.0f - s);
+        }
+        float* o = part + (((int64_t)b * nch + ch) * 2) * dim;
+        st_coherent(o + c, p0);
+        st_coherent(o + dim + c, p1);
     }
-    if (mode == 1) p0 *= -s * (1.0f - s);
-    float* o = part + (((int64_t)b * nch + ch) * 2) * dim;
-    o[c] = p0;
-    o[dim + c] = p1;
+    if (!counters) return;
+    __shared__ int s_last;
+    if (!arrive_last(&counters[blockIdx.z * gridDim.x + blockIdx.x], nch, &s_last)) return;
+    if (ok) {
+        float s0 = 0.f, s1 = 0.f;
+        for (int k = 0; k < nch; ++k) {
+            const float* o = part + (((int64_t)b * nch + k) * 2) * dim;
+            s0 += ld_coherent(o + c);
+            s1 += ld_coherent(o + dim + c);
+        }
+        dssg[((int64_t)b * 6 + part0) * dim + c] += s0;
+        if (mode == 0) dssg[((int64_t)b * 6 + part0 + 1) * dim + c] += s1;
+    }
 }
 
 // dssg[b][part0][c] += sum_ch part[b][ch][0][c]; (mode 0) dssg[b][part0+1][c] += sum part[..][1][c]
@@ -325,10 +365,13 @@ void launch(sa3k_ctx* ctx, const char* name, void (*kernel)(KArgs...), dim3 grid
 void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const float* x, const float* rstd,
             const float* gamma, int g_part, int part0) {
     const int chunk = (int)ceil_div(w->S, w->part_chunks);
+    const int64_t ctrs = nblk(w->dim) * (int64_t)w->B;
+    int* counters = ctx->gemm_fixup && ctrs <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
     launch(ctx, "blk_colred", colred_kernel, dim3(nblk(w->dim), (unsigned)w->part_chunks, (unsigned)w->B), mode, a, x,
-           rstd, gamma, (const float*)w->modv, g_part, w->S, w->dim, chunk, w->part);
-    launch(ctx, "blk_colred", colred_sum_kernel, dim3(nblk((int64_t)w->B * w->dim)), (const float*)w->part,
-           w->part_chunks, w->dim, w->B, part0, (int)(mode == 0), w->dssg);
+           rstd, gamma, (const float*)w->modv, g_part, w->S, w->dim, chunk, w->part, part0, w->dssg, counters);
+    if (!counters)
+        launch(ctx, "blk_colred", colred_sum_kernel, dim3(nblk((int64_t)w->B * w->dim)), (const float*)w->part,
+               w->part_chunks, w->dim, w->B, part0, (int)(mode == 0), w->dssg);
 }
 
 }  // namespace

@@ -37,6 +37,7 @@ struct DmaParams {
     float* ws;
     int kps;
     const void* zero;   // >= 16 zero bytes
+    int* counters;      // split-K arrival counters per tile (all zero between launches), or null
 };
 
 namespace {
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
         compute(t);
     }
 
-    if (p.ws) {  // split-K partial sums, reduced by gemm_dma_splitk_reduce
+    if (p.ws) {  // split-K partial sums
         float* w = p.ws + (int64_t)z * Mt * p.N;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -250,8 +251,21 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int64_t m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + v;
-                    if (m < Mt) w[m * p.N + n] = acc[i][j][v];
+                    if (m < Mt) st_coherent(w + m * p.N + n, acc[i][j][v]);
                 }
+        }
+        if (!p.counters) return;   // reduced by gemm_dma_splitk_reduce
+        // The last split of this tile to arrive sums the partials in split order (deterministic:
+        // independent of the arrival order) and runs the epilogue; nobody waits for anybody.
+        __shared__ int s_last;
+        if (!arrive_last(&p.counters[bid], (int)gridDim.y, &s_last)) return;
+        const int splits = (int)gridDim.y;
+        for (int e = tid; e < BM * BN; e += kThreads) {
+            const int64_t m = m0 + e / BN, n = n0 + e % BN;
+            if (m >= Mt || n >= p.N) continue;
+            float sum = 0.f;
+            for (int zz = 0; zz < splits; ++zz) sum += ld_coherent(p.ws + (int64_t)zz * Mt * p.N + m * p.N + n);
+            epilogue_elem(p, m, n, sum);
         }
         return;
     }
@@ -291,8 +305,11 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     p.kps = std::max(1, (KT + splits - 1) / splits);
     splits = std::max(1, (KT + p.kps - 1) / p.kps);
     p.ws = nullptr;
-    if (splits > 1)
+    p.counters = nullptr;
+    if (splits > 1) {
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
+        if (ctx->gemm_fixup && tiles <= kMaxFixupTiles) p.counters = ctx->tile_counters;
+    }
     dim3 g((unsigned)grid, (unsigned)splits);
     {
         // profiled per kernel instantiation, with its algorithmic flops (padding excluded)
@@ -302,7 +319,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         gemm_dma_kernel<BM, BN, WMW, STAGES, BF16><<<g, kThreads, 0, ctx->stream>>>(p);
         SA3K_LAUNCHED();
     }
-    if (splits > 1) {
+    if (splits > 1 && !p.counters) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
         gemm_dma_splitk_reduce<<<(unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
     }

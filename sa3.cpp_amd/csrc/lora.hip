@@ -328,7 +328,8 @@ template <int MODE, class QT>
 __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restrict__ Q, const bf16* __restrict__ P, int r,
                                                              const bf16* __restrict__ U, const float* __restrict__ d,
                                                              bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
-                                                             int64_t cols, int64_t rows_per) {
+                                                             int64_t cols, int64_t rows_per, float* __restrict__ out,
+                                                             int accumulate, int* __restrict__ counters) {
     __shared__ __attribute__((aligned(16))) bf16 qt[TN_COLS * TN_LD];
     __shared__ __attribute__((aligned(16))) bf16 pt[32 * TN_LD];
     __shared__ float red[TN_ROWS][TN_COLS + 1];
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int64_t c = c0 + wave * 16 + 4 * g + v;
-            if (c < cols) part[((int64_t)z * RS + row0 + a) * cols + c] = acc[t][v];
+            if (c < cols) st_coherent(part + ((int64_t)z * RS + row0 + a) * cols + c, acc[t][v]);
         }
     }
     if constexpr (MODE == TN_DY) {   // gd: sum the 32 token-row slots of each column
@@ -419,8 +420,24 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
         if (tid < TN_COLS) {
             float s = 0.f;
             for (int k = 0; k < TN_ROWS; ++k) s += red[k][tid];
-            if (c0 + tid < cols) part[((int64_t)z * RS) * cols + c0 + tid] = s;
+            if (c0 + tid < cols) st_coherent(part + ((int64_t)z * RS) * cols + c0 + tid, s);
         }
+    }
+    if (!counters) return;   // reduced by sum_splits_kernel
+    // The last split of this column tile to arrive sums the partials in split order
+    // (deterministic) into out[row][c] (= or +=); nobody waits for anybody.
+    __shared__ int s_last;
+    if (!arrive_last(&counters[blockIdx.x], (int)gridDim.y, &s_last)) return;
+    const int nrows = MODE == TN_DY ? r + 1 : r;
+    const int splits = (int)gridDim.y;
+    for (int e = tid; e < nrows * TN_COLS; e += kThreads) {
+        const int row = e / TN_COLS;
+        const int64_t c = c0 + (e % TN_COLS);
+        if (c >= cols) continue;
+        float s = 0.f;
+        for (int zz = 0; zz < splits; ++zz) s += ld_coherent(part + ((int64_t)zz * RS + row) * cols + c);
+        float* o = out + (int64_t)row * cols + c;
+        *o = accumulate ? *o + s : s;
     }
 }
 
@@ -632,18 +649,21 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         const int64_t rows_per = tn_rows_per(out, N);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
+        int* counters = ctx->gemm_fixup && ceil_div(out, TN_COLS) <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
         {
             KernelScope ks(ctx, "lin_bwd_colred_dy", 2.0 * N * out * r);
             skinny_tn_kernel<TN_DY, float><<<dim3((unsigned)ceil_div(out, TN_COLS), (unsigned)S), kThreads, 0,
                                                ctx->stream>>>(
                 dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
-                L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per);
+                L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per, L->red, 0, counters);
             SA3K_LAUNCHED();
         }
-        KernelScope ks(ctx, "lin_bwd_reduce");
-        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(r + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
-            part, (int64_t)33 * out, S, (int64_t)(r + 1) * out, L->red, 0);
-        SA3K_LAUNCHED();
+        if (!counters) {
+            KernelScope ks(ctx, "lin_bwd_reduce");
+            sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(r + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
+                part, (int64_t)33 * out, S, (int64_t)(r + 1) * out, L->red, 0);
+            SA3K_LAUNCHED();
+        }
     } else {
         const int S = choose_splits(out, N);
         const int64_t rows_per = ceil_div(N, S);
@@ -728,23 +748,26 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         const int64_t rows_per = tn_rows_per(in, N);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 32 * in * sizeof(float));
+        int* counters = ctx->gemm_fixup && ceil_div(in, TN_COLS) <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
         const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)S);
         {
             KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);
             if (x_src == SRC_F32)
                 skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
                     static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
-                    N, in, rows_per);
+                    N, in, rows_per, dA, 1, counters);
             else
                 skinny_tn_kernel<TN_X, bf16><<<grid, kThreads, 0, ctx->stream>>>(
                     static_cast<const bf16*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
-                    N, in, rows_per);
+                    N, in, rows_per, dA, 1, counters);
             SA3K_LAUNCHED();
         }
-        KernelScope ks(ctx, "lin_bwd_reduce");
-        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
-            part, (int64_t)32 * in, S, (int64_t)r * in, dA, 1);
-        SA3K_LAUNCHED();
+        if (!counters) {
+            KernelScope ks(ctx, "lin_bwd_reduce");
+            sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
+                part, (int64_t)32 * in, S, (int64_t)r * in, dA, 1);
+            SA3K_LAUNCHED();
+        }
     } else {
         const int S = choose_splits(in, N);
         const int64_t rows_per = ceil_div(N, S);

@@ -70,11 +70,14 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
         if (const char* e = std::getenv("SA3K_GEMM_SPLIT")) ctx->gemm_split = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_FIXUP")) ctx->gemm_fixup = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_GEMM_DMA")) ctx->gemm_dma = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
+        SA3K_HIP(hipMalloc(&ctx->tile_counters, sizeof(int) * kMaxFixupTiles));
+        SA3K_HIP(hipMemsetAsync(ctx->tile_counters, 0, sizeof(int) * kMaxFixupTiles, ctx->stream));
         SA3K_HIP(hipMalloc(&ctx->adamw_partials, sizeof(double) * kAdamwMaxBlocks));
         SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
         SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
@@ -97,6 +100,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->red_ws) (void)hipFree(ctx->red_ws);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
+    if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
     for (const ProfRecord& r : ctx->prof_pending) {
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);
@@ -168,6 +172,18 @@ SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
 
 SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
     return sa3k_guard(ctx, "sa3k_sync", [&] { SA3K_HIP(hipStreamSynchronize(ctx->stream)); });
+}
+
+SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
+    return sa3k_guard(ctx, "sa3k_set_option", [&] {
+        SA3K_REQUIRE(name != nullptr, "null option name");
+        const std::string n(name);
+        if (n == "gemm_split") ctx->gemm_split = value != 0;
+        else if (n == "gemm_fixup") ctx->gemm_fixup = value != 0;
+        else if (n == "gemm_dma") ctx->gemm_dma = value != 0;
+        else if (n == "gemm_cfg") ctx->gemm_cfg = value;
+        else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
+    });
 }
 
 SA3K_API int sa3k_timer_start(sa3k_ctx* ctx) {

@@ -48,6 +48,8 @@ struct sa3k_ctx {
     int gemm_wg_per_cu = 2;               // resident workgroups per CU assumed by the split choice
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
     size_t red_ws_bytes = 0;
+    int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch)
+    int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
 };
@@ -121,3 +123,34 @@ private:
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// capacity of sa3k_ctx::tile_counters (tiles of one split-K / split-reduction launch)
+constexpr int kMaxFixupTiles = 8192;
+
+// Split partial sums handed from one workgroup to another inside a launch ("the last split to
+// arrive reduces"): device-coherent (sc1) accesses, so no cache level can hold a stale copy and no
+// L2-wide write-back fence is needed. The writer waits for its coherent stores to complete before
+// the workgroup barrier that precedes its arrival on the tile counter. On MI355X these uncached
+// accesses cost more than the separate reduction launch they replace (a device-scope release
+// fence instead writes back a whole L2 per workgroup, costlier still), so the option is off by
+// default; it stays selectable and is tested bit-identical to the separate launch.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+// arrival of this workgroup on counter c of `expected` arrivals; true for the last one, which
+// also resets the counter. Every thread must call it (it contains workgroup barriers).
+__device__ __forceinline__ bool arrive_last(int* c, int expected, int* s_flag) {
+    wait_stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = prev == expected - 1;
+        if (*s_flag) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}

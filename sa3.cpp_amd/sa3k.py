@@ -82,6 +82,7 @@ def _declare(lib):
         "sa3k_copy_d2d": (I, [P, P, P, C.c_size_t]),
         "sa3k_memset": (I, [P, P, I, C.c_size_t]),
         "sa3k_sync": (I, [P]),
+        "sa3k_set_option": (I, [P, C.c_char_p, I]),
         "sa3k_timer_start": (I, [P]),
         "sa3k_timer_stop": (I, [P, C.POINTER(F)]),
         "sa3k_profile_enable": (I, [P, I]),
@@ -247,6 +248,9 @@ class Context:
 
     def sync(self):
         self.check(self.lib.sa3k_sync(self.h))
+
+    def set_option(self, name, value):
+        self.check(self.lib.sa3k_set_option(self.h, name.encode(), int(value)))
 
     def timer_start(self):
         self.check(self.lib.sa3k_timer_start(self.h))

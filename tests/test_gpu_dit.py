@@ -167,6 +167,25 @@ def test_dit_graph_replays_match_eager(ctx):
             d.destroy()
 
 
+def test_dit_in_kernel_reductions_match_separate_launches(ctx):
+    # every split reduction done by the last arriving workgroup (GEMM split-K, the column
+    # reductions, the modulation gradients) gives the separate-launch results bit for bit
+    cfg = dict(CFG, window=4)
+    tensors, adapters, inputs = db.random_dit(45, cfg, "full")
+    res = []
+    try:
+        for fixup in (0, 1):
+            ctx.set_option("gemm_fixup", fixup)
+            d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
+            up, _ = upload_inputs(ctx, inputs)
+            loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+            res.append((loss, d.arena(1).numpy()))
+            d.destroy()
+    finally:
+        ctx.set_option("gemm_fixup", 0)
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+
+
 def test_dit_full_size_step(ctx):
     # 24 blocks, dim 1536, 24 heads, FFN 6144, io 64, batch 2 x (64 + 1024), 128 context tokens of 768
     c = sa3k.dit_config(64, 1536, 24, 24, 768, 64, 256, 6144, window=256)

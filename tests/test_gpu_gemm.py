@@ -108,3 +108,24 @@ def test_gemm_rejects_bad_shapes(ctx):
     a = ctx.zeros((64, 100))
     with pytest.raises(sa3k.Sa3kError):
         ctx.gemm_nt(a, a, 64, 64, 100, C=ctx.zeros((64, 64)))   # K not a multiple of 64
+
+
+@pytest.mark.parametrize("M,N,K", [(2176, 1536, 1536), (2048, 32, 6144), (32, 1536, 6144), (2208, 1536, 6144)])
+def test_split_k_fixup_matches_separate_reduction(ctx, M, N, K):
+    # split-K partial sums reduced inside the kernel by the last split to arrive give exactly the
+    # separate reduction launch's result (same split order), for several launches in a row
+    r = rng(M + N + K)
+    A = bf16_bits(r.normal(0, 1, (M, K)).astype(np.float32))
+    B = bf16_bits(r.normal(0, 0.02, (N, K)).astype(np.float32))
+    bias = r.normal(0, 1, N).astype(np.float32)
+    out = {}
+    try:
+        for fixup in (0, 1, 0, 1):
+            ctx.set_option("gemm_fixup", fixup)
+            res = run(ctx, A, B, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, sa3k.TYPE_BF16, bias=bias)
+            if fixup in out:
+                assert np.array_equal(res, out[fixup]), "not deterministic"
+            out[fixup] = res
+    finally:
+        ctx.set_option("gemm_fixup", 0)
+    assert np.array_equal(out[0], out[1])
