@@ -137,6 +137,12 @@ SA3K_API int sa3k_adamw_clip(sa3k_ctx* ctx, float* param, const float* grad, flo
                              int64_t n, const sa3k_adamw_params* hp, int step, int count,
                              double* grad_norm_out);
 
+/* train_average_and_clip (src/train_loop.h:147-171) in place on a device arena of n gradients:
+ * g := g * (1/count) if count > 1, then g := g * (float)(clip/(norm+1e-6)) if clip > 0 and the
+ * double global norm exceeds clip. grad_norm_out (nullable, synchronises) gets the pre-clip norm. */
+SA3K_API int sa3k_average_and_clip(sa3k_ctx* ctx, float* grad, int64_t n, int count, float grad_clip,
+                                   double* grad_norm_out);
+
 /* The float clip scale and pre-clip norm the last sa3k_adamw_clip on this context used
  * (scale = 1 when no clipping happened). Synchronises the stream. */
 SA3K_API int sa3k_adamw_clip_scale(sa3k_ctx* ctx, double* norm_out, float* scale_out);
@@ -191,6 +197,10 @@ SA3K_API int sa3k_weight_drop_working_copy(sa3k_ctx* ctx, sa3k_weight* w);
  * over the decoded weight; outputs are device [out] f32. */
 SA3K_API int sa3k_weight_row_norm_sq(sa3k_ctx* ctx, const sa3k_weight* w, float eps, float* nsq);
 SA3K_API int sa3k_weight_row_norms(sa3k_ctx* ctx, const sa3k_weight* w, float* norms);
+/* The same two reductions over a dense device matrix W [out][in] of element type f32 / f16 / bf16
+ * with no shape constraint: mode 0 norms, mode 1 norm_sq (+ in*eps); result device f32 [out]. */
+SA3K_API int sa3k_row_norms(sa3k_ctx* ctx, int type, int64_t in, int64_t out, const void* W, int mode, float eps,
+                            float* result);
 
 /* ---------------------------------------------------------------- K1-K4: dit_lin (lora / dora-rows) */
 
@@ -354,6 +364,12 @@ SA3K_API int sa3k_dit_set_tensor(sa3k_ctx* ctx, sa3k_dit* dit, const char* name,
 /* Synthetic model on the device (counter-based Philox4x32-10 + Box-Muller): 2-D weights
  * N(0, w_sd), biases N(0, 0.02), ssg tables N(0, 0.1), gammas 1 + N(0, 0.1), memory tokens N(0, 1). */
 SA3K_API int sa3k_dit_init_random(sa3k_ctx* ctx, sa3k_dit* dit, uint64_t seed, float w_sd);
+/* Row norms of the named 2-D weight (decoded): mode 0 writes norms[o] = sqrt(sum_i W[o][i]^2)
+ * (train_row_norms, src/train_lora.h:141-155), mode 1 writes sum_i W[o][i]^2 + in*eps
+ * (train_row_norm_sq, :160-174); double accumulation, out device f32 [rows]. Valid before and
+ * after sa3k_dit_setup. */
+SA3K_API int sa3k_dit_weight_row_norms(sa3k_ctx* ctx, sa3k_dit* dit, const char* name, int mode, float eps,
+                                       float* out);
 /* Build the frozen weights (decoded bf16 working copies, base_norm_sq), the adapted linears, the
  * flat adapter arena and the activation workspaces for one micro-batch shape. */
 SA3K_API int sa3k_dit_setup(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_dit_train* train);

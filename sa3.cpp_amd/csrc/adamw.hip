@@ -148,6 +148,33 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
     }
 }
 
+// train_average_and_clip in place: g := g*inv (count > 1), then g := g*scale when clipping
+__global__ __launch_bounds__(kThreads) void average_clip_kernel(float* __restrict__ g, int64_t n, float inv, int avg,
+                                                                 float clip, const double* __restrict__ partials,
+                                                                 int n_partials, double* __restrict__ result) {
+    __shared__ double sh[kThreads / 64 + 1];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < n_partials; i += kThreads) acc += partials[i];
+    const double norm = sqrt(block_sum_double(acc, sh));
+    int do_clip = 0;
+    float scale = 1.0f;
+    if (clip > 0.0f && norm > (double)clip) {
+        scale = (float)((double)clip / (norm + 1e-6));
+        do_clip = 1;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        result[0] = norm;
+        result[1] = (double)scale;
+    }
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        float x = g[i];
+        if (avg) x = x * inv;
+        if (do_clip) x = x * scale;
+        g[i] = x;
+    }
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 }  // namespace
@@ -196,6 +223,38 @@ SA3K_API int sa3k_adamw_clip(sa3k_ctx* ctx, float* param, const float* grad, flo
             else
                 adamw_update_kernel<false><<<nb2, kThreads, 0, ctx->stream>>>(param, grad, m, v, n, s,
                                                                               ctx->adamw_partials, nb1, ctx->adamw_result);
+            SA3K_LAUNCHED();
+        }
+        if (grad_norm_out) {
+            double r[2];
+            SA3K_HIP(hipMemcpyAsync(r, ctx->adamw_result, sizeof r, hipMemcpyDeviceToHost, ctx->stream));
+            SA3K_HIP(hipStreamSynchronize(ctx->stream));
+            *grad_norm_out = r[0];
+        }
+    });
+}
+
+SA3K_API int sa3k_average_and_clip(sa3k_ctx* ctx, float* grad, int64_t n, int count, float grad_clip,
+                                   double* grad_norm_out) {
+    return sa3k_guard(ctx, "sa3k_average_and_clip", [&] {
+        SA3K_REQUIRE(count > 0, "cannot apply empty gradient batch");
+        SA3K_REQUIRE(n >= 0 && (n == 0 || grad), "bad arena");
+        const int avg = count > 1 ? 1 : 0;
+        const float inv = 1.0f / (float)count;
+        const bool vec = aligned16(grad);
+        const int64_t work = vec ? ceil_div(n, 4) : n;
+        const int nb1 = (int)std::max<int64_t>(1, std::min<int64_t>(kSumBlocks, ceil_div(work, kThreads)));
+        const int nb2 = (int)std::max<int64_t>(1, std::min<int64_t>(8192, ceil_div(n, kThreads * 2)));
+        {
+            KernelScope ks(ctx, "adamw_sumsq");
+            if (vec) adamw_sumsq_kernel<true><<<nb1, kThreads, 0, ctx->stream>>>(grad, n, inv, avg, ctx->adamw_partials);
+            else adamw_sumsq_kernel<false><<<nb1, kThreads, 0, ctx->stream>>>(grad, n, inv, avg, ctx->adamw_partials);
+            SA3K_LAUNCHED();
+        }
+        {
+            KernelScope ks(ctx, "average_clip");
+            average_clip_kernel<<<nb2, kThreads, 0, ctx->stream>>>(grad, n, inv, avg, grad_clip, ctx->adamw_partials, nb1,
+                                                                  ctx->adamw_result);
             SA3K_LAUNCHED();
         }
         if (grad_norm_out) {

@@ -773,6 +773,31 @@ SA3K_API int sa3k_dit_init_random(sa3k_ctx* ctx, sa3k_dit* dit, uint64_t seed, f
     });
 }
 
+SA3K_API int sa3k_dit_weight_row_norms(sa3k_ctx* ctx, sa3k_dit* dit, const char* name, int mode, float eps,
+                                       float* out) {
+    return sa3k_guard(ctx, "sa3k_dit_weight_row_norms", [&] {
+        SA3K_REQUIRE(dit && name && out && (mode == 0 || mode == 1), "bad arguments");
+        Tensor& t = tensor(dit, name);
+        SA3K_REQUIRE(t.kind == 0, "not a 2-D weight: " + t.name);
+        const sa3k_weight* w = nullptr;
+        if (dit->ready) {   // the built weight objects (the raw storage is released at setup)
+            for (int l = 0; l < dit->cfg.depth && !w; ++l)
+                for (int k = 0; k < 7; ++k)
+                    if (t.name == "dit." + std::to_string(l) + "." + kBlockTargets[k] + ".weight") w = dit->blocks[l]->W[k];
+            for (int h = 0; h < H_N && !w; ++h)
+                if (t.name == std::string("dit.") + kHeadNames[h] + ".weight") w = dit->hw[h];
+            SA3K_REQUIRE(w != nullptr, "weight not found: " + t.name);
+            chk(ctx, mode == 0 ? sa3k_weight_row_norms(ctx, w, out) : sa3k_weight_row_norm_sq(ctx, w, eps, out));
+            return;
+        }
+        sa3k_weight* tmp = nullptr;   // a temporary weight object over the raw tensor
+        chk(ctx, sa3k_weight_create(ctx, t.type, t.cols, t.rows, t.raw, 1, &tmp));
+        const int rc = mode == 0 ? sa3k_weight_row_norms(ctx, tmp, out) : sa3k_weight_row_norm_sq(ctx, tmp, eps, out);
+        chk(ctx, sa3k_weight_destroy(ctx, tmp));
+        chk(ctx, rc);
+    });
+}
+
 SA3K_API int sa3k_dit_setup(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_dit_train* train) {
     return sa3k_guard(ctx, "sa3k_dit_setup", [&] {
         SA3K_REQUIRE(dit && train, "null pointer");

@@ -1100,6 +1100,20 @@ SA3K_API int sa3k_weight_row_norm_sq(sa3k_ctx* ctx, const sa3k_weight* w, float 
     });
 }
 
+SA3K_API int sa3k_row_norms(sa3k_ctx* ctx, int type, int64_t in, int64_t out, const void* W, int mode, float eps,
+                            float* result) {
+    return sa3k_guard(ctx, "sa3k_row_norms", [&] {
+        SA3K_REQUIRE(W && result && in > 0 && out > 0 && (mode == 0 || mode == 1), "bad arguments");
+        SA3K_REQUIRE(type == SA3K_TYPE_F32 || type == SA3K_TYPE_F16 || type == SA3K_TYPE_BF16,
+                     "row norms of an element type (f32 / f16 / bf16)");
+        sa3k_weight w;   // a view: no copy, no working copies
+        w.type = type; w.in = in; w.out = out; w.w = const_cast<void*>(W);
+        KernelScope ks(ctx, "weight_row_norm");
+        row_norm_kernel<<<(unsigned)out, kThreads, 0, ctx->stream>>>(w, eps, mode == 0 ? 1 : 0, result);
+        SA3K_LAUNCHED();
+    });
+}
+
 SA3K_API int sa3k_weight_row_norms(sa3k_ctx* ctx, const sa3k_weight* w, float* norms) {
     return sa3k_guard(ctx, "sa3k_weight_row_norms", [&] {
         SA3K_REQUIRE(w && norms, "null pointer");

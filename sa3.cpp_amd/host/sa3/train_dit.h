@@ -1,0 +1,109 @@
+// train_dit.h - the DiT training graph of the reference's src/train_dit.h:30-218 (TrainDitGraph,
+// build_train_dit_forward_graph, free_train_dit_graph) over the device-resident DiT step: building
+// the "graph" sets the model up for one sample of `frames` latent frames and `ctx_len` context
+// tokens, lays the adapters out in the arena in the reference's target order, and allocates the
+// step inputs. The rectified-flow sample and the conditioning keep the reference's host structs
+// (src/train_diffusion.h:12-17, src/train_conditioning.h:16-22); their producers (sampler, text
+// encoder) are outside this build.
+#pragma once
+
+#include "train_lora.h"
+
+#include <string>
+#include <vector>
+
+namespace sa3 {
+
+struct TrainDiffusionSample {
+    float t = 0.0f;
+    std::vector<float> noise;
+    std::vector<float> x_t;              // [io, T] (ggml order: T rows of io)
+    std::vector<float> velocity_target;  // [io, T]
+};
+
+struct TrainConditioning {
+    std::vector<float> cross;   // [cond_dim, ctx_len] (ggml order)
+    std::vector<float> global;  // [cond_dim]
+    int cond_dim = 0;
+    int ctx_len = 0;
+    int token_count = 0;
+};
+
+struct TrainDitGraph {
+    struct Slot {   // one adapted target in the arena
+        int64_t off_a = 0, off_b = 0, off_m = -1, n_a = 0, n_b = 0, n_m = 0;
+    };
+    DitModel* model = nullptr;
+    int frames = 0, cond_dim = 0, ctx_len = 0;
+    float* params = nullptr;   // device adapter arena (owned by the model)
+    float* grads = nullptr;
+    int64_t n_params = 0;
+    std::vector<Slot> slots;   // aligned with TrainLoraState::params
+    DeviceF32 x, target, t, cross, global;
+};
+
+inline void free_train_dit_graph(TrainDitGraph& g) { g = TrainDitGraph{}; }
+
+// The model's adapters are those of `lora` (its targets must be a scope this build runs: every
+// block projection, with or without the 12 head/tail linears). A model is set up once.
+inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames,
+                                          int cond_dim, int ctx_len, TrainDitGraph& out, std::string& err,
+                                          bool inpaint = false) {
+    if (frames <= 0 || cond_dim <= 0 || ctx_len <= 0) {
+        err = "invalid DiT training graph dimensions";
+        return false;
+    }
+    if (inpaint) {
+        err = "inpainting training graphs are not implemented";
+        return false;
+    }
+    if (cond_dim != dc.cond_dim) {
+        err = "conditioning width differs from the model's cond_dim";
+        return false;
+    }
+    if (lora.adapter_type != "lora" && lora.adapter_type != "dora-rows") {
+        err = "adapter type " + lora.adapter_type + " is not implemented (lora, dora-rows)";
+        return false;
+    }
+    bool all_blocks = true;
+    for (const TrainLoraParam& p : lora.params) all_blocks = all_blocks && train_lora_is_block_weight(p.target.weight_name);
+    const int scope = all_blocks ? SA3K_SCOPE_CORE : SA3K_SCOPE_FULL;
+    sa3k_ctx* ctx = dit.ctx();
+    sa3k_dit_train tr{lora.rank, lora.alpha, lora.adapter_type == "dora-rows" ? 1 : 0, scope, 1, frames, ctx_len, 0};
+    if (sa3k_dit_setup(ctx, dit.handle(), &tr) != SA3K_OK) return sa3k_fail(ctx, err);
+    free_train_dit_graph(out);
+    out.model = &dit;
+    out.frames = frames;
+    out.cond_dim = cond_dim;
+    out.ctx_len = ctx_len;
+    int nt = 0;
+    if (sa3k_dit_target_count(ctx, dit.handle(), &nt) != SA3K_OK) return sa3k_fail(ctx, err);
+    if ((size_t)nt != lora.params.size()) {
+        err = "the adapter targets are not a scope this build runs (core or full)";
+        return false;
+    }
+    char name[256];
+    for (int i = 0; i < nt; ++i) {
+        int64_t in = 0, o = 0;
+        TrainDitGraph::Slot s;
+        if (sa3k_dit_target_info(ctx, dit.handle(), i, name, (int)sizeof name, &in, &o, &s.off_a, &s.off_b, &s.off_m) !=
+            SA3K_OK)
+            return sa3k_fail(ctx, err);
+        if (lora.params[i].target.weight_name != name) {
+            err = std::string("adapter target order differs from the model's: ") + name;
+            return false;
+        }
+        s.n_a = (int64_t)lora.rank * in;
+        s.n_b = o * lora.rank;
+        s.n_m = s.off_m >= 0 ? o : 0;
+        out.slots.push_back(s);
+    }
+    if (sa3k_dit_arena(ctx, dit.handle(), 0, &out.params, &out.n_params) != SA3K_OK ||
+        sa3k_dit_arena(ctx, dit.handle(), 1, &out.grads, nullptr) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    const size_t nx = (size_t)dc.io * frames;
+    return out.x.alloc(ctx, nx, err) && out.target.alloc(ctx, nx, err) && out.t.alloc(ctx, 1, err) &&
+           out.cross.alloc(ctx, (size_t)cond_dim * ctx_len, err) && out.global.alloc(ctx, (size_t)cond_dim, err);
+}
+
+}  // namespace sa3

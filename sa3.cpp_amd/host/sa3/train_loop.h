@@ -1,0 +1,224 @@
+// train_loop.h - the training-step helpers of the reference's src/train_loop.h:21-441 over the
+// GPU: loop/accumulator state, averaging + global clip, the accumulated AdamW update, and one
+// micro-batch of the DiT step (run_train_dit_accumulate). Names, fields, argument meaning and the
+// bool/err convention are the reference's; the arithmetic runs through the sa3k C ABI.
+//
+// Difference of signature: the reference's first argument of run_train_dit_accumulate is the ggml
+// backend; here the graph carries its device (sa3k) context, so that argument is gone.
+#pragma once
+
+#include "train_dit.h"
+#include "train_optimizer.h"
+
+#include <string>
+#include <vector>
+
+namespace sa3 {
+
+struct TrainLoopState {
+    int step = 0;
+    std::vector<TrainAdamWTensorState> A_state;
+    std::vector<TrainAdamWTensorState> B_state;
+    std::vector<TrainAdamWTensorState> mxs_state;
+    std::vector<TrainAdamWTensorState> mag_state;
+    std::vector<TrainAdamWTensorState> mag_r_state;
+    std::vector<TrainAdamWTensorState> mag_c_state;
+};
+
+struct TrainLoraGradAccum {
+    int count = 0;
+    std::vector<std::vector<float>> A;
+    std::vector<std::vector<float>> B;
+    std::vector<std::vector<float>> mxs;
+    std::vector<std::vector<float>> mag;
+    std::vector<std::vector<float>> mag_r;
+    std::vector<std::vector<float>> mag_c;
+};
+
+inline void train_accum_add(std::vector<float>& dst, const std::vector<float>& grad) {
+    if (dst.empty()) dst.assign(grad.size(), 0.0f);
+    for (size_t i = 0; i < grad.size(); ++i) dst[i] += grad[i];
+}
+
+inline void train_clear_accum(TrainLoraGradAccum& accum) { accum = TrainLoraGradAccum{}; }
+
+namespace detail {
+
+// every accumulated vector in the reference's visit order (A, B, mxs, mag, mag_r, mag_c per target)
+inline std::vector<std::vector<float>*> accum_vectors(TrainLoraGradAccum& a) {
+    std::vector<std::vector<float>*> v;
+    for (size_t i = 0; i < a.A.size(); ++i)
+        for (auto* g : {&a.A[i], &a.B[i], &a.mxs[i], &a.mag[i], &a.mag_r[i], &a.mag_c[i]}) v.push_back(g);
+    return v;
+}
+
+inline size_t total_size(const std::vector<std::vector<float>*>& v) {
+    size_t n = 0;
+    for (auto* x : v) n += x->size();
+    return n;
+}
+
+}  // namespace detail
+
+// train_average_and_clip (src/train_loop.h:147-171): mean over the window (count > 1), then scale
+// every vector so the global L2 norm is <= grad_clip; grad_norm_out gets the pre-clip norm.
+inline void train_average_and_clip(TrainLoraGradAccum& accum, const TrainAdamWParams& hp,
+                                   double* grad_norm_out = nullptr) {
+    auto vecs = detail::accum_vectors(accum);
+    const size_t n = detail::total_size(vecs);
+    std::string err;
+    sa3k_ctx* ctx = sa3k_default_ctx(err);
+    DeviceF32 g;
+    if (!ctx || !g.alloc(ctx, n, err)) throw std::runtime_error("train_average_and_clip: " + err);
+    size_t off = 0;
+    for (auto* x : vecs) {
+        if (!g.upload(x->data(), x->size(), off, err)) throw std::runtime_error("train_average_and_clip: " + err);
+        off += x->size();
+    }
+    double norm = 0.0;
+    if (sa3k_average_and_clip(ctx, g.get(), (int64_t)n, accum.count > 0 ? accum.count : 1, hp.grad_clip, &norm) !=
+        SA3K_OK)
+        throw std::runtime_error(std::string("train_average_and_clip: ") + sa3k_last_error(ctx));
+    if (grad_norm_out) *grad_norm_out = norm;
+    off = 0;
+    for (auto* x : vecs) {
+        if (!g.download(x->data(), x->size(), off, err)) throw std::runtime_error("train_average_and_clip: " + err);
+        off += x->size();
+    }
+}
+
+// train_apply_accumulated_adamw (src/train_loop.h:173-211): loop.step += 1, mean + global clip,
+// AdamW on every trained vector, accumulator cleared. One fused pass over all vectors on the GPU
+// (sa3k_adamw_clip), bit-identical to the reference's per-vector host loops.
+inline bool train_apply_accumulated_adamw(TrainLoraState& state, TrainLoraGradAccum& accum, TrainLoopState& loop,
+                                          const TrainAdamWParams& hp, std::string& err,
+                                          double* grad_norm_out = nullptr) {
+    if (accum.count <= 0) {
+        err = "cannot apply empty gradient batch";
+        return false;
+    }
+    loop.step += 1;
+    const size_t np = state.params.size();
+    for (auto* s : {&loop.A_state, &loop.B_state, &loop.mxs_state, &loop.mag_state, &loop.mag_r_state,
+                    &loop.mag_c_state})
+        s->resize(np);
+    for (auto* a : {&accum.A, &accum.B, &accum.mxs, &accum.mag, &accum.mag_r, &accum.mag_c}) a->resize(np);
+    // the trained vectors, their gradients and moments, in visit order
+    struct Slot { std::vector<float>* p; std::vector<float>* g; TrainAdamWTensorState* st; };
+    std::vector<Slot> slots;
+    for (size_t i = 0; i < np; ++i) {
+        TrainLoraParam& q = state.params[i];
+        const Slot s[6] = {{&q.lora_A, &accum.A[i], &loop.A_state[i]},      {&q.lora_B, &accum.B[i], &loop.B_state[i]},
+                           {&q.M_xs, &accum.mxs[i], &loop.mxs_state[i]},     {&q.magnitude, &accum.mag[i], &loop.mag_state[i]},
+                           {&q.magnitude_r, &accum.mag_r[i], &loop.mag_r_state[i]},
+                           {&q.magnitude_c, &accum.mag_c[i], &loop.mag_c_state[i]}};
+        for (const Slot& x : s) {
+            if (x.p->empty()) continue;
+            if (x.g->size() != x.p->size()) {
+                err = "AdamW parameter/gradient size mismatch";
+                return false;
+            }
+            if (x.st->m.size() != x.p->size()) x.st->m.assign(x.p->size(), 0.0f);
+            if (x.st->v.size() != x.p->size()) x.st->v.assign(x.p->size(), 0.0f);
+            slots.push_back(x);
+        }
+    }
+    size_t n = 0;
+    for (const Slot& x : slots) n += x.p->size();
+    sa3k_ctx* ctx = sa3k_default_ctx(err);
+    if (!ctx) return false;
+    DeviceF32 buf;   // [p | g | m | v], each n long
+    if (!buf.alloc(ctx, 4 * n, err)) return false;
+    size_t off = 0;
+    for (const Slot& x : slots) {
+        const size_t k = x.p->size();
+        if (!buf.upload(x.p->data(), k, off, err) || !buf.upload(x.g->data(), k, n + off, err) ||
+            !buf.upload(x.st->m.data(), k, 2 * n + off, err) || !buf.upload(x.st->v.data(), k, 3 * n + off, err))
+            return false;
+        off += k;
+    }
+    sa3k_adamw_params p{hp.learning_rate, hp.beta1, hp.beta2, hp.eps, hp.weight_decay, hp.grad_clip};
+    float* b = buf.get();
+    double norm = 0.0;
+    if (sa3k_adamw_clip(ctx, b, b + n, b + 2 * n, b + 3 * n, (int64_t)n, &p, loop.step, accum.count, &norm) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    if (grad_norm_out) *grad_norm_out = norm;
+    off = 0;
+    for (const Slot& x : slots) {
+        const size_t k = x.p->size();
+        if (!buf.download(x.p->data(), k, off, err) || !buf.download(x.st->m.data(), k, 2 * n + off, err) ||
+            !buf.download(x.st->v.data(), k, 3 * n + off, err))
+            return false;
+        off += k;
+    }
+    train_clear_accum(accum);
+    return true;
+}
+
+// upload_train_lora_state (src/train_loop.h:42-60): the host adapters into the graph's arena
+inline bool upload_train_lora_state(const TrainLoraState& state, TrainDitGraph& graph, std::string& err) {
+    sa3k_ctx* ctx = graph.model->ctx();
+    for (size_t i = 0; i < state.params.size(); ++i) {
+        const TrainLoraParam& q = state.params[i];
+        const TrainDitGraph::Slot& s = graph.slots[i];
+        if (q.lora_A.size() != (size_t)s.n_a || q.lora_B.size() != (size_t)s.n_b ||
+            (s.off_m >= 0 && q.magnitude.size() != (size_t)s.n_m)) {
+            err = "adapter state does not match the training graph: " + q.target.weight_name;
+            return false;
+        }
+        if (sa3k_upload(ctx, graph.params + s.off_a, q.lora_A.data(), q.lora_A.size() * 4) != SA3K_OK ||
+            sa3k_upload(ctx, graph.params + s.off_b, q.lora_B.data(), q.lora_B.size() * 4) != SA3K_OK ||
+            (s.off_m >= 0 &&
+             sa3k_upload(ctx, graph.params + s.off_m, q.magnitude.data(), q.magnitude.size() * 4) != SA3K_OK))
+            return sa3k_fail(ctx, err);
+    }
+    if (sa3k_dit_adapters_changed(ctx, graph.model->handle()) != SA3K_OK) return sa3k_fail(ctx, err);
+    return true;
+}
+
+// run_train_dit_accumulate (src/train_loop.h:212-256): one sample through the DiT, velocity MSE,
+// and the adapter gradients added into accum (count += 1). The inpaint variant is not implemented.
+inline bool run_train_dit_accumulate(TrainDitGraph& graph, const TrainLoraState& lora, TrainLoraGradAccum& accum,
+                                     const TrainDiffusionSample& sample, const TrainConditioning& cond,
+                                     const DitConfig& dc, float& loss_out, std::string& err) {
+    if (sample.x_t.empty() || sample.velocity_target.empty() || cond.cross.empty() || cond.global.empty()) {
+        err = "training step inputs are empty";
+        return false;
+    }
+    const size_t nx = (size_t)dc.io * graph.frames;
+    if (sample.x_t.size() != nx || sample.velocity_target.size() != nx ||
+        cond.cross.size() < (size_t)graph.cond_dim * graph.ctx_len || cond.global.size() != (size_t)graph.cond_dim) {
+        err = "training step inputs do not match the graph's dimensions";
+        return false;
+    }
+    if (!upload_train_lora_state(lora, graph, err)) return false;
+    sa3k_ctx* ctx = graph.model->ctx();
+    if (!graph.x.upload(sample.x_t.data(), nx, 0, err) || !graph.target.upload(sample.velocity_target.data(), nx, 0, err) ||
+        !graph.t.upload(&sample.t, 1, 0, err) ||
+        !graph.cross.upload(cond.cross.data(), (size_t)graph.cond_dim * graph.ctx_len, 0, err) ||
+        !graph.global.upload(cond.global.data(), (size_t)graph.cond_dim, 0, err))
+        return false;
+    // this call's gradients alone, then added into the host accumulator like the reference reads
+    // them back from its graph (train_accumulate_adamw_gradients)
+    if (sa3k_memset(ctx, graph.grads, 0, (size_t)graph.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
+    double loss = 0.0;
+    if (sa3k_dit_accumulate(ctx, graph.model->handle(), graph.x.get(), graph.target.get(), graph.t.get(),
+                            graph.cross.get(), graph.global.get(), nullptr, &loss) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    loss_out = (float)loss;
+    std::vector<float> g((size_t)graph.n_params);
+    if (sa3k_download(ctx, g.data(), graph.grads, g.size() * 4) != SA3K_OK) return sa3k_fail(ctx, err);
+    const size_t np = lora.params.size();
+    for (auto* a : {&accum.A, &accum.B, &accum.mxs, &accum.mag, &accum.mag_r, &accum.mag_c}) a->resize(np);
+    for (size_t i = 0; i < np; ++i) {
+        const TrainDitGraph::Slot& s = graph.slots[i];
+        train_accum_add(accum.A[i], std::vector<float>(g.begin() + s.off_a, g.begin() + s.off_a + s.n_a));
+        train_accum_add(accum.B[i], std::vector<float>(g.begin() + s.off_b, g.begin() + s.off_b + s.n_b));
+        if (s.off_m >= 0)
+            train_accum_add(accum.mag[i], std::vector<float>(g.begin() + s.off_m, g.begin() + s.off_m + s.n_m));
+    }
+    accum.count += 1;
+    return true;
+}
+
+}  // namespace sa3

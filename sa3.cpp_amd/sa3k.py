@@ -90,6 +90,7 @@ def _declare(lib):
         "sa3k_profile_report": (I, [P, C.c_char_p, I]),
         "sa3k_adamw_clip": (I, [P, P, P, P, P, I64, C.POINTER(AdamWParams), I, I, C.POINTER(D)]),
         "sa3k_adamw_clip_scale": (I, [P, C.POINTER(D), C.POINTER(F)]),
+        "sa3k_average_and_clip": (I, [P, P, I64, I, F, C.POINTER(D)]),
         "sa3k_q8_0_dequant": (I, [P, P, P, I64]),
         "sa3k_q8_0_quantize": (I, [P, P, P, I64]),
         "sa3k_gemm_nt": (I, [P, I, I, P, I64, I, P, I64, P, I64, I64, I64, I64, F, P, P, P, I64, I]),
@@ -98,6 +99,7 @@ def _declare(lib):
         "sa3k_weight_drop_working_copy": (I, [P, P]),
         "sa3k_weight_row_norm_sq": (I, [P, P, F, P]),
         "sa3k_weight_row_norms": (I, [P, P, P]),
+        "sa3k_row_norms": (I, [P, I, I64, I64, P, I, F, P]),
         "sa3k_lin_create": (I, [P, P, I, I, I64, C.POINTER(P)]),
         "sa3k_lin_destroy": (I, [P, P]),
         "sa3k_lin_prepare": (I, [P, P, P, P, F, I, P, P]),
@@ -120,6 +122,7 @@ def _declare(lib):
         "sa3k_dit_set_tensor": (I, [P, P, C.c_char_p, P, I64]),
         "sa3k_dit_init_random": (I, [P, P, C.c_uint64, F]),
         "sa3k_dit_setup": (I, [P, P, C.POINTER(DitTrain)]),
+        "sa3k_dit_weight_row_norms": (I, [P, P, C.c_char_p, I, F, P]),
         "sa3k_dit_arena": (I, [P, P, I, C.POINTER(P), C.POINTER(I64)]),
         "sa3k_dit_target_count": (I, [P, P, C.POINTER(I)]),
         "sa3k_dit_target_info": (I, [P, P, I, C.c_char_p, I, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64),

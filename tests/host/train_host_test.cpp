@@ -1,0 +1,312 @@
+// Host-interface test of the trainer mirror (sa3.cpp_amd/host/sa3/*.h), in the style of the
+// reference's tests/train_optimizer_test.cpp and tests/train_lora_test.cpp. Mode "cpu" checks the
+// host-only parts (InverseLR schedule, target scopes); mode "gpu" also runs the device-backed
+// parts: AdamW, row norms, adapter init, the DiT training graph and the accumulated update, and
+// checks the mirror's packing against the C ABI's own arena path.
+#include "sa3/train_loop.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+static int fails = 0;
+static void expect(bool ok, const char* msg) {
+    if (!ok) {
+        std::fprintf(stderr, "FAIL: %s\n", msg);
+        fails++;
+    }
+}
+
+static void test_cpu() {
+    // InverseLR at base_lr 1e-4, inv_gamma 1e6, power 0.5, warmup 0.995, final_lr 0
+    // (tests/train_optimizer_test.cpp:32-44 of the reference)
+    struct { int n; float lr; } ref[] = {
+        {0, 5.0000000000e-07f},   {1, 9.9749950125e-07f},   {10, 5.3645151961e-06f},  {100, 3.9723855426e-05f},
+        {500, 9.1860637497e-05f}, {1000, 9.9288298382e-05f}, {2499, 9.9874922989e-05f},
+    };
+    for (auto& r : ref) {
+        const float got = sa3::inverse_lr(1.0e-4f, r.n, 1.0e6f, 0.5f, 0.995f, 0.0f);
+        expect(std::fabs(got - r.lr) / r.lr < 1.0e-5f, "inverse_lr matches the published values");
+    }
+    expect(std::fabs(sa3::inverse_lr(1.0e-4f, 0, 1.0e6f, 0.5f, 0.0f, 0.0f) - 1.0e-4f) < 1.0e-10f,
+           "inverse_lr without warmup: step 0 == base_lr");
+    // final_lr is a floor
+    expect(sa3::inverse_lr(1.0e-4f, 1000000, 1.0f, 1.0f, 0.0f, 3.0e-5f) == 3.0e-5f, "inverse_lr floor");
+
+    // scopes over names (tests/train_lora_test.cpp:35-61)
+    const char* names[] = {"dit.0.self.qkv.weight", "dit.0.cross.kv.weight", "dit.0.local.0.weight",
+                           "dit.proj_in.weight"};
+    auto count = [&](const sa3::TrainLoraScope& s) {
+        int n = 0;
+        for (const char* x : names) n += sa3::train_lora_target_selected(x, s) ? 1 : 0;
+        return n;
+    };
+    sa3::TrainLoraScope full, core, only_cross, no_self, core_no_cross;
+    core.name = "core";
+    only_cross.include = {"cross."};
+    no_self.exclude = {"self."};
+    core_no_cross.name = "core";
+    core_no_cross.exclude = {"cross."};
+    expect(count(full) == 4, "full scope keeps all");
+    expect(count(core) == 2, "core drops local + non-block");
+    expect(count(only_cross) == 1, "include filters");
+    expect(count(no_self) == 3, "exclude filters");
+    expect(count(core_no_cross) == 1, "scope then exclude");
+    expect(sa3::train_lora_is_block_weight("dit.11.ff.out.weight"), "block weight detected");
+    expect(!sa3::train_lora_is_block_weight("dit.proj_in.weight"), "non-block detected");
+    expect(!sa3::train_lora_is_block_weight("dit.time_embed.0.weight"), "embed is not a block");
+    expect(sa3::train_lora_scope_known("core") && !sa3::train_lora_scope_known("attn"), "scope names");
+}
+
+// AdamW on the host in float, term by term (the reference's loop, src/train_optimizer.h:55-64)
+static void host_adamw(std::vector<float>& p, const std::vector<float>& g, std::vector<float>& m,
+                       std::vector<float>& v, const sa3::TrainAdamWParams& hp, int step) {
+    const float b1c = 1.0f - std::pow(hp.beta1, (float)step);
+    const float b2c = 1.0f - std::pow(hp.beta2, (float)step);
+    for (size_t i = 0; i < p.size(); ++i) {
+        m[i] = hp.beta1 * m[i] + (1.0f - hp.beta1) * g[i];
+        v[i] = hp.beta2 * v[i] + (1.0f - hp.beta2) * g[i] * g[i];
+        const float mh = m[i] / b1c, vh = v[i] / b2c;
+        p[i] -= hp.learning_rate * (mh / (std::sqrt(vh) + hp.eps) + hp.weight_decay * p[i]);
+    }
+}
+
+static double max_rel(const std::vector<float>& a, const std::vector<float>& b) {
+    double d = 0, s = 0;
+    for (size_t i = 0; i < a.size(); ++i) {
+        d = std::max(d, std::fabs((double)a[i] - b[i]));
+        s = std::max(s, std::fabs((double)b[i]));
+    }
+    return s > 0 ? d / s : d;
+}
+
+static void test_gpu() {
+    std::string err;
+    // ---- AdamW (tests/train_optimizer_test.cpp:17-30) + the float update term by term
+    {
+        std::vector<float> p = {1.0f, -1.0f}, g = {0.5f, -0.25f};
+        sa3::TrainAdamWTensorState st;
+        sa3::TrainAdamWParams hp;
+        hp.learning_rate = 0.1f;
+        hp.weight_decay = 0.01f;
+        expect(sa3::adamw_update_vector(p, g, st, hp, 1, err), "adamw update");
+        expect(p[0] < 1.0f, "positive grad decreases param");
+        expect(p[1] > -1.0f, "negative grad increases param");
+        expect(st.m.size() == 2 && st.v.size() == 2, "state initialized");
+        std::vector<float> bad = {1.0f};
+        expect(!sa3::adamw_update_vector(p, bad, st, hp, 2, err), "size mismatch rejected");
+        expect(!sa3::adamw_update_vector(p, g, st, hp, 0, err), "step 0 rejected");
+
+        std::mt19937 rng(5);
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        std::vector<float> q(1000), gq(1000), hq, hm(1000, 0.0f), hv(1000, 0.0f);
+        for (float& x : q) x = nd(rng);
+        hq = q;
+        sa3::TrainAdamWTensorState sq;
+        for (int step = 1; step <= 3; ++step) {
+            for (float& x : gq) x = nd(rng);
+            expect(sa3::adamw_update_vector(q, gq, sq, hp, step, err), "adamw continuation");
+            host_adamw(hq, gq, hm, hv, hp, step);
+        }
+        expect(max_rel(q, hq) < 1e-6 && max_rel(sq.m, hm) < 1e-6 && max_rel(sq.v, hv) < 1e-6,
+               "adamw continuation matches the float update");
+    }
+    // ---- row norms of W = 1..32 as [8 rows][4] (tests/train_lora_test.cpp:19-24, :73)
+    {
+        std::vector<float> w(32);
+        for (int i = 0; i < 32; ++i) w[i] = (float)(i + 1);
+        std::vector<float> n = sa3::train_row_norms(w, 4, 8), nsq = sa3::train_row_norm_sq(w, 4, 8, 1e-3f);
+        expect(n[0] > 5.47f && n[0] < 5.48f, "dora row norm");
+        bool ok = true;
+        for (int r = 0; r < 8; ++r) {
+            double s = 0;
+            for (int c = 0; c < 4; ++c) s += (double)w[r * 4 + c] * w[r * 4 + c];
+            ok = ok && std::fabs(n[r] - std::sqrt(s)) <= 1e-6 * std::sqrt(s);
+            ok = ok && std::fabs(nsq[r] - (s + 4 * 1e-3)) <= 1e-6 * s;
+        }
+        expect(ok, "row norms and norm_sq match the closed form");
+        expect(sa3::train_row_norms(std::vector<float>(), 4, 8) == std::vector<float>(8, 1.0f), "missing tensor: ones");
+    }
+    // ---- a depth-2 DiT: targets, adapter init, training graph, accumulate, AdamW
+    sa3::DitConfig dc;
+    dc.io = 64; dc.dim = 128; dc.depth = 2; dc.heads = 2; dc.head_dim = 64; dc.cond_dim = 64; dc.mem_tokens = 4;
+    dc.time_dim = 64; dc.inner = 128; dc.window = 0;
+    sa3::DitModel dit;
+    if (!dit.create(dc, SA3K_TYPE_F32, err)) {
+        expect(false, ("dit create: " + err).c_str());
+        return;
+    }
+    expect(dit.init_random(11, 0.05f, err), "dit init");
+    // a weight with known rows: W[o][i] = (o*in + i + 1) / 1000
+    {
+        const std::string name = "dit.1.cross.q.weight";
+        const int64_t in = dit.ne0(name), out = dit.ne1(name);
+        std::vector<float> w((size_t)(in * out));
+        for (size_t i = 0; i < w.size(); ++i) w[i] = (float)(i + 1) / 1000.0f;
+        expect(dit.set_tensor(name, w.data(), w.size() * 4, err), "set tensor");
+        std::vector<float> n = sa3::train_row_norms(dit, name), ref = sa3::train_row_norms(w, in, out);
+        expect(max_rel(n, ref) < 1e-6, "model row norms == host-vector row norms");
+    }
+    sa3::TrainLoraScope full, core, cross;
+    core.name = "core";
+    cross.include = {"cross."};
+    std::vector<sa3::TrainLoraTarget> targets = sa3::enumerate_train_lora_targets(dit, full);
+    expect(targets.size() == 2 * 7 + 12, "full scope: 7 per block + 12 head/tail");
+    expect(sa3::enumerate_train_lora_targets(dit, core).size() == 14, "core scope: 7 per block");
+    expect(sa3::enumerate_train_lora_targets(dit, cross).size() == 6, "include cross.: q, kv, out per block");
+    bool sorted = true;
+    for (size_t i = 1; i < targets.size(); ++i) sorted = sorted && targets[i - 1].weight_name < targets[i].weight_name;
+    expect(sorted, "targets sorted by weight name");
+    expect(targets[0].stem + ".weight" == targets[0].weight_name, "target stem");
+
+    sa3::TrainLoraState st;
+    expect(!sa3::init_train_lora_state(dit, targets, "lora", 129, 8.0f, 7, st, err), "infeasible rank rejected");
+    expect(!sa3::init_train_lora_state(dit, targets, "bora", 8, 8.0f, 7, st, err), "unimplemented family rejected");
+    expect(sa3::init_train_lora_state(dit, targets, "dora-rows", 8, 16.0f, 7, st, err), "init dora rows");
+    sa3::TrainLoraState st2;
+    expect(sa3::init_train_lora_state(dit, targets, "dora-rows", 8, 16.0f, 7, st2, err) &&
+               st2.params[3].lora_A == st.params[3].lora_A,
+           "same seed, same A");
+    bool shapes = st.params.size() == targets.size();
+    for (size_t i = 0; shapes && i < targets.size(); ++i) {
+        const sa3::TrainLoraParam& p = st.params[i];
+        const float bound = 1.0f / std::sqrt((float)targets[i].in);
+        shapes = p.lora_A.size() == (size_t)(8 * targets[i].in) && p.lora_B.size() == (size_t)(8 * targets[i].out) &&
+                 p.magnitude.size() == (size_t)targets[i].out;
+        for (float a : p.lora_A) shapes = shapes && std::fabs(a) <= bound;
+        for (float b : p.lora_B) shapes = shapes && b == 0.0f;
+    }
+    expect(shapes, "adapter shapes, Kaiming bound, B = 0");
+
+    sa3::TrainDitGraph graph;
+    const int frames = 12, ctx_len = 5;
+    if (!sa3::build_train_dit_forward_graph(dit, dc, st, frames, dc.cond_dim, ctx_len, graph, err)) {
+        expect(false, ("build graph: " + err).c_str());
+        return;
+    }
+    // B ~ small noise so every gradient term is live
+    std::mt19937 rng(3);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    for (sa3::TrainLoraParam& p : st.params)
+        for (float& b : p.lora_B) b = 0.01f * nd(rng);
+    sa3::TrainDiffusionSample s;
+    sa3::TrainConditioning c;
+    s.t = 0.4f;
+    s.x_t.resize((size_t)dc.io * frames);
+    s.velocity_target.resize(s.x_t.size());
+    for (float& x : s.x_t) x = nd(rng);
+    for (float& x : s.velocity_target) x = nd(rng);
+    c.cond_dim = dc.cond_dim;
+    c.ctx_len = ctx_len;
+    c.cross.resize((size_t)dc.cond_dim * ctx_len);
+    c.global.resize((size_t)dc.cond_dim);
+    for (float& x : c.cross) x = nd(rng);
+    for (float& x : c.global) x = nd(rng);
+
+    sa3::TrainLoraGradAccum accum;
+    sa3::TrainLoopState loop;
+    sa3::TrainAdamWParams hp;
+    hp.learning_rate = 1e-3f;
+    hp.weight_decay = 0.01f;
+    hp.grad_clip = 1.0f;
+    expect(!sa3::train_apply_accumulated_adamw(st, accum, loop, hp, err) && err == "cannot apply empty gradient batch",
+           "empty batch rejected");
+    sa3::TrainDiffusionSample bad = s;
+    bad.x_t.pop_back();
+    float loss0 = 0.0f, loss1 = 0.0f;
+    expect(!sa3::run_train_dit_accumulate(graph, st, accum, bad, c, dc, loss0, err), "input size mismatch rejected");
+    expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss0, err), "accumulate 1");
+    const sa3::TrainLoraGradAccum once = accum;
+    expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss1, err), "accumulate 2");
+    expect(std::isfinite(loss0) && loss0 > 0.0f && loss0 == loss1, "loss finite and deterministic");
+    expect(accum.count == 2, "two samples counted");
+    bool twice = true, live = false;
+    for (size_t i = 0; i < accum.A.size(); ++i) {
+        for (size_t k = 0; k < accum.A[i].size(); ++k) twice = twice && accum.A[i][k] == 2.0f * once.A[i][k];
+        for (size_t k = 0; k < accum.B[i].size(); ++k) twice = twice && accum.B[i][k] == 2.0f * once.B[i][k];
+        for (size_t k = 0; k < accum.mag[i].size(); ++k) twice = twice && accum.mag[i][k] == 2.0f * once.mag[i][k];
+        for (float g : once.A[i]) live = live || g != 0.0f;
+    }
+    expect(twice, "two identical samples accumulate exactly twice the gradients");
+    expect(live, "A gradients are live");
+
+    // the C ABI's arena path on the same state: gradients of two accumulate calls, then one
+    // sa3k_adamw_clip over the whole arena with count 2 == the mirror's packed update
+    sa3k_ctx* ctx = dit.ctx();
+    float *mom = nullptr, *var = nullptr;
+    sa3k_dit_arena(ctx, dit.handle(), 2, &mom, nullptr);
+    sa3k_dit_arena(ctx, dit.handle(), 3, &var, nullptr);
+    const size_t n = (size_t)graph.n_params;
+    expect(sa3::upload_train_lora_state(st, graph, err), "upload state");
+    sa3k_memset(ctx, graph.grads, 0, n * 4);
+    sa3k_memset(ctx, mom, 0, n * 4);
+    sa3k_memset(ctx, var, 0, n * 4);
+    double l2[1];
+    expect(sa3k_dit_accumulate(ctx, dit.handle(), graph.x.get(), graph.target.get(), graph.t.get(), graph.cross.get(),
+                               graph.global.get(), nullptr, l2) == SA3K_OK &&
+               sa3k_dit_accumulate(ctx, dit.handle(), graph.x.get(), graph.target.get(), graph.t.get(),
+                                   graph.cross.get(), graph.global.get(), nullptr, l2) == SA3K_OK,
+           "arena accumulate");
+    std::vector<float> ga(n);
+    sa3k_download(ctx, ga.data(), graph.grads, n * 4);
+    bool same_grads = true;
+    for (size_t i = 0; i < graph.slots.size(); ++i) {
+        const sa3::TrainDitGraph::Slot& sl = graph.slots[i];
+        same_grads = same_grads && std::memcmp(&ga[sl.off_a], accum.A[i].data(), sl.n_a * 4) == 0 &&
+                     std::memcmp(&ga[sl.off_b], accum.B[i].data(), sl.n_b * 4) == 0 &&
+                     std::memcmp(&ga[sl.off_m], accum.mag[i].data(), sl.n_m * 4) == 0;
+    }
+    expect(same_grads, "mirror accumulator == arena gradients, bitwise");
+    sa3k_adamw_params p{hp.learning_rate, hp.beta1, hp.beta2, hp.eps, hp.weight_decay, hp.grad_clip};
+    double norm_abi = 0.0, norm_mirror = 0.0;
+    expect(sa3k_adamw_clip(ctx, graph.params, graph.grads, mom, var, (int64_t)n, &p, 1, 2, &norm_abi) == SA3K_OK,
+           "arena adamw");
+    expect(sa3::train_apply_accumulated_adamw(st, accum, loop, hp, err, &norm_mirror), "mirror adamw");
+    expect(loop.step == 1 && accum.count == 0 && accum.A.empty(), "step counted, accumulator cleared");
+    expect(std::fabs(norm_abi - norm_mirror) <= 1e-9 * norm_abi, "same pre-clip norm");
+    std::vector<float> pa(n), ma(n);
+    sa3k_download(ctx, pa.data(), graph.params, n * 4);
+    sa3k_download(ctx, ma.data(), mom, n * 4);
+    double worst = 0.0;
+    for (size_t i = 0; i < graph.slots.size(); ++i) {
+        const sa3::TrainDitGraph::Slot& sl = graph.slots[i];
+        worst = std::max(worst, max_rel(std::vector<float>(pa.begin() + sl.off_a, pa.begin() + sl.off_a + sl.n_a),
+                                        st.params[i].lora_A));
+        worst = std::max(worst, max_rel(std::vector<float>(pa.begin() + sl.off_b, pa.begin() + sl.off_b + sl.n_b),
+                                        st.params[i].lora_B));
+        worst = std::max(worst, max_rel(std::vector<float>(pa.begin() + sl.off_m, pa.begin() + sl.off_m + sl.n_m),
+                                        st.params[i].magnitude));
+        worst = std::max(worst, max_rel(std::vector<float>(ma.begin() + sl.off_b, ma.begin() + sl.off_b + sl.n_b),
+                                        loop.B_state[i].m));
+    }
+    expect(worst < 1e-6, "mirror AdamW == arena AdamW");
+
+    // a few updates on the fixed sample lower the loss
+    float first = 0.0f, last = 0.0f;
+    for (int it = 0; it < 6; ++it) {
+        float l = 0.0f;
+        expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, l, err), "train accumulate");
+        expect(sa3::train_apply_accumulated_adamw(st, accum, loop, hp, err), "train adamw");
+        if (it == 0) first = l;
+        last = l;
+    }
+    expect(loop.step == 7, "seven optimizer steps");
+    expect(last < first, "loss falls over updates");
+    std::printf("loss %.6f -> %.6f over %d steps\n", first, last, loop.step - 1);
+    sa3::free_train_dit_graph(graph);
+}
+
+int main(int argc, char** argv) {
+    const bool gpu = argc > 1 && std::strcmp(argv[1], "gpu") == 0;
+    test_cpu();
+    if (gpu) test_gpu();
+    if (fails) {
+        std::fprintf(stderr, "train_host_test: %d failure(s)\n", fails);
+        return 1;
+    }
+    std::printf("train_host_test (%s): ok\n", gpu ? "gpu" : "cpu");
+    return 0;
+}
