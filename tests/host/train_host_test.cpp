@@ -252,14 +252,19 @@ static void test_gpu() {
            "arena accumulate");
     std::vector<float> ga(n);
     sa3k_download(ctx, ga.data(), graph.grads, n * 4);
-    bool same_grads = true;
+    // the mirror adds per-sample gradients on the host (as the reference reads them back); the
+    // arena accumulates in place term by term, so the two sums agree to rounding
+    double gworst = 0.0;
     for (size_t i = 0; i < graph.slots.size(); ++i) {
         const sa3::TrainDitGraph::Slot& sl = graph.slots[i];
-        same_grads = same_grads && std::memcmp(&ga[sl.off_a], accum.A[i].data(), sl.n_a * 4) == 0 &&
-                     std::memcmp(&ga[sl.off_b], accum.B[i].data(), sl.n_b * 4) == 0 &&
-                     std::memcmp(&ga[sl.off_m], accum.mag[i].data(), sl.n_m * 4) == 0;
+        gworst = std::max(gworst, max_rel(std::vector<float>(ga.begin() + sl.off_a, ga.begin() + sl.off_a + sl.n_a),
+                                          accum.A[i]));
+        gworst = std::max(gworst, max_rel(std::vector<float>(ga.begin() + sl.off_b, ga.begin() + sl.off_b + sl.n_b),
+                                          accum.B[i]));
+        gworst = std::max(gworst, max_rel(std::vector<float>(ga.begin() + sl.off_m, ga.begin() + sl.off_m + sl.n_m),
+                                          accum.mag[i]));
     }
-    expect(same_grads, "mirror accumulator == arena gradients, bitwise");
+    expect(gworst < 1e-6, "mirror accumulator == arena gradients");
     sa3k_adamw_params p{hp.learning_rate, hp.beta1, hp.beta2, hp.eps, hp.weight_decay, hp.grad_clip};
     double norm_abi = 0.0, norm_mirror = 0.0;
     expect(sa3k_adamw_clip(ctx, graph.params, graph.grads, mom, var, (int64_t)n, &p, 1, 2, &norm_abi) == SA3K_OK,
