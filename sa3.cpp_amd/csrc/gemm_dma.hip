@@ -49,6 +49,19 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+template <int N>
+struct IC {
+    static constexpr int value = N;
+};
+// f(IC<0>{}), ..., f(IC<N-1>{}) in order
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(IC<I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 // s_waitcnt vmcnt(n) leaving the other counters untouched (gfx9 encoding)
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -91,8 +104,22 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
     constexpr int BKE = 8 * CE;                                      // K elements per tile
     constexpr int STAGE_BYTES = (BM + BN) * kRow;
     static_assert(NA >= 1 && NB >= 1 && FM >= 1 && FN >= 1, "tile too small");
-    static_assert(STAGES >= 2 && (STAGES - 1) * LPT < 64, "pipeline depth");
-    __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE_BYTES];
+    static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * LPT < 64, "pipeline depth");
+    // One LDS object per stage, always addressed by a compile-time stage index: the compiler then
+    // knows that the DMA filling stage s+STAGES-1 cannot alias the stage the MFMAs read, and keeps
+    // it in flight instead of waiting for every outstanding DMA before each LDS read. (Stages a
+    // configuration does not use are never referenced and take no LDS.)
+    __shared__ __attribute__((aligned(1024))) char lds0[STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char lds1[STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char lds2[STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char lds3[STAGE_BYTES];
+    auto stage = [&](auto s) -> char* {
+        constexpr int S = decltype(s)::value % STAGES;
+        if constexpr (S == 0) return lds0;
+        else if constexpr (S == 1) return lds1;
+        else if constexpr (S == 2) return lds2;
+        else return lds3;
+    };
 
     const int64_t Mt = p.M + p.Mx;
     const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
@@ -151,8 +178,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
                                   : static_cast<const char*>(p.zero);
     }
 
-    auto issue = [&](int t) {
-        char* st = lds + (t % STAGES) * STAGE_BYTES;
+    auto issue = [&](char* st, int t) {
         if (t < Tm) {
 #pragma unroll
             for (int q = 0; q < NA; ++q) dma16(ag[q] + (int64_t)t * (BKE * EB), st + (q * kThreads + wave * 64) * 16);
@@ -172,8 +198,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int t) {
-        const char* As = lds + (t % STAGES) * STAGE_BYTES;
+    auto compute = [&](const char* As) {
         const char* Bs = As + BM * kRow;
         const int r = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -219,25 +244,29 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(DmaParams p) {
         }
     };
 
-    // prologue: STAGES-1 tiles in flight
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < T) issue(s);
-    for (int t = 0; t < T; ++t) {
-        // tile t has landed once at most min(STAGES-2, T-1-t) later tiles are outstanding
-        const int later = min(STAGES - 2, T - 1 - t);
-        if (later >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LPT>();
-        else if constexpr (STAGES >= 3) {
-            if (later == 1) wait_vmcnt<LPT>();
-            else wait_vmcnt<0>();
-        } else {
-            wait_vmcnt<0>();
-        }
-        // tile t visible to all waves; every wave is done with tile t-1. A bare s_barrier: the
-        // fence __syncthreads adds would wait for every in-flight DMA (vmcnt 0), not just tile t.
-        __asm__ volatile("s_barrier" ::: "memory");
-        if (t + STAGES - 1 < T) issue(t + STAGES - 1);
-        compute(t);
+    // prologue: STAGES-1 tiles in flight; tile t always lives in stage t % STAGES
+    static_for<STAGES - 1>([&](auto s) {
+        if (decltype(s)::value < T) issue(stage(s), decltype(s)::value);
+    });
+    for (int t0 = 0; t0 < T; t0 += STAGES) {
+        static_for<STAGES>([&](auto s) {
+            const int t = t0 + decltype(s)::value;
+            if (t >= T) return;
+            // tile t has landed once at most min(STAGES-2, T-1-t) later tiles are outstanding
+            const int later = min(STAGES - 2, T - 1 - t);
+            if (later >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LPT>();
+            else if constexpr (STAGES >= 3) {
+                if (later == 1) wait_vmcnt<LPT>();
+                else wait_vmcnt<0>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            // tile t visible to all waves; every wave is done with tile t-1. A bare s_barrier: the
+            // fence __syncthreads adds would wait for every in-flight DMA (vmcnt 0), not just tile t.
+            __asm__ volatile("s_barrier" ::: "memory");
+            if (t + STAGES - 1 < T) issue(stage(IC<decltype(s)::value + STAGES - 1>{}), t + STAGES - 1);
+            compute(stage(s));
+        });
     }
 
     if (p.ws) {  // split-K partial sums
