@@ -45,7 +45,7 @@ struct sa3k_ctx {
     int gemm_split = 1;                   // allow split-K
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
-    int gemm_wg_per_cu = 2;               // resident workgroups per CU assumed by the split choice
+    int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
     size_t red_ws_bytes = 0;
     int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch)
