@@ -84,11 +84,14 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
 /* Implementation knobs of a context (no reference counterpart; for tests and measurement):
  *   "gemm_split"  1: split K when a GEMM's output tiles cannot fill the chip (default 1)
  *   "gemm_fixup"  1: split partial sums are reduced by the last split to arrive, in split order,
- *                 inside the producing kernel; 0: by a separate reduction launch (default 0)
+ *                 inside the producing kernel; 0: by a separate reduction launch; 2: in-kernel for
+ *                 outputs of at most 2^18 floats, a separate launch for larger ones (default 0)
  *   "gemm_dma"    1: DMA-fed kernel for compute-type operands (default 1)
  *   "gemm_cfg"    DMA kernel tile configuration (default 0)
- * Every setting gives results identical to the defaults bit for bit except gemm_split and gemm_cfg,
- * which change the f32 summation order. Not to be changed while a graph is being captured. */
+ *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
+ *                 fill the chip (default 2: 64x128 tiles; 0: the default tile, split over K)
+ * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg and
+ * gemm_small, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

@@ -366,7 +366,7 @@ void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const flo
             const float* gamma, int g_part, int part0) {
     const int chunk = (int)ceil_div(w->S, w->part_chunks);
     const int64_t ctrs = nblk(w->dim) * (int64_t)w->B;
-    int* counters = ctx->gemm_fixup && ctrs <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
+    int* counters = use_fixup(ctx, (int64_t)w->B * w->dim, ctrs) ? ctx->tile_counters : nullptr;
     launch(ctx, "blk_colred", colred_kernel, dim3(nblk(w->dim), (unsigned)w->part_chunks, (unsigned)w->B), mode, a, x,
            rstd, gamma, (const float*)w->modv, g_part, w->S, w->dim, chunk, w->part, part0, w->dssg, counters);
     if (!counters)

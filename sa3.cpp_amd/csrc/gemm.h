@@ -70,6 +70,7 @@ struct GemmDesc {
     float* Cx = nullptr;
     int64_t ldcx = 0;
     int accumulate_x = 0;
+    bf16* Cbx = nullptr;   // instead of Cx: extra rows stored as bf16 [Mx][ldcx] (no accumulation)
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

@@ -30,6 +30,7 @@ struct KParams {
     const void* Ax; int64_t ldax;
     const void* A2x; int64_t lda2x;
     float* Cx; int64_t ldcx; int accumulate_x;
+    bf16* Cbx;
     float* ws;   // split-K partials [splits][M+Mx][N] (null: no split)
     int kps;     // K tiles per split
 };
@@ -160,6 +161,10 @@ __device__ inline void mma_tile(const char* As, const char* Bs, int wm0, int wn0
 __device__ inline void epilogue_elem(const KParams& p, int64_t m, int64_t n, float acc) {
     float x = p.alpha * acc;
     if (m >= p.M) {
+        if (p.Cbx) {
+            p.Cbx[(m - p.M) * p.ldcx + n] = (bf16)x;
+            return;
+        }
         float* cx = p.Cx + (m - p.M) * p.ldcx + n;
         *cx = p.accumulate_x ? *cx + x : x;
         return;
@@ -480,8 +485,8 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
         if (d.b_src == SRC_Q8T) SA3K_REQUIRE(d.N % 32 == 0 && d.ldbs % 8 == 0 && al16(d.Bs), "Q8_0 transposed layout misaligned");
     }
     SA3K_REQUIRE(d.Mx >= 0, "negative extra rows");
-    SA3K_REQUIRE(d.Mx == 0 || (d.Ax && d.Cx && al16(d.Ax) && (d.K2 == 0 || (d.A2x && al16(d.A2x)))),
-                 "GEMM extra rows need Ax, Cx (and A2x with a second segment)");
+    SA3K_REQUIRE(d.Mx == 0 || (d.Ax && (d.Cx || d.Cbx) && al16(d.Ax) && (d.K2 == 0 || (d.A2x && al16(d.A2x)))),
+                 "GEMM extra rows need Ax, Cx or Cbx (and A2x with a second segment)");
     const int ct_src = bf ? SRC_BF16 : SRC_F32;
     if (d.a_src == ct_src && d.b_src == ct_src && ctx->gemm_dma) {
         SA3K_REQUIRE((d.ldb * (bf ? 2 : 4)) % 16 == 0 && (d.Mx == 0 || (d.ldax * (bf ? 2 : 4)) % 16 == 0),
@@ -493,7 +498,7 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     }
     KParams p{d.A, d.lda, d.B, d.ldb, d.Bs, d.ldbs, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K,
               d.alpha, d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
-              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, nullptr, 0};
+              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0};
     KernelScope ks(ctx, prof_name);
     if (bf) {
         if (d.a_src == SRC_BF16) launch_b<SRC_BF16, true>(ctx, p, d.b_src);

@@ -34,6 +34,7 @@ struct DmaParams {
     const void* Ax; int64_t ldax;
     const void* A2x; int64_t lda2x;
     float* Cx; int64_t ldcx; int accumulate_x;
+    bf16* Cbx;
     float* ws;
     int kps;
     const void* zero;   // >= 16 zero bytes
@@ -117,6 +118,10 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
 __device__ inline void epilogue_elem(const DmaParams& p, int64_t m, int64_t n, float acc) {
     float x = p.alpha * acc;
     if (m >= p.M) {
+        if (p.Cbx) {
+            p.Cbx[(m - p.M) * p.ldcx + n] = (bf16)x;
+            return;
+        }
         float* cx = p.Cx + (m - p.M) * p.ldcx + n;
         *cx = p.accumulate_x ? *cx + x : x;
         return;
@@ -137,6 +142,11 @@ __device__ inline void epilogue_elem(const DmaParams& p, int64_t m, int64_t n, f
 __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a) {
     float4 x = make_float4(p.alpha * a.x, p.alpha * a.y, p.alpha * a.z, p.alpha * a.w);
     if (m >= p.M) {
+        if (p.Cbx) {
+            bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
+            *reinterpret_cast<uint2*>(p.Cbx + (m - p.M) * p.ldcx + n) = __builtin_bit_cast(uint2, b);
+            return;
+        }
         float4* cx = reinterpret_cast<float4*>(p.Cx + (m - p.M) * p.ldcx + n);
         if (p.accumulate_x) {
             const float4 o = *cx;
@@ -542,11 +552,12 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
             return q == nullptr || (ld % 4 == 0 && (uintptr_t)q % (uintptr_t)align == 0);
         };
         p.vec_epi = p.N % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) &&
-                    ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.colscale, 4, 16) && ok(p.bias, 4, 16);
+                    ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) &&
+                    ok(p.bias, 4, 16);
     }
     if (splits > 1) {
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
-        if (ctx->gemm_fixup && tiles <= kMaxFixupTiles) p.counters = ctx->tile_counters;
+        if (use_fixup(ctx, (p.M + p.Mx) * p.N, tiles)) p.counters = ctx->tile_counters;
     }
     dim3 g((unsigned)grid, (unsigned)splits);
     {
@@ -571,13 +582,20 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, BF16>(ctx, p);
     if (p.N <= 32) return launch_dma<128, 32, 4, 4, BF16>(ctx, p);
     if (p.N <= 64) return launch_dma<128, 64, 4, 4, BF16>(ctx, p);
+    // Grids of 128x128 tiles that leave a quarter of the two-per-CU slots idle: with a short K a
+    // 64x128 tile and no split (2176 x 1536 x 1536: 21 us instead of 28 with split-K); with a long
+    // K (>= 4096) the 128x128 tile split over K stays faster.
+    const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+    if (tiles128 < 384 && p.K < (BF16 ? 4096 : 2048)) {
+        switch (ctx->gemm_small) {
+            case 1: return launch_dma<64, 128, 2, 2, BF16>(ctx, p);
+            case 2: return launch_dma<64, 128, 1, 3, BF16>(ctx, p);
+            case 3: return launch_dma<128, 64, 2, 2, BF16>(ctx, p);
+            default: break;
+        }
+    }
     switch (ctx->gemm_cfg) {
-        case 1: return launch_dma<128, 128, 2, 4, BF16>(ctx, p);
-        case 2: return launch_dma<256, 128, 2, 3, BF16>(ctx, p);
-        case 3: return launch_dma<128, 256, 2, 3, BF16>(ctx, p);
         case 4: return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);   // 144 KiB LDS, 8 waves of 64x64
-        case 5: return launch_dma<256, 128, 4, 3, BF16, 8>(ctx, p);
-        case 6: return launch_dma<128, 128, 2, 4, BF16, 8>(ctx, p);   // 128 KiB LDS, 8 waves of 64x32
         case 7: return launch_dma<128, 256, 2, 2, BF16, 8>(ctx, p);
         default: return launch_dma<128, 128, 2, 2, BF16>(ctx, p);   // 64 KiB LDS: two workgroups per CU
     }
@@ -588,7 +606,7 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
 void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     DmaParams p{d.A, d.lda, d.B, d.ldb, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K, d.alpha,
                 d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
-                d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, nullptr, 0, ctx->zero_page};
+                d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0, ctx->zero_page};
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

@@ -649,7 +649,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         const int64_t rows_per = tn_rows_per(out, N);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
-        int* counters = ctx->gemm_fixup && ceil_div(out, TN_COLS) <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
+        int* counters = use_fixup(ctx, (int64_t)33 * out, ceil_div(out, TN_COLS)) ? ctx->tile_counters : nullptr;
         {
             KernelScope ks(ctx, "lin_bwd_colred_dy", 2.0 * N * out * r);
             skinny_tn_kernel<TN_DY, float><<<dim3((unsigned)ceil_div(out, TN_COLS), (unsigned)S), kThreads, 0,
@@ -692,24 +692,15 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             static_cast<CT*>(L->Ax));
         SA3K_LAUNCHED();
     }
-    if (L->dora) {
-        // A2x = 2 s^2 B^T diag(gn) B = s * (Ax . Bt^T), K = out (a rank x rank GEMM, split over K)
-        if (out % (bf ? 64 : 32) == 0) {
-            GemmDesc g;
-            g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = g.a_src;
-            g.A = L->Ax; g.lda = out; g.B = L->Bt; g.ldb = out;
-            g.M = r; g.N = r; g.K = out; g.alpha = L->s;
-            if (bf) { g.Cb = static_cast<bf16*>(L->A2x); g.ldcb = r; }
-            else { g.C = static_cast<float*>(L->A2x); g.ldc = r; }
-            gemm_run(ctx, g, "lin_bwd_btgb");
-        } else {
-            KernelScope ks(ctx, "lin_bwd_btgb");
-            btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
-                                                                             static_cast<CT*>(L->A2x));
-            SA3K_LAUNCHED();
-        }
+    // 2. sdUB = s dU B; dora: A2x = 2 s^2 B^T diag(gn) B = s * (Ax . Bt^T) contracts the same Bt
+    //    over out, so it rides on the same GEMM as r extra rows
+    const bool fold_btgb = L->dora && out % (bf ? 64 : 32) == 0;
+    if (L->dora && !fold_btgb) {
+        KernelScope ks(ctx, "lin_bwd_btgb");
+        btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
+                                                                         static_cast<CT*>(L->A2x));
+        SA3K_LAUNCHED();
     }
-    // 2. sdUB = s dU B
     {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = bf ? SRC_BF16 : SRC_F32;
@@ -717,6 +708,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.M = N; g.N = r; g.K = out; g.alpha = L->s;
         if (bf) { g.Cb = static_cast<bf16*>(L->sdUB); g.ldcb = r; }
         else { g.C = static_cast<float*>(L->sdUB); g.ldc = r; }
+        if (fold_btgb) {
+            g.Mx = r; g.Ax = L->Ax; g.ldax = out; g.ldcx = r;
+            if (bf) g.Cbx = static_cast<bf16*>(L->A2x);
+            else g.Cx = static_cast<float*>(L->A2x);
+        }
         gemm_run(ctx, g, "lin_bwd_dub");
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
@@ -748,7 +744,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         const int64_t rows_per = tn_rows_per(in, N);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 32 * in * sizeof(float));
-        int* counters = ctx->gemm_fixup && ceil_div(in, TN_COLS) <= kMaxFixupTiles ? ctx->tile_counters : nullptr;
+        int* counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
         const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)S);
         {
             KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);

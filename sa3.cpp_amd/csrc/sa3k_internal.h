@@ -45,10 +45,12 @@ struct sa3k_ctx {
     int gemm_split = 1;                   // allow split-K
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
+    int gemm_small = 2;                   // tile configuration for small grids (0: the default tile + split-K)
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
     size_t red_ws_bytes = 0;
-    int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch)
+    int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch):
+                                          // 0 never, 1 always, 2 for small outputs only
     int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
@@ -126,6 +128,16 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // capacity of sa3k_ctx::tile_counters (tiles of one split-K / split-reduction launch)
 constexpr int kMaxFixupTiles = 8192;
+// Outputs of at most this many floats are reduced in-kernel under gemm_fixup = 2. (Measured on
+// MI355X, even these small in-kernel reductions cost more than the separate launch: the coherent
+// partial loads of the last workgroup serialize; 2 stays selectable, 0 is the default.)
+constexpr int64_t kSmallFixupElems = (int64_t)1 << 18;
+
+// whether a split reduction over an output of `elems` floats is done by the last split to arrive
+inline bool use_fixup(const sa3k_ctx* ctx, int64_t elems, int64_t tiles) {
+    if (tiles > kMaxFixupTiles) return false;
+    return ctx->gemm_fixup == 1 || (ctx->gemm_fixup == 2 && elems <= kSmallFixupElems);
+}
 
 // Split partial sums handed from one workgroup to another inside a launch ("the last split to
 // arrive reduces"): device-coherent (sc1) accesses, so no cache level can hold a stale copy and no

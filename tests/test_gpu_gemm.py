@@ -120,7 +120,7 @@ def test_split_k_fixup_matches_separate_reduction(ctx, M, N, K):
     bias = r.normal(0, 1, N).astype(np.float32)
     out = {}
     try:
-        for fixup in (0, 1, 0, 1):
+        for fixup in (0, 1, 2, 0, 1, 2):
             ctx.set_option("gemm_fixup", fixup)
             res = run(ctx, A, B, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, sa3k.TYPE_BF16, bias=bias)
             if fixup in out:
@@ -128,4 +128,4 @@ def test_split_k_fixup_matches_separate_reduction(ctx, M, N, K):
             out[fixup] = res
     finally:
         ctx.set_option("gemm_fixup", 0)
-    assert np.array_equal(out[0], out[1])
+    assert np.array_equal(out[0], out[1]) and np.array_equal(out[0], out[2])
