@@ -13,9 +13,14 @@
 //
 // MFMA layout (v_mfma_f32_16x16x32_bf16): scores are computed transposed, S^T = K Q^T, so that a
 // lane holds one query (lane % 16) and 4 keys per 16-key tile; two adjacent key tiles give the 8
-// key-values that lane feeds as the A operand of P V. The B operand for that product is read from
-// a transposed V tile (dims x keys) with the same key pattern, so both operands agree on K order.
-// The dK/dV kernel computes S = Q K^T instead (lane = one key) for the same reason.
+// key-values that lane feeds as the A operand of P V. The operand on the other side (V for P V,
+// Q and dO for dK and dV, K for dQ) contracts over the tile's row index; it is read with
+// ds_read_b64_tr_b16 straight from the row-major tile in the same key order, so both operands
+// agree on K order. The dK/dV kernel computes S = Q K^T instead (lane = one key).
+//
+// Tiles are [64 rows][64] bf16, 128-byte XOR-swizzled LDS rows, filled by buffer_load ... lds DMA
+// through a per-tile buffer descriptor whose extent ends at the last valid row, so rows past the
+// sequence read as zeros. Two LDS stages: the DMA of block i+1 runs while block i is computed.
 //
 // window > 0 keeps keys with |q - k| <= window/2 (self-attention only); 0 is dense.
 #include "sa3k_internal.h"
@@ -31,7 +36,6 @@ constexpr int kThreads = 256;
 constexpr int HD = 64;          // head dim
 constexpr int BLK = 64;         // queries / keys per block
 constexpr int ROW = 128;        // bytes per [row][64] bf16 LDS row (swizzled, unpadded)
-constexpr int TROW = 136;       // bytes per transposed [64][64] LDS row (padded by 4 bf16)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // XOR swizzle of the eight 16-byte chunks of a 128-byte LDS row. MFMA operand reads (lane l reads
@@ -52,32 +56,68 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ bf16x8 ld_row(const char* t, int r, int c) {
     return *reinterpret_cast<const bf16x8*>(t + r * ROW + ((c ^ swz(r)) << 4));
 }
-__device__ __forceinline__ void st_row(char* t, int r, int c, uint4 v) {
-    *reinterpret_cast<uint4*>(t + r * ROW + ((c ^ swz(r)) << 4)) = v;
-}
-// 4 consecutive columns (8 bytes) of row r in a transposed [64][64] tile
-__device__ __forceinline__ bf16x4 ld_t4(const char* t, int r, int col) {
-    return *reinterpret_cast<const bf16x4*>(t + r * TROW + col * 2);
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Transposed read (ds_read_b64_tr_b16) of a swizzled tile: every 16-lane group returns, in lane
+// j of the group, the 4 values T[k0 .. k0+3][n0 + j]. Lane j of the group addresses row k0 + j/4,
+// columns n0 + 4*(j%4) .. +3 (the instruction hands element i%4 of the chunks of lanes
+// i/4, i/4+4, i/4+8, i/4+12 to lane i). k0 and n0 may differ between the four groups.
+__device__ __forceinline__ bf16x4 ld_tr(const char* t, int k0, int n0, int lane) {
+    const int j = lane & 15, row = k0 + (j >> 2), n = n0 + 4 * (j & 3);
+    const char* a = t + row * ROW + (((n >> 3) ^ swz(row)) << 4) + (n & 7) * 2;
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(
+        (lds_ptr_t)a)));
 }
 __device__ __forceinline__ bf16x8 cat44(bf16x4 a, bf16x4 b) {
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Load a [64 rows][64] bf16 tile (rows r0.., row stride 64 elems, rows >= nrows zero) into LDS as
-// a swizzled row tile and/or a transposed (dims x rows) tile.
-__device__ __forceinline__ void load_tile(const bf16* __restrict__ src, int r0, int nrows, char* row_t,
-                                          char* tr_t) {
-    for (int k = threadIdx.x; k < BLK * 8; k += kThreads) {
-        const int r = k >> 3, c = k & 7;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (r0 + r < nrows) v = *reinterpret_cast<const uint4*>(src + (int64_t)(r0 + r) * HD + c * 8);
-        if (row_t) st_row(row_t, r, c, v);
-        if (tr_t) {
-            const bf16x8 e = __builtin_bit_cast(bf16x8, v);
+// Raw buffer descriptor over [base, base + bytes): loads past the end return zeros.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const unsigned long long a = (unsigned long long)(uintptr_t)base;
+    u32x4 r;
+    // the descriptor lives in SGPRs: make its (wave-uniform) words provably uniform
+    r.x = __builtin_amdgcn_readfirstlane((unsigned)a);
+    r.y = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32) & 0xffffu);   // stride 0
+    r.z = __builtin_amdgcn_readfirstlane(bytes);                           // num_records
+    r.w = 0x00020000u;                                                     // 32-bit format, no swizzle
+    return r;
+}
+
+// Issue the DMA of rows row0 .. row0+63 of a [nrows][64] bf16 matrix into a swizzled LDS tile
+// (512 16-byte slots, two per thread; slot s holds row s/8, logical chunk (s%8) ^ swz(row)).
+// Inline asm so that the compiler's waits do not drain the DMA before unrelated LDS reads; the
+// kernels order it with vmcnt waits and barriers.
+__device__ __forceinline__ void tile_dma(const bf16* base, int nrows, int row0, const char* lds_tile, int tid,
+                                         int wave) {
+    const int valid = max(0, min(BLK, nrows - row0));
+    const u32x4 rs = buffer_rsrc(base + (int64_t)row0 * HD, (uint32_t)valid * ROW);
+    const uint32_t tile = (uint32_t)(uintptr_t)(lds_ptr_t)lds_tile;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *reinterpret_cast<bf16*>(tr_t + (c * 8 + j) * TROW + r * 2) = e[j];
-        }
+    for (int q = 0; q < 2; ++q) {
+        const int sl = q * kThreads + tid, row = sl >> 3, kc = (sl & 7) ^ swz(row);
+        const uint32_t voff = (uint32_t)(row * ROW + kc * 16);
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + (uint32_t)((q * kThreads + wave * 64) * 16));
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
+                     : "memory");
     }
+}
+// DMA of 64 floats v[i0 .. i0+63] (zeros past n) into LDS, by one wave (one dword per lane)
+__device__ __forceinline__ void vec_dma(const float* v, int n, int i0, const float* lds_vec, int lane) {
+    const int valid = max(0, min(BLK, n - i0));
+    const u32x4 rs = buffer_rsrc(v + i0, (uint32_t)valid * 4);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)lds_vec);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"((uint32_t)lane * 4),
+                 "s"(rs)
+                 : "memory");
+}
+// this wave's DMAs have landed; then a barrier makes every wave's visible
+__device__ __forceinline__ void dma_wait_all() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ bool vis(int q, int k, int nk, int window) {
@@ -110,10 +150,9 @@ struct FwdArgs {
 };
 
 __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
-    __shared__ __attribute__((aligned(16))) char k1s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char k2s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char vts[HD * TROW];
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {K1, K2, V}
     const int bh = blockIdx.y, qb = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
     const int qrow = qb * BLK + w * 16 + r;        // this lane's query for the S^T layout
@@ -137,12 +176,20 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
 
     int kb_lo, kb_hi;
     band_range(qb, a.Sk, a.window, kb_lo, kb_hi);
+    auto issue = [&](int st, int kb) {
+        char* t = lds + st * 3 * BLK * ROW;
+        tile_dma(a.k1 + koff, a.Sk, kb * BLK, t, threadIdx.x, wave);
+        tile_dma(a.k2 + koff, a.Sk, kb * BLK, t + BLK * ROW, threadIdx.x, wave);
+        tile_dma(a.v + koff, a.Sk, kb * BLK, t + 2 * BLK * ROW, threadIdx.x, wave);
+    };
+    if (kb_lo < kb_hi) issue(0, kb_lo);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
-        __syncthreads();
-        load_tile(a.k1 + koff, kb * BLK, a.Sk, k1s, nullptr);
-        load_tile(a.k2 + koff, kb * BLK, a.Sk, k2s, nullptr);
-        load_tile(a.v + koff, kb * BLK, a.Sk, nullptr, vts);
-        __syncthreads();
+        const int st = (kb - kb_lo) & 1;
+        dma_wait_all();   // block kb landed; every wave is done with block kb-1 (the other stage)
+        if (kb + 1 < kb_hi) issue(st ^ 1, kb + 1);
+        const char* k1s = lds + st * 3 * BLK * ROW;
+        const char* k2s = k1s + BLK * ROW;
+        const char* vs = k1s + 2 * BLK * ROW;
         // S^T tiles: keys kt*16 + 4g + v, query qrow
         f32x4 s1[4], s2[4];
 #pragma unroll
@@ -207,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
         for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const bf16x8 vb = cat44(ld_t4(vts, dt * 16 + r, 32 * ch + 4 * g), ld_t4(vts, dt * 16 + r, 32 * ch + 16 + 4 * g));
+                const bf16x8 vb = cat44(ld_tr(vs, 32 * ch + 4 * g, dt * 16, lane), ld_tr(vs, 32 * ch + 16 + 4 * g, dt * 16, lane));
                 o1[dt] = mfma(p1[ch], vb, o1[dt]);
                 o2[dt] = mfma(p2[ch], vb, o2[dt]);
             }
@@ -274,14 +321,10 @@ struct BwdArgs {
 
 // Per key block: dK1, dK2, dV. S = Q K^T with lane = key (lane%16), queries 4g+v per 16-query tile.
 __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) char q1s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char q2s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char dos[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char q1t[HD * TROW];
-    __shared__ __attribute__((aligned(16))) char q2t[HD * TROW];
-    __shared__ __attribute__((aligned(16))) char dot[HD * TROW];
-    __shared__ float sl1[BLK], sl2[BLK], sd1[BLK], sd2[BLK];
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {Q1, Q2, dO}
+    __shared__ __attribute__((aligned(16))) float vec[2][4][BLK];            // lse1, lse2, dn1, dn2
     const int bh = blockIdx.y, kb = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
     const int key = kb * BLK + w * 16 + r;     // this lane's key
@@ -306,20 +349,31 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     int qb_lo, qb_hi;
     band_range(kb, a.Sq, a.window, qb_lo, qb_hi);
-    for (int qb = qb_lo; qb < qb_hi; ++qb) {
-        __syncthreads();
-        load_tile(a.q1 + qoff, qb * BLK, a.Sq, q1s, q1t);
-        load_tile(a.q2 + qoff, qb * BLK, a.Sq, q2s, q2t);
-        load_tile(a.dO + qoff, qb * BLK, a.Sq, dos, dot);
-        if (threadIdx.x < BLK) {
-            const int q = qb * BLK + threadIdx.x;
-            const bool ok = q < a.Sq;
-            sl1[threadIdx.x] = ok ? a.lse1[(int64_t)bh * a.Sq + q] : 0.f;
-            sl2[threadIdx.x] = ok ? a.lse2[(int64_t)bh * a.Sq + q] : 0.f;
-            sd1[threadIdx.x] = ok ? a.dn1[(int64_t)bh * a.Sq + q] : 0.f;
-            sd2[threadIdx.x] = ok ? a.dn2[(int64_t)bh * a.Sq + q] : 0.f;
+    const int64_t voff = (int64_t)bh * a.Sq;
+    auto issue = [&](int st, int qb) {
+        char* t = lds + st * 3 * BLK * ROW;
+        tile_dma(a.q1 + qoff, a.Sq, qb * BLK, t, threadIdx.x, wave);
+        tile_dma(a.q2 + qoff, a.Sq, qb * BLK, t + BLK * ROW, threadIdx.x, wave);
+        tile_dma(a.dO + qoff, a.Sq, qb * BLK, t + 2 * BLK * ROW, threadIdx.x, wave);
+        if (wave == 0) {
+            vec_dma(a.lse1 + voff, a.Sq, qb * BLK, vec[st][0], lane);
+            vec_dma(a.lse2 + voff, a.Sq, qb * BLK, vec[st][1], lane);
+            vec_dma(a.dn1 + voff, a.Sq, qb * BLK, vec[st][2], lane);
+            vec_dma(a.dn2 + voff, a.Sq, qb * BLK, vec[st][3], lane);
         }
-        __syncthreads();
+    };
+    if (qb_lo < qb_hi) issue(0, qb_lo);
+    for (int qb = qb_lo; qb < qb_hi; ++qb) {
+        const int st = (qb - qb_lo) & 1;
+        dma_wait_all();   // block qb landed; every wave is done with block qb-1 (the other stage)
+        if (qb + 1 < qb_hi) issue(st ^ 1, qb + 1);
+        const char* q1s = lds + st * 3 * BLK * ROW;
+        const char* q2s = q1s + BLK * ROW;
+        const char* dos = q1s + 2 * BLK * ROW;
+        const float* sl1 = vec[st][0];
+        const float* sl2 = vec[st][1];
+        const float* sd1 = vec[st][2];
+        const float* sd2 = vec[st][3];
         // per 16-query tile qt: S1, S2, dP with rows = queries qt*16 + 4g + v, col = key
         bf16x8 pd[2], ds1[2], ds2[2];    // (P1 - P2), dS1, dS2 as B operands over query pairs
 #pragma unroll
@@ -348,10 +402,10 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
         for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const int row = dt * 16 + r, c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
-                dvt[dt] = mfma(cat44(ld_t4(dot, row, c0), ld_t4(dot, row, c1)), pd[ch], dvt[dt]);
-                dk1t[dt] = mfma(cat44(ld_t4(q1t, row, c0), ld_t4(q1t, row, c1)), ds1[ch], dk1t[dt]);
-                dk2t[dt] = mfma(cat44(ld_t4(q2t, row, c0), ld_t4(q2t, row, c1)), ds2[ch], dk2t[dt]);
+                const int c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
+                dvt[dt] = mfma(cat44(ld_tr(dos, c0, dt * 16, lane), ld_tr(dos, c1, dt * 16, lane)), pd[ch], dvt[dt]);
+                dk1t[dt] = mfma(cat44(ld_tr(q1s, c0, dt * 16, lane), ld_tr(q1s, c1, dt * 16, lane)), ds1[ch], dk1t[dt]);
+                dk2t[dt] = mfma(cat44(ld_tr(q2s, c0, dt * 16, lane), ld_tr(q2s, c1, dt * 16, lane)), ds2[ch], dk2t[dt]);
             }
     }
     if (key >= a.Sk) return;
@@ -368,12 +422,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
 // Per query block: dQ1, dQ2. S^T = K Q^T (lane = query), dP^T = V dO^T.
 __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) char k1s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char k2s[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char vs[BLK * ROW];
-    __shared__ __attribute__((aligned(16))) char k1t[HD * TROW];
-    __shared__ __attribute__((aligned(16))) char k2t[HD * TROW];
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {K1, K2, V}
     const int bh = blockIdx.y, qb = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
     const int qrow = qb * BLK + w * 16 + r;
@@ -403,12 +454,20 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
 
     int kb_lo, kb_hi;
     band_range(qb, a.Sk, a.window, kb_lo, kb_hi);
+    auto issue = [&](int st, int kb) {
+        char* t = lds + st * 3 * BLK * ROW;
+        tile_dma(a.k1 + koff, a.Sk, kb * BLK, t, threadIdx.x, wave);
+        tile_dma(a.k2 + koff, a.Sk, kb * BLK, t + BLK * ROW, threadIdx.x, wave);
+        tile_dma(a.v + koff, a.Sk, kb * BLK, t + 2 * BLK * ROW, threadIdx.x, wave);
+    };
+    if (kb_lo < kb_hi) issue(0, kb_lo);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
-        __syncthreads();
-        load_tile(a.k1 + koff, kb * BLK, a.Sk, k1s, k1t);
-        load_tile(a.k2 + koff, kb * BLK, a.Sk, k2s, k2t);
-        load_tile(a.v + koff, kb * BLK, a.Sk, vs, nullptr);
-        __syncthreads();
+        const int st = (kb - kb_lo) & 1;
+        dma_wait_all();   // block kb landed; every wave is done with block kb-1 (the other stage)
+        if (kb + 1 < kb_hi) issue(st ^ 1, kb + 1);
+        const char* k1s = lds + st * 3 * BLK * ROW;
+        const char* k2s = k1s + BLK * ROW;
+        const char* vs = k1s + 2 * BLK * ROW;
         bf16x8 ds1[2], ds2[2];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
@@ -435,9 +494,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
         for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const int row = dt * 16 + r, c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
-                dq1[dt] = mfma(ds1[ch], cat44(ld_t4(k1t, row, c0), ld_t4(k1t, row, c1)), dq1[dt]);
-                dq2[dt] = mfma(ds2[ch], cat44(ld_t4(k2t, row, c0), ld_t4(k2t, row, c1)), dq2[dt]);
+                const int c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
+                dq1[dt] = mfma(ds1[ch], cat44(ld_tr(k1s, c0, dt * 16, lane), ld_tr(k1s, c1, dt * 16, lane)), dq1[dt]);
+                dq2[dt] = mfma(ds2[ch], cat44(ld_tr(k2s, c0, dt * 16, lane), ld_tr(k2s, c1, dt * 16, lane)), dq2[dt]);
             }
     }
 #pragma unroll
