@@ -25,6 +25,12 @@
 // window > 0 keeps keys with |q - k| <= window/2 (self-attention only); 0 is dense.
 #include "sa3k_internal.h"
 
+#include <algorithm>
+
+namespace sa3k {
+float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);   // gemm.hip: context-owned scratch
+}
+
 namespace {
 
 typedef __bf16 bf16;
@@ -317,6 +323,10 @@ struct BwdArgs {
     int Sq, Sk, window;
     float scale;
     float *dq1, *dq2, *dk1, *dk2, *dv;        // [BH][S][64] f32
+    // dK/dV with the query blocks of a key block split over qsplit workgroups (blockIdx.z): raw
+    // partial sums [qsplit][3 = dV, dK1, dK2][BH][Sk][64] in part, summed by attn_bwd_dkdv_sum
+    int qsplit;
+    float* part;
 };
 
 // Per key block: dK1, dK2, dV. S = Q K^T with lane = key (lane%16), queries 4g+v per 16-query tile.
@@ -349,6 +359,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     int qb_lo, qb_hi;
     band_range(kb, a.Sq, a.window, qb_lo, qb_hi);
+    if (a.qsplit > 1) {   // this workgroup's share of the query blocks
+        const int per = (qb_hi - qb_lo + a.qsplit - 1) / a.qsplit;
+        qb_lo = min(qb_hi, qb_lo + (int)blockIdx.z * per);
+        qb_hi = min(qb_hi, qb_lo + per);
+    }
     const int64_t voff = (int64_t)bh * a.Sq;
     auto issue = [&](int st, int qb) {
         char* t = lds + st * 3 * BLK * ROW;
@@ -409,6 +424,20 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
             }
     }
     if (key >= a.Sk) return;
+    if (a.qsplit > 1) {
+        const int64_t plane = (int64_t)gridDim.y * a.Sk * HD;
+        float* pz = a.part + (int64_t)blockIdx.z * 3 * plane;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t idx = koff + (int64_t)key * HD + dt * 16 + 4 * g + v;
+                pz[idx] = dvt[dt][v];
+                pz[plane + idx] = dk1t[dt][v];
+                pz[2 * plane + idx] = dk2t[dt][v];
+            }
+        return;
+    }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -418,6 +447,24 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
             a.dk1[idx] = a.scale * dk1t[dt][v];
             a.dk2[idx] = a.scale * dk2t[dt][v];
         }
+}
+
+// dV, dK1, dK2 from the query-split partials, summed in split order (4 values per thread)
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_sum(BwdArgs a, int64_t plane) {
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (i >= plane) return;
+    float4 s[3];
+#pragma unroll
+    for (int o = 0; o < 3; ++o) s[o] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < a.qsplit; ++z)
+#pragma unroll
+        for (int o = 0; o < 3; ++o) {
+            const float4 v = *reinterpret_cast<const float4*>(a.part + ((int64_t)z * 3 + o) * plane + i);
+            s[o] = make_float4(s[o].x + v.x, s[o].y + v.y, s[o].z + v.z, s[o].w + v.w);
+        }
+    *reinterpret_cast<float4*>(a.dv + i) = s[0];
+    *reinterpret_cast<float4*>(a.dk1 + i) = make_float4(a.scale * s[1].x, a.scale * s[1].y, a.scale * s[1].z, a.scale * s[1].w);
+    *reinterpret_cast<float4*>(a.dk2 + i) = make_float4(a.scale * s[2].x, a.scale * s[2].y, a.scale * s[2].z, a.scale * s[2].w);
 }
 
 // Per query block: dQ1, dQ2. S^T = K Q^T (lane = query), dP^T = V dO^T.
@@ -524,7 +571,7 @@ void attn_forward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2,
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     FwdArgs a{q1, k1, q2, k2, v, H, Sq, Sk, window, scale, o, o1, o2, lse1, lse2};
     dim3 grid((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H));
-    KernelScope ks(ctx, "attn_fwd");
+    KernelScope ks(ctx, Sq == Sk ? "attn_fwd" : "attn_fwd_cross");
     attn_fwd_kernel<<<grid, kThreads, 0, ctx->stream>>>(a);
     SA3K_LAUNCHED();
 }
@@ -537,20 +584,32 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     const int BH = B * H;
     {
-        KernelScope ks(ctx, "attn_bwd_dot");
+        KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dot" : "attn_bwd_dot_cross");
         const int64_t items = (int64_t)BH * Sq;
         attn_bwd_dot_kernel<<<(unsigned)ceil_div(items, kThreads / 64), kThreads, 0, ctx->stream>>>(
             dO, o1, o2, BH, H, Sq, dOh, dn1, dn2);
         SA3K_LAUNCHED();
     }
-    BwdArgs a{q1, k1, q2, k2, v, dOh, lse1, lse2, dn1, dn2, Sq, Sk, window, scale, dq1, dq2, dk1, dk2, dv};
-    {
-        KernelScope ks(ctx, "attn_bwd_dkdv");
-        attn_bwd_dkdv_kernel<<<dim3((unsigned)ceil_div(Sk, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
-        SA3K_LAUNCHED();
+    BwdArgs a{q1, k1, q2, k2, v, dOh, lse1, lse2, dn1, dn2, Sq, Sk, window, scale, dq1, dq2, dk1, dk2, dv, 1, nullptr};
+    // Few key blocks (cross-attention to a short context): split every key block's query range
+    // over several workgroups so the grid fills the chip, then sum the partials.
+    const int nkb = (int)ceil_div(Sk, BLK), nqb = (int)ceil_div(Sq, BLK);
+    const int64_t plane = (int64_t)BH * Sk * HD;
+    if (window == 0 && (int64_t)nkb * BH < 512) {
+        a.qsplit = (int)std::min<int64_t>({(int64_t)nqb, 16, ceil_div(512, (int64_t)nkb * BH)});
+        if (a.qsplit > 1) a.part = gemm_workspace_bytes(ctx, (size_t)a.qsplit * 3 * plane * sizeof(float));
     }
     {
-        KernelScope ks(ctx, "attn_bwd_dq");
+        KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dkdv" : "attn_bwd_dkdv_cross");
+        attn_bwd_dkdv_kernel<<<dim3((unsigned)nkb, (unsigned)BH, (unsigned)a.qsplit), kThreads, 0, ctx->stream>>>(a);
+        SA3K_LAUNCHED();
+        if (a.qsplit > 1) {
+            attn_bwd_dkdv_sum<<<(unsigned)ceil_div(plane / 4, kThreads), kThreads, 0, ctx->stream>>>(a, plane);
+            SA3K_LAUNCHED();
+        }
+    }
+    {
+        KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dq" : "attn_bwd_dq_cross");
         attn_bwd_dq_kernel<<<dim3((unsigned)ceil_div(Sq, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
         SA3K_LAUNCHED();
     }
