@@ -434,6 +434,22 @@ class DitWorkload:
                           f"(batch {self.B}) in {dt:.1f} s, scaled by the algorithmic flop ratio {ratio:.1f}"}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summaries under profiles/ (a line
+    'traffic: kernel=<name> bytes_per_launch=<B>', written from rocprofv3 FETCH_SIZE + WRITE_SIZE
+    runs scaled by the counters' reading for a copy of known size), or None."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    for f in sorted(os.listdir(pdir)):
+        if not f.endswith(".md"):
+            continue
+        for line in open(os.path.join(pdir, f)):
+            if line.startswith("traffic:") and f"kernel={kernel} " in line + " ":
+                return float(line.split("bytes_per_launch=")[1].split()[0])
+    return None
+
+
 def gemm_roofline(prof, steps):
     """Roofline of the GEMM kernel instantiation with the largest total time. The library counts
     each launch's algorithmic flops, 2 (M + extra rows) N (K + rank extension), at launch time, so
@@ -444,7 +460,7 @@ def gemm_roofline(prof, steps):
     peak = BF16_PEAK_TFLOPS if k.endswith("bf16>") else FP32_MFMA_PEAK_TFLOPS
     ach = work / (ms * 1e-3) / 1e12
     return {"kernel": k, "bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(ach / peak, 4), "traffic": None, "avg_launch_ms": round(ms / cnt, 5),
+            "frac": round(ach / peak, 4), "traffic": measured_traffic(k), "avg_launch_ms": round(ms / cnt, 5),
             "launches_per_step": round(cnt / steps, 1), "algorithmic_flops_per_launch": work / cnt}
 
 
@@ -464,6 +480,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run 5 device-to-device copies of this many bytes (the reference kernel of "
+                         "known traffic that scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -472,6 +491,14 @@ def main():
 
     sa3k = _load("sa3k", os.path.join(ROOT, "sa3.cpp_amd", "sa3k.py"))
     ctx = sa3k.Context(0)
+    if a.copy_bytes > 0:
+        src, dst = ctx.empty(a.copy_bytes // 4, np.float32), ctx.empty(a.copy_bytes // 4, np.float32)
+        for _ in range(5):
+            ctx.copy_d2d(dst, src, a.copy_bytes // 4 * 4)
+        ctx.sync()
+        print(json.dumps({"copy_bytes": a.copy_bytes // 4 * 4, "copies": 5}), flush=True)
+        ctx.close()
+        return
     log(f"workload {a.workload}: setting up")
     wl = WORKLOADS[a.workload](ctx)
     ctx.sync()

@@ -90,6 +90,7 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "gemm_cfg"    DMA kernel tile configuration (default 0)
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
  *                 fill the chip (default 2: 64x128 tiles; 0: the default tile, split over K)
+ *   "gemm_nt_store" 1: GEMM outputs are written with non-temporal stores (default 1)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg and
  * gemm_small, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);

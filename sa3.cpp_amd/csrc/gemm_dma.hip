@@ -43,6 +43,7 @@ struct DmaParams {
     // 32-bit offsets of a buffer descriptor, which then carries the main-segment loads
     uint32_t a_bytes, ax_bytes, b_bytes;
     int vec_epi;   // outputs allow the 16-byte staged epilogue (aligned rows, N % 4 == 0)
+    int nt_store;  // staged-epilogue output stores are non-temporal
 };
 
 namespace {
@@ -137,6 +138,20 @@ __device__ inline void epilogue_elem(const DmaParams& p, int64_t m, int64_t n, f
     if (p.Cb) p.Cb[m * p.ldcb + n] = (bf16)x;
 }
 
+// Output stores of the staged epilogue, optionally non-temporal (context option gemm_nt_store): the
+// output stream (tens of MB per launch) then does not evict the operand lines the other tiles of the
+// launch still reuse from L2.
+typedef float f32v4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32v2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_out(bool nt, float4* p, float4 v) {
+    if (nt) __builtin_nontemporal_store(f32v4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32v4*>(p));
+    else *p = v;
+}
+__device__ __forceinline__ void st_out(bool nt, uint2* p, uint2 v) {
+    if (nt) __builtin_nontemporal_store(u32v2{v.x, v.y}, reinterpret_cast<u32v2*>(p));
+    else *p = v;
+}
+
 // Epilogue of four consecutive columns n..n+3 of row m (host-checked: 16-byte aligned rows, N a
 // multiple of 4), same operations and order as epilogue_elem.
 __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a) {
@@ -155,10 +170,10 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
         *cx = x;
         return;
     }
-    if (p.U) *reinterpret_cast<float4*>(p.U + m * p.ldu + n) = x;
+    if (p.U) st_out(p.nt_store, reinterpret_cast<float4*>(p.U + m * p.ldu + n), x);
     if (p.Ub) {
         bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
-        *reinterpret_cast<uint2*>(p.Ub + m * p.ldu + n) = __builtin_bit_cast(uint2, b);
+        st_out(p.nt_store, reinterpret_cast<uint2*>(p.Ub + m * p.ldu + n), __builtin_bit_cast(uint2, b));
     }
     if (p.colscale) {
         const float4 c = *reinterpret_cast<const float4*>(p.colscale + n);
@@ -174,11 +189,11 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
             const float4 o = *c;
             x = make_float4(o.x + x.x, o.y + x.y, o.z + x.z, o.w + x.w);
         }
-        *c = x;
+        st_out(p.nt_store, c, x);
     }
     if (p.Cb) {
         bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
-        *reinterpret_cast<uint2*>(p.Cb + m * p.ldcb + n) = __builtin_bit_cast(uint2, b);
+        st_out(p.nt_store, reinterpret_cast<uint2*>(p.Cb + m * p.ldcb + n), __builtin_bit_cast(uint2, b));
     }
 }
 
@@ -551,6 +566,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         auto ok = [](const void* q, int64_t ld, int align) {
             return q == nullptr || (ld % 4 == 0 && (uintptr_t)q % (uintptr_t)align == 0);
         };
+        p.nt_store = ctx->gemm_nt_store;
         p.vec_epi = p.N % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) &&
                     ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) &&
                     ok(p.bias, 4, 16);

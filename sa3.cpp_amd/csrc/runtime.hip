@@ -74,6 +74,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_GEMM_DMA")) ctx->gemm_dma = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_SMALL")) ctx->gemm_small = std::atoi(e);
+        if (const char* e = std::getenv("SA3K_GEMM_NT")) ctx->gemm_nt_store = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
@@ -184,6 +185,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_dma") ctx->gemm_dma = value != 0;
         else if (n == "gemm_cfg") ctx->gemm_cfg = value;
         else if (n == "gemm_small") ctx->gemm_small = value;
+        else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

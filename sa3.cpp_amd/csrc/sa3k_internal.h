@@ -45,6 +45,7 @@ struct sa3k_ctx {
     int gemm_split = 1;                   // allow split-K
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
+    int gemm_nt_store = 1;                // GEMM outputs written with non-temporal stores
     int gemm_small = 2;                   // tile configuration for small grids (0: the default tile + split-K)
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)

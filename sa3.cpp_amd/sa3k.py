@@ -249,6 +249,9 @@ class Context:
         assert arr.nbytes == dst.nbytes
         self.check(self.lib.sa3k_upload(self.h, dst.ptr, arr.ctypes.data, arr.nbytes))
 
+    def copy_d2d(self, dst, src, nbytes):
+        self.check(self.lib.sa3k_copy_d2d(self.h, dst.ptr, src.ptr, nbytes))
+
     def sync(self):
         self.check(self.lib.sa3k_sync(self.h))
 
