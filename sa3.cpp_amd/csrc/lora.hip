@@ -474,23 +474,27 @@ __global__ __launch_bounds__(kThreads) void sum_splits_kernel(const float* __res
     y[j] = accumulate ? y[j] + s : s;
 }
 
-// after gd: dm += gd/sqrt(nsq); gn = -gd m nsq^-3/2 / 2; dB[o][a] += dUtH[a][o] + 2s gn P[o][a] + 2s^2 gn BG[o][a];
+// gd[o] and dUtH[a][o] are the split sums (in split order) of the column-reduction partials
+// part[sp][row][o], row 0 = gd, row 1 + a = dUtH[a]; then
+// dm += gd/sqrt(nsq); gn = -gd m nsq^-3/2 / 2; dB[o][a] += dUtH[a][o] + 2s gn P[o][a] + 2s^2 gn BG[o][a];
 // Ax[a][o] = 2s B[o][a] gn[o]  (lora: dB += dUtH only)
 template <class CT>
-__global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __restrict__ gd, const float* __restrict__ redT,
+__global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __restrict__ part, int S, int64_t stride,
                                                                  const float* __restrict__ nsq, const float* __restrict__ mag,
                                                                  const float* __restrict__ Pt, const float* __restrict__ BG,
                                                                  const float* __restrict__ B, int64_t out, int r, float s,
                                                                  int dora, float* __restrict__ dB, float* __restrict__ dm,
                                                                  float* __restrict__ gn_out, CT* __restrict__ Ax) {
-    // thread (row, a): 8 output rows per block, a < 32 the rank index
-    const int ol = threadIdx.x >> 5, a = threadIdx.x & 31;
-    const int64_t o = (int64_t)blockIdx.x * 8 + ol;
+    // thread (o, a): 64 consecutive output rows x 4 rank indices per block (o fastest, so the
+    // partial sums read whole lines)
+    const int64_t o = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+    const int a = (int)blockIdx.y * 4 + (threadIdx.x >> 6);
     if (o >= out) return;
     float gn = 0.f;
     if (dora) {
+        float g = 0.f;
+        for (int sp = 0; sp < S; ++sp) g += part[(int64_t)sp * stride + o];
         const float n2 = nsq[o], sq = sqrtf(n2);
-        const float g = gd[o];
         gn = -0.5f * g * mag[o] / (n2 * sq);
         if (a == 0) {
             if (dm) dm[o] += g / sq;
@@ -498,7 +502,8 @@ __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __
         }
     }
     if (a >= r) return;
-    float v = redT[(int64_t)a * out + o];
+    float v = 0.f;
+    for (int sp = 0; sp < S; ++sp) v += part[(int64_t)sp * stride + (int64_t)(a + 1) * out + o];
     if (dora) {
         v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
         Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
@@ -644,7 +649,10 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, "lin_bwd_dx");
         return;
     }
-    // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens)
+    // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens); the split partials rp[rS][rows][out]
+    const float* rp = nullptr;
+    int rS = 1;
+    int64_t rstride = 0;
     if constexpr (sizeof(CT) == 2) {
         const int64_t rows_per = tn_rows_per(out, N);
         const int S = (int)ceil_div(N, rows_per);
@@ -658,12 +666,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
                 L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per, L->red, 0, counters);
             SA3K_LAUNCHED();
         }
-        if (!counters) {
-            KernelScope ks(ctx, "lin_bwd_reduce");
-            sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(r + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
-                part, (int64_t)33 * out, S, (int64_t)(r + 1) * out, L->red, 0);
-            SA3K_LAUNCHED();
-        }
+        // the rows kernel below sums the S partials (or, after the in-kernel reduction, reads the
+        // one sum in L->red)
+        if (counters) { rp = L->red; rS = 1; }
+        else { rp = part; rS = S; }
+        rstride = (int64_t)33 * out;
     } else {
         const int S = choose_splits(out, N);
         const int64_t rows_per = ceil_div(N, S);
@@ -676,19 +683,13 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
                 static_cast<const CT*>(L->Hc), static_cast<CT*>(L->dU), part, N, out, r, rows_per);
             SA3K_LAUNCHED();
         }
-        KernelScope ks(ctx, "lin_bwd_reduce");
-        // gd -> L->gd ; rows a+1 -> red[a][out]
-        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)(R + 1) * out, kThreads), kThreads, 0, ctx->stream>>>(
-            part, (int64_t)(R + 1) * out, S, (int64_t)(R + 1) * out, L->red, 0);
-        SA3K_LAUNCHED();
+        rp = part; rS = S; rstride = (int64_t)(R + 1) * out;
     }
-    // L->red holds [gd | dUtH rows]: gd = red[0..out), dUtH[a] = red[(a+1)*out ...]
-    const float* gd = L->red;
-    const float* redT = L->red + out;
     {
         KernelScope ks(ctx, "lin_bwd_rows");
-        dora_bwd_rows_kernel<CT><<<(unsigned)ceil_div(out, 8), kThreads, 0, ctx->stream>>>(
-            gd, redT, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
+        const dim3 grid((unsigned)ceil_div(out, 64), (unsigned)ceil_div(std::max(r, 1), 4));
+        dora_bwd_rows_kernel<CT><<<grid, kThreads, 0, ctx->stream>>>(
+            rp, rS, rstride, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
             static_cast<CT*>(L->Ax));
         SA3K_LAUNCHED();
     }
