@@ -318,11 +318,32 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
 //          sum_n Hc[n][a] dU[n][c]                                   (dU^T Hc, stride 33 rows)
 //   TN_X:  part[z][a][c] = sum_n G[n][a] X[n][c]                      ((s dU B)^T X, stride 32 rows)
 // over the token rows of split z. A workgroup owns 64 columns; per 32-token step the Q tile (dU or
-// X) and the P tile (Hc or G, rank padded to 32) are stored transposed in LDS so that each MFMA
-// operand is one 16-byte read of 8 consecutive tokens; each wave owns 16 columns x 32 ranks (two
-// v_mfma_f32_16x16x32_bf16 per step). The kernel is bound by streaming Q once.
+// X, 32 tokens x 64 columns) and the P tile (Hc or G, 32 tokens x rank padded to 32) are stored
+// row-major in LDS with 16- / 8-byte writes and read back with ds_read_b64_tr_b16, which hands
+// each lane 4 consecutive tokens of one column: two of them make the 8-token MFMA operand. Each
+// wave owns 16 columns x 32 ranks (two v_mfma_f32_16x16x32_bf16 per step). Two LDS buffers and
+// the next step's global loads issued before the current step's LDS traffic keep the stream of
+// Q in flight; the kernel is bound by streaming Q once.
 constexpr int TN_DY = 0, TN_X = 1;
-constexpr int TN_COLS = 64, TN_ROWS = 32, TN_LD = 40;   // LDS row: 32 tokens + 8 pad (80 bytes)
+constexpr int TN_COLS = 64, TN_ROWS = 32;
+constexpr int TN_QLD = 144;   // bytes per token row of the Q tile (128 + 16: the four rows a transposed read touches sit in distinct banks)
+constexpr int TN_PLD = 80;    // bytes per token row of the P tile (64 + 16)
+
+typedef short tn_v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 tn_bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+// T[k0 .. k0+3][n0 + (lane%16)] of a row-major bf16 LDS tile with `ld` bytes per row (every 16-lane
+// group of the wave may use its own k0, n0)
+__device__ __forceinline__ tn_bf16x4 tn_ld_tr(const char* t, int ld, int k0, int n0, int lane) {
+    const int j = lane & 15;
+    const char* a = t + (k0 + (j >> 2)) * ld + (n0 + 4 * (j & 3)) * 2;
+    return __builtin_bit_cast(tn_bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                               (__attribute__((address_space(3))) tn_v4s*)(
+                                                   (__attribute__((address_space(3))) void*)a)));
+}
+
+__device__ __forceinline__ bf16x8 cat44(tn_bf16x4 a, tn_bf16x4 b) {
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 template <int MODE, class QT>
 __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restrict__ Q, const bf16* __restrict__ P, int r,
@@ -330,8 +351,8 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
                                                              bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
                                                              int64_t cols, int64_t rows_per, float* __restrict__ out,
                                                              int accumulate, int* __restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) bf16 qt[TN_COLS * TN_LD];
-    __shared__ __attribute__((aligned(16))) bf16 pt[32 * TN_LD];
+    __shared__ __attribute__((aligned(16))) char qt[2][TN_ROWS * TN_QLD];
+    __shared__ __attribute__((aligned(16))) char pt[2][TN_ROWS * TN_PLD];
     __shared__ float red[TN_ROWS][TN_COLS + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t c0 = (int64_t)blockIdx.x * TN_COLS;
@@ -349,60 +370,84 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
         dd[j] = (MODE == TN_DY && d && col_ok) ? d[col + j] : 1.0f;
     }
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    const int r16 = lane & 15, g = lane >> 4;
-    for (int64_t n0 = r0; n0 < r1; n0 += TN_ROWS) {
+    const int g = lane >> 4;
+
+    // one step's global operands of this thread, loaded ahead of use
+    struct Regs {
+        float4 ya, yb;     // dY (DY) or f32 X
+        bf16x8 u;          // U (DY) or bf16 X
+        uint2 pv;          // 4 bf16 of P
+    };
+    auto load = [&](int64_t n0, Regs& R) {
         const int64_t n = n0 + lrow;
         const bool row_ok = n < r1;
-        float q[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = 0.f;
+        R.ya = R.yb = make_float4(0.f, 0.f, 0.f, 0.f);
+        R.u = bf16x8{};
+        R.pv = make_uint2(0, 0);
         if (row_ok && col_ok) {
-            if constexpr (MODE == TN_DY) {
+            if constexpr (MODE == TN_DY || sizeof(QT) == 4) {
                 const float4* y4 = reinterpret_cast<const float4*>(Q + n * cols + col);
-                const float4 ya = y4[0], yb = y4[1];
-                const float y[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
-                bf16x8 ub;
-                if (U) ub = *reinterpret_cast<const bf16x8*>(U + n * cols + col);
-                bf16x8 du;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    q[j] = y[j] * dd[j];
-                    du[j] = (bf16)q[j];
-                    if (U) gd[j] += y[j] * (float)ub[j];
-                }
-                *reinterpret_cast<bf16x8*>(dU + n * cols + col) = du;
-            } else if constexpr (sizeof(QT) == 4) {
-                const float4* x4 = reinterpret_cast<const float4*>(Q + n * cols + col);
-                const float4 xa = x4[0], xb = x4[1];
-                q[0] = xa.x; q[1] = xa.y; q[2] = xa.z; q[3] = xa.w; q[4] = xb.x; q[5] = xb.y; q[6] = xb.z; q[7] = xb.w;
-            } else {
-                const bf16x8 xv = *reinterpret_cast<const bf16x8*>(Q + n * cols + col);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = (float)xv[j];
+                R.ya = y4[0];
+                R.yb = y4[1];
+            }
+            if constexpr (MODE == TN_DY) {
+                if (U) R.u = *reinterpret_cast<const bf16x8*>(U + n * cols + col);
+            } else if constexpr (sizeof(QT) == 2) {
+                R.u = *reinterpret_cast<const bf16x8*>(Q + n * cols + col);
             }
         }
-        float pv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (row_ok && a4 < r) {
-            const bf16* pp = P + n * r + a4;
+        if (row_ok && a4 < r) R.pv = *reinterpret_cast<const uint2*>(P + n * r + a4);
+    };
+    // LDS tiles of one step (and, DY, dU out + the gd partials)
+    auto stage = [&](int64_t n0, const Regs& R, int b) {
+        const int64_t n = n0 + lrow;
+        bf16x8 qv;
+        if constexpr (MODE == TN_DY) {
+            const float y[8] = {R.ya.x, R.ya.y, R.ya.z, R.ya.w, R.yb.x, R.yb.y, R.yb.z, R.yb.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pv[j] = (float)pp[j];
+            for (int j = 0; j < 8; ++j) {
+                const float q = y[j] * dd[j];
+                qv[j] = (bf16)q;
+                if (U) gd[j] += y[j] * (float)R.u[j];
+            }
+            if (n < r1 && col_ok) *reinterpret_cast<bf16x8*>(dU + n * cols + col) = qv;
+        } else if constexpr (sizeof(QT) == 4) {
+            const float y[8] = {R.ya.x, R.ya.y, R.ya.z, R.ya.w, R.yb.x, R.yb.y, R.yb.z, R.yb.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qv[j] = (bf16)y[j];
+        } else {
+            qv = R.u;
         }
-        __syncthreads();   // the previous step's MFMAs are done with the LDS tiles
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qt[(c8 + j) * TN_LD + lrow] = (bf16)q[j];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pt[(a4 + j) * TN_LD + lrow] = (bf16)pv[j];
-        __syncthreads();
-        const bf16x8 af = *reinterpret_cast<const bf16x8*>(qt + (wave * 16 + r16) * TN_LD + 8 * g);
+        *reinterpret_cast<bf16x8*>(qt[b] + lrow * TN_QLD + c8 * 2) = qv;
+        *reinterpret_cast<uint2*>(pt[b] + lrow * TN_PLD + a4 * 2) = R.pv;
+    };
+    // D[i][j] += sum over the step's 32 tokens: i = column wave*16 + 4g+v, j = rank t*16 + lane%16
+    auto mma = [&](int b) {
+        const bf16x8 af = cat44(tn_ld_tr(qt[b], TN_QLD, 8 * g, wave * 16, lane),
+                                tn_ld_tr(qt[b], TN_QLD, 8 * g + 4, wave * 16, lane));
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(pt + (t * 16 + r16) * TN_LD + 8 * g);
+            const bf16x8 bfr = cat44(tn_ld_tr(pt[b], TN_PLD, 8 * g, t * 16, lane),
+                                     tn_ld_tr(pt[b], TN_PLD, 8 * g + 4, t * 16, lane));
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[t], 0, 0, 0);
         }
+    };
+
+    Regs cur, nxt;
+    if (r0 < r1) load(r0, cur);
+    int b = 0;
+    for (int64_t n0 = r0; n0 < r1; n0 += TN_ROWS) {
+        if (n0 + TN_ROWS < r1) load(n0 + TN_ROWS, nxt);   // in flight during this step
+        stage(n0, cur, b);
+        __syncthreads();   // step n0 in buffer b; every wave is done with buffer b's previous use
+        mma(b);
+        b ^= 1;
+        cur = nxt;
     }
-    // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + r16
+    // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + lane%16
     constexpr int RS = MODE == TN_DY ? 33 : 32;
     const int row0 = MODE == TN_DY ? 1 : 0;
+    const int r16 = lane & 15;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int a = t * 16 + r16;
@@ -410,7 +455,10 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int64_t c = c0 + wave * 16 + 4 * g + v;
-            if (c < cols) st_coherent(part + ((int64_t)z * RS + row0 + a) * cols + c, acc[t][v]);
+            if (c >= cols) continue;
+            float* dst = part + ((int64_t)z * RS + row0 + a) * cols + c;
+            if (counters) st_coherent(dst, acc[t][v]);   // read by the last split in this launch
+            else *dst = acc[t][v];
         }
     }
     if constexpr (MODE == TN_DY) {   // gd: sum the 32 token-row slots of each column
@@ -420,10 +468,14 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
         if (tid < TN_COLS) {
             float s = 0.f;
             for (int k = 0; k < TN_ROWS; ++k) s += red[k][tid];
-            if (c0 + tid < cols) st_coherent(part + ((int64_t)z * RS) * cols + c0 + tid, s);
+            if (c0 + tid < cols) {
+                float* dst = part + ((int64_t)z * RS) * cols + c0 + tid;
+                if (counters) st_coherent(dst, s);
+                else *dst = s;
+            }
         }
     }
-    if (!counters) return;   // reduced by sum_splits_kernel
+    if (!counters) return;   // reduced by the consumer (rows kernel) or sum_splits_kernel
     // The last split of this column tile to arrive sums the partials in split order
     // (deterministic) into out[row][c] (= or +=); nobody waits for anybody.
     __shared__ int s_last;
@@ -491,9 +543,22 @@ __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __
     const int a = (int)blockIdx.y * 4 + (threadIdx.x >> 6);
     if (o >= out) return;
     float gn = 0.f;
+    // split sums in split order; loads issued 8 at a time
+    auto split_sum = [&](const float* p0) {
+        float acc = 0.f;
+        int sp = 0;
+        for (; sp + 8 <= S; sp += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = p0[(int64_t)(sp + k) * stride];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc += v[k];
+        }
+        for (; sp < S; ++sp) acc += p0[(int64_t)sp * stride];
+        return acc;
+    };
     if (dora) {
-        float g = 0.f;
-        for (int sp = 0; sp < S; ++sp) g += part[(int64_t)sp * stride + o];
+        const float g = split_sum(part + o);
         const float n2 = nsq[o], sq = sqrtf(n2);
         gn = -0.5f * g * mag[o] / (n2 * sq);
         if (a == 0) {
@@ -502,8 +567,7 @@ __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __
         }
     }
     if (a >= r) return;
-    float v = 0.f;
-    for (int sp = 0; sp < S; ++sp) v += part[(int64_t)sp * stride + (int64_t)(a + 1) * out + o];
+    float v = split_sum(part + (int64_t)(a + 1) * out + o);
     if (dora) {
         v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
         Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
