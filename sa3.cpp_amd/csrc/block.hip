@@ -166,8 +166,13 @@ __global__ __launch_bounds__(kThreads) void colred_kernel(int mode, const float*
             p0 *= -s * (1.0f - s);
         }
         float* o = part + (((int64_t)b * nch + ch) * 2) * dim;
-        st_coherent(o + c, p0);
-        st_coherent(o + dim + c, p1);
+        if (counters) {   // read back by the last chunk to arrive in this launch
+            st_coherent(o + c, p0);
+            st_coherent(o + dim + c, p1);
+        } else {
+            o[c] = p0;
+            o[dim + c] = p1;
+        }
     }
     if (!counters) return;
     __shared__ int s_last;

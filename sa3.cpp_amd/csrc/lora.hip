@@ -493,10 +493,19 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     }
 }
 
-// token rows per split of a skinny TN reduction over `cols` columns: about 1024 workgroups
+// target workgroup count of a skinny TN reduction (environment SA3K_TN_WGS, for measurement)
+int64_t ctx_tn_wgs() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("SA3K_TN_WGS");
+        return e ? std::max<int64_t>(64, std::atoll(e)) : (int64_t)512;   // measured best of 256..2048
+    }();
+    return v;
+}
+
+// token rows per split of a skinny TN reduction over `cols` columns: about ctx_tn_wgs() workgroups
 int64_t tn_rows_per(int64_t cols, int64_t N) {
     const int64_t tiles = ceil_div(cols, TN_COLS);
-    return std::max<int64_t>(TN_ROWS, ceil_div(ceil_div(N * tiles, 1024), TN_ROWS) * TN_ROWS);
+    return std::max<int64_t>(TN_ROWS, ceil_div(ceil_div(N * tiles, ctx_tn_wgs()), TN_ROWS) * TN_ROWS);
 }
 
 // partial sums of the column reductions: one buffer per context, shared by every linear (used
