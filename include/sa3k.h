@@ -91,6 +91,10 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
  *                 fill the chip (default 2: 64x128 tiles; 0: the default tile, split over K)
  *   "gemm_nt_store" 1: GEMM outputs are written with non-temporal stores (default 1)
+ *   "side_stream" 1: independent kernels of a backward pass (column reductions, attention dQ, the
+ *                 context K/V projection) run on a second stream of the context beside the main
+ *                 one, joined before the call returns (default 1; off while gemm_fixup is not 0
+ *                 or a profiler scope is open)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg and
  * gemm_small, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
@@ -408,10 +412,12 @@ SA3K_API int sa3k_dit_accumulate(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t,
  * accumulated sample count, global clip, AdamW (sa3k_adamw_clip), then clear the accumulator. */
 SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw_params* hp, int step,
                                   double* grad_norm_out);
-/* Replay the accumulate step as a captured HIP graph (default on; environment SA3K_DIT_GRAPH=0
- * turns it off): the first call runs eagerly, the next captures the step for its input pointers
+/* Replay the accumulate step as a captured HIP graph (default off; environment SA3K_DIT_GRAPH=1
+ * turns it on): the first call runs eagerly, the next captures the step for its input pointers
  * (with and without the adapter refresh), later calls with the same pointers replay it. Results
- * are identical to the eager path. While profiling is on the step always runs eagerly. */
+ * are identical to the eager path. While profiling is on the step always runs eagerly. The eager
+ * step is as fast on MI355X (launches hide behind the kernels) and runs the second stream's kernels
+ * (option "side_stream") concurrently, which a replay of the graph does not. */
 SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
 /* Forward only: velocity [B][T][io] (dit_forward, src/dit.h:327-338). */
 SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* t, const float* cross,

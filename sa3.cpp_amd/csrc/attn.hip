@@ -599,6 +599,15 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
         a.qsplit = (int)std::min<int64_t>({(int64_t)nqb, 16, ceil_div(512, (int64_t)nkb * BH)});
         if (a.qsplit > 1) a.part = gemm_workspace_bytes(ctx, (size_t)a.qsplit * 3 * plane * sizeof(float));
     }
+    // dQ (second stream) and dK/dV (main stream) only share inputs: they run side by side
+    const bool side = side_usable(ctx);
+    if (side) side_fork(ctx);
+    {
+        OnSide os(ctx, side);
+        KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dq" : "attn_bwd_dq_cross");
+        attn_bwd_dq_kernel<<<dim3((unsigned)ceil_div(Sq, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
+        SA3K_LAUNCHED();
+    }
     {
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dkdv" : "attn_bwd_dkdv_cross");
         attn_bwd_dkdv_kernel<<<dim3((unsigned)nkb, (unsigned)BH, (unsigned)a.qsplit), kThreads, 0, ctx->stream>>>(a);
@@ -608,11 +617,7 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
             SA3K_LAUNCHED();
         }
     }
-    {
-        KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dq" : "attn_bwd_dq_cross");
-        attn_bwd_dq_kernel<<<dim3((unsigned)ceil_div(Sq, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
-        SA3K_LAUNCHED();
-    }
+    if (side) side_join(ctx);   // the callers consume dQ next
 }
 
 }  // namespace sa3k

@@ -366,9 +366,14 @@ void launch(sa3k_ctx* ctx, const char* name, void (*kernel)(KArgs...), dim3 grid
     SA3K_LAUNCHED();
 }
 
-// per-sample column reductions into dssg (deterministic: fixed chunking and summation order)
+// per-sample column reductions into dssg (deterministic: fixed chunking and summation order); they
+// feed nothing else in the block, so they run on the second stream when it is usable (the block
+// backward joins it at its end)
 void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const float* x, const float* rstd,
             const float* gamma, int g_part, int part0) {
+    const bool side = side_usable(ctx);
+    if (side) side_fork(ctx);
+    OnSide os(ctx, side);
     const int chunk = (int)ceil_div(w->S, w->part_chunks);
     const int64_t ctrs = nblk(w->dim) * (int64_t)w->B;
     int* counters = use_fixup(ctx, (int64_t)w->B * w->dim, ctrs) ? ctx->tile_counters : nullptr;
@@ -617,6 +622,9 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         for (int t = 0; t < NT; ++t) dmt[t] = dm ? dm[t] : nullptr;
         const float* mv = w->modv;
         w->dssg = dgcond;   // the column reductions add each of the 6 modulation parts once
+        // work forked to the second stream (column reductions, cross K/V projection backward, dA
+        // partial sums) reads activations and scratch that the next block reuses: join at the end
+        SideDeferScope defer(ctx);
         const int64_t nq = (int64_t)B * H * S;
         // out = x2 + yf * s_f
         launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D)), dout, mv, 5, S, D, N * D, w->dyf);
@@ -638,8 +646,14 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, c.rope_base,
                        {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, w->dkv};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(NC * H)), bk, NC);
+        {   // the context K/V projection (Ctx tokens, small kernels) beside the query projection
+            const bool side = side_usable(ctx);
+            if (side) side_fork(ctx);
+            OnSide os(ctx, side);
+            chk(ctx, sa3k_lin_backward(ctx, b->L[3], SA3K_TYPE_F32, w->ctxf, NC, w->dkv, dcontext, 1, dA[3], dB[3],
+                                       dmt[3]));
+        }
         chk(ctx, sa3k_lin_backward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dqf, w->dhc, 0, dA[2], dB[2], dmt[2]));
-        chk(ctx, sa3k_lin_backward(ctx, b->L[3], SA3K_TYPE_F32, w->ctxf, NC, w->dkv, dcontext, 1, dA[3], dB[3], dmt[3]));
         launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dhc, (const float*)w->x1,
                (const float*)w->rs_c, (const float*)b->cross_g, (const float*)nullptr, 0, S, D, (const float*)w->dx2,
                w->dx1);
@@ -657,6 +671,7 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         colred(ctx, w, 0, w->dh, w->x, w->rs_a, b->pre_g, 0, 0);
         launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dh, (const float*)w->x,
                (const float*)w->rs_a, (const float*)b->pre_g, mv, 0, S, D, (const float*)w->dx1, dx);
+        if (side_usable(ctx)) side_join(ctx);
         w->dssg = nullptr;
     }
 }

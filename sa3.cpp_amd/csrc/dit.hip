@@ -280,8 +280,9 @@ struct sa3k_dit {
     double *loss_part, *loss;
     int loss_chunks = 1;
     // HIP graphs of the accumulate step (index 1: with the adapter prepare, 0: without), keyed by
-    // the input pointers they were captured with
-    bool use_graph = true, warm = false;
+    // the input pointers they were captured with. Off by default: a replay runs the captured
+    // second-stream branches one after another, the eager step runs them beside the main stream.
+    bool use_graph = false, warm = false;
     hipGraphExec_t gexec[2] = {nullptr, nullptr};
     const void* gkey[2][6] = {};
 };

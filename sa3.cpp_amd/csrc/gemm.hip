@@ -39,18 +39,22 @@ struct KParams {
 
 // split-K workspace owned by the context (grows on demand; kernels on one stream use it in turn)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes) {
-    if (bytes > ctx->gemm_ws_bytes) {
+    // one workspace per stream: work on the second stream runs beside the main stream's
+    const bool side = ctx->stream == ctx->side_stream;
+    void*& ws = side ? ctx->gemm_ws_side : ctx->gemm_ws;
+    size_t& have = side ? ctx->gemm_ws_side_bytes : ctx->gemm_ws_bytes;
+    if (bytes > have) {
         SA3K_REQUIRE(!ctx->capturing, "the split-K workspace cannot grow while a graph is being captured");
-        if (ctx->gemm_ws) {
+        if (ws) {
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
-            SA3K_HIP(hipFree(ctx->gemm_ws));
-            ctx->gemm_ws = nullptr;
-            ctx->gemm_ws_bytes = 0;
+            SA3K_HIP(hipFree(ws));
+            ws = nullptr;
+            have = 0;
         }
-        SA3K_HIP(hipMalloc(&ctx->gemm_ws, bytes));
-        ctx->gemm_ws_bytes = bytes;
+        SA3K_HIP(hipMalloc(&ws, bytes));
+        have = bytes;
     }
-    return static_cast<float*>(ctx->gemm_ws);
+    return static_cast<float*>(ws);
 }
 
 namespace {

@@ -511,18 +511,21 @@ int64_t tn_rows_per(int64_t cols, int64_t N) {
 // partial sums of the column reductions: one buffer per context, shared by every linear (used
 // in turn on the context stream); it grows outside graph capture only
 float* reduce_workspace(sa3k_ctx* ctx, size_t bytes) {
-    if (bytes > ctx->red_ws_bytes) {
+    const bool side = ctx->stream == ctx->side_stream;   // one workspace per stream
+    void*& ws = side ? ctx->red_ws_side : ctx->red_ws;
+    size_t& have = side ? ctx->red_ws_side_bytes : ctx->red_ws_bytes;
+    if (bytes > have) {
         SA3K_REQUIRE(!ctx->capturing, "the reduction workspace cannot grow while a graph is being captured");
-        if (ctx->red_ws) {
+        if (ws) {
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
-            SA3K_HIP(hipFree(ctx->red_ws));
-            ctx->red_ws = nullptr;
-            ctx->red_ws_bytes = 0;
+            SA3K_HIP(hipFree(ws));
+            ws = nullptr;
+            have = 0;
         }
-        SA3K_HIP(hipMalloc(&ctx->red_ws, bytes));
-        ctx->red_ws_bytes = bytes;
+        SA3K_HIP(hipMalloc(&ws, bytes));
+        have = bytes;
     }
-    return static_cast<float*>(ctx->red_ws);
+    return static_cast<float*>(ws);
 }
 
 // y[j] (+)= sum_s part[s][j], j < n (fixed summation order: deterministic)
@@ -789,6 +792,64 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         }
         gemm_run(ctx, g, "lin_bwd_dub");
     }
+    // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
+    //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
+    //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
+    //     reduction the partials kernel adds into dA itself and therefore runs after step 3.
+    int64_t x_rows_per = 0;
+    int x_S = 0;
+    float* x_part = nullptr;
+    int* x_counters = nullptr;
+    if constexpr (sizeof(CT) == 2) {
+        x_rows_per = tn_rows_per(in, N);
+        x_S = (int)ceil_div(N, x_rows_per);
+        x_counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
+    } else {
+        x_S = choose_splits(in, N);
+        x_rows_per = ceil_div(N, x_S);
+    }
+    auto x_partials = [&] {
+        if constexpr (sizeof(CT) == 2) {
+            x_part = reduce_workspace(ctx, (size_t)x_S * 32 * in * sizeof(float));
+            const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)x_S);
+            KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);
+            if (x_src == SRC_F32)
+                skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr,
+                    x_part, N, in, x_rows_per, dA, 1, x_counters);
+            else
+                skinny_tn_kernel<TN_X, bf16><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const bf16*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr,
+                    x_part, N, in, x_rows_per, dA, 1, x_counters);
+            SA3K_LAUNCHED();
+        } else {
+            x_part = reduce_workspace(ctx, (size_t)x_S * R * in * sizeof(float));
+            const dim3 grid((unsigned)ceil_div(in, kThreads), (unsigned)x_S);
+            KernelScope ks(ctx, "lin_bwd_colred_x");
+            if (x_src == SRC_F32)
+                colred_x_kernel<float, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), x_part, N, in, r, x_rows_per);
+            else
+                colred_x_kernel<bf16, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const bf16*>(X), static_cast<const CT*>(L->sdUB), x_part, N, in, r, x_rows_per);
+            SA3K_LAUNCHED();
+        }
+    };
+    auto x_sum = [&] {
+        if (x_counters) return;   // summed in-kernel
+        KernelScope ks(ctx, "lin_bwd_reduce");
+        const int64_t stride = (sizeof(CT) == 2 ? (int64_t)32 : (int64_t)R) * in;
+        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
+            x_part, stride, x_S, (int64_t)r * in, dA, 1);
+        SA3K_LAUNCHED();
+    };
+    const bool early = x_counters == nullptr;
+    const bool side = early && side_usable(ctx);
+    if (early) {
+        if (side) side_fork(ctx);   // sdUB and X are ready
+        OnSide os(ctx, side);
+        x_partials();
+    }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
     //    of the same GEMM (they share the W^T tiles)
     const WOp wt = weight_operand(W, bf, true);
@@ -813,50 +874,16 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.C = dA; g.ldc = in; g.accumulate = 1;
         gemm_run(ctx, g, "lin_bwd_dora_da");
     }
-    // 4. dA += sdUB^T X
-    if constexpr (sizeof(CT) == 2) {
-        const int64_t rows_per = tn_rows_per(in, N);
-        const int S = (int)ceil_div(N, rows_per);
-        float* part = reduce_workspace(ctx, (size_t)S * 32 * in * sizeof(float));
-        int* counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
-        const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)S);
+    // 4b. the partial sums into dA, after step 3
+    if (early) {
+        if (side) side_fork(ctx);   // the dX GEMM has added its dA rows
         {
-            KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);
-            if (x_src == SRC_F32)
-                skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
-                    N, in, rows_per, dA, 1, counters);
-            else
-                skinny_tn_kernel<TN_X, bf16><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const bf16*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr, part,
-                    N, in, rows_per, dA, 1, counters);
-            SA3K_LAUNCHED();
+            OnSide os(ctx, side);
+            x_sum();
         }
-        if (!counters) {
-            KernelScope ks(ctx, "lin_bwd_reduce");
-            sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
-                part, (int64_t)32 * in, S, (int64_t)r * in, dA, 1);
-            SA3K_LAUNCHED();
-        }
+        if (side) side_join_unless_deferred(ctx);
     } else {
-        const int S = choose_splits(in, N);
-        const int64_t rows_per = ceil_div(N, S);
-        float* part = reduce_workspace(ctx, (size_t)S * R * in * sizeof(float));
-        dim3 grid((unsigned)ceil_div(in, kThreads), (unsigned)S);
-        {
-            KernelScope ks(ctx, "lin_bwd_colred_x");
-            if (x_src == SRC_F32)
-                colred_x_kernel<float, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), part, N, in, r, rows_per);
-            else
-                colred_x_kernel<bf16, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const bf16*>(X), static_cast<const CT*>(L->sdUB), part, N, in, r, rows_per);
-            SA3K_LAUNCHED();
-        }
-        KernelScope ks(ctx, "lin_bwd_reduce");
-        sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
-            part, (int64_t)R * in, S, (int64_t)r * in, dA, 1);
-        SA3K_LAUNCHED();
+        x_partials();
     }
 }
 

@@ -66,6 +66,10 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
                        std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
         // Default-priority stream (non-blocking w.r.t. the null stream).
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        ctx->main_stream = ctx->stream;
+        SA3K_HIP(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking));
+        for (hipEvent_t& e : ctx->side_ev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
@@ -96,11 +100,16 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
 SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
-    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->main_stream) (void)hipStreamSynchronize(ctx->main_stream);
+    if (ctx->side_stream) (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->adamw_partials) (void)hipFree(ctx->adamw_partials);
     if (ctx->adamw_result) (void)hipFree(ctx->adamw_result);
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->red_ws) (void)hipFree(ctx->red_ws);
+    if (ctx->gemm_ws_side) (void)hipFree(ctx->gemm_ws_side);
+    if (ctx->red_ws_side) (void)hipFree(ctx->red_ws_side);
+    for (hipEvent_t e : ctx->side_ev)
+        if (e) (void)hipEventDestroy(e);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
     for (const ProfRecord& r : ctx->prof_pending) {
@@ -110,7 +119,8 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     for (hipEvent_t e : ctx->prof_pool) (void)hipEventDestroy(e);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
-    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+    if (ctx->main_stream) (void)hipStreamDestroy(ctx->main_stream);
     delete ctx;
 }
 
@@ -173,7 +183,10 @@ SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
 }
 
 SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
-    return sa3k_guard(ctx, "sa3k_sync", [&] { SA3K_HIP(hipStreamSynchronize(ctx->stream)); });
+    return sa3k_guard(ctx, "sa3k_sync", [&] {
+        SA3K_HIP(hipStreamSynchronize(ctx->side_stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->main_stream));
+    });
 }
 
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
@@ -186,6 +199,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_cfg") ctx->gemm_cfg = value;
         else if (n == "gemm_small") ctx->gemm_small = value;
         else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
+        else if (n == "side_stream") ctx->use_side = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

@@ -27,9 +27,19 @@ struct ProfTotal {
     double work = 0.0;
 };
 
+constexpr int kSideEvents = 64;
+
 struct sa3k_ctx {
     int device = 0;
+    // The stream launches go to: the context's main stream, or, while side work is being enqueued
+    // (OnSide below), its second stream. Both have the default priority.
     hipStream_t stream = nullptr;
+    hipStream_t main_stream = nullptr;
+    hipStream_t side_stream = nullptr;
+    hipEvent_t side_ev[kSideEvents] = {};   // fork/join events, reused round-robin
+    int side_ev_i = 0;
+    int use_side = 1;                      // run independent chains on the second stream
+    int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
     std::string last_error;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     bool prof_on = false;
@@ -50,6 +60,10 @@ struct sa3k_ctx {
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
     size_t red_ws_bytes = 0;
+    void* gemm_ws_side = nullptr;        // the same two workspaces for work on the second stream
+    size_t gemm_ws_side_bytes = 0;
+    void* red_ws_side = nullptr;
+    size_t red_ws_side_bytes = 0;
     int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch):
                                           // 0 never, 1 always, 2 for small outputs only
     int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
@@ -126,6 +140,56 @@ private:
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- a second stream for independent chains of work (e.g. a column reduction beside the GEMM
+// that does not need it). Used only while launches go to the main stream, outside profiling
+// (per-kernel timing stays serial) and without in-kernel split reductions (their tile counters are
+// shared). Every function that forks joins before it returns, so no side work outlives a call.
+inline bool side_usable(const sa3k_ctx* c) {
+    return c->use_side && c->side_stream && !c->prof_on && c->gemm_fixup == 0 && c->stream == c->main_stream;
+}
+inline hipEvent_t side_event(sa3k_ctx* c) {
+    hipEvent_t e = c->side_ev[c->side_ev_i];
+    c->side_ev_i = (c->side_ev_i + 1) % kSideEvents;
+    return e;
+}
+// the second stream waits for everything enqueued on the main stream so far
+inline void side_fork(sa3k_ctx* c) {
+    hipEvent_t e = side_event(c);
+    SA3K_HIP(hipEventRecord(e, c->main_stream));
+    SA3K_HIP(hipStreamWaitEvent(c->side_stream, e, 0));
+}
+// the main stream waits for everything enqueued on the second stream so far
+inline void side_join(sa3k_ctx* c) {
+    hipEvent_t e = side_event(c);
+    SA3K_HIP(hipEventRecord(e, c->side_stream));
+    SA3K_HIP(hipStreamWaitEvent(c->main_stream, e, 0));
+}
+// A caller that joins the second stream itself at its end (see SideDeferScope) lets the functions
+// it calls leave their side work running; otherwise every forking function joins before returning.
+inline void side_join_unless_deferred(sa3k_ctx* c) {
+    if (c->side_defer == 0) side_join(c);
+}
+struct SideDeferScope {
+    sa3k_ctx* c;
+    explicit SideDeferScope(sa3k_ctx* ctx) : c(ctx) { ++c->side_defer; }
+    ~SideDeferScope() { --c->side_defer; }
+    SideDeferScope(const SideDeferScope&) = delete;
+    SideDeferScope& operator=(const SideDeferScope&) = delete;
+};
+// launches inside the scope go to the second stream (when `on`)
+struct OnSide {
+    sa3k_ctx* c;
+    bool on;
+    OnSide(sa3k_ctx* ctx, bool enable) : c(ctx), on(enable) {
+        if (on) c->stream = c->side_stream;
+    }
+    ~OnSide() {
+        if (on) c->stream = c->main_stream;
+    }
+    OnSide(const OnSide&) = delete;
+    OnSide& operator=(const OnSide&) = delete;
+};
 
 // capacity of sa3k_ctx::tile_counters (tiles of one split-K / split-reduction launch)
 constexpr int kMaxFixupTiles = 8192;

@@ -167,6 +167,31 @@ def test_dit_graph_replays_match_eager(ctx):
             d.destroy()
 
 
+def test_dit_side_stream_matches_one_stream(ctx):
+    # the backward kernels forked to the context's second stream give the one-stream results bit for
+    # bit, over two updates (adapter refresh and AdamW in between)
+    cfg = dict(CFG, window=5)
+    tensors, adapters, inputs = db.random_dit(46, cfg, "full")
+    res = []
+    try:
+        for side in (0, 1):
+            ctx.set_option("side_stream", side)
+            d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
+            up, _ = upload_inputs(ctx, inputs)
+            out = []
+            for step in (1, 2):
+                loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+                out += [loss, d.arena(1).numpy()]
+                d.apply_adamw(HP, step)
+            out.append(d.arena(0).numpy())
+            res.append(out)
+            d.destroy()
+    finally:
+        ctx.set_option("side_stream", 1)
+    for a, b in zip(res[0], res[1]):
+        assert np.array_equal(a, b), "second stream changes the results"
+
+
 def test_dit_in_kernel_reductions_match_separate_launches(ctx):
     # every split reduction done by the last arriving workgroup (GEMM split-K, the column
     # reductions, the modulation gradients) gives the separate-launch results bit for bit
