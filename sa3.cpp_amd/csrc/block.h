@@ -34,6 +34,8 @@ struct sa3k_block_ws {
     float *dyf, *dg, *dF, *dfin, *dx2, *doc, *dqf, *dkv, *dhc, *dx1, *dy, *dob, *dqkv, *dh;
     sa3k::bf16* dOh; float* dn; float *dq1, *dk1, *dq2, *dk2, *dv;
     float* dssg; float* part; int part_chunks;
+    // RoPE cos/sin table of positions 0..S-1 for (rope_tab_dims, rope_tab_base); 0: not built yet
+    float* rope_tab; int rope_tab_dims = 0; float rope_tab_base = 0.f;
     std::vector<void*> allocs;
 };
 

@@ -47,15 +47,6 @@ T* dalloc(size_t n) {
     return static_cast<T*>(p);
 }
 
-__device__ inline float block_sum(float v, float* sh) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float t = sh[0] + sh[1] + sh[2] + sh[3];
-    __syncthreads();
-    return t;
-}
-
 __device__ inline float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
 
 // ---------------------------------------------------------------- modulation vector
@@ -66,50 +57,135 @@ __global__ void modv_kernel(const float* __restrict__ ssg, const float* __restri
     if (i < n) modv[i] = ssg[i % per] + gcond[i];
 }
 
-// ---------------------------------------------------------------- rms norm (+ modulation)
-// h = x * rstd * gamma [* (1 + sc) + sh]; one block per token row
-__global__ __launch_bounds__(kThreads) void norm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                            const float* __restrict__ modv, int sc_part, int S,
-                                                            int dim, float eps, bf16* __restrict__ h,
-                                                            float* __restrict__ rstd) {
-    __shared__ float sh[4];
-    const int64_t n = blockIdx.x;
-    const float* xr = x + n * dim;
+// ---------------------------------------------------------------- row kernels
+// One wave per token row; lane l keeps the columns 4 (l + 64 k), k < V, of the row in registers as
+// float4 (dim % 4 == 0, dim <= 256 V), so every row is read from memory once.
+typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+
+__device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ inline void st4(float* p, const float4& v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ inline void st4(bf16* p, const float4& v) {
+    const bf16x4 b = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
+    *reinterpret_cast<bf16x4*>(p) = b;
+}
+__device__ inline float dot4(const float4& a, const float4& b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+__device__ inline float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+// apply f to the four components
+template <class F>
+__device__ inline float4 map4(const float4& a, const float4& b, F f) {
+    return make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+}
+
+// Residual + rms norm (+ modulation), one wave per row:
+//   xr = x + y * sigmoid(1 - g_b)  (g_part >= 0)  |  x + y  (g_part < 0)  |  x  (y null);  xo = xr
+//   h  = xr * rstd * gamma [* (1 + sc) + sh]  (sc_part >= 0: modulation parts sc_part, sc_part + 1)
+template <int V>
+__global__ __launch_bounds__(kThreads) void resnorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                                                               int g_part, float* __restrict__ xo,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ modv, int sc_part, int S,
+                                                               int dim, int rows, float eps, bf16* __restrict__ h,
+                                                               float* __restrict__ rstd) {
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int64_t base = (int64_t)row * dim;
+    const float* mv = modv ? modv + (int64_t)(row / S) * 6 * dim : nullptr;
+    float4 v[V];
     float ss = 0.f;
-    for (int c = threadIdx.x; c < dim; c += kThreads) ss += xr[c] * xr[c];
-    ss = block_sum(ss, sh);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < dim) v[k] = ld4(x + base + c);
+    }
+    if (y) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const int c = 4 * (lane + 64 * k);
+            if (c >= dim) continue;
+            const float4 yv = ld4(y + base + c);
+            if (g_part >= 0) {
+                const float4 g = ld4(mv + g_part * dim + c);
+                v[k] = make_float4(v[k].x + yv.x * sigmoidf_(1.0f - g.x), v[k].y + yv.y * sigmoidf_(1.0f - g.y),
+                                   v[k].z + yv.z * sigmoidf_(1.0f - g.z), v[k].w + yv.w * sigmoidf_(1.0f - g.w));
+            } else {
+                v[k] = map4(v[k], yv, [](float a, float b) { return a + b; });
+            }
+            st4(xo + base + c, v[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) ss += dot4(v[k], v[k]);
+    ss = wave_sum(ss);
     const float r = 1.0f / sqrtf(ss / dim + eps);
-    if (threadIdx.x == 0) rstd[n] = r;
-    const float* mv = modv ? modv + (n / S) * 6 * dim : nullptr;
-    for (int c = threadIdx.x; c < dim; c += kThreads) {
-        float v = xr[c] * r * gamma[c];
-        if (mv) v = v * (1.0f + mv[sc_part * dim + c]) + mv[(sc_part + 1) * dim + c];
-        h[n * dim + c] = (bf16)v;
+    if (lane == 0) rstd[row] = r;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        if (c >= dim) continue;
+        float4 o = map4(v[k], ld4(gamma + c), [r](float a, float g) { return a * r * g; });
+        if (sc_part >= 0) {
+            o = map4(o, ld4(mv + sc_part * dim + c), [](float a, float s) { return a * (1.0f + s); });
+            o = map4(o, ld4(mv + (sc_part + 1) * dim + c), [](float a, float s) { return a + s; });
+        }
+        st4(h + base + c, o);
     }
 }
 
-// dx = dres + rstd * dn * gamma - rstd^3 * x * <dn gamma, x> / dim, dn = dh * (1 + sc) (or dh);
-// dres is the residual branch's gradient
+// rms norm backward, one wave per row:
+//   dn = dh * (1 + sc) (sc_part >= 0) or dh;  dx = dres + rstd * dn * gamma - rstd^3 * x * <dn gamma, x> / dim
+//   dgated = dx * sigmoid(1 - g_b) when g_part >= 0 (the gradient of the gated branch that produced x)
+// dres is the residual branch's gradient.
+template <int V>
 __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ x,
-                                                            const float* __restrict__ rstd, const float* __restrict__ gamma,
+                                                            const float* __restrict__ rstd,
+                                                            const float* __restrict__ gamma,
                                                             const float* __restrict__ modv, int sc_part, int S, int dim,
-                                                            const float* __restrict__ dres, float* __restrict__ dx) {
-    __shared__ float sh[4];
-    const int64_t n = blockIdx.x;
-    const float* xr = x + n * dim;
-    const float* dr = dh + n * dim;
-    const float* mv = modv ? modv + (n / S) * 6 * dim + sc_part * dim : nullptr;
-    const float r = rstd[n];
+                                                            int rows, const float* __restrict__ dres,
+                                                            float* __restrict__ dx, int g_part,
+                                                            float* __restrict__ dgated) {
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int64_t base = (int64_t)row * dim;
+    const float* mv = modv ? modv + (int64_t)(row / S) * 6 * dim : nullptr;
+    const float r = rstd[row];
+    float4 dg[V], xv[V];
     float dot = 0.f;
-    for (int c = threadIdx.x; c < dim; c += kThreads) {
-        const float dn = mv ? dr[c] * (1.0f + mv[c]) : dr[c];
-        dot += dn * gamma[c] * xr[c];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        dg[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[k] = dg[k];
+        if (c < dim) {
+            dg[k] = ld4(dh + base + c);
+            xv[k] = ld4(x + base + c);
+        }
     }
-    dot = block_sum(dot, sh);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        if (c >= dim) continue;
+        if (sc_part >= 0) dg[k] = map4(dg[k], ld4(mv + sc_part * dim + c), [](float d, float s) { return d * (1.0f + s); });
+        dg[k] = map4(dg[k], ld4(gamma + c), [](float d, float g) { return d * g; });
+        dot += dot4(dg[k], xv[k]);
+    }
+    dot = wave_sum(dot);
     const float k3 = r * r * r * dot / dim;
-    for (int c = threadIdx.x; c < dim; c += kThreads) {
-        const float dn = mv ? dr[c] * (1.0f + mv[c]) : dr[c];
-        dx[n * dim + c] = dres[n * dim + c] + (r * dn * gamma[c] - k3 * xr[c]);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        if (c >= dim) continue;
+        const float4 t = map4(dg[k], xv[k], [r, k3](float d, float xx) { return r * d - k3 * xx; });
+        const float4 o = map4(ld4(dres + base + c), t, [](float a, float b) { return a + b; });
+        st4(dx + base + c, o);
+        if (g_part >= 0)
+            st4(dgated + base + c, map4(o, ld4(mv + g_part * dim + c),
+                                        [](float d, float g) { return d * sigmoidf_(1.0f - g); }));
     }
 }
 
@@ -205,56 +281,72 @@ __global__ __launch_bounds__(kThreads) void colred_sum_kernel(const float* __res
     if (two) dssg[((int64_t)b * 6 + part0 + 1) * dim + c] += s1;
 }
 
-// ---------------------------------------------------------------- gate + residual, add, swiglu
-// out = x + y * sigmoid(1 - g_b)
+// ---------------------------------------------------------------- gate, swiglu (4 elements per thread)
+// out = x + y * sigmoid(1 - g_b); n4 = rows * dim / 4 (< 2^31)
 __global__ void gate_res_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ modv,
-                                int g_part, int S, int dim, int64_t n, float* __restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int64_t row = i / dim;
-    const int c = (int)(i - row * dim);
-    const float g = modv[((row / S) * 6 + g_part) * dim + c];
-    out[i] = x[i] + y[i] * sigmoidf_(1.0f - g);
+                                int g_part, int S, int dim, int n4, float* __restrict__ out) {
+    const int i4 = blockIdx.x * kThreads + threadIdx.x;
+    if (i4 >= n4) return;
+    const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)dim, c = e - row * (unsigned)dim;
+    const float4 g = ld4(modv + ((int64_t)(row / (unsigned)S) * 6 + g_part) * dim + c);
+    const float4 xv = ld4(x + e), yv = ld4(y + e);
+    st4(out + e, make_float4(xv.x + yv.x * sigmoidf_(1.0f - g.x), xv.y + yv.y * sigmoidf_(1.0f - g.y),
+                             xv.z + yv.z * sigmoidf_(1.0f - g.z), xv.w + yv.w * sigmoidf_(1.0f - g.w)));
 }
 
-// dy = dout * sigmoid(1 - g_b)
+// dy = dout * sigmoid(1 - g_b); n4 = rows * dim / 4 (< 2^31)
 __global__ void gate_bwd_kernel(const float* __restrict__ dout, const float* __restrict__ modv, int g_part, int S, int dim,
-                                int64_t n, float* __restrict__ dy) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int64_t row = i / dim;
-    const int c = (int)(i - row * dim);
-    dy[i] = dout[i] * sigmoidf_(1.0f - modv[((row / S) * 6 + g_part) * dim + c]);
+                                int n4, float* __restrict__ dy) {
+    const int i4 = blockIdx.x * kThreads + threadIdx.x;
+    if (i4 >= n4) return;
+    const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)dim, c = e - row * (unsigned)dim;
+    const float4 g = ld4(modv + ((int64_t)(row / (unsigned)S) * 6 + g_part) * dim + c);
+    st4(dy + e, map4(ld4(dout + e), g, [](float d, float gg) { return d * sigmoidf_(1.0f - gg); }));
 }
 
-__global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t n, float* __restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i < n) out[i] = a[i] + b[i];
+// g[n][c] = F[n][c] * silu(F[n][I + c]); n4 = rows * I / 4 (< 2^31)
+__global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int n4, bf16* __restrict__ g) {
+    const int i4 = blockIdx.x * kThreads + threadIdx.x;
+    if (i4 >= n4) return;
+    const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
+    const float* f = F + (int64_t)row * 2 * I + c;
+    st4(g + e, map4(ld4(f), ld4(f + I), [](float val, float glu) { return val * glu * sigmoidf_(glu); }));
 }
 
-// g[n][c] = F[n][c] * silu(F[n][I + c])
-__global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int64_t n, bf16* __restrict__ g) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int64_t row = i / I;
-    const int c = (int)(i - row * I);
-    const float val = F[row * 2 * I + c], glu = F[row * 2 * I + I + c];
-    g[i] = (bf16)(val * glu * sigmoidf_(glu));
-}
-
-__global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __restrict__ F, int I, int64_t n,
+__global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __restrict__ F, int I, int n4,
                                   float* __restrict__ dF) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int64_t row = i / I;
-    const int c = (int)(i - row * I);
-    const float val = F[row * 2 * I + c], glu = F[row * 2 * I + I + c];
-    const float sg = sigmoidf_(glu), d = dg[i];
-    dF[row * 2 * I + c] = d * glu * sg;
-    dF[row * 2 * I + I + c] = d * val * (sg + glu * sg * (1.0f - sg));
+    const int i4 = blockIdx.x * kThreads + threadIdx.x;
+    if (i4 >= n4) return;
+    const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
+    const int64_t o = (int64_t)row * 2 * I + c;
+    const float4 val = ld4(F + o), glu = ld4(F + o + I), d = ld4(dg + e);
+    float dv[4], dgl[4];
+    const float vs[4] = {val.x, val.y, val.z, val.w}, gs[4] = {glu.x, glu.y, glu.z, glu.w}, ds[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float sg = sigmoidf_(gs[u]);
+        dv[u] = ds[u] * gs[u] * sg;
+        dgl[u] = ds[u] * vs[u] * (sg + gs[u] * sg * (1.0f - sg));
+    }
+    st4(dF + o, make_float4(dv[0], dv[1], dv[2], dv[3]));
+    st4(dF + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]));
 }
 
 // ---------------------------------------------------------------- q/k-norm + RoPE prep
+// RoPE table of one sequence length: tab[t][i] = cos(theta), tab[t][half + i] = sin(theta),
+// theta = t * base^(-2i/rope), i < half = rope/2 (pairs (i, i + half) of NEOX rotation)
+__global__ void rope_table_kernel(int S, int rope, float base, float* __restrict__ tab) {
+    const int half = rope >> 1;
+    const int idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= S * half) return;
+    const int t = idx / half, i = idx - t * half;
+    const float th = (float)t * powf(base, -2.0f * (float)i / (float)rope);
+    float sn, cs;
+    sincosf(th, &sn, &cs);
+    tab[t * rope + i] = cs;
+    tab[t * rope + half + i] = sn;
+}
+
 struct PrepPart {
     bf16* out;            // [B*H][Sx][64]
     const float* gamma;   // [64]; null: plain copy (v)
@@ -263,45 +355,61 @@ struct PrepPart {
 struct PrepArgs {
     const float* in;      // [B*Sx][parts*dim]
     int parts, Sx, H, dim, rope_dims;
-    float base, eps;
+    float eps;
+    const float* tab;     // RoPE table [Sx][rope_dims] (parts with rope only)
     PrepPart p[5];
     float* rstd;          // [B*Sx][H][parts]
 };
 
-// rotate pairs (i, i + rope/2), i < rope/2, by theta_i = pos * base^(-2i/rope); lanes = dims
-__device__ inline float rope_lane(float y, int d, int rope, float pos, float base, bool inverse) {
+// 16 lanes per (row, head), lane j holding dims 4j..4j+3 (rope_dims % 8 == 0, so a rotation pair
+// (i, i + half) is the same component of lanes j and j + half/4). Rotates y in place; lanes past
+// rope_dims keep y. sign -1: the inverse rotation.
+__device__ inline void rope4(float4& y, int d0, int rope, const float* __restrict__ row_tab, float sign) {
     const int half = rope >> 1;
-    const int i = d < half ? d : d - half;
-    const float partner = __shfl(y, d < half ? d + half : d - half, 64);
-    if (d >= rope) return y;
-    const float th = pos * powf(base, -2.0f * (float)i / (float)rope);
-    float sn, cs;
-    sincosf(th, &sn, &cs);
-    if (inverse) sn = -sn;
-    return d < half ? y * cs - partner * sn : partner * sn + y * cs;
+    const bool rot = d0 < rope, first = d0 < half;
+    const int lane = threadIdx.x & 63;
+    const int src = rot ? (first ? lane + (half >> 2) : lane - (half >> 2)) : lane;
+    const float4 p = make_float4(__shfl(y.x, src, 64), __shfl(y.y, src, 64), __shfl(y.z, src, 64), __shfl(y.w, src, 64));
+    if (!rot) return;
+    const int i = first ? d0 : d0 - half;
+    const float4 cs = ld4(row_tab + i), sn = ld4(row_tab + half + i);
+    const float ys[4] = {y.x, y.y, y.z, y.w}, ps[4] = {p.x, p.y, p.z, p.w};
+    const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sign * sn.x, sign * sn.y, sign * sn.z, sign * sn.w};
+    float o[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = first ? ys[u] * cc[u] - ps[u] * ss[u] : ps[u] * ss[u] + ys[u] * cc[u];
+    y = make_float4(o[0], o[1], o[2], o[3]);
 }
 
-// one wave per (row, head)
-__global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int64_t rows) {
-    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const int d = threadIdx.x & 63;
-    if (item >= rows * a.H) return;
-    const int64_t row = item / a.H;
-    const int h = (int)(item % a.H);
-    const int b = (int)(row / a.Sx), t = (int)(row % a.Sx);
-    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d;
-    for (int k = 0; k < a.parts; ++k) {
-        const float x = a.in[row * a.parts * a.dim + (int64_t)k * a.dim + h * HD + d];
-        float y = x;
+__device__ inline float group16_sum(float v) {
+    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
+    return v;
+}
+
+// items = rows * H (< 2^31); every part's loads are issued before any is used
+__global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int items) {
+    const int item = blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    if (item >= items) return;   // whole 16-lane groups leave together
+    const int d0 = 4 * (threadIdx.x & 15);
+    const int row = item / a.H, h = item - row * a.H;
+    const int b = row / a.Sx, t = row - b * a.Sx;
+    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
+    const float* src = a.in + (int64_t)row * a.parts * a.dim + h * HD + d0;
+    float4 x[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+        if (k < a.parts) x[k] = ld4(src + (int64_t)k * a.dim);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        if (k >= a.parts) break;
+        float4 y = x[k];
         if (a.p[k].gamma) {
-            float ss = x * x;
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-            const float r = 1.0f / sqrtf(ss / HD + a.eps);
-            if (d == 0) a.rstd[(row * a.H + h) * a.parts + k] = r;
-            y = x * r * a.p[k].gamma[d];
-            if (a.p[k].rope) y = rope_lane(y, d, a.rope_dims, (float)t, a.base, false);
+            const float r = 1.0f / sqrtf(group16_sum(dot4(y, y)) / HD + a.eps);
+            if (d0 == 0) a.rstd[(int64_t)item * a.parts + k] = r;
+            y = map4(y, ld4(a.p[k].gamma + d0), [r](float v, float g) { return v * r * g; });
+            if (a.p[k].rope) rope4(y, d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, 1.0f);
         }
-        a.p[k].out[ho] = (bf16)y;
+        st4(a.p[k].out + ho, y);
     }
 }
 
@@ -313,32 +421,41 @@ struct PrepBwdPart {
 struct PrepBwdArgs {
     const float* in;      // forward input [B*Sx][parts*dim] (pre-norm values)
     int parts, Sx, H, dim, rope_dims;
-    float base;
+    const float* tab;
     PrepBwdPart p[5];
     const float* rstd;
     float* din;           // [B*Sx][parts*dim]
 };
 
-__global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int64_t rows) {
-    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const int d = threadIdx.x & 63;
-    if (item >= rows * a.H) return;
-    const int64_t row = item / a.H;
-    const int h = (int)(item % a.H);
-    const int b = (int)(row / a.Sx), t = (int)(row % a.Sx);
-    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d;
-    for (int k = 0; k < a.parts; ++k) {
-        float g = a.p[k].dy[ho];
-        const int64_t xi = row * a.parts * a.dim + (int64_t)k * a.dim + h * HD + d;
+__global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int items) {
+    const int item = blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    if (item >= items) return;
+    const int d0 = 4 * (threadIdx.x & 15);
+    const int row = item / a.H, h = item - row * a.H;
+    const int b = row / a.Sx, t = row - b * a.Sx;
+    const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
+    const int64_t xo = (int64_t)row * a.parts * a.dim + h * HD + d0;
+    float4 g[5], x[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        if (k >= a.parts) break;
+        g[k] = ld4(a.p[k].dy + ho);
+        if (a.p[k].gamma) x[k] = ld4(a.in + xo + (int64_t)k * a.dim);
+    }
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        if (k >= a.parts) break;
+        float4 gv = g[k];
         if (a.p[k].gamma) {
-            if (a.p[k].rope) g = rope_lane(g, d, a.rope_dims, (float)t, a.base, true);
-            const float x = a.in[xi], gm = a.p[k].gamma[d];
-            const float r = a.rstd[(row * a.H + h) * a.parts + k];
-            float dot = g * gm * x;
-            for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
-            g = r * g * gm - r * r * r * x * dot / HD;
+            if (a.p[k].rope) rope4(gv, d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, -1.0f);
+            const float4 gm = ld4(a.p[k].gamma + d0);
+            const float r = a.rstd[(int64_t)item * a.parts + k];
+            const float dot = group16_sum(dot4(map4(gv, gm, [](float u, float w) { return u * w; }), x[k]));
+            const float c3 = r * r * r * dot / HD;
+            const float4 gg = map4(gv, gm, [r](float u, float w) { return r * u * w; });
+            gv = map4(gg, x[k], [c3](float u, float xx) { return u - c3 * xx; });
         }
-        a.din[xi] = g;
+        st4(a.din + xo + (int64_t)k * a.dim, gv);
     }
 }
 
@@ -357,6 +474,24 @@ void target_dims(const sa3k_block_config& c, int t, int64_t& in, int64_t& out) {
 
 inline unsigned nblk(int64_t n) { return (unsigned)ceil_div(n, kThreads); }
 inline unsigned nwave_blk(int64_t items) { return (unsigned)ceil_div(items, kThreads / 64); }
+inline unsigned ngroup16_blk(int64_t items) { return (unsigned)ceil_div(items, kThreads / 16); }
+
+// the row kernels keep ceil(dim / 256) float4 per lane
+constexpr int kMaxRowV = 8;
+template <class F>
+void with_row_v(int dim, F&& f) {
+    switch (ceil_div(dim, 256)) {
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 3: f(std::integral_constant<int, 3>{}); break;
+        case 4: f(std::integral_constant<int, 4>{}); break;
+        case 5: f(std::integral_constant<int, 5>{}); break;
+        case 6: f(std::integral_constant<int, 6>{}); break;
+        case 7: f(std::integral_constant<int, 7>{}); break;
+        case 8: f(std::integral_constant<int, 8>{}); break;
+        default: sa3k_throw(SA3K_ERR_UNSUPPORTED, "dim above 2048");
+    }
+}
 
 // launch a kernel of this file on the context stream under a profiler scope
 template <class... KArgs, class... Args>
@@ -405,8 +540,11 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
                         const float* const* bias, const float* const* vecs, int on_device, int rank,
                         int64_t max_tokens, int64_t max_ctx) {
     SA3K_REQUIRE(cfg.head_dim == HD && cfg.dim == cfg.heads * HD, "dim must be heads * 64");
-    SA3K_REQUIRE(cfg.rope_dims > 0 && cfg.rope_dims <= HD && cfg.rope_dims % 2 == 0, "rope_dims");
-    SA3K_REQUIRE(cfg.inner > 0 && cfg.window >= 0, "inner / window");
+    // the q/k prep keeps 4 dims per lane: rotation pairs (i, i + rope/2) then sit in the same
+    // component of two lanes
+    SA3K_REQUIRE(cfg.rope_dims > 0 && cfg.rope_dims <= HD && cfg.rope_dims % 8 == 0, "rope_dims must be a multiple of 8");
+    SA3K_REQUIRE(cfg.dim <= 256 * kMaxRowV, "dim above 2048");
+    SA3K_REQUIRE(cfg.inner > 0 && cfg.inner % 4 == 0 && cfg.window >= 0, "inner / window");
     SA3K_REQUIRE(max_tokens > 0 && max_ctx > 0, "token budgets must be positive");
     sa3k_block* b = new sa3k_block();
     b->cfg = cfg;
@@ -474,6 +612,7 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
         w->oc = B16(N * D); w->co1 = B16(BHS); w->co2 = B16(BHS); w->cl1 = F32(BHq); w->cl2 = F32(BHq);
         w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D); w->F = F32(N * 2 * I);
         w->g = B16(N * I); w->yf = F32(N * D);
+        w->rope_tab = F32((size_t)S * HD);
         w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
         if (share) {
             w->yc = share->yc;
@@ -571,41 +710,52 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         w->x = x;
         w->ctxf = context;
         const float* mv = w->modv;
+        // element-wise kernels index with 32-bit ints
+        SA3K_REQUIRE(N * 2 * I < ((int64_t)1 << 31) && N * H * 5 < ((int64_t)1 << 31), "too many tokens");
+        if (w->rope_tab_dims != c.rope_dims || w->rope_tab_base != c.rope_base) {
+            launch(ctx, "blk_rope_table", rope_table_kernel, dim3(nblk((int64_t)S * c.rope_dims / 2)), S, c.rope_dims,
+                   c.rope_base, w->rope_tab);
+            w->rope_tab_dims = c.rope_dims;
+            w->rope_tab_base = c.rope_base;
+        }
+        // xo = x [+ y [* sigmoid(1 - g)]], h = rms_norm(xo) * gamma [* (1 + sc) + sh]
+        auto resnorm = [&](const float* xin, const float* yin, int g_part, float* xo, const float* gamma, int sc_part,
+                           bf16* h, float* rs) {
+            with_row_v(D, [&](auto v) {
+                launch(ctx, "blk_norm_fwd", resnorm_fwd_kernel<decltype(v)::value>, dim3(nwave_blk(N)), xin, yin,
+                       g_part, xo, gamma, mv, sc_part, S, D, (int)N, c.norm_eps, h, rs);
+            });
+        };
         launch(ctx, "blk_modv", modv_kernel, dim3(nblk((int64_t)B * 6 * D)), (const float*)b->ssg, gcond,
                (int64_t)B * 6 * D, 6 * D, w->modv);
         // self attention
-        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), x, (const float*)b->pre_g, mv, 0, S, D,
-               c.norm_eps, w->h, w->rs_a);
+        resnorm(x, nullptr, -1, nullptr, b->pre_g, 0, w->h, w->rs_a);
         chk(ctx, sa3k_lin_forward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, nullptr, w->qkv));
-        PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+        PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.qk_eps, w->rope_tab,
                     {{w->q1, b->sq_g, 1}, {w->k1, b->sk_g, 1}, {w->v, nullptr, 0}, {w->q2, b->sq_g, 1}, {w->k2, b->sk_g, 1}},
                     w->rq};
-        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(N * H)), ps, N);
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), ps, (int)(N * H));
         attn_forward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, B, H, S, S, c.window, scale, w->o, w->o1, w->o2, w->l1, w->l2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, nullptr, w->y));
-        launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D)), x, (const float*)w->y, mv, 2, S, D, N * D, w->x1);
-        // cross attention
-        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), (const float*)w->x1, (const float*)b->cross_g,
-               (const float*)nullptr, 0, S, D, c.norm_eps, w->hc, w->rs_c);
+        // cross attention: x1 = x + y * sigmoid(1 - g_a), hc = rms_norm(x1) * cross_g
+        resnorm(x, w->y, 2, w->x1, b->cross_g, -1, w->hc, w->rs_c);
         chk(ctx, sa3k_lin_forward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, nullptr, w->qf));
         chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
-        PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+        PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.qk_eps, nullptr,
                     {{w->cq1, b->cq_g, 0}, {w->cq2, b->cq_g, 0}, {}, {}, {}}, w->rcq};
-        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(N * H)), pq, N);
-        PrepArgs pk{w->kv, 3, Ctx, H, D, c.rope_dims, c.rope_base, c.qk_eps,
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), pq, (int)(N * H));
+        PrepArgs pk{w->kv, 3, Ctx, H, D, c.rope_dims, c.qk_eps, nullptr,
                     {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck};
-        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(nwave_blk(NC * H)), pk, NC);
+        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(NC * H)), pk, (int)(NC * H));
         attn_forward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, B, H, S, Ctx, 0, scale, w->oc, w->co1, w->co2, w->cl1, w->cl2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, nullptr, w->yc));
-        launch(ctx, "blk_add", add_kernel, dim3(nblk(N * D)), (const float*)w->x1, (const float*)w->yc, N * D, w->x2);
-        // feed-forward
-        launch(ctx, "blk_norm_fwd", norm_fwd_kernel, dim3((unsigned)N), (const float*)w->x2, (const float*)b->ff_g, mv, 3,
-               S, D, c.norm_eps, w->fin, w->rs_f);
+        // feed-forward: x2 = x1 + yc, fin = rms_norm(x2) * ff_g * (1 + sc_f) + sh_f
+        resnorm(w->x1, w->yc, -1, w->x2, b->ff_g, 3, w->fin, w->rs_f);
         chk(ctx, sa3k_lin_forward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, b->bias[5], w->F));
-        launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I)), (const float*)w->F, I, N * I, w->g);
+        launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->F, I, (int)(N * I / 4), w->g);
         chk(ctx, sa3k_lin_forward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, b->bias[6], w->yf));
-        launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D)), (const float*)w->x2, (const float*)w->yf, mv, 5, S, D,
-               N * D, out);
+        launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D / 4)), (const float*)w->x2, (const float*)w->yf, mv, 5,
+               S, D, (int)(N * D / 4), out);
     }
 }
 
@@ -626,26 +776,33 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         // partial sums) reads activations and scratch that the next block reuses: join at the end
         SideDeferScope defer(ctx);
         const int64_t nq = (int64_t)B * H * S;
+        // dx = dres + norm backward (dh); dgated = dx * sigmoid(1 - g) when g_part >= 0
+        auto norm_bwd = [&](const float* dh, const float* xin, const float* rs, const float* gamma, int sc_part,
+                            const float* dres, float* dxo, int g_part, float* dgated) {
+            with_row_v(D, [&](auto v) {
+                launch(ctx, "blk_norm_bwd", norm_bwd_kernel<decltype(v)::value>, dim3(nwave_blk(N)), dh, xin, rs, gamma,
+                       mv, sc_part, S, D, (int)N, dres, dxo, g_part, dgated);
+            });
+        };
         // out = x2 + yf * s_f
-        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D)), dout, mv, 5, S, D, N * D, w->dyf);
+        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D / 4)), dout, mv, 5, S, D, (int)(N * D / 4), w->dyf);
         colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
         chk(ctx, sa3k_lin_backward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dyf, w->dg, 0, dA[6], dB[6], dmt[6]));
-        launch(ctx, "blk_swiglu", swiglu_bwd_kernel, dim3(nblk(N * I)), (const float*)w->dg, (const float*)w->F, I,
-               N * I, w->dF);
+        launch(ctx, "blk_swiglu", swiglu_bwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->dg, (const float*)w->F, I,
+               (int)(N * I / 4), w->dF);
         chk(ctx, sa3k_lin_backward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dF, w->dfin, 0, dA[5], dB[5], dmt[5]));
         colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
-        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dfin, (const float*)w->x2,
-               (const float*)w->rs_f, (const float*)b->ff_g, mv, 3, S, D, dout, w->dx2);
+        norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, nullptr);
         // x2 = x1 + yc
         chk(ctx, sa3k_lin_backward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->dx2, w->doc, 0, dA[4], dB[4], dmt[4]));
         attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
-        PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, c.rope_base,
+        PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, nullptr,
                        {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, w->dqf};
-        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(N * H)), bq, N);
-        PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, c.rope_base,
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bq, (int)(N * H));
+        PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
                        {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, w->dkv};
-        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(NC * H)), bk, NC);
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(NC * H)), bk, (int)(NC * H));
         {   // the context K/V projection (Ctx tokens, small kernels) beside the query projection
             const bool side = side_usable(ctx);
             if (side) side_fork(ctx);
@@ -654,23 +811,19 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                                        dmt[3]));
         }
         chk(ctx, sa3k_lin_backward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dqf, w->dhc, 0, dA[2], dB[2], dmt[2]));
-        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dhc, (const float*)w->x1,
-               (const float*)w->rs_c, (const float*)b->cross_g, (const float*)nullptr, 0, S, D, (const float*)w->dx2,
-               w->dx1);
-        // x1 = x + y * s_a
-        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D)), (const float*)w->dx1, mv, 2, S, D, N * D, w->dy);
+        // x1 = x + y * s_a: dy = dx1 * s_a comes out of the same pass
+        norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, w->dy);
         colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
         chk(ctx, sa3k_lin_backward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dy, w->dob, 0, dA[1], dB[1], dmt[1]));
         attn_backward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, w->o1, w->o2, w->l1, w->l2, w->dob, B, H, S, S, c.window,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
-        PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, c.rope_base,
+        PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, w->rope_tab,
                        {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
                        w->rq, w->dqkv};
-        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(nwave_blk(N * H)), bs, N);
+        launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bs, (int)(N * H));
         chk(ctx, sa3k_lin_backward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, w->dqkv, w->dh, 0, dA[0], dB[0], dmt[0]));
         colred(ctx, w, 0, w->dh, w->x, w->rs_a, b->pre_g, 0, 0);
-        launch(ctx, "blk_norm_bwd", norm_bwd_kernel, dim3((unsigned)N), (const float*)w->dh, (const float*)w->x,
-               (const float*)w->rs_a, (const float*)b->pre_g, mv, 0, S, D, (const float*)w->dx1, dx);
+        norm_bwd(w->dh, w->x, w->rs_a, b->pre_g, 0, w->dx1, dx, -1, nullptr);
         if (side_usable(ctx)) side_join(ctx);
         w->dssg = nullptr;
     }
