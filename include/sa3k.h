@@ -91,12 +91,18 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
  *                 fill the chip (default 2: 64x128 tiles; 0: the default tile, split over K)
  *   "gemm_nt_store" 1: GEMM outputs are written with non-temporal stores (default 1)
+ *   "gemm_skinny" 1: bf16 products with at most 32 output columns and a plain epilogue (the rank
+ *                 products s X A^T and s dU B) run on a kernel that splits K across the waves of
+ *                 one workgroup instead of over workgroups (default 1)
+ *   "gemm_big"    bf16 products on 256 x 256 tiles (8 waves, one workgroup per CU): 0 never,
+ *                 1 where they fill the chip about as evenly as 128 x 128 tiles (default), 2 always
+ *                 (when operand extents and output alignment allow)
  *   "side_stream" 1: independent kernels of a backward pass (column reductions, attention dQ, the
  *                 context K/V projection) run on a second stream of the context beside the main
  *                 one, joined before the call returns (default 1; off while gemm_fixup is not 0
  *                 or a profiler scope is open)
- * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg and
- * gemm_small, which change the f32 summation order. Not to be changed while a graph is being captured. */
+ * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
+ * gemm_small, gemm_skinny and gemm_big, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

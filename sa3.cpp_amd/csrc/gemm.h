@@ -78,6 +78,9 @@ struct GemmDesc {
 // any other source type the kernel that decodes it on its way into LDS (gemm.hip).
 void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name);
 void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d);
+// bf16 products with at most 32 output columns and a plain epilogue (gemm_skinny.hip)
+bool gemm_skinny_ok(const sa3k_ctx* ctx, const GemmDesc& d);
+void gemm_run_skinny(sa3k_ctx* ctx, const GemmDesc& d);
 // split-K partial-sum workspace owned by the context (grows on demand)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);
 

@@ -491,6 +491,11 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     SA3K_REQUIRE(d.Mx >= 0, "negative extra rows");
     SA3K_REQUIRE(d.Mx == 0 || (d.Ax && (d.Cx || d.Cbx) && al16(d.Ax) && (d.K2 == 0 || (d.A2x && al16(d.A2x)))),
                  "GEMM extra rows need Ax, Cx or Cbx (and A2x with a second segment)");
+    if (gemm_skinny_ok(ctx, d)) {
+        KernelScope ks(ctx, prof_name);
+        gemm_run_skinny(ctx, d);
+        return;
+    }
     const int ct_src = bf ? SRC_BF16 : SRC_F32;
     if (d.a_src == ct_src && d.b_src == ct_src && ctx->gemm_dma) {
         SA3K_REQUIRE((d.ldb * (bf ? 2 : 4)) % 16 == 0 && (d.Mx == 0 || (d.ldax * (bf ? 2 : 4)) % 16 == 0),

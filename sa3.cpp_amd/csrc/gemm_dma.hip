@@ -510,6 +510,200 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     }
 }
 
+// 256 x 256 tiles for bf16 operands, one workgroup of 8 waves per CU (128 KiB of LDS in two
+// stages). Per K tile of 64 a CU then moves 64 KiB from L2 for 8.4 MFLOP, half the bytes per flop
+// of two 128 x 128 workgroups (which need the CU's whole 64 B/clk vector-memory path at the MFMA
+// peak), and its waves own 64 x 128 blocks (2 x 4 MFMA blocks of 32 x 32), which cut LDS reads per
+// flop by a quarter against 64 x 64.
+//
+// Every operand load goes through a buffer descriptor with a 32-bit per-lane offset (no 64-bit
+// pointers, which would not leave room for the 128 accumulator registers): host-checked extents
+// below 4 GiB. A (q, wave) DMA slot covers 8 consecutive rows, so with M % 8 == 0 its rows all come
+// from A or all from the extra rows Ax, a choice made per slot on the scalar unit. Rows past the
+// end are clamped to the last valid row of the same source. The rank segment (K2 <= 64) has its
+// own descriptors; its chunks past K2 get an offset beyond the descriptor extent, which loads zeros.
+struct BigSeg {
+    uint32_t off[4];
+};
+
+__global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
+    constexpr int BM = 256, BN = 256, NW = 8, NT = 512, WMW = 4;
+    constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW);   // 64 x 128
+    constexpr int FM = WTM / 32, FN = WTN / 32;             // 2 x 4 MFMA blocks
+    constexpr int NA = BM * 8 / NT, NB = BN * 8 / NT;       // 4 + 4 DMA chunks per thread and tile
+    constexpr int LPT = NA + NB;
+    constexpr int STAGES = 2;
+    constexpr int STAGE_BYTES = (BM + BN) * kRow;           // 64 KiB
+    constexpr int EROW = BN + 8;
+    constexpr int ER = 64;                                  // epilogue rows staged per pass
+    static_assert(ER * EROW * 4 <= STAGES * STAGE_BYTES, "epilogue staging does not fit");
+    __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE_BYTES];
+
+    const int64_t Mt = p.M + p.Mx;
+    const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    const int nwg = gridDim.x;
+    const int bid = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+    if (bid >= tiles_m * tiles_n) return;
+    constexpr int G = 8;
+    const int per_group = G * tiles_n;
+    const int group = bid / per_group;
+    const int first_m = group * G;
+    const int gsz = min(tiles_m - first_m, G);
+    const int in_g = bid - group * per_group;
+    const int tm = first_m + in_g % gsz, tn = in_g / gsz;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = (wave % WMW) * WTM, wn0 = (wave / WMW) * WTN;
+
+    const int KT = (int)(p.K / 64);
+    const int z = blockIdx.y;
+    const int kt0 = z * p.kps;
+    const int Tm = max(0, min(KT, kt0 + p.kps) - kt0);
+    const bool ext = p.K2 > 0 && z == (int)gridDim.y - 1;
+    const int T = Tm + (ext ? 1 : 0);
+    const uint32_t k0b = (uint32_t)kt0 * 128u;   // byte offset of the split's first K tile
+
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
+    const u32x4 rs_a = buffer_rsrc(p.A, p.a_bytes), rs_ax = buffer_rsrc(p.Ax, p.ax_bytes);
+    const u32x4 rs_b = buffer_rsrc(p.B, p.b_bytes);
+    // the rank segment's descriptors: [rows][ld2] bf16, K2 valid columns
+    const uint32_t a2_bytes = p.K2 > 0 ? (uint32_t)(((p.M - 1) * p.lda2 + p.K2) * 2) : 0u;
+    const uint32_t a2x_bytes = p.K2 > 0 && p.Mx > 0 ? (uint32_t)(((p.Mx - 1) * p.lda2x + p.K2) * 2) : 0u;
+    const uint32_t b2_bytes = p.K2 > 0 ? (uint32_t)(((p.N - 1) * p.ldb2 + p.K2) * 2) : 0u;
+    const u32x4 rs_a2 = buffer_rsrc(p.A2, a2_bytes), rs_a2x = buffer_rsrc(p.A2x, a2x_bytes);
+    const u32x4 rs_b2 = buffer_rsrc(p.B2, b2_bytes);
+    constexpr uint32_t kNoData = 0xFFFFFFF0u;   // past every extent: loads zeros
+
+    // per-thread DMA sources: slot s = q * NT + tid of the A (B) region, row s / 8, chunk kc. The 8
+    // rows of slot (q, wave) start at m0 + 64 q + 8 wave, so their source is decided from
+    // wave-uniform values (M % 8 == 0 when there are extra rows).
+    BigSeg ao, a2o, bo, b2o;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+        const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
+        int64_t gm = m0 + row;
+        if (gm >= Mt) gm = Mt - 1;
+        const bool x = gm >= p.M;
+        const int64_t lr = x ? gm - p.M : gm;
+        ao.off[q] = (uint32_t)((lr * (x ? p.ldax : p.lda) + kc * 8) * 2);
+        a2o.off[q] = kc * 8 < p.K2 ? (uint32_t)((lr * (x ? p.lda2x : p.lda2) + kc * 8) * 2) : kNoData;
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
+        int64_t gn = n0 + row;
+        if (gn >= p.N) gn = p.N - 1;
+        bo.off[q] = (uint32_t)((gn * p.ldb + kc * 8) * 2);
+        b2o.off[q] = kc * 8 < p.K2 ? (uint32_t)((gn * p.ldb2 + kc * 8) * 2) : kNoData;
+    }
+    auto slot_x = [&](int q) {   // wave-uniform: slot q's rows are extra rows
+        const int64_t r0 = min(m0 + 64 * q + 8 * wave, Mt - 1);
+        return r0 >= p.M;
+    };
+
+    auto issue = [&](auto s_c, int t) {
+        constexpr uint32_t so_lds = (uint32_t)((decltype(s_c)::value % STAGES) * STAGE_BYTES);
+        const uint32_t dst0 = lds_base + wave * 64 * 16 + so_lds;
+        if (t < Tm) {
+            const uint32_t so = k0b + (uint32_t)t * 128u;
+#pragma unroll
+            for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_ax : rs_a, ao.off[q], so, dst0 + q * NT * 16);
+#pragma unroll
+            for (int q = 0; q < NB; ++q) dma16b(rs_b, bo.off[q], so, dst0 + BM * kRow + q * NT * 16);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_a2x : rs_a2, a2o.off[q], 0u, dst0 + q * NT * 16);
+#pragma unroll
+            for (int q = 0; q < NB; ++q) dma16b(rs_b2, b2o.off[q], 0u, dst0 + BM * kRow + q * NT * 16);
+        }
+    };
+
+    typedef float accv __attribute__((__vector_size__(16 * sizeof(float))));
+    accv acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    auto frag = [&](const char* base, int row, int kc) { return base + row * kRow + ((kc ^ swz(row)) << 4); };
+    // two K steps of fragments at a time: the reads of steps 2-3 go out while steps 0-1 compute
+    auto compute = [&](const char* As) {
+        const char* Bs = As + BM * kRow;
+        const int r = lane & 31, g = lane >> 5;
+        bf16x8 af[2][FM], bfr[2][FN];
+        auto load = [&](int ks, int slot) {
+            const int kc = 2 * ks + g;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[slot][i] = *reinterpret_cast<const bf16x8*>(frag(As, wm0 + 32 * i + r, kc));
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bfr[slot][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
+        };
+        auto mma = [&](int slot) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+        };
+        load(0, 0);
+        load(1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(0);
+        load(2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(1);
+        load(3, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(0);
+        mma(1);
+    };
+
+    if (T > 0) issue(IC<0>{}, 0);
+    for (int t0 = 0; t0 < T; t0 += STAGES) {
+        static_for<STAGES>([&](auto s) {
+            const int t = t0 + decltype(s)::value;
+            if (t >= T) return;
+            wait_vmcnt<0>();   // tile t landed (the only DMA group in flight)
+            __asm__ volatile("s_barrier" ::: "memory");   // visible to all waves; tile t-1 consumed
+            if (t + 1 < T) issue(IC<decltype(s)::value + 1>{}, t + 1);
+            compute(lds + decltype(s)::value * STAGE_BYTES);
+        });
+    }
+
+    // staged epilogue only (the host routes outputs that do not allow 16-byte stores elsewhere)
+    auto out_row = [&](int v) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); };
+    float* st = reinterpret_cast<float*>(lds);
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < BM; rb += ER) {
+        if (wm0 == rb) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int c = wn0 + 32 * j + (lane & 31);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) st[(32 * i + out_row(v)) * EROW + c] = acc[i][j][v];
+            }
+        }
+        __syncthreads();
+        constexpr int CPR = BN / 4;
+        for (int e = tid; e < ER * CPR; e += NT) {
+            const int r = e / CPR, c = (e % CPR) * 4;
+            const int64_t m = m0 + rb + r, n = n0 + c;
+            if (m >= Mt || n >= p.N) continue;
+            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + c);
+            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.N + m * p.N + n) = a;
+            else epilogue_vec4(p, m, n, a);
+        }
+        if (rb + ER < BM) __syncthreads();
+    }
+}
+
 // Sum of the split partials in split order, then the epilogue: 4 consecutive columns per thread
 // when the outputs allow 16-byte accesses, one element otherwise.
 __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, int splits) {
@@ -592,8 +786,78 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     }
 }
 
+// Whether gemm_big_kernel can take this bf16 product: every extent addressable by a buffer
+// descriptor, extra rows starting on an 8-row boundary, no in-kernel split reduction.
+bool big_ok(const sa3k_ctx* ctx, const DmaParams& p) {
+    auto extent = [&](int64_t rows, int64_t ld, int64_t k) -> int64_t { return rows > 0 ? ((rows - 1) * ld + k) * 2 : 0; };
+    const int64_t lim = (int64_t)1 << 31;
+    if (ctx->gemm_fixup != 0) return false;
+    if (extent(p.M, p.lda, p.K) >= lim || extent(p.N, p.ldb, p.K) >= lim) return false;
+    if (p.Mx > 0 && (p.M % 8 != 0 || extent(p.Mx, p.ldax, p.K) >= lim)) return false;
+    if (p.K2 > 0 && (extent(p.M, p.lda2, p.K2) >= lim || extent(p.N, p.ldb2, p.K2) >= lim ||
+                     (p.Mx > 0 && extent(p.Mx, p.lda2x, p.K2) >= lim)))
+        return false;
+    return true;
+}
+
+// outputs allow the staged epilogue's 4-column stores: rows and vectors 16-byte (f32) / 8-byte
+// (bf16) aligned
+bool vec_epi_ok(const DmaParams& p) {
+    auto ok = [](const void* q, int64_t ld, int align) {
+        return q == nullptr || (ld % 4 == 0 && (uintptr_t)q % (uintptr_t)align == 0);
+    };
+    return p.N % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) && ok(p.Cb, p.ldcb, 8) &&
+           ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) && ok(p.bias, 4, 16);
+}
+
+void launch_big(sa3k_ctx* ctx, DmaParams p) {
+    constexpr int BM = 256, BN = 256;
+    const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.N, BN);
+    const int64_t grid = ceil_div(tiles, 8) * 8;
+    const int KT = (int)(p.K / 64);
+    int splits = 1;
+    const int64_t slots = 256;   // one workgroup per CU (128 KiB of LDS)
+    if (ctx->gemm_split && tiles < slots && KT >= 8)
+        splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
+    p.kps = std::max(1, (KT + splits - 1) / splits);
+    splits = std::max(1, (KT + p.kps - 1) / p.kps);
+    p.ws = nullptr;
+    p.counters = nullptr;
+    auto extent = [&](int64_t rows, int64_t ld) -> uint32_t { return rows > 0 ? (uint32_t)(((rows - 1) * ld + p.K) * 2) : 0u; };
+    p.a_bytes = extent(p.M, p.lda);
+    p.ax_bytes = extent(p.Mx, p.ldax);
+    p.b_bytes = extent(p.N, p.ldb);
+    p.nt_store = ctx->gemm_nt_store;
+    p.vec_epi = 1;
+    if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
+    {
+        KernelScope ks(ctx, "gemm_big<256,256,bf16>", 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
+        gemm_big_kernel<<<dim3((unsigned)grid, (unsigned)splits), 512, 0, ctx->stream>>>(p);
+        SA3K_LAUNCHED();
+    }
+    if (splits > 1) {
+        KernelScope ks(ctx, "gemm_splitk_reduce");
+        const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.N / 4 : (p.M + p.Mx) * p.N;
+        gemm_dma_splitk_reduce<<<(unsigned)ceil_div(items, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
+        SA3K_LAUNCHED();
+    }
+}
+
 template <bool BF16>
 void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
+    if constexpr (BF16) {
+        if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.N > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
+            // 256 x 256 tiles (one per CU) where they fill the chip about as evenly as 128 x 128 tiles
+            // (two per CU) do and need no split over K; measured on MI355X at 2176 rows: FFN
+            // up-projection 2176 x 12288 x 1536 107 vs 111 us, 2176 x 6144 x 1536 52 vs 56 us,
+            // 8192^3 877 vs 1057 us; the 2176 x 7680 QKV projection (270 tiles) 98 vs 62 us.
+            const int64_t Mt = p.M + p.Mx;
+            const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.N, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+            const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
+            const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
+            if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return launch_big(ctx, p);
+        }
+    }
     const int64_t Mt = p.M + p.Mx;
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, BF16>(ctx, p);
     if (p.N <= 32) return launch_dma<128, 32, 4, 4, BF16>(ctx, p);

@@ -79,11 +79,15 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_SMALL")) ctx->gemm_small = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_NT")) ctx->gemm_nt_store = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_SKINNY")) ctx->gemm_skinny = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_BIG")) ctx->gemm_big = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
         SA3K_HIP(hipMalloc(&ctx->tile_counters, sizeof(int) * kMaxFixupTiles));
         SA3K_HIP(hipMemsetAsync(ctx->tile_counters, 0, sizeof(int) * kMaxFixupTiles, ctx->stream));
+        SA3K_HIP(hipMalloc(&ctx->skinny_counters, sizeof(int) * 2 * kSkinnyMaxTiles));
+        SA3K_HIP(hipMemsetAsync(ctx->skinny_counters, 0, sizeof(int) * 2 * kSkinnyMaxTiles, ctx->stream));
         SA3K_HIP(hipMalloc(&ctx->adamw_partials, sizeof(double) * kAdamwMaxBlocks));
         SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
         SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
@@ -112,6 +116,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
         if (e) (void)hipEventDestroy(e);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
+    if (ctx->skinny_counters) (void)hipFree(ctx->skinny_counters);
     for (const ProfRecord& r : ctx->prof_pending) {
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);
@@ -199,6 +204,8 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_cfg") ctx->gemm_cfg = value;
         else if (n == "gemm_small") ctx->gemm_small = value;
         else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
+        else if (n == "gemm_skinny") ctx->gemm_skinny = value != 0;
+        else if (n == "gemm_big") ctx->gemm_big = value;
         else if (n == "side_stream") ctx->use_side = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });

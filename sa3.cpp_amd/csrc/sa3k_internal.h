@@ -28,6 +28,8 @@ struct ProfTotal {
 };
 
 constexpr int kSideEvents = 64;
+// row tiles (32 rows each) of one skinny-product launch that may split K over workgroups
+constexpr int kSkinnyMaxTiles = 8192;
 
 struct sa3k_ctx {
     int device = 0;
@@ -56,6 +58,8 @@ struct sa3k_ctx {
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
     int gemm_cfg = 0;                     // DMA kernel tile configuration
     int gemm_nt_store = 1;                // GEMM outputs written with non-temporal stores
+    int gemm_skinny = 1;                  // products with <= 32 output columns on the skinny kernel
+    int gemm_big = 1;                     // 256 x 256 bf16 tiles: 0 never, 1 where they fill the chip, 2 always
     int gemm_small = 2;                   // tile configuration for small grids (0: the default tile + split-K)
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
@@ -67,6 +71,8 @@ struct sa3k_ctx {
     int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch):
                                           // 0 never, 1 always, 2 for small outputs only
     int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
+    int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
+                                          // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
 };

@@ -7,7 +7,7 @@ f32 compute (v_mfma_f32_16x16x4_f32): reference is the float64 product of the f3
 import numpy as np
 import pytest
 
-from conftest import bf16_bits, bf16_round, oracle, q8_0_split, rel_err, rng, sa3k
+from conftest import bf16_bits, bf16_round, max_rel_err, oracle, q8_0_split, rel_err, rng, sa3k
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +129,52 @@ def test_split_k_fixup_matches_separate_reduction(ctx, M, N, K):
     finally:
         ctx.set_option("gemm_fixup", 0)
     assert np.array_equal(out[0], out[1]) and np.array_equal(out[0], out[2])
+
+
+@pytest.mark.parametrize("M,N,K", [(2176, 32, 1536), (2176, 32, 12288), (2208, 32, 7680), (37, 20, 128),
+                                   (1, 1, 64), (130, 17, 192), (16, 32, 64), (300, 31, 6144)])
+def test_skinny_gemm(ctx, M, N, K):
+    # products with <= 32 output columns (the rank products s X A^T, s dU B) run on the skinny
+    # kernel: f32 accumulation error only, bit-identical on a repeat, and within rounding of the
+    # tiled kernel (gemm_skinny = 0), which sums K in another order
+    r = rng(M * 31 + N * 7 + K)
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    ref = bf16_round(A).astype(np.float64) @ bf16_round(W).astype(np.float64).T
+    args = (bf16_bits(A), bf16_bits(W), M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, sa3k.TYPE_BF16)
+    got = run(ctx, *args)
+    again = run(ctx, *args)
+    try:
+        ctx.set_option("gemm_skinny", 0)
+        tiled = run(ctx, *args)
+    finally:
+        ctx.set_option("gemm_skinny", 1)
+    assert np.array_equal(got, again), "not deterministic"
+    assert rel_err(got, ref) < 1e-5
+    assert rel_err(tiled, ref) < 1e-5
+    assert max_rel_err(got, tiled) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(2176, 12288, 1536), (2176, 6144, 1536), (300, 640, 256), (520, 1000, 192),
+                                   (2176, 1536, 6144)])
+def test_big_tile_gemm(ctx, M, N, K):
+    # 256 x 256 tiles forced (gemm_big = 2): f32 accumulation error only, within rounding of the
+    # 128 x 128 kernel, and bit-identical on a repeat; ragged M and N clamp their loads
+    r = rng(M + 3 * N + K)
+    A = r.normal(0, 1, (M, K)).astype(np.float32)
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    bias = r.normal(0, 1, N).astype(np.float32)
+    cs = r.uniform(0.5, 1.5, N).astype(np.float32)
+    args = (bf16_bits(A), bf16_bits(W), M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, sa3k.TYPE_BF16)
+    ref = (bf16_round(A).astype(np.float64) @ bf16_round(W).astype(np.float64).T) * cs + bias
+    try:
+        ctx.set_option("gemm_big", 2)
+        got = run(ctx, *args, bias=bias, colscale=cs)
+        again = run(ctx, *args, bias=bias, colscale=cs)
+        ctx.set_option("gemm_big", 0)
+        small = run(ctx, *args, bias=bias, colscale=cs)
+    finally:
+        ctx.set_option("gemm_big", 1)
+    assert np.array_equal(got, again), "not deterministic"
+    assert rel_err(got, ref) < 1e-5
+    assert max_rel_err(got, small) < 1e-5

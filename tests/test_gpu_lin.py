@@ -112,6 +112,27 @@ def test_linear_small_shapes(ctx, prec, wt, dora, decode):
             assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
 
 
+@pytest.mark.parametrize("N,in_,out_,r", [(2048, 1536, 6144, 32), (264, 192, 320, 8)])
+def test_dora_linear_big_tiles(ctx, N, in_, out_, r):
+    # bf16 DoRA linear with every eligible GEMM on 256 x 256 tiles (gemm_big = 2): the rank segment
+    # (K2 = r) and the r extra dA rows of the dX GEMM go through the big kernel's descriptors
+    X, dY, W, A, B = make_inputs(4, N, in_, out_, r)
+    Wh = W.astype(np.float16)
+    Wdec = Wh.astype(np.float32)
+    mag = (oracle.row_norms(Wdec) * 1.05).astype(np.float32)
+    try:
+        ctx.set_option("gemm_big", 2)
+        got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16)
+        ctx.set_option("gemm_big", 0)
+        small = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16)
+    finally:
+        ctx.set_option("gemm_big", 1)
+    ref = run_oracle(X, dY, Wdec, A, B, 1.5, True, mag)
+    for k in ("Y", "dX", "dA", "dB", "dm"):
+        assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
+        assert rel_err(got[k], small[k]) < 1e-5, k
+
+
 def test_gradients_accumulate(ctx):
     # dA/dB/dm are accumulators: two identical micro-batches give twice the gradient
     N, in_, out_, r = 64, 128, 256, 16
