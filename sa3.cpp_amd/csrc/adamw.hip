@@ -18,7 +18,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSumBlocks = 512;
+constexpr int kSumBlocks = 1024;
 
 __device__ inline double block_sum_double(double v, double* sh) {
     // wave64 butterfly, then the 4 wave results in a fixed order
@@ -48,14 +48,23 @@ __global__ __launch_bounds__(kThreads) void adamw_sumsq_kernel(const float* __re
     if (VEC) {
         const int64_t n4 = n >> 2;
         const float4* g4 = reinterpret_cast<const float4*>(g);
-        for (int64_t i = tid; i < n4; i += stride) {
-            float4 x = g4[i];
+        auto add = [&](float4 x) {
             if (avg) { x.x = x.x * inv; x.y = x.y * inv; x.z = x.z * inv; x.w = x.w * inv; }
             acc += (double)x.x * x.x;
             acc += (double)x.y * x.y;
             acc += (double)x.z * x.z;
             acc += (double)x.w * x.w;
+        };
+        // four independent 16-byte loads in flight per thread, summed in index order
+        int64_t i = tid;
+        for (; i + 3 * stride < n4; i += 4 * stride) {
+            const float4 a = g4[i], b = g4[i + stride], c = g4[i + 2 * stride], d = g4[i + 3 * stride];
+            add(a);
+            add(b);
+            add(c);
+            add(d);
         }
+        for (; i < n4; i += stride) add(g4[i]);
         for (int64_t i = (n4 << 2) + tid; i < n; i += stride) {
             float x = g[i];
             if (avg) x = x * inv;

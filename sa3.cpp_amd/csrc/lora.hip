@@ -326,6 +326,8 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
 // Q in flight; the kernel is bound by streaming Q once.
 constexpr int TN_DY = 0, TN_X = 1;
 constexpr int TN_COLS = 64, TN_ROWS = 32;
+constexpr int TN_H = 2;                    // 32-token halves per step (each thread loads TN_H token rows)
+constexpr int TN_STEP = TN_ROWS * TN_H;    // tokens per step (one barrier per step)
 constexpr int TN_QLD = 144;   // bytes per token row of the Q tile (128 + 16: the four rows a transposed read touches sit in distinct banks)
 constexpr int TN_PLD = 80;    // bytes per token row of the P tile (64 + 16)
 
@@ -351,14 +353,14 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
                                                              bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
                                                              int64_t cols, int64_t rows_per, float* __restrict__ out,
                                                              int accumulate, int* __restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) char qt[2][TN_ROWS * TN_QLD];
-    __shared__ __attribute__((aligned(16))) char pt[2][TN_ROWS * TN_PLD];
+    __shared__ __attribute__((aligned(16))) char qt[2][TN_STEP * TN_QLD];
+    __shared__ __attribute__((aligned(16))) char pt[2][TN_STEP * TN_PLD];
     __shared__ float red[TN_ROWS][TN_COLS + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t c0 = (int64_t)blockIdx.x * TN_COLS;
     const int z = blockIdx.y;
     const int64_t r0 = (int64_t)z * rows_per, r1 = min(N, r0 + rows_per);
-    const int lrow = tid >> 3;            // token row of this thread's loads within a step
+    const int lrow = tid >> 3;            // token row of this thread's loads within a step half
     const int c8 = (tid & 7) * 8;         // its 8 columns
     const int a4 = (tid & 7) * 4;         // its 4 ranks of the P tile
     const int64_t col = c0 + c8;
@@ -374,75 +376,104 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
 
     // one step's global operands of this thread, loaded ahead of use
     struct Regs {
-        float4 ya, yb;     // dY (DY) or f32 X
-        bf16x8 u;          // U (DY) or bf16 X
-        uint2 pv;          // 4 bf16 of P
+        float4 ya[TN_H], yb[TN_H];   // dY (DY) or f32 X
+        bf16x8 u[TN_H];              // U (DY) or bf16 X
+        uint2 pv[TN_H];              // 4 bf16 of P
     };
+    // Loads through buffer descriptors whose extents end at this split's last token row: rows past
+    // it, absent U (extent 0) and columns past the end (offset beyond every extent) read as zeros
+    // with no branch, so the loads of a step are one straight run the wait counter can track.
+    typedef unsigned tn_v4u __attribute__((ext_vector_type(4)));
+    typedef unsigned tn_v2u __attribute__((ext_vector_type(2)));
+    constexpr uint32_t kOut = 0xFFFFFFF0u;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<QT*>(Q), (short)0, (int)(r1 * cols * (int64_t)sizeof(QT)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(MODE == TN_DY && U ? U : static_cast<const bf16*>(nullptr)), (short)0,
+        (MODE == TN_DY && U) ? (int)(r1 * cols * 2) : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(P), (short)0,
+                                                                        (int)(r1 * r * 2), 0x00020000);
     auto load = [&](int64_t n0, Regs& R) {
-        const int64_t n = n0 + lrow;
-        const bool row_ok = n < r1;
-        R.ya = R.yb = make_float4(0.f, 0.f, 0.f, 0.f);
-        R.u = bf16x8{};
-        R.pv = make_uint2(0, 0);
-        if (row_ok && col_ok) {
+#pragma unroll
+        for (int h = 0; h < TN_H; ++h) {
+            const int64_t n = n0 + lrow + TN_ROWS * h;
+            const uint32_t e = col_ok ? (uint32_t)(n * cols + col) : 0u;   // element offset of the 8 columns
+            const uint32_t pe = a4 < r ? (uint32_t)(n * r + a4) : 0u;
             if constexpr (MODE == TN_DY || sizeof(QT) == 4) {
-                const float4* y4 = reinterpret_cast<const float4*>(Q + n * cols + col);
-                R.ya = y4[0];
-                R.yb = y4[1];
+                const uint32_t off = col_ok ? e * 4u : kOut;
+                R.ya[h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+                R.yb[h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16u, 0, 0));
             }
             if constexpr (MODE == TN_DY) {
-                if (U) R.u = *reinterpret_cast<const bf16x8*>(U + n * cols + col);
+                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? e * 2u : kOut, 0, 0));
             } else if constexpr (sizeof(QT) == 2) {
-                R.u = *reinterpret_cast<const bf16x8*>(Q + n * cols + col);
+                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, col_ok ? e * 2u : kOut, 0, 0));
             }
+            R.pv[h] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, a4 < r ? pe * 2u : kOut, 0, 0));
         }
-        if (row_ok && a4 < r) R.pv = *reinterpret_cast<const uint2*>(P + n * r + a4);
     };
     // LDS tiles of one step (and, DY, dU out + the gd partials)
     auto stage = [&](int64_t n0, const Regs& R, int b) {
-        const int64_t n = n0 + lrow;
-        bf16x8 qv;
-        if constexpr (MODE == TN_DY) {
-            const float y[8] = {R.ya.x, R.ya.y, R.ya.z, R.ya.w, R.yb.x, R.yb.y, R.yb.z, R.yb.w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float q = y[j] * dd[j];
-                qv[j] = (bf16)q;
-                if (U) gd[j] += y[j] * (float)R.u[j];
+        for (int h = 0; h < TN_H; ++h) {
+            const int64_t n = n0 + lrow + TN_ROWS * h;
+            bf16x8 qv;
+            if constexpr (MODE == TN_DY) {
+                const float y[8] = {R.ya[h].x, R.ya[h].y, R.ya[h].z, R.ya[h].w,
+                                    R.yb[h].x, R.yb[h].y, R.yb[h].z, R.yb[h].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float q = y[j] * dd[j];
+                    qv[j] = (bf16)q;
+                    if (U) gd[j] += y[j] * (float)R.u[h][j];
+                }
+                if (n < r1 && col_ok) *reinterpret_cast<bf16x8*>(dU + n * cols + col) = qv;
+            } else if constexpr (sizeof(QT) == 4) {
+                const float y[8] = {R.ya[h].x, R.ya[h].y, R.ya[h].z, R.ya[h].w,
+                                    R.yb[h].x, R.yb[h].y, R.yb[h].z, R.yb[h].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qv[j] = (bf16)y[j];
+            } else {
+                qv = R.u[h];
             }
-            if (n < r1 && col_ok) *reinterpret_cast<bf16x8*>(dU + n * cols + col) = qv;
-        } else if constexpr (sizeof(QT) == 4) {
-            const float y[8] = {R.ya.x, R.ya.y, R.ya.z, R.ya.w, R.yb.x, R.yb.y, R.yb.z, R.yb.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qv[j] = (bf16)y[j];
-        } else {
-            qv = R.u;
+            const int lr = lrow + TN_ROWS * h;
+            *reinterpret_cast<bf16x8*>(qt[b] + lr * TN_QLD + c8 * 2) = qv;
+            *reinterpret_cast<uint2*>(pt[b] + lr * TN_PLD + a4 * 2) = R.pv[h];
         }
-        *reinterpret_cast<bf16x8*>(qt[b] + lrow * TN_QLD + c8 * 2) = qv;
-        *reinterpret_cast<uint2*>(pt[b] + lrow * TN_PLD + a4 * 2) = R.pv;
     };
-    // D[i][j] += sum over the step's 32 tokens: i = column wave*16 + 4g+v, j = rank t*16 + lane%16
+    // D[i][j] += sum over the step's tokens: i = column wave*16 + 4g+v, j = rank t*16 + lane%16
     auto mma = [&](int b) {
-        const bf16x8 af = cat44(tn_ld_tr(qt[b], TN_QLD, 8 * g, wave * 16, lane),
-                                tn_ld_tr(qt[b], TN_QLD, 8 * g + 4, wave * 16, lane));
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const bf16x8 bfr = cat44(tn_ld_tr(pt[b], TN_PLD, 8 * g, t * 16, lane),
-                                     tn_ld_tr(pt[b], TN_PLD, 8 * g + 4, t * 16, lane));
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[t], 0, 0, 0);
+        for (int h = 0; h < TN_H; ++h) {
+            const int k0 = TN_ROWS * h + 8 * g;
+            const bf16x8 af = cat44(tn_ld_tr(qt[b], TN_QLD, k0, wave * 16, lane),
+                                    tn_ld_tr(qt[b], TN_QLD, k0 + 4, wave * 16, lane));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const bf16x8 bfr = cat44(tn_ld_tr(pt[b], TN_PLD, k0, t * 16, lane),
+                                         tn_ld_tr(pt[b], TN_PLD, k0 + 4, t * 16, lane));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[t], 0, 0, 0);
+            }
         }
     };
 
-    Regs cur, nxt;
-    if (r0 < r1) load(r0, cur);
-    int b = 0;
-    for (int64_t n0 = r0; n0 < r1; n0 += TN_ROWS) {
-        if (n0 + TN_ROWS < r1) load(n0 + TN_ROWS, nxt);   // in flight during this step
-        stage(n0, cur, b);
-        __syncthreads();   // step n0 in buffer b; every wave is done with buffer b's previous use
-        mma(b);
-        b ^= 1;
-        cur = nxt;
+    // Two register sets, the loop unrolled by two steps: while step n0 is staged from set A, set B
+    // holds step n0 + TN_STEP in flight, and A is refilled with step n0 + 2 TN_STEP right after its
+    // stage. The loads are issued unconditionally (rows past the split read zeros), so the
+    // compiler's wait before each stage counts only the other set's loads.
+    Regs ra, rb;
+    load(r0, ra);
+    load(r0 + TN_STEP, rb);
+    for (int64_t n0 = r0; n0 < r1; n0 += 2 * TN_STEP) {
+        stage(n0, ra, 0);
+        __syncthreads();   // step n0 in buffer 0; every wave is done with buffer 0's previous use
+        mma(0);
+        load(n0 + 2 * TN_STEP, ra);
+        if (n0 + TN_STEP >= r1) break;
+        stage(n0 + TN_STEP, rb, 1);
+        __syncthreads();
+        mma(1);
+        load(n0 + 3 * TN_STEP, rb);
     }
     // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + lane%16
     constexpr int RS = MODE == TN_DY ? 33 : 32;
@@ -497,15 +528,39 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
 int64_t ctx_tn_wgs() {
     static const int64_t v = [] {
         const char* e = std::getenv("SA3K_TN_WGS");
-        return e ? std::max<int64_t>(64, std::atoll(e)) : (int64_t)512;   // measured best of 256..2048
+        return e ? std::max<int64_t>(64, std::atoll(e)) : (int64_t)0;
     }();
     return v;
 }
 
-// token rows per split of a skinny TN reduction over `cols` columns: about ctx_tn_wgs() workgroups
+// Token rows per split of a skinny TN reduction over `cols` columns. The launch has tiles x splits
+// workgroups of 64 columns, up to 3 resident per CU (160 VGPRs, 37 KiB of LDS). Two of them on one
+// CU overlap each other's memory latency; more share the CU's throughput. So a CU holding w of
+// them takes about rows x max(1, w / 2) token rows of streaming time (8 bytes per element: dY or X,
+// U, the dU store), and the rows kernel then reads splits x 33 x cols partial sums spread over the
+// chip. The split count minimising that cost is taken; it keeps the busiest CU's load close to
+// the average (576 workgroups over 256 CUs put 3 on some CUs and 2 on the rest).
 int64_t tn_rows_per(int64_t cols, int64_t N) {
     const int64_t tiles = ceil_div(cols, TN_COLS);
-    return std::max<int64_t>(TN_ROWS, ceil_div(ceil_div(N * tiles, ctx_tn_wgs()), TN_ROWS) * TN_ROWS);
+    if (const int64_t w = ctx_tn_wgs())
+        return std::max<int64_t>(TN_STEP, ceil_div(ceil_div(N * tiles, w), TN_STEP) * TN_STEP);
+    constexpr int64_t kCUs = 256;
+    int64_t best_rows = ceil_div(N, TN_STEP) * TN_STEP;
+    double best = 1e300;
+    for (int64_t S = 1; S <= 64; ++S) {
+        const int64_t rows = std::max<int64_t>(2 * TN_STEP, ceil_div(ceil_div(N, S), TN_STEP) * TN_STEP);
+        const int64_t splits = ceil_div(N, rows);
+        const int64_t wgs = tiles * splits;
+        if (ceil_div(wgs, kCUs) > 3 && S > 1) break;   // more than 3 resident per CU: no gain
+        const double w = (double)ceil_div(wgs, kCUs);
+        const double cost = std::max(1.0, w / 2.0) * (double)rows * TN_COLS * 8.0 +
+                            (double)splits * 33.0 * (double)cols * 4.0 / (double)kCUs;
+        if (cost < best - 1e-9) {
+            best = cost;
+            best_rows = rows;
+        }
+    }
+    return best_rows;
 }
 
 // partial sums of the column reductions: one buffer per context, shared by every linear (used
@@ -730,6 +785,10 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     int rS = 1;
     int64_t rstride = 0;
     if constexpr (sizeof(CT) == 2) {
+        // the skinny TN kernels address dY / X through 32-bit buffer offsets (with a few steps of
+        // look-ahead past the last token row)
+        SA3K_REQUIRE((N + 4 * TN_STEP) * std::max(in, out) * 4 < ((int64_t)1 << 32),
+                     "tokens x features too large for one adapted-linear backward");
         const int64_t rows_per = tn_rows_per(out, N);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
