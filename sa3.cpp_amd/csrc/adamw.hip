@@ -55,16 +55,21 @@ __global__ __launch_bounds__(kThreads) void adamw_sumsq_kernel(const float* __re
             acc += (double)x.z * x.z;
             acc += (double)x.w * x.w;
         };
-        // four independent 16-byte loads in flight per thread, summed in index order
-        int64_t i = tid;
-        for (; i + 3 * stride < n4; i += 4 * stride) {
-            const float4 a = g4[i], b = g4[i + stride], c = g4[i + 2 * stride], d = g4[i + 3 * stride];
-            add(a);
-            add(b);
-            add(c);
-            add(d);
+        // Each block streams one contiguous chunk, eight 16-byte loads in flight per thread one
+        // block-width (4 KiB) apart, the last batch guarded per lane; summed in index order.
+        constexpr int U = 8;
+        const int64_t chunk = (n4 + gridDim.x - 1) / gridDim.x;
+        const int64_t beg = (int64_t)blockIdx.x * chunk, end = min(n4, beg + chunk);
+        for (int64_t i = beg + threadIdx.x; i < end; i += U * kThreads) {
+            float4 x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t j = i + u * kThreads;
+                x[u] = j < end ? g4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) add(x[u]);
         }
-        for (; i < n4; i += stride) add(g4[i]);
         for (int64_t i = (n4 << 2) + tid; i < n; i += stride) {
             float x = g[i];
             if (avg) x = x * inv;
@@ -131,8 +136,7 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
         const float4* g4 = reinterpret_cast<const float4*>(g);
         float4* m4 = reinterpret_cast<float4*>(m);
         float4* v4 = reinterpret_cast<float4*>(v);
-        for (int64_t i = tid; i < n4; i += stride) {
-            float4 pp = p4[i], gg = g4[i], mm = m4[i], vv = v4[i];
+        auto upd = [&](int64_t i, float4 pp, float4 gg, float4 mm, float4 vv) {
             pp.x = adamw_elem(pp.x, gg.x, mm.x, vv.x, s, scale, do_clip);
             pp.y = adamw_elem(pp.y, gg.y, mm.y, vv.y, s, scale, do_clip);
             pp.z = adamw_elem(pp.z, gg.z, mm.z, vv.z, s, scale, do_clip);
@@ -140,7 +144,20 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
             p4[i] = pp;
             m4[i] = mm;
             v4[i] = vv;
+        };
+        // each block updates one contiguous chunk, two float4 groups (one block-width apart) per
+        // iteration: eight 16-byte loads in flight per thread
+        const int64_t chunk = (n4 + gridDim.x - 1) / gridDim.x;
+        const int64_t beg = (int64_t)blockIdx.x * chunk, end = min(n4, beg + chunk);
+        int64_t i = beg + threadIdx.x;
+        for (; i + kThreads < end; i += 2 * kThreads) {
+            const float4 p0 = p4[i], g0 = g4[i], m0 = m4[i], v0 = v4[i];
+            const int64_t j = i + kThreads;
+            const float4 p1 = p4[j], g1 = g4[j], m1 = m4[j], v1 = v4[j];
+            upd(i, p0, g0, m0, v0);
+            upd(j, p1, g1, m1, v1);
         }
+        if (i < end) upd(i, p4[i], g4[i], m4[i], v4[i]);
         for (int64_t i = (n4 << 2) + tid; i < n; i += stride) {
             float mm = m[i], vv = v[i];
             p[i] = adamw_elem(p[i], g[i], mm, vv, s, scale, do_clip);
