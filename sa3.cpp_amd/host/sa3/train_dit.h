@@ -3,23 +3,18 @@
 // the "graph" sets the model up for one sample of `frames` latent frames and `ctx_len` context
 // tokens, lays the adapters out in the arena in the reference's target order, and allocates the
 // step inputs. The rectified-flow sample and the conditioning keep the reference's host structs
-// (src/train_diffusion.h:12-17, src/train_conditioning.h:16-22); their producers (sampler, text
-// encoder) are outside this build.
+// (src/train_diffusion.h:12-17, src/train_conditioning.h:16-22); the sample comes from
+// TrainDiffusionSampler (train_diffusion.h), the conditioning's producer (text encoder) is outside
+// this build.
 #pragma once
 
+#include "train_diffusion.h"
 #include "train_lora.h"
 
 #include <string>
 #include <vector>
 
 namespace sa3 {
-
-struct TrainDiffusionSample {
-    float t = 0.0f;
-    std::vector<float> noise;
-    std::vector<float> x_t;              // [io, T] (ggml order: T rows of io)
-    std::vector<float> velocity_target;  // [io, T]
-};
 
 struct TrainConditioning {
     std::vector<float> cross;   // [cond_dim, ctx_len] (ggml order)

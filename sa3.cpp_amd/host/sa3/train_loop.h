@@ -7,7 +7,9 @@
 // backend; here the graph carries its device (sa3k) context, so that argument is gone.
 #pragma once
 
+#include "train_diffusion.h"
 #include "train_dit.h"
+#include "train_inpaint.h"
 #include "train_optimizer.h"
 
 #include <string>
@@ -177,12 +179,19 @@ inline bool upload_train_lora_state(const TrainLoraState& state, TrainDitGraph& 
 }
 
 // run_train_dit_accumulate (src/train_loop.h:212-256): one sample through the DiT, velocity MSE,
-// and the adapter gradients added into accum (count += 1). The inpaint variant is not implemented.
+// and the adapter gradients added into accum (count += 1). The device DiT has no local-conditioning
+// input (dit.local.*), so, like the reference's graph built without one, it answers an inpaint
+// sample with the reference's mismatch error.
 inline bool run_train_dit_accumulate(TrainDitGraph& graph, const TrainLoraState& lora, TrainLoraGradAccum& accum,
                                      const TrainDiffusionSample& sample, const TrainConditioning& cond,
-                                     const DitConfig& dc, float& loss_out, std::string& err) {
+                                     const DitConfig& dc, float& loss_out, std::string& err,
+                                     const TrainInpaint* inpaint = nullptr) {
     if (sample.x_t.empty() || sample.velocity_target.empty() || cond.cross.empty() || cond.global.empty()) {
         err = "training step inputs are empty";
+        return false;
+    }
+    if (inpaint != nullptr) {
+        err = "inpaint graph/sample mismatch (local-cond present in one but not the other)";
         return false;
     }
     const size_t nx = (size_t)dc.io * graph.frames;

@@ -3,6 +3,7 @@
 // host-only parts (InverseLR schedule, target scopes); mode "gpu" also runs the device-backed
 // parts: AdamW, row norms, adapter init, the DiT training graph and the accumulated update, and
 // checks the mirror's packing against the C ABI's own arena path.
+#include "sa3/dist_shift.h"
 #include "sa3/train_loop.h"
 
 #include <cmath>
@@ -192,13 +193,18 @@ static void test_gpu() {
     std::normal_distribution<float> nd(0.0f, 1.0f);
     for (sa3::TrainLoraParam& p : st.params)
         for (float& b : p.lora_B) b = 0.01f * nd(rng);
+    // the step's sample from the rectified-flow sampler: a clean latent, a truncated logit-normal t
+    // warped by the LogSNR distribution shift, the noised x_t and the velocity target
+    std::vector<float> z((size_t)dc.io * frames);
+    for (float& x : z) x = nd(rng);
+    sa3::TrainDiffusionSampler sampler(77, "trunc_logit_normal");
+    float p1, p2, p3, p4;
+    sa3::dist_shift_defaults("LogSNR", p1, p2, p3, p4);
+    const float t_warped = sa3::dist_shift_warp("LogSNR", sampler.draw_t(), frames, p1, p2, p3, p4);
     sa3::TrainDiffusionSample s;
+    expect(sampler.sample_at(z, t_warped, s, err), "sampler");
+    expect(s.t == t_warped && s.t > 0.0f && s.t < 1.0f, "warped t in (0,1)");
     sa3::TrainConditioning c;
-    s.t = 0.4f;
-    s.x_t.resize((size_t)dc.io * frames);
-    s.velocity_target.resize(s.x_t.size());
-    for (float& x : s.x_t) x = nd(rng);
-    for (float& x : s.velocity_target) x = nd(rng);
     c.cond_dim = dc.cond_dim;
     c.ctx_len = ctx_len;
     c.cross.resize((size_t)dc.cond_dim * ctx_len);
@@ -218,6 +224,15 @@ static void test_gpu() {
     bad.x_t.pop_back();
     float loss0 = 0.0f, loss1 = 0.0f;
     expect(!sa3::run_train_dit_accumulate(graph, st, accum, bad, c, dc, loss0, err), "input size mismatch rejected");
+    {
+        std::mt19937_64 mrng(5);
+        sa3::InpaintMaskType ty;
+        const std::vector<float> mask = sa3::generate_inpaint_mask(frames, frames, {0.1, 0.8, 0.1}, mrng, ty);
+        const sa3::TrainInpaint ip = sa3::build_train_inpaint(z, mask, dc.io, frames, dc.io + 1, 1.0f);
+        expect(!sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss0, err, &ip) &&
+                   err.find("inpaint graph/sample mismatch") == 0,
+               "inpaint sample rejected (no local-conditioning input)");
+    }
     expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss0, err), "accumulate 1");
     const sa3::TrainLoraGradAccum once = accum;
     expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss1, err), "accumulate 2");
