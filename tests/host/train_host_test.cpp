@@ -4,6 +4,7 @@
 // parts: AdamW, row norms, adapter init, the DiT training graph and the accumulated update, and
 // checks the mirror's packing against the C ABI's own arena path.
 #include "sa3/dist_shift.h"
+#include "sa3/train_checkpoint.h"
 #include "sa3/train_loop.h"
 
 #include <cmath>
@@ -316,6 +317,31 @@ static void test_gpu() {
     expect(loop.step == 7, "seven optimizer steps");
     expect(last < first, "loss falls over updates");
     std::printf("loss %.6f -> %.6f over %d steps\n", first, last, loop.step - 1);
+
+    // the trained adapters through an adapter checkpoint: written, read back bit for bit (targets in
+    // stem order), and the reloaded state gives the same loss on the same sample
+    {
+        const std::string path = "train_host_test_adapter.gguf";
+        expect(sa3::write_train_lora_gguf(st, path, err), "write adapter checkpoint");
+        sa3::TrainLoraState back;
+        expect(sa3::load_train_lora_gguf(path, back, err), "load adapter checkpoint");
+        std::remove(path.c_str());
+        bool same = back.adapter_type == st.adapter_type && back.rank == st.rank && back.alpha == st.alpha &&
+                    back.params.size() == st.params.size();
+        for (size_t i = 0; same && i < st.params.size(); ++i) {
+            const sa3::TrainLoraParam& a = st.params[i];   // targets are already sorted by name
+            const sa3::TrainLoraParam& b = back.params[i];
+            same = a.target.stem == b.target.stem && a.target.in == b.target.in && a.target.out == b.target.out &&
+                   a.lora_A == b.lora_A && a.lora_B == b.lora_B && a.magnitude == b.magnitude;
+        }
+        expect(same, "checkpoint round trip is bitwise");
+        float l_st = 0.0f, l_back = 0.0f;
+        sa3::TrainLoraGradAccum scratch;
+        expect(sa3::run_train_dit_accumulate(graph, st, scratch, s, c, dc, l_st, err) &&
+                   sa3::run_train_dit_accumulate(graph, back, scratch, s, c, dc, l_back, err),
+               "accumulate with the reloaded adapters");
+        expect(l_st == l_back, "reloaded adapters give the same loss");
+    }
     sa3::free_train_dit_graph(graph);
 }
 
