@@ -97,12 +97,14 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "gemm_big"    bf16 products on 256 x 256 tiles (8 waves, one workgroup per CU): 0 never,
  *                 1 where they fill the chip about as evenly as 128 x 128 tiles (default), 2 always
  *                 (when operand extents and output alignment allow)
+ *   "gemm_splits" > 0: the split-K count of DMA-fed GEMMs that split, in place of the one chosen
+ *                 from the grid (clamped to the number of K tiles; default 0: chosen)
  *   "side_stream" 1: independent kernels of a backward pass (column reductions, attention dQ, the
  *                 context K/V projection) run on a second stream of the context beside the main
  *                 one, joined before the call returns (default 1; off while gemm_fixup is not 0
  *                 or a profiler scope is open)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny and gemm_big, which change the f32 summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big and gemm_splits, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

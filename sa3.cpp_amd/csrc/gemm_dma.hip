@@ -741,6 +741,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t slots = (int64_t)256 * wg_per_cu;
     if (ctx->gemm_split && tiles < slots && KT >= 8)
         splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
+    if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
     p.kps = std::max(1, (KT + splits - 1) / splits);
     splits = std::max(1, (KT + p.kps - 1) / p.kps);
     p.ws = nullptr;
@@ -819,6 +820,7 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     const int64_t slots = 256;   // one workgroup per CU (128 KiB of LDS)
     if (ctx->gemm_split && tiles < slots && KT >= 8)
         splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
+    if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
     p.kps = std::max(1, (KT + splits - 1) / splits);
     splits = std::max(1, (KT + p.kps - 1) / p.kps);
     p.ws = nullptr;

@@ -947,121 +947,211 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
 }
 
 // ---------------------------------------------------------------- grouped adapter refresh
-// One descriptor per member linear; every stage is one launch over the whole group.
+// One descriptor per member linear; every stage is one launch over the whole group. The grids are
+// compact: block_member[b] names the member a block works for and the member's first block of the
+// stage sits in PrepDesc::blk0[stage], so no block is launched for a member that has no work there
+// (a grid sized for the largest member times the member count launches hundreds of thousands of
+// empty blocks).
+enum PrepStage { kStageConvert = 0, kStagePt = 1, kStageGram = 2, kStageTerms = 3, kStages = 4 };
+constexpr int kPtRows = 256;                  // rows of P^T per block (4 waves x 64)
+constexpr int kTermRows = 64;                 // DoRA rows per block (8 passes of 8)
+
 struct PrepDesc {
     const float *A, *B, *mag, *bnsq;   // adapter (device) [r][in], [out][r], [out], [out]
     bf16 *Ac, *At, *Bc, *Bt;           // compute-type copies [r][in], [in][r], [out][r], [r][out]
     const bf16* W;                     // bf16 working copy of the base [out][in]
     float *Pt, *G, *BG, *nsq, *d;
-    int in, out, tile0;                // tile0: first 64-row tile of this member in the P stage
+    int in, out;
+    int blk0[kStages];                 // first block of this member in each stage's grid
 };
 
-// Ac/At/Bc/Bt from A and B (grid.y = member)
-__global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc* __restrict__ ds, int r) {
-    const PrepDesc& q = ds[blockIdx.y];
-    const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t na = (int64_t)r * q.in, nb = (int64_t)q.out * r;
-    if (e < na) {
-        const int64_t a = e / q.in, i = e - a * q.in;
-        const bf16 v = (bf16)q.A[e];
-        q.Ac[e] = v;
-        q.At[i * r + a] = v;
-    } else if (e < na + nb) {
-        const int64_t f = e - na, o = f / r, a = f - o * r;
-        const bf16 v = (bf16)q.B[f];
-        q.Bc[f] = v;
-        q.Bt[a * q.out + o] = v;
+// Ac/At/Bc/Bt from A and B. A block converts one 64-wide tile: columns [64t, 64t + 64) of A
+// (all r rows) for its first ceil(in/64) blocks, then rows [64t, 64t + 64) of B (all r columns).
+// The copies in the source layout are written as read; the transposed copies go through LDS so
+// every store is a contiguous row (a direct transposed store touches one cache segment per value).
+__global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc* __restrict__ ds,
+                                                                 const int* __restrict__ block_member, int r) {
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
+    __shared__ bf16 tile[64][34];   // [tile index][rank], padded
+    const int t = blockIdx.x - q.blk0[kStageConvert];
+    const int a_tiles = (q.in + 63) / 64;
+    const bool is_a = t < a_tiles;
+    const int64_t base = (int64_t)(is_a ? t : t - a_tiles) * 64;
+    const int64_t extent = is_a ? q.in : q.out;
+    // load: element (rank a, index base + j); A is [r][in] (index along a row), B is [out][r]
+    for (int e = threadIdx.x; e < 64 * 32; e += kThreads) {
+        int a, j;
+        if (is_a) { a = e / 64; j = e % 64; }   // consecutive threads: consecutive columns of row a
+        else { j = e / 32; a = e % 32; }        // consecutive threads: consecutive ranks of row j
+        const int64_t idx = base + j;
+        if (a >= r || idx >= extent) continue;
+        const float v = is_a ? q.A[(int64_t)a * q.in + idx] : q.B[idx * r + a];
+        const bf16 b = (bf16)v;
+        tile[j][a] = b;
+        if (is_a) q.Ac[(int64_t)a * q.in + idx] = b;
+        else q.Bc[idx * r + a] = b;
     }
-}
-
-// P^T[a][o] = sum_i A[a][i] W[o][i] for every member: one workgroup per 64 rows o of one member,
-// each wave 16 rows o x 32 ranks on v_mfma_f32_16x16x32_bf16. Both operands are read straight from
-// global memory (a lane's 8 consecutive K elements are 16 contiguous bytes of a row of W / Ac),
-// so W streams once with no LDS; 4 K-steps are issued ahead of their MFMAs.
-__global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __restrict__ ds,
-                                                            const int* __restrict__ tile_member, int r) {
-    const int m = tile_member[blockIdx.x];
-    const PrepDesc& q = ds[m];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
-    const int64_t o0 = (int64_t)(blockIdx.x - q.tile0) * 64 + wave * 16;
-    if (o0 >= q.out) return;
-    const bf16* wrow = q.W + (o0 + r16) * (int64_t)q.in + 8 * g;
-    const bf16* a0row = q.Ac + (int64_t)r16 * q.in + 8 * g;
-    const bf16* a1row = q.Ac + (int64_t)(16 + r16) * q.in + 8 * g;
-    const bool hi = r > 16;   // the second 16-rank tile exists
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    constexpr int U = 4;
-    for (int k0 = 0; k0 < q.in; k0 += 32 * U) {
-        bf16x8 w[U], a0[U], a1[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int k = k0 + 32 * u;
-            if (k < q.in) {
-                w[u] = *reinterpret_cast<const bf16x8*>(wrow + k);
-                a0[u] = r16 < r ? *reinterpret_cast<const bf16x8*>(a0row + k) : bf16x8{};
-                a1[u] = (hi && 16 + r16 < r) ? *reinterpret_cast<const bf16x8*>(a1row + k) : bf16x8{};
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (k0 + 32 * u < q.in) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], a0[u], acc0, 0, 0, 0);
-                if (hi) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], a1[u], acc1, 0, 0, 0);
-            }
-        }
-    }
-    // D[i][j]: o = o0 + 4g + v, rank j = r16 (+16)
-    if (r16 < r)
-        *reinterpret_cast<float4*>(q.Pt + (int64_t)r16 * q.out + o0 + 4 * g) = make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
-    if (hi && 16 + r16 < r)
-        *reinterpret_cast<float4*>(q.Pt + (int64_t)(16 + r16) * q.out + o0 + 4 * g) =
-            make_float4(acc1[0], acc1[1], acc1[2], acc1[3]);
-}
-
-// G = A A^T (double accumulation), grid (r*r, members)
-__global__ __launch_bounds__(kThreads) void group_gram_kernel(const PrepDesc* __restrict__ ds, int r) {
-    const PrepDesc& q = ds[blockIdx.y];
-    __shared__ double sh[kThreads / 64];
-    const int a = blockIdx.x / r, b = blockIdx.x % r;
-    double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < q.in; i += kThreads) acc += (double)q.A[a * q.in + i] * q.A[b * q.in + i];
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) q.G[a * r + b] = (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+    // transposed stores: At [in][r] (rows of r ranks), Bt [r][out] (rows of 64 indices)
+    for (int e = threadIdx.x; e < 64 * 32; e += kThreads) {
+        int a, j;
+        if (is_a) { j = e / 32; a = e % 32; }
+        else { a = e / 64; j = e % 64; }
+        const int64_t idx = base + j;
+        if (a >= r || idx >= extent) continue;
+        if (is_a) q.At[idx * r + a] = tile[j][a];
+        else q.Bt[(int64_t)a * q.out + idx] = tile[j][a];
+    }
 }
 
-// dora_terms_kernel for every member, grid (ceil(max out / 8), members)
-__global__ __launch_bounds__(kThreads) void group_dora_terms_kernel(const PrepDesc* __restrict__ ds, int r, float s) {
-    const PrepDesc& q = ds[blockIdx.y];
+// P^T[a][o] = sum_i A[a][i] W[o][i] for every member, v_mfma_f32_16x16x32_bf16: one block per 256
+// rows o of one member, each wave 64 rows (4 row blocks of 16) x 32 ranks, so a fragment of A
+// serves 4 MFMAs (A is read from L2 once per 64 rows of W, not per 16). Both operands come straight
+// from global memory (a lane's 8 consecutive K elements are 16 contiguous bytes of a row). The K
+// loop runs over 64-wide chunks with two register sets: the next chunk's loads are issued before
+// the current chunk's MFMAs; the loads are unconditional (rows and chunks clamped into range), so
+// the wait before each chunk counts only the other set's loads.
+__global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __restrict__ ds,
+                                                            const int* __restrict__ block_member, int r) {
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g = lane >> 4;
+    const int64_t o0 = (int64_t)(blockIdx.x - q.blk0[kStagePt]) * kPtRows + wave * 64;
+    if (o0 >= q.out) return;   // wave-uniform
+    constexpr int WR = 4;
+    const bf16* wrow[WR];
+#pragma unroll
+    for (int j = 0; j < WR; ++j) wrow[j] = q.W + std::min<int64_t>(o0 + 16 * j + r16, q.out - 1) * q.in + 8 * g;
+    const bf16* a0row = q.Ac + (int64_t)min(r16, r - 1) * q.in + 8 * g;
+    const bf16* a1row = q.Ac + (int64_t)min(16 + r16, r - 1) * q.in + 8 * g;
+    const bool hi = r > 16;   // the second 16-rank block exists
+    struct Set {
+        bf16x8 w[2][WR], a0[2], a1[2];
+    };
+    auto load = [&](Set& S, int c) {   // chunk c: K [64c, 64c + 64), two K32 steps
+        const int64_t k = (int64_t)c * 64;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int j = 0; j < WR; ++j) S.w[st][j] = *reinterpret_cast<const bf16x8*>(wrow[j] + k + 32 * st);
+            S.a0[st] = *reinterpret_cast<const bf16x8*>(a0row + k + 32 * st);
+            S.a1[st] = *reinterpret_cast<const bf16x8*>(a1row + k + 32 * st);
+        }
+    };
+    f32x4 acc[WR][2];
+#pragma unroll
+    for (int j = 0; j < WR; ++j) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const Set& S) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int j = 0; j < WR; ++j) {
+                acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(S.w[st][j], S.a0[st], acc[j][0], 0, 0, 0);
+                if (hi) acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(S.w[st][j], S.a1[st], acc[j][1], 0, 0, 0);
+            }
+    };
+    const int nc = q.in / 64;
+    Set sa, sb;
+    load(sa, 0);
+    for (int c = 0; c < nc; c += 2) {
+        load(sb, min(c + 1, nc - 1));
+        mma(sa);
+        if (c + 1 >= nc) break;
+        load(sa, min(c + 2, nc - 1));
+        mma(sb);
+    }
+    // D[i][j]: o = o0 + 16 jr + 4g + v, rank = r16 (+16)
+#pragma unroll
+    for (int j = 0; j < WR; ++j) {
+        const int64_t o = o0 + 16 * j + 4 * g;
+        if (o >= q.out) continue;   // out is a multiple of 16: whole 4-row groups
+        if (r16 < r)
+            *reinterpret_cast<float4*>(q.Pt + (int64_t)r16 * q.out + o) =
+                make_float4(acc[j][0][0], acc[j][0][1], acc[j][0][2], acc[j][0][3]);
+        if (hi && 16 + r16 < r)
+            *reinterpret_cast<float4*>(q.Pt + (int64_t)(16 + r16) * q.out + o) =
+                make_float4(acc[j][1][0], acc[j][1][1], acc[j][1][2], acc[j][1][3]);
+    }
+}
+
+// G = A A^T in double, two launches. Pass 1: one block per 256 columns of one member forms the
+// r x r partial sum over its columns (A's 32 x 256 slice staged in LDS; each thread owns 4 entries
+// (a, b) and adds the columns in order). Pass 2: one block per member sums its partials in column
+// order. Deterministic; each entry is a double sum rounded once to float.
+constexpr int kGramCols = 256;
+__global__ __launch_bounds__(kThreads) void group_gram_part_kernel(const PrepDesc* __restrict__ ds,
+                                                                   const int* __restrict__ block_member, int r,
+                                                                   double* __restrict__ part) {
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
+    const int c = blockIdx.x - q.blk0[kStageGram];
+    __shared__ float sa[32][kGramCols + 1];
+    const int64_t k0 = (int64_t)c * kGramCols;
+    const int kn = (int)std::min<int64_t>(kGramCols, q.in - k0);
+    for (int e = threadIdx.x; e < 32 * kGramCols; e += kThreads) {
+        const int a = e / kGramCols, k = e % kGramCols;
+        sa[a][k] = (a < r && k < kn) ? q.A[(int64_t)a * q.in + k0 + k] : 0.f;
+    }
+    __syncthreads();
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    const int a = threadIdx.x / 8, b0 = (threadIdx.x % 8) * 4;   // entries (a, b0..b0+3)
+    for (int k = 0; k < kn; ++k) {
+        const double x = sa[a][k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += x * (double)sa[b0 + j][k];
+    }
+    double* out = part + (int64_t)blockIdx.x * 1024;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[a * 32 + b0 + j] = acc[j];
+}
+
+__global__ __launch_bounds__(kThreads) void group_gram_sum_kernel(const PrepDesc* __restrict__ ds, int r,
+                                                                  const double* __restrict__ part) {
+    const PrepDesc& q = ds[blockIdx.x];
+    const int chunks = (q.in + kGramCols - 1) / kGramCols;
+    for (int e = threadIdx.x; e < 32 * 32; e += kThreads) {
+        const int a = e / 32, b = e % 32;
+        if (a >= r || b >= r) continue;
+        double sum = 0.0;
+        for (int c = 0; c < chunks; ++c) sum += part[(int64_t)(q.blk0[kStageGram] + c) * 1024 + e];
+        q.G[a * r + b] = (float)sum;
+    }
+}
+
+// nsq, d and BG = B G for kTermRows rows of one member per block (G staged in LDS once per block)
+__global__ __launch_bounds__(kThreads) void group_dora_terms_kernel(const PrepDesc* __restrict__ ds,
+                                                                    const int* __restrict__ block_member, int r,
+                                                                    float s) {
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
     __shared__ float gs[32][33];
     __shared__ float bs[8][32];
     const int ol = threadIdx.x >> 5, a = threadIdx.x & 31;
-    if ((int64_t)blockIdx.x * 8 >= q.out) return;   // uniform per block
-    const int64_t o = (int64_t)blockIdx.x * 8 + ol;
+    const int64_t row0 = (int64_t)(blockIdx.x - q.blk0[kStageTerms]) * kTermRows;
     for (int k = threadIdx.x; k < 32 * 32; k += kThreads) {
         const int i = k >> 5, j = k & 31;
         gs[i][j] = (i < r && j < r) ? q.G[i * r + j] : 0.f;
     }
-    bs[ol][a] = (o < q.out && a < r) ? q.B[o * r + a] : 0.f;
-    __syncthreads();
-    float gv = 0.f;
+    for (int pass = 0; pass < kTermRows / 8; ++pass) {
+        const int64_t o = row0 + pass * 8 + ol;
+        __syncthreads();   // G staged; the previous pass is done with bs
+        bs[ol][a] = (o < q.out && a < r) ? q.B[o * r + a] : 0.f;
+        __syncthreads();
+        float gv = 0.f;
 #pragma unroll 8
-    for (int c = 0; c < 32; ++c) gv += bs[ol][c] * gs[c][a];
-    float t2 = 0.f, t3 = 0.f;
-    if (o < q.out && a < r) {
-        q.BG[o * r + a] = gv;
-        t2 = q.Pt[(int64_t)a * q.out + o] * bs[ol][a];
-        t3 = bs[ol][a] * gv;
-    }
-    for (int off = 16; off > 0; off >>= 1) {
-        t2 += __shfl_xor(t2, off, 32);
-        t3 += __shfl_xor(t3, off, 32);
-    }
-    if (a == 0 && o < q.out) {
-        const float n2 = q.bnsq[o] + 2.0f * s * t2 + s * s * t3;
-        q.nsq[o] = n2;
-        q.d[o] = q.mag[o] / sqrtf(n2);
+        for (int c = 0; c < 32; ++c) gv += bs[ol][c] * gs[c][a];
+        float t2 = 0.f, t3 = 0.f;
+        if (o < q.out && a < r) {
+            q.BG[o * r + a] = gv;
+            t2 = q.Pt[(int64_t)a * q.out + o] * bs[ol][a];
+            t3 = bs[ol][a] * gv;
+        }
+        for (int off = 16; off > 0; off >>= 1) {
+            t2 += __shfl_xor(t2, off, 32);
+            t3 += __shfl_xor(t3, off, 32);
+        }
+        if (a == 0 && o < q.out) {
+            const float n2 = q.bnsq[o] + 2.0f * s * t2 + s * s * t3;
+            q.nsq[o] = n2;
+            q.d[o] = q.mag[o] / sqrtf(n2);
+        }
     }
 }
 
@@ -1073,16 +1163,17 @@ struct LinGroup {
     std::vector<sa3k_lin*> lins;
     std::vector<const float*> B, mag;
     PrepDesc* dev = nullptr;
-    int* tile_member = nullptr;
-    int n = 0, r = 0, dora = 0, tiles = 0;
-    int64_t max_conv = 0, max_out = 0;
+    int* block_member[kStages] = {};   // per stage: the member of every block
+    int blocks[kStages] = {};
+    int n = 0, r = 0, dora = 0;
     float s = 1.0f;
 };
 
 void lin_group_free(LinGroup* g) {
     if (!g) return;
     if (g->dev) (void)hipFree(g->dev);
-    if (g->tile_member) (void)hipFree(g->tile_member);
+    for (int* b : g->block_member)
+        if (b) (void)hipFree(b);
     delete g;
 }
 
@@ -1096,7 +1187,7 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
         g->dora = dora ? 1 : 0;
         g->s = scale;
         std::vector<PrepDesc> h(n);
-        std::vector<int> tm;
+        std::vector<int> bm[kStages];
         for (int i = 0; i < n; ++i) {
             sa3k_lin* L = lins[i];
             SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && L->W->wb && L->rank == g->r && g->r > 0,
@@ -1111,19 +1202,24 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
             q.W = static_cast<const bf16*>(L->W->wb);
             q.Pt = L->Pt; q.G = L->G; q.BG = L->BG; q.nsq = L->nsq; q.d = L->d;
             q.in = (int)in; q.out = (int)out;
-            q.tile0 = (int)tm.size();
-            for (int64_t t = 0; t < ceil_div(out, 64); ++t) tm.push_back(i);
-            g->max_conv = std::max(g->max_conv, (int64_t)g->r * (in + out));
-            g->max_out = std::max(g->max_out, out);
+            const int64_t per_stage[kStages] = {ceil_div(in, 64) + ceil_div(out, 64), ceil_div(out, kPtRows),
+                                                ceil_div(in, kGramCols), ceil_div(out, kTermRows)};
+            for (int st = 0; st < kStages; ++st) {
+                q.blk0[st] = (int)bm[st].size();
+                bm[st].insert(bm[st].end(), (size_t)per_stage[st], i);
+            }
             g->lins.push_back(L);
             g->B.push_back(B[i]);
             g->mag.push_back(dora ? mag[i] : nullptr);
         }
-        g->tiles = (int)tm.size();
         SA3K_HIP(hipMalloc(&g->dev, sizeof(PrepDesc) * n));
-        SA3K_HIP(hipMalloc(&g->tile_member, sizeof(int) * tm.size()));
         SA3K_HIP(hipMemcpyAsync(g->dev, h.data(), sizeof(PrepDesc) * n, hipMemcpyHostToDevice, ctx->stream));
-        SA3K_HIP(hipMemcpyAsync(g->tile_member, tm.data(), sizeof(int) * tm.size(), hipMemcpyHostToDevice, ctx->stream));
+        for (int st = 0; st < kStages; ++st) {
+            g->blocks[st] = (int)bm[st].size();
+            SA3K_HIP(hipMalloc(&g->block_member[st], sizeof(int) * bm[st].size()));
+            SA3K_HIP(hipMemcpyAsync(g->block_member[st], bm[st].data(), sizeof(int) * bm[st].size(),
+                                    hipMemcpyHostToDevice, ctx->stream));
+        }
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     } catch (...) {
         lin_group_free(g);
@@ -1142,8 +1238,8 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
     }
     {
         KernelScope ks(ctx, "group_convert");
-        group_convert_kernel<<<dim3((unsigned)ceil_div(g->max_conv, kThreads), (unsigned)g->n), kThreads, 0,
-                               ctx->stream>>>(g->dev, g->r);
+        group_convert_kernel<<<(unsigned)g->blocks[kStageConvert], kThreads, 0, ctx->stream>>>(
+            g->dev, g->block_member[kStageConvert], g->r);
         SA3K_LAUNCHED();
     }
     if (!g->dora) return;
@@ -1151,18 +1247,23 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
         double flops = 0.0;
         for (sa3k_lin* L : g->lins) flops += 2.0 * g->r * (double)L->W->in * (double)L->W->out;
         KernelScope ks(ctx, "group_pt", flops);
-        group_pt_kernel<<<(unsigned)g->tiles, kThreads, 0, ctx->stream>>>(g->dev, g->tile_member, g->r);
+        group_pt_kernel<<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStagePt],
+                                                                                      g->r);
         SA3K_LAUNCHED();
     }
     {
         KernelScope ks(ctx, "group_gram");
-        group_gram_kernel<<<dim3((unsigned)(g->r * g->r), (unsigned)g->n), kThreads, 0, ctx->stream>>>(g->dev, g->r);
+        double* part = reinterpret_cast<double*>(reduce_workspace(ctx, (size_t)g->blocks[kStageGram] * 1024 * sizeof(double)));
+        group_gram_part_kernel<<<(unsigned)g->blocks[kStageGram], kThreads, 0, ctx->stream>>>(
+            g->dev, g->block_member[kStageGram], g->r, part);
+        SA3K_LAUNCHED();
+        group_gram_sum_kernel<<<(unsigned)g->n, kThreads, 0, ctx->stream>>>(g->dev, g->r, part);
         SA3K_LAUNCHED();
     }
     {
         KernelScope ks(ctx, "group_dora_terms");
-        group_dora_terms_kernel<<<dim3((unsigned)ceil_div(g->max_out, 8), (unsigned)g->n), kThreads, 0, ctx->stream>>>(
-            g->dev, g->r, g->s);
+        group_dora_terms_kernel<<<(unsigned)g->blocks[kStageTerms], kThreads, 0, ctx->stream>>>(
+            g->dev, g->block_member[kStageTerms], g->r, g->s);
         SA3K_LAUNCHED();
     }
 }

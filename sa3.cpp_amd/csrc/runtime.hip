@@ -206,6 +206,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
         else if (n == "gemm_skinny") ctx->gemm_skinny = value != 0;
         else if (n == "gemm_big") ctx->gemm_big = value;
+        else if (n == "gemm_splits") ctx->gemm_splits = std::max(0, value);
         else if (n == "side_stream") ctx->use_side = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
