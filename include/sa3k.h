@@ -261,7 +261,8 @@ SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const voi
  * src/nn.h:135-144): per (batch, head) O = softmax(Q1 K1^T scale) V - softmax(Q2 K2^T scale) V,
  * without materialising the scores. q1, q2 [B*H][Sq][64] and k1, k2, v [B*H][Sk][64] are bf16
  * (head-major); window 0 is dense (the reference), window > 0 keeps |q - k| <= window/2 and needs
- * Sq == Sk. Outputs: o bf16 [B][Sq][H*64] (token-major, the out-projection input), o1, o2 bf16
+ * Sq == Sk. Attention weights below 2^-126 (keys more than ~87 nats under the row maximum) are
+ * flushed to zero. Outputs: o bf16 [B][Sq][H*64] (token-major, the out-projection input), o1, o2 bf16
  * [B*H][Sq][64] (the normalised branch outputs) and lse1, lse2 f32 [B*H][Sq] (base-2 log-sum-exp
  * of scale*log2(e)*scores), which the backward consumes. */
 SA3K_API int sa3k_diff_attn_fwd(sa3k_ctx* ctx, const void* q1, const void* k1, const void* q2, const void* k2,

@@ -26,6 +26,7 @@
 #include "sa3k_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace sa3k {
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);   // gemm.hip: context-owned scratch
@@ -126,11 +127,26 @@ __device__ __forceinline__ void dma_wait_all() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-__device__ __forceinline__ bool vis(int q, int k, int nk, int window) {
-    if (k >= nk) return false;
+// 2^x on the hardware's exp unit (v_exp_f32, no denormal rescaling: results below 2^-126, the
+// weights of keys more than ~87 nats under the row maximum, flush to zero)
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The keys one query sees form the range [lo, lo + n): |q - k| <= window/2 (window > 0) and
+// k < nk. With it a visibility test is one unsigned compare: (unsigned)(k - lo) < n.
+struct Span {
+    int lo, n;
+};
+__device__ __forceinline__ Span visible(int q, int nk, int window) {
+    if (window <= 0) return Span{0, nk};
+    const int half = window / 2, lo = max(0, q - half), hi = min(nk - 1, q + half);
+    return Span{lo, max(0, hi - lo + 1)};
+}
+// every (q, k) of query block qb x key block kb is visible and in range (a block-uniform test)
+__device__ __forceinline__ bool block_full(int qb, int kb, int nq, int nk, int window) {
+    if ((qb + 1) * BLK > nq || (kb + 1) * BLK > nk) return false;
     if (window <= 0) return true;
-    const int d = q > k ? q - k : k - q;
-    return 2 * d <= window;
+    const int far = max(qb * BLK + BLK - 1 - kb * BLK, kb * BLK + BLK - 1 - qb * BLK);
+    return 2 * far <= window;
 }
 
 // key/query block range [lo, hi) that can interact with block b under the window
@@ -163,6 +179,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
     const int qrow = qb * BLK + w * 16 + r;        // this lane's query for the S^T layout
     const float c = a.scale * kLog2e;
+    const Span sp = visible(qrow, a.Sk, a.window);
 
     bf16x8 q1f[2], q2f[2];
 #pragma unroll
@@ -190,6 +207,9 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
     };
     if (kb_lo < kb_hi) issue(0, kb_lo);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
+        // no contraction of the score scaling into the exponent's subtraction: the row maximum's
+        // weight must come out exactly 2^0 = 1
+#pragma clang fp contract(off)
         const int st = (kb - kb_lo) & 1;
         dma_wait_all();   // block kb landed; every wave is done with block kb-1 (the other stage)
         if (kb + 1 < kb_hi) issue(st ^ 1, kb + 1);
@@ -207,18 +227,29 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
                 s2[kt] = mfma(ld_row(k2s, kt * 16 + r, ks * 4 + g), q2f[ks], s2[kt]);
             }
         }
-        // wait: the MFMA output layout is rows = 4*(lane/16)+v of the A operand (keys), col = lane%16
+        // The MFMA output layout is rows = 4*(lane/16)+v of the A operand (keys), col = lane%16
         // (queries); the A rows fed above were keys kt*16 + r, so output row index 4g+v is key
-        // kt*16 + 4g + v and the column is query w*16 + r.
+        // kt*16 + 4g + v and the column is query w*16 + r. Only blocks that cross the window's
+        // edge or the sequence end are masked (a block-uniform branch).
+        if (!block_full(qb, kb, a.Sq, a.Sk, a.window)) {
+            const int rel = kb * BLK + 4 * g - sp.lo;   // key kt*16 + 4g + v, less lo, is rel + 16 kt + v
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const bool ok = (unsigned)(rel + 16 * kt + v) < (unsigned)sp.n;
+                    s1[kt][v] = ok ? s1[kt][v] : -INFINITY;
+                    s2[kt][v] = ok ? s2[kt][v] : -INFINITY;
+                }
+        }
+        // scaled scores (rounded once, so the row maximum's weight is exactly 2^0 = 1) and maxima
         float mx1 = -INFINITY, mx2 = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int key = kb * BLK + kt * 16 + 4 * g + v;
-                const bool ok = vis(qrow, key, a.Sk, a.window);
-                s1[kt][v] = ok ? s1[kt][v] * c : -INFINITY;
-                s2[kt][v] = ok ? s2[kt][v] * c : -INFINITY;
+                s1[kt][v] *= c;
+                s2[kt][v] *= c;
                 mx1 = fmaxf(mx1, s1[kt][v]);
                 mx2 = fmaxf(mx2, s2[kt][v]);
             }
@@ -228,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
         mx2 = fmaxf(mx2, __shfl_xor(mx2, 32, 64));
         const float mn1 = fmaxf(m1, mx1), mn2 = fmaxf(m2, mx2);
         const float base1 = mn1 == -INFINITY ? 0.f : mn1, base2 = mn2 == -INFINITY ? 0.f : mn2;
-        const float al1 = exp2f(m1 - base1), al2 = exp2f(m2 - base2);   // 0 when m was -inf
+        const float al1 = ex2(m1 - base1), al2 = ex2(m2 - base2);   // 0 when m was -inf
         m1 = mn1;
         m2 = mn2;
         float ps1 = 0.f, ps2 = 0.f;
@@ -237,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float e1 = exp2f(s1[kt][v] - base1), e2 = exp2f(s2[kt][v] - base2);
+                const float e1 = ex2(s1[kt][v] - base1), e2 = ex2(s2[kt][v] - base2);
                 ps1 += e1;
                 ps2 += e2;
                 p1[kt >> 1][(kt & 1) * 4 + v] = (bf16)e1;
@@ -339,6 +370,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
     const int key = kb * BLK + w * 16 + r;     // this lane's key
     const float c = a.scale * kLog2e;
+    // the queries that see this key: |q - key| <= window/2 and q < Sq (none for a key past Sk)
+    const Span qsp = key < a.Sk ? visible(key, a.Sq, a.window) : Span{0, 0};
 
     bf16x8 k1f[2], k2f[2], vf[2];
 #pragma unroll
@@ -391,6 +424,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const float* sd2 = vec[st][3];
         // per 16-query tile qt: S1, S2, dP with rows = queries qt*16 + 4g + v, col = key
         bf16x8 pd[2], ds1[2], ds2[2];    // (P1 - P2), dS1, dS2 as B operands over query pairs
+        const bool full = block_full(qb, kb, a.Sq, a.Sk, a.window);   // block-uniform: no masking
+        const int rel = qb * BLK + 4 * g - qsp.lo;   // query qt*16 + 4g + v, less lo, is rel + 16 qt + v
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) {
             f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
@@ -400,12 +435,19 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 s2 = mfma(ld_row(q2s, qt * 16 + r, ks * 4 + g), k2f[ks], s2);
                 dp = mfma(ld_row(dos, qt * 16 + r, ks * 4 + g), vf[ks], dp);
             }
+            if (!full) {   // hidden pairs get score -inf, hence weight 0 and dS 0
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const bool ok = (unsigned)(rel + 16 * qt + v) < (unsigned)qsp.n;
+                    s1[v] = ok ? s1[v] : -INFINITY;
+                    s2[v] = ok ? s2[v] : -INFINITY;
+                }
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int ql = qt * 16 + 4 * g + v, q = qb * BLK + ql;
-                const bool ok = q < a.Sq && vis(q, key, a.Sk, a.window);
-                const float p1 = ok ? exp2f(s1[v] * c - sl1[ql]) : 0.f;
-                const float p2 = ok ? exp2f(s2[v] * c - sl2[ql]) : 0.f;
+                const int ql = qt * 16 + 4 * g + v;
+                const float p1 = ex2(fmaf(s1[v], c, -sl1[ql]));
+                const float p2 = ex2(fmaf(s2[v], c, -sl2[ql]));
                 const int e = (qt & 1) * 4 + v;
                 pd[qt >> 1][e] = (bf16)(p1 - p2);
                 ds1[qt >> 1][e] = (bf16)(p1 * (dp[v] - sd1[ql]));
@@ -491,6 +533,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
         dof[ks] = __builtin_bit_cast(bf16x8, u3);
     }
     const bool qok = qrow < a.Sq;
+    const Span sp = qok ? visible(qrow, a.Sk, a.window) : Span{0, 0};   // keys this query sees
     const float L1 = qok ? a.lse1[(int64_t)bh * a.Sq + qrow] : 0.f;
     const float L2 = qok ? a.lse2[(int64_t)bh * a.Sq + qrow] : 0.f;
     const float D1 = qok ? a.dn1[(int64_t)bh * a.Sq + qrow] : 0.f;
@@ -516,6 +559,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
         const char* k2s = k1s + BLK * ROW;
         const char* vs = k1s + 2 * BLK * ROW;
         bf16x8 ds1[2], ds2[2];
+        const bool full = block_full(qb, kb, a.Sq, a.Sk, a.window);   // block-uniform: no masking
+        const int rel = kb * BLK + 4 * g - sp.lo;   // key kt*16 + 4g + v, less lo, is rel + 16 kt + v
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
             f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
@@ -525,12 +570,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
                 s2 = mfma(ld_row(k2s, kt * 16 + r, ks * 4 + g), q2f[ks], s2);
                 dp = mfma(ld_row(vs, kt * 16 + r, ks * 4 + g), dof[ks], dp);
             }
+            if (!full) {   // hidden pairs get score -inf, hence weight 0 and dS 0
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const bool ok = (unsigned)(rel + 16 * kt + v) < (unsigned)sp.n;
+                    s1[v] = ok ? s1[v] : -INFINITY;
+                    s2[v] = ok ? s2[v] : -INFINITY;
+                }
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int k = kb * BLK + kt * 16 + 4 * g + v;
-                const bool ok = qok && vis(qrow, k, a.Sk, a.window);
-                const float p1 = ok ? exp2f(s1[v] * c - L1) : 0.f;
-                const float p2 = ok ? exp2f(s2[v] * c - L2) : 0.f;
+                const float p1 = ex2(fmaf(s1[v], c, -L1));
+                const float p2 = ex2(fmaf(s2[v], c, -L2));
                 const int e = (kt & 1) * 4 + v;
                 ds1[kt >> 1][e] = (bf16)(p1 * (dp[v] - D1));
                 ds2[kt >> 1][e] = (bf16)(-p2 * (dp[v] - D2));

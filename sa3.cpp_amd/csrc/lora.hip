@@ -954,6 +954,14 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
 // empty blocks).
 enum PrepStage { kStageConvert = 0, kStagePt = 1, kStageGram = 2, kStageTerms = 3, kStages = 4 };
 constexpr int kPtRows = 256;                  // rows of P^T per block (4 waves x 64)
+
+// 16 bytes of global memory. The group kernels read their pointers from descriptors in device
+// memory, so the compiler cannot infer the address space and would emit flat loads, which it waits
+// for together with LDS traffic (lgkmcnt(0)): every load in flight would be drained before the
+// first use of any of them.
+__device__ __forceinline__ bf16x8 ld_global16(const bf16* p) {
+    return *(const __attribute__((address_space(1))) bf16x8*)(p);
+}
 constexpr int kTermRows = 64;                 // DoRA rows per block (8 passes of 8)
 
 struct PrepDesc {
@@ -1011,6 +1019,7 @@ __global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc*
 // loop runs over 64-wide chunks with two register sets: the next chunk's loads are issued before
 // the current chunk's MFMAs; the loads are unconditional (rows and chunks clamped into range), so
 // the wait before each chunk counts only the other set's loads.
+template <bool HI>   // HI: the rank exceeds 16, so a second 16-rank block of P^T rows exists
 __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __restrict__ ds,
                                                             const int* __restrict__ block_member, int r) {
     const PrepDesc& q = ds[block_member[blockIdx.x]];
@@ -1023,7 +1032,6 @@ __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __re
     for (int j = 0; j < WR; ++j) wrow[j] = q.W + std::min<int64_t>(o0 + 16 * j + r16, q.out - 1) * q.in + 8 * g;
     const bf16* a0row = q.Ac + (int64_t)min(r16, r - 1) * q.in + 8 * g;
     const bf16* a1row = q.Ac + (int64_t)min(16 + r16, r - 1) * q.in + 8 * g;
-    const bool hi = r > 16;   // the second 16-rank block exists
     struct Set {
         bf16x8 w[2][WR], a0[2], a1[2];
     };
@@ -1032,9 +1040,9 @@ __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __re
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
 #pragma unroll
-            for (int j = 0; j < WR; ++j) S.w[st][j] = *reinterpret_cast<const bf16x8*>(wrow[j] + k + 32 * st);
-            S.a0[st] = *reinterpret_cast<const bf16x8*>(a0row + k + 32 * st);
-            S.a1[st] = *reinterpret_cast<const bf16x8*>(a1row + k + 32 * st);
+            for (int j = 0; j < WR; ++j) S.w[st][j] = ld_global16(wrow[j] + k + 32 * st);
+            S.a0[st] = ld_global16(a0row + k + 32 * st);
+            if (HI) S.a1[st] = ld_global16(a1row + k + 32 * st);
         }
     };
     f32x4 acc[WR][2];
@@ -1046,18 +1054,29 @@ __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __re
 #pragma unroll
             for (int j = 0; j < WR; ++j) {
                 acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(S.w[st][j], S.a0[st], acc[j][0], 0, 0, 0);
-                if (hi) acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(S.w[st][j], S.a1[st], acc[j][1], 0, 0, 0);
+                if (HI) acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(S.w[st][j], S.a1[st], acc[j][1], 0, 0, 0);
             }
     };
     const int nc = q.in / 64;
     Set sa, sb;
-    load(sa, 0);
-    for (int c = 0; c < nc; c += 2) {
-        load(sb, min(c + 1, nc - 1));
+    int c = 0;
+    if (nc & 1) {   // an odd chunk first, so the pipelined loop below runs whole pairs
+        load(sa, 0);
         mma(sa);
-        if (c + 1 >= nc) break;
-        load(sa, min(c + 2, nc - 1));
+        c = 1;
+    }
+    load(sa, c);
+    // the scheduling barriers keep each set's loads ahead of the other set's products (the compiler
+    // would otherwise sink them to their first use and serialize load and MFMA)
+    for (; c < nc; c += 2) {
+        load(sb, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(sa);
+        __builtin_amdgcn_sched_barrier(0);
+        load(sa, min(c + 2, nc - 1));   // past the last pair: a discarded reload of the last chunk
+        __builtin_amdgcn_sched_barrier(0);
         mma(sb);
+        __builtin_amdgcn_sched_barrier(0);
     }
     // D[i][j]: o = o0 + 16 jr + 4g + v, rank = r16 (+16)
 #pragma unroll
@@ -1067,7 +1086,7 @@ __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __re
         if (r16 < r)
             *reinterpret_cast<float4*>(q.Pt + (int64_t)r16 * q.out + o) =
                 make_float4(acc[j][0][0], acc[j][0][1], acc[j][0][2], acc[j][0][3]);
-        if (hi && 16 + r16 < r)
+        if (HI && 16 + r16 < r)
             *reinterpret_cast<float4*>(q.Pt + (int64_t)(16 + r16) * q.out + o) =
                 make_float4(acc[j][1][0], acc[j][1][1], acc[j][1][2], acc[j][1][3]);
     }
@@ -1247,8 +1266,8 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
         double flops = 0.0;
         for (sa3k_lin* L : g->lins) flops += 2.0 * g->r * (double)L->W->in * (double)L->W->out;
         KernelScope ks(ctx, "group_pt", flops);
-        group_pt_kernel<<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStagePt],
-                                                                                      g->r);
+        auto* kern = g->r > 16 ? group_pt_kernel<true> : group_pt_kernel<false>;
+        kern<<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStagePt], g->r);
         SA3K_LAUNCHED();
     }
     {
