@@ -161,6 +161,21 @@ __device__ __forceinline__ void band_range(int b, int n_other, int window, int& 
     }
 }
 
+// This workgroup's (block, bh) from its place in dispatch order (x fastest, then y): the blocks
+// go out from the middle of the sequence to its ends, every (batch, head) of one block before the
+// next block. Under a window the middle blocks meet the most key (query) blocks and the end ones
+// the fewest, so the grid starts with the longest workgroups and ends with the shortest, and the
+// last wave of workgroups is short. Consecutive workgroups differ in bh, so with BH a multiple of 8
+// every workgroup of one (batch, head) runs on the same XCD (dispatch deals them out round-robin)
+// and shares its L2.
+__device__ __forceinline__ void heavy_first(int& blk, int& bh) {
+    const int n = gridDim.x, BH = gridDim.y;
+    const int L = blockIdx.x + n * blockIdx.y;
+    const int k = L / BH;
+    bh = L - k * BH;
+    blk = (k & 1) ? n / 2 - (k + 1) / 2 : n / 2 + k / 2;
+}
+
 // ------------------------------------------------------------------------------------ forward
 struct FwdArgs {
     const bf16 *q1, *k1, *q2, *k2, *v;   // [BH][S][64]
@@ -173,7 +188,8 @@ struct FwdArgs {
 
 __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {K1, K2, V}
-    const int bh = blockIdx.y, qb = blockIdx.x;
+    int qb, bh;
+    heavy_first(qb, bh);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
@@ -364,7 +380,8 @@ struct BwdArgs {
 __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {Q1, Q2, dO}
     __shared__ __attribute__((aligned(16))) float vec[2][4][BLK];            // lse1, lse2, dn1, dn2
-    const int bh = blockIdx.y, kb = blockIdx.x;
+    int kb, bh;
+    heavy_first(kb, bh);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
@@ -512,7 +529,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_sum(BwdArgs a, int64_t
 // Per query block: dQ1, dQ2. S^T = K Q^T (lane = query), dP^T = V dO^T.
 __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {K1, K2, V}
-    const int bh = blockIdx.y, qb = blockIdx.x;
+    int qb, bh;
+    heavy_first(qb, bh);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, r = lane & 15;
     const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
