@@ -339,26 +339,40 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------ backward
-// Dn_i[bh][q] = sum_d dO[b][q][h][d] * O_i[bh][q][d]; dOh[bh][q][d] = bf16(dO) (head-major)
+// Dn_i[bh][q] = sum_d dO[b][q][h][d] * O_i[bh][q][d]; dOh[bh][q][d] = bf16(dO) (head-major).
+// Eight lanes per (bh, q), 8 dims each (32-byte dO, 16-byte O_i loads), the dot products summed
+// over the eight lanes by butterfly shuffles.
 __global__ __launch_bounds__(kThreads) void attn_bwd_dot_kernel(const float* __restrict__ dO, const bf16* __restrict__ o1,
                                                                 const bf16* __restrict__ o2, int BH, int H, int Sq,
                                                                 bf16* __restrict__ dOh, float* __restrict__ dn1,
                                                                 float* __restrict__ dn2) {
-    // one wave per (bh, q): 64 lanes = 64 dims
-    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const int d = threadIdx.x & 63;
-    if (item >= (int64_t)BH * Sq) return;
-    const int bh = (int)(item / Sq), q = (int)(item % Sq);
-    const int b = bh / H, h = bh % H;
-    const float x = dO[((int64_t)b * Sq + q) * (H * HD) + h * HD + d];
-    const int64_t idx = item * HD + d;
-    dOh[idx] = (bf16)x;
-    float s1 = x * (float)o1[idx], s2 = x * (float)o2[idx];
-    for (int off = 32; off > 0; off >>= 1) {
+    const unsigned item = (blockIdx.x * kThreads + threadIdx.x) >> 3;
+    const int d0 = (threadIdx.x & 7) * 8;
+    const bool ok = item < (unsigned)BH * (unsigned)Sq;
+    float s1 = 0.f, s2 = 0.f;
+    if (ok) {
+        const unsigned bh = item / (unsigned)Sq, q = item - bh * (unsigned)Sq;
+        const unsigned b = bh / (unsigned)H, h = bh - b * (unsigned)H;
+        const float* src = dO + ((int64_t)b * Sq + q) * (H * HD) + h * HD + d0;
+        const float4 xa = *reinterpret_cast<const float4*>(src), xb = *reinterpret_cast<const float4*>(src + 4);
+        const int64_t idx = (int64_t)item * HD + d0;
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(o1 + idx), a2 = *reinterpret_cast<const bf16x8*>(o2 + idx);
+        const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        bf16x8 xo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            xo[j] = (bf16)x[j];
+            s1 += x[j] * (float)a1[j];
+            s2 += x[j] * (float)a2[j];
+        }
+        *reinterpret_cast<bf16x8*>(dOh + idx) = xo;
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
         s1 += __shfl_xor(s1, off, 64);
         s2 += __shfl_xor(s2, off, 64);
     }
-    if (d == 0) {
+    if (ok && (threadIdx.x & 7) == 0) {
         dn1[item] = s1;
         dn2[item] = s2;
     }
@@ -655,7 +669,8 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
     {
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dot" : "attn_bwd_dot_cross");
         const int64_t items = (int64_t)BH * Sq;
-        attn_bwd_dot_kernel<<<(unsigned)ceil_div(items, kThreads / 64), kThreads, 0, ctx->stream>>>(
+        SA3K_REQUIRE(items * 8 < ((int64_t)1 << 32), "too many (batch, head, query) rows for one attention call");
+        attn_bwd_dot_kernel<<<(unsigned)ceil_div(items * 8, kThreads), kThreads, 0, ctx->stream>>>(
             dO, o1, o2, BH, H, Sq, dOh, dn1, dn2);
         SA3K_LAUNCHED();
     }
