@@ -666,12 +666,16 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
                    float* dq1, float* dk1, float* dq2, float* dk2, float* dv) {
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     const int BH = B * H;
+    // dQ (second stream) and dK/dV (main stream) only share inputs: they run side by side once the
+    // row dots are done (the dot kernel records the fork event)
+    const bool side = side_usable(ctx);
+    if (side) fork_arm(ctx);
     {
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dot" : "attn_bwd_dot_cross");
         const int64_t items = (int64_t)BH * Sq;
         SA3K_REQUIRE(items * 8 < ((int64_t)1 << 32), "too many (batch, head, query) rows for one attention call");
-        attn_bwd_dot_kernel<<<(unsigned)ceil_div(items * 8, kThreads), kThreads, 0, ctx->stream>>>(
-            dO, o1, o2, BH, H, Sq, dOh, dn1, dn2);
+        launch_k(ctx, true, attn_bwd_dot_kernel, dim3((unsigned)ceil_div(items * 8, kThreads)), dim3(kThreads), 0, dO,
+                 o1, o2, BH, H, Sq, dOh, dn1, dn2);
         SA3K_LAUNCHED();
     }
     BwdArgs a{q1, k1, q2, k2, v, dOh, lse1, lse2, dn1, dn2, Sq, Sk, window, scale, dq1, dq2, dk1, dk2, dv, 1, nullptr};
@@ -683,9 +687,7 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
         a.qsplit = (int)std::min<int64_t>({(int64_t)nqb, 16, ceil_div(512, (int64_t)nkb * BH)});
         if (a.qsplit > 1) a.part = gemm_workspace_bytes(ctx, (size_t)a.qsplit * 3 * plane * sizeof(float));
     }
-    // dQ (second stream) and dK/dV (main stream) only share inputs: they run side by side
-    const bool side = side_usable(ctx);
-    if (side) side_fork(ctx);
+    if (side) fork_fire(ctx);
     {
         OnSide os(ctx, side);
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dq" : "attn_bwd_dq_cross");

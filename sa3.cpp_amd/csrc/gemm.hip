@@ -427,13 +427,17 @@ void launch(sa3k_ctx* ctx, KParams p) {
                                         "," + std::to_string(WMW) + ",a" + std::to_string(ASRC) + ",b" +
                                         std::to_string(BSRC) + (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
-        if (ctx->gemm_pd == 2) gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 2><<<g, kThreads, 0, ctx->stream>>>(p);
-        else gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 1><<<g, kThreads, 0, ctx->stream>>>(p);
+        if (ctx->gemm_pd == 2)
+            launch_k(ctx, splits == 1, gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 2>, g, dim3(kThreads), 0, p);
+        else
+            launch_k(ctx, splits == 1, gemm_kernel<BM, BN, WMW, ASRC, BSRC, BF16, 1>, g, dim3(kThreads), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
-        gemm_splitk_reduce<<<(unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
+        launch_k(ctx, true, gemm_splitk_reduce, dim3((unsigned)ceil_div((p.M + p.Mx) * p.N, kThreads)), dim3(kThreads),
+                 0, p, splits);
+        SA3K_LAUNCHED();
     }
 }
 

@@ -777,13 +777,16 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                                         std::to_string(WMW) + "," + std::to_string(STAGES) +
                                         (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
-        gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW><<<g, NW * 64, 0, ctx->stream>>>(p);
+        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW>, g,
+                 dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1 && !p.counters) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
         const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.N / 4 : (p.M + p.Mx) * p.N;
-        gemm_dma_splitk_reduce<<<(unsigned)ceil_div(items, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
+        launch_k(ctx, true, gemm_dma_splitk_reduce, dim3((unsigned)ceil_div(items, kThreads)), dim3(kThreads), 0, p,
+                 splits);
+        SA3K_LAUNCHED();
     }
 }
 
@@ -834,13 +837,14 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
     {
         KernelScope ks(ctx, "gemm_big<256,256,bf16>", 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
-        gemm_big_kernel<<<dim3((unsigned)grid, (unsigned)splits), 512, 0, ctx->stream>>>(p);
+        launch_k(ctx, splits == 1, gemm_big_kernel, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
         const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.N / 4 : (p.M + p.Mx) * p.N;
-        gemm_dma_splitk_reduce<<<(unsigned)ceil_div(items, kThreads), kThreads, 0, ctx->stream>>>(p, splits);
+        launch_k(ctx, true, gemm_dma_splitk_reduce, dim3((unsigned)ceil_div(items, kThreads)), dim3(kThreads), 0, p,
+                 splits);
         SA3K_LAUNCHED();
     }
 }

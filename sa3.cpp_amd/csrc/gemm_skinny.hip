@@ -161,7 +161,7 @@ void gemm_run_skinny(sa3k_ctx* ctx, const GemmDesc& d) {
                    static_cast<const bf16*>(d.B), d.ldb, (int)d.N, (int)(d.K / 64), halves, tiles, d.alpha,
                    d.C, d.Cb, d.Cb ? d.ldcb : d.ldc, d.Cx, d.Cbx, d.ldcx};
     KernelScope ks(ctx, "skinny_nt", 2.0 * (double)Mt * (double)d.N * (double)d.K);
-    skinny_nt_kernel<<<(unsigned)blocks, kSkThreads, 0, ctx->stream>>>(p);
+    launch_k(ctx, true, skinny_nt_kernel, dim3((unsigned)blocks), dim3(kSkThreads), 0, p);
     SA3K_LAUNCHED();
 }
 

@@ -837,6 +837,22 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
                                                                          static_cast<CT*>(L->A2x));
         SA3K_LAUNCHED();
     }
+    int64_t x_rows_per = 0;
+    int x_S = 0;
+    float* x_part = nullptr;
+    int* x_counters = nullptr;
+    if constexpr (sizeof(CT) == 2) {
+        x_rows_per = tn_rows_per(in, N);
+        x_S = (int)ceil_div(N, x_rows_per);
+        x_counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
+    } else {
+        x_S = choose_splits(in, N);
+        x_rows_per = ceil_div(N, x_S);
+    }
+    // the partials go to the second stream once sdUB is ready: its GEMM records the fork event
+    const bool early = x_counters == nullptr;
+    const bool side = early && side_usable(ctx);
+    if (side) fork_arm(ctx);
     {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = bf ? SRC_BF16 : SRC_F32;
@@ -855,18 +871,6 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
     //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
     //     reduction the partials kernel adds into dA itself and therefore runs after step 3.
-    int64_t x_rows_per = 0;
-    int x_S = 0;
-    float* x_part = nullptr;
-    int* x_counters = nullptr;
-    if constexpr (sizeof(CT) == 2) {
-        x_rows_per = tn_rows_per(in, N);
-        x_S = (int)ceil_div(N, x_rows_per);
-        x_counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
-    } else {
-        x_S = choose_splits(in, N);
-        x_rows_per = ceil_div(N, x_S);
-    }
     auto x_partials = [&] {
         if constexpr (sizeof(CT) == 2) {
             x_part = reduce_workspace(ctx, (size_t)x_S * 32 * in * sizeof(float));
@@ -902,15 +906,14 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             x_part, stride, x_S, (int64_t)r * in, dA, 1);
         SA3K_LAUNCHED();
     };
-    const bool early = x_counters == nullptr;
-    const bool side = early && side_usable(ctx);
     if (early) {
-        if (side) side_fork(ctx);   // sdUB and X are ready
+        if (side) fork_fire(ctx);   // sdUB and X are ready
         OnSide os(ctx, side);
         x_partials();
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
-    //    of the same GEMM (they share the W^T tiles)
+    //    of the same GEMM (they share the W^T tiles). Its last kernel records the next fork.
+    if (side) fork_arm(ctx);
     const WOp wt = weight_operand(W, bf, true);
     if (dX) {
         GemmDesc g;
@@ -935,7 +938,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     }
     // 4b. the partial sums into dA, after step 3
     if (early) {
-        if (side) side_fork(ctx);   // the dX GEMM has added its dA rows
+        if (side) fork_fire(ctx);   // the dX GEMM has added its dA rows
         {
             OnSide os(ctx, side);
             x_sum();

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
@@ -42,6 +43,9 @@ struct sa3k_ctx {
     int side_ev_i = 0;
     int use_side = 1;                      // run independent chains on the second stream
     int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
+    hipEvent_t tail_ev = nullptr;          // fork event armed for the producer about to launch (fork_arm)
+    uint64_t launch_seq = 0;               // launches made through launch_k
+    uint64_t tail_seq = 0;                 // launch_seq of the launch that last recorded tail_ev (0: none)
     std::string last_error;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     bool prof_on = false;
@@ -164,6 +168,37 @@ inline hipEvent_t side_event(sa3k_ctx* c) {
 inline void side_fork(sa3k_ctx* c) {
     hipEvent_t e = side_event(c);
     SA3K_HIP(hipEventRecord(e, c->main_stream));
+    SA3K_HIP(hipStreamWaitEvent(c->side_stream, e, 0));
+}
+// Fork after a producer without a separate event record (a marker packet on the main stream that
+// costs ~4.6 us; a kernel's own completion event costs ~0.9 us): fork_arm, then the producer's
+// launches through launch_k (the last of them passes last = true and records the armed event at
+// its completion), then fork_fire makes the second stream wait on it. fork_fire records the event
+// itself unless the most recent launch_k launch was the one that recorded it, so a producer path
+// that records nothing, or launches again after recording, still forks correctly.
+template <class T>
+struct ident {
+    using type = T;
+};
+template <class... KArgs>
+inline void launch_k(sa3k_ctx* c, bool last, void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
+                     typename ident<KArgs>::type... args) {
+    ++c->launch_seq;
+    if (last && c->tail_ev && c->stream == c->main_stream) {
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, c->stream, nullptr, c->tail_ev, 0, args...);
+        c->tail_seq = c->launch_seq;
+    } else {
+        kernel<<<grid, block, shmem, c->stream>>>(args...);
+    }
+}
+inline void fork_arm(sa3k_ctx* c) {
+    c->tail_ev = side_event(c);
+    c->tail_seq = 0;
+}
+inline void fork_fire(sa3k_ctx* c) {
+    hipEvent_t e = c->tail_ev;
+    c->tail_ev = nullptr;
+    if (c->tail_seq == 0 || c->tail_seq != c->launch_seq) SA3K_HIP(hipEventRecord(e, c->main_stream));
     SA3K_HIP(hipStreamWaitEvent(c->side_stream, e, 0));
 }
 // the main stream waits for everything enqueued on the second stream so far
