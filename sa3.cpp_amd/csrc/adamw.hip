@@ -254,6 +254,7 @@ SA3K_API int sa3k_adamw_clip(sa3k_ctx* ctx, float* param, const float* grad, flo
         if (grad_norm_out) {
             double r[2];
             SA3K_HIP(hipMemcpyAsync(r, ctx->adamw_result, sizeof r, hipMemcpyDeviceToHost, ctx->stream));
+            sa3k_note_main(ctx);
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
             *grad_norm_out = r[0];
         }
@@ -286,6 +287,7 @@ SA3K_API int sa3k_average_and_clip(sa3k_ctx* ctx, float* grad, int64_t n, int co
         if (grad_norm_out) {
             double r[2];
             SA3K_HIP(hipMemcpyAsync(r, ctx->adamw_result, sizeof r, hipMemcpyDeviceToHost, ctx->stream));
+            sa3k_note_main(ctx);
             SA3K_HIP(hipStreamSynchronize(ctx->stream));
             *grad_norm_out = r[0];
         }
@@ -296,6 +298,7 @@ SA3K_API int sa3k_adamw_clip_scale(sa3k_ctx* ctx, double* norm_out, float* scale
     return sa3k_guard(ctx, "sa3k_adamw_clip_scale", [&] {
         double r[2];
         SA3K_HIP(hipMemcpyAsync(r, ctx->adamw_result, sizeof r, hipMemcpyDeviceToHost, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
         if (norm_out) *norm_out = r[0];
         if (scale_out) *scale_out = (float)r[1];

@@ -497,7 +497,7 @@ void with_row_v(int dim, F&& f) {
 template <class... KArgs, class... Args>
 void launch(sa3k_ctx* ctx, const char* name, void (*kernel)(KArgs...), dim3 grid, Args&&... args) {
     KernelScope ks(ctx, name);
-    kernel<<<grid, kThreads, 0, ctx->stream>>>(std::forward<Args>(args)...);
+    launch_k(ctx, true, kernel, grid, dim3(kThreads), 0, std::forward<Args>(args)...);
     SA3K_LAUNCHED();
 }
 
@@ -563,6 +563,7 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
             if (bias && bias[t]) {
                 b->bias[t] = dalloc<float>((size_t)o);
                 SA3K_HIP(hipMemcpyAsync(b->bias[t], bias[t], o * 4, hipMemcpyDefault, ctx->stream));
+                sa3k_note_main(ctx);
             }
         }
         const size_t dim = cfg.dim;
@@ -572,6 +573,7 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
             SA3K_REQUIRE(vecs[i] != nullptr, "missing block vector");
             *dst[i] = dalloc<float>(len[i]);
             SA3K_HIP(hipMemcpyAsync(*dst[i], vecs[i], len[i] * 4, hipMemcpyDefault, ctx->stream));
+            sa3k_note_main(ctx);
         }
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     } catch (...) {
@@ -784,7 +786,8 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                        mv, sc_part, S, D, (int)N, dres, dxo, g_part, dgated);
             });
         };
-        // out = x2 + yf * s_f
+        // out = x2 + yf * s_f (its kernel records the fork of the column reduction that follows)
+        if (side_usable(ctx)) fork_arm(ctx);
         launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D / 4)), dout, mv, 5, S, D, (int)(N * D / 4), w->dyf);
         colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
         chk(ctx, sa3k_lin_backward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dyf, w->dg, 0, dA[6], dB[6], dmt[6]));
@@ -802,6 +805,7 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bq, (int)(N * H));
         PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
                        {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, w->dkv};
+        if (side_usable(ctx)) fork_arm(ctx);   // recorded by the next kernel, for the K/V projection
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(NC * H)), bk, (int)(NC * H));
         {   // the context K/V projection (Ctx tokens, small kernels) beside the query projection
             const bool side = side_usable(ctx);
@@ -811,7 +815,9 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                                        dmt[3]));
         }
         chk(ctx, sa3k_lin_backward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dqf, w->dhc, 0, dA[2], dB[2], dmt[2]));
-        // x1 = x + y * s_a: dy = dx1 * s_a comes out of the same pass
+        // x1 = x + y * s_a: dy = dx1 * s_a comes out of the same pass (which records the fork of
+        // the column reduction that follows)
+        if (side_usable(ctx)) fork_arm(ctx);
         norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, w->dy);
         colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
         chk(ctx, sa3k_lin_backward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dy, w->dob, 0, dA[1], dB[1], dmt[1]));

@@ -681,6 +681,7 @@ void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* targe
     d->count += B;
     if (loss_out) {
         SA3K_HIP(hipMemcpyAsync(loss_out, d->loss, sizeof(double) * B, hipMemcpyDeviceToHost, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     }
 }
@@ -751,6 +752,7 @@ SA3K_API int sa3k_dit_set_tensor(sa3k_ctx* ctx, sa3k_dit* dit, const char* name,
         Tensor& t = tensor(dit, name);
         SA3K_REQUIRE(bytes == (int64_t)t.bytes(), "byte count differs from the tensor's size: " + t.name);
         SA3K_HIP(hipMemcpyAsync(t.raw, data, t.bytes(), hipMemcpyDefault, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
@@ -925,6 +927,7 @@ SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, co
         forward(ctx, dit, x_t, t, cross, glob);
         const int64_t n = (int64_t)dit->tr.batch * dit->tr.frames * dit->cfg.io;
         SA3K_HIP(hipMemcpyAsync(velocity, dit->vel, sizeof(float) * n, hipMemcpyDeviceToDevice, ctx->stream));
+        sa3k_note_main(ctx);
     });
 }
 

@@ -1236,11 +1236,13 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
         }
         SA3K_HIP(hipMalloc(&g->dev, sizeof(PrepDesc) * n));
         SA3K_HIP(hipMemcpyAsync(g->dev, h.data(), sizeof(PrepDesc) * n, hipMemcpyHostToDevice, ctx->stream));
+        sa3k_note_main(ctx);
         for (int st = 0; st < kStages; ++st) {
             g->blocks[st] = (int)bm[st].size();
             SA3K_HIP(hipMalloc(&g->block_member[st], sizeof(int) * bm[st].size()));
             SA3K_HIP(hipMemcpyAsync(g->block_member[st], bm[st].data(), sizeof(int) * bm[st].size(),
                                     hipMemcpyHostToDevice, ctx->stream));
+            sa3k_note_main(ctx);
         }
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     } catch (...) {
@@ -1316,6 +1318,7 @@ SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out
             if (!data_on_device) {
                 SA3K_HIP(hipMalloc(&staging, raw_bytes));
                 SA3K_HIP(hipMemcpyAsync(staging, data, raw_bytes, hipMemcpyHostToDevice, ctx->stream));
+                sa3k_note_main(ctx);
                 src = staging;
             }
             if (type == SA3K_TYPE_Q8_0) {
@@ -1333,6 +1336,7 @@ SA3K_API int sa3k_weight_create(sa3k_ctx* ctx, int type, int64_t in, int64_t out
                 SA3K_HIP(hipMalloc(&w->w, (size_t)n * es));
                 SA3K_HIP(hipMalloc(&w->wt, (size_t)n * es));
                 SA3K_HIP(hipMemcpyAsync(w->w, src, (size_t)n * es, hipMemcpyDeviceToDevice, ctx->stream));
+                sa3k_note_main(ctx);
                 if (es == 4) transpose<uint32_t>(ctx, static_cast<uint32_t*>(w->w), static_cast<uint32_t*>(w->wt), out, in);
                 else transpose<uint16_t>(ctx, static_cast<uint16_t*>(w->w), static_cast<uint16_t*>(w->wt), out, in);
             }

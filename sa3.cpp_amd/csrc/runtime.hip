@@ -70,6 +70,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking));
         for (hipEvent_t& e : ctx->side_ev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_FORK_TAIL")) ctx->fork_tail = std::atoi(e) != 0;
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
@@ -84,13 +85,17 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipMalloc(&ctx->tile_counters, sizeof(int) * kMaxFixupTiles));
         SA3K_HIP(hipMemsetAsync(ctx->tile_counters, 0, sizeof(int) * kMaxFixupTiles, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipMalloc(&ctx->skinny_counters, sizeof(int) * 2 * kSkinnyMaxTiles));
         SA3K_HIP(hipMemsetAsync(ctx->skinny_counters, 0, sizeof(int) * 2 * kSkinnyMaxTiles, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipMalloc(&ctx->adamw_partials, sizeof(double) * kAdamwMaxBlocks));
         SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
         SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     });
     if (rc != SA3K_OK) {
@@ -156,6 +161,7 @@ SA3K_API int sa3k_upload(sa3k_ctx* ctx, void* dst, const void* src, size_t bytes
         if (!bytes) return;
         SA3K_REQUIRE(dst && src, "null pointer");
         SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+        sa3k_note_main(ctx);
         // pageable source: the runtime stages it, but keep the contract simple for callers that
         // reuse the host buffer right away
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
@@ -167,6 +173,7 @@ SA3K_API int sa3k_download(sa3k_ctx* ctx, void* dst, const void* src, size_t byt
         if (!bytes) return;
         SA3K_REQUIRE(dst && src, "null pointer");
         SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        sa3k_note_main(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
@@ -176,6 +183,7 @@ SA3K_API int sa3k_copy_d2d(sa3k_ctx* ctx, void* dst, const void* src, size_t byt
         if (!bytes) return;
         SA3K_REQUIRE(dst && src, "null pointer");
         SA3K_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+        sa3k_note_main(ctx);
     });
 }
 
@@ -184,6 +192,7 @@ SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
         if (!bytes) return;
         SA3K_REQUIRE(dst, "null pointer");
         SA3K_HIP(hipMemsetAsync(dst, value, bytes, ctx->stream));
+        sa3k_note_main(ctx);
     });
 }
 
@@ -208,6 +217,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_big") ctx->gemm_big = value;
         else if (n == "gemm_splits") ctx->gemm_splits = std::max(0, value);
         else if (n == "side_stream") ctx->use_side = value != 0;
+        else if (n == "fork_tail") ctx->fork_tail = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

@@ -43,9 +43,11 @@ struct sa3k_ctx {
     int side_ev_i = 0;
     int use_side = 1;                      // run independent chains on the second stream
     int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
+    int fork_tail = 1;                     // forks recorded by the producer kernel's completion (fork_arm)
     hipEvent_t tail_ev = nullptr;          // fork event armed for the producer about to launch (fork_arm)
-    uint64_t launch_seq = 0;               // launches made through launch_k
-    uint64_t tail_seq = 0;                 // launch_seq of the launch that last recorded tail_ev (0: none)
+    uint64_t tail_seq = 0;                 // main_seq right after the launch that last recorded tail_ev
+    uint64_t main_seq = 0;                 // operations enqueued on the main stream (note_main)
+    uint64_t side_synced = ~(uint64_t)0;   // main_seq up to which the second stream already waits
     std::string last_error;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     bool prof_on = false;
@@ -124,7 +126,14 @@ inline int sa3k_guard(sa3k_ctx* ctx, const char* fn, F&& body) {
 }
 
 // Launch-error check after a kernel launch on the context stream.
-#define SA3K_LAUNCHED() SA3K_HIP(hipGetLastError())
+// after every kernel launch (and, as note_main, after every async copy or fill): checks the launch
+// and counts work enqueued on the main stream, so a fork can tell whether the second stream already
+// waits for all of it
+#define SA3K_LAUNCHED()                   \
+    do {                                  \
+        SA3K_HIP(hipGetLastError());      \
+        sa3k_note_main(ctx);              \
+    } while (0)
 
 hipEvent_t prof_event(sa3k_ctx* ctx);
 void prof_collect(sa3k_ctx* ctx);
@@ -152,6 +161,10 @@ private:
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+inline void sa3k_note_main(sa3k_ctx* c) {
+    if (c->stream == c->main_stream) ++c->main_seq;
+}
+
 // ---- a second stream for independent chains of work (e.g. a column reduction beside the GEMM
 // that does not need it). Used only while launches go to the main stream, outside profiling
 // (per-kernel timing stays serial) and without in-kernel split reductions (their tile counters are
@@ -164,18 +177,24 @@ inline hipEvent_t side_event(sa3k_ctx* c) {
     c->side_ev_i = (c->side_ev_i + 1) % kSideEvents;
     return e;
 }
-// the second stream waits for everything enqueued on the main stream so far
+// the second stream waits for everything enqueued on the main stream so far (nothing to do when
+// nothing was enqueued there since the last fork)
+inline void fork_fire(sa3k_ctx* c);
 inline void side_fork(sa3k_ctx* c) {
+    if (c->tail_ev) return fork_fire(c);   // armed before the producer
+    if (c->side_synced == c->main_seq) return;
     hipEvent_t e = side_event(c);
     SA3K_HIP(hipEventRecord(e, c->main_stream));
     SA3K_HIP(hipStreamWaitEvent(c->side_stream, e, 0));
+    c->side_synced = c->main_seq;
 }
 // Fork after a producer without a separate event record (a marker packet on the main stream that
 // costs ~4.6 us; a kernel's own completion event costs ~0.9 us): fork_arm, then the producer's
 // launches through launch_k (the last of them passes last = true and records the armed event at
-// its completion), then fork_fire makes the second stream wait on it. fork_fire records the event
-// itself unless the most recent launch_k launch was the one that recorded it, so a producer path
-// that records nothing, or launches again after recording, still forks correctly.
+// its completion), then fork_fire (or side_fork) makes the second stream wait on it. The event is
+// used only if the recording launch is the last operation enqueued on the main stream (main_seq);
+// otherwise fork_fire records it itself, so a producer that records nothing, or anything enqueued
+// after the recording launch, still forks correctly.
 template <class T>
 struct ident {
     using type = T;
@@ -183,23 +202,25 @@ struct ident {
 template <class... KArgs>
 inline void launch_k(sa3k_ctx* c, bool last, void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
                      typename ident<KArgs>::type... args) {
-    ++c->launch_seq;
     if (last && c->tail_ev && c->stream == c->main_stream) {
         hipExtLaunchKernelGGL(kernel, grid, block, shmem, c->stream, nullptr, c->tail_ev, 0, args...);
-        c->tail_seq = c->launch_seq;
+        c->tail_seq = c->main_seq + 1;   // main_seq once the caller's SA3K_LAUNCHED() has counted it
     } else {
         kernel<<<grid, block, shmem, c->stream>>>(args...);
     }
 }
 inline void fork_arm(sa3k_ctx* c) {
+    if (!c->fork_tail) return;
     c->tail_ev = side_event(c);
-    c->tail_seq = 0;
+    c->tail_seq = ~(uint64_t)0;
 }
 inline void fork_fire(sa3k_ctx* c) {
+    if (!c->tail_ev) return side_fork(c);   // not armed (fork_tail off)
     hipEvent_t e = c->tail_ev;
     c->tail_ev = nullptr;
-    if (c->tail_seq == 0 || c->tail_seq != c->launch_seq) SA3K_HIP(hipEventRecord(e, c->main_stream));
+    if (c->tail_seq != c->main_seq) SA3K_HIP(hipEventRecord(e, c->main_stream));
     SA3K_HIP(hipStreamWaitEvent(c->side_stream, e, 0));
+    c->side_synced = c->main_seq;
 }
 // the main stream waits for everything enqueued on the second stream so far
 inline void side_join(sa3k_ctx* c) {
