@@ -106,6 +106,10 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "fork_tail"   1: the second stream waits on the completion event of the kernel that produces
  *                 its inputs (recorded by that kernel's launch) rather than on a separate event
  *                 record on the main stream (default 1)
+ *   "late_join"   1: in a DiT backward over resident activations, the second-stream work at the
+ *                 end of one block (its last column reduction and dA sums) runs beside the next
+ *                 block, which waits for it only before it rewrites the scratch that work reads
+ *                 (default 1)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big and gemm_splits, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);

@@ -54,7 +54,12 @@ void block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const fl
                    const float* const* mag, float scale, int dora);
 void block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* x, const float* context,
                    const float* gcond, float* out);
+// late_join: leave the second stream's last work of the block running past the return (its
+// completion is recorded in ctx->block_tail_ev and waited for before this workspace's scratch is
+// written again, by the next block_backward on a workspace that shares it); the caller joins the
+// second stream after its last block. Only for workspaces whose activations are not rewritten in
+// between (no recompute).
 void block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx, float* dcontext,
-                    float* dgcond, float* const* dA, float* const* dB, float* const* dm);
+                    float* dgcond, float* const* dA, float* const* dB, float* const* dm, bool late_join = false);
 
 }  // namespace sa3k

@@ -762,7 +762,8 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
 }
 
 void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const float* dout, float* dx,
-                          float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm) {
+                          float* dcontext, float* dgcond, float* const* dA, float* const* dB, float* const* dm,
+                          bool late_join) {
     {
         SA3K_REQUIRE(b && w && dout && dx && dcontext && dgcond && dA && dB, "null pointer");
         SA3K_REQUIRE(w->x != nullptr, "backward needs a preceding forward on this workspace");
@@ -827,10 +828,22 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                        {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
                        w->rq, w->dqkv};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bs, (int)(N * H));
+        // the previous block's last second-stream work (late_join) reads w->dh, written next
+        if (ctx->block_tail_pending) {
+            SA3K_HIP(hipStreamWaitEvent(ctx->main_stream, ctx->block_tail_ev, 0));
+            ctx->block_tail_pending = false;
+        }
         chk(ctx, sa3k_lin_backward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, w->dqkv, w->dh, 0, dA[0], dB[0], dmt[0]));
         colred(ctx, w, 0, w->dh, w->x, w->rs_a, b->pre_g, 0, 0);
         norm_bwd(w->dh, w->x, w->rs_a, b->pre_g, 0, w->dx1, dx, -1, nullptr);
-        if (side_usable(ctx)) side_join(ctx);
+        if (side_usable(ctx)) {
+            if (late_join) {   // the column reduction and dA sums of this block finish beside the next block
+                SA3K_HIP(hipEventRecord(ctx->block_tail_ev, ctx->side_stream));
+                ctx->block_tail_pending = true;
+            } else {
+                side_join(ctx);
+            }
+        }
         w->dssg = nullptr;
     }
 }

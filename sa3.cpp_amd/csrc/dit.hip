@@ -607,9 +607,13 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
             dB[t] = d->g + tg.off_b;
             dm[t] = d->tr.dora ? d->g + tg.off_m : nullptr;
         }
-        block_backward(ctx, d->blocks[l], w, dcur, dnext, d->dctx, d->dgcond, dA, dB, d->tr.dora ? dm : nullptr);
+        // resident activations: a block's last second-stream work may run on beside the next block
+        block_backward(ctx, d->blocks[l], w, dcur, dnext, d->dctx, d->dgcond, dA, dB, d->tr.dora ? dm : nullptr,
+                       ctx->late_join && !d->tr.recompute);
         std::swap(dcur, dnext);
     }
+    if (side_usable(ctx)) side_join(ctx);   // the head reads dgcond; AdamW reads every dA
+    ctx->block_tail_pending = false;
     // head backward (only adapter gradients are wanted: the inputs are data)
     if (d->tr.scope == SA3K_SCOPE_FULL) {
         launch(ctx, "dit_head", gather_frames_kernel, dim3(nblk(NT * D)), (const float*)dcur, B, T, c.mem_tokens, (int)D,

@@ -69,8 +69,10 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         ctx->main_stream = ctx->stream;
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking));
         for (hipEvent_t& e : ctx->side_ev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        SA3K_HIP(hipEventCreateWithFlags(&ctx->block_tail_ev, hipEventDisableTiming));
         if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_FORK_TAIL")) ctx->fork_tail = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_LATE_JOIN")) ctx->late_join = std::atoi(e) != 0;
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
@@ -119,6 +121,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->red_ws_side) (void)hipFree(ctx->red_ws_side);
     for (hipEvent_t e : ctx->side_ev)
         if (e) (void)hipEventDestroy(e);
+    if (ctx->block_tail_ev) (void)hipEventDestroy(ctx->block_tail_ev);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
     if (ctx->skinny_counters) (void)hipFree(ctx->skinny_counters);
@@ -218,6 +221,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "gemm_splits") ctx->gemm_splits = std::max(0, value);
         else if (n == "side_stream") ctx->use_side = value != 0;
         else if (n == "fork_tail") ctx->fork_tail = value != 0;
+        else if (n == "late_join") ctx->late_join = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

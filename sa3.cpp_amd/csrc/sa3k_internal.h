@@ -44,6 +44,9 @@ struct sa3k_ctx {
     int use_side = 1;                      // run independent chains on the second stream
     int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
     int fork_tail = 1;                     // forks recorded by the producer kernel's completion (fork_arm)
+    int late_join = 1;                     // a DiT block's last second-stream work may overlap the next block
+    hipEvent_t block_tail_ev = nullptr;    // second-stream work of a block backward left running (late_join)
+    bool block_tail_pending = false;       // block_tail_ev holds a record not yet waited for
     hipEvent_t tail_ev = nullptr;          // fork event armed for the producer about to launch (fork_arm)
     uint64_t tail_seq = 0;                 // main_seq right after the launch that last recorded tail_ev
     uint64_t main_seq = 0;                 // operations enqueued on the main stream (note_main)
