@@ -958,13 +958,6 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
 enum PrepStage { kStageConvert = 0, kStagePt = 1, kStageGram = 2, kStageTerms = 3, kStages = 4 };
 constexpr int kPtRows = 256;                  // rows of P^T per block (4 waves x 64)
 
-// 16 bytes of global memory. The group kernels read their pointers from descriptors in device
-// memory, so the compiler cannot infer the address space and would emit flat loads, which it waits
-// for together with LDS traffic (lgkmcnt(0)): every load in flight would be drained before the
-// first use of any of them.
-__device__ __forceinline__ bf16x8 ld_global16(const bf16* p) {
-    return *(const __attribute__((address_space(1))) bf16x8*)(p);
-}
 constexpr int kTermRows = 64;                 // DoRA rows per block (8 passes of 8)
 
 struct PrepDesc {
@@ -1030,22 +1023,32 @@ __global__ __launch_bounds__(kThreads) void group_pt_kernel(const PrepDesc* __re
     const int64_t o0 = (int64_t)(blockIdx.x - q.blk0[kStagePt]) * kPtRows + wave * 64;
     if (o0 >= q.out) return;   // wave-uniform
     constexpr int WR = 4;
-    const bf16* wrow[WR];
+    // buffer loads: the member's W and Ac in two descriptors (extents checked on the host to fit
+    // 31 bits), a loop-invariant 32-bit byte offset per lane and row, the chunk's K in the scalar
+    // offset; the last rows are clamped to the last valid row (their results are not stored)
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(q.W), (short)0, (int)((int64_t)q.out * q.in * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(q.Ac, (short)0, (int)((int64_t)r * q.in * 2), 0x00020000);
+    uint32_t wof[WR];
 #pragma unroll
-    for (int j = 0; j < WR; ++j) wrow[j] = q.W + std::min<int64_t>(o0 + 16 * j + r16, q.out - 1) * q.in + 8 * g;
-    const bf16* a0row = q.Ac + (int64_t)min(r16, r - 1) * q.in + 8 * g;
-    const bf16* a1row = q.Ac + (int64_t)min(16 + r16, r - 1) * q.in + 8 * g;
+    for (int j = 0; j < WR; ++j) wof[j] = (uint32_t)((std::min<int64_t>(o0 + 16 * j + r16, q.out - 1) * q.in + 8 * g) * 2);
+    const uint32_t a0of = (uint32_t)(((int64_t)min(r16, r - 1) * q.in + 8 * g) * 2);
+    const uint32_t a1of = (uint32_t)(((int64_t)min(16 + r16, r - 1) * q.in + 8 * g) * 2);
     struct Set {
         bf16x8 w[2][WR], a0[2], a1[2];
     };
+    auto ld16 = [](__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so) {
+        return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)so, 0));
+    };
     auto load = [&](Set& S, int c) {   // chunk c: K [64c, 64c + 64), two K32 steps
-        const int64_t k = (int64_t)c * 64;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
+            const uint32_t ko = (uint32_t)(c * 64 + 32 * st) * 2;   // wave-uniform
 #pragma unroll
-            for (int j = 0; j < WR; ++j) S.w[st][j] = ld_global16(wrow[j] + k + 32 * st);
-            S.a0[st] = ld_global16(a0row + k + 32 * st);
-            if (HI) S.a1[st] = ld_global16(a1row + k + 32 * st);
+            for (int j = 0; j < WR; ++j) S.w[st][j] = ld16(rw, wof[j], ko);
+            S.a0[st] = ld16(ra, a0of, ko);
+            if (HI) S.a1[st] = ld16(ra, a1of, ko);
         }
     };
     f32x4 acc[WR][2];
@@ -1217,6 +1220,7 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
             SA3K_REQUIRE(A[i] && B[i] && (!dora || (mag[i] && bnsq[i])), "missing adapter pointer");
             const int64_t in = L->W->in, out = L->W->out;
             SA3K_REQUIRE(out % 64 == 0 || out % 16 == 0, "group output dimension must be a multiple of 16");
+            SA3K_REQUIRE((int64_t)out * in * 2 < ((int64_t)1 << 31), "group member weight above 2 GiB");
             PrepDesc& q = h[i];
             q.A = A[i]; q.B = B[i]; q.mag = dora ? mag[i] : nullptr; q.bnsq = dora ? bnsq[i] : nullptr;
             q.Ac = static_cast<bf16*>(L->Ac); q.At = static_cast<bf16*>(L->At);
