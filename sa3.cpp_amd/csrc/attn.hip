@@ -454,47 +454,51 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const float* sd1 = vec[st][2];
         const float* sd2 = vec[st][3];
         // per 16-query tile qt: S1, S2, dP with rows = queries qt*16 + 4g + v, col = key
-        bf16x8 pd[2], ds1[2], ds2[2];    // (P1 - P2), dS1, dS2 as B operands over query pairs
         const bool full = block_full(qb, kb, a.Sq, a.Sk, a.window);   // block-uniform: no masking
         const int rel = qb * BLK + 4 * g - qsp.lo;   // query qt*16 + 4g + v, less lo, is rel + 16 qt + v
+        // one 32-query chunk at a time (fewer live registers): its two 16-query tiles give
+        // (P1 - P2), dS1, dS2 as B operands over 8 queries per lane group, then
+        // dV^T += dO^T (P1 - P2); dK_i^T += Q_i^T dS_i  (A: transposed tiles)
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
-            f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
+        for (int ch = 0; ch < 2; ++ch) {
+            bf16x8 pd, ds1, ds2;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                s1 = mfma(ld_row(q1s, qt * 16 + r, ks * 4 + g), k1f[ks], s1);
-                s2 = mfma(ld_row(q2s, qt * 16 + r, ks * 4 + g), k2f[ks], s2);
-                dp = mfma(ld_row(dos, qt * 16 + r, ks * 4 + g), vf[ks], dp);
-            }
-            if (!full) {   // hidden pairs get score -inf, hence weight 0 and dS 0
+            for (int qq = 0; qq < 2; ++qq) {
+                const int qt = 2 * ch + qq;
+                f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, dp = s1;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    s1 = mfma(ld_row(q1s, qt * 16 + r, ks * 4 + g), k1f[ks], s1);
+                    s2 = mfma(ld_row(q2s, qt * 16 + r, ks * 4 + g), k2f[ks], s2);
+                    dp = mfma(ld_row(dos, qt * 16 + r, ks * 4 + g), vf[ks], dp);
+                }
+                if (!full) {   // hidden pairs get score -inf, hence weight 0 and dS 0
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const bool ok = (unsigned)(rel + 16 * qt + v) < (unsigned)qsp.n;
+                        s1[v] = ok ? s1[v] : -INFINITY;
+                        s2[v] = ok ? s2[v] : -INFINITY;
+                    }
+                }
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const bool ok = (unsigned)(rel + 16 * qt + v) < (unsigned)qsp.n;
-                    s1[v] = ok ? s1[v] : -INFINITY;
-                    s2[v] = ok ? s2[v] : -INFINITY;
+                    const int ql = qt * 16 + 4 * g + v;
+                    const float p1 = ex2(fmaf(s1[v], c, -sl1[ql]));
+                    const float p2 = ex2(fmaf(s2[v], c, -sl2[ql]));
+                    const int e = qq * 4 + v;
+                    pd[e] = (bf16)(p1 - p2);
+                    ds1[e] = (bf16)(p1 * (dp[v] - sd1[ql]));
+                    ds2[e] = (bf16)(-p2 * (dp[v] - sd2[ql]));
                 }
             }
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int ql = qt * 16 + 4 * g + v;
-                const float p1 = ex2(fmaf(s1[v], c, -sl1[ql]));
-                const float p2 = ex2(fmaf(s2[v], c, -sl2[ql]));
-                const int e = (qt & 1) * 4 + v;
-                pd[qt >> 1][e] = (bf16)(p1 - p2);
-                ds1[qt >> 1][e] = (bf16)(p1 * (dp[v] - sd1[ql]));
-                ds2[qt >> 1][e] = (bf16)(-p2 * (dp[v] - sd2[ql]));
-            }
-        }
-        // dV^T += dO^T (P1 - P2); dK_i^T += Q_i^T dS_i  (A: transposed tiles, 8 queries per lane group)
-#pragma unroll
-        for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 const int c0 = 32 * ch + 4 * g, c1 = 32 * ch + 16 + 4 * g;
-                dvt[dt] = mfma(cat44(ld_tr(dos, c0, dt * 16, lane), ld_tr(dos, c1, dt * 16, lane)), pd[ch], dvt[dt]);
-                dk1t[dt] = mfma(cat44(ld_tr(q1s, c0, dt * 16, lane), ld_tr(q1s, c1, dt * 16, lane)), ds1[ch], dk1t[dt]);
-                dk2t[dt] = mfma(cat44(ld_tr(q2s, c0, dt * 16, lane), ld_tr(q2s, c1, dt * 16, lane)), ds2[ch], dk2t[dt]);
+                dvt[dt] = mfma(cat44(ld_tr(dos, c0, dt * 16, lane), ld_tr(dos, c1, dt * 16, lane)), pd, dvt[dt]);
+                dk1t[dt] = mfma(cat44(ld_tr(q1s, c0, dt * 16, lane), ld_tr(q1s, c1, dt * 16, lane)), ds1, dk1t[dt]);
+                dk2t[dt] = mfma(cat44(ld_tr(q2s, c0, dt * 16, lane), ld_tr(q2s, c1, dt * 16, lane)), ds2, dk2t[dt]);
             }
+        }
     }
     if (key >= a.Sk) return;
     if (a.qsplit > 1) {
