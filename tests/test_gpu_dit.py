@@ -169,13 +169,18 @@ def test_dit_graph_replays_match_eager(ctx):
 
 def test_dit_side_stream_matches_one_stream(ctx):
     # the backward kernels forked to the context's second stream give the one-stream results bit for
-    # bit, over two updates (adapter refresh and AdamW in between)
+    # bit, over two updates (adapter refresh and AdamW in between): with forks recorded by the
+    # producer kernels or by separate event records, and with each block's last second-stream work
+    # joined at the block's end or overlapping the next block (two blocks)
     cfg = dict(CFG, window=5)
     tensors, adapters, inputs = db.random_dit(46, cfg, "full")
+    schedules = [dict(side_stream=0), dict(side_stream=1, fork_tail=0, late_join=0),
+                 dict(side_stream=1, fork_tail=1, late_join=0), dict(side_stream=1, fork_tail=1, late_join=1)]
     res = []
     try:
-        for side in (0, 1):
-            ctx.set_option("side_stream", side)
+        for sched in schedules:
+            for k, v in sched.items():
+                ctx.set_option(k, v)
             d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
             up, _ = upload_inputs(ctx, inputs)
             out = []
@@ -187,9 +192,11 @@ def test_dit_side_stream_matches_one_stream(ctx):
             res.append(out)
             d.destroy()
     finally:
-        ctx.set_option("side_stream", 1)
-    for a, b in zip(res[0], res[1]):
-        assert np.array_equal(a, b), "second stream changes the results"
+        for k in ("side_stream", "fork_tail", "late_join"):
+            ctx.set_option(k, 1)
+    for sched, r in zip(schedules[1:], res[1:]):
+        for a, b in zip(res[0], r):
+            assert np.array_equal(a, b), f"stream schedule {sched} changes the results"
 
 
 def test_dit_in_kernel_reductions_match_separate_launches(ctx):
