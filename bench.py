@@ -485,8 +485,8 @@ def main():
                          "known traffic that scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the data-parallel design is described in DESIGN.md).", file=sys.stderr)
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
+              "(data-parallel sharding of the update over ranks is not implemented).", file=sys.stderr)
         sys.exit(2)
 
     sa3k = _load("sa3k", os.path.join(ROOT, "sa3.cpp_amd", "sa3k.py"))
