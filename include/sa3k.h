@@ -197,6 +197,21 @@ SA3K_API int sa3k_gemm_nt(sa3k_ctx* ctx, int prec, int a_type, const void* A, in
                           int64_t M, int64_t N, int64_t K, float alpha, const float* colscale,
                           const float* bias, float* C, int64_t ldc, int accumulate);
 
+/* sa3k_gemm_nt for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No reference counterpart: ggml allocates
+ * its graphs up front (src/train_ckpt.h), and this entry point serves those callers instead.
+ * Same arguments, kernels and results (bit for bit) as sa3k_gemm_nt, but the split-K partial sums
+ * go to a fixed 32 MiB scratch array in device memory that the library's code object carries (one
+ * copy per GPU, held until the process ends), and the call never allocates. Every split plan the
+ * dispatch chooses by itself fits; a plan that would need more (only possible when the
+ * "gemm_splits" option forces a split count) fails with SA3K_ERR_INVALID before anything is
+ * launched. All calls on one GPU share that array, from every context: calls that overlap on one
+ * GPU (two streams, two contexts, two threads) race and must be serialised by the caller. */
+SA3K_API int sa3k_gemm_nt_noalloc(sa3k_ctx* ctx, int prec, int a_type, const void* A, int64_t lda,
+                                  int b_type, const void* B, int64_t ldb, const void* B_scales, int64_t ldbs,
+                                  int64_t M, int64_t N, int64_t K, float alpha, const float* colscale,
+                                  const float* bias, float* C, int64_t ldc, int accumulate);
+
 /* ---------------------------------------------------------------- frozen base weights */
 
 typedef struct sa3k_weight sa3k_weight;

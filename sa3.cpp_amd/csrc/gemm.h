@@ -83,5 +83,8 @@ bool gemm_skinny_ok(const sa3k_ctx* ctx, const GemmDesc& d);
 void gemm_run_skinny(sa3k_ctx* ctx, const GemmDesc& d);
 // split-K partial-sum workspace owned by the context (grows on demand)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);
+// Look up this device's copy of the allocation-free entry point's scratch array (once per
+// device, with the context's device current) and keep its address in the context.
+void gemm_noalloc_setup(sa3k_ctx* ctx);
 
 }  // namespace sa3k

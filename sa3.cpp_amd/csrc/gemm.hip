@@ -2,6 +2,7 @@
 #include "gemm.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace sa3k {
 namespace {
@@ -37,8 +38,45 @@ struct KParams {
 
 }  // namespace
 
+// Scratch of sa3k_gemm_nt_noalloc: the split-K partial sums of one GEMM, in device memory that
+// the code object itself carries (no hipMalloc at any call). 32 MiB covers every split plan the
+// dispatch chooses by itself: a GEMM splits only while its tiles fill fewer than the chip's
+// resident slots (512 for 128 x 128 tiles), so splits x tiles x 128 x 128 floats <= 2^23.
+// Every GPU that loads the library holds its own copy until the process ends.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 23;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};   // per device: its copy of `scratch`
+}  // namespace
+
+void gemm_noalloc_setup(sa3k_ctx* ctx) {
+    SA3K_REQUIRE(ctx->device >= 0 && ctx->device < kMaxDevices, "device ordinal beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    float*& ptr = g_scratch_dev[ctx->device];
+    if (!ptr) {
+        // the host-side name of the array is only a stand-in: the device address comes from the
+        // runtime, with this device current (sa3k_create has selected it)
+        void* p = nullptr;
+        SA3K_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        SA3K_REQUIRE(p != nullptr, "no device address for the GEMM scratch array");
+        ptr = static_cast<float*>(p);
+    }
+    ctx->noalloc_scratch = ptr;
+}
+
 // split-K workspace owned by the context (grows on demand; kernels on one stream use it in turn)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes) {
+    if (ctx->ws_fixed) {
+        // a caller that cannot allocate: the fixed buffer or an error, never a hipMalloc
+        if (bytes > ctx->ws_fixed_bytes)
+            sa3k_throw(SA3K_ERR_INVALID, "split-K partials need " + std::to_string(bytes) +
+                                             " bytes of scratch, more than the " +
+                                             std::to_string(ctx->ws_fixed_bytes) + " bytes available");
+        return ctx->ws_fixed;
+    }
     // one workspace per stream: work on the second stream runs beside the main stream's
     const bool side = ctx->stream == ctx->side_stream;
     void*& ws = side ? ctx->gemm_ws_side : ctx->gemm_ws;
@@ -527,6 +565,54 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
 }  // namespace sa3k
 
 // ---------------------------------------------------------------------------------- C ABI
+namespace sa3k {
+namespace {
+
+GemmDesc gemm_nt_desc(int prec, int a_type, const void* A, int64_t lda, int b_type, const void* B, int64_t ldb,
+                      const void* B_scales, int64_t ldbs, int64_t M, int64_t N, int64_t K, float alpha,
+                      const float* colscale, const float* bias, float* C, int64_t ldc, int accumulate) {
+    auto src_of = [](int t, bool transposed_q8) -> int {
+        switch (t) {
+            case SA3K_TYPE_BF16: return SRC_BF16;
+            case SA3K_TYPE_F16: return SRC_F16;
+            case SA3K_TYPE_F32: return SRC_F32;
+            case SA3K_TYPE_Q8_0: return transposed_q8 ? SRC_Q8T : SRC_Q8;
+        }
+        sa3k_throw(SA3K_ERR_UNSUPPORTED, "unknown operand type");
+        return 0;
+    };
+    GemmDesc d;
+    d.prec = prec;
+    d.a_src = src_of(a_type, false);
+    d.b_src = src_of(b_type < 0 ? SA3K_TYPE_Q8_0 : b_type, b_type < 0);
+    d.A = A; d.lda = lda; d.B = B; d.ldb = ldb; d.Bs = B_scales; d.ldbs = ldbs;
+    d.M = M; d.N = N; d.K = K; d.alpha = alpha; d.colscale = colscale; d.bias = bias;
+    d.C = C; d.ldc = ldc; d.accumulate = accumulate;
+    return d;
+}
+
+// For the duration of one call: split-K partials go to the device's scratch array and split sums
+// are reduced by the separate launch (the in-kernel reduction's tile counters are not used).
+struct FixedScratchScope {
+    sa3k_ctx* c;
+    int fixup;
+    explicit FixedScratchScope(sa3k_ctx* ctx) : c(ctx), fixup(ctx->gemm_fixup) {
+        c->ws_fixed = c->noalloc_scratch;
+        c->ws_fixed_bytes = kNoAllocScratchFloats * sizeof(float);
+        c->gemm_fixup = 0;
+    }
+    ~FixedScratchScope() {
+        c->ws_fixed = nullptr;
+        c->ws_fixed_bytes = 0;
+        c->gemm_fixup = fixup;
+    }
+    FixedScratchScope(const FixedScratchScope&) = delete;
+    FixedScratchScope& operator=(const FixedScratchScope&) = delete;
+};
+
+}  // namespace
+}  // namespace sa3k
+
 extern "C" SA3K_API int sa3k_gemm_nt(sa3k_ctx* ctx, int prec, int a_type, const void* A, int64_t lda,
                                      int b_type, const void* B, int64_t ldb, const void* B_scales,
                                      int64_t ldbs, int64_t M, int64_t N, int64_t K, float alpha,
@@ -534,23 +620,24 @@ extern "C" SA3K_API int sa3k_gemm_nt(sa3k_ctx* ctx, int prec, int a_type, const 
                                      int accumulate) {
     using namespace sa3k;
     return sa3k_guard(ctx, "sa3k_gemm_nt", [&] {
-        auto src_of = [](int t, bool transposed_q8) -> int {
-            switch (t) {
-                case SA3K_TYPE_BF16: return SRC_BF16;
-                case SA3K_TYPE_F16: return SRC_F16;
-                case SA3K_TYPE_F32: return SRC_F32;
-                case SA3K_TYPE_Q8_0: return transposed_q8 ? SRC_Q8T : SRC_Q8;
-            }
-            sa3k_throw(SA3K_ERR_UNSUPPORTED, "unknown operand type");
-            return 0;
-        };
-        GemmDesc d;
-        d.prec = prec;
-        d.a_src = src_of(a_type, false);
-        d.b_src = src_of(b_type < 0 ? SA3K_TYPE_Q8_0 : b_type, b_type < 0);
-        d.A = A; d.lda = lda; d.B = B; d.ldb = ldb; d.Bs = B_scales; d.ldbs = ldbs;
-        d.M = M; d.N = N; d.K = K; d.alpha = alpha; d.colscale = colscale; d.bias = bias;
-        d.C = C; d.ldc = ldc; d.accumulate = accumulate;
+        const GemmDesc d = gemm_nt_desc(prec, a_type, A, lda, b_type, B, ldb, B_scales, ldbs, M, N, K, alpha,
+                                        colscale, bias, C, ldc, accumulate);
+        gemm_run(ctx, d, "gemm_nt");
+    });
+}
+
+extern "C" SA3K_API int sa3k_gemm_nt_noalloc(sa3k_ctx* ctx, int prec, int a_type, const void* A, int64_t lda,
+                                             int b_type, const void* B, int64_t ldb, const void* B_scales,
+                                             int64_t ldbs, int64_t M, int64_t N, int64_t K, float alpha,
+                                             const float* colscale, const float* bias, float* C, int64_t ldc,
+                                             int accumulate) {
+    using namespace sa3k;
+    return sa3k_guard(ctx, "sa3k_gemm_nt_noalloc", [&] {
+        SA3K_REQUIRE(ctx->noalloc_scratch != nullptr, "the device scratch array was not set up");
+        SA3K_REQUIRE(ctx->stream == ctx->main_stream, "called while work is routed to the second stream");
+        const GemmDesc d = gemm_nt_desc(prec, a_type, A, lda, b_type, B, ldb, B_scales, ldbs, M, N, K, alpha,
+                                        colscale, bias, C, ldc, accumulate);
+        FixedScratchScope scope(ctx);
         gemm_run(ctx, d, "gemm_nt");
     });
 }

@@ -1,5 +1,6 @@
 // Context, device memory and stream timing for the sa3k C ABI.
 #include "sa3k_internal.h"
+#include "gemm.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -98,6 +99,8 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipMalloc(&ctx->adamw_result, sizeof(double) * 2));
         SA3K_HIP(hipMemsetAsync(ctx->adamw_result, 0, sizeof(double) * 2, ctx->stream));
         sa3k_note_main(ctx);
+        // this device's address of the allocation-free GEMM's scratch array
+        sa3k::gemm_noalloc_setup(ctx);
         SA3K_HIP(hipStreamSynchronize(ctx->stream));
     });
     if (rc != SA3K_OK) {

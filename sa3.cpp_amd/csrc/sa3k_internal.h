@@ -85,6 +85,13 @@ struct sa3k_ctx {
                                           // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
     void* zero_page = nullptr;            // 256 zero bytes
+    // This device's address of the file-scope scratch array of the allocation-free GEMM entry
+    // point (gemm.hip), looked up once per device when the context is created.
+    float* noalloc_scratch = nullptr;
+    // While set, the split-K partials of GEMMs on this context go to this fixed buffer of
+    // ws_fixed_bytes instead of the growing workspace (a launch that needs more fails).
+    float* ws_fixed = nullptr;
+    size_t ws_fixed_bytes = 0;
 };
 
 // An error that carries an sa3k status code across the internal call chain; every C entry point

@@ -94,6 +94,7 @@ def _declare(lib):
         "sa3k_q8_0_dequant": (I, [P, P, P, I64]),
         "sa3k_q8_0_quantize": (I, [P, P, P, I64]),
         "sa3k_gemm_nt": (I, [P, I, I, P, I64, I, P, I64, P, I64, I64, I64, I64, F, P, P, P, I64, I]),
+        "sa3k_gemm_nt_noalloc": (I, [P, I, I, P, I64, I, P, I64, P, I64, I64, I64, I64, F, P, P, P, I64, I]),
         "sa3k_weight_create": (I, [P, I, I64, I64, P, I, C.POINTER(P)]),
         "sa3k_weight_destroy": (I, [P, P]),
         "sa3k_weight_drop_working_copy": (I, [P, P]),
@@ -305,8 +306,10 @@ class Context:
 
     # -- GEMM
     def gemm_nt(self, A, B, M, N, K, prec=PREC_BF16, a_type=TYPE_F32, b_type=TYPE_F32, lda=None, ldb=None,
-                B_scales=None, ldbs=0, alpha=1.0, colscale=None, bias=None, C=None, ldc=None, accumulate=False):
-        self.check(self.lib.sa3k_gemm_nt(
+                B_scales=None, ldbs=0, alpha=1.0, colscale=None, bias=None, C=None, ldc=None, accumulate=False,
+                noalloc=False):
+        fn = self.lib.sa3k_gemm_nt_noalloc if noalloc else self.lib.sa3k_gemm_nt
+        self.check(fn(
             self.h, prec, a_type, A.ptr, lda if lda is not None else K, b_type, B.ptr,
             ldb if ldb is not None else K, B_scales.ptr if B_scales is not None else None, ldbs,
             M, N, K, alpha, colscale.ptr if colscale is not None else None,
