@@ -507,7 +507,8 @@ def main():
         wl.step()
     ctx.sync()
     # timed region: K steps bracketed by stream events (single process: the barrier is a no-op);
-    # per-kernel event timing is off here, so the DiT step replays its captured HIP graph
+    # per-kernel event timing is off here, so the DiT step runs eagerly on the library's two
+    # streams (HIP-graph replay is an option of the library, off by default)
     log(f"timing {a.steps} steps")
     ctx.sync()
     t0 = time.perf_counter()

@@ -66,6 +66,8 @@ struct TensorInfo {
     std::vector<int64_t> ne;
     uint32_t type = kTensorF32;
     uint64_t offset = 0;   // into the data section
+    // element count; the parser has checked that every extent is in [1, 2^62) and that their
+    // product fits in int64
     int64_t elements() const {
         int64_t n = 1;
         for (int64_t e : ne) n *= e;
@@ -204,11 +206,13 @@ public:
             err = "tensor " + t.name + ": unsupported type " + std::to_string(t.type);
             return false;
         }
-        const uint64_t start = data_ + t.offset;
-        if (n < 0 || t.offset > buf_.size() || start > buf_.size() || (uint64_t)n > (buf_.size() - start) / esz) {
+        // offset and n * esz must both stay inside the data section (no wrap-around)
+        if (n <= 0 || data_ > buf_.size() || t.offset > buf_.size() - data_ ||
+            (uint64_t)n > (buf_.size() - data_ - t.offset) / esz) {
             err = "tensor " + t.name + ": data past the end of the file";
             return false;
         }
+        const uint64_t start = data_ + t.offset;
         out.resize((size_t)n);
         if (esz == 4) {
             std::memcpy(out.data(), buf_.data() + start, (size_t)n * 4);
@@ -311,7 +315,13 @@ private:
             uint32_t type;
             Value v;
             if (!get_str(key) || !get(type) || !get_value(type, v)) return false;
-            if (key == "general.alignment" && type == kU32 && v.u != 0) alignment = v.u;
+            if (key == "general.alignment" && type == kU32) {
+                if (v.u == 0 || (v.u & (v.u - 1)) != 0) {
+                    err_ = "general.alignment is not a power of two";
+                    return false;
+                }
+                alignment = v.u;
+            }
             kv_.emplace_back(key, v);
         }
         for (uint64_t k = 0; k < n_tensors; ++k) {
@@ -323,9 +333,14 @@ private:
                 return false;
             }
             t.ne.resize(nd);
+            int64_t count = 1;
             for (uint32_t d = 0; d < nd; ++d) {
                 uint64_t e;
                 if (!get(e)) return false;
+                if (e == 0 || e >= ((uint64_t)1 << 62) || __builtin_mul_overflow(count, (int64_t)e, &count)) {
+                    err_ = "tensor " + t.name + ": bad extent";
+                    return false;
+                }
                 t.ne[d] = (int64_t)e;
             }
             if (!get(t.type) || !get(t.offset)) return false;

@@ -196,7 +196,7 @@ inline bool run_train_dit_accumulate(TrainDitGraph& graph, const TrainLoraState&
     }
     const size_t nx = (size_t)dc.io * graph.frames;
     if (sample.x_t.size() != nx || sample.velocity_target.size() != nx ||
-        cond.cross.size() < (size_t)graph.cond_dim * graph.ctx_len || cond.global.size() != (size_t)graph.cond_dim) {
+        cond.cross.size() != (size_t)graph.cond_dim * graph.ctx_len || cond.global.size() != (size_t)graph.cond_dim) {
         err = "training step inputs do not match the graph's dimensions";
         return false;
     }

@@ -211,3 +211,32 @@ def test_full_scope_adapter_write_read_time(tool, tmp_path):
     r = subprocess.run([tool, "bench", str(tmp_path / "big.gguf")], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     print(r.stdout.strip())
+
+
+@pytest.mark.parametrize("patch", ["zero_extent", "huge_extent", "product_overflow", "offset_wrap", "offset_past_end",
+                                   "alignment"])
+def test_rejects_malformed_extents_and_offsets(tool, tmp_path, patch):
+    # tensor infos from an untrusted file: extents must be in [1, 2^62) with an int64 product, and
+    # offset + bytes must stay inside the data section; the alignment must be a power of two
+    path = str(tmp_path / "m.gguf")
+    write_gguf(path, [("general.alignment", 4, 32), ("lora.rank", 4, 2), ("lora.alpha", 6, 1.0)],
+               [("x.lora_A", [4, 2], np.zeros(8, np.float32)), ("x.lora_B", [2, 3], np.zeros(6, np.float32))])
+    data = bytearray(open(path, "rb").read())
+    i = data.find(b"x.lora_A") + 8 + 4          # the first extent of x.lora_A
+    ty_off = i + 16                              # type, then the u64 offset
+    if patch == "zero_extent":
+        data[i:i + 8] = struct.pack("<Q", 0)
+    elif patch == "huge_extent":
+        data[i:i + 8] = struct.pack("<Q", 1 << 62)
+    elif patch == "product_overflow":
+        data[i:i + 16] = struct.pack("<QQ", (1 << 61) + 1, 1 << 4)
+    elif patch == "offset_wrap":
+        data[ty_off + 4:ty_off + 12] = struct.pack("<Q", (1 << 64) - 16)
+    elif patch == "offset_past_end":
+        data[ty_off + 4:ty_off + 12] = struct.pack("<Q", len(data))
+    else:
+        j = data.find(b"general.alignment") + len(b"general.alignment") + 4
+        data[j:j + 4] = struct.pack("<I", 48)
+    open(path, "wb").write(bytes(data))
+    rc, lines = summary(tool, path)
+    assert rc == 1, lines
