@@ -52,47 +52,54 @@ struct TrainLoraScope {
 
 inline bool train_lora_scope_known(const std::string& s) { return s == "full" || s == "core"; }
 
+namespace detail {
+inline bool ends_with(const std::string& s, const std::string& suffix) {
+    return s.size() >= suffix.size() && std::equal(suffix.rbegin(), suffix.rend(), s.rbegin());
+}
+inline bool contains_any(const std::string& s, const std::vector<std::string>& parts) {
+    return std::any_of(parts.begin(), parts.end(),
+                       [&](const std::string& p) { return s.find(p) != std::string::npos; });
+}
+}  // namespace detail
+
+// A per-block tensor is named "dit.<block index>.<rest>": a non-empty run of decimal digits right
+// after the "dit." prefix, closed by a dot (src/train_lora.h:64-75).
 inline bool train_lora_is_block_weight(const std::string& name) {
-    size_t i = 4;   // past "dit."
-    if (name.size() <= i || !std::isdigit((unsigned char)name[i])) return false;
-    while (i < name.size() && std::isdigit((unsigned char)name[i])) i++;
-    return i < name.size() && name[i] == '.';
+    constexpr size_t kPrefix = 4;   // "dit."
+    const size_t digits_end = name.find_first_not_of("0123456789", kPrefix);
+    return digits_end != std::string::npos && digits_end > kPrefix && name[digits_end] == '.';
 }
 
+// Scope rules (src/train_lora.h:77-97): "core" keeps only per-block tensors and drops the inpaint
+// local-conditioning branch; then a non-empty include list needs one matching substring, and any
+// matching exclude substring drops the weight.
 inline bool train_lora_target_selected(const std::string& name, const TrainLoraScope& scope) {
-    if (scope.name == "core") {
-        if (!train_lora_is_block_weight(name)) return false;
-        if (name.find(".local.") != std::string::npos) return false;
-    }
-    if (!scope.include.empty()) {
-        bool hit = false;
-        for (const std::string& p : scope.include)
-            if (name.find(p) != std::string::npos) { hit = true; break; }
-        if (!hit) return false;
-    }
-    for (const std::string& p : scope.exclude)
-        if (name.find(p) != std::string::npos) return false;
-    return true;
+    const bool in_scope = scope.name != "core" ||
+                          (train_lora_is_block_weight(name) && name.find(".local.") == std::string::npos);
+    const bool included = scope.include.empty() || detail::contains_any(name, scope.include);
+    return in_scope && included && !detail::contains_any(name, scope.exclude);
 }
 
-// every selected 2-D dit.*.weight, sorted by name (src/train_lora.h:99-121)
+// The adapter targets (src/train_lora.h:99-121): every 2-D tensor named dit.*.weight that the scope
+// selects, with in = ne0 and out = ne1, in ascending order of weight name (which fixes the order of
+// the trained state and of the optimizer moments).
 inline std::vector<TrainLoraTarget> enumerate_train_lora_targets(const DitModel& dit, const TrainLoraScope& scope = {}) {
-    std::vector<TrainLoraTarget> out;
+    static const std::string kSuffix = ".weight";
+    std::vector<TrainLoraTarget> targets;
     for (const std::string& name : dit.tensor_names()) {
-        if (name.rfind("dit.", 0) != 0) continue;
-        if (name.size() < 7 || name.compare(name.size() - 7, 7, ".weight") != 0) continue;
-        if (!dit.is_2d(name)) continue;
-        if (!train_lora_target_selected(name, scope)) continue;
+        const bool candidate = name.compare(0, 4, "dit.") == 0 && detail::ends_with(name, kSuffix) &&
+                               dit.is_2d(name) && train_lora_target_selected(name, scope);
+        if (!candidate || dit.ne0(name) <= 0 || dit.ne1(name) <= 0) continue;
         TrainLoraTarget t;
         t.weight_name = name;
-        t.stem = name.substr(0, name.size() - 7);
+        t.stem = name.substr(0, name.size() - kSuffix.size());
         t.in = dit.ne0(name);
         t.out = dit.ne1(name);
-        if (t.in > 0 && t.out > 0) out.push_back(t);
+        targets.push_back(std::move(t));
     }
-    std::sort(out.begin(), out.end(),
+    std::sort(targets.begin(), targets.end(),
               [](const TrainLoraTarget& a, const TrainLoraTarget& b) { return a.weight_name < b.weight_name; });
-    return out;
+    return targets;
 }
 
 // Row norms of a host weight W [out][in] (the reference's ggml_tensor argument, src/train_lora.h:
