@@ -367,3 +367,13 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
 }
 
 }  // extern "C"
+
+// exported for the oracle's own tests: rope_vec over n head vectors of 64 floats at positions pos[j]
+extern "C" void orc_rope_neox(float* v, int n, int rope, const float* pos, float base) {
+    for (int j = 0; j < n; ++j) {
+        double d[64];
+        for (int e = 0; e < 64; ++e) d[e] = v[64 * j + e];
+        rope_vec(d, rope, (double)pos[j], (double)base, false);
+        for (int e = 0; e < 64; ++e) v[64 * j + e] = (float)d[e];
+    }
+}

@@ -101,6 +101,8 @@ typedef struct orc_block {
     int rank, dora;
     float scale;
 } orc_block;
+/* the block's NEOX rotary (rope_dims of each 64-wide head vector, positions pos[j]), exported for tests */
+void orc_rope_neox(float* v, int n, int rope, const float* pos, float base);
 void orc_block_fwd(const orc_block* p, const float* x, const float* ctx, const float* gcond, float* out);
 void orc_block_bwd(const orc_block* p, const float* x, const float* ctx, const float* gcond, const float* dout,
                    float* dx, float* dctx, float* dgcond, float* const* dA, float* const* dB, float* const* dm);

@@ -60,6 +60,19 @@ def max_rel_err(a, b):
     return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-300))
 
 
+def elem_rel_err(a, b, floor_frac=0.1):
+    """element-wise relative error with a floor: max_i |a_i - b_i| / max(|b_i|, floor), floor =
+    floor_frac * rms(b). Elements at least as large as the floor are held to their own relative
+    error; smaller ones (near the reference's zero crossings, where a ratio is meaningless) to the
+    absolute error floor * bound."""
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    if not b.size:
+        return 0.0
+    floor = floor_frac * max(float(np.sqrt(np.mean(b * b))), 1e-300)
+    return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), floor)))
+
+
 def bf16_round(x):
     """float32 -> nearest-even bfloat16, returned as float32 (finite inputs)"""
     u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)

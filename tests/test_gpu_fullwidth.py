@@ -1,0 +1,93 @@
+"""Full-width parity against the oracle: the shapes the benchmark runs, at sequence lengths the
+double-precision oracle finishes in seconds.
+
+* one DiT block at dim 1536, 24 heads, FFN inner 6144, DoRA rank 32 on all 7 projections, f16
+  base, batch 2 x (64 memory + 72 latent) tokens, 128 context tokens, windows 256 and 0 (dense);
+* a depth-1 DiT at full width (io 64, cond 768, time 256, 64 memory tokens, T 72, Ctx 128, window
+  256, full scope with the 12 head/tail targets, DoRA rank 32, f16 base);
+every output and every adapter gradient to the bf16 bar (normwise relative error <= 2e-2, cosine
+>= 0.9999; losses to 1e-3). At these widths the GEMMs take the tile shapes, split-K counts,
+skinny-product and column-reduction splits, and the attention kernels their grids and query
+splits, that the 1536-wide model uses; the small-width tests elsewhere do not reach them.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, cosine, rel_err, rng, sa3k
+from test_gpu_block import GpuBlock, run_gpu, to_f16_grid
+from test_gpu_dit import grads_by_target, make_gpu, upload_inputs
+
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+import block_binding as bb  # noqa: E402
+import dit_binding as db  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL, TOL_COS = 2e-2, 0.9999
+
+
+def check(got, ref, what, worst):
+    e, c = rel_err(got, ref), cosine(got, ref)
+    worst.append((e, c, what))
+    assert e <= TOL_REL and c >= TOL_COS, f"{what}: rel {e:.3e} cos {c:.6f}"
+
+
+@pytest.mark.parametrize("window", [256, 0])
+def test_block_full_width_vs_oracle(ctx, window):
+    B, S, Ctx = 2, 64 + 72, 128
+    print(f"full-width block vs oracle: window {window}, B {B}, S {S}, Ctx {Ctx}", flush=True)
+    cfg, w, x, cx, gc = bb.random_block(51 + window, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
+                                        alpha=32.0, dora=True, window=window, w_sd=0.02, b_sd=0.01)
+    w["W"] = [to_f16_grid(W) for W in w["W"]]   # the oracle sees the f16 values the GPU decodes
+    w["bnsq"] = [((W.astype(np.float64) ** 2).sum(1) + W.shape[1] * 1e-12).astype(np.float32) for W in w["W"]]
+    dout = rng(52 + window).normal(0, 1e-2, x.shape).astype(np.float32)
+    gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
+    try:
+        got = run_gpu(ctx, gb, x, cx, gc, dout)
+    finally:
+        gb.destroy()
+    ref_out = bb.block_fwd(cfg, w, x, cx, gc)
+    ref = bb.block_bwd(cfg, w, x, cx, gc, dout)
+    worst = []
+    check(got["out"] - x, ref_out - x, "out - x", worst)
+    check(got["dx"] - dout, ref["dx"] - dout, "dx - dout", worst)
+    check(got["dctx"], ref["dctx"], "dcontext", worst)
+    check(got["dgcond"], ref["dgcond"], "dgcond", worst)
+    for t in range(7):
+        check(got["dA"][t], ref["dA"][t], f"dA[{t}]", worst)
+        check(got["dB"][t], ref["dB"][t], f"dB[{t}]", worst)
+        check(got["dm"][t], ref["dm"][t], f"dm[{t}]", worst)
+    e, c, what = max(worst)
+    print(f"worst normwise error {e:.3e} ({what}), lowest cosine {min(x[1] for x in worst):.7f}")
+
+
+def test_dit_depth1_full_width_vs_oracle(ctx):
+    cfg = dict(B=2, T=72, Ctx=128, io=64, dim=1536, heads=24, inner=6144, depth=1, mem=64, cond_dim=768,
+               time_dim=256, rope_dims=32, window=256, rank=32, alpha=32.0, dora=True)
+    print("full-width depth-1 DiT vs oracle: T 72, Ctx 128, window 256, DoRA r32 full scope", flush=True)
+    tensors, adapters, inputs = db.random_dit(53, cfg, "full", w_sd=0.02, b_sd=0.01)
+    tensors = {k: (v.astype(np.float16).astype(np.float32) if k.endswith(".weight") else v)
+               for k, v in tensors.items()}
+    d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
+    try:
+        up, _ = upload_inputs(ctx, inputs)
+        loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+        vel = ctx.empty((cfg["B"], cfg["T"], cfg["io"]))
+        d.forward(up["x_t"], up["t"], up["cross"], up["glob"], vel)
+        got = grads_by_target(d, d.arena(1).numpy())
+        ref_loss, ref_vel, ref = db.dit_loss(cfg, tensors, adapters, inputs)
+        assert np.allclose(loss, ref_loss, rtol=1e-3), (loss, ref_loss)
+        worst = []
+        check(vel.numpy(), ref_vel, "velocity", worst)
+        assert len(ref) == 19
+        for n, (dA, dB, dm) in ref.items():
+            check(got[n][0], dA, f"dA {n}", worst)
+            check(got[n][1], dB, f"dB {n}", worst)
+            check(got[n][2], dm, f"dm {n}", worst)
+        e, c, what = max(worst)
+        print(f"worst normwise error {e:.3e} ({what}), lowest cosine {min(x[1] for x in worst):.7f}")
+    finally:
+        d.destroy()
