@@ -450,6 +450,12 @@ SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw
  * step is as fast on MI355X (launches hide behind the kernels) and runs the second stream's kernels
  * (option "side_stream") concurrently, which a replay of the graph does not. */
 SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
+/* run_eval_dit_loss (src/train_loop.h:455-476): the forward and the per-sample velocity MSE of
+ * sa3k_dit_accumulate (same kernels, so the same losses bit for bit) without the backward; the
+ * gradient arena and the accumulated sample count are untouched. loss_out (host, required) receives
+ * the B per-sample losses; synchronises the stream. */
+SA3K_API int sa3k_dit_eval_loss(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* target, const float* t,
+                                const float* cross, const float* glob, const float* loss_weight, double* loss_out);
 /* Forward only: velocity [B][T][io] (dit_forward, src/dit.h:327-338). */
 SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* t, const float* cross,
                               const float* glob, float* velocity);

@@ -571,6 +571,15 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
            d->vel);
 }
 
+// per-sample velocity MSE of the last forward into d->loss, and its seed gradient into d->dv
+void loss_and_seed(sa3k_ctx* ctx, sa3k_dit* d, const float* target, const float* lw) {
+    const int B = d->tr.batch, T = d->tr.frames;
+    const int chunk = (int)ceil_div(T, d->loss_chunks);
+    launch(ctx, "dit_loss", mse_kernel, dim3((unsigned)d->loss_chunks, (unsigned)B), (const float*)d->vel, target, lw, T,
+           d->cfg.io, chunk, d->loss_part, d->dv);
+    launch(ctx, "dit_loss", mse_sum_kernel, dim3(1), (const double*)d->loss_part, d->loss_chunks, B, d->loss);
+}
+
 void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* target, const float* t,
                      const float* cross, const float* glob, const float* lw) {
     const sa3k_dit_config& c = d->cfg;
@@ -578,11 +587,7 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
     const int64_t NT = (int64_t)B * T, NC = (int64_t)B * d->tr.ctx_tokens, D = c.dim;
     KernelScope ks(ctx, "dit_step");
     forward(ctx, d, x_t, t, cross, glob);
-    // loss and its seed
-    const int chunk = (int)ceil_div(T, d->loss_chunks);
-    launch(ctx, "dit_loss", mse_kernel, dim3((unsigned)d->loss_chunks, (unsigned)B), (const float*)d->vel, target, lw, T,
-           c.io, chunk, d->loss_part, d->dv);
-    launch(ctx, "dit_loss", mse_sum_kernel, dim3(1), (const double*)d->loss_part, d->loss_chunks, B, d->loss);
+    loss_and_seed(ctx, d, target, lw);
     // tail backward: v = post_conv(v0) + v0, v0 = proj_out(x_depth[mem:])
     launch(ctx, "dit_tail", copy_kernel, dim3(nblk(NT * c.io)), (const float*)d->dv, NT * c.io, d->dv0);
     lin_bwd(ctx, d, H_POST_CONV, d->v0, NT, d->dv, d->dv0, 1);
@@ -920,6 +925,21 @@ SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on) {
                 SA3K_HIP(hipGraphExecDestroy(e));
                 e = nullptr;
             }
+    });
+}
+
+SA3K_API int sa3k_dit_eval_loss(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* target, const float* t,
+                                const float* cross, const float* glob, const float* loss_weight, double* loss_out) {
+    return sa3k_guard(ctx, "sa3k_dit_eval_loss", [&] {
+        SA3K_REQUIRE(dit && dit->ready, "the model is not set up");
+        SA3K_REQUIRE(x_t && target && t && cross && glob, "evaluation inputs are empty");
+        SA3K_REQUIRE(loss_out != nullptr, "loss_out is null");
+        forward(ctx, dit, x_t, t, cross, glob);
+        loss_and_seed(ctx, dit, target, loss_weight);
+        SA3K_HIP(hipMemcpyAsync(loss_out, dit->loss, sizeof(double) * dit->tr.batch, hipMemcpyDeviceToHost,
+                                ctx->stream));
+        sa3k_note_main(ctx);
+        SA3K_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
 

@@ -1,6 +1,7 @@
-// gguf_io.h - a small reader and writer of GGUF version 3 files, enough for adapter checkpoints:
-// scalar metadata (strings, integers, floats, bools; arrays are skipped when read) and f32 / f16
-// tensors. The format, little-endian throughout:
+// gguf_io.h - a small reader and writer of GGUF version 3 files, enough for adapter checkpoints and
+// the trainer-state sidecar: scalar metadata (strings, integers, floats, bools), arrays of u64 and of
+// strings (arrays of other element types are skipped when read) and f32 / f16 tensors. The format,
+// little-endian throughout:
 //   "GGUF", u32 version 3, u64 tensor count, u64 metadata count;
 //   metadata: string key, u32 value type, value (string = u64 byte length + bytes);
 //   tensor infos: string name, u32 n_dims, u64 ne[n_dims] (ne[0] the contiguous extent), u32 type,
@@ -59,6 +60,9 @@ struct Value {
     uint64_t u = 0;     // unsigned integers and bools
     int64_t i = 0;      // signed integers
     double f = 0.0;     // floats
+    uint32_t arr_type = 0;               // kArray: element type
+    std::vector<uint64_t> au;            // kArray of kU64
+    std::vector<std::string> as;         // kArray of kString
 };
 
 struct TensorInfo {
@@ -77,7 +81,12 @@ struct TensorInfo {
 
 class Writer {
 public:
-    void set_str(const std::string& k, const std::string& v) { kv_.push_back({k, Value{kString, v}}); }
+    void set_str(const std::string& k, const std::string& v) {
+        Value x;
+        x.type = kString;
+        x.s = v;
+        kv_.push_back({k, x});
+    }
     void set_u32(const std::string& k, uint32_t v) {
         Value x;
         x.type = kU32;
@@ -88,6 +97,26 @@ public:
         Value x;
         x.type = kF32;
         x.f = v;
+        kv_.push_back({k, x});
+    }
+    void set_u64(const std::string& k, uint64_t v) {
+        Value x;
+        x.type = kU64;
+        x.u = v;
+        kv_.push_back({k, x});
+    }
+    void set_arr_u64(const std::string& k, const std::vector<uint64_t>& v) {
+        Value x;
+        x.type = kArray;
+        x.arr_type = kU64;
+        x.au = v;
+        kv_.push_back({k, x});
+    }
+    void set_arr_str(const std::string& k, const std::vector<std::string>& v) {
+        Value x;
+        x.type = kArray;
+        x.arr_type = kString;
+        x.as = v;
         kv_.push_back({k, x});
     }
     // an f32 tensor; ne[0] is the contiguous extent; `data` must stay alive until write()
@@ -114,11 +143,25 @@ public:
             switch (kv.second.type) {
                 case kString: put_str(kv.second.s); break;
                 case kU32: put_u32((uint32_t)kv.second.u); break;
+                case kU64: put_u64(kv.second.u); break;
                 case kF32: {
                     const float f = (float)kv.second.f;
                     put(&f, 4);
                     break;
                 }
+                case kArray:
+                    put_u32(kv.second.arr_type);
+                    if (kv.second.arr_type == kU64) {
+                        put_u64(kv.second.au.size());
+                        for (uint64_t v : kv.second.au) put_u64(v);
+                    } else if (kv.second.arr_type == kString) {
+                        put_u64(kv.second.as.size());
+                        for (const std::string& v : kv.second.as) put_str(v);
+                    } else {
+                        err = "gguf writer: unsupported array type";
+                        return false;
+                    }
+                    break;
                 default: err = "gguf writer: unsupported metadata type"; return false;
             }
         }
@@ -272,20 +315,29 @@ private:
             case kI64: return get(v.i);
             case kF32: { float x; if (!get(x)) return false; v.f = x; return true; }
             case kF64: return get(v.f);
-            case kArray: {   // skipped: element type, count, elements
+            case kArray: {   // element type, count, elements: u64 and string arrays are kept
                 uint32_t et;
                 uint64_t n;
                 if (!get(et) || !get(n)) return false;
+                v.arr_type = et;
                 if (et == kString) {
-                    std::string s;
+                    if (n > (buf_.size() - pos_) / 8) {   // every element needs its 8-byte length
+                        err_ = "bad array";
+                        return false;
+                    }
+                    v.as.resize((size_t)n);
                     for (uint64_t k = 0; k < n; ++k)
-                        if (!get_str(s)) return false;
+                        if (!get_str(v.as[(size_t)k])) return false;
                     return true;
                 }
                 const uint64_t es = scalar_size(et);
                 if (es == 0 || n > (buf_.size() - pos_) / es) {
                     err_ = "bad array";
                     return false;
+                }
+                if (et == kU64) {
+                    v.au.resize((size_t)n);
+                    if (n) std::memcpy(v.au.data(), buf_.data() + pos_, (size_t)n * 8);
                 }
                 pos_ += n * es;
                 return true;

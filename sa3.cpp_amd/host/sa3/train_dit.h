@@ -24,7 +24,13 @@ struct TrainConditioning {
     int token_count = 0;
 };
 
-struct TrainDitGraph {
+namespace detail {
+
+// What a training "graph" of this build holds: the device model in one activation schedule, its
+// adapter arena (one slot per target, in the order of TrainLoraState::params) and the device
+// buffers of one sample's inputs. TrainDitGraph (monolithic) and TrainDitCkpt (checkpointed) are
+// both this; they differ in the schedule the model is set up with.
+struct DitDeviceStep {
     struct Slot {   // one adapted target in the arena
         int64_t off_a = 0, off_b = 0, off_m = -1, n_a = 0, n_b = 0, n_m = 0;
     };
@@ -37,13 +43,12 @@ struct TrainDitGraph {
     DeviceF32 x, target, t, cross, global;
 };
 
-inline void free_train_dit_graph(TrainDitGraph& g) { g = TrainDitGraph{}; }
-
-// The model's adapters are those of `lora` (its targets must be a scope this build runs: every
-// block projection, with or without the 12 head/tail linears). A model is set up once.
-inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames,
-                                          int cond_dim, int ctx_len, TrainDitGraph& out, std::string& err,
-                                          bool inpaint = false) {
+// Set `dit` up for one sample of `frames` latent frames and `ctx_len` context tokens with the
+// adapters of `lora` (a scope this build runs: every block projection, with or without the 12
+// head/tail linears) in the given schedule (recompute = 1: the checkpointed one), and fill `out`.
+// A model is set up once.
+inline bool setup_dit_step(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames, int cond_dim,
+                           int ctx_len, int recompute, DitDeviceStep& out, std::string& err, bool inpaint) {
     if (frames <= 0 || cond_dim <= 0 || ctx_len <= 0) {
         err = "invalid DiT training graph dimensions";
         return false;
@@ -64,13 +69,14 @@ inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, co
     for (const TrainLoraParam& p : lora.params) all_blocks = all_blocks && train_lora_is_block_weight(p.target.weight_name);
     const int scope = all_blocks ? SA3K_SCOPE_CORE : SA3K_SCOPE_FULL;
     sa3k_ctx* ctx = dit.ctx();
-    sa3k_dit_train tr{lora.rank, lora.alpha, lora.adapter_type == "dora-rows" ? 1 : 0, scope, 1, frames, ctx_len, 0};
+    sa3k_dit_train tr{lora.rank, lora.alpha, lora.adapter_type == "dora-rows" ? 1 : 0, scope, 1, frames, ctx_len,
+                      recompute};
     if (sa3k_dit_setup(ctx, dit.handle(), &tr) != SA3K_OK) return sa3k_fail(ctx, err);
-    free_train_dit_graph(out);
     out.model = &dit;
     out.frames = frames;
     out.cond_dim = cond_dim;
     out.ctx_len = ctx_len;
+    out.slots.clear();
     int nt = 0;
     if (sa3k_dit_target_count(ctx, dit.handle(), &nt) != SA3K_OK) return sa3k_fail(ctx, err);
     if ((size_t)nt != lora.params.size()) {
@@ -80,7 +86,7 @@ inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, co
     char name[256];
     for (int i = 0; i < nt; ++i) {
         int64_t in = 0, o = 0;
-        TrainDitGraph::Slot s;
+        DitDeviceStep::Slot s;
         if (sa3k_dit_target_info(ctx, dit.handle(), i, name, (int)sizeof name, &in, &o, &s.off_a, &s.off_b, &s.off_m) !=
             SA3K_OK)
             return sa3k_fail(ctx, err);
@@ -99,6 +105,21 @@ inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, co
     const size_t nx = (size_t)dc.io * frames;
     return out.x.alloc(ctx, nx, err) && out.target.alloc(ctx, nx, err) && out.t.alloc(ctx, 1, err) &&
            out.cross.alloc(ctx, (size_t)cond_dim * ctx_len, err) && out.global.alloc(ctx, (size_t)cond_dim, err);
+}
+
+}  // namespace detail
+
+// The monolithic training graph (src/train_dit.h:30-48): every block keeps its forward activations.
+struct TrainDitGraph : detail::DitDeviceStep {};
+
+inline void free_train_dit_graph(TrainDitGraph& g) { g = TrainDitGraph{}; }
+
+// build_train_dit_forward_graph (src/train_dit.h:57-218): the model's adapters are those of `lora`.
+inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames,
+                                          int cond_dim, int ctx_len, TrainDitGraph& out, std::string& err,
+                                          bool inpaint = false) {
+    free_train_dit_graph(out);
+    return detail::setup_dit_step(dit, dc, lora, frames, cond_dim, ctx_len, 0, out, err, inpaint);
 }
 
 }  // namespace sa3

@@ -1,12 +1,16 @@
-// train_loop.h - the training-step helpers of the reference's src/train_loop.h:21-441 over the
-// GPU: loop/accumulator state, averaging + global clip, the accumulated AdamW update, and one
-// micro-batch of the DiT step (run_train_dit_accumulate). Names, fields, argument meaning and the
+// train_loop.h - the training-step helpers of the reference's src/train_loop.h:21-476 over the
+// GPU: loop/accumulator state, averaging + global clip, the accumulated AdamW update, one
+// micro-batch of the DiT step in the monolithic or the checkpointed schedule
+// (run_train_dit_accumulate, run_train_dit_accumulate_ckpt), the one-sample update
+// (run_train_dit_step) and the evaluation loss (run_eval_dit_loss). Names, fields, argument meaning and the
 // bool/err convention are the reference's; the arithmetic runs through the sa3k C ABI.
 //
-// Difference of signature: the reference's first argument of run_train_dit_accumulate is the ggml
-// backend; here the graph carries its device (sa3k) context, so that argument is gone.
+// Difference of signature: the reference's first argument of run_train_dit_accumulate[_ckpt],
+// run_train_dit_step and run_eval_dit_loss is the ggml backend; here the graph carries its device
+// (sa3k) context, so that argument is gone.
 #pragma once
 
+#include "train_ckpt.h"
 #include "train_diffusion.h"
 #include "train_dit.h"
 #include "train_inpaint.h"
@@ -158,7 +162,11 @@ inline bool train_apply_accumulated_adamw(TrainLoraState& state, TrainLoraGradAc
 }
 
 // upload_train_lora_state (src/train_loop.h:42-60): the host adapters into the graph's arena
-inline bool upload_train_lora_state(const TrainLoraState& state, TrainDitGraph& graph, std::string& err) {
+inline bool upload_train_lora_state(const TrainLoraState& state, detail::DitDeviceStep& graph, std::string& err) {
+    if (state.params.size() != graph.slots.size()) {
+        err = "adapter state does not match the training graph's targets";
+        return false;
+    }
     sa3k_ctx* ctx = graph.model->ctx();
     for (size_t i = 0; i < state.params.size(); ++i) {
         const TrainLoraParam& q = state.params[i];
@@ -178,55 +186,133 @@ inline bool upload_train_lora_state(const TrainLoraState& state, TrainDitGraph& 
     return true;
 }
 
-// run_train_dit_accumulate (src/train_loop.h:212-256): one sample through the DiT, velocity MSE,
-// and the adapter gradients added into accum (count += 1). The device DiT has no local-conditioning
-// input (dit.local.*), so, like the reference's graph built without one, it answers an inpaint
-// sample with the reference's mismatch error.
-inline bool run_train_dit_accumulate(TrainDitGraph& graph, const TrainLoraState& lora, TrainLoraGradAccum& accum,
-                                     const TrainDiffusionSample& sample, const TrainConditioning& cond,
-                                     const DitConfig& dc, float& loss_out, std::string& err,
-                                     const TrainInpaint* inpaint = nullptr) {
+namespace detail {
+
+// The inputs of one sample into the step's device buffers, after the reference's checks.
+inline bool upload_step_inputs(DitDeviceStep& st, const TrainDiffusionSample& sample, const TrainConditioning& cond,
+                               const DitConfig& dc, const char* empty_msg, std::string& err) {
+    if (sample.x_t.empty() || sample.velocity_target.empty() || cond.cross.empty() || cond.global.empty()) {
+        err = empty_msg;
+        return false;
+    }
+    const size_t nx = (size_t)dc.io * st.frames;
+    if (sample.x_t.size() != nx || sample.velocity_target.size() != nx ||
+        cond.cross.size() != (size_t)st.cond_dim * st.ctx_len || cond.global.size() != (size_t)st.cond_dim) {
+        err = "training step inputs do not match the graph's dimensions";
+        return false;
+    }
+    return st.x.upload(sample.x_t.data(), nx, 0, err) && st.target.upload(sample.velocity_target.data(), nx, 0, err) &&
+           st.t.upload(&sample.t, 1, 0, err) &&
+           st.cross.upload(cond.cross.data(), (size_t)st.cond_dim * st.ctx_len, 0, err) &&
+           st.global.upload(cond.global.data(), (size_t)st.cond_dim, 0, err);
+}
+
+// One sample through the model in whichever schedule it was set up with: forward, velocity MSE,
+// backward; this call's gradients are read back and added into accum target by target, in the
+// order of `visit` (count += 1).
+inline bool accumulate_step(DitDeviceStep& st, const TrainLoraState& lora, TrainLoraGradAccum& accum,
+                            const TrainDiffusionSample& sample, const TrainConditioning& cond, const DitConfig& dc,
+                            float& loss_out, std::string& err, const TrainInpaint* inpaint,
+                            const std::vector<size_t>& visit) {
     if (sample.x_t.empty() || sample.velocity_target.empty() || cond.cross.empty() || cond.global.empty()) {
         err = "training step inputs are empty";
         return false;
     }
+    // the device DiT has no local-conditioning input (dit.local.*): like the reference's graph built
+    // without one, it answers an inpaint sample with the reference's mismatch error
     if (inpaint != nullptr) {
         err = "inpaint graph/sample mismatch (local-cond present in one but not the other)";
         return false;
     }
-    const size_t nx = (size_t)dc.io * graph.frames;
-    if (sample.x_t.size() != nx || sample.velocity_target.size() != nx ||
-        cond.cross.size() != (size_t)graph.cond_dim * graph.ctx_len || cond.global.size() != (size_t)graph.cond_dim) {
-        err = "training step inputs do not match the graph's dimensions";
-        return false;
-    }
-    if (!upload_train_lora_state(lora, graph, err)) return false;
-    sa3k_ctx* ctx = graph.model->ctx();
-    if (!graph.x.upload(sample.x_t.data(), nx, 0, err) || !graph.target.upload(sample.velocity_target.data(), nx, 0, err) ||
-        !graph.t.upload(&sample.t, 1, 0, err) ||
-        !graph.cross.upload(cond.cross.data(), (size_t)graph.cond_dim * graph.ctx_len, 0, err) ||
-        !graph.global.upload(cond.global.data(), (size_t)graph.cond_dim, 0, err))
-        return false;
+    if (!upload_step_inputs(st, sample, cond, dc, "training step inputs are empty", err)) return false;
+    if (!upload_train_lora_state(lora, st, err)) return false;
+    sa3k_ctx* ctx = st.model->ctx();
     // this call's gradients alone, then added into the host accumulator like the reference reads
-    // them back from its graph (train_accumulate_adamw_gradients)
-    if (sa3k_memset(ctx, graph.grads, 0, (size_t)graph.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
+    // them back from its graphs (train_accum_read_subset)
+    if (sa3k_memset(ctx, st.grads, 0, (size_t)st.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
     double loss = 0.0;
-    if (sa3k_dit_accumulate(ctx, graph.model->handle(), graph.x.get(), graph.target.get(), graph.t.get(),
-                            graph.cross.get(), graph.global.get(), nullptr, &loss) != SA3K_OK)
+    if (sa3k_dit_accumulate(ctx, st.model->handle(), st.x.get(), st.target.get(), st.t.get(), st.cross.get(),
+                            st.global.get(), nullptr, &loss) != SA3K_OK)
         return sa3k_fail(ctx, err);
     loss_out = (float)loss;
-    std::vector<float> g((size_t)graph.n_params);
-    if (sa3k_download(ctx, g.data(), graph.grads, g.size() * 4) != SA3K_OK) return sa3k_fail(ctx, err);
+    std::vector<float> g((size_t)st.n_params);
+    if (sa3k_download(ctx, g.data(), st.grads, g.size() * 4) != SA3K_OK) return sa3k_fail(ctx, err);
     const size_t np = lora.params.size();
     for (auto* a : {&accum.A, &accum.B, &accum.mxs, &accum.mag, &accum.mag_r, &accum.mag_c}) a->resize(np);
-    for (size_t i = 0; i < np; ++i) {
-        const TrainDitGraph::Slot& s = graph.slots[i];
-        train_accum_add(accum.A[i], std::vector<float>(g.begin() + s.off_a, g.begin() + s.off_a + s.n_a));
-        train_accum_add(accum.B[i], std::vector<float>(g.begin() + s.off_b, g.begin() + s.off_b + s.n_b));
-        if (s.off_m >= 0)
-            train_accum_add(accum.mag[i], std::vector<float>(g.begin() + s.off_m, g.begin() + s.off_m + s.n_m));
+    auto slice = [&](int64_t off, int64_t n) {
+        return std::vector<float>(g.begin() + off, g.begin() + off + n);
+    };
+    for (size_t i : visit) {
+        const DitDeviceStep::Slot& s = st.slots[i];
+        train_accum_add(accum.A[i], slice(s.off_a, s.n_a));
+        train_accum_add(accum.B[i], slice(s.off_b, s.n_b));
+        if (s.off_m >= 0) train_accum_add(accum.mag[i], slice(s.off_m, s.n_m));
     }
     accum.count += 1;
+    return true;
+}
+
+inline std::vector<size_t> all_targets(size_t n) {
+    std::vector<size_t> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = i;
+    return v;
+}
+
+}  // namespace detail
+
+// run_train_dit_accumulate (src/train_loop.h:212-256): one sample through the DiT, velocity MSE,
+// and the adapter gradients added into accum (count += 1).
+inline bool run_train_dit_accumulate(TrainDitGraph& graph, const TrainLoraState& lora, TrainLoraGradAccum& accum,
+                                     const TrainDiffusionSample& sample, const TrainConditioning& cond,
+                                     const DitConfig& dc, float& loss_out, std::string& err,
+                                     const TrainInpaint* inpaint = nullptr) {
+    return detail::accumulate_step(graph, lora, accum, sample, cond, dc, loss_out, err, inpaint,
+                                   detail::all_targets(lora.params.size()));
+}
+
+// run_train_dit_accumulate_ckpt (src/train_loop.h:309-441): the same step in the checkpointed
+// schedule (one block's activations, each block recomputed before its backward). The gradients are
+// read back segment by segment in the reference's order: tail (T), blocks depth-1 .. 0 (B_l), head
+// (H). Each target belongs to exactly one segment, so the accumulated values are those of
+// run_train_dit_accumulate bit for bit.
+inline bool run_train_dit_accumulate_ckpt(TrainDitCkpt& ck, const TrainLoraState& lora, TrainLoraGradAccum& accum,
+                                          const TrainDiffusionSample& sample, const TrainConditioning& cond,
+                                          const DitConfig& dc, float& loss_out, std::string& err,
+                                          const TrainInpaint* inpaint = nullptr) {
+    std::vector<size_t> visit(ck.tail_param_idx);
+    for (int l = ck.depth - 1; l >= 0; --l)
+        visit.insert(visit.end(), ck.block_param_idx[(size_t)l].begin(), ck.block_param_idx[(size_t)l].end());
+    visit.insert(visit.end(), ck.head_param_idx.begin(), ck.head_param_idx.end());
+    if (visit.size() != lora.params.size()) {
+        err = "checkpointed graph does not match the adapter state";
+        return false;
+    }
+    return detail::accumulate_step(ck, lora, accum, sample, cond, dc, loss_out, err, inpaint, visit);
+}
+
+// run_train_dit_step (src/train_loop.h:443-451): one sample's gradients, then the AdamW update.
+inline bool run_train_dit_step(TrainDitGraph& graph, TrainLoraState& lora, TrainLoopState& loop,
+                               const TrainAdamWParams& opt, const TrainDiffusionSample& sample,
+                               const TrainConditioning& cond, const DitConfig& dc, float& loss_out, std::string& err) {
+    TrainLoraGradAccum accum;
+    if (!run_train_dit_accumulate(graph, lora, accum, sample, cond, dc, loss_out, err)) return false;
+    return train_apply_accumulated_adamw(lora, accum, loop, opt, err);
+}
+
+// run_eval_dit_loss (src/train_loop.h:453-476): the loss of one sample under the adapters of
+// `lora`, forward only (no gradient is computed or accumulated). The same device kernels as the
+// training step compute it, so it equals the loss run_train_dit_accumulate reports.
+inline bool run_eval_dit_loss(detail::DitDeviceStep& graph, const TrainLoraState& lora,
+                              const TrainDiffusionSample& sample, const TrainConditioning& cond, const DitConfig& dc,
+                              float& loss_out, std::string& err) {
+    if (!detail::upload_step_inputs(graph, sample, cond, dc, "evaluation inputs are empty", err)) return false;
+    if (!upload_train_lora_state(lora, graph, err)) return false;
+    sa3k_ctx* ctx = graph.model->ctx();
+    double loss = 0.0;
+    if (sa3k_dit_eval_loss(ctx, graph.model->handle(), graph.x.get(), graph.target.get(), graph.t.get(),
+                           graph.cross.get(), graph.global.get(), nullptr, &loss) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    loss_out = (float)loss;
     return true;
 }
 

@@ -133,6 +133,7 @@ def _declare(lib):
         "sa3k_dit_accumulate": (I, [P, P, P, P, P, P, P, P, P]),
         "sa3k_dit_apply_adamw": (I, [P, P, C.POINTER(AdamWParams), I, C.POINTER(D)]),
         "sa3k_dit_forward": (I, [P, P, P, P, P, P, P]),
+        "sa3k_dit_eval_loss": (I, [P, P, P, P, P, P, P, P, C.POINTER(D)]),
         "sa3k_dit_set_graphs": (I, [P, P, I]),
     }
     for name, (res, args) in sig.items():
@@ -517,6 +518,13 @@ class Dit:
                                                         glob.ptr, loss_weight.ptr if loss_weight is not None else None,
                                                         loss if want_loss else None))
         return np.array(loss[:]) if want_loss else None
+
+    def eval_loss(self, x_t, target, t, cross, glob, loss_weight=None):
+        loss = (C.c_double * self.train.batch)()
+        self.ctx.check(self.ctx.lib.sa3k_dit_eval_loss(self.ctx.h, self.h, x_t.ptr, target.ptr, t.ptr, cross.ptr,
+                                                       glob.ptr, loss_weight.ptr if loss_weight is not None else None,
+                                                       loss))
+        return np.array(loss[:])
 
     def apply_adamw(self, hp, step, want_norm=False):
         p = AdamWParams(*hp)

@@ -6,8 +6,10 @@
 #include "sa3/dist_shift.h"
 #include "sa3/train_checkpoint.h"
 #include "sa3/train_loop.h"
+#include "sa3/train_resume.h"
 
 #include <cmath>
+#include <filesystem>
 #include <cstdio>
 #include <cstring>
 #include <random>
@@ -85,7 +87,88 @@ static double max_rel(const std::vector<float>& a, const std::vector<float>& b) 
     return s > 0 ? d / s : d;
 }
 
+// Exact continuation (the reference's tests/train_checkpoint_test.cpp:55-190, its inputs): six
+// uninterrupted updates == three, the checkpoint pair written, reloaded into fresh state, three
+// more; parameters and both AdamW moments bit for bit. The updates run on the GPU.
+static void test_gpu_resume() {
+    namespace fs = std::filesystem;
+    sa3::TrainLoraState st;
+    st.adapter_type = "lora";
+    st.rank = 2;
+    st.alpha = 4.0f;
+    sa3::TrainLoraParam p;
+    p.target.weight_name = "dit.0.self.qkv.weight";
+    p.target.stem = "dit.0.self.qkv";
+    p.target.in = 3;
+    p.target.out = 5;
+    p.lora_A = {0, 1, 2, 3, 4, 5};
+    p.lora_B = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9};
+    st.params.push_back(p);
+    auto apply_step = [&](sa3::TrainLoraState& state, sa3::TrainLoopState& loop, int update) {
+        sa3::TrainLoraGradAccum accum;
+        const size_t n = state.params.size();
+        accum.count = 1;
+        accum.A.resize(n); accum.B.resize(n); accum.mxs.resize(n);
+        accum.mag.resize(n); accum.mag_r.resize(n); accum.mag_c.resize(n);
+        for (size_t i = 0; i < n; ++i) {
+            accum.A[i].resize(state.params[i].lora_A.size());
+            accum.B[i].resize(state.params[i].lora_B.size());
+            for (size_t j = 0; j < accum.A[i].size(); ++j) accum.A[i][j] = 0.01f * (float)(update + 1) + 0.001f * (float)j;
+            for (size_t j = 0; j < accum.B[i].size(); ++j) accum.B[i][j] = -0.02f * (float)(update + 1) + 0.0005f * (float)j;
+        }
+        sa3::TrainAdamWParams hp;
+        hp.learning_rate = 1.0e-3f;
+        hp.beta1 = 0.9f;
+        hp.beta2 = 0.95f;
+        hp.weight_decay = 0.01f;
+        std::string e;
+        return sa3::train_apply_accumulated_adamw(state, accum, loop, hp, e);
+    };
+    sa3::TrainLoraState uninterrupted = st, split = st;
+    sa3::TrainLoopState u_loop, s_loop;
+    for (int i = 0; i < 6; ++i) expect(apply_step(uninterrupted, u_loop, i), "uninterrupted AdamW step");
+    for (int i = 0; i < 3; ++i) expect(apply_step(split, s_loop, i), "pre-checkpoint AdamW step");
+    std::string err;
+    sa3::TrainResumeProgress progress;
+    progress.epoch = 2;
+    progress.next_sample = 1;
+    progress.order = {1, 0};
+    progress.compatibility = "test-compatibility";
+    std::mt19937_64 rng(12345);
+    progress.shuffle_rng = progress.crop_rng = progress.cfg_rng = progress.prompt_rng = progress.inpaint_rng =
+        sa3::train_serialize_random_state(rng);
+    progress.diffusion_rng = sa3::TrainDiffusionSampler(6789, "trunc_logit_normal").serialize_state();
+    const fs::path dir = fs::temp_directory_path() / "sa3_train_host_test_resume";
+    fs::remove_all(dir);
+    fs::create_directories(dir);
+    const fs::path adapter = dir / "adapter-step-3.gguf", state = dir / "trainer-state-step-3.gguf";
+    expect(sa3::write_train_checkpoint_pair(split, s_loop, progress, adapter.string(), state.string(), err),
+           "write checkpoint pair");
+    expect(!sa3::write_train_checkpoint_pair(split, s_loop, progress, adapter.string(), state.string(), err),
+           "immutable checkpoint overwrite rejected");
+    sa3::TrainLoraState reloaded, continued = st;   // expected targets and shapes from the current model
+    sa3::TrainLoopState c_loop;
+    sa3::TrainResumeProgress rp;
+    expect(sa3::load_train_lora_gguf(adapter.string(), reloaded, err) &&
+               sa3::train_restore_adapter_values(continued, reloaded, err) &&
+               sa3::load_train_state_gguf(state.string(), continued, c_loop, rp, err),
+           "reload the pair");
+    expect(c_loop.step == 3 && rp.order == progress.order && rp.next_sample == 1, "step and cursor restored");
+    expect(sa3::train_validate_resume_adapter_fingerprint(adapter.string(), rp.adapter_fingerprint, err),
+           "adapter matches its sidecar");
+    for (int i = 3; i < 6; ++i) expect(apply_step(continued, c_loop, i), "post-resume AdamW step");
+    expect(c_loop.step == u_loop.step, "final optimizer step exact");
+    expect(continued.params[0].lora_A == uninterrupted.params[0].lora_A &&
+               continued.params[0].lora_B == uninterrupted.params[0].lora_B,
+           "final adapter parameters exact");
+    expect(c_loop.A_state[0].m == u_loop.A_state[0].m && c_loop.A_state[0].v == u_loop.A_state[0].v &&
+               c_loop.B_state[0].m == u_loop.B_state[0].m && c_loop.B_state[0].v == u_loop.B_state[0].v,
+           "final AdamW moments exact");
+    fs::remove_all(dir);
+}
+
 static void test_gpu() {
+    test_gpu_resume();
     std::string err;
     // ---- AdamW (tests/train_optimizer_test.cpp:17-30) + the float update term by term
     {
@@ -248,6 +331,62 @@ static void test_gpu() {
     }
     expect(twice, "two identical samples accumulate exactly twice the gradients");
     expect(live, "A gradients are live");
+
+    // ---- the reference's default path (tools/sa3-train.cpp:574-714): the checkpointed schedule on a
+    // second model with the same weights: build_train_dit_ckpt -> the sampler's sample ->
+    // run_train_dit_accumulate_ckpt -> train_apply_accumulated_adamw, against the monolithic path
+    {
+        sa3::DitModel dit2;
+        expect(dit2.create(dc, SA3K_TYPE_F32, err) && dit2.init_random(11, 0.05f, err), "second model");
+        {
+            const std::string name = "dit.1.cross.q.weight";
+            std::vector<float> w((size_t)(dit2.ne0(name) * dit2.ne1(name)));
+            for (size_t i = 0; i < w.size(); ++i) w[i] = (float)(i + 1) / 1000.0f;
+            expect(dit2.set_tensor(name, w.data(), w.size() * 4, err), "second model tensor");
+        }
+        sa3::TrainDitCkpt ck;
+        expect(sa3::build_train_dit_ckpt(dit2, dc, st, frames, dc.cond_dim, ctx_len, ck, err), "build ckpt");
+        expect(ck.depth == 2 && ck.tail_param_idx.size() == 2 && ck.head_param_idx.size() == 10 &&
+                   ck.block_param_idx.size() == 2 && ck.block_param_idx[0].size() == 7 &&
+                   ck.block_param_idx[1].size() == 7,
+               "segments: tail 2, blocks 7 each, head 10");
+        expect(sa3::train_ckpt_segment("dit.post_conv", 2) == -2 && sa3::train_ckpt_segment("dit.1.ff.out", 2) == 1 &&
+                   sa3::train_ckpt_segment("dit.gce.0", 2) == -1 && sa3::train_ckpt_segment("dit.7.ff.out", 2) == -1,
+               "segment of a stem");
+        sa3::TrainLoraGradAccum acc_ck;
+        float loss_ck = 0.0f;
+        expect(!sa3::run_train_dit_accumulate_ckpt(ck, st, acc_ck, bad, c, dc, loss_ck, err), "ckpt: bad input rejected");
+        expect(sa3::run_train_dit_accumulate_ckpt(ck, st, acc_ck, s, c, dc, loss_ck, err), "accumulate ckpt");
+        expect(loss_ck == loss0 && acc_ck.count == 1, "checkpointed loss == monolithic loss");
+        bool same = acc_ck.A.size() == once.A.size();
+        for (size_t i = 0; same && i < once.A.size(); ++i)
+            same = acc_ck.A[i] == once.A[i] && acc_ck.B[i] == once.B[i] && acc_ck.mag[i] == once.mag[i];
+        expect(same, "checkpointed gradients == monolithic gradients, bit for bit");
+        // the evaluation loss on either schedule is the training step's loss
+        float le = 0.0f, le_ck = 0.0f;
+        expect(sa3::run_eval_dit_loss(graph, st, s, c, dc, le, err) && le == loss0, "eval loss == accumulate loss");
+        expect(sa3::run_eval_dit_loss(ck, st, s, c, dc, le_ck, err) && le_ck == loss0, "eval loss (ckpt)");
+        expect(!sa3::run_eval_dit_loss(graph, st, bad, c, dc, le, err), "eval: bad input rejected");
+        // one update from each schedule's accumulator, and run_train_dit_step, agree bit for bit
+        sa3::TrainLoraState s_mono = st, s_ck = st, s_step = st;
+        sa3::TrainLoopState l_mono, l_ck, l_step;
+        sa3::TrainLoraGradAccum a_mono = once;
+        expect(sa3::train_apply_accumulated_adamw(s_mono, a_mono, l_mono, hp, err) &&
+                   sa3::train_apply_accumulated_adamw(s_ck, acc_ck, l_ck, hp, err),
+               "adamw from both schedules");
+        float l_st = 0.0f;
+        expect(sa3::run_train_dit_step(graph, s_step, l_step, hp, s, c, dc, l_st, err) && l_st == loss0 &&
+                   l_step.step == 1,
+               "run_train_dit_step");
+        bool upd = true;
+        for (size_t i = 0; upd && i < st.params.size(); ++i)
+            upd = s_ck.params[i].lora_A == s_mono.params[i].lora_A && s_ck.params[i].lora_B == s_mono.params[i].lora_B &&
+                  s_ck.params[i].magnitude == s_mono.params[i].magnitude &&
+                  s_step.params[i].lora_A == s_mono.params[i].lora_A && s_step.params[i].lora_B == s_mono.params[i].lora_B &&
+                  s_step.params[i].magnitude == s_mono.params[i].magnitude;
+        expect(upd, "updated adapters equal across schedules and run_train_dit_step");
+        sa3::free_train_dit_ckpt(ck);
+    }
 
     // the C ABI's arena path on the same state: gradients of two accumulate calls, then one
     // sa3k_adamw_clip over the whole arena with count 2 == the mirror's packed update

@@ -8,6 +8,12 @@ and a GGUF writer written here from the published layout (independent of gguf_io
 byte the mirror writes and produce files the mirror must read (f16 tensors, array metadata, a
 non-default alignment, unrelated tensors, a missing adapter type), and tests/host/checkpoint_test.cpp
 covers the round trip and every rejected input.
+
+The trainer-state sidecar and the checkpoint pair (sa3.cpp_amd/host/sa3/train_resume.h; the
+reference's src/train_resume.h:23-538) are checked the same way: the sidecar's keys, value types,
+arrays and moment tensors against the published layout, and the pair's contract (immutable,
+resolvable from either file, bound to its adapter by fingerprint, exact RNG continuation) with the
+inputs of the reference's tests/train_checkpoint_test.cpp.
 """
 import os
 import struct
@@ -49,11 +55,15 @@ def parse_gguf(data):
         pos += n
         return s
 
-    def value(t):
+    arr_types = {}
+
+    def value(t, key=None):
         if t == 8:
             return string()
         if t == 9:
             et, n = take("<I"), take("<Q")
+            if key is not None:
+                arr_types[key] = et
             return [value(et) for _ in range(n)]
         return take(KV_SCALAR[t])
 
@@ -64,7 +74,7 @@ def parse_gguf(data):
     for _ in range(n_kv):
         k = string()
         t = take("<I")
-        kv[k], kv_types[k] = value(t), t
+        kv[k], kv_types[k] = value(t, k), t
     infos = []
     for _ in range(n_t):
         name = string()
@@ -74,7 +84,8 @@ def parse_gguf(data):
     align = kv.get("general.alignment", 32)
     meta_end = pos
     start = (pos + align - 1) // align * align
-    return dict(version=version, kv=kv, kv_types=kv_types, infos=infos, start=start, meta_end=meta_end, align=align)
+    return dict(version=version, kv=kv, kv_types=kv_types, arr_types=arr_types, infos=infos, start=start,
+                meta_end=meta_end, align=align)
 
 
 def write_gguf(path, kvs, tensors, align=32):
@@ -240,3 +251,41 @@ def test_rejects_malformed_extents_and_offsets(tool, tmp_path, patch):
     open(path, "wb").write(bytes(data))
     rc, lines = summary(tool, path)
     assert rc == 1, lines
+
+
+def test_trainer_state_sidecar_layout(tool, tmp_path):
+    path = str(tmp_path / "trainer-state-step-3.gguf")
+    assert subprocess.run([tool, "state", path], capture_output=True).returncode == 0
+    data = open(path, "rb").read()
+    g = parse_gguf(data)
+    kv, ty = g["kv"], g["kv_types"]
+    # the reference's keys and value types (src/train_resume.h:346-366): u32 = 4, u64 = 10, string = 8
+    assert kv["general.architecture"] == "sa3-trainer-state" and ty["general.architecture"] == 8
+    assert kv["general.name"] == "sa3 native trainer continuation state"
+    assert kv["trainer.state_version"] == 1 and ty["trainer.state_version"] == 4
+    for k, v in (("trainer.step", 3), ("trainer.epoch", 2), ("trainer.next_sample", 1)):
+        assert kv[k] == v and ty[k] == 10, k
+    assert kv["trainer.n_targets"] == 1 and ty["trainer.n_targets"] == 4
+    assert kv["trainer.adapter_file"] == "adapter-step-3.gguf"
+    assert kv["trainer.adapter_fingerprint"] == "fnv1a64:0123456789abcdef"
+    assert kv["trainer.compatibility"] == "test-compatibility"
+    # an mt19937_64 in the standard stream format: 312 words and the position
+    for k in ("shuffle", "crop", "cfg", "prompt", "inpaint"):
+        assert len(kv[f"trainer.rng.{k}"].split()) == 313 and ty[f"trainer.rng.{k}"] == 8
+    assert ty["trainer.rng.diffusion"] == 8 and kv["trainer.rng.diffusion"]
+    assert kv["trainer.order"] == [1, 0] and ty["trainer.order"] == 9 and g["arr_types"]["trainer.order"] == 10
+    assert kv["trainer.targets"] == ["dit.0.self.qkv"] and g["arr_types"]["trainer.targets"] == 8
+    # moments: optimizer.<stem>.<kind>.m / .v, 1-D f32, in visit order
+    names = [(n, ne, t) for n, ne, t, _ in g["infos"]]
+    assert names == [("optimizer.dit.0.self.qkv.lora_A.m", [6], 0), ("optimizer.dit.0.self.qkv.lora_A.v", [6], 0),
+                     ("optimizer.dit.0.self.qkv.lora_B.m", [10], 0), ("optimizer.dit.0.self.qkv.lora_B.v", [10], 0)]
+    off = dict((n, o) for n, _, _, o in g["infos"])
+    k = np.arange(6, dtype=np.float32)
+    m = np.frombuffer(data, np.float32, 6, g["start"] + off["optimizer.dit.0.self.qkv.lora_A.m"])
+    assert np.array_equal(m, np.float32(1.0) + np.float32(0.125) * k)
+
+
+def test_checkpoint_pair_contract(tool, tmp_path):
+    r = subprocess.run([tool, "resume", str(tmp_path)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "checkpoint_test resume: ok" in r.stdout

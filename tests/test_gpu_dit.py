@@ -97,7 +97,12 @@ def test_dit_step_vs_oracle(ctx, name):
         loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"], lw_d)
         vel = ctx.empty((cfg["B"], cfg["T"], cfg["io"]))
         d.forward(up["x_t"], up["t"], up["cross"], up["glob"], vel)
-        got = grads_by_target(d, d.arena(1).numpy())
+        g_arena = d.arena(1).numpy()
+        # run_eval_dit_loss: the same losses bit for bit, gradients untouched
+        ev = d.eval_loss(up["x_t"], up["target"], up["t"], up["cross"], up["glob"], lw_d)
+        assert np.array_equal(ev, loss)
+        assert np.array_equal(d.arena(1).numpy(), g_arena)
+        got = grads_by_target(d, g_arena)
         ref_loss, ref_vel, ref = db.dit_loss(cfg, tensors, adapters, inputs, loss_weight=lw)
         assert np.allclose(loss, ref_loss, rtol=1e-3), (loss, ref_loss)
         check(vel.numpy(), ref_vel, "velocity")
