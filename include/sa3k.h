@@ -277,6 +277,42 @@ SA3K_API int sa3k_lin_backward(sa3k_ctx* ctx, sa3k_lin* l, int x_type, const voi
                                const float* dY, float* dX, int dx_accumulate, float* dA, float* dB,
                                float* dm);
 
+/* ---------------------------------------------------------------- inference: adapter chains */
+
+/* One adapter of a chain over a frozen base weight (LoraAdapter, src/lora.h:28-34, with its tensors
+ * for one target on the device): the residual scale is (alpha / rank) * strength, and an adapter of
+ * strength 0 is the identity (skipped, as apply_loras skips it). */
+typedef struct {
+    int dora;                  /* 0: lora, 1: dora-rows */
+    int rank;                  /* > 0 */
+    float alpha;
+    float strength;
+    const float* A;            /* [rank][in] device f32 (GGUF lora_A ne = [in, rank]) */
+    const float* B;            /* [out][rank] device f32 (GGUF lora_B ne = [rank, out]) */
+    const float* magnitude;    /* [out] device f32 (dora-rows), else NULL */
+} sa3k_chain_adapter;
+
+typedef struct sa3k_lora_chain sa3k_lora_chain;
+
+/* build_functional_lora (src/lora.h:372-622) for one target: up to 8 adapters applied in order over
+ * the frozen base W (f32 / f16 / bf16 / Q8_0, which is never dequantised into HBM), whose active
+ * ranks add up to at most 64. Folds every dora-rows row scale into constants once, in double
+ * precision: base_scale c0 [out] and the row-scaled B'_k, so that the chain's output equals merging
+ * the adapters into W one after another (apply_loras, src/lora.h:111-143). Scratch for up to
+ * max_tokens rows. The adapter pointers are read during this call only. */
+SA3K_API int sa3k_lora_chain_create(sa3k_ctx* ctx, const sa3k_weight* W, int n_adapters,
+                                    const sa3k_chain_adapter* adapters, int64_t max_tokens, sa3k_lora_chain** out);
+SA3K_API int sa3k_lora_chain_destroy(sa3k_ctx* ctx, sa3k_lora_chain* chain);
+/* dit_lin over the chain (src/dit.h:108-117): Y [N][out] f32 = c0 (.) (X W^T) + sum_k s_k (X A_k^T) B'_k^T
+ * + bias (nullable); X [N][in] f32 or bf16 (x_type). bf16 MFMA with f32 accumulation; a Q8_0 / f16
+ * base without a bf16 working copy is decoded on its way into LDS. */
+SA3K_API int sa3k_lora_chain_forward(sa3k_ctx* ctx, sa3k_lora_chain* chain, int x_type, const void* X, int64_t N,
+                                     const float* bias, float* Y);
+/* The folded constants (device f32, nullable outputs): base_scale [out] and B' [out][R], the active
+ * adapters' B'_k side by side in chain order; total_rank receives R. */
+SA3K_API int sa3k_lora_chain_constants(sa3k_ctx* ctx, const sa3k_lora_chain* chain, float* base_scale, float* Bp,
+                                       int* total_rank);
+
 /* ---------------------------------------------------------------- K5: differential attention */
 
 /* Flash-style differential attention (dit_diff_attn, src/dit.h:151-158, over nn::sdpa,

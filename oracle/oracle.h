@@ -75,6 +75,25 @@ void orc_dit_lin_bwd(const float* X, int64_t N, const float* W, int64_t in, int6
 /* plain double-accumulated products used by tests: C[M][N] = A[M][K] * B[N][K]^T */
 void orc_gemm_nt(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
 
+/* ---- composed adapter chains over a frozen base (src/lora.h:111-143, 372-622; src/dit.h:108-117) ---- */
+typedef struct {
+    int dora;            /* 0: lora, 1: dora-rows */
+    int rank;
+    float alpha, strength;   /* residual scale (alpha / rank) * strength; strength 0 skips the adapter */
+    const float* A;      /* [rank][in] */
+    const float* B;      /* [out][rank] */
+    const float* mag;    /* [out] (dora-rows) */
+} orc_chain_adapter;
+/* sequential merge of the chain into W_eff [out][in] (apply_loras for lora / dora-rows) */
+void orc_chain_merge(const float* W, int64_t in, int64_t out, int n, const orc_chain_adapter* ad, float* Weff);
+/* build_functional_lora's constants: base_scale [out]; Bp [out][R] = the active adapters' row-scaled B'
+ * side by side in chain order (R = sum of their ranks); scales [n_active] = (alpha/rank)*strength */
+void orc_chain_fold(const float* W, int64_t in, int64_t out, int n, const orc_chain_adapter* ad, float* base_scale,
+                    float* Bp, float* scales);
+/* the composed functional forward Y [N][out] = base_scale * (X W^T) + sum_k s_k (X A_k^T) B'_k^T (+ bias) */
+void orc_chain_forward(const float* X, int64_t N, const float* W, int64_t in, int64_t out, int n,
+                       const orc_chain_adapter* ad, const float* bias, float* Y);
+
 /* ---- differential attention (src/dit.h:151-158, src/nn.h:135-144), double accumulation ----
  * Q1, Q2 [BH][Sq][D]; K1, K2, V [BH][Sk][D]; window 0 = dense, else |i-j| <= window/2.
  * fwd: O = O1 - O2 [BH][Sq][D] (O1, O2, lse1, lse2 [BH][Sq] nullable; lse natural log of the

@@ -246,3 +246,73 @@ def diff_attn_bwd(Q1, K1, Q2, K2, V, dO, scale=0.125, window=0):
     dK1, dK2, dV = np.empty_like(K1), np.empty_like(K2), np.empty_like(V)
     _attn_sig().orc_diff_attn_bwd(Q1, K1, Q2, K2, V, dO, BH, Sq, Sk, D, scale, window, dQ1, dK1, dQ2, dK2, dV)
     return dict(dQ1=dQ1, dK1=dK1, dQ2=dQ2, dK2=dK2, dV=dV)
+
+
+class _ChainAd(C.Structure):
+    _fields_ = [("dora", C.c_int), ("rank", C.c_int), ("alpha", C.c_float), ("strength", C.c_float),
+                ("A", C.c_void_p), ("B", C.c_void_p), ("mag", C.c_void_p)]
+
+
+def _chain(adapters):
+    """adapters: [(dora, rank, alpha, strength, A [r][in], B [out][r], mag [out] | None)] -> ctypes array, keep"""
+    keep = []
+    arr = (_ChainAd * max(1, len(adapters)))()
+    for i, (dora, rank, alpha, strength, A, B, mag) in enumerate(adapters):
+        A, B = f32(A), f32(B)
+        mag = f32(mag) if mag is not None else None
+        keep += [A, B, mag]
+        arr[i] = _ChainAd(int(dora), int(rank), float(alpha), float(strength), A.ctypes.data, B.ctypes.data,
+                          mag.ctypes.data if mag is not None else None)
+    return arr, keep
+
+
+def _chain_sigs(L):
+    if getattr(L, "_chain_declared", False):
+        return
+    I64, I, P = C.c_int64, C.c_int, C.c_void_p
+    L.orc_chain_merge.restype = None
+    L.orc_chain_merge.argtypes = [f32p, I64, I64, I, P, f32p]
+    L.orc_chain_fold.restype = None
+    L.orc_chain_fold.argtypes = [f32p, I64, I64, I, P, f32p, f32p, f32p]
+    L.orc_chain_forward.restype = None
+    L.orc_chain_forward.argtypes = [f32p, I64, f32p, I64, I64, I, P, C.c_void_p, f32p]
+    L._chain_declared = True
+
+
+def chain_merge(W, adapters):
+    """apply_loras' sequential merge of the chain into W_eff [out][in]"""
+    L = lib()
+    _chain_sigs(L)
+    W = f32(W)
+    out_, in_ = W.shape
+    arr, keep = _chain(adapters)
+    Weff = np.empty_like(W)
+    L.orc_chain_merge(W, in_, out_, len(adapters), C.cast(arr, C.c_void_p), Weff)
+    return Weff
+
+
+def chain_fold(W, adapters):
+    """build_functional_lora's constants: (base_scale [out], B' [out][R], scales [n_active])"""
+    L = lib()
+    _chain_sigs(L)
+    W = f32(W)
+    out_, in_ = W.shape
+    act = [a for a in adapters if a[3] != 0.0]
+    R = sum(a[1] for a in act)
+    arr, keep = _chain(adapters)
+    c0, Bp, sc = np.empty(out_, np.float32), np.empty((out_, max(R, 1)), np.float32), np.empty(max(len(act), 1), np.float32)
+    L.orc_chain_fold(W, in_, out_, len(adapters), C.cast(arr, C.c_void_p), c0, Bp, sc)
+    return c0, Bp[:, :R], sc[:len(act)]
+
+
+def chain_forward(X, W, adapters, bias=None):
+    """Y [N][out] = base_scale * (X W^T) + sum_k s_k (X A_k^T) B'_k^T (+ bias), double accumulation"""
+    L = lib()
+    _chain_sigs(L)
+    X, W = f32(X), f32(W)
+    out_, in_ = W.shape
+    arr, keep = _chain(adapters)
+    b = f32(bias) if bias is not None else None
+    Y = np.empty((X.shape[0], out_), np.float32)
+    L.orc_chain_forward(X, X.shape[0], W, in_, out_, len(adapters), C.cast(arr, C.c_void_p), _p(b), Y)
+    return Y

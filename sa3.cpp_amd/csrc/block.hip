@@ -14,6 +14,7 @@
 // recomputes block l into a shared one right before its backward (the gradient-checkpointed
 // schedule of src/train_ckpt.h:386-431).
 #include "block.h"
+#include "lora.h"
 
 #include <cmath>
 #include <vector>
@@ -558,6 +559,8 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
             SA3K_REQUIRE(W[t] != nullptr, "missing block weight");
             chk(ctx, sa3k_weight_create(ctx, weight_type, in, o, W[t], on_device, &b->W[t]));
             chk(ctx, sa3k_lin_create(ctx, b->W[t], rank, SA3K_PREC_BF16, t == 3 ? max_ctx : max_tokens, &b->L[t]));
+            static const char* const kTags[7] = {"qkv", "out", "cross.q", "cross.kv", "cross.out", "ff.proj", "ff.out"};
+            lin_set_tag(b->L[t], kTags[t]);
             b->bnsq[t] = dalloc<float>((size_t)o);
             chk(ctx, sa3k_weight_row_norm_sq(ctx, b->W[t], 1e-12f, b->bnsq[t]));
             if (bias && bias[t]) {

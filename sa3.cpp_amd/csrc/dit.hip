@@ -401,6 +401,7 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         chk(ctx, sa3k_weight_create(ctx, d->wtype, t.cols, t.rows, t.raw, 1, &d->hw[i]));
         const int r = tr.scope == SA3K_SCOPE_FULL ? tr.rank : 0;
         chk(ctx, sa3k_lin_create(ctx, d->hw[i], r, SA3K_PREC_BF16, head_tokens[i], &d->hl[i]));
+        lin_set_tag(d->hl[i], "head");
         if (r && tr.dora) {
             d->hbnsq[i] = dalloc<float>((size_t)t.rows);
             chk(ctx, sa3k_weight_row_norm_sq(ctx, d->hw[i], 1e-12f, d->hbnsq[i]));

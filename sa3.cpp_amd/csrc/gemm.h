@@ -18,7 +18,8 @@
 // Extra rows (Mx) let a rank-sized product that contracts the same B operand ride on the same
 // GEMM: the DoRA term 2s B^T diag(gn) W of dA shares the W^T tiles of dX.
 //
-// Epilogue per column n: v = alpha*acc; U = v (optional pre-scale copy); v *= colscale[n];
+// Epilogue per column n: v = alpha*acc; U = v (optional pre-scale copy); v *= colscale[n] (unless
+// prescale: then the main segment's accumulators were scaled before the second segment was added);
 // v += bias[n]; C = v (or C += v); Cb = bf16(v).
 #pragma once
 
@@ -71,6 +72,9 @@ struct GemmDesc {
     int64_t ldcx = 0;
     int accumulate_x = 0;
     bf16* Cbx = nullptr;   // instead of Cx: extra rows stored as bf16 [Mx][ldcx] (no accumulation)
+    // 1: colscale multiplies the main segment A . B^T only, before the second segment is added
+    // (C = colscale (.) (A B^T) + A2 B2^T); needs colscale, no extra rows and no U / Ub copies
+    int prescale = 0;
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

@@ -34,6 +34,7 @@ struct KParams {
     bf16* Cbx;
     float* ws;   // split-K partials [splits][M+Mx][N] (null: no split)
     int kps;     // K tiles per split
+    int prescale;
 };
 
 }  // namespace
@@ -213,7 +214,7 @@ __device__ inline void epilogue_elem(const KParams& p, int64_t m, int64_t n, flo
     }
     if (p.U) p.U[m * p.ldu + n] = x;
     if (p.Ub) p.Ub[m * p.ldu + n] = (bf16)x;
-    if (p.colscale) x = x * p.colscale[n];
+    if (p.colscale && !p.prescale) x = x * p.colscale[n];
     if (p.bias) x = x + p.bias[n];
     if (p.C) {
         if (p.accumulate) p.C[m * p.ldc + n] += x;
@@ -365,6 +366,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(KParams p) {
         const char* base = lds + buf * (BM + BN) * kRowBytes;
         mma_tile<FM, FN, BF16>(base, base + BM * kRowBytes, wm0, wn0, lane, acc);
     };
+    // prescale: the main segment's sums times colscale[n], before the second segment is added
+    auto scale_acc = [&] {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t n = n0 + wn0 + 16 * j + (lane & 15);
+            const float c = n < p.N ? p.colscale[n] : 0.f;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[i][j][v] = acc[i][j][v] * c;
+        }
+    };
 
     if constexpr (PD == 2) {
         uint4 ra0[NA], rb0[NB], ra1[NA], rb1[NB];
@@ -375,11 +388,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(KParams p) {
         if (T > 2) load(2, ra0, rb0);
         for (int t = 0; t < T; t += 2) {
             // tile t in LDS buffer 0; tile t+1 in ra1/rb1; tile t+2 in flight into ra0/rb0
+            if (p.prescale && t == Tm) scale_acc();
             compute(0);
             if (t + 1 < T) store(1, ra1, rb1);
             __syncthreads();
             if (t + 3 < T) load(t + 3, ra1, rb1);
             if (t + 1 >= T) break;
+            if (p.prescale && t + 1 == Tm) scale_acc();
             compute(1);
             if (t + 2 < T) store(0, ra0, rb0);
             __syncthreads();
@@ -395,11 +410,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(KParams p) {
         __syncthreads();
         for (int t = 0; t < T; ++t) {
             if (t + 1 < T) load(t + 1, ra, rb);
+            if (p.prescale && t == Tm) scale_acc();
             compute(t & 1);
             if (t + 1 < T) store((t + 1) & 1, ra, rb);
             __syncthreads();
         }
     }
+    if (p.prescale && !ext) scale_acc();   // a split without the second segment
 
     // lane holds rows 4*(lane/16)+v, column lane%16 of each 16x16 block
     if (p.ws) {  // split-K partial sums, reduced (and epilogued) by gemm_splitk_reduce
@@ -533,6 +550,8 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     SA3K_REQUIRE(d.Mx >= 0, "negative extra rows");
     SA3K_REQUIRE(d.Mx == 0 || (d.Ax && (d.Cx || d.Cbx) && al16(d.Ax) && (d.K2 == 0 || (d.A2x && al16(d.A2x)))),
                  "GEMM extra rows need Ax, Cx or Cbx (and A2x with a second segment)");
+    SA3K_REQUIRE(!d.prescale || (d.colscale && d.Mx == 0 && !d.U && !d.Ub),
+                 "GEMM prescale needs colscale and no extra rows or pre-scale copies");
     if (gemm_skinny_ok(ctx, d)) {
         KernelScope ks(ctx, prof_name);
         gemm_run_skinny(ctx, d);
@@ -549,7 +568,7 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     }
     KParams p{d.A, d.lda, d.B, d.ldb, d.Bs, d.ldbs, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K,
               d.alpha, d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
-              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0};
+              d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0, d.prescale};
     KernelScope ks(ctx, prof_name);
     if (bf) {
         if (d.a_src == SRC_BF16) launch_b<SRC_BF16, true>(ctx, p, d.b_src);

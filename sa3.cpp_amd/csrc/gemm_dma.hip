@@ -44,6 +44,7 @@ struct DmaParams {
     uint32_t a_bytes, ax_bytes, b_bytes;
     int vec_epi;   // outputs allow the 16-byte staged epilogue (aligned rows, N % 4 == 0)
     int nt_store;  // staged-epilogue output stores are non-temporal
+    int prescale;  // colscale applied to the main segment in the K loop, not in the epilogue
 };
 
 namespace {
@@ -129,7 +130,7 @@ __device__ inline void epilogue_elem(const DmaParams& p, int64_t m, int64_t n, f
     }
     if (p.U) p.U[m * p.ldu + n] = x;
     if (p.Ub) p.Ub[m * p.ldu + n] = (bf16)x;
-    if (p.colscale) x = x * p.colscale[n];
+    if (p.colscale && !p.prescale) x = x * p.colscale[n];
     if (p.bias) x = x + p.bias[n];
     if (p.C) {
         if (p.accumulate) p.C[m * p.ldc + n] += x;
@@ -175,7 +176,7 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
         bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
         st_out(p.nt_store, reinterpret_cast<uint2*>(p.Ub + m * p.ldu + n), __builtin_bit_cast(uint2, b));
     }
-    if (p.colscale) {
+    if (p.colscale && !p.prescale) {
         const float4 c = *reinterpret_cast<const float4*>(p.colscale + n);
         x = make_float4(x.x * c.x, x.y * c.y, x.z * c.z, x.w * c.w);
     }
@@ -406,6 +407,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     };
     // output row (within a block) of accumulator register v of this lane; the column is lane % MT
     auto out_row = [&](int v) { return BF16 ? 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3) : 4 * (lane >> 4) + v; };
+    // prescale: the main segment's sums times colscale[n], before the second segment is added
+    auto scale_acc = [&] {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t n = n0 + wn0 + MT * j + (lane & (MT - 1));
+            const float c = n < p.N ? p.colscale[n] : 0.f;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int v = 0; v < AE; ++v) acc[i][j][v] = acc[i][j][v] * c;
+        }
+    };
 
     // prologue: STAGES-1 tiles in flight; tile t always lives in stage t % STAGES
     static_for<STAGES - 1>([&](auto s) {
@@ -428,9 +441,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             // fence __syncthreads adds would wait for every in-flight DMA (vmcnt 0), not just tile t.
             __asm__ volatile("s_barrier" ::: "memory");
             if (t + STAGES - 1 < T) issue(IC<decltype(s)::value + STAGES - 1>{}, t + STAGES - 1);
+            if (p.prescale && t == Tm) scale_acc();
             compute(lds + decltype(s)::value * STAGE_BYTES);
         });
     }
+    if (p.prescale && !ext) scale_acc();   // a split without the second segment
 
     if (p.ws && p.counters) {  // split-K with in-kernel reduction: coherent partials, element-wise
         float* w = p.ws + (int64_t)z * Mt * p.N;
@@ -795,7 +810,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
 bool big_ok(const sa3k_ctx* ctx, const DmaParams& p) {
     auto extent = [&](int64_t rows, int64_t ld, int64_t k) -> int64_t { return rows > 0 ? ((rows - 1) * ld + k) * 2 : 0; };
     const int64_t lim = (int64_t)1 << 31;
-    if (ctx->gemm_fixup != 0) return false;
+    if (ctx->gemm_fixup != 0 || p.prescale) return false;
     if (extent(p.M, p.lda, p.K) >= lim || extent(p.N, p.ldb, p.K) >= lim) return false;
     if (p.Mx > 0 && (p.M % 8 != 0 || extent(p.Mx, p.ldax, p.K) >= lim)) return false;
     if (p.K2 > 0 && (extent(p.M, p.lda2, p.K2) >= lim || extent(p.N, p.ldb2, p.K2) >= lim ||
@@ -893,6 +908,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     DmaParams p{d.A, d.lda, d.B, d.ldb, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K, d.alpha,
                 d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
                 d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0, ctx->zero_page};
+    p.prescale = d.prescale;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

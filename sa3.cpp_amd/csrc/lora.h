@@ -4,6 +4,24 @@
 
 #include "gemm.h"
 
+// A frozen base weight W [out][in] of the C ABI (opaque to callers).
+struct sa3k_weight {
+    int type = SA3K_TYPE_F32;
+    int64_t in = 0, out = 0;
+    void* w = nullptr;      // forward layout [out][in] (Q8_0: int8 quants)
+    void* ws = nullptr;     // Q8_0: f16 scales [out][in/32]
+    void* wt = nullptr;     // transposed [in][out] (Q8_0: int8 quants)
+    void* wts = nullptr;    // Q8_0: f16 scales [in/32][out]
+    // bf16 working copies of the decoded weight, [out][in] and [in][out], built at load for every
+    // non-bf16 type: the frozen base is contracted three times per training step (forward,
+    // checkpoint recompute, dX), and the bf16-MFMA kernels round every decoded element to bf16
+    // anyway, so decoding once keeps bit-identical results and takes the per-element decode off
+    // the GEMM's inner loop. sa3k_weight_drop_working_copy frees them; the GEMMs then decode the
+    // stored blocks in the global->LDS path instead.
+    void* wb = nullptr;
+    void* wbt = nullptr;
+};
+
 namespace sa3k {
 
 struct LinGroup;
@@ -15,5 +33,12 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
 // the grouped equivalent of sa3k_lin_prepare on every member
 void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g);
 void lin_group_free(LinGroup* g);
+// A short role name ("qkv", "ff.out", ...) appended to the linear's profiler scope names, so a
+// per-kernel profile separates the projections (no effect while profiling is off).
+void lin_set_tag(sa3k_lin* l, const char* tag);
+// The B operand of X W^T (forward orientation) in g's precision: the bf16 working copy when the
+// weight has one and the precision is bf16, else the stored elements or Q8_0 planes, which the
+// GEMM decodes on their way into LDS.
+void weight_fwd_operand(const sa3k_weight* W, GemmDesc& g);
 
 }  // namespace sa3k

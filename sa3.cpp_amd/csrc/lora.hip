@@ -16,29 +16,14 @@
 //                       dX = dU W + sdUB A  and, as r extra GEMM rows sharing the W^T tiles,
 //                       dA += 2s B^T diag(gn) W + 2s^2 (B^T diag(gn) B) A
 //                       dA += sdUB^T X                     (column reduction)
-#include "gemm.h"
+#include "lora.h"
 
 #include <cmath>
+#include <set>
+#include <string>
 #include <vector>
 
 using namespace sa3k;
-
-struct sa3k_weight {
-    int type = SA3K_TYPE_F32;
-    int64_t in = 0, out = 0;
-    void* w = nullptr;      // forward layout [out][in] (Q8_0: int8 quants)
-    void* ws = nullptr;     // Q8_0: f16 scales [out][in/32]
-    void* wt = nullptr;     // transposed [in][out] (Q8_0: int8 quants)
-    void* wts = nullptr;    // Q8_0: f16 scales [in/32][out]
-    // bf16 working copies of the decoded weight, [out][in] and [in][out], built at load for every
-    // non-bf16 type: the frozen base is contracted three times per training step (forward,
-    // checkpoint recompute, dX), and the bf16-MFMA kernels round every decoded element to bf16
-    // anyway, so decoding once keeps bit-identical results and takes the per-element decode off
-    // the GEMM's inner loop. sa3k_weight_drop_working_copy frees them; the GEMMs then decode the
-    // stored blocks in the global->LDS path instead.
-    void* wb = nullptr;
-    void* wbt = nullptr;
-};
 
 struct sa3k_lin {
     const sa3k_weight* W = nullptr;
@@ -71,11 +56,19 @@ struct sa3k_lin {
     void* Ax = nullptr;                 // [r][out] compute type: 2s (B*gn)^T
     void* A2x = nullptr;                // [r][r]   compute type: 2s^2 B^T diag(gn) B
     float* red = nullptr;               // [out][r] reduced dU^T Hc
+    const char* tag = nullptr;          // role name for profiler scopes (lin_set_tag)
 };
 
 namespace {
 
 constexpr int kThreads = 256;
+
+// "<base>.<tag>" while profiling a tagged linear, else base; names are interned (scopes keep the pointer)
+const char* scope(const sa3k_ctx* ctx, const sa3k_lin* L, const char* base) {
+    if (!ctx->prof_on || !L->tag) return base;
+    static std::set<std::string> names;
+    return names.insert(std::string(base) + "." + L->tag).first->c_str();
+}
 
 template <class T>
 T* dev_alloc(size_t n) {
@@ -721,7 +714,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     const bool bf = L->prec == SA3K_PREC_BF16;
     if (bf && x_src == SRC_F32) {   // one pass to bf16 so both GEMMs stream compute-type operands
         const int64_t n = N * W->in;
-        KernelScope ks(ctx, "lin_fwd_cvt_x");
+        KernelScope ks(ctx, scope(ctx, L, "lin_fwd_cvt_x"));
         cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(
             static_cast<const float*>(X), static_cast<bf16*>(L->Xb), n, 1.0f);
         SA3K_LAUNCHED();
@@ -736,7 +729,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
         h.M = N; h.N = L->rank; h.K = W->in; h.alpha = L->s;
         if (bf) { h.Cb = static_cast<bf16*>(L->Hc); h.ldcb = L->rank; }
         else { h.C = static_cast<float*>(L->Hc); h.ldc = L->rank; }
-        gemm_run(ctx, h, "lin_fwd_h");
+        gemm_run(ctx, h, scope(ctx, L, "lin_fwd_h"));
     }
     const WOp wo = weight_operand(W, bf, false);
     GemmDesc g;
@@ -749,7 +742,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     g.C = Y; g.ldc = W->out;
     g.ldu = W->out;
     if (L->dora) { if (bf) g.Ub = static_cast<bf16*>(L->U); else g.U = static_cast<float*>(L->U); }
-    gemm_run(ctx, g, "lin_fwd_main");
+    gemm_run(ctx, g, scope(ctx, L, "lin_fwd_main"));
     L->saved_tokens = N;
 }
 
@@ -765,7 +758,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         const void* dyc = dY;
         if (bf) {
             const int64_t n = N * out;
-            KernelScope ks(ctx, "lin_bwd_cvt_dy");
+            KernelScope ks(ctx, scope(ctx, L, "lin_bwd_cvt_dy"));
             cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(dY, static_cast<bf16*>(L->dU),
                                                                                         n, 1.0f);
             SA3K_LAUNCHED();
@@ -777,7 +770,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.A = dyc; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
-        gemm_run(ctx, g, "lin_bwd_dx");
+        gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dx"));
         return;
     }
     // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens); the split partials rp[rS][rows][out]
@@ -794,7 +787,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
         int* counters = use_fixup(ctx, (int64_t)33 * out, ceil_div(out, TN_COLS)) ? ctx->tile_counters : nullptr;
         {
-            KernelScope ks(ctx, "lin_bwd_colred_dy", 2.0 * N * out * r);
+            KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_dy"), 2.0 * N * out * r);
             skinny_tn_kernel<TN_DY, float><<<dim3((unsigned)ceil_div(out, TN_COLS), (unsigned)S), kThreads, 0,
                                                ctx->stream>>>(
                 dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
@@ -812,7 +805,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         float* part = reduce_workspace(ctx, (size_t)S * (R + 1) * out * sizeof(float));
         dim3 grid((unsigned)ceil_div(out, kThreads), (unsigned)S);
         {
-            KernelScope ks(ctx, "lin_bwd_colred_dy");
+            KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_dy"));
             colred_dy_kernel<CT, R><<<grid, kThreads, 0, ctx->stream>>>(
                 dY, static_cast<const CT*>(L->dora ? L->U : nullptr), L->dora ? L->d : nullptr,
                 static_cast<const CT*>(L->Hc), static_cast<CT*>(L->dU), part, N, out, r, rows_per);
@@ -821,7 +814,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         rp = part; rS = S; rstride = (int64_t)(R + 1) * out;
     }
     {
-        KernelScope ks(ctx, "lin_bwd_rows");
+        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_rows"));
         const dim3 grid((unsigned)ceil_div(out, 64), (unsigned)ceil_div(std::max(r, 1), 4));
         dora_bwd_rows_kernel<CT><<<grid, kThreads, 0, ctx->stream>>>(
             rp, rS, rstride, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
@@ -832,7 +825,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     //    over out, so it rides on the same GEMM as r extra rows
     const bool fold_btgb = L->dora && out % (bf ? 64 : 32) == 0;
     if (L->dora && !fold_btgb) {
-        KernelScope ks(ctx, "lin_bwd_btgb");
+        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_btgb"));
         btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
                                                                          static_cast<CT*>(L->A2x));
         SA3K_LAUNCHED();
@@ -865,7 +858,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             if (bf) g.Cbx = static_cast<bf16*>(L->A2x);
             else g.Cx = static_cast<float*>(L->A2x);
         }
-        gemm_run(ctx, g, "lin_bwd_dub");
+        gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dub"));
     }
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
@@ -875,7 +868,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         if constexpr (sizeof(CT) == 2) {
             x_part = reduce_workspace(ctx, (size_t)x_S * 32 * in * sizeof(float));
             const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)x_S);
-            KernelScope ks(ctx, "lin_bwd_colred_x", 2.0 * N * in * r);
+            KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_x"), 2.0 * N * in * r);
             if (x_src == SRC_F32)
                 skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
                     static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr,
@@ -888,7 +881,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         } else {
             x_part = reduce_workspace(ctx, (size_t)x_S * R * in * sizeof(float));
             const dim3 grid((unsigned)ceil_div(in, kThreads), (unsigned)x_S);
-            KernelScope ks(ctx, "lin_bwd_colred_x");
+            KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_x"));
             if (x_src == SRC_F32)
                 colred_x_kernel<float, CT, R><<<grid, kThreads, 0, ctx->stream>>>(
                     static_cast<const float*>(X), static_cast<const CT*>(L->sdUB), x_part, N, in, r, x_rows_per);
@@ -900,7 +893,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     };
     auto x_sum = [&] {
         if (x_counters) return;   // summed in-kernel
-        KernelScope ks(ctx, "lin_bwd_reduce");
+        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_reduce"));
         const int64_t stride = (sizeof(CT) == 2 ? (int64_t)32 : (int64_t)R) * in;
         sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
             x_part, stride, x_S, (int64_t)r * in, dA, 1);
@@ -926,7 +919,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             g.Mx = r; g.Ax = L->Ax; g.ldax = out; g.A2x = L->A2x; g.lda2x = r;
             g.Cx = dA; g.ldcx = in; g.accumulate_x = 1;
         }
-        gemm_run(ctx, g, "lin_bwd_dx");
+        gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dx"));
     } else if (L->dora) {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
@@ -934,7 +927,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
         g.M = r; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dA; g.ldc = in; g.accumulate = 1;
-        gemm_run(ctx, g, "lin_bwd_dora_da");
+        gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dora_da"));
     }
     // 4b. the partial sums into dA, after step 3
     if (early) {
@@ -1183,6 +1176,17 @@ __global__ __launch_bounds__(kThreads) void group_dora_terms_kernel(const PrepDe
 }  // namespace
 
 namespace sa3k {
+
+void lin_set_tag(sa3k_lin* l, const char* tag) { l->tag = tag; }
+
+void weight_fwd_operand(const sa3k_weight* W, GemmDesc& g) {
+    const WOp wo = weight_operand(W, g.prec == SA3K_PREC_BF16, false);
+    g.b_src = wo.src;
+    g.B = wo.p;
+    g.ldb = wo.ld;
+    g.Bs = wo.s;
+    g.ldbs = wo.lds;
+}
 
 struct LinGroup {
     std::vector<sa3k_lin*> lins;

@@ -30,6 +30,11 @@ class AdamWParams(C.Structure):
                 ("eps", C.c_float), ("weight_decay", C.c_float), ("grad_clip", C.c_float)]
 
 
+class ChainAdapter(C.Structure):
+    _fields_ = [("dora", C.c_int), ("rank", C.c_int), ("alpha", C.c_float), ("strength", C.c_float),
+                ("A", C.c_void_p), ("B", C.c_void_p), ("magnitude", C.c_void_p)]
+
+
 class BlockConfig(C.Structure):
     _fields_ = [("dim", C.c_int), ("heads", C.c_int), ("head_dim", C.c_int), ("inner", C.c_int),
                 ("rope_dims", C.c_int), ("window", C.c_int), ("rope_base", C.c_float), ("norm_eps", C.c_float),
@@ -106,6 +111,10 @@ def _declare(lib):
         "sa3k_lin_prepare": (I, [P, P, P, P, F, I, P, P]),
         "sa3k_lin_forward": (I, [P, P, I, P, I64, P, P]),
         "sa3k_lin_backward": (I, [P, P, I, P, I64, P, P, I, P, P, P]),
+        "sa3k_lora_chain_create": (I, [P, P, I, C.POINTER(ChainAdapter), I64, C.POINTER(P)]),
+        "sa3k_lora_chain_destroy": (I, [P, P]),
+        "sa3k_lora_chain_forward": (I, [P, P, I, P, I64, P, P]),
+        "sa3k_lora_chain_constants": (I, [P, P, P, P, C.POINTER(I)]),
         "sa3k_diff_attn_fwd": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P]),
         "sa3k_diff_attn_bwd": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, F, P, P, P, P, P, P, P]),
         "sa3k_block_create": (I, [P, C.POINTER(BlockConfig), C.POINTER(BlockWeights), I, I64, I64, C.POINTER(P)]),
@@ -329,6 +338,16 @@ class Context:
         self.check(self.lib.sa3k_weight_create(self.h, wtype, in_, out_, data.ctypes.data, 0, C.byref(h)))
         return Weight(self, h.value, in_, out_, wtype)
 
+    def lora_chain(self, weight, adapters, max_tokens):
+        """adapters: [(dora, rank, alpha, strength, A DeviceArray, B DeviceArray, magnitude DeviceArray | None)]"""
+        arr = (ChainAdapter * max(1, len(adapters)))()
+        for i, (dora, rank, alpha, strength, A, B, mag) in enumerate(adapters):
+            arr[i] = ChainAdapter(int(dora), int(rank), float(alpha), float(strength), A.ptr, B.ptr,
+                                  mag.ptr if mag is not None else None)
+        h = C.c_void_p()
+        self.check(self.lib.sa3k_lora_chain_create(self.h, weight.h, len(adapters), arr, max_tokens, C.byref(h)))
+        return LoraChain(self, h.value, weight)
+
     def lin(self, weight, rank, prec, max_tokens):
         h = C.c_void_p()
         self.check(self.lib.sa3k_lin_create(self.h, weight.h, rank, prec, max_tokens, C.byref(h)))
@@ -355,6 +374,31 @@ class Weight:
     def destroy(self):
         if self.h:
             self.ctx.check(self.ctx.lib.sa3k_weight_destroy(self.ctx.h, self.h))
+            self.h = None
+
+
+class LoraChain:
+    def __init__(self, ctx, h, weight):
+        self.ctx, self.h, self.weight = ctx, h, weight
+
+    def forward(self, X, N, Y, bias=None, x_type=TYPE_F32):
+        self.ctx.check(self.ctx.lib.sa3k_lora_chain_forward(self.ctx.h, self.h, x_type, X.ptr, N,
+                                                            bias.ptr if bias is not None else None, Y.ptr))
+
+    def constants(self):
+        """(base_scale [out], B' [out][R]) as numpy, or (None, None) for an empty chain"""
+        R = C.c_int()
+        self.ctx.check(self.ctx.lib.sa3k_lora_chain_constants(self.ctx.h, self.h, None, None, C.byref(R)))
+        if R.value == 0:
+            return None, None
+        out_ = self.weight.out_
+        c0, Bp = self.ctx.empty(out_), self.ctx.empty((out_, R.value))
+        self.ctx.check(self.ctx.lib.sa3k_lora_chain_constants(self.ctx.h, self.h, c0.ptr, Bp.ptr, None))
+        return c0.numpy(), Bp.numpy()
+
+    def destroy(self):
+        if self.h:
+            self.ctx.check(self.ctx.lib.sa3k_lora_chain_destroy(self.ctx.h, self.h))
             self.h = None
 
 

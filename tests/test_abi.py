@@ -1,8 +1,8 @@
 """The C-ABI library and the oracle build and export what their headers declare (no GPU calls)."""
-import ctypes
 import os
 import re
 import subprocess
+import sys
 
 from conftest import ROOT, sa3k
 
@@ -30,11 +30,14 @@ def test_no_other_exports():
 
 def test_create_fails_cleanly_without_device():
     # On a machine without a GPU (or with an out-of-range ordinal) creation returns NULL + message.
-    lib = sa3k.load_library()
-    err = ctypes.create_string_buffer(256)
-    h = lib.sa3k_create(1 << 20, err, 256)
-    assert not h
-    assert err.value
+    # Run in a child process: the call initialises the HIP runtime, which the rest of the CPU suite
+    # (oracle, subprocess-heavy tests) should not share a process with.
+    code = ("import ctypes, sys; sys.path.insert(0, %r); import sa3k; lib = sa3k.load_library(); "
+            "err = ctypes.create_string_buffer(256); h = lib.sa3k_create(1 << 20, err, 256); "
+            "print('null' if not h else 'handle', err.value.decode())") % os.path.dirname(sa3k.LIB_PATH)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.startswith("null ") and len(r.stdout.strip()) > len("null")
 
 
 def test_oracle_exports():
