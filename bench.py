@@ -193,16 +193,27 @@ class LinearWorkload:
             if self.kind == "dora_q8" else self.W_host
         mag = oracle.row_norms(Wd) if self.dora else None
         bnsq = oracle.row_norm_sq(Wd) if self.dora else None
-        times = []
-        t_end = time.time() + 10.0
-        while time.time() < t_end or not times:
-            t0 = time.perf_counter()
+        def once():
             oracle.dit_lin_fwd(self.X_host, Wd, self.A_host, self.B_host, self.s, self.dora, mag, bnsq)
             oracle.dit_lin_bwd(self.X_host, Wd, self.dY_host, self.A_host, self.B_host, self.s, self.dora, mag, bnsq)
-            times.append(time.perf_counter() - t0)
-        return {"value": round(float(np.median(times)) * 1e3, 1), "unit": "ms/update (fwd+bwd, same shapes)",
+        with oracle.f32_mode():
+            t, times = _median_time(once, runs=5)
+        return {"value": round(t * 1e3, 1), "unit": "ms/update (fwd+bwd, same shapes)",
                 "cores": oracle.lib().orc_num_threads(), "kind": "port",
-                "sample": f"{len(times)} full-size fwd+bwd of the oracle restatement (double accumulation, OpenMP)"}
+                "sample": f"median of {len(times)} full-size fwd+bwd after a warm-up: the oracle restatement in its "
+                          f"f32 mode (float accumulation, AVX2/FMA products, OpenMP)"}
+
+
+def _median_time(fn, runs=3):
+    """one untimed warm-up call (it also maps the memory the later calls reuse), then the median of
+    `runs` timed calls: (median seconds, [seconds])"""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times
 
 
 def block_flops(B, S, Ctx, dim, inner, r, window, dora=True, heads=None):
@@ -313,26 +324,27 @@ class BlockWorkload:
         return {"algorithmic_gflop_per_update": round((fwd + bwd) / 1e9, 2),
                 "tflops_whole_update": round((fwd + bwd) / (ms_per_step * 1e-3) / 1e12, 1)}
 
-    def cpu_baseline(self):
+    def oracle_block(self):
+        """the oracle's view of this block (full size): (block_binding, cfg, weights, x, ctx, gcond, dout)"""
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
         bb = _load("block_binding", os.path.join(ROOT, "oracle", "block_binding.py"))
-        S_s = 136   # bounded sample: 64 memory + 72 latent tokens per sample, same weights
-        cfg = dict(B=self.B, S=S_s, Ctx=self.Ctx, dim=self.dim, heads=self.heads, inner=self.inner,
+        cfg = dict(B=self.B, S=self.S, Ctx=self.Ctx, dim=self.dim, heads=self.heads, inner=self.inner,
                    window=self.window, rank=self.r, alpha=32.0, dora=True)
         W = [w.astype(np.float32) for w in self.W_host]
         w = dict(self.vecs, W=W, bias=self.bias_host, A=self.A_host, B=self.B_host, mag=self.mag_host,
                  bnsq=[((x.astype(np.float64) ** 2).sum(1) + x.shape[1] * 1e-12).astype(np.float32) for x in W])
-        x, dout = self.x_host[:, :S_s], self.dout_host[:, :S_s]
-        t0 = time.perf_counter()
-        bb.block_bwd(cfg, w, x, self.ctx_host, self.gc_host, dout)   # forward + backward
-        dt = time.perf_counter() - t0
-        f_s = sum(block_flops(self.B, S_s, self.Ctx, self.dim, self.inner, self.r, self.window))
-        f_full = sum(self.flops())
-        return {"value": round(dt * f_full / f_s * 1e3, 1), "unit": "ms/update (fwd+bwd, scaled by algorithmic flops)",
+        return bb, cfg, w, self.x_host, self.ctx_host, self.gc_host, self.dout_host
+
+    def cpu_baseline(self):
+        bb, cfg, w, x, ctx, gc, dout = self.oracle_block()
+        with sys.modules["oracle"].f32_mode():
+            t, times = _median_time(lambda: bb.block_bwd(cfg, w, x, ctx, gc, dout), runs=3)
+        return {"value": round(t * 1e3, 1), "unit": "ms/update (block fwd+bwd at full size)",
                 "cores": bb.lib().orc_num_threads(), "kind": "port",
-                "sample": f"one fwd+bwd of the oracle block at S={S_s} (batch {self.B}) in {dt:.1f} s, scaled "
-                          f"by the algorithmic flop ratio {f_full / f_s:.2f}"}
+                "sample": f"median of {len(times)} runs after a warm-up ({', '.join(f'{v:.2f}' for v in times)} s) "
+                          f"of the oracle block forward + backward at B={self.B}, S={self.S} in its f32 mode "
+                          f"(float accumulation, AVX2/FMA products, OpenMP); the adapter update itself not included"}
 
 
 def dit_head_flops(B, T, Ctx, io, dim, cond_dim, time_dim, r, dora=True, adapted=True):
@@ -410,28 +422,43 @@ class DitWorkload:
                 "tflops_whole_update": round((fwd + bwd) / (ms_per_step * 1e-3) / 1e12, 1)}
 
     def cpu_baseline(self):
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
-        _load("block_binding", os.path.join(ROOT, "oracle", "block_binding.py"))
+        """The oracle in its f32 mode on the host cores, timed, not extrapolated: one block of this model
+        at full size (B 2, S 64 + 1024, window 256, DoRA r 32 on all 7 projections), forward + backward,
+        median of 3 runs after a warm-up; the head and tail (a depth-0 DiT loss + gradient at T 1024,
+        median of 3); the update = head/tail + 24 x block. The AdamW step is not included."""
+        blk = BlockWorkload.__new__(BlockWorkload)
+        g = rng(7)
+        nd = lambda shape, sd: g.normal(0, sd, shape).astype(np.float32)
+        S = self.mem + self.T
+        dims = sys.modules["sa3k"].block_target_dims(self.dim, self.inner)
+        blk.B, blk.S, blk.Ctx, blk.dim, blk.heads, blk.inner, blk.r, blk.window = \
+            self.B, S, self.Ctx, self.dim, self.heads, self.inner, self.r, self.window
+        blk.W_host = [nd((o, i), 0.02) for i, o in dims]
+        blk.bias_host = [None] * 5 + [nd(dims[5][1], 0.02), nd(dims[6][1], 0.02)]
+        blk.vecs = dict(ssg=nd(6 * self.dim, 0.1), pre_g=1 + nd(self.dim, 0.1), cross_g=1 + nd(self.dim, 0.1),
+                        ff_g=1 + nd(self.dim, 0.1), sq_g=1 + nd(64, 0.1), sk_g=1 + nd(64, 0.1),
+                        cq_g=1 + nd(64, 0.1), ck_g=1 + nd(64, 0.1))
+        blk.A_host = [g.uniform(-1 / np.sqrt(i), 1 / np.sqrt(i), (self.r, i)).astype(np.float32) for i, o in dims]
+        blk.B_host = [nd((o, self.r), 0.01) for i, o in dims]
+        blk.mag_host = [np.sqrt((W.astype(np.float64) ** 2).sum(1)).astype(np.float32) for W in blk.W_host]
+        blk.x_host, blk.ctx_host = nd((self.B, S, self.dim), 1.0), nd((self.B, self.Ctx, self.dim), 1.0)
+        blk.gc_host, blk.dout_host = nd((self.B, 6 * self.dim), 0.1), nd((self.B, S, self.dim), 1e-2)
+        bb, cfg, w, x, ctx, gc, dout = blk.oracle_block()
         db = _load("dit_binding", os.path.join(ROOT, "oracle", "dit_binding.py"))
-        # bounded sample: the same model shape with 1 block and 72 frames (batch 2), scaled by
-        # the algorithmic flop ratio to 24 blocks x 1024 frames
-        T_s, depth_s = 72, 1
-        cfg = dict(B=self.B, T=T_s, Ctx=self.Ctx, io=self.io, dim=self.dim, heads=self.heads, inner=self.inner,
-                   depth=depth_s, mem=self.mem, cond_dim=self.cond_dim, time_dim=self.time_dim, rope_dims=32,
-                   window=self.window, rank=self.r, alpha=32.0, dora=True)
-        tensors, adapters, inputs = db.random_dit(3, cfg, "full", w_sd=0.02, b_sd=0.01)
-        t0 = time.perf_counter()
-        db.dit_loss(cfg, tensors, adapters, inputs)
-        dt = time.perf_counter() - t0
-        S_s = self.mem + T_s
-        f, b = block_flops(self.B, S_s, self.Ctx, self.dim, self.inner, self.r, self.window)
-        hf, hb = dit_head_flops(self.B, T_s, self.Ctx, self.io, self.dim, self.cond_dim, self.time_dim, self.r)
-        ratio = sum(self.flops()) / (depth_s * (f + b) + hf + hb)
-        return {"value": round(dt * ratio * 1e3, 1), "unit": "ms/update (fwd+bwd, scaled by algorithmic flops)",
-                "cores": db.lib().orc_num_threads(), "kind": "port",
-                "sample": f"one loss+gradient pass of the oracle DiT with {depth_s} block and {T_s} frames "
-                          f"(batch {self.B}) in {dt:.1f} s, scaled by the algorithmic flop ratio {ratio:.1f}"}
+        hcfg = dict(B=self.B, T=self.T, Ctx=self.Ctx, io=self.io, dim=self.dim, heads=self.heads,
+                    inner=self.inner, depth=0, mem=self.mem, cond_dim=self.cond_dim, time_dim=self.time_dim,
+                    rope_dims=32, window=self.window, rank=self.r, alpha=32.0, dora=True)
+        tensors, adapters, inputs = db.random_dit(3, hcfg, "full", w_sd=0.02, b_sd=0.01)
+        with sys.modules["oracle"].f32_mode():
+            t_b, tb = _median_time(lambda: bb.block_bwd(cfg, w, x, ctx, gc, dout), runs=3)
+            t_h, th = _median_time(lambda: db.dit_loss(hcfg, tensors, adapters, inputs), runs=3)
+        value = t_h + self.depth * t_b
+        return {"value": round(value * 1e3, 1), "unit": "ms/update (forward + backward, no AdamW)",
+                "cores": bb.lib().orc_num_threads(), "kind": "port",
+                "sample": f"the oracle in its f32 mode (float accumulation, AVX2/FMA products, OpenMP): one "
+                          f"full-size block fwd+bwd (B {self.B}, S {S}), median of {len(tb)} after a warm-up "
+                          f"= {t_b:.2f} s ({', '.join(f'{v:.2f}' for v in tb)}); head + tail (depth-0 DiT "
+                          f"loss+grad, T {self.T}) median {t_h:.2f} s; update = head/tail + {self.depth} x block"}
 
 
 def measured_traffic(kernel):

@@ -64,6 +64,7 @@ dvec lin_bwd(const Lin& L, const dvec& X, int N, const dvec& dY, float* dA, floa
 void rms_fwd(const dvec& x, int n, int w, const float* g, double eps, dvec& y, dvec& rstd) {
     y.resize((size_t)n * w);
     rstd.resize((size_t)n);
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < n; ++i) {
         double ss = 0;
         for (int j = 0; j < w; ++j) ss += x[(size_t)i * w + j] * x[(size_t)i * w + j];
@@ -75,6 +76,7 @@ void rms_fwd(const dvec& x, int n, int w, const float* g, double eps, dvec& y, d
 // dx from dy for y = x * rstd * gamma
 void rms_bwd(const dvec& x, const dvec& rstd, int n, int w, const float* g, const dvec& dy, dvec& dx) {
     dx.assign((size_t)n * w, 0.0);
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < n; ++i) {
         const double r = rstd[(size_t)i];
         double dot = 0;
@@ -109,6 +111,7 @@ struct Fwd {
 // heads: take column block `part` (width dim) of a [n][parts*dim] matrix -> [B*H][Sx][64]
 dvec heads(const dvec& m, int B, int Sx, int parts, int part, int dim, int H) {
     dvec o((size_t)B * H * Sx * 64);
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int t = 0; t < Sx; ++t)
             for (int hh = 0; hh < H; ++hh)
@@ -118,6 +121,7 @@ dvec heads(const dvec& m, int B, int Sx, int parts, int part, int dim, int H) {
     return o;
 }
 void unheads_add(const dvec& hv, int B, int Sx, int parts, int part, int dim, int H, dvec& m) {
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int t = 0; t < Sx; ++t)
             for (int hh = 0; hh < H; ++hh)
@@ -129,6 +133,7 @@ void unheads_add(const dvec& hv, int B, int Sx, int parts, int part, int dim, in
 // per-head rms norm (over 64) then optional rope; pre = normalised (before gamma) for backward
 void qk_fwd(dvec& hv, int BH, int Sx, const float* g, double eps, int rope, double base, dvec& rstd) {
     rstd.resize((size_t)BH * Sx);
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < BH * Sx; ++i) {
         double* p = &hv[(size_t)i * 64];
         double ss = 0;
@@ -142,6 +147,7 @@ void qk_fwd(dvec& hv, int BH, int Sx, const float* g, double eps, int rope, doub
 // backward of qk_fwd given the pre-norm input `in`
 dvec qk_bwd(const dvec& in, const dvec& rstd, int BH, int Sx, const float* g, int rope, double base, dvec dy) {
     dvec dx((size_t)BH * Sx * 64);
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < BH * Sx; ++i) {
         double* d = &dy[(size_t)i * 64];
         if (rope) rope_vec(d, rope, (double)(i % Sx), base, true);   // rotation transpose
@@ -165,6 +171,7 @@ dvec attn_fwd(const dvec& q1, const dvec& k1, const dvec& q2, const dvec& k2, co
 // [B*H][S][64] -> token-major [B*S][H*64]
 dvec tokmajor(const dvec& hv, int B, int H, int Sx) {
     dvec o((size_t)B * Sx * H * 64);
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int hh = 0; hh < H; ++hh)
             for (int t = 0; t < Sx; ++t)
@@ -174,6 +181,7 @@ dvec tokmajor(const dvec& hv, int B, int H, int Sx) {
 }
 dvec headmajor(const dvec& tm, int B, int H, int Sx) {
     dvec o((size_t)B * H * Sx * 64);
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int hh = 0; hh < H; ++hh)
             for (int t = 0; t < Sx; ++t)
@@ -202,6 +210,7 @@ static void block_forward(const orc_block* p, const float* xin, const float* ctx
     // self attention
     rms_fwd(f.x, N, dim, p->pre_g, eps, f.hn_a, f.rs_a);
     f.h.resize((size_t)N * dim);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < dim; ++c)
             f.h[(size_t)n * dim + c] = f.hn_a[(size_t)n * dim + c] * (1 + mod(n / S, 0, c)) + mod(n / S, 1, c);
@@ -217,6 +226,7 @@ static void block_forward(const orc_block* p, const float* xin, const float* ctx
     f.o = tokmajor(attn_fwd(f.q, f.k, f.qd, f.kd, f.v, B * H, S, S, p->window), B, H, S);
     f.y = lin_fwd(mk(p, 1), f.o, N);
     f.x1.resize((size_t)N * dim);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < dim; ++c)
             f.x1[(size_t)n * dim + c] = f.x[(size_t)n * dim + c] + f.y[(size_t)n * dim + c] * sigm(1 - mod(n / S, 2, c));
@@ -241,12 +251,14 @@ static void block_forward(const orc_block* p, const float* xin, const float* ctx
     // feed-forward
     rms_fwd(f.x2, N, dim, p->ff_g, eps, f.fn, f.rs_f);
     f.f_in.resize((size_t)N * dim);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < dim; ++c)
             f.f_in[(size_t)n * dim + c] = f.fn[(size_t)n * dim + c] * (1 + mod(n / S, 3, c)) + mod(n / S, 4, c);
     f.F = lin_fwd(mk(p, 5), f.f_in, N);
     const int I = p->inner;
     f.g.resize((size_t)N * I);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < I; ++c) {
             const double val = f.F[(size_t)n * 2 * I + c], glu = f.F[(size_t)n * 2 * I + I + c];
@@ -254,6 +266,7 @@ static void block_forward(const orc_block* p, const float* xin, const float* ctx
         }
     f.yf = lin_fwd(mk(p, 6), f.g, N);
     f.out.resize((size_t)N * dim);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < dim; ++c)
             f.out[(size_t)n * dim + c] = f.x2[(size_t)n * dim + c] + f.yf[(size_t)n * dim + c] * sigm(1 - mod(n / S, 5, c));
@@ -278,8 +291,9 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
     dvec d3 = fv(dout, (size_t)N * dim);
     // out = x2 + yf * s_f
     dvec dyf((size_t)N * dim), dx2 = d3;
-    for (int n = 0; n < N; ++n)
-        for (int c = 0; c < dim; ++c) {
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < dim; ++c)
+        for (int n = 0; n < N; ++n) {
             const size_t i = (size_t)n * dim + c;
             const double s = sigm(1 - mod(n / S, 5, c));
             dyf[i] = d3[i] * s;
@@ -287,6 +301,7 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
         }
     const dvec dg = lin_bwd(mk(p, 6), f.g, N, dyf, dA[6], dB[6], dm[6]);
     dvec dF((size_t)N * 2 * I);
+#pragma omp parallel for schedule(static)
     for (int n = 0; n < N; ++n)
         for (int c = 0; c < I; ++c) {
             const double val = f.F[(size_t)n * 2 * I + c], glu = f.F[(size_t)n * 2 * I + I + c];
@@ -296,8 +311,9 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
         }
     const dvec dfin = lin_bwd(mk(p, 5), f.f_in, N, dF, dA[5], dB[5], dm[5]);
     dvec dfn((size_t)N * dim);
-    for (int n = 0; n < N; ++n)
-        for (int c = 0; c < dim; ++c) {
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < dim; ++c)
+        for (int n = 0; n < N; ++n) {
             const size_t i = (size_t)n * dim + c;
             dfn[i] = dfin[i] * (1 + mod(n / S, 3, c));
             dmod(n / S, 3, c) += dfin[i] * f.fn[i];
@@ -330,8 +346,9 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
     }
     // x1 = x + y * s_a
     dvec dy((size_t)N * dim), dxx = dx1;
-    for (int n = 0; n < N; ++n)
-        for (int c = 0; c < dim; ++c) {
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < dim; ++c)
+        for (int n = 0; n < N; ++n) {
             const size_t i = (size_t)n * dim + c;
             const double s = sigm(1 - mod(n / S, 2, c));
             dy[i] = dx1[i] * s;
@@ -352,8 +369,9 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
         unheads_add(qk_bwd(f.pre[3], f.rq[3], B * H, S, p->sk_g, p->rope_dims, base, dvec(dk2.begin(), dk2.end())), B, S, 5, 4, dim, H, dqkv);
         const dvec dh = lin_bwd(mk(p, 0), f.h, N, dqkv, dA[0], dB[0], dm[0]);
         dvec dhn((size_t)N * dim);
-        for (int n = 0; n < N; ++n)
-            for (int c = 0; c < dim; ++c) {
+#pragma omp parallel for schedule(static)
+        for (int c = 0; c < dim; ++c)
+            for (int n = 0; n < N; ++n) {
                 const size_t i = (size_t)n * dim + c;
                 dhn[i] = dh[i] * (1 + mod(n / S, 0, c));
                 dmod(n / S, 0, c) += dh[i] * f.hn_a[i];

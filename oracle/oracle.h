@@ -157,6 +157,13 @@ void orc_expo_features(float t, float* out, int dim, float min_f, float max_f);
 
 int orc_num_threads(void);
 
+/* 1: the linears (orc_dit_lin_*, and through them the block and DiT functions) and the attention
+ * compute in float, with AVX2/FMA products where orc_f32_fast() says the CPU has them: the CPU
+ * baseline's mode. 0 (the default): double, the pinned oracle. Not thread-safe; set it between
+ * calls. */
+void orc_set_f32(int on);
+int orc_f32_fast(void);
+
 #ifdef __cplusplus
 }
 #endif

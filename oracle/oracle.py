@@ -53,12 +53,28 @@ def lib():
                                    optf, optf, optf, optf]),
         "orc_gemm_nt": (None, [f32p, f32p, f32p, I64, I64, I64]),
         "orc_num_threads": (I, []),
+        "orc_set_f32": (None, [I]),
+        "orc_f32_fast": (I, []),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
         fn.restype, fn.argtypes = res, args
     _lib = L
     return L
+
+
+class f32_mode:
+    """with f32_mode(): the linears and the attention (and the block / DiT functions over them)
+    compute in float with the AVX2/FMA products: the CPU baseline's mode. The double oracle is
+    restored on exit."""
+
+    def __enter__(self):
+        lib().orc_set_f32(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_f32(0)
+        return False
 
 
 def _p(a):
