@@ -110,8 +110,15 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 end of one block (its last column reduction and dA sums) runs beside the next
  *                 block, which waits for it only before it rewrites the scratch that work reads
  *                 (default 1)
+ *   "lin_merge"   1: a bf16-precision adapted linear prepared from now on contracts the merged
+ *                 weight W + s B A, rounded once to bf16 and refreshed by every prepare, in its
+ *                 forward and dX products (the rank products s X A^T and s dU B then only feed
+ *                 the adapter gradients and run beside them); 0: the base and the rank term as two
+ *                 segments of one product (default 1). It holds for a linear or linear group from
+ *                 its next prepare (a DiT: from its setup).
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny, gemm_big and gemm_splits, which change the f32 summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big, gemm_splits and lin_merge, which change the f32 summation
+ * order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

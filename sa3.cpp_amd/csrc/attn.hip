@@ -659,7 +659,7 @@ void attn_forward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2,
     FwdArgs a{q1, k1, q2, k2, v, H, Sq, Sk, window, scale, o, o1, o2, lse1, lse2};
     dim3 grid((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H));
     KernelScope ks(ctx, Sq == Sk ? "attn_fwd" : "attn_fwd_cross");
-    attn_fwd_kernel<<<grid, kThreads, 0, ctx->stream>>>(a);
+    launch_k(ctx, true, attn_fwd_kernel, grid, dim3(kThreads), 0, a);
     SA3K_LAUNCHED();
 }
 

@@ -715,6 +715,12 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         w->x = x;
         w->ctxf = context;
         const float* mv = w->modv;
+        // the rank products of merged linears (read by this block's backward only) run on the second
+        // stream beside the main products; joined at the end unless a caller joins
+        const bool join_here = ctx->side_defer == 0;
+        const uint64_t forks0 = ctx->side_forks;
+        SideDeferScope defer(ctx);
+        auto arm = [&] { if (side_usable(ctx)) fork_arm(ctx); };   // the next kernel records the fork
         // element-wise kernels index with 32-bit ints
         SA3K_REQUIRE(N * 2 * I < ((int64_t)1 << 31) && N * H * 5 < ((int64_t)1 << 31), "too many tokens");
         if (w->rope_tab_dims != c.rope_dims || w->rope_tab_base != c.rope_base) {
@@ -734,15 +740,18 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         launch(ctx, "blk_modv", modv_kernel, dim3(nblk((int64_t)B * 6 * D)), (const float*)b->ssg, gcond,
                (int64_t)B * 6 * D, 6 * D, w->modv);
         // self attention
+        arm();
         resnorm(x, nullptr, -1, nullptr, b->pre_g, 0, w->h, w->rs_a);
         chk(ctx, sa3k_lin_forward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, nullptr, w->qkv));
         PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.qk_eps, w->rope_tab,
                     {{w->q1, b->sq_g, 1}, {w->k1, b->sk_g, 1}, {w->v, nullptr, 0}, {w->q2, b->sq_g, 1}, {w->k2, b->sk_g, 1}},
                     w->rq};
         launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), ps, (int)(N * H));
+        arm();
         attn_forward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, B, H, S, S, c.window, scale, w->o, w->o1, w->o2, w->l1, w->l2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, nullptr, w->y));
         // cross attention: x1 = x + y * sigmoid(1 - g_a), hc = rms_norm(x1) * cross_g
+        arm();
         resnorm(x, w->y, 2, w->x1, b->cross_g, -1, w->hc, w->rs_c);
         chk(ctx, sa3k_lin_forward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, nullptr, w->qf));
         chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
@@ -752,15 +761,19 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         PrepArgs pk{w->kv, 3, Ctx, H, D, c.rope_dims, c.qk_eps, nullptr,
                     {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck};
         launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(NC * H)), pk, (int)(NC * H));
+        arm();
         attn_forward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, B, H, S, Ctx, 0, scale, w->oc, w->co1, w->co2, w->cl1, w->cl2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, nullptr, w->yc));
         // feed-forward: x2 = x1 + yc, fin = rms_norm(x2) * ff_g * (1 + sc_f) + sh_f
+        arm();
         resnorm(w->x1, w->yc, -1, w->x2, b->ff_g, 3, w->fin, w->rs_f);
         chk(ctx, sa3k_lin_forward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, b->bias[5], w->F));
+        arm();
         launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->F, I, (int)(N * I / 4), w->g);
         chk(ctx, sa3k_lin_forward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, b->bias[6], w->yf));
         launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D / 4)), (const float*)w->x2, (const float*)w->yf, mv, 5,
                S, D, (int)(N * D / 4), out);
+        if (join_here) side_join_since(ctx, forks0);
     }
 }
 

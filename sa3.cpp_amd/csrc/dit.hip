@@ -545,6 +545,11 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     const int B = d->tr.batch, T = d->tr.frames, Ctx = d->tr.ctx_tokens, S = d->S;
     const int64_t NT = (int64_t)B * T, NC = (int64_t)B * Ctx, D = c.dim;
     prepare(ctx, d);
+    // the rank products of merged linears run on the second stream, read by the backward only: one
+    // join at the end (per block under recompute, whose blocks share one workspace)
+    const bool join_here = ctx->side_defer == 0;
+    const uint64_t forks0 = ctx->side_forks;
+    SideDeferScope defer(ctx);
     // conditioning
     launch(ctx, "dit_head", expo_kernel, dim3(nblk((int64_t)B * (c.time_dim / 2))), t, B, c.time_dim,
            logf(c.time_min_freq), logf(c.time_max_freq), d->tf);
@@ -561,8 +566,10 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B, T,
            c.mem_tokens, (int)D, d->xs[0]);
     // blocks
-    for (int l = 0; l < c.depth; ++l)
+    for (int l = 0; l < c.depth; ++l) {
         block_forward(ctx, d->blocks[l], d->ws[d->tr.recompute ? 0 : l], d->xs[l], d->context, d->gcond, d->xs[l + 1]);
+        if (d->tr.recompute) side_join_since(ctx, forks0);
+    }
     // tail
     launch(ctx, "dit_tail", gather_frames_kernel, dim3(nblk(NT * D)), (const float*)d->xs[c.depth], B, T, c.mem_tokens,
            (int)D, d->xt);
@@ -570,6 +577,7 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     lin_fwd(ctx, d, H_POST_CONV, d->v0, NT, d->vel);
     launch(ctx, "dit_tail", add_kernel, dim3(nblk(NT * c.io)), (const float*)d->vel, (const float*)d->v0, NT * c.io,
            d->vel);
+    if (join_here) side_join_since(ctx, forks0);
 }
 
 // per-sample velocity MSE of the last forward into d->loss, and its seed gradient into d->dv

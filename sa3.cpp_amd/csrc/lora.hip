@@ -18,6 +18,7 @@
 //                       dA += sdUB^T X                     (column reduction)
 #include "lora.h"
 
+#include <algorithm>
 #include <cmath>
 #include <set>
 #include <string>
@@ -57,6 +58,14 @@ struct sa3k_lin {
     void* A2x = nullptr;                // [r][r]   compute type: 2s^2 B^T diag(gn) B
     float* red = nullptr;               // [out][r] reduced dU^T Hc
     const char* tag = nullptr;          // role name for profiler scopes (lin_set_tag)
+    // merged mode (bf16 precision): the products contract W_eff = W + s B A, refreshed by prepare
+    int merged = 0;
+    void* Wm = nullptr;                 // [out][in] bf16 W_eff
+    void* Wmt = nullptr;                // [in][out] bf16 W_eff^T
+    sa3k::LinGroup* solo = nullptr;     // one-member group refreshing a separately prepared linear
+    const float* solo_key[4] = {};      // its A, B, magnitude, base_norm_sq pointers
+    float solo_s = 0.0f;
+    int solo_dora = -1;
 };
 
 namespace {
@@ -589,7 +598,8 @@ __global__ __launch_bounds__(kThreads) void sum_splits_kernel(const float* __res
 // gd[o] and dUtH[a][o] are the split sums (in split order) of the column-reduction partials
 // part[sp][row][o], row 0 = gd, row 1 + a = dUtH[a]; then
 // dm += gd/sqrt(nsq); gn = -gd m nsq^-3/2 / 2; dB[o][a] += dUtH[a][o] + 2s gn P[o][a] + 2s^2 gn BG[o][a];
-// Ax[a][o] = 2s B[o][a] gn[o]  (lora: dB += dUtH only)
+// Ax[a][o] = 2s B[o][a] gn[o]  (lora: dB += dUtH only). With BG null, P is W_eff A^T = P + s B G and
+// the last term is left out.
 template <class CT>
 __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __restrict__ part, int S, int64_t stride,
                                                                  const float* __restrict__ nsq, const float* __restrict__ mag,
@@ -629,7 +639,8 @@ __global__ __launch_bounds__(kThreads) void dora_bwd_rows_kernel(const float* __
     if (a >= r) return;
     float v = split_sum(part + (int64_t)(a + 1) * out + o);
     if (dora) {
-        v += 2.0f * s * gn * Pt[(int64_t)a * out + o] + 2.0f * s * s * gn * BG[o * r + a];
+        v += 2.0f * s * gn * Pt[(int64_t)a * out + o];
+        if (BG) v += 2.0f * s * s * gn * BG[o * r + a];   // null: Pt already holds W_eff A^T
         Ax[(int64_t)a * out + o] = (CT)(2.0f * s * B[o * r + a] * gn);
     }
     dB[o * r + a] += v;
@@ -678,9 +689,10 @@ void free_weight(sa3k_weight* w) {
 
 void free_lin(sa3k_lin* L) {
     if (!L) return;
+    if (L->solo) lin_group_free(L->solo);
     for (void* p : {L->Xb, L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
                     (void*)L->d, L->Hc, L->U, L->dU, L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x,
-                    (void*)L->red})
+                    (void*)L->red, L->Wm, L->Wmt})
         if (p) (void)hipFree(p);
     delete L;
 }
@@ -712,11 +724,15 @@ template <class CT>
 void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* bias, float* Y) {
     const sa3k_weight* W = L->W;
     const bool bf = L->prec == SA3K_PREC_BF16;
+    // merged: Hc feeds only the backward's dB reduction, so it is computed beside the main product
+    const bool merged = L->merged && L->rank > 0;
+    const bool side = merged && side_usable(ctx);
     if (bf && x_src == SRC_F32) {   // one pass to bf16 so both GEMMs stream compute-type operands
         const int64_t n = N * W->in;
+        if (side) fork_arm(ctx);   // the conversion records the fork of the rank product
         KernelScope ks(ctx, scope(ctx, L, "lin_fwd_cvt_x"));
-        cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(
-            static_cast<const float*>(X), static_cast<bf16*>(L->Xb), n, 1.0f);
+        launch_k(ctx, true, cvt_kernel<bf16>, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                 static_cast<const float*>(X), static_cast<bf16*>(L->Xb), n, 1.0f);
         SA3K_LAUNCHED();
         X = L->Xb;
         x_src = SRC_BF16;
@@ -729,13 +745,20 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
         h.M = N; h.N = L->rank; h.K = W->in; h.alpha = L->s;
         if (bf) { h.Cb = static_cast<bf16*>(L->Hc); h.ldcb = L->rank; }
         else { h.C = static_cast<float*>(L->Hc); h.ldc = L->rank; }
+        if (side) fork_fire(ctx);   // X is ready
+        OnSide os(ctx, side);
         gemm_run(ctx, h, scope(ctx, L, "lin_fwd_h"));
     }
-    const WOp wo = weight_operand(W, bf, false);
     GemmDesc g;
-    g.prec = L->prec; g.a_src = x_src; g.b_src = wo.src;
-    g.A = X; g.lda = W->in; g.B = wo.p; g.ldb = wo.ld; g.Bs = wo.s; g.ldbs = wo.lds;
-    if (L->rank > 0) { g.A2 = L->Hc; g.lda2 = L->rank; g.B2 = L->Bc; g.ldb2 = L->rank; g.K2 = L->rank; }
+    g.prec = L->prec; g.a_src = x_src;
+    g.A = X; g.lda = W->in;
+    if (merged) {   // Y = d (.) (X W_eff^T) + bias
+        g.b_src = SRC_BF16; g.B = L->Wm; g.ldb = W->in;
+    } else {        // Y = d (.) (X W^T + Hc B^T) + bias: the rank term as the second segment
+        const WOp wo = weight_operand(W, bf, false);
+        g.b_src = wo.src; g.B = wo.p; g.ldb = wo.ld; g.Bs = wo.s; g.ldbs = wo.lds;
+        if (L->rank > 0) { g.A2 = L->Hc; g.lda2 = L->rank; g.B2 = L->Bc; g.ldb2 = L->rank; g.K2 = L->rank; }
+    }
     g.M = N; g.N = W->out; g.K = W->in; g.alpha = 1.0f;
     g.colscale = L->dora ? L->d : nullptr;
     g.bias = bias;
@@ -743,6 +766,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     g.ldu = W->out;
     if (L->dora) { if (bf) g.Ub = static_cast<bf16*>(L->U); else g.U = static_cast<float*>(L->U); }
     gemm_run(ctx, g, scope(ctx, L, "lin_fwd_main"));
+    if (side) side_join_unless_deferred(ctx);
     L->saved_tokens = N;
 }
 
@@ -813,26 +837,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         }
         rp = part; rS = S; rstride = (int64_t)(R + 1) * out;
     }
-    {
-        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_rows"));
-        const dim3 grid((unsigned)ceil_div(out, 64), (unsigned)ceil_div(std::max(r, 1), 4));
-        dora_bwd_rows_kernel<CT><<<grid, kThreads, 0, ctx->stream>>>(
-            rp, rS, rstride, L->nsq, L->mag, L->Pt, L->BG, L->B, out, r, L->s, L->dora, dB, dm, L->gn,
-            static_cast<CT*>(L->Ax));
-        SA3K_LAUNCHED();
-    }
-    // 2. sdUB = s dU B; dora: A2x = 2 s^2 B^T diag(gn) B = s * (Ax . Bt^T) contracts the same Bt
-    //    over out, so it rides on the same GEMM as r extra rows
-    const bool fold_btgb = L->dora && out % (bf ? 64 : 32) == 0;
-    if (L->dora && !fold_btgb) {
-        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_btgb"));
-        btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
-                                                                         static_cast<CT*>(L->A2x));
-        SA3K_LAUNCHED();
-    }
+    // merged: the rows kernel's outputs (Ax) are the last inputs of the dX GEMM, and sdUB with its
+    // column reduction only feeds dA: they go to the second stream as soon as dU and Ax are ready
+    const bool merged = L->merged && sizeof(CT) == 2;
     int64_t x_rows_per = 0;
     int x_S = 0;
-    float* x_part = nullptr;
     int* x_counters = nullptr;
     if constexpr (sizeof(CT) == 2) {
         x_rows_per = tn_rows_per(in, N);
@@ -842,11 +851,32 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         x_S = choose_splits(in, N);
         x_rows_per = ceil_div(N, x_S);
     }
-    // the partials go to the second stream once sdUB is ready: its GEMM records the fork event
     const bool early = x_counters == nullptr;
     const bool side = early && side_usable(ctx);
-    if (side) fork_arm(ctx);
+    if (side && merged) fork_arm(ctx);   // recorded by the rows kernel
     {
+        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_rows"));
+        const dim3 grid((unsigned)ceil_div(out, 64), (unsigned)ceil_div(std::max(r, 1), 4));
+        // merged: Pt holds W_eff A^T = P + s B G, so the B G term is already in it
+        launch_k(ctx, true, dora_bwd_rows_kernel<CT>, grid, dim3(kThreads), 0, rp, rS, rstride,
+                 (const float*)L->nsq, (const float*)L->mag, (const float*)L->Pt,
+                 (const float*)(merged ? nullptr : L->BG), L->B, out, r, L->s, L->dora, dB, dm, L->gn,
+                 static_cast<CT*>(L->Ax));
+        SA3K_LAUNCHED();
+    }
+    // 2. sdUB = s dU B; dora: A2x = 2 s^2 B^T diag(gn) B = s * (Ax . Bt^T) contracts the same Bt
+    //    over out, so it rides on the same GEMM as r extra rows (not needed when merged)
+    const bool fold_btgb = L->dora && !merged && out % (bf ? 64 : 32) == 0;
+    if (L->dora && !merged && !fold_btgb) {
+        KernelScope ks(ctx, scope(ctx, L, "lin_bwd_btgb"));
+        btgb_kernel<CT><<<(unsigned)(r * r), kThreads, 0, ctx->stream>>>(L->B, L->gn, out, r, L->s,
+                                                                         static_cast<CT*>(L->A2x));
+        SA3K_LAUNCHED();
+    }
+    float* x_part = nullptr;
+    // the partials go to the second stream once sdUB is ready: its GEMM records the fork event
+    if (side && !merged) fork_arm(ctx);
+    auto sdub = [&] {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = bf ? SRC_BF16 : SRC_F32;
         g.A = L->dU; g.lda = out; g.B = L->Bt; g.ldb = out;
@@ -859,7 +889,8 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             else g.Cx = static_cast<float*>(L->A2x);
         }
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dub"));
-    }
+    };
+    if (!merged) sdub();
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
     //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
@@ -900,23 +931,30 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         SA3K_LAUNCHED();
     };
     if (early) {
-        if (side) fork_fire(ctx);   // sdUB and X are ready
+        if (side) fork_fire(ctx);   // sdUB (merged: dU) and X are ready
         OnSide os(ctx, side);
+        if (merged) sdub();
         x_partials();
+    } else if (merged) {
+        sdub();
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
     //    of the same GEMM (they share the W^T tiles). Its last kernel records the next fork.
     if (side) fork_arm(ctx);
-    const WOp wt = weight_operand(W, bf, true);
+    // the B operand: W^T (stored layout or working copy) with the rank term as a second segment, or
+    // W_eff^T when merged
+    WOp wt = weight_operand(W, bf, true);
+    if (merged) wt = WOp{SRC_BF16, L->Wmt, nullptr, out, 0};
     if (dX) {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
         g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
-        g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
+        if (!merged) { g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
         if (L->dora) {
-            g.Mx = r; g.Ax = L->Ax; g.ldax = out; g.A2x = L->A2x; g.lda2x = r;
+            g.Mx = r; g.Ax = L->Ax; g.ldax = out;
+            if (!merged) { g.A2x = L->A2x; g.lda2x = r; }
             g.Cx = dA; g.ldcx = in; g.accumulate_x = 1;
         }
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dx"));
@@ -924,7 +962,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
         g.A = L->Ax; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
-        g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r;
+        if (!merged) { g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
         g.M = r; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dA; g.ldc = in; g.accumulate = 1;
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dora_da"));
@@ -948,7 +986,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
 // stage sits in PrepDesc::blk0[stage], so no block is launched for a member that has no work there
 // (a grid sized for the largest member times the member count launches hundreds of thousands of
 // empty blocks).
-enum PrepStage { kStageConvert = 0, kStagePt = 1, kStageGram = 2, kStageTerms = 3, kStages = 4 };
+enum PrepStage { kStageConvert = 0, kStagePt = 1, kStageGram = 2, kStageTerms = 3, kStageMerge = 4, kStages = 5 };
 constexpr int kPtRows = 256;                  // rows of P^T per block (4 waves x 64)
 
 constexpr int kTermRows = 64;                 // DoRA rows per block (8 passes of 8)
@@ -960,6 +998,12 @@ struct PrepDesc {
     float *Pt, *G, *BG, *nsq, *d;
     int in, out;
     int blk0[kStages];                 // first block of this member in each stage's grid
+    // merged mode: the stored base (element type wtype; Q8_0: quants in Wsrc, f16 scales in Wsc)
+    // and the bf16 W_eff = W + s B A in both layouts
+    const void* Wsrc;
+    const void* Wsc;
+    int wtype;
+    bf16 *Wm, *Wmt;
 };
 
 // Ac/At/Bc/Bt from A and B. A block converts one 64-wide tile: columns [64t, 64t + 64) of A
@@ -1173,6 +1217,208 @@ __global__ __launch_bounds__(kThreads) void group_dora_terms_kernel(const PrepDe
     }
 }
 
+
+// ---- merged refresh: W_eff = W + s B A, once per optimizer step
+// One block per 64 output rows of one member walks the member's input dimension in 64-wide chunks:
+//   * the stored base chunk (f32 / f16 / bf16, or Q8_0 quants times their f16 scale: the exact
+//     decoded value) is staged in LDS as f32, the next chunk's raw bytes already in flight;
+//   * delta = B A on v_mfma_f32_16x16x32_bf16 (each wave 16 rows x 64 columns, the rank as K),
+//     W_eff = W + s delta rounded once to bf16 and staged in LDS in both layouts, from which every
+//     thread stores 32 contiguous bytes of a row of W_eff [out][in] and of W_eff^T [in][out];
+//   * dora: nsq = bnsq + sum_i (2 W s delta + (s delta)^2) in double (the expansion of
+//     |W + s B A|^2 - |W|^2, so no cancellation against bnsq), and P = W_eff A^T on MFMA from the
+//     bf16 W_eff rows, which the backward's dB term 2 s gn P and the magnitude d = m / sqrt(nsq)
+//     need. The row sums are reduced in a fixed lane order: deterministic.
+constexpr int kMergeRows = 64;
+constexpr int kMergeEP = 72;   // bf16 row pitch of the staged W_eff chunks (144 bytes: 16-byte aligned rows)
+
+// stored element type of a merge launch: its raw bytes per element and its decode
+template <int TYPE>
+struct MergeType;
+template <>
+struct MergeType<SA3K_TYPE_F32> {
+    static constexpr int kBytes = 4;
+    __device__ static float get(const char* row, int k, float) { return reinterpret_cast<const float*>(row)[k]; }
+};
+template <>
+struct MergeType<SA3K_TYPE_F16> {
+    static constexpr int kBytes = 2;
+    __device__ static float get(const char* row, int k, float) {
+        return (float)__builtin_bit_cast(_Float16, reinterpret_cast<const uint16_t*>(row)[k]);
+    }
+};
+template <>
+struct MergeType<SA3K_TYPE_BF16> {
+    static constexpr int kBytes = 2;
+    __device__ static float get(const char* row, int k, float) {
+        return __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(row)[k] << 16);
+    }
+};
+template <>
+struct MergeType<SA3K_TYPE_Q8_0> {   // quants; the f16 block scale is passed in (exact decode d * q)
+    static constexpr int kBytes = 1;
+    __device__ static float get(const char* row, int k, float sc) { return (float)reinterpret_cast<const int8_t*>(row)[k] * sc; }
+};
+
+// 16-byte global-memory load (address space 1: counted by vmcnt only, unlike a flat access)
+typedef unsigned u32x4g __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4g g_cu4;
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+    const u32x4g v = *(g_cu4*)p;
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
+// Every chunk's operands (the raw base chunk, the 64 rows of A^T and the r x 64 slice of A) are
+// loaded cooperatively one chunk ahead, all before the current chunk's stores: the wait for them at
+// the next chunk then does not include those stores (vmcnt counts loads and stores in issue order).
+template <int TYPE>
+__global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* __restrict__ ds,
+                                                               const int* __restrict__ block_member, int r, float s) {
+    using MT = MergeType<TYPE>;
+    constexpr int RB = 64 * MT::kBytes;                    // raw bytes of one chunk row
+    constexpr int RP = RB + 16;                             // LDS pitch of the raw chunk rows
+    constexpr int NQ = RB * kMergeRows / 16 / kThreads;     // 16-byte raw loads per thread per chunk (1, 2 or 4)
+    constexpr int TPR = RB / 16;                            // threads per raw chunk row
+    constexpr int AP = 80;                                  // LDS pitch of the A^T rows (64 bytes + 16)
+    constexpr int CP = 144;                                 // LDS pitch of the A rows (128 bytes + 16)
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
+    if (q.wtype != TYPE) return;   // a member of another element type (its own launch)
+    __shared__ __attribute__((aligned(16))) char wraw[kMergeRows * RP];
+    __shared__ __attribute__((aligned(16))) char ats[64 * AP];                  // A^T rows of the chunk [i][a]
+    __shared__ __attribute__((aligned(16))) char acs[32 * CP];                  // A rows of the chunk [a][i]
+    __shared__ __attribute__((aligned(16))) float wsc[kMergeRows][2];           // Q8_0 scales of the chunk
+    __shared__ __attribute__((aligned(16))) bf16 et[kMergeRows][kMergeEP];      // W_eff [o][i] of the chunk
+    __shared__ __attribute__((aligned(16))) bf16 ett[kMergeRows][kMergeEP];     // W_eff^T [i][o] of the chunk
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
+    const int64_t in = q.in, out = q.out;
+    const int64_t o0 = (int64_t)(blockIdx.x - q.blk0[kStageMerge]) * kMergeRows;
+    const bool dora = q.mag != nullptr;
+    const bool hi = r > 16;
+    const char* wsrc = static_cast<const char*>(q.Wsrc);
+    // this thread's slice of the A^T rows (row tid / 4, bytes 16 (tid % 4)) and of the A rows
+    // (row tid / 8, bytes 16 (tid % 8)); slices past the rank read a valid address and are zeroed
+    const int at_row = tid >> 2, at_b = 16 * (tid & 3), ac_row = tid >> 3, ac_b = 16 * (tid & 7);
+    const bool at_ok = at_b < 2 * r, ac_ok = ac_row < r;
+    const char* at_src = reinterpret_cast<const char*>(q.At) + (int64_t)at_row * r * 2 + (at_ok ? at_b : 0);
+    const char* ac_src = reinterpret_cast<const char*>(q.Ac) + (int64_t)(ac_ok ? ac_row : 0) * in * 2 + ac_b;
+    struct Stage {
+        uint4 w[NQ], at, ac;
+        uint32_t sc;   // Q8_0: the chunk row's two f16 block scales (threads < 64)
+    } st;
+    auto load = [&](int64_t i0) {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int e = tid + k * kThreads, row = e / TPR;
+            const int64_t o = min(o0 + row, out - 1);   // rows past out are never stored
+            st.w[k] = ldg16(wsrc + (o * in + i0) * MT::kBytes + (e % TPR) * 16);
+        }
+        st.at = ldg16(at_src + i0 * r * 2);
+        st.ac = ldg16(ac_src + i0 * 2);
+        if constexpr (TYPE == SA3K_TYPE_Q8_0) {
+            const int64_t o = min(o0 + (tid & 63), out - 1);
+            st.sc = *(__attribute__((address_space(1))) const uint32_t*)(static_cast<const uint16_t*>(q.Wsc) + o * (in / 32) + i0 / 32);
+        }
+    };
+    // delta's A operand: the rank entries 8g.. of B row o (this wave's 16 rows), loop-invariant
+    const int64_t ob = min(o0 + 16 * wave + l16, out - 1);
+    const bf16x8 zero8 = {};
+    const bf16x8 bop = 8 * g < r ? __builtin_bit_cast(bf16x8, ldg16(q.Bc + ob * r + (8 * g < r ? 8 * g : 0))) : zero8;
+    double nacc[4] = {0.0, 0.0, 0.0, 0.0};   // rows 16 wave + 4g + v, this lane's columns
+    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t wbytes = (uint32_t)(out * in * 2);   // < 2^31 (checked when the group is built)
+    const __amdgpu_buffer_rsrc_t rs_m = __builtin_amdgcn_make_buffer_rsrc(q.Wm, (short)0, (int)wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_mt = __builtin_amdgcn_make_buffer_rsrc(q.Wmt, (short)0, (int)wbytes, 0x00020000);
+    load(0);
+    // the first chunk landed: the loop head's wait then only reflects the loop body's issue order
+    // (a scheduler-reordered prologue would otherwise force a full wait there every chunk)
+    __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0)
+    const int nc = (int)(in / 64);
+    for (int c = 0; c < nc; ++c) {
+        const int64_t i0 = (int64_t)c * 64;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int e = tid + k * kThreads;
+            *reinterpret_cast<uint4*>(wraw + (e / TPR) * RP + (e % TPR) * 16) = st.w[k];
+        }
+        {   // slices past the rank are zeroed arithmetically (no branch: see the stores below)
+            const uint32_t ma = at_ok ? ~0u : 0u, mc = ac_ok ? ~0u : 0u;
+            *reinterpret_cast<uint4*>(ats + at_row * AP + at_b) = uint4{st.at.x & ma, st.at.y & ma, st.at.z & ma, st.at.w & ma};
+            *reinterpret_cast<uint4*>(acs + ac_row * CP + ac_b) = uint4{st.ac.x & mc, st.ac.y & mc, st.ac.z & mc, st.ac.w & mc};
+        }
+        if constexpr (TYPE == SA3K_TYPE_Q8_0) {
+            if (tid < kMergeRows) {
+                wsc[tid][0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(st.sc & 0xffffu));
+                wsc[tid][1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(st.sc >> 16));
+            }
+        }
+        if (c + 1 < nc) load(i0 + 64);   // the next chunk in flight
+        __syncthreads();   // the chunk is staged; the previous chunk's W_eff tiles are consumed
+        // W_eff at (row 16 wave + 4g + v, column 16j + l16)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16x8 atj = *reinterpret_cast<const bf16x8*>(ats + (16 * j + l16) * AP + 16 * g);
+            const f32x4 dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bop, atj, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            bf16 e4[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = 16 * wave + 4 * g + v, col = 16 * j + l16;
+                const float sc = TYPE == SA3K_TYPE_Q8_0 ? wsc[row][col / 32] : 0.f;
+                const float w = MT::get(wraw + row * RP, col, sc);
+                const float sd = s * dl[v];
+                const bf16 e = (bf16)(w + sd);
+                e4[v] = e;
+                et[row][col] = e;
+                if (dora) nacc[v] += (double)sd * (2.0 * (double)w + (double)sd);
+            }
+            *reinterpret_cast<uint2*>(&ett[16 * j + l16][16 * wave + 4 * g]) = __builtin_bit_cast(uint2, e4);
+        }
+        __syncthreads();   // et, ett staged
+        if (dora) {   // P += W_eff A^T over the chunk (rows 16 wave + l16 of W_eff as the A operand)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&et[16 * wave + l16][32 * ks + 8 * g]);
+                const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(acs + l16 * CP + (32 * ks + 8 * g) * 2);
+                p0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, a0, p0, 0, 0, 0);
+                if (hi) {
+                    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(acs + (16 + l16) * CP + (32 * ks + 8 * g) * 2);
+                    p1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, a1, p1, 0, 0, 0);
+                }
+            }
+        }
+        {   // 32 contiguous bytes of a W_eff row and of a W_eff^T row per thread, after every load.
+            // Buffer stores: rows past out get an offset beyond the extent, which the hardware drops,
+            // so no branch makes the wait for the next chunk's loads also wait for these stores.
+            const int lr = tid >> 2, lc = 16 * (tid & 3);
+            const uint4* fr = reinterpret_cast<const uint4*>(&et[lr][lc]);
+            const uint4* tr = reinterpret_cast<const uint4*>(&ett[lr][lc]);
+            const uint32_t fo = o0 + lr < out ? (uint32_t)(((o0 + lr) * in + i0 + lc) * 2) : 0xFFFFFFE0u;
+            const uint32_t to = o0 + lc < out ? (uint32_t)(((i0 + lr) * out + o0 + lc) * 2) : 0xFFFFFFE0u;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, fr[0]), rs_m, fo, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, fr[1]), rs_m, fo + 16, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[0]), rs_mt, to, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[1]), rs_mt, to + 16, 0, 0);
+        }
+    }
+    if (!dora) return;
+    // row sums over the 16 lanes of a group (fixed butterfly order), then nsq, d and P^T
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+        for (int off = 1; off < 16; off <<= 1) nacc[v] += __shfl_xor(nacc[v], off, 16);
+    const int64_t orow = o0 + 16 * wave + 4 * g;
+    if (orow >= out) return;   // out is a multiple of 16: a 4-row group is wholly in or out
+    if (l16 == 0) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float n2 = (float)((double)q.bnsq[orow + v] + nacc[v]);
+            q.nsq[orow + v] = n2;
+            q.d[orow + v] = q.mag[orow + v] / sqrtf(n2);
+        }
+    }
+    if (l16 < r) *reinterpret_cast<float4*>(q.Pt + (int64_t)l16 * out + orow) = make_float4(p0[0], p0[1], p0[2], p0[3]);
+    if (hi && 16 + l16 < r)
+        *reinterpret_cast<float4*>(q.Pt + (int64_t)(16 + l16) * out + orow) = make_float4(p1[0], p1[1], p1[2], p1[3]);
+}
+
 }  // namespace
 
 namespace sa3k {
@@ -1194,7 +1440,7 @@ struct LinGroup {
     PrepDesc* dev = nullptr;
     int* block_member[kStages] = {};   // per stage: the member of every block
     int blocks[kStages] = {};
-    int n = 0, r = 0, dora = 0;
+    int n = 0, r = 0, dora = 0, merged = 0;
     float s = 1.0f;
 };
 
@@ -1215,12 +1461,13 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
         g->r = lins[0]->rank;
         g->dora = dora ? 1 : 0;
         g->s = scale;
+        g->merged = ctx->lin_merge ? 1 : 0;
         std::vector<PrepDesc> h(n);
         std::vector<int> bm[kStages];
         for (int i = 0; i < n; ++i) {
             sa3k_lin* L = lins[i];
-            SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && L->W->wb && L->rank == g->r && g->r > 0,
-                         "a linear group needs bf16 linears of one rank with bf16 working copies");
+            SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && (g->merged || L->W->wb) && L->rank == g->r && g->r > 0,
+                         "a linear group needs bf16 linears of one rank (with bf16 working copies unless merged)");
             SA3K_REQUIRE(A[i] && B[i] && (!dora || (mag[i] && bnsq[i])), "missing adapter pointer");
             const int64_t in = L->W->in, out = L->W->out;
             SA3K_REQUIRE(out % 64 == 0 || out % 16 == 0, "group output dimension must be a multiple of 16");
@@ -1232,9 +1479,19 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
             q.W = static_cast<const bf16*>(L->W->wb);
             q.Pt = L->Pt; q.G = L->G; q.BG = L->BG; q.nsq = L->nsq; q.d = L->d;
             q.in = (int)in; q.out = (int)out;
+            q.Wsrc = L->W->w; q.Wsc = L->W->ws; q.wtype = L->W->type;
+            q.Wm = q.Wmt = nullptr;
+            if (g->merged) {
+                if (!L->Wm) L->Wm = dev_alloc<bf16>(in * out);
+                if (!L->Wmt) L->Wmt = dev_alloc<bf16>(in * out);
+                q.Wm = static_cast<bf16*>(L->Wm);
+                q.Wmt = static_cast<bf16*>(L->Wmt);
+            }
             const int64_t per_stage[kStages] = {ceil_div(in, 64) + ceil_div(out, 64), ceil_div(out, kPtRows),
-                                                ceil_div(in, kGramCols), ceil_div(out, kTermRows)};
+                                                ceil_div(in, kGramCols), ceil_div(out, kTermRows),
+                                                ceil_div(out, kMergeRows)};
             for (int st = 0; st < kStages; ++st) {
+                if (st == kStageMerge) continue;
                 q.blk0[st] = (int)bm[st].size();
                 bm[st].insert(bm[st].end(), (size_t)per_stage[st], i);
             }
@@ -1242,11 +1499,21 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
             g->B.push_back(B[i]);
             g->mag.push_back(dora ? mag[i] : nullptr);
         }
+        {   // merge blocks walk a member's whole input dimension: the longest members go first
+            std::vector<int> order(n);
+            for (int i = 0; i < n; ++i) order[i] = i;
+            std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return h[a].in > h[b].in; });
+            for (int i : order) {
+                h[i].blk0[kStageMerge] = (int)bm[kStageMerge].size();
+                bm[kStageMerge].insert(bm[kStageMerge].end(), (size_t)ceil_div(h[i].out, kMergeRows), i);
+            }
+        }
         SA3K_HIP(hipMalloc(&g->dev, sizeof(PrepDesc) * n));
         SA3K_HIP(hipMemcpyAsync(g->dev, h.data(), sizeof(PrepDesc) * n, hipMemcpyHostToDevice, ctx->stream));
         sa3k_note_main(ctx);
         for (int st = 0; st < kStages; ++st) {
             g->blocks[st] = (int)bm[st].size();
+            if (bm[st].empty()) continue;
             SA3K_HIP(hipMalloc(&g->block_member[st], sizeof(int) * bm[st].size()));
             SA3K_HIP(hipMemcpyAsync(g->block_member[st], bm[st].data(), sizeof(int) * bm[st].size(),
                                     hipMemcpyHostToDevice, ctx->stream));
@@ -1267,12 +1534,31 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
         L->dora = g->dora;
         L->B = g->B[i];
         L->mag = g->mag[i];
+        L->merged = g->merged;
     }
     {
         KernelScope ks(ctx, "group_convert");
         group_convert_kernel<<<(unsigned)g->blocks[kStageConvert], kThreads, 0, ctx->stream>>>(
             g->dev, g->block_member[kStageConvert], g->r);
         SA3K_LAUNCHED();
+    }
+    if (g->merged) {
+        double bytes = 0.0;
+        for (sa3k_lin* L : g->lins) bytes += (double)L->W->in * (double)L->W->out * (type_size(L->W->type) + 4.0);
+        KernelScope ks(ctx, "group_merge", bytes);
+        // one launch per element type present (blocks of other members exit at once)
+        bool has[4] = {false, false, false, false};
+        for (sa3k_lin* L : g->lins) has[L->W->type == SA3K_TYPE_F32 ? 0 : L->W->type == SA3K_TYPE_F16 ? 1 : L->W->type == SA3K_TYPE_BF16 ? 2 : 3] = true;
+        void (*kern[4])(const PrepDesc*, const int*, int, float) = {
+            group_merge_kernel<SA3K_TYPE_F32>, group_merge_kernel<SA3K_TYPE_F16>, group_merge_kernel<SA3K_TYPE_BF16>,
+            group_merge_kernel<SA3K_TYPE_Q8_0>};
+        for (int t = 0; t < 4; ++t) {
+            if (!has[t]) continue;
+            kern[t]<<<(unsigned)g->blocks[kStageMerge], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStageMerge],
+                                                                                 g->r, g->s);
+            SA3K_LAUNCHED();
+        }
+        return;
     }
     if (!g->dora) return;
     {
@@ -1473,6 +1759,25 @@ SA3K_API int sa3k_lin_prepare(sa3k_ctx* ctx, sa3k_lin* L, const float* A, const 
         SA3K_REQUIRE(A && B, "adapter A/B are null");
         SA3K_REQUIRE(!dora || (magnitude && base_norm_sq), "dora needs magnitude and base_norm_sq");
         const bool bf = L->prec == SA3K_PREC_BF16;
+        L->merged = 0;
+        if (bf && ctx->lin_merge && out % 16 == 0) {
+            // the merged refresh through a one-member group, rebuilt when the adapter changes
+            const float* key[4] = {A, B, dora ? magnitude : nullptr, dora ? base_norm_sq : nullptr};
+            if (!L->solo || !std::equal(key, key + 4, L->solo_key) || L->solo_s != scale || L->solo_dora != dora) {
+                if (L->solo) {
+                    SA3K_HIP(hipStreamSynchronize(ctx->stream));
+                    lin_group_free(L->solo);
+                    L->solo = nullptr;
+                }
+                sa3k_lin* one = L;
+                L->solo = lin_group_create(ctx, &one, 1, &key[0], &key[1], &key[2], &key[3], scale, dora);
+                std::copy(key, key + 4, L->solo_key);
+                L->solo_s = scale;
+                L->solo_dora = dora;
+            }
+            lin_group_prepare(ctx, L->solo);
+            return;
+        }
         KernelScope ks(ctx, "lin_prepare");
         auto cvt = [&](const float* src, void* dst, int64_t n) {
             if (bf) cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(src, static_cast<bf16*>(dst), n, 1.0f);

@@ -225,6 +225,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "side_stream") ctx->use_side = value != 0;
         else if (n == "fork_tail") ctx->fork_tail = value != 0;
         else if (n == "late_join") ctx->late_join = value != 0;
+        else if (n == "lin_merge") ctx->lin_merge = value != 0;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

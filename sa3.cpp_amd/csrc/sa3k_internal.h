@@ -45,12 +45,14 @@ struct sa3k_ctx {
     int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
     int fork_tail = 1;                     // forks recorded by the producer kernel's completion (fork_arm)
     int late_join = 1;                     // a DiT block's last second-stream work may overlap the next block
+    int lin_merge = 1;                     // bf16 adapted linears contract W + s B A, refreshed per prepare
     hipEvent_t block_tail_ev = nullptr;    // second-stream work of a block backward left running (late_join)
     bool block_tail_pending = false;       // block_tail_ev holds a record not yet waited for
     hipEvent_t tail_ev = nullptr;          // fork event armed for the producer about to launch (fork_arm)
     uint64_t tail_seq = 0;                 // main_seq right after the launch that last recorded tail_ev
     uint64_t main_seq = 0;                 // operations enqueued on the main stream (note_main)
     uint64_t side_synced = ~(uint64_t)0;   // main_seq up to which the second stream already waits
+    uint64_t side_forks = 0;               // forks so far (each precedes work enqueued on the second stream)
     std::string last_error;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     bool prof_on = false;
@@ -192,6 +194,7 @@ inline hipEvent_t side_event(sa3k_ctx* c) {
 inline void fork_fire(sa3k_ctx* c);
 inline void side_fork(sa3k_ctx* c) {
     if (c->tail_ev) return fork_fire(c);   // armed before the producer
+    ++c->side_forks;
     if (c->side_synced == c->main_seq) return;
     hipEvent_t e = side_event(c);
     SA3K_HIP(hipEventRecord(e, c->main_stream));
@@ -226,6 +229,7 @@ inline void fork_arm(sa3k_ctx* c) {
 }
 inline void fork_fire(sa3k_ctx* c) {
     if (!c->tail_ev) return side_fork(c);   // not armed (fork_tail off)
+    ++c->side_forks;
     hipEvent_t e = c->tail_ev;
     c->tail_ev = nullptr;
     if (c->tail_seq != c->main_seq) SA3K_HIP(hipEventRecord(e, c->main_stream));
@@ -237,6 +241,10 @@ inline void side_join(sa3k_ctx* c) {
     hipEvent_t e = side_event(c);
     SA3K_HIP(hipEventRecord(e, c->side_stream));
     SA3K_HIP(hipStreamWaitEvent(c->main_stream, e, 0));
+}
+// the main stream waits for the second stream if anything was forked since side_forks was `mark`
+inline void side_join_since(sa3k_ctx* c, uint64_t mark) {
+    if (c->side_forks != mark) side_join(c);
 }
 // A caller that joins the second stream itself at its end (see SideDeferScope) lets the functions
 // it calls leave their side work running; otherwise every forking function joins before returning.

@@ -3,7 +3,8 @@ src/train_loop.h:173-441) on the GPU vs the whole-DiT oracle (oracle/dit.cpp, pi
 torch float64 autograd in tests/test_oracle_dit.py).
 
 * depth-2 model, full scope (12 head/tail targets + blocks, DoRA, dense attention) and core scope
-  (blocks only, LoRA, banded attention, per-frame loss weights), f32 and f16 bases: per-sample
+  (blocks only, LoRA, banded attention, per-frame loss weights), f32 and f16 bases, adapted
+  products over the merged weight W + s B A and with the rank term as a second segment: per-sample
   losses, the velocity and every adapter gradient to the bf16 bar (normwise relative error
   <= 2e-2 and cosine >= 0.9999; the loss to 1e-3);
 * the arena layout is the reference's: targets in sorted weight-name order, [A | B | m] each;
@@ -73,14 +74,18 @@ def check(got, ref, what):
     assert e <= 2e-2 and c >= 0.9999, f"{what}: rel {e:.3e} cos {c:.6f}"
 
 
-CASES = {"full_dora_dense_f32": (41, "full", True, 0, False, sa3k.TYPE_F32),
-         "full_dora_dense_f16": (41, "full", True, 0, False, sa3k.TYPE_F16),
-         "core_lora_band_weighted_f16": (42, "core", False, 6, True, sa3k.TYPE_F16)}
+CASES = {"full_dora_dense_f32": (41, "full", True, 0, False, sa3k.TYPE_F32, 1),
+         "full_dora_dense_f16": (41, "full", True, 0, False, sa3k.TYPE_F16, 1),
+         "full_dora_dense_f16_segments": (41, "full", True, 0, False, sa3k.TYPE_F16, 0),
+         "core_lora_band_weighted_f16": (42, "core", False, 6, True, sa3k.TYPE_F16, 1),
+         "core_lora_band_weighted_f16_segments": (42, "core", False, 6, True, sa3k.TYPE_F16, 0)}
 
 
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_dit_step_vs_oracle(ctx, name):
-    seed, scope, dora, window, weighted, wtype = CASES[name]
+    # lin_merge 1 (default): the adapted products contract W + s B A; 0: the rank term as a second
+    # segment of each product
+    seed, scope, dora, window, weighted, wtype, merge = CASES[name]
     cfg = dict(CFG, dora=dora, window=window)
     tensors, adapters, inputs = db.random_dit(seed, cfg, scope)
     if wtype == sa3k.TYPE_F16:   # the oracle sees the f16 values the GPU decodes
@@ -90,7 +95,11 @@ def test_dit_step_vs_oracle(ctx, name):
     if weighted:
         lw = np.random.Generator(np.random.Philox(seed + 7)).uniform(
             0, 2.0 / (cfg["io"] * cfg["T"]), (cfg["B"], cfg["T"])).astype(np.float32)
-    d = make_gpu(ctx, cfg, tensors, adapters, scope, wtype)
+    ctx.set_option("lin_merge", merge)
+    try:
+        d = make_gpu(ctx, cfg, tensors, adapters, scope, wtype)
+    finally:
+        ctx.set_option("lin_merge", 1)
     try:
         assert [t[0] for t in d.targets()] == db.target_names(cfg, scope)
         up, lw_d = upload_inputs(ctx, inputs, lw)

@@ -6,7 +6,10 @@ Configurations:
     element by element with a floor of a tenth of the output's RMS (conftest.elem_rel_err);
   * DoRA linear 1536 -> 6144 over a Q8_0 base, rank 32: bf16 MFMA, outputs within 2e-2 normwise
     relative error and cosine >= 0.9999 of the oracle run on the exactly decoded Q8_0 weight;
-  * smaller and ragged shapes, f16 and f32 bases, lora and dora, both precisions.
+  * smaller and ragged shapes, f16 and f32 bases, lora and dora, both precisions;
+  * bf16 linears both merged (the products contract W + s B A, rounded once to bf16 by the
+    refresh) and with the rank term as the second segment of each product (option lin_merge 0),
+    and with the frozen base decoded on its way into LDS (no working copy, unmerged).
 The oracle is the double-precision restatement in oracle/dit_lin.cpp (pinned in
 tests/test_oracle_dit_lin.py).
 """
@@ -29,18 +32,23 @@ def make_inputs(seed, N, in_, out_, r, w_sd=0.02, b_sd=0.01):
     return X, dY, W, A, B
 
 
-def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1, decode_in_gemm=False):
+def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1, decode_in_gemm=False, merge=True):
     N, in_ = X.shape
     out_ = dY.shape[1]
     r = A.shape[0]
     w = ctx.weight(Wop, wtype)
     if decode_in_gemm:
+        assert not merge, "the merged products read the refreshed W + s B A, not the stored base"
         w.drop_working_copy()
     lin = ctx.lin(w, r, prec, N)
     dA_, dB_ = ctx.upload(A), ctx.upload(B)
     dmag = ctx.upload(mag) if dora else None
     bnsq = w.row_norm_sq(1e-12) if dora else None
-    lin.prepare(dA_, dB_, s, dora, dmag, bnsq)
+    ctx.set_option("lin_merge", 1 if merge else 0)
+    try:
+        lin.prepare(dA_, dB_, s, dora, dmag, bnsq)
+    finally:
+        ctx.set_option("lin_merge", 1)
     dX_, dY_ = ctx.upload(X), ctx.upload(dY)
     Y = ctx.empty((N, out_))
     gX, gA, gB, gm = ctx.empty((N, in_)), ctx.zeros((r, in_)), ctx.zeros((out_, r)), ctx.zeros(out_)
@@ -75,8 +83,9 @@ def test_lora_f32_linear(ctx, N):
         assert e < 1e-4, (k, e)
 
 
-@pytest.mark.parametrize("N,decode", [(256, False), (2048, False), (2048, True)])
-def test_dora_q8_0_linear(ctx, N, decode):
+@pytest.mark.parametrize("N,decode,merge", [(256, False, True), (2048, False, True), (2048, False, False),
+                                            (2048, True, False)])
+def test_dora_q8_0_linear(ctx, N, decode, merge):
     # DoRA linear 1536 -> 6144, Q8_0 base quantised from N(0, 0.02), rank 32, alpha 32, m = row norms
     in_, out_, r = 1536, 6144, 32
     X, dY, W, A, B = make_inputs(1, N, in_, out_, r)
@@ -84,7 +93,7 @@ def test_dora_q8_0_linear(ctx, N, decode):
     _, _, Wdec = q8_0_split(blocks, out_, in_)
     mag = oracle.row_norms(Wdec)
     got = run_gpu(ctx, X, dY, (blocks, in_, out_), sa3k.TYPE_Q8_0, A, B, 1.0, True, mag, sa3k.PREC_BF16,
-                  decode_in_gemm=decode)
+                  decode_in_gemm=decode, merge=merge)
     ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
     np.testing.assert_allclose(got["bnsq"], ref["bnsq"], rtol=1e-6)
     for k in ("Y", "dX", "dA", "dB", "dm"):
@@ -92,11 +101,12 @@ def test_dora_q8_0_linear(ctx, N, decode):
         assert cosine(got[k], ref[k]) >= 0.9999, k
 
 
-@pytest.mark.parametrize("prec", [sa3k.PREC_F32, sa3k.PREC_BF16])
+@pytest.mark.parametrize("prec,mode", [(sa3k.PREC_F32, "stored"), (sa3k.PREC_F32, "decode"),
+                                       (sa3k.PREC_BF16, "merged"), (sa3k.PREC_BF16, "stored"),
+                                       (sa3k.PREC_BF16, "decode")])
 @pytest.mark.parametrize("wt", ["f32", "f16"])
 @pytest.mark.parametrize("dora", [False, True])
-@pytest.mark.parametrize("decode", [False, True])
-def test_linear_small_shapes(ctx, prec, wt, dora, decode):
+def test_linear_small_shapes(ctx, prec, mode, wt, dora):
     # ragged token count, non-square, bias on the output
     N, in_, out_, r = 77, 192, 320, 8
     X, dY, W, A, B = make_inputs(2, N, in_, out_, r, w_sd=0.1, b_sd=0.05)
@@ -107,7 +117,8 @@ def test_linear_small_shapes(ctx, prec, wt, dora, decode):
         Wop, wtype, Wdec = W, sa3k.TYPE_F32, W
     mag = (oracle.row_norms(Wdec) * 1.1 + 0.05).astype(np.float32)
     bias = rng(3).normal(0, 1, out_).astype(np.float32)
-    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 2.0, dora, mag, prec, bias=bias, decode_in_gemm=decode)
+    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 2.0, dora, mag, prec, bias=bias, decode_in_gemm=mode == "decode",
+                  merge=mode == "merged")
     ref = run_oracle(X, dY, Wdec, A, B, 2.0, dora, mag, bias)
     keys = ("Y", "dX", "dA", "dB") + (("dm",) if dora else ())
     for k in keys:
@@ -118,18 +129,19 @@ def test_linear_small_shapes(ctx, prec, wt, dora, decode):
 
 
 @pytest.mark.parametrize("N,in_,out_,r", [(2048, 1536, 6144, 32), (264, 192, 320, 8)])
-def test_dora_linear_big_tiles(ctx, N, in_, out_, r):
+@pytest.mark.parametrize("merge", [True, False])
+def test_dora_linear_big_tiles(ctx, N, in_, out_, r, merge):
     # bf16 DoRA linear with every eligible GEMM on 256 x 256 tiles (gemm_big = 2): the rank segment
-    # (K2 = r) and the r extra dA rows of the dX GEMM go through the big kernel's descriptors
+    # (K2 = r, unmerged) and the r extra dA rows of the dX GEMM go through the big kernel's descriptors
     X, dY, W, A, B = make_inputs(4, N, in_, out_, r)
     Wh = W.astype(np.float16)
     Wdec = Wh.astype(np.float32)
     mag = (oracle.row_norms(Wdec) * 1.05).astype(np.float32)
     try:
         ctx.set_option("gemm_big", 2)
-        got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16)
+        got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16, merge=merge)
         ctx.set_option("gemm_big", 0)
-        small = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16)
+        small = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16, merge=merge)
     finally:
         ctx.set_option("gemm_big", 1)
     ref = run_oracle(X, dY, Wdec, A, B, 1.5, True, mag)
@@ -171,3 +183,34 @@ def test_lin_rejects_bad_calls(ctx):
         lin.forward(X, 32, ctx.empty((32, 64)))     # more tokens than max_tokens
     lin.destroy()
     w.destroy()
+
+
+@pytest.mark.parametrize("wt", ["f32", "f16", "bf16", "q8_0"])
+@pytest.mark.parametrize("r", [8, 24, 32])
+def test_merged_refresh_terms(ctx, wt, r):
+    """The merged refresh against the oracle's definitions: d = m / sqrt(|W + s B A|^2 + in eps) per
+    row, and the products it feeds. Ragged rank counts (8, 24) exercise the zero-padded MFMA operands;
+    every stored element type goes through its own decode (Q8_0: the exact d * q)."""
+    N, in_, out_ = 96, 256, 192
+    X, dY, W, A, B = make_inputs(11, N, in_, out_, r, w_sd=0.05, b_sd=0.05)
+    if wt == "f16":
+        Wop, wtype = W.astype(np.float16), sa3k.TYPE_F16
+        Wdec = Wop.astype(np.float32)
+    elif wt == "bf16":
+        bits = (W.view(np.uint32) >> 16).astype(np.uint16)    # truncated to bf16: exact values
+        Wdec = (bits.astype(np.uint32) << 16).view(np.float32)
+        Wop, wtype = bits, sa3k.TYPE_BF16
+    elif wt == "q8_0":
+        blocks = oracle.q8_0_quantize(W)
+        _, _, Wdec = q8_0_split(blocks, out_, in_)
+        Wop, wtype = (blocks, in_, out_), sa3k.TYPE_Q8_0
+    else:
+        Wop, wtype, Wdec = W, sa3k.TYPE_F32, W
+    mag = (oracle.row_norms(Wdec) * 0.9 + 0.01).astype(np.float32)
+    got = run_gpu(ctx, X, dY, Wop, wtype, A, B, 0.75, True, mag, sa3k.PREC_BF16, merge=True)
+    seg = run_gpu(ctx, X, dY, Wop, wtype, A, B, 0.75, True, mag, sa3k.PREC_BF16, merge=False)
+    ref = run_oracle(X, dY, Wdec, A, B, 0.75, True, mag)
+    for k in ("Y", "dX", "dA", "dB", "dm"):
+        assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
+        # the two formulations differ only by bf16 roundings of the operands
+        assert rel_err(got[k], seg[k]) < 1e-2, k
