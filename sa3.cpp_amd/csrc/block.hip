@@ -64,6 +64,16 @@ __global__ void modv_kernel(const float* __restrict__ ssg, const float* __restri
 typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
 
 __device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// An adapted linear's dU = bf16(scale (.) dY) for four consecutive output columns c..c+3 (scale
+// null: 1), written by the kernel that produces dY instead of dY itself (lin_du / lin_backward_du)
+__device__ inline void st_du4(bf16* p, float4 v, const float* scale, int64_t c) {
+    if (scale) {
+        const float4 s = ld4(scale + c);
+        v = make_float4(v.x * s.x, v.y * s.y, v.z * s.z, v.w * s.w);
+    }
+    const bf16 b[4] = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
+    *reinterpret_cast<uint2*>(p) = __builtin_bit_cast(uint2, b);
+}
 __device__ inline void st4(float* p, const float4& v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ inline void st4(bf16* p, const float4& v) {
     const bf16x4 b = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
@@ -148,7 +158,9 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
                                                             const float* __restrict__ modv, int sc_part, int S, int dim,
                                                             int rows, const float* __restrict__ dres,
                                                             float* __restrict__ dx, int g_part,
-                                                            float* __restrict__ dgated) {
+                                                            float* __restrict__ dgated, bf16* __restrict__ du_x,
+                                                            const float* __restrict__ dsc_x,
+                                                            bf16* __restrict__ du_g, const float* __restrict__ dsc_g) {
     const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -184,9 +196,12 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
         const float4 t = map4(dg[k], xv[k], [r, k3](float d, float xx) { return r * d - k3 * xx; });
         const float4 o = map4(ld4(dres + base + c), t, [](float a, float b) { return a + b; });
         st4(dx + base + c, o);
-        if (g_part >= 0)
-            st4(dgated + base + c, map4(o, ld4(mv + g_part * dim + c),
-                                        [](float d, float g) { return d * sigmoidf_(1.0f - g); }));
+        if (du_x) st_du4(du_x + base + c, o, dsc_x, c);
+        if (g_part >= 0) {
+            const float4 gd = map4(o, ld4(mv + g_part * dim + c), [](float d, float g) { return d * sigmoidf_(1.0f - g); });
+            if (du_g) st_du4(du_g + base + c, gd, dsc_g, c);
+            else st4(dgated + base + c, gd);
+        }
     }
 }
 
@@ -295,14 +310,16 @@ __global__ void gate_res_kernel(const float* __restrict__ x, const float* __rest
                              xv.z + yv.z * sigmoidf_(1.0f - g.z), xv.w + yv.w * sigmoidf_(1.0f - g.w)));
 }
 
-// dy = dout * sigmoid(1 - g_b); n4 = rows * dim / 4 (< 2^31)
+// dy = dout * sigmoid(1 - g_b) (du: written as the consuming linear's dU); n4 = rows * dim / 4 (< 2^31)
 __global__ void gate_bwd_kernel(const float* __restrict__ dout, const float* __restrict__ modv, int g_part, int S, int dim,
-                                int n4, float* __restrict__ dy) {
+                                int n4, float* __restrict__ dy, bf16* __restrict__ du, const float* __restrict__ dsc) {
     const int i4 = blockIdx.x * kThreads + threadIdx.x;
     if (i4 >= n4) return;
     const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)dim, c = e - row * (unsigned)dim;
     const float4 g = ld4(modv + ((int64_t)(row / (unsigned)S) * 6 + g_part) * dim + c);
-    st4(dy + e, map4(ld4(dout + e), g, [](float d, float gg) { return d * sigmoidf_(1.0f - gg); }));
+    const float4 v = map4(ld4(dout + e), g, [](float d, float gg) { return d * sigmoidf_(1.0f - gg); });
+    if (du) st_du4(du + e, v, dsc, c);
+    else st4(dy + e, v);
 }
 
 // g[n][c] = F[n][c] * silu(F[n][I + c]); n4 = rows * I / 4 (< 2^31)
@@ -314,8 +331,9 @@ __global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int n4, bf
     st4(g + e, map4(ld4(f), ld4(f + I), [](float val, float glu) { return val * glu * sigmoidf_(glu); }));
 }
 
+// dF (du: written as the FFN up-projection's dU, scale over its 2I columns)
 __global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __restrict__ F, int I, int n4,
-                                  float* __restrict__ dF) {
+                                  float* __restrict__ dF, bf16* __restrict__ du, const float* __restrict__ dsc) {
     const int i4 = blockIdx.x * kThreads + threadIdx.x;
     if (i4 >= n4) return;
     const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
@@ -329,8 +347,13 @@ __global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __r
         dv[u] = ds[u] * gs[u] * sg;
         dgl[u] = ds[u] * vs[u] * (sg + gs[u] * sg * (1.0f - sg));
     }
-    st4(dF + o, make_float4(dv[0], dv[1], dv[2], dv[3]));
-    st4(dF + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]));
+    if (du) {
+        st_du4(du + o, make_float4(dv[0], dv[1], dv[2], dv[3]), dsc, c);
+        st_du4(du + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]), dsc, (int64_t)I + c);
+    } else {
+        st4(dF + o, make_float4(dv[0], dv[1], dv[2], dv[3]));
+        st4(dF + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]));
+    }
 }
 
 // ---------------------------------------------------------------- q/k-norm + RoPE prep
@@ -426,6 +449,8 @@ struct PrepBwdArgs {
     PrepBwdPart p[5];
     const float* rstd;
     float* din;           // [B*Sx][parts*dim]
+    bf16* du;             // instead of din: the input projection's dU [B*Sx][parts*dim]
+    const float* dsc;     // its column scale (null: 1)
 };
 
 __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int items) {
@@ -456,7 +481,8 @@ __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int i
             const float4 gg = map4(gv, gm, [r](float u, float w) { return r * u * w; });
             gv = map4(gg, x[k], [c3](float u, float xx) { return u - c3 * xx; });
         }
-        st4(a.din + xo + (int64_t)k * a.dim, gv);
+        if (a.du) st_du4(a.du + xo + (int64_t)k * a.dim, gv, a.dsc, (int64_t)k * a.dim + h * HD + d0);
+        else st4(a.din + xo + (int64_t)k * a.dim, gv);
     }
 }
 
@@ -796,62 +822,68 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         SideDeferScope defer(ctx);
         const int64_t nq = (int64_t)B * H * S;
         // dx = dres + norm backward (dh); dgated = dx * sigmoid(1 - g) when g_part >= 0
+        // lx / lg: the linear whose dU is dxo / the gated branch's gradient (written as that dU)
         auto norm_bwd = [&](const float* dh, const float* xin, const float* rs, const float* gamma, int sc_part,
-                            const float* dres, float* dxo, int g_part, float* dgated) {
+                            const float* dres, float* dxo, int g_part, sa3k_lin* lx, sa3k_lin* lg) {
             with_row_v(D, [&](auto v) {
                 launch(ctx, "blk_norm_bwd", norm_bwd_kernel<decltype(v)::value>, dim3(nwave_blk(N)), dh, xin, rs, gamma,
-                       mv, sc_part, S, D, (int)N, dres, dxo, g_part, dgated);
+                       mv, sc_part, S, D, (int)N, dres, dxo, g_part, (float*)nullptr, lx ? lin_du(lx) : nullptr,
+                       lx ? lin_du_scale(lx) : nullptr, lg ? lin_du(lg) : nullptr, lg ? lin_du_scale(lg) : nullptr);
             });
         };
         // out = x2 + yf * s_f (its kernel records the fork of the column reduction that follows)
         if (side_usable(ctx)) fork_arm(ctx);
-        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D / 4)), dout, mv, 5, S, D, (int)(N * D / 4), w->dyf);
+        // Each adapted linear's output gradient is written by its producer as the linear's bf16 dU
+        // (lin_du), which its backward reads (lin_backward_du): no f32 dY round trip.
+        launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D / 4)), dout, mv, 5, S, D, (int)(N * D / 4),
+               (float*)nullptr, lin_du(b->L[6]), lin_du_scale(b->L[6]));
         colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
-        chk(ctx, sa3k_lin_backward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dyf, w->dg, 0, dA[6], dB[6], dmt[6]));
+        lin_backward_du(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dg, 0, dA[6], dB[6], dmt[6]);
         launch(ctx, "blk_swiglu", swiglu_bwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->dg, (const float*)w->F, I,
-               (int)(N * I / 4), w->dF);
-        chk(ctx, sa3k_lin_backward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dF, w->dfin, 0, dA[5], dB[5], dmt[5]));
+               (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
+        lin_backward_du(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dfin, 0, dA[5], dB[5], dmt[5]);
         colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
-        norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, nullptr);
+        norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, b->L[4], nullptr);
         // x2 = x1 + yc
-        chk(ctx, sa3k_lin_backward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->dx2, w->doc, 0, dA[4], dB[4], dmt[4]));
+        lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4]);
         attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
         PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, nullptr,
-                       {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, w->dqf};
+                       {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, nullptr,
+                       lin_du(b->L[2]), lin_du_scale(b->L[2])};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bq, (int)(N * H));
         PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
-                       {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, w->dkv};
+                       {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, nullptr,
+                       lin_du(b->L[3]), lin_du_scale(b->L[3])};
         if (side_usable(ctx)) fork_arm(ctx);   // recorded by the next kernel, for the K/V projection
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(NC * H)), bk, (int)(NC * H));
         {   // the context K/V projection (Ctx tokens, small kernels) beside the query projection
             const bool side = side_usable(ctx);
             if (side) side_fork(ctx);
             OnSide os(ctx, side);
-            chk(ctx, sa3k_lin_backward(ctx, b->L[3], SA3K_TYPE_F32, w->ctxf, NC, w->dkv, dcontext, 1, dA[3], dB[3],
-                                       dmt[3]));
+            lin_backward_du(ctx, b->L[3], SA3K_TYPE_F32, w->ctxf, NC, dcontext, 1, dA[3], dB[3], dmt[3]);
         }
-        chk(ctx, sa3k_lin_backward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dqf, w->dhc, 0, dA[2], dB[2], dmt[2]));
+        lin_backward_du(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, w->dhc, 0, dA[2], dB[2], dmt[2]);
         // x1 = x + y * s_a: dy = dx1 * s_a comes out of the same pass (which records the fork of
         // the column reduction that follows)
         if (side_usable(ctx)) fork_arm(ctx);
-        norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, w->dy);
+        norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, nullptr, b->L[1]);
         colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
-        chk(ctx, sa3k_lin_backward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dy, w->dob, 0, dA[1], dB[1], dmt[1]));
+        lin_backward_du(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dob, 0, dA[1], dB[1], dmt[1]);
         attn_backward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, w->o1, w->o2, w->l1, w->l2, w->dob, B, H, S, S, c.window,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
         PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, w->rope_tab,
                        {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
-                       w->rq, w->dqkv};
+                       w->rq, nullptr, lin_du(b->L[0]), lin_du_scale(b->L[0])};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bs, (int)(N * H));
         // the previous block's last second-stream work (late_join) reads w->dh, written next
         if (ctx->block_tail_pending) {
             SA3K_HIP(hipStreamWaitEvent(ctx->main_stream, ctx->block_tail_ev, 0));
             ctx->block_tail_pending = false;
         }
-        chk(ctx, sa3k_lin_backward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, w->dqkv, w->dh, 0, dA[0], dB[0], dmt[0]));
+        lin_backward_du(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, w->dh, 0, dA[0], dB[0], dmt[0]);
         colred(ctx, w, 0, w->dh, w->x, w->rs_a, b->pre_g, 0, 0);
-        norm_bwd(w->dh, w->x, w->rs_a, b->pre_g, 0, w->dx1, dx, -1, nullptr);
+        norm_bwd(w->dh, w->x, w->rs_a, b->pre_g, 0, w->dx1, dx, -1, nullptr, nullptr);
         if (side_usable(ctx)) {
             if (late_join) {   // the column reduction and dA sums of this block finish beside the next block
                 SA3K_HIP(hipEventRecord(ctx->block_tail_ev, ctx->side_stream));

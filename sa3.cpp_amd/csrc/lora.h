@@ -36,6 +36,14 @@ void lin_group_free(LinGroup* g);
 // A short role name ("qkv", "ff.out", ...) appended to the linear's profiler scope names, so a
 // per-kernel profile separates the projections (no effect while profiling is off).
 void lin_set_tag(sa3k_lin* l, const char* tag);
+// The output-gradient hand-off of a bf16-precision linear: a kernel producing the gradient dY of
+// the linear's output may write dU = bf16(scale (.) dY) into lin_du(L) ([tokens][out]), with scale
+// = lin_du_scale(L) per output column (the DoRA row scale d; null: 1), and then call
+// lin_backward_du, which is sa3k_lin_backward on that dU (the f32 dY is never materialised).
+bf16* lin_du(sa3k_lin* L);
+const float* lin_du_scale(const sa3k_lin* L);
+void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, float* dX, int dx_accumulate,
+                     float* dA, float* dB, float* dm);
 // The B operand of X W^T (forward orientation) in g's precision: the bf16 working copy when the
 // weight has one and the precision is bf16, else the stored elements or Q8_0 planes, which the
 // GEMM decodes on their way into LDS.

@@ -319,6 +319,8 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
 //   TN_DY: Q = dU = dY * d (written out as bf16), part[z][0][c] = sum_n dY*U, part[z][1+a][c] =
 //          sum_n Hc[n][a] dU[n][c]                                   (dU^T Hc, stride 33 rows)
 //   TN_X:  part[z][a][c] = sum_n G[n][a] X[n][c]                      ((s dU B)^T X, stride 32 rows)
+//   TN_DU: as TN_DY with Q = dU already written by the producer of dY: part[z][0][c] =
+//          (sum_n dU*U) / d[c], part[z][1+a][c] = sum_n Hc[n][a] dU[n][c]
 // over the token rows of split z. A workgroup owns 64 columns; per 32-token step the Q tile (dU or
 // X, 32 tokens x 64 columns) and the P tile (Hc or G, 32 tokens x rank padded to 32) are stored
 // row-major in LDS with 16- / 8-byte writes and read back with ds_read_b64_tr_b16, which hands
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
 // wave owns 16 columns x 32 ranks (two v_mfma_f32_16x16x32_bf16 per step). Two LDS buffers and
 // the next step's global loads issued before the current step's LDS traffic keep the stream of
 // Q in flight; the kernel is bound by streaming Q once.
-constexpr int TN_DY = 0, TN_X = 1;
+constexpr int TN_DY = 0, TN_X = 1, TN_DU = 2;
 constexpr int TN_COLS = 64, TN_ROWS = 32;
 constexpr int TN_H = 2;                    // 32-token halves per step (each thread loads TN_H token rows)
 constexpr int TN_STEP = TN_ROWS * TN_H;    // tokens per step (one barrier per step)
@@ -379,7 +381,8 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     // one step's global operands of this thread, loaded ahead of use
     struct Regs {
         float4 ya[TN_H], yb[TN_H];   // dY (DY) or f32 X
-        bf16x8 u[TN_H];              // U (DY) or bf16 X
+        bf16x8 u[TN_H];              // U (DY, DU) or bf16 X
+        bf16x8 q[TN_H];              // dU (DU)
         uint2 pv[TN_H];              // 4 bf16 of P
     };
     // Loads through buffer descriptors whose extents end at this split's last token row: rows past
@@ -390,9 +393,10 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     constexpr uint32_t kOut = 0xFFFFFFF0u;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<QT*>(Q), (short)0, (int)(r1 * cols * (int64_t)sizeof(QT)), 0x00020000);
+    constexpr bool kGd = MODE == TN_DY || MODE == TN_DU;   // the magnitude column sums gd
     const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16*>(MODE == TN_DY && U ? U : static_cast<const bf16*>(nullptr)), (short)0,
-        (MODE == TN_DY && U) ? (int)(r1 * cols * 2) : 0, 0x00020000);
+        const_cast<bf16*>(kGd && U ? U : static_cast<const bf16*>(nullptr)), (short)0,
+        (kGd && U) ? (int)(r1 * cols * 2) : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(P), (short)0,
                                                                         (int)(r1 * r * 2), 0x00020000);
     auto load = [&](int64_t n0, Regs& R) {
@@ -407,6 +411,9 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
                 R.yb[h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16u, 0, 0));
             }
             if constexpr (MODE == TN_DY) {
+                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? e * 2u : kOut, 0, 0));
+            } else if constexpr (MODE == TN_DU) {
+                R.q[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, col_ok ? e * 2u : kOut, 0, 0));
                 R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? e * 2u : kOut, 0, 0));
             } else if constexpr (sizeof(QT) == 2) {
                 R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, col_ok ? e * 2u : kOut, 0, 0));
@@ -430,6 +437,12 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
                     if (U) gd[j] += y[j] * (float)R.u[h][j];
                 }
                 if (n < r1 && col_ok) *reinterpret_cast<bf16x8*>(dU + n * cols + col) = qv;
+            } else if constexpr (MODE == TN_DU) {
+                qv = R.q[h];
+                if (U) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) gd[j] += (float)qv[j] * (float)R.u[h][j];
+                }
             } else if constexpr (sizeof(QT) == 4) {
                 const float y[8] = {R.ya[h].x, R.ya[h].y, R.ya[h].z, R.ya[h].w,
                                     R.yb[h].x, R.yb[h].y, R.yb[h].z, R.yb[h].w};
@@ -478,8 +491,8 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
         load(n0 + 3 * TN_STEP, rb);
     }
     // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + lane%16
-    constexpr int RS = MODE == TN_DY ? 33 : 32;
-    const int row0 = MODE == TN_DY ? 1 : 0;
+    constexpr int RS = kGd ? 33 : 32;
+    const int row0 = kGd ? 1 : 0;
     const int r16 = lane & 15;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -494,7 +507,7 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
             else *dst = acc[t][v];
         }
     }
-    if constexpr (MODE == TN_DY) {   // gd: sum the 32 token-row slots of each column
+    if constexpr (kGd) {   // gd: sum the 32 token-row slots of each column
 #pragma unroll
         for (int j = 0; j < 8; ++j) red[lrow][c8 + j] = gd[j];
         __syncthreads();
@@ -502,6 +515,7 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
             float s = 0.f;
             for (int k = 0; k < TN_ROWS; ++k) s += red[k][tid];
             if (c0 + tid < cols) {
+                if (MODE == TN_DU && d) s = s / d[c0 + tid];   // sum dU U = d sum dY U
                 float* dst = part + ((int64_t)z * RS) * cols + c0 + tid;
                 if (counters) st_coherent(dst, s);
                 else *dst = s;
@@ -513,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     // (deterministic) into out[row][c] (= or +=); nobody waits for anybody.
     __shared__ int s_last;
     if (!arrive_last(&counters[blockIdx.x], (int)gridDim.y, &s_last)) return;
-    const int nrows = MODE == TN_DY ? r + 1 : r;
+    const int nrows = kGd ? r + 1 : r;
     const int splits = (int)gridDim.y;
     for (int e = tid; e < nrows * TN_COLS; e += kThreads) {
         const int row = e / TN_COLS;
@@ -770,6 +784,8 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     L->saved_tokens = N;
 }
 
+// dY null: the producer of the output gradient has written dU = bf16(d (.) dY) (d = 1 without
+// DoRA) into L->dU itself (bf16 precision only)
 template <class CT, int R>
 void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* dY, float* dX,
                     int dx_acc, float* dA, float* dB, float* dm) {
@@ -777,10 +793,12 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     const bool bf = L->prec == SA3K_PREC_BF16;
     const int64_t in = W->in, out = W->out;
     const int r = L->rank;
+    const bool du_ready = dY == nullptr;
+    SA3K_REQUIRE(!du_ready || sizeof(CT) == 2, "a precomputed dU needs bf16 precision");
     if (r == 0) {   // plain mul_mat: dX = dY W only
         if (!dX) return;
-        const void* dyc = dY;
-        if (bf) {
+        const void* dyc = du_ready ? L->dU : dY;
+        if (bf && !du_ready) {
             const int64_t n = N * out;
             KernelScope ks(ctx, scope(ctx, L, "lin_bwd_cvt_dy"));
             cvt_kernel<bf16><<<(unsigned)ceil_div(n, kThreads), kThreads, 0, ctx->stream>>>(dY, static_cast<bf16*>(L->dU),
@@ -812,10 +830,16 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         int* counters = use_fixup(ctx, (int64_t)33 * out, ceil_div(out, TN_COLS)) ? ctx->tile_counters : nullptr;
         {
             KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_dy"), 2.0 * N * out * r);
-            skinny_tn_kernel<TN_DY, float><<<dim3((unsigned)ceil_div(out, TN_COLS), (unsigned)S), kThreads, 0,
-                                               ctx->stream>>>(
-                dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
-                L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per, L->red, 0, counters);
+            const dim3 grid((unsigned)ceil_div(out, TN_COLS), (unsigned)S);
+            if (du_ready)
+                skinny_tn_kernel<TN_DU, bf16><<<grid, kThreads, 0, ctx->stream>>>(
+                    static_cast<const bf16*>(L->dU), static_cast<const bf16*>(L->Hc), r,
+                    static_cast<const bf16*>(L->dora ? L->U : nullptr), L->dora ? L->d : nullptr, nullptr, part, N,
+                    out, rows_per, L->red, 0, counters);
+            else
+                skinny_tn_kernel<TN_DY, float><<<grid, kThreads, 0, ctx->stream>>>(
+                    dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
+                    L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per, L->red, 0, counters);
             SA3K_LAUNCHED();
         }
         // the rows kernel below sums the S partials (or, after the in-kernel reduction, reads the
@@ -1424,6 +1448,23 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
 namespace sa3k {
 
 void lin_set_tag(sa3k_lin* l, const char* tag) { l->tag = tag; }
+
+bf16* lin_du(sa3k_lin* L) { return static_cast<bf16*>(L->dU); }
+
+const float* lin_du_scale(const sa3k_lin* L) { return L->rank > 0 && L->dora ? L->d : nullptr; }
+
+void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, float* dX, int dx_accumulate,
+                     float* dA, float* dB, float* dm) {
+    SA3K_REQUIRE(L && X, "null pointer");
+    SA3K_REQUIRE(L->prec == SA3K_PREC_BF16, "a precomputed dU needs a bf16-precision linear");
+    SA3K_REQUIRE(N == L->saved_tokens, "backward must follow a forward over the same tokens");
+    SA3K_REQUIRE(L->rank == 0 || (dA && dB), "adapter gradients need dA/dB buffers");
+    SA3K_REQUIRE(!L->dora || dm, "dora needs a magnitude gradient buffer");
+    SA3K_REQUIRE(x_type == SA3K_TYPE_F32 || x_type == SA3K_TYPE_BF16, "activation type must be f32 or bf16");
+    const int xs = x_type == SA3K_TYPE_F32 ? SRC_F32 : SRC_BF16;
+    if (L->rank <= 16) lin_backward_t<bf16, 16>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm);
+    else lin_backward_t<bf16, 32>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm);
+}
 
 void weight_fwd_operand(const sa3k_weight* W, GemmDesc& g) {
     const WOp wo = weight_operand(W, g.prec == SA3K_PREC_BF16, false);
