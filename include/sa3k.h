@@ -87,7 +87,8 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 inside the producing kernel; 0: by a separate reduction launch; 2: in-kernel for
  *                 outputs of at most 2^18 floats, a separate launch for larger ones (default 0)
  *   "gemm_dma"    1: DMA-fed kernel for compute-type operands (default 1)
- *   "gemm_cfg"    DMA kernel tile configuration (default 0)
+ *   "gemm_cfg"    DMA kernel tile configuration: 0 (default) 128 x 256 tiles for bf16 and
+ *                 128 x 128 for f32; 1: 128 x 128; 4: 128 x 256 (3 stages); 7: 128 x 256 (2 stages)
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
  *                 fill the chip (default 2: 64x128 tiles; 0: the default tile, split over K)
  *   "gemm_nt_store" 1: GEMM outputs are written with non-temporal stores (default 1)

@@ -754,7 +754,10 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     constexpr int kLdsBytes = STAGES * (BM + BN) * kRow + 64;
     const int wg_per_cu = ctx->gemm_wg_per_cu > 0 ? ctx->gemm_wg_per_cu : std::max(1, (160 * 1024) / kLdsBytes);
     const int64_t slots = (int64_t)256 * wg_per_cu;
-    if (ctx->gemm_split && tiles < slots && KT >= 8)
+    // split K only when there are K tiles to spare: below 16 (the 256-token context projection,
+    // K = 768) the split partials and their reduction launch cost more than the idle slots (measured
+    // on MI355X: 256 x 4608 x 768 10.6 us unsplit, 16.9 us in 3 splits)
+    if (ctx->gemm_split && tiles < slots && KT >= 16)
         splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
     if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
     p.kps = std::max(1, (KT + splits - 1) / splits);
@@ -836,7 +839,7 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     const int KT = (int)(p.K / 64);
     int splits = 1;
     const int64_t slots = 256;   // one workgroup per CU (128 KiB of LDS)
-    if (ctx->gemm_split && tiles < slots && KT >= 8)
+    if (ctx->gemm_split && tiles < slots && KT >= 16)
         splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
     if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
     p.kps = std::max(1, (KT + splits - 1) / splits);
@@ -895,10 +898,19 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
             default: break;
         }
     }
+    // bf16: 128 x 256 tiles, 8 waves of 64 x 64, three stages in 144 KiB of LDS (one workgroup per
+    // CU). Against two 128 x 128 workgroups per CU they move a quarter fewer operand bytes per flop
+    // through the CU's vector-memory path, which the MFMA rate otherwise saturates; measured on
+    // MI355X at 2176 rows: QKV 2176 x 7680 x 1536 58.2 vs 64.7 us, 2176 x 3072 x 1536 27.4 vs
+    // 31.0 us, the split-K products 2176 x 1536 x 6144 / 7680 / 12288 53.4 / 63.5 / 93.5 vs
+    // 59.4 / 70.7 / 102.2 us.
     switch (ctx->gemm_cfg) {
-        case 4: return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);   // 144 KiB LDS, 8 waves of 64x64
+        case 1: return launch_dma<128, 128, 2, 2, BF16>(ctx, p);    // 64 KiB LDS: two workgroups per CU
+        case 4: return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);
         case 7: return launch_dma<128, 256, 2, 2, BF16, 8>(ctx, p);
-        default: return launch_dma<128, 128, 2, 2, BF16>(ctx, p);   // 64 KiB LDS: two workgroups per CU
+        default:
+            if constexpr (BF16) return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);
+            else return launch_dma<128, 128, 2, 2, BF16>(ctx, p);
     }
 }
 

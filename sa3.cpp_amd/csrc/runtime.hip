@@ -74,6 +74,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_FORK_TAIL")) ctx->fork_tail = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_LATE_JOIN")) ctx->late_join = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_LIN_MERGE")) ctx->lin_merge = std::atoi(e) != 0;
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
