@@ -670,7 +670,7 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
                    float* dq1, float* dk1, float* dq2, float* dk2, float* dv) {
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     const int BH = B * H;
-    // dQ (second stream) and dK/dV (main stream) only share inputs: they run side by side once the
+    // dQ (third stream) and dK/dV (main stream) only share inputs: they run side by side once the
     // row dots are done (the dot kernel records the fork event)
     const bool side = side_usable(ctx);
     if (side) fork_arm(ctx);
@@ -691,9 +691,9 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
         a.qsplit = (int)std::min<int64_t>({(int64_t)nqb, 16, ceil_div(512, (int64_t)nkb * BH)});
         if (a.qsplit > 1) a.part = gemm_workspace_bytes(ctx, (size_t)a.qsplit * 3 * plane * sizeof(float));
     }
-    if (side) fork_fire(ctx);
+    if (side) quick_fork(ctx);
     {
-        OnSide os(ctx, side);
+        OnQuick os(ctx, side);
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dq" : "attn_bwd_dq_cross");
         attn_bwd_dq_kernel<<<dim3((unsigned)ceil_div(Sq, BLK), (unsigned)BH), kThreads, 0, ctx->stream>>>(a);
         SA3K_LAUNCHED();
@@ -707,7 +707,7 @@ void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2
             SA3K_LAUNCHED();
         }
     }
-    if (side) side_join(ctx);   // the callers consume dQ next
+    if (side) quick_join(ctx);   // the callers consume dQ next
 }
 
 }  // namespace sa3k

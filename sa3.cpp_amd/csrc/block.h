@@ -31,7 +31,7 @@ struct sa3k_block_ws {
     // scratch of the forward (yc) and the backward: may be shared by several workspaces that are
     // used one at a time on the same stream
     float* yc;
-    float *dyf, *dg, *dF, *dfin, *dx2, *doc, *dqf, *dkv, *dhc, *dx1, *dy, *dob, *dqkv, *dh;
+    float *dg, *dfin, *dx2, *doc, *dhc, *dx1, *dob, *dh;
     sa3k::bf16* dOh; float* dn; float *dq1, *dk1, *dq2, *dk2, *dv;
     float* dssg; float* part; int part_chunks;
     // RoPE cos/sin table of positions 0..S-1 for (rope_tab_dims, rope_tab_base); 0: not built yet

@@ -645,19 +645,22 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
         w->g = B16(N * I); w->yf = F32(N * D);
         w->rope_tab = F32((size_t)S * HD);
         w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
+        // dfin and dx1 are read by second-stream column reductions that may still run while the next
+        // block's backward (resident activations, late join) writes the shared scratch: per workspace
+        w->dfin = F32(N * D);
+        w->dx1 = F32(N * D);
         if (share) {
             w->yc = share->yc;
-            w->dyf = share->dyf; w->dg = share->dg; w->dF = share->dF; w->dfin = share->dfin; w->dx2 = share->dx2;
-            w->doc = share->doc; w->dqf = share->dqf; w->dkv = share->dkv; w->dhc = share->dhc; w->dx1 = share->dx1;
-            w->dy = share->dy; w->dob = share->dob; w->dqkv = share->dqkv; w->dh = share->dh;
+            w->dg = share->dg; w->dx2 = share->dx2; w->doc = share->doc; w->dhc = share->dhc;
+            w->dob = share->dob; w->dh = share->dh;
             w->dOh = share->dOh; w->dn = share->dn;
             w->dq1 = share->dq1; w->dk1 = share->dk1; w->dq2 = share->dq2; w->dk2 = share->dk2; w->dv = share->dv;
             w->part = share->part;
         } else {
             w->yc = F32(N * D);
-            w->dyf = F32(N * D); w->dg = F32(N * I); w->dF = F32(N * 2 * I); w->dfin = F32(N * D); w->dx2 = F32(N * D);
-            w->doc = F32(N * D); w->dqf = F32(N * 2 * D); w->dkv = F32(NC * 3 * D); w->dhc = F32(N * D);
-            w->dx1 = F32(N * D); w->dy = F32(N * D); w->dob = F32(N * D); w->dqkv = F32(N * 5 * D); w->dh = F32(N * D);
+            // the adapted linears' output gradients go straight into their dU buffers (lin_du)
+            w->dg = F32(N * I); w->dx2 = F32(N * D); w->doc = F32(N * D); w->dhc = F32(N * D);
+            w->dob = F32(N * D); w->dh = F32(N * D);
             w->dOh = B16(BHS); w->dn = F32(2 * BHq);
             const size_t BHK = std::max(BHS, BHC);   // dK/dV of self (S keys) and cross (Ctx keys)
             w->dq1 = F32(BHS); w->dk1 = F32(BHK); w->dq2 = F32(BHS); w->dk2 = F32(BHK); w->dv = F32(BHK);

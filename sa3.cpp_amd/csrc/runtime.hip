@@ -69,6 +69,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
         ctx->main_stream = ctx->stream;
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking));
+        SA3K_HIP(hipStreamCreateWithFlags(&ctx->quick_stream, hipStreamNonBlocking));
         for (hipEvent_t& e : ctx->side_ev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         SA3K_HIP(hipEventCreateWithFlags(&ctx->block_tail_ev, hipEventDisableTiming));
         if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
@@ -117,6 +118,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->main_stream) (void)hipStreamSynchronize(ctx->main_stream);
     if (ctx->side_stream) (void)hipStreamSynchronize(ctx->side_stream);
+    if (ctx->quick_stream) (void)hipStreamSynchronize(ctx->quick_stream);
     if (ctx->adamw_partials) (void)hipFree(ctx->adamw_partials);
     if (ctx->adamw_result) (void)hipFree(ctx->adamw_result);
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
@@ -137,6 +139,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+    if (ctx->quick_stream) (void)hipStreamDestroy(ctx->quick_stream);
     if (ctx->main_stream) (void)hipStreamDestroy(ctx->main_stream);
     delete ctx;
 }
@@ -206,6 +209,7 @@ SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
 SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
     return sa3k_guard(ctx, "sa3k_sync", [&] {
         SA3K_HIP(hipStreamSynchronize(ctx->side_stream));
+        SA3K_HIP(hipStreamSynchronize(ctx->quick_stream));
         SA3K_HIP(hipStreamSynchronize(ctx->main_stream));
     });
 }

@@ -39,6 +39,7 @@ struct sa3k_ctx {
     hipStream_t stream = nullptr;
     hipStream_t main_stream = nullptr;
     hipStream_t side_stream = nullptr;
+    hipStream_t quick_stream = nullptr;    // third stream: short branches the main stream joins right away
     hipEvent_t side_ev[kSideEvents] = {};   // fork/join events, reused round-robin
     int side_ev_i = 0;
     int use_side = 1;                      // run independent chains on the second stream
@@ -242,6 +243,26 @@ inline void side_join(sa3k_ctx* c) {
     SA3K_HIP(hipEventRecord(e, c->side_stream));
     SA3K_HIP(hipStreamWaitEvent(c->main_stream, e, 0));
 }
+// ---- a third stream for short branches that the main stream joins right away (attention dQ beside
+// dK/dV): joining the second stream instead would also wait for every longer chain queued there
+// first (streams run their work in order)
+inline void quick_fork(sa3k_ctx* c) {
+    hipEvent_t e;
+    if (c->tail_ev) {   // armed before the producer: its completion event, unless more work followed
+        e = c->tail_ev;
+        c->tail_ev = nullptr;
+        if (c->tail_seq != c->main_seq) SA3K_HIP(hipEventRecord(e, c->main_stream));
+    } else {
+        e = side_event(c);
+        SA3K_HIP(hipEventRecord(e, c->main_stream));
+    }
+    SA3K_HIP(hipStreamWaitEvent(c->quick_stream, e, 0));
+}
+inline void quick_join(sa3k_ctx* c) {
+    hipEvent_t e = side_event(c);
+    SA3K_HIP(hipEventRecord(e, c->quick_stream));
+    SA3K_HIP(hipStreamWaitEvent(c->main_stream, e, 0));
+}
 // the main stream waits for the second stream if anything was forked since side_forks was `mark`
 inline void side_join_since(sa3k_ctx* c, uint64_t mark) {
     if (c->side_forks != mark) side_join(c);
@@ -257,6 +278,19 @@ struct SideDeferScope {
     ~SideDeferScope() { --c->side_defer; }
     SideDeferScope(const SideDeferScope&) = delete;
     SideDeferScope& operator=(const SideDeferScope&) = delete;
+};
+// launches inside the scope go to the third stream (when `on`)
+struct OnQuick {
+    sa3k_ctx* c;
+    bool on;
+    OnQuick(sa3k_ctx* ctx, bool enable) : c(ctx), on(enable) {
+        if (on) c->stream = c->quick_stream;
+    }
+    ~OnQuick() {
+        if (on) c->stream = c->main_stream;
+    }
+    OnQuick(const OnQuick&) = delete;
+    OnQuick& operator=(const OnQuick&) = delete;
 };
 // launches inside the scope go to the second stream (when `on`)
 struct OnSide {
