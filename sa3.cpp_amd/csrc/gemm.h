@@ -72,6 +72,16 @@ struct GemmDesc {
     int64_t ldcx = 0;
     int accumulate_x = 0;
     bf16* Cbx = nullptr;   // instead of Cx: extra rows stored as bf16 [Mx][ldcx] (no accumulation)
+    // Nx extra columns appended after B's N rows (bf16, [Nx][ldbx], K-contiguous; DMA-fed kernels,
+    // no second segment): they share every A tile with the main columns, and alpha_x times their
+    // sums goes to Cbn [M][ldcn] as bf16, without colscale, bias, U or accumulation. The corner of
+    // extra rows and extra columns is not stored.
+    int64_t Nx = 0;
+    const void* Bx = nullptr;
+    int64_t ldbx = 0;
+    float alpha_x = 1.0f;
+    bf16* Cbn = nullptr;
+    int64_t ldcn = 0;
     // 1: colscale multiplies the main segment A . B^T only, before the second segment is added
     // (C = colscale (.) (A B^T) + A2 B2^T); needs colscale, no extra rows and no U / Ub copies
     int prescale = 0;
@@ -82,6 +92,9 @@ struct GemmDesc {
 // any other source type the kernel that decodes it on its way into LDS (gemm.hip).
 void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name);
 void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d);
+// whether Nx extra output columns ride on a bf16 Mt x N x K product without another round of
+// workgroups
+bool gemm_extra_cols_free(const sa3k_ctx* ctx, int64_t Mt, int64_t N, int64_t K, int64_t Nx);
 // bf16 products with at most 32 output columns and a plain epilogue (gemm_skinny.hip)
 bool gemm_skinny_ok(const sa3k_ctx* ctx, const GemmDesc& d);
 void gemm_run_skinny(sa3k_ctx* ctx, const GemmDesc& d);

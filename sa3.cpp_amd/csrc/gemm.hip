@@ -553,6 +553,12 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
                  "GEMM extra rows need Ax, Cx or Cbx (and A2x with a second segment)");
     SA3K_REQUIRE(!d.prescale || (d.colscale && d.Mx == 0 && !d.U && !d.Ub),
                  "GEMM prescale needs colscale and no extra rows or pre-scale copies");
+    SA3K_REQUIRE(d.Nx >= 0, "negative extra columns");
+    SA3K_REQUIRE(d.Nx == 0 || (bf && d.a_src == SRC_BF16 && d.b_src == SRC_BF16 && ctx->gemm_dma && d.K2 == 0 &&
+                               !d.prescale && d.N % 8 == 0 && d.Nx % 8 == 0 && d.Bx && al16(d.Bx) &&
+                               (d.ldbx * 2) % 16 == 0 && d.Cbn && d.ldcn >= d.Nx),
+                 "GEMM extra columns need bf16 operands on the DMA kernel, no second segment, 8-column "
+                 "multiples and an aligned Bx with a Cbn output");
     if (gemm_skinny_ok(ctx, d)) {
         KernelScope ks(ctx, prof_name);
         gemm_run_skinny(ctx, d);

@@ -45,6 +45,12 @@ struct DmaParams {
     int vec_epi;   // outputs allow the 16-byte staged epilogue (aligned rows, N % 4 == 0)
     int nt_store;  // staged-epilogue output stores are non-temporal
     int prescale;  // colscale applied to the main segment in the K loop, not in the epilogue
+    // extra columns (GemmDesc::Nx): B rows N .. Nt-1 come from Bx; Nt = N + Nx
+    int64_t Nx, Nt;
+    const void* Bx; int64_t ldbx;
+    float alpha_x;
+    bf16* Cbn; int64_t ldcn;
+    uint32_t bx_bytes;
 };
 
 namespace {
@@ -87,6 +93,17 @@ __device__ __forceinline__ void dma16b(const u32x4& rsrc, uint32_t voff, uint32_
                  : "memory");
 }
 
+// one of two descriptors on a wave-uniform condition, kept in scalar registers
+__device__ __forceinline__ u32x4 pick_rsrc(bool c, const u32x4& a, const u32x4& b) {
+    const bool u = __builtin_amdgcn_readfirstlane((int)c) != 0;
+    u32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane(u ? a.x : b.x);
+    r.y = __builtin_amdgcn_readfirstlane(u ? a.y : b.y);
+    r.z = __builtin_amdgcn_readfirstlane(u ? a.z : b.z);
+    r.w = __builtin_amdgcn_readfirstlane(u ? a.w : b.w);
+    return r;
+}
+
 template <int N>
 struct IC {
     static constexpr int value = N;
@@ -118,6 +135,10 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
 }
 
 __device__ inline void epilogue_elem(const DmaParams& p, int64_t m, int64_t n, float acc) {
+    if (n >= p.N) {   // extra column
+        if (m < p.M) p.Cbn[m * p.ldcn + (n - p.N)] = (bf16)(p.alpha_x * acc);
+        return;
+    }
     float x = p.alpha * acc;
     if (m >= p.M) {
         if (p.Cbx) {
@@ -156,6 +177,14 @@ __device__ __forceinline__ void st_out(bool nt, uint2* p, uint2 v) {
 // Epilogue of four consecutive columns n..n+3 of row m (host-checked: 16-byte aligned rows, N a
 // multiple of 4), same operations and order as epilogue_elem.
 __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a) {
+    if (n >= p.N) {   // four extra columns (N % 4 == 0)
+        if (m < p.M) {
+            const bf16 b[4] = {(bf16)(p.alpha_x * a.x), (bf16)(p.alpha_x * a.y), (bf16)(p.alpha_x * a.z),
+                               (bf16)(p.alpha_x * a.w)};
+            *reinterpret_cast<uint2*>(p.Cbn + m * p.ldcn + (n - p.N)) = __builtin_bit_cast(uint2, b);
+        }
+        return;
+    }
     float4 x = make_float4(p.alpha * a.x, p.alpha * a.y, p.alpha * a.z, p.alpha * a.w);
     if (m >= p.M) {
         if (p.Cbx) {
@@ -232,7 +261,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE_BYTES];
 
     const int64_t Mt = p.M + p.Mx;
-    const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.Nt + BN - 1) / BN);
     const int nwg = gridDim.x;
     const int bid = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
     if (bid >= tiles_m * tiles_n) return;
@@ -291,19 +320,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
         int64_t gn = n0 + row;
-        if (gn >= p.N) gn = 0;
-        bg[q] = static_cast<const char*>(p.B) + (gn * p.ldb + k0 + kc * CE) * EB;
-        b2g[q] = (kc * CE < p.K2) ? static_cast<const char*>(p.B2) + (gn * p.ldb2 + kc * CE) * EB
-                                  : static_cast<const char*>(p.zero);
+        if (gn >= p.Nt) gn = 0;
+        bg[q] = gn < p.N ? static_cast<const char*>(p.B) + (gn * p.ldb + k0 + kc * CE) * EB
+                         : static_cast<const char*>(p.Bx) + ((gn - p.N) * p.ldbx + k0 + kc * CE) * EB;
+        b2g[q] = (kc * CE < p.K2 && gn < p.N) ? static_cast<const char*>(p.B2) + (gn * p.ldb2 + kc * CE) * EB
+                                              : static_cast<const char*>(p.zero);
     }
 
     // Main-segment loads through buffer descriptors when the operand extents allow it and the
     // tile's rows come from one source (A only, or the extra rows Ax only); otherwise, and for the
     // second segment, per-lane global addresses.
-    const bool use_buf = p.a_bytes != 0 && p.b_bytes != 0;
+    const bool use_buf = p.a_bytes != 0 && p.b_bytes != 0 && (p.Nx == 0 || p.bx_bytes != 0);
     const int a_src = !use_buf ? 0 : (p.Mx == 0 || m0 + BM <= p.M) ? 1 : (m0 >= p.M && m0 + BM <= Mt && p.ax_bytes) ? 2 : 0;
     const u32x4 rs_a = buffer_rsrc(a_src == 2 ? p.Ax : p.A, a_src == 2 ? p.ax_bytes : p.a_bytes);
-    const u32x4 rs_b = buffer_rsrc(p.B, p.b_bytes);
+    const u32x4 rs_b = buffer_rsrc(p.B, p.b_bytes), rs_bx = buffer_rsrc(p.Bx, p.bx_bytes);
     uint32_t aoff[NA], boff[NB];
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
@@ -316,9 +346,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
         int64_t gn = n0 + row;
-        if (gn >= p.N) gn = 0;
-        boff[q] = (uint32_t)((gn * p.ldb + kc * CE) * EB);
+        if (gn >= p.Nt) gn = 0;
+        boff[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * CE) * EB) : (uint32_t)(((gn - p.N) * p.ldbx + kc * CE) * EB);
     }
+    // the 8 rows of B slot (q, wave) start at n0 + (q * NT + 64 wave) / 8: one source per slot
+    // (N % 8 == 0), chosen on the scalar unit
+    auto slot_bx = [&](int q) { return n0 + (q * NT + wave * 64) / 8 < p.Nt && n0 + (q * NT + wave * 64) / 8 >= p.N; };
 
     auto issue = [&](auto s_c, int t) {
         constexpr uint32_t so_lds = (uint32_t)((decltype(s_c)::value % STAGES) * STAGE_BYTES);
@@ -328,7 +361,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
                 for (int q = 0; q < NA; ++q) dma16b(rs_a, aoff[q], so, dst[q] + so_lds);
 #pragma unroll
-                for (int q = 0; q < NB; ++q) dma16b(rs_b, boff[q], so, dst[NA + q] + so_lds);
+                for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), boff[q], so, dst[NA + q] + so_lds);
             } else {
 #pragma unroll
                 for (int q = 0; q < NA; ++q) dma16(ag[q] + (int64_t)t * (BKE * EB), dst[q] + so_lds);
@@ -448,17 +481,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     if (p.prescale && !ext) scale_acc();   // a split without the second segment
 
     if (p.ws && p.counters) {  // split-K with in-kernel reduction: coherent partials, element-wise
-        float* w = p.ws + (int64_t)z * Mt * p.N;
+        float* w = p.ws + (int64_t)z * Mt * p.Nt;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int64_t n = n0 + wn0 + MT * j + (lane & (MT - 1));
-            if (n >= p.N) continue;
+            if (n >= p.Nt) continue;
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int v = 0; v < AE; ++v) {
                     const int64_t m = m0 + wm0 + MT * i + out_row(v);
-                    if (m < Mt) st_coherent(w + m * p.N + n, acc[i][j][v]);
+                    if (m < Mt) st_coherent(w + m * p.Nt + n, acc[i][j][v]);
                 }
         }
         // The last split of this tile to arrive sums the partials in split order (deterministic:
@@ -468,9 +501,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
         const int splits = (int)gridDim.y;
         for (int e = tid; e < BM * BN; e += NT) {
             const int64_t m = m0 + e / BN, n = n0 + e % BN;
-            if (m >= Mt || n >= p.N) continue;
+            if (m >= Mt || n >= p.Nt) continue;
             float sum = 0.f;
-            for (int zz = 0; zz < splits; ++zz) sum += ld_coherent(p.ws + (int64_t)zz * Mt * p.N + m * p.N + n);
+            for (int zz = 0; zz < splits; ++zz) sum += ld_coherent(p.ws + (int64_t)zz * Mt * p.Nt + m * p.Nt + n);
             epilogue_elem(p, m, n, sum);
         }
         return;
@@ -480,14 +513,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int64_t n = n0 + wn0 + MT * j + (lane & (MT - 1));
-            if (n >= p.N) continue;
+            if (n >= p.Nt) continue;
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int v = 0; v < AE; ++v) {
                     const int64_t m = m0 + wm0 + MT * i + out_row(v);
                     if (m >= Mt) continue;
-                    if (p.ws) p.ws[(int64_t)z * Mt * p.N + m * p.N + n] = acc[i][j][v];
+                    if (p.ws) p.ws[(int64_t)z * Mt * p.Nt + m * p.Nt + n] = acc[i][j][v];
                     else epilogue_elem(p, m, n, acc[i][j][v]);
                 }
         }
@@ -516,9 +549,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
         for (int e = tid; e < ER * CPR; e += NT) {
             const int r = e / CPR, c = (e % CPR) * 4;
             const int64_t m = m0 + rb + r, n = n0 + c;
-            if (m >= Mt || n >= p.N) continue;
+            if (m >= Mt || n >= p.Nt) continue;
             const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + c);
-            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.N + m * p.N + n) = a;
+            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + n) = a;
             else epilogue_vec4(p, m, n, a);
         }
         if (rb + ER < BM) __syncthreads();
@@ -555,7 +588,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE_BYTES];
 
     const int64_t Mt = p.M + p.Mx;
-    const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.N + BN - 1) / BN);
+    const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.Nt + BN - 1) / BN);
     const int nwg = gridDim.x;
     const int bid = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
     if (bid >= tiles_m * tiles_n) return;
@@ -582,7 +615,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
     const u32x4 rs_a = buffer_rsrc(p.A, p.a_bytes), rs_ax = buffer_rsrc(p.Ax, p.ax_bytes);
-    const u32x4 rs_b = buffer_rsrc(p.B, p.b_bytes);
+    const u32x4 rs_b = buffer_rsrc(p.B, p.b_bytes), rs_bx = buffer_rsrc(p.Bx, p.bx_bytes);
     // the rank segment's descriptors: [rows][ld2] bf16, K2 valid columns
     const uint32_t a2_bytes = p.K2 > 0 ? (uint32_t)(((p.M - 1) * p.lda2 + p.K2) * 2) : 0u;
     const uint32_t a2x_bytes = p.K2 > 0 && p.Mx > 0 ? (uint32_t)(((p.Mx - 1) * p.lda2x + p.K2) * 2) : 0u;
@@ -609,10 +642,14 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
         int64_t gn = n0 + row;
-        if (gn >= p.N) gn = p.N - 1;
-        bo.off[q] = (uint32_t)((gn * p.ldb + kc * 8) * 2);
-        b2o.off[q] = kc * 8 < p.K2 ? (uint32_t)((gn * p.ldb2 + kc * 8) * 2) : kNoData;
+        if (gn >= p.Nt) gn = p.Nt - 1;
+        bo.off[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * 8) * 2) : (uint32_t)(((gn - p.N) * p.ldbx + kc * 8) * 2);
+        b2o.off[q] = kc * 8 < p.K2 && gn < p.N ? (uint32_t)((gn * p.ldb2 + kc * 8) * 2) : kNoData;
     }
+    auto slot_bx = [&](int q) {   // wave-uniform: slot q's B rows are extra columns (N % 8 == 0)
+        const int64_t r0 = min(n0 + 64 * q + 8 * wave, p.Nt - 1);
+        return r0 >= p.N;
+    };
     auto slot_x = [&](int q) {   // wave-uniform: slot q's rows are extra rows
         const int64_t r0 = min(m0 + 64 * q + 8 * wave, Mt - 1);
         return r0 >= p.M;
@@ -626,7 +663,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 #pragma unroll
             for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_ax : rs_a, ao.off[q], so, dst0 + q * NT * 16);
 #pragma unroll
-            for (int q = 0; q < NB; ++q) dma16b(rs_b, bo.off[q], so, dst0 + BM * kRow + q * NT * 16);
+            for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), bo.off[q], so, dst0 + BM * kRow + q * NT * 16);
         } else {
 #pragma unroll
             for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_a2x : rs_a2, a2o.off[q], 0u, dst0 + q * NT * 16);
@@ -710,9 +747,9 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
         for (int e = tid; e < ER * CPR; e += NT) {
             const int r = e / CPR, c = (e % CPR) * 4;
             const int64_t m = m0 + rb + r, n = n0 + c;
-            if (m >= Mt || n >= p.N) continue;
+            if (m >= Mt || n >= p.Nt) continue;
             const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + c);
-            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.N + m * p.N + n) = a;
+            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + n) = a;
             else epilogue_vec4(p, m, n, a);
         }
         if (rb + ER < BM) __syncthreads();
@@ -723,7 +760,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 // when the outputs allow 16-byte accesses, one element otherwise.
 __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, int splits) {
     const int64_t Mt = p.M + p.Mx;
-    const int64_t plane = Mt * p.N;
+    const int64_t plane = Mt * p.Nt;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (p.vec_epi) {
         const int64_t e = idx * 4;
@@ -733,20 +770,20 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
             const float4 v = *reinterpret_cast<const float4*>(p.ws + (int64_t)z * plane + e);
             s = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
         }
-        const int64_t m = e / p.N, n = e - m * p.N;
+        const int64_t m = e / p.Nt, n = e - m * p.Nt;
         epilogue_vec4(p, m, n, s);
         return;
     }
     if (idx >= plane) return;
     float s = 0.f;
     for (int z = 0; z < splits; ++z) s += p.ws[(int64_t)z * plane + idx];
-    const int64_t m = idx / p.N, n = idx - m * p.N;
+    const int64_t m = idx / p.Nt, n = idx - m * p.Nt;
     epilogue_elem(p, m, n, s);
 }
 
 template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
-    const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.N, BN);
+    const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
     const int KT = (int)(p.K / (BF16 ? 64 : 32));
     int splits = 1;
@@ -774,19 +811,20 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         p.a_bytes = extent(p.M, p.lda);
         p.ax_bytes = p.Mx > 0 ? extent(p.Mx, p.ldax) : 0u;
         p.b_bytes = extent(p.N, p.ldb);
+        p.bx_bytes = p.Nx > 0 ? extent(p.Nx, p.ldbx) : 0u;
         // the staged epilogue stores 4 columns at once: rows and vectors must be 16-byte (f32) /
         // 8-byte (bf16) aligned
         auto ok = [](const void* q, int64_t ld, int align) {
             return q == nullptr || (ld % 4 == 0 && (uintptr_t)q % (uintptr_t)align == 0);
         };
         p.nt_store = ctx->gemm_nt_store;
-        p.vec_epi = p.N % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) &&
-                    ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) &&
-                    ok(p.bias, 4, 16);
+        p.vec_epi = p.N % 4 == 0 && p.Nt % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) &&
+                    ok(p.Ub, p.ldu, 8) && ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) &&
+                    ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
     if (splits > 1) {
-        p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
-        if (use_fixup(ctx, (p.M + p.Mx) * p.N, tiles)) p.counters = ctx->tile_counters;
+        p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
+        if (use_fixup(ctx, (p.M + p.Mx) * p.Nt, tiles)) p.counters = ctx->tile_counters;
     }
     dim3 g((unsigned)grid, (unsigned)splits);
     {
@@ -794,14 +832,14 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         static const std::string name = std::string("gemm_dma<") + std::to_string(BM) + "," + std::to_string(BN) + "," +
                                         std::to_string(WMW) + "," + std::to_string(STAGES) +
                                         (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (BF16 ? ",bf16>" : ",f32>");
-        KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
+        KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
         launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW>, g,
                  dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1 && !p.counters) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
-        const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.N / 4 : (p.M + p.Mx) * p.N;
+        const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.Nt / 4 : (p.M + p.Mx) * p.Nt;
         launch_k(ctx, true, gemm_dma_splitk_reduce, dim3((unsigned)ceil_div(items, kThreads)), dim3(kThreads), 0, p,
                  splits);
         SA3K_LAUNCHED();
@@ -815,6 +853,7 @@ bool big_ok(const sa3k_ctx* ctx, const DmaParams& p) {
     const int64_t lim = (int64_t)1 << 31;
     if (ctx->gemm_fixup != 0 || p.prescale) return false;
     if (extent(p.M, p.lda, p.K) >= lim || extent(p.N, p.ldb, p.K) >= lim) return false;
+    if (p.Nx > 0 && (p.N % 8 != 0 || extent(p.Nx, p.ldbx, p.K) >= lim)) return false;
     if (p.Mx > 0 && (p.M % 8 != 0 || extent(p.Mx, p.ldax, p.K) >= lim)) return false;
     if (p.K2 > 0 && (extent(p.M, p.lda2, p.K2) >= lim || extent(p.N, p.ldb2, p.K2) >= lim ||
                      (p.Mx > 0 && extent(p.Mx, p.lda2x, p.K2) >= lim)))
@@ -828,13 +867,14 @@ bool vec_epi_ok(const DmaParams& p) {
     auto ok = [](const void* q, int64_t ld, int align) {
         return q == nullptr || (ld % 4 == 0 && (uintptr_t)q % (uintptr_t)align == 0);
     };
-    return p.N % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) && ok(p.Cb, p.ldcb, 8) &&
-           ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) && ok(p.bias, 4, 16);
+    return p.N % 4 == 0 && p.Nt % 4 == 0 && ok(p.C, p.ldc, 16) && ok(p.U, p.ldu, 16) && ok(p.Ub, p.ldu, 8) &&
+           ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) && ok(p.colscale, 4, 16) &&
+           ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
 }
 
 void launch_big(sa3k_ctx* ctx, DmaParams p) {
     constexpr int BM = 256, BN = 256;
-    const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.N, BN);
+    const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
     const int KT = (int)(p.K / 64);
     int splits = 1;
@@ -850,17 +890,18 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     p.a_bytes = extent(p.M, p.lda);
     p.ax_bytes = extent(p.Mx, p.ldax);
     p.b_bytes = extent(p.N, p.ldb);
+    p.bx_bytes = extent(p.Nx, p.ldbx);
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
-    if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.N * sizeof(float));
+    if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
     {
-        KernelScope ks(ctx, "gemm_big<256,256,bf16>", 2.0 * (double)(p.M + p.Mx) * (double)p.N * (double)(p.K + p.K2));
+        KernelScope ks(ctx, "gemm_big<256,256,bf16>", 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
         launch_k(ctx, splits == 1, gemm_big_kernel, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1) {
         KernelScope ks(ctx, "gemm_splitk_reduce");
-        const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.N / 4 : (p.M + p.Mx) * p.N;
+        const int64_t items = p.vec_epi ? (p.M + p.Mx) * p.Nt / 4 : (p.M + p.Mx) * p.Nt;
         launch_k(ctx, true, gemm_dma_splitk_reduce, dim3((unsigned)ceil_div(items, kThreads)), dim3(kThreads), 0, p,
                  splits);
         SA3K_LAUNCHED();
@@ -870,13 +911,13 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
 template <bool BF16>
 void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if constexpr (BF16) {
-        if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.N > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
+        if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.Nt > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
             // 256 x 256 tiles (one per CU) where they fill the chip about as evenly as 128 x 128 tiles
             // (two per CU) do and need no split over K; measured on MI355X at 2176 rows: FFN
             // up-projection 2176 x 12288 x 1536 107 vs 111 us, 2176 x 6144 x 1536 52 vs 56 us,
             // 8192^3 877 vs 1057 us; the 2176 x 7680 QKV projection (270 tiles) 98 vs 62 us.
             const int64_t Mt = p.M + p.Mx;
-            const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.N, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+            const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.Nt, 128);
             const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
             const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
             if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return launch_big(ctx, p);
@@ -884,12 +925,12 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     }
     const int64_t Mt = p.M + p.Mx;
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, BF16>(ctx, p);
-    if (p.N <= 32) return launch_dma<128, 32, 4, 4, BF16>(ctx, p);
-    if (p.N <= 64) return launch_dma<128, 64, 4, 4, BF16>(ctx, p);
+    if (p.Nt <= 32) return launch_dma<128, 32, 4, 4, BF16>(ctx, p);
+    if (p.Nt <= 64) return launch_dma<128, 64, 4, 4, BF16>(ctx, p);
     // Grids of 128x128 tiles that leave a quarter of the two-per-CU slots idle: with a short K a
     // 64x128 tile and no split (2176 x 1536 x 1536: 21 us instead of 28 with split-K); with a long
     // K (>= 4096) the 128x128 tile split over K stays faster.
-    const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+    const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.Nt, 128);
     if (tiles128 < 384 && p.K < (BF16 ? 4096 : 2048)) {
         switch (ctx->gemm_small) {
             case 1: return launch_dma<64, 128, 2, 2, BF16>(ctx, p);
@@ -914,13 +955,49 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     }
 }
 
+// Rounds of resident workgroups a bf16 DMA GEMM of Mt x Nt x K takes under the dispatch above
+// (the tile and split choices, ignoring operand alignment): splits x tiles / slots, rounded up.
+int64_t dma_rounds(const sa3k_ctx* ctx, int64_t Mt, int64_t Nt, int64_t K) {
+    const int64_t KT = K / 64;
+    auto rounds = [&](int64_t tiles, int64_t slots, bool may_split) {
+        int64_t splits = 1;
+        if (may_split && ctx->gemm_split && tiles < slots && KT >= 16)
+            splits = std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
+        splits = std::max<int64_t>(1, ceil_div(KT, std::max<int64_t>(1, ceil_div(KT, splits))));
+        return ceil_div(tiles * splits, slots);
+    };
+    if (ctx->gemm_big != 0 && Mt > 32 && Nt > 64) {
+        const int64_t t256 = ceil_div(Mt, 256) * ceil_div(Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
+        const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
+        const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
+        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return rounds(t256, 256, true);
+    }
+    if (Mt <= 32 || Nt <= 64) return 1;
+    const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
+    if (tiles128 < 384 && K < 4096 && ctx->gemm_small == 2) return rounds(ceil_div(Mt, 64) * ceil_div(Nt, 128), 512, true);
+    if (ctx->gemm_cfg == 1) return rounds(tiles128, 512, true);
+    return rounds(ceil_div(Mt, 128) * ceil_div(Nt, 256), 256, true);
+}
+
 }  // namespace
+
+// Whether Nx extra output columns ride on a bf16 Mt x N x K product without costing it another
+// round of workgroups (their tiles fill slots the product leaves idle).
+bool gemm_extra_cols_free(const sa3k_ctx* ctx, int64_t Mt, int64_t N, int64_t K, int64_t Nx) {
+    return dma_rounds(ctx, Mt, N + Nx, K) <= dma_rounds(ctx, Mt, N, K);
+}
 
 void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     DmaParams p{d.A, d.lda, d.B, d.ldb, d.A2, d.lda2, d.B2, d.ldb2, d.K2, d.M, d.N, d.K, d.alpha,
                 d.colscale, d.bias, d.C, d.ldc, d.accumulate, d.Cb, d.ldcb, d.U, d.Ub, d.ldu,
                 d.Mx, d.Ax, d.ldax, d.A2x, d.lda2x, d.Cx, d.ldcx, d.accumulate_x, d.Cbx, nullptr, 0, ctx->zero_page};
     p.prescale = d.prescale;
+    p.Nx = d.Nx;
+    p.Nt = d.N + d.Nx;
+    p.Bx = d.Bx; p.ldbx = d.ldbx;
+    p.alpha_x = d.alpha_x;
+    p.Cbn = d.Cbn; p.ldcn = d.ldcn;
+    p.bx_bytes = 0;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

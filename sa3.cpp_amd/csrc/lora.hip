@@ -751,8 +751,11 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
         X = L->Xb;
         x_src = SRC_BF16;
     }
+    // merged: Hc = s X A^T as r extra output columns of the main product (B rows from A) when they
+    // cost it no extra round of workgroups, else as its own product beside it
+    const bool h_cols = merged && bf && (ctx->rank_cols & 1) && gemm_extra_cols_free(ctx, N, W->out, W->in, L->rank);
     // Hc = s X A^T
-    if (L->rank > 0) {
+    if (L->rank > 0 && !h_cols) {
         GemmDesc h;
         h.prec = L->prec; h.a_src = x_src; h.b_src = bf ? SRC_BF16 : SRC_F32;
         h.A = X; h.lda = W->in; h.B = L->Ac; h.ldb = W->in;
@@ -768,6 +771,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     g.A = X; g.lda = W->in;
     if (merged) {   // Y = d (.) (X W_eff^T) + bias
         g.b_src = SRC_BF16; g.B = L->Wm; g.ldb = W->in;
+        if (h_cols) { g.Nx = L->rank; g.Bx = L->Ac; g.ldbx = W->in; g.alpha_x = L->s; g.Cbn = static_cast<bf16*>(L->Hc); g.ldcn = L->rank; }
     } else {        // Y = d (.) (X W^T + Hc B^T) + bias: the rank term as the second segment
         const WOp wo = weight_operand(W, bf, false);
         g.b_src = wo.src; g.B = wo.p; g.ldb = wo.ld; g.Bs = wo.s; g.ldbs = wo.lds;
@@ -915,6 +919,9 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dub"));
     };
     if (!merged) sdub();
+    // merged: sdUB = s dU B as r extra output columns of the dX GEMM (B rows from B^T) when they cost
+    // it no extra round of workgroups; the dA partials then follow that GEMM
+    const bool sdub_cols = merged && dX && (ctx->rank_cols & 2) && gemm_extra_cols_free(ctx, N + (L->dora ? r : 0), in, out, r);
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
     //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
@@ -954,12 +961,12 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             x_part, stride, x_S, (int64_t)r * in, dA, 1);
         SA3K_LAUNCHED();
     };
-    if (early) {
+    if (early && !sdub_cols) {
         if (side) fork_fire(ctx);   // sdUB (merged: dU) and X are ready
         OnSide os(ctx, side);
         if (merged) sdub();
         x_partials();
-    } else if (merged) {
+    } else if (merged && !sdub_cols) {
         sdub();
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
@@ -974,6 +981,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
         g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
         if (!merged) { g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
+        if (sdub_cols) { g.Nx = r; g.Bx = L->Bt; g.ldbx = out; g.alpha_x = L->s; g.Cbn = static_cast<bf16*>(L->sdUB); g.ldcn = r; }
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
         if (L->dora) {
@@ -993,9 +1001,10 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     }
     // 4b. the partial sums into dA, after step 3
     if (early) {
-        if (side) fork_fire(ctx);   // the dX GEMM has added its dA rows
+        if (side) fork_fire(ctx);   // the dX GEMM has added its dA rows (and written sdUB)
         {
             OnSide os(ctx, side);
+            if (sdub_cols) x_partials();
             x_sum();
         }
         if (side) side_join_unless_deferred(ctx);

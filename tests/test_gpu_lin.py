@@ -147,7 +147,10 @@ def test_dora_linear_big_tiles(ctx, N, in_, out_, r, merge):
     ref = run_oracle(X, dY, Wdec, A, B, 1.5, True, mag)
     for k in ("Y", "dX", "dA", "dB", "dm"):
         assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
-        assert rel_err(got[k], small[k]) < 1e-5, k
+        # the tile families differ in f32 summation order only; merged, the rank products ride on
+        # the tiled products as extra columns and are rounded to bf16 after that order, so an
+        # element of s dU B or s X A^T may round the other way
+        assert rel_err(got[k], small[k]) < (1e-4 if merge else 1e-5), k
 
 
 def test_gradients_accumulate(ctx):
@@ -214,3 +217,27 @@ def test_merged_refresh_terms(ctx, wt, r):
         assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
         # the two formulations differ only by bf16 roundings of the operands
         assert rel_err(got[k], seg[k]) < 1e-2, k
+
+
+@pytest.mark.parametrize("cols", [0, 1, 2, 3])
+def test_rank_products_as_extra_columns(ctx, cols):
+    """Merged DoRA linear with s X A^T (bit 0) and s dU B (bit 1) as extra output columns of the
+    forward / dX products (option rank_cols), at the DiT's 2176-token shape (the 256 x 256, 128 x 256
+    and split-K tilings all carry them) and a ragged one: within the bf16 bar of the oracle, and
+    within bf16 rounding of the separate products."""
+    for N, in_, out_, r in ((2176, 1536, 6144, 32), (2176, 6144, 1536, 32), (120, 192, 320, 16)):
+        X, dY, W, A, B = make_inputs(21, N, in_, out_, r)
+        Wh = W.astype(np.float16)
+        Wdec = Wh.astype(np.float32)
+        mag = (oracle.row_norms(Wdec) * 1.02).astype(np.float32)
+        try:
+            ctx.set_option("rank_cols", cols)
+            got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
+            ctx.set_option("rank_cols", 0)
+            sep = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
+        finally:
+            ctx.set_option("rank_cols", 1)
+        ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
+        for k in ("Y", "dX", "dA", "dB", "dm"):
+            assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, (N, k)
+            assert rel_err(got[k], sep[k]) < 1e-4, (N, k)
