@@ -120,10 +120,14 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "rank_cols"   bit 0: a merged linear's rank product s X A^T rides on its forward product as r
  *                 extra output columns where they cost it no extra round of workgroups (default 1);
  *                 bit 1: likewise s dU B on its dX product (default 0: measured slower on MI355X
- *                 than the separate product beside it)
+ *                 than the separate product beside it; needs merge_kn 0)
+ *   "merge_kn"    1: a merged linear's dX product reads W + s B A in its stored [out][in] layout as
+ *                 a K-major operand (transposed by the LDS reads), so the refresh writes one bf16
+ *                 copy; 0: the refresh also writes the transposed copy [in][out] and dX reads
+ *                 that (default 1). It holds from a linear's next prepare (a DiT: its setup).
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny, gemm_big, gemm_splits, lin_merge and rank_cols, which change the f32
- * summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big, gemm_splits, lin_merge, rank_cols and merge_kn, which change
+ * the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

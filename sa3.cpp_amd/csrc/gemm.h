@@ -76,6 +76,9 @@ struct GemmDesc {
     // no second segment): they share every A tile with the main columns, and alpha_x times their
     // sums goes to Cbn [M][ldcn] as bf16, without colscale, bias, U or accumulation. The corner of
     // extra rows and extra columns is not stored.
+    // 1: B is stored [K][ldb] (N contiguous: the dX product dU W reads W [out][in] as it lies);
+    // bf16 on the DMA-fed kernels, no second segment and no extra columns
+    int b_kn = 0;
     int64_t Nx = 0;
     const void* Bx = nullptr;
     int64_t ldbx = 0;

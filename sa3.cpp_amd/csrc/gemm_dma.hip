@@ -51,6 +51,7 @@ struct DmaParams {
     float alpha_x;
     bf16* Cbn; int64_t ldcn;
     uint32_t bx_bytes;
+    int b_kn;   // B stored [K][ldb], N contiguous (GemmDesc::b_kn)
 };
 
 namespace {
@@ -71,6 +72,22 @@ __device__ __forceinline__ int swz(int r) {
 }
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// B operand stored [K][N] (b_kn): a stage's B region holds BN/64 sub-tiles of [64 k][64 n] bf16,
+// 128-byte rows with the chunk swizzle above. ld_tr reads them transposed (ds_read_b64_tr_b16):
+// every 16-lane group returns, in lane j of the group, T[k0 .. k0+3][n0 + j] of a sub-tile (lane
+// j addresses row k0 + j/4, columns n0 + 4 (j%4) .. +3); k0, n0 may differ between the groups.
+__device__ __forceinline__ bf16x4 ld_tr(const char* t, int k0, int n0, int lane) {
+    const int j = lane & 15, row = k0 + (j >> 2), n = n0 + 4 * (j & 3);
+    const char* a = t + row * kRow + (((n >> 3) ^ swz(row)) << 4) + (n & 7) * 2;
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                          (__attribute__((address_space(3))) v4s*)((lds_ptr_t)a)));
+}
+__device__ __forceinline__ bf16x8 cat44(bf16x4 a, bf16x4 b) {
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 // Raw buffer descriptor over [base, base + bytes): loads past the end return zeros.
 __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
@@ -230,7 +247,7 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
 // NW wave64s per workgroup (4 or 8): WMW of them along M, NW/WMW along N, each owning a
 // (BM/WMW) x (BN/(NW/WMW)) block of the tile. With 8 waves two share each SIMD, so one wave's
 // LDS reads and waits overlap the other's MFMAs inside a single workgroup.
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4>
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false>
 __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     constexpr int NT = NW * 64;
     constexpr int WNW = NW / WMW;
@@ -255,6 +272,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     static_assert(ER >= WTM, "epilogue staging does not fit");
     static_assert(NA >= 1 && NB >= 1 && FM >= 1 && FN >= 1, "tile too small");
     static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * LPT < 64, "pipeline depth");
+    static_assert(!KN || (BF16 && BN % 64 == 0), "a [K][N] B operand needs bf16 and whole 64-column sub-tiles");
     // The stages are consecutive STAGE_BYTES regions of one LDS array, each always addressed at a
     // compile-time offset. Every LDS write of the K loop is an inline-asm DMA, so the compiler
     // inserts no waits of its own; the loop orders DMA and reads with vmcnt waits and barriers.
@@ -349,6 +367,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
         if (gn >= p.Nt) gn = 0;
         boff[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * CE) * EB) : (uint32_t)(((gn - p.N) * p.ldbx + kc * CE) * EB);
     }
+    if constexpr (KN) {
+        // [K][N] B: slot s of the B region is sub-tile s / 512, row k = (s % 512) / 8 of the K tile,
+        // logical chunk (s % 8) ^ swz(k): 8 columns at n0 + 64 (s / 512) + 8 chunk (columns past N
+        // read a valid column; their results are never stored). The K tile moves in soff.
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            const int s = q * NT + tid, t = s >> 9, k = (s & 511) >> 3, kc = (s & 7) ^ swz(k);
+            int64_t gn = n0 + 64 * t + 8 * kc;
+            if (gn + 8 > p.N) gn = p.N - 8;
+            boff[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
+        }
+    }
     // the 8 rows of B slot (q, wave) start at n0 + (q * NT + 64 wave) / 8: one source per slot
     // (N % 8 == 0), chosen on the scalar unit
     auto slot_bx = [&](int q) { return n0 + (q * NT + wave * 64) / 8 < p.Nt && n0 + (q * NT + wave * 64) / 8 >= p.N; };
@@ -356,15 +386,22 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     auto issue = [&](auto s_c, int t) {
         constexpr uint32_t so_lds = (uint32_t)((decltype(s_c)::value % STAGES) * STAGE_BYTES);
         if (t < Tm) {
+            const uint32_t so = (uint32_t)((k0 + (int64_t)t * BKE) * EB);
             if (a_src != 0) {
-                const uint32_t so = (uint32_t)((k0 + (int64_t)t * BKE) * EB);
 #pragma unroll
                 for (int q = 0; q < NA; ++q) dma16b(rs_a, aoff[q], so, dst[q] + so_lds);
-#pragma unroll
-                for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), boff[q], so, dst[NA + q] + so_lds);
             } else {
 #pragma unroll
                 for (int q = 0; q < NA; ++q) dma16(ag[q] + (int64_t)t * (BKE * EB), dst[q] + so_lds);
+            }
+            if constexpr (KN) {   // always through the descriptor: the K tile is a row offset
+                const uint32_t sob = (uint32_t)((k0 + (int64_t)t * BKE) * p.ldb * 2);
+#pragma unroll
+                for (int q = 0; q < NB; ++q) dma16b(rs_b, boff[q], sob, dst[NA + q] + so_lds);
+            } else if (a_src != 0) {
+#pragma unroll
+                for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), boff[q], so, dst[NA + q] + so_lds);
+            } else {
 #pragma unroll
                 for (int q = 0; q < NB; ++q) dma16(bg[q] + (int64_t)t * (BKE * EB), dst[NA + q] + so_lds);
             }
@@ -403,7 +440,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i) af[ks][i] = *reinterpret_cast<const bf16x8*>(frag(As, wm0 + 32 * i + r, kc));
 #pragma unroll
-                for (int j = 0; j < FN; ++j) bfr[ks][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
+                for (int j = 0; j < FN; ++j) {
+                    if constexpr (KN) {
+                        // lane: column nb + lane%32, K rows 16 ks + 8 (lane/32) .. +7 of the sub-tile
+                        const int nb = wn0 + 32 * j;
+                        const char* sub = Bs + (nb >> 6) * (64 * kRow);
+                        const int nl = (nb & 63) + 16 * ((lane >> 4) & 1), kb = 16 * ks + 8 * g;
+                        bfr[ks][j] = cat44(ld_tr(sub, kb, nl, lane), ld_tr(sub, kb + 4, nl, lane));
+                    } else {
+                        bfr[ks][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
+                    }
+                }
             }
             // keep the reads ahead of the MFMAs (the LDS counter tracks at most 15 reads, so the
             // first half's MFMAs can start with the second half's reads still outstanding)
@@ -574,6 +621,7 @@ struct BigSeg {
     uint32_t off[4];
 };
 
+template <bool KN>
 __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     constexpr int BM = 256, BN = 256, NW = 8, NT = 512, WMW = 4;
     constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW);   // 64 x 128
@@ -650,6 +698,17 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
         const int64_t r0 = min(n0 + 64 * q + 8 * wave, p.Nt - 1);
         return r0 >= p.N;
     };
+    if constexpr (KN) {
+        // [K][N] B: slot s of the B region is sub-tile s / 512 (64 columns), row k = (s % 512) / 8 of
+        // the K tile, logical chunk (s % 8) ^ swz(k); columns past N read a valid column
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            const int s = q * NT + tid, t = s >> 9, k = (s & 511) >> 3, kc = (s & 7) ^ swz(k);
+            int64_t gn = n0 + 64 * t + 8 * kc;
+            if (gn + 8 > p.N) gn = p.N - 8;
+            bo.off[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
+        }
+    }
     auto slot_x = [&](int q) {   // wave-uniform: slot q's rows are extra rows
         const int64_t r0 = min(m0 + 64 * q + 8 * wave, Mt - 1);
         return r0 >= p.M;
@@ -662,8 +721,15 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
             const uint32_t so = k0b + (uint32_t)t * 128u;
 #pragma unroll
             for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_ax : rs_a, ao.off[q], so, dst0 + q * NT * 16);
+            if constexpr (KN) {   // the K tile is a row offset of the [K][N] operand
+                const uint32_t sob = (uint32_t)(((int64_t)kt0 + t) * 64 * p.ldb * 2);
 #pragma unroll
-            for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), bo.off[q], so, dst0 + BM * kRow + q * NT * 16);
+                for (int q = 0; q < NB; ++q) dma16b(rs_b, bo.off[q], sob, dst0 + BM * kRow + q * NT * 16);
+            } else {
+#pragma unroll
+                for (int q = 0; q < NB; ++q)
+                    dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), bo.off[q], so, dst0 + BM * kRow + q * NT * 16);
+            }
         } else {
 #pragma unroll
             for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_a2x : rs_a2, a2o.off[q], 0u, dst0 + q * NT * 16);
@@ -692,7 +758,16 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) af[slot][i] = *reinterpret_cast<const bf16x8*>(frag(As, wm0 + 32 * i + r, kc));
 #pragma unroll
-            for (int j = 0; j < FN; ++j) bfr[slot][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (KN) {
+                    const int nb = wn0 + 32 * j;
+                    const char* sub = Bs + (nb >> 6) * (64 * kRow);
+                    const int nl = (nb & 63) + 16 * ((lane >> 4) & 1), kb = 16 * ks + 8 * g;
+                    bfr[slot][j] = cat44(ld_tr(sub, kb, nl, lane), ld_tr(sub, kb + 4, nl, lane));
+                } else {
+                    bfr[slot][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
+                }
+            }
         };
         auto mma = [&](int slot) {
 #pragma unroll
@@ -781,7 +856,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     epilogue_elem(p, m, n, s);
 }
 
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4>
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
@@ -811,6 +886,12 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         p.a_bytes = extent(p.M, p.lda);
         p.ax_bytes = p.Mx > 0 ? extent(p.Mx, p.ldax) : 0u;
         p.b_bytes = extent(p.N, p.ldb);
+        if (KN) {   // [K][ldb]: the whole matrix (the kernel addresses it through the descriptor only)
+            const int64_t b = p.K * p.ldb * eb;
+            p.b_bytes = b < ((int64_t)1 << 32) ? (uint32_t)b : 0u;
+            SA3K_REQUIRE(p.b_bytes != 0 && p.a_bytes != 0 && (p.Mx == 0 || p.ax_bytes != 0),
+                         "a [K][N] B operand needs buffer-addressable operands");
+        }
         p.bx_bytes = p.Nx > 0 ? extent(p.Nx, p.ldbx) : 0u;
         // the staged epilogue stores 4 columns at once: rows and vectors must be 16-byte (f32) /
         // 8-byte (bf16) aligned
@@ -831,9 +912,10 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         // profiled per kernel instantiation, with its algorithmic flops (padding excluded)
         static const std::string name = std::string("gemm_dma<") + std::to_string(BM) + "," + std::to_string(BN) + "," +
                                         std::to_string(WMW) + "," + std::to_string(STAGES) +
-                                        (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (BF16 ? ",bf16>" : ",f32>");
+                                        (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (KN ? ",kn" : "") +
+                                        (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW>, g,
+        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN>, g,
                  dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
@@ -853,6 +935,7 @@ bool big_ok(const sa3k_ctx* ctx, const DmaParams& p) {
     const int64_t lim = (int64_t)1 << 31;
     if (ctx->gemm_fixup != 0 || p.prescale) return false;
     if (extent(p.M, p.lda, p.K) >= lim || extent(p.N, p.ldb, p.K) >= lim) return false;
+    if (p.b_kn && p.K * p.ldb * 2 >= lim) return false;
     if (p.Nx > 0 && (p.N % 8 != 0 || extent(p.Nx, p.ldbx, p.K) >= lim)) return false;
     if (p.Mx > 0 && (p.M % 8 != 0 || extent(p.Mx, p.ldax, p.K) >= lim)) return false;
     if (p.K2 > 0 && (extent(p.M, p.lda2, p.K2) >= lim || extent(p.N, p.ldb2, p.K2) >= lim ||
@@ -891,12 +974,15 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     p.ax_bytes = extent(p.Mx, p.ldax);
     p.b_bytes = extent(p.N, p.ldb);
     p.bx_bytes = extent(p.Nx, p.ldbx);
+    if (p.b_kn) p.b_bytes = (uint32_t)(p.K * p.ldb * 2);   // the whole [K][ldb] operand (big_ok: < 2 GiB)
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
     if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
     {
-        KernelScope ks(ctx, "gemm_big<256,256,bf16>", 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        launch_k(ctx, splits == 1, gemm_big_kernel, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
+        KernelScope ks(ctx, p.b_kn ? "gemm_big<256,256,kn,bf16>" : "gemm_big<256,256,bf16>",
+                       2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
+        if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true>, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
+        else launch_k(ctx, splits == 1, gemm_big_kernel<false>, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1) {
@@ -908,9 +994,27 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     }
 }
 
+// [K][N] B operands (bf16): the tiles of the default dispatch that have whole 64-column sub-tiles
+void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
+    const int64_t Mt = p.M + p.Mx;
+    if (ctx->gemm_big != 0 && Mt > 32 && p.N > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
+        const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.N, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+        const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
+        const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
+        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return launch_big(ctx, p);
+    }
+    if (Mt <= 32) return launch_dma<32, 128, 1, 4, true, 4, true>(ctx, p);
+    if (p.N <= 64) return launch_dma<128, 64, 4, 4, true, 4, true>(ctx, p);
+    const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
+    if (tiles128 < 384 && p.K < 4096 && ctx->gemm_small == 2) return launch_dma<64, 128, 1, 3, true, 4, true>(ctx, p);
+    if (ctx->gemm_cfg == 1) return launch_dma<128, 128, 2, 2, true, 4, true>(ctx, p);
+    return launch_dma<128, 256, 2, 3, true, 8, true>(ctx, p);
+}
+
 template <bool BF16>
 void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if constexpr (BF16) {
+        if (p.b_kn) return dispatch_dma_kn(ctx, p);
         if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.Nt > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
             // 256 x 256 tiles (one per CU) where they fill the chip about as evenly as 128 x 128 tiles
             // (two per CU) do and need no split over K; measured on MI355X at 2176 rows: FFN
@@ -998,6 +1102,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.alpha_x = d.alpha_x;
     p.Cbn = d.Cbn; p.ldcn = d.ldcn;
     p.bx_bytes = 0;
+    p.b_kn = d.b_kn;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kSkThreads) void skinny_nt_kernel(SkinnyParams p) {
 }  // namespace
 
 bool gemm_skinny_ok(const sa3k_ctx* ctx, const GemmDesc& d) {
-    if (d.prescale || d.Nx > 0) return false;
+    if (d.prescale || d.Nx > 0 || d.b_kn) return false;
     if (!ctx->gemm_skinny) return false;
     if (d.prec != SA3K_PREC_BF16 || d.a_src != SRC_BF16 || d.b_src != SRC_BF16) return false;
     if (d.N > 2 * kSkCols || d.K2 != 0 || d.K % 64 != 0 || d.K == 0) return false;

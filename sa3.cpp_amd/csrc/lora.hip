@@ -921,7 +921,8 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     if (!merged) sdub();
     // merged: sdUB = s dU B as r extra output columns of the dX GEMM (B rows from B^T) when they cost
     // it no extra round of workgroups; the dA partials then follow that GEMM
-    const bool sdub_cols = merged && dX && (ctx->rank_cols & 2) && gemm_extra_cols_free(ctx, N + (L->dora ? r : 0), in, out, r);
+    const bool sdub_cols = merged && dX && L->Wmt && (ctx->rank_cols & 2) &&
+                           gemm_extra_cols_free(ctx, N + (L->dora ? r : 0), in, out, r);
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
     //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
@@ -975,11 +976,13 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     // the B operand: W^T (stored layout or working copy) with the rank term as a second segment, or
     // W_eff^T when merged
     WOp wt = weight_operand(W, bf, true);
-    if (merged) wt = WOp{SRC_BF16, L->Wmt, nullptr, out, 0};
+    // merged: W_eff^T, or W_eff itself read as a [K][N] operand when there is no transposed copy
+    const int kn = merged && !L->Wmt ? 1 : 0;
+    if (merged) wt = kn ? WOp{SRC_BF16, L->Wm, nullptr, in, 0} : WOp{SRC_BF16, L->Wmt, nullptr, out, 0};
     if (dX) {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
-        g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
+        g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds; g.b_kn = kn;
         if (!merged) { g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
         if (sdub_cols) { g.Nx = r; g.Bx = L->Bt; g.ldbx = out; g.alpha_x = L->s; g.Cbn = static_cast<bf16*>(L->sdUB); g.ldcn = r; }
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
@@ -993,7 +996,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     } else if (L->dora) {
         GemmDesc g;
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
-        g.A = L->Ax; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
+        g.A = L->Ax; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds; g.b_kn = kn;
         if (!merged) { g.A2 = L->A2x; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
         g.M = r; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dA; g.ldc = in; g.accumulate = 1;
@@ -1403,7 +1406,7 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
                 et[row][col] = e;
                 if (dora) nacc[v] += (double)sd * (2.0 * (double)w + (double)sd);
             }
-            *reinterpret_cast<uint2*>(&ett[16 * j + l16][16 * wave + 4 * g]) = __builtin_bit_cast(uint2, e4);
+            if (q.Wmt) *reinterpret_cast<uint2*>(&ett[16 * j + l16][16 * wave + 4 * g]) = __builtin_bit_cast(uint2, e4);
         }
         __syncthreads();   // et, ett staged
         if (dora) {   // P += W_eff A^T over the chunk (rows 16 wave + l16 of W_eff as the A operand)
@@ -1428,8 +1431,10 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
             const uint32_t to = o0 + lc < out ? (uint32_t)(((i0 + lr) * out + o0 + lc) * 2) : 0xFFFFFFE0u;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, fr[0]), rs_m, fo, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, fr[1]), rs_m, fo + 16, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[0]), rs_mt, to, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[1]), rs_mt, to + 16, 0, 0);
+            if (q.Wmt) {
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[0]), rs_mt, to, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4g, tr[1]), rs_mt, to + 16, 0, 0);
+            }
         }
     }
     if (!dora) return;
@@ -1532,8 +1537,14 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
             q.Wsrc = L->W->w; q.Wsc = L->W->ws; q.wtype = L->W->type;
             q.Wm = q.Wmt = nullptr;
             if (g->merged) {
+                // the dX product reads W_eff as it lies ([out][in] as a [K][N] operand) unless the
+                // transposed copy is asked for (option merge_kn 0)
                 if (!L->Wm) L->Wm = dev_alloc<bf16>(in * out);
-                if (!L->Wmt) L->Wmt = dev_alloc<bf16>(in * out);
+                if (!ctx->merge_kn && !L->Wmt) L->Wmt = dev_alloc<bf16>(in * out);
+                if (ctx->merge_kn && L->Wmt) {
+                    SA3K_HIP(hipFree(L->Wmt));
+                    L->Wmt = nullptr;
+                }
                 q.Wm = static_cast<bf16*>(L->Wm);
                 q.Wmt = static_cast<bf16*>(L->Wmt);
             }

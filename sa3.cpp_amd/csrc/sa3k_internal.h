@@ -48,6 +48,7 @@ struct sa3k_ctx {
     int late_join = 1;                     // a DiT block's last second-stream work may overlap the next block
     int lin_merge = 1;                     // bf16 adapted linears contract W + s B A, refreshed per prepare
     int rank_cols = 1;                     // merged: s X A^T (1) / s dU B (2) as extra GEMM output columns
+    int merge_kn = 1;                      // merged: dX reads W_eff [out][in] as a [K][N] operand (no W_eff^T copy)
     hipEvent_t block_tail_ev = nullptr;    // second-stream work of a block backward left running (late_join)
     bool block_tail_pending = false;       // block_tail_ev holds a record not yet waited for
     hipEvent_t tail_ev = nullptr;          // fork event armed for the producer about to launch (fork_arm)

@@ -224,20 +224,51 @@ def test_rank_products_as_extra_columns(ctx, cols):
     """Merged DoRA linear with s X A^T (bit 0) and s dU B (bit 1) as extra output columns of the
     forward / dX products (option rank_cols), at the DiT's 2176-token shape (the 256 x 256, 128 x 256
     and split-K tilings all carry them) and a ragged one: within the bf16 bar of the oracle, and
-    within bf16 rounding of the separate products."""
+    within bf16 rounding of the separate products. The dX product's columns need the transposed
+    merged copy, so these runs keep it (merge_kn 0)."""
     for N, in_, out_, r in ((2176, 1536, 6144, 32), (2176, 6144, 1536, 32), (120, 192, 320, 16)):
         X, dY, W, A, B = make_inputs(21, N, in_, out_, r)
         Wh = W.astype(np.float16)
         Wdec = Wh.astype(np.float32)
         mag = (oracle.row_norms(Wdec) * 1.02).astype(np.float32)
         try:
+            ctx.set_option("merge_kn", 0)
             ctx.set_option("rank_cols", cols)
             got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
             ctx.set_option("rank_cols", 0)
             sep = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
         finally:
             ctx.set_option("rank_cols", 1)
+            ctx.set_option("merge_kn", 1)
         ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, (N, k)
             assert rel_err(got[k], sep[k]) < 1e-4, (N, k)
+
+
+@pytest.mark.parametrize("big", [0, 1, 2])
+def test_dx_k_major_operand(ctx, big):
+    """Merged linears' dX product reads W + s B A in its stored [out][in] layout as a K-major B
+    operand (option merge_kn 1, transposed through the LDS reads) instead of a transposed copy
+    (merge_kn 0): the same f32 sums over the same K tiles, on every tile family (gemm_big 0/1/2:
+    never, by shape, always 256 x 256), at the DiT's shapes and small ones whose tiles reach past
+    the last column (those sub-tiles read a clamped valid column and are never stored)."""
+    for N, in_, out_, r in ((2176, 1536, 6144, 32), (2176, 6144, 1536, 32), (120, 192, 320, 16),
+                            (264, 192, 320, 8)):
+        X, dY, W, A, B = make_inputs(31, N, in_, out_, r)
+        Wh = W.astype(np.float16)
+        Wdec = Wh.astype(np.float32)
+        mag = (oracle.row_norms(Wdec) * 0.97).astype(np.float32)
+        try:
+            ctx.set_option("gemm_big", big)
+            ctx.set_option("merge_kn", 1)
+            kn = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
+            ctx.set_option("merge_kn", 0)
+            nk = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
+        finally:
+            ctx.set_option("merge_kn", 1)
+            ctx.set_option("gemm_big", 1)
+        ref = run_oracle(X, dY, Wdec, A, B, 1.25, True, mag)
+        for k in ("Y", "dX", "dA", "dB", "dm"):
+            assert rel_err(kn[k], ref[k]) < 2e-2 and cosine(kn[k], ref[k]) >= 0.9999, (N, k)
+            assert rel_err(kn[k], nk[k]) < 1e-5, (N, k)
