@@ -102,8 +102,8 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 from the grid (clamped to the number of K tiles; default 0: chosen)
  *   "side_stream" 1: independent kernels of a backward pass (column reductions, attention dQ, the
  *                 context K/V projection) run on a second stream of the context beside the main
- *                 one, joined before the call returns (default 1; off while gemm_fixup is not 0
- *                 or a profiler scope is open)
+ *                 one, joined before the call returns (default 1; off while a profiler scope is
+ *                 open)
  *   "fork_tail"   1: the second stream waits on the completion event of the kernel that produces
  *                 its inputs (recorded by that kernel's launch) rather than on a separate event
  *                 record on the main stream (default 1)
@@ -121,6 +121,11 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 extra output columns where they cost it no extra round of workgroups (default 1);
  *                 bit 1: likewise s dU B on its dX product (default 0: measured slower on MI355X
  *                 than the separate product beside it; needs merge_kn 0)
+ *   "tn_fuse"     bit mask of split reductions summed by their own last split to arrive instead of
+ *                 a separate launch (each stream has its own arrival counters): 1 the block's
+ *                 modulation-gradient column sums, 2 an adapted linear's dA sums, 4 an adapted
+ *                 linear's dU column reduction with its per-row step (dm, dB, the dA rows operand)
+ *                 (default 5)
  *   "merge_kn"    1: a merged linear's dX product reads W + s B A in its stored [out][in] layout as
  *                 a K-major operand (transposed by the LDS reads), so the refresh writes one bf16
  *                 copy; 0: the refresh also writes the transposed copy [in][out] and dX reads

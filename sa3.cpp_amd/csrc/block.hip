@@ -270,14 +270,15 @@ __global__ __launch_bounds__(kThreads) void colred_kernel(int mode, const float*
     __shared__ int s_last;
     if (!arrive_last(&counters[blockIdx.z * gridDim.x + blockIdx.x], nch, &s_last)) return;
     if (ok) {
-        float s0 = 0.f, s1 = 0.f;
-        for (int k = 0; k < nch; ++k) {
-            const float* o = part + (((int64_t)b * nch + k) * 2) * dim;
-            s0 += ld_coherent(o + c);
-            s1 += ld_coherent(o + dim + c);
-        }
-        dssg[((int64_t)b * 6 + part0) * dim + c] += s0;
-        if (mode == 0) dssg[((int64_t)b * 6 + part0 + 1) * dim + c] += s1;
+        // chunk sums in chunk order (as colred_sum_kernel adds them)
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            part, (short)0, (int)((int64_t)gridDim.z * nch * 2 * dim * 4), 0x00020000);
+        const uint32_t base = (uint32_t)(((int64_t)b * nch * 2 * dim + c) * 4);
+        const uint32_t off[2] = {base, base + (uint32_t)dim * 4u};
+        float sum[2];
+        coherent_split_sums(rp, off, (uint32_t)(2 * dim * 4), nch, sum);
+        dssg[((int64_t)b * 6 + part0) * dim + c] += sum[0];
+        if (mode == 0) dssg[((int64_t)b * 6 + part0 + 1) * dim + c] += sum[1];
     }
 }
 
@@ -538,7 +539,7 @@ void colred(sa3k_ctx* ctx, sa3k_block_ws* w, int mode, const float* a, const flo
     OnSide os(ctx, side);
     const int chunk = (int)ceil_div(w->S, w->part_chunks);
     const int64_t ctrs = nblk(w->dim) * (int64_t)w->B;
-    int* counters = use_fixup(ctx, (int64_t)w->B * w->dim, ctrs) ? ctx->tile_counters : nullptr;
+    int* counters = tn_counters(ctx, ctrs, kFuseColred);
     launch(ctx, "blk_colred", colred_kernel, dim3(nblk(w->dim), (unsigned)w->part_chunks, (unsigned)w->B), mode, a, x,
            rstd, gamma, (const float*)w->modv, g_part, w->S, w->dim, chunk, w->part, part0, w->dssg, counters);
     if (!counters)

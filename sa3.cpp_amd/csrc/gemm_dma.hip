@@ -905,7 +905,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     }
     if (splits > 1) {
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
-        if (use_fixup(ctx, (p.M + p.Mx) * p.Nt, tiles)) p.counters = ctx->tile_counters;
+        if (use_fixup(ctx, (p.M + p.Mx) * p.Nt, tiles)) p.counters = stream_counters(ctx);
     }
     dim3 g((unsigned)grid, (unsigned)splits);
     {

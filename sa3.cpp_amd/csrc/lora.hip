@@ -351,12 +351,23 @@ __device__ __forceinline__ bf16x8 cat44(tn_bf16x4 a, tn_bf16x4 b) {
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// The per-output-row step that follows the dY column reduction of an adapted linear (the rows
+// kernel's formulas, dora_bwd_rows_kernel below), run by the reduction's last split to arrive when
+// dB is set.
+struct RowsArgs {
+    const float *nsq, *mag, *Pt, *BG, *B;
+    float s;
+    int dora;
+    float *dB, *dm, *gn;
+    bf16* Ax;
+};
+
 template <int MODE, class QT>
 __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restrict__ Q, const bf16* __restrict__ P, int r,
                                                              const bf16* __restrict__ U, const float* __restrict__ d,
                                                              bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
                                                              int64_t cols, int64_t rows_per, float* __restrict__ out,
-                                                             int accumulate, int* __restrict__ counters) {
+                                                             int accumulate, int* __restrict__ counters, RowsArgs rows) {
     __shared__ __attribute__((aligned(16))) char qt[2][TN_STEP * TN_QLD];
     __shared__ __attribute__((aligned(16))) char pt[2][TN_STEP * TN_PLD];
     __shared__ float red[TN_ROWS][TN_COLS + 1];
@@ -490,27 +501,42 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
         mma(1);
         load(n0 + 3 * TN_STEP, rb);
     }
-    // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + lane%16
+    // D[i][j]: i = column 4g + v of this wave's 16, j = rank t*16 + lane%16. The tile goes through
+    // LDS (the Q staging buffer, free after the loop) so that every thread stores a whole 16-byte run
+    // of a partial row: each 64-byte segment is written once and whole, which the device-coherent
+    // (write-through) stores of the in-kernel reduction need to stay cheap.
     constexpr int RS = kGd ? 33 : 32;
     const int row0 = kGd ? 1 : 0;
     const int r16 = lane & 15;
+    constexpr int TP = TN_COLS + 4;   // LDS tile pitch in floats (16-byte aligned rows)
+    static_assert(32 * TP * 4 <= TN_STEP * TN_QLD, "partial tile does not fit the Q staging buffer");
+    float* tile = reinterpret_cast<float*>(qt[0]);
+    const __amdgpu_buffer_rsrc_t rpart = __builtin_amdgcn_make_buffer_rsrc(
+        part, (short)0, (int)((int64_t)gridDim.y * RS * cols * 4), 0x00020000);
+    __syncthreads();   // every wave is done with the Q tiles
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int a = t * 16 + r16;
-        if (a >= r) continue;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int64_t c = c0 + wave * 16 + 4 * g + v;
-            if (c >= cols) continue;
-            float* dst = part + ((int64_t)z * RS + row0 + a) * cols + c;
-            if (counters) st_coherent(dst, acc[t][v]);   // read by the last split in this launch
-            else *dst = acc[t][v];
-        }
-    }
-    if constexpr (kGd) {   // gd: sum the 32 token-row slots of each column
+        for (int v = 0; v < 4; ++v) tile[(t * 16 + r16) * TP + wave * 16 + 4 * g + v] = acc[t][v];
+    if constexpr (kGd) {   // gd: the 32 token-row slots of each column
 #pragma unroll
         for (int j = 0; j < 8; ++j) red[lrow][c8 + j] = gd[j];
-        __syncthreads();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {   // 16 threads per rank row, 4 columns each
+        const int a = h * 16 + tid / 16, cc = (tid % 16) * 4;
+        const int64_t c = c0 + cc;
+        if (a < r && c < cols) {
+            const float4 v = *reinterpret_cast<const float4*>(tile + a * TP + cc);
+            const int64_t e = ((int64_t)z * RS + row0 + a) * cols + c;
+            if (counters)   // read by the last split in this launch
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(tn_v4u, v), rpart, (uint32_t)(e * 4), 0, kSc1);
+            else
+                *reinterpret_cast<float4*>(part + e) = v;
+        }
+    }
+    if constexpr (kGd) {
         if (tid < TN_COLS) {
             float s = 0.f;
             for (int k = 0; k < TN_ROWS; ++k) s += red[k][tid];
@@ -524,19 +550,89 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     }
     if (!counters) return;   // reduced by the consumer (rows kernel) or sum_splits_kernel
     // The last split of this column tile to arrive sums the partials in split order
-    // (deterministic) into out[row][c] (= or +=); nobody waits for anybody.
+    // (deterministic) into out[row][c] (= or +=), or runs the rows step on them; nobody waits for
+    // anybody.
     __shared__ int s_last;
+    const uint32_t zstride = (uint32_t)(RS * cols * 4);
+    if constexpr (kGd) {
+        if (rows.dB) {
+            // thread (column c0 + tid % 64, ranks tid / 64 + 4 i): the rows kernel's sums (split
+            // order, from zero) and formulas, so the results are the same bit for bit. Its inputs
+            // are loaded before the arrival (every split), so the last one's tail waits only for
+            // the partial sums; every thread sums its column's gd itself (no barrier).
+            constexpr int NG = kThreads / TN_COLS, NR = 32 / NG;
+            const int cl = tid & (TN_COLS - 1), ag = tid / TN_COLS;
+            const int64_t o = c0 + cl;
+            const bool ok = o < cols;
+            const int64_t oc = ok ? o : 0;
+            const float n2 = rows.dora ? rows.nsq[oc] : 1.f, mg = rows.dora ? rows.mag[oc] : 0.f;
+            float pt[NR], bb[NR], bg[NR], db[NR];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const int a = min(ag + NG * i, r - 1);
+                pt[i] = rows.dora ? rows.Pt[(int64_t)a * cols + oc] : 0.f;
+                bb[i] = rows.dora ? rows.B[oc * r + a] : 0.f;
+                bg[i] = rows.dora && rows.BG ? rows.BG[oc * r + a] : 0.f;
+                db[i] = rows.dB[oc * r + a];
+            }
+            if (!arrive_last(&counters[blockIdx.x], (int)gridDim.y, &s_last)) return;
+            const int splits = (int)gridDim.y;
+            uint32_t off[NR + 1];
+            float sum[NR + 1];
+            off[0] = ok ? (uint32_t)(o * 4) : kOut;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const int a = ag + NG * i;
+                off[1 + i] = ok && a < r ? (uint32_t)(((int64_t)(a + 1) * cols + o) * 4) : kOut;
+            }
+            coherent_split_sums(rpart, off, zstride, splits, sum);
+            if (!ok) return;
+            float gn = 0.f;
+            if (rows.dora) {
+                const float gs = sum[0];
+                const float sq = sqrtf(n2);
+                gn = -0.5f * gs * mg / (n2 * sq);
+                if (ag == 0) {
+                    if (rows.dm) rows.dm[o] += gs / sq;
+                    rows.gn[o] = gn;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const int a = ag + NG * i;
+                if (a >= r) break;
+                float v = sum[1 + i];
+                if (rows.dora) {
+                    v += 2.0f * rows.s * gn * pt[i];
+                    if (rows.BG) v += 2.0f * rows.s * rows.s * gn * bg[i];
+                    rows.Ax[(int64_t)a * cols + o] = (bf16)(2.0f * rows.s * bb[i] * gn);
+                }
+                rows.dB[o * r + a] = db[i] + v;
+            }
+            return;
+        }
+    }
     if (!arrive_last(&counters[blockIdx.x], (int)gridDim.y, &s_last)) return;
-    const int nrows = kGd ? r + 1 : r;
     const int splits = (int)gridDim.y;
-    for (int e = tid; e < nrows * TN_COLS; e += kThreads) {
-        const int row = e / TN_COLS;
+    // element e = tid + kThreads k of the (rows x 64) tile: row e / 64, column c0 + e % 64
+    constexpr int NE = (RS * TN_COLS + kThreads - 1) / kThreads;
+    const int nrows = kGd ? r + 1 : r;
+    uint32_t off[NE];
+    float sum[NE];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int e = tid + kThreads * k, row = e / TN_COLS;
         const int64_t c = c0 + (e % TN_COLS);
-        if (c >= cols) continue;
-        float s = 0.f;
-        for (int zz = 0; zz < splits; ++zz) s += ld_coherent(part + ((int64_t)zz * RS + row) * cols + c);
+        off[k] = row < nrows && c < cols ? (uint32_t)(((int64_t)row * cols + c) * 4) : kOut;
+    }
+    coherent_split_sums(rpart, off, zstride, splits, sum);
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int e = tid + kThreads * k, row = e / TN_COLS;
+        const int64_t c = c0 + (e % TN_COLS);
+        if (row >= nrows || c >= cols) continue;
         float* o = out + (int64_t)row * cols + c;
-        *o = accumulate ? *o + s : s;
+        *o = accumulate ? *o + sum[k] : sum[k];
     }
 }
 
@@ -553,10 +649,12 @@ int64_t ctx_tn_wgs() {
 // workgroups of 64 columns, up to 3 resident per CU (160 VGPRs, 37 KiB of LDS). Two of them on one
 // CU overlap each other's memory latency; more share the CU's throughput. So a CU holding w of
 // them takes about rows x max(1, w / 2) token rows of streaming time (8 bytes per element: dY or X,
-// U, the dU store), and the rows kernel then reads splits x 33 x cols partial sums spread over the
-// chip. The split count minimising that cost is taken; it keeps the busiest CU's load close to
-// the average (576 workgroups over 256 CUs put 3 on some CUs and 2 on the rest).
-int64_t tn_rows_per(int64_t cols, int64_t N) {
+// U, the dU store), and then each column tile's last split to arrive reads splits x rs x 64 partial
+// sums (rs rows of partials) at about a CU's streaming rate (environment SA3K_TN_RED scales that
+// term, for measurement). The split count minimising the sum is taken; it keeps the busiest CU's
+// load close to the average (576 workgroups over 256 CUs put 3 on some CUs and 2 on the rest). The
+// same count serves the separate reduce launches (option tn_fuse 0), so both give the same sums.
+int64_t tn_rows_per(int64_t cols, int64_t N, int rs) {
     const int64_t tiles = ceil_div(cols, TN_COLS);
     if (const int64_t w = ctx_tn_wgs())
         return std::max<int64_t>(TN_STEP, ceil_div(ceil_div(N * tiles, w), TN_STEP) * TN_STEP);
@@ -569,8 +667,12 @@ int64_t tn_rows_per(int64_t cols, int64_t N) {
         const int64_t wgs = tiles * splits;
         if (ceil_div(wgs, kCUs) > 3 && S > 1) break;   // more than 3 resident per CU: no gain
         const double w = (double)ceil_div(wgs, kCUs);
-        const double cost = std::max(1.0, w / 2.0) * (double)rows * TN_COLS * 8.0 +
-                            (double)splits * 33.0 * (double)cols * 4.0 / (double)kCUs;
+        static const double red_scale = [] {
+            const char* e = std::getenv("SA3K_TN_RED");
+            return e ? std::atof(e) : 1.0;
+        }();
+        const double red = red_scale * (double)splits * rs * TN_COLS * 4.0;
+        const double cost = std::max(1.0, w / 2.0) * (double)rows * TN_COLS * 8.0 + red;
         if (cost < best - 1e-9) {
             best = cost;
             best_rows = rows;
@@ -819,6 +921,23 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dx"));
         return;
     }
+    const bool merged = L->merged && sizeof(CT) == 2;
+    const bool side = side_usable(ctx);
+    // the dA column reduction X^T sdUB: its split partials summed by its own last split to arrive
+    // (option tn_fuse, or gemm_fixup) or by a separate launch
+    int64_t x_rows_per = 0;
+    int x_S = 0;
+    bool x_fused = false;
+    if constexpr (sizeof(CT) == 2) {
+        const int64_t x_tiles = ceil_div(in, TN_COLS);
+        x_fused = tn_counters(ctx, x_tiles, kFuseXSum) != nullptr || use_fixup(ctx, (int64_t)32 * in, x_tiles);
+        x_rows_per = tn_rows_per(in, N, 32);
+        x_S = (int)ceil_div(N, x_rows_per);
+    } else {
+        x_S = choose_splits(in, N);
+        x_rows_per = ceil_div(N, x_S);
+    }
+    bool rows_fused = false;   // the rows step runs in the column reduction's last split
     // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens); the split partials rp[rS][rows][out]
     const float* rp = nullptr;
     int rS = 1;
@@ -828,22 +947,32 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         // look-ahead past the last token row)
         SA3K_REQUIRE((N + 4 * TN_STEP) * std::max(in, out) * 4 < ((int64_t)1 << 32),
                      "tokens x features too large for one adapted-linear backward");
-        const int64_t rows_per = tn_rows_per(out, N);
+        // tn_fuse: the reduction's last split per column tile runs the rows step itself; else
+        // (gemm_fixup) it sums the partials into L->red for the rows kernel, or that kernel sums them
+        int* counters = tn_counters(ctx, ceil_div(out, TN_COLS), kFuseRows);
+        rows_fused = counters != nullptr;
+        if (!counters && use_fixup(ctx, (int64_t)33 * out, ceil_div(out, TN_COLS))) counters = stream_counters(ctx);
+        const int64_t rows_per = tn_rows_per(out, N, 33);
         const int S = (int)ceil_div(N, rows_per);
         float* part = reduce_workspace(ctx, (size_t)S * 33 * out * sizeof(float));
-        int* counters = use_fixup(ctx, (int64_t)33 * out, ceil_div(out, TN_COLS)) ? ctx->tile_counters : nullptr;
+        RowsArgs ra{};
+        if (rows_fused)
+            ra = RowsArgs{L->nsq, L->mag, L->Pt, L->merged ? nullptr : L->BG, L->B, L->s, L->dora, dB, dm, L->gn,
+                          static_cast<bf16*>(L->Ax)};
+        if (rows_fused && side && L->merged) fork_arm(ctx);   // recorded by this kernel: dU and Ax ready
         {
             KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_dy"), 2.0 * N * out * r);
             const dim3 grid((unsigned)ceil_div(out, TN_COLS), (unsigned)S);
             if (du_ready)
-                skinny_tn_kernel<TN_DU, bf16><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const bf16*>(L->dU), static_cast<const bf16*>(L->Hc), r,
-                    static_cast<const bf16*>(L->dora ? L->U : nullptr), L->dora ? L->d : nullptr, nullptr, part, N,
-                    out, rows_per, L->red, 0, counters);
+                launch_k(ctx, true, skinny_tn_kernel<TN_DU, bf16>, grid, dim3(kThreads), 0,
+                         static_cast<const bf16*>(L->dU), static_cast<const bf16*>(L->Hc), r,
+                         static_cast<const bf16*>(L->dora ? L->U : nullptr), (const float*)(L->dora ? L->d : nullptr),
+                         (bf16*)nullptr, part, N, out, rows_per, L->red, 0, counters, ra);
             else
-                skinny_tn_kernel<TN_DY, float><<<grid, kThreads, 0, ctx->stream>>>(
-                    dY, static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
-                    L->dora ? L->d : nullptr, static_cast<bf16*>(L->dU), part, N, out, rows_per, L->red, 0, counters);
+                launch_k(ctx, true, skinny_tn_kernel<TN_DY, float>, grid, dim3(kThreads), 0, dY,
+                         static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
+                         (const float*)(L->dora ? L->d : nullptr), static_cast<bf16*>(L->dU), part, N, out, rows_per,
+                         L->red, 0, counters, ra);
             SA3K_LAUNCHED();
         }
         // the rows kernel below sums the S partials (or, after the in-kernel reduction, reads the
@@ -865,24 +994,10 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         }
         rp = part; rS = S; rstride = (int64_t)(R + 1) * out;
     }
-    // merged: the rows kernel's outputs (Ax) are the last inputs of the dX GEMM, and sdUB with its
+    // merged: the rows step's outputs (Ax) are the last inputs of the dX GEMM, and sdUB with its
     // column reduction only feeds dA: they go to the second stream as soon as dU and Ax are ready
-    const bool merged = L->merged && sizeof(CT) == 2;
-    int64_t x_rows_per = 0;
-    int x_S = 0;
-    int* x_counters = nullptr;
-    if constexpr (sizeof(CT) == 2) {
-        x_rows_per = tn_rows_per(in, N);
-        x_S = (int)ceil_div(N, x_rows_per);
-        x_counters = use_fixup(ctx, (int64_t)32 * in, ceil_div(in, TN_COLS)) ? ctx->tile_counters : nullptr;
-    } else {
-        x_S = choose_splits(in, N);
-        x_rows_per = ceil_div(N, x_S);
-    }
-    const bool early = x_counters == nullptr;
-    const bool side = early && side_usable(ctx);
-    if (side && merged) fork_arm(ctx);   // recorded by the rows kernel
-    {
+    if (!rows_fused) {
+        if (side && merged) fork_arm(ctx);   // recorded by the rows kernel
         KernelScope ks(ctx, scope(ctx, L, "lin_bwd_rows"));
         const dim3 grid((unsigned)ceil_div(out, 64), (unsigned)ceil_div(std::max(r, 1), 4));
         // merged: Pt holds W_eff A^T = P + s B G, so the B G term is already in it
@@ -925,21 +1040,28 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
                            gemm_extra_cols_free(ctx, N + (L->dora ? r : 0), in, out, r);
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
-    //     extra dA rows (step 3), keeping the accumulation order of dA fixed. With the in-kernel
-    //     reduction the partials kernel adds into dA itself and therefore runs after step 3.
+    //     extra dA rows (step 3), keeping the accumulation order of dA fixed. When the partials
+    //     kernel sums them into dA itself (x_fused), the whole kernel runs after step 3.
     auto x_partials = [&] {
         if constexpr (sizeof(CT) == 2) {
             x_part = reduce_workspace(ctx, (size_t)x_S * 32 * in * sizeof(float));
+            // the counters of the stream this runs on
+            int* xc = nullptr;
+            if (x_fused) {
+                xc = tn_counters(ctx, ceil_div(in, TN_COLS), kFuseXSum);
+                if (!xc) xc = stream_counters(ctx);
+                SA3K_REQUIRE(xc != nullptr, "in-kernel reduction on a stream without counters");
+            }
             const dim3 grid((unsigned)ceil_div(in, TN_COLS), (unsigned)x_S);
             KernelScope ks(ctx, scope(ctx, L, "lin_bwd_colred_x"), 2.0 * N * in * r);
             if (x_src == SRC_F32)
-                skinny_tn_kernel<TN_X, float><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const float*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr,
-                    x_part, N, in, x_rows_per, dA, 1, x_counters);
+                launch_k(ctx, true, skinny_tn_kernel<TN_X, float>, grid, dim3(kThreads), 0, static_cast<const float*>(X),
+                         static_cast<const bf16*>(L->sdUB), r, (const bf16*)nullptr, (const float*)nullptr,
+                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{});
             else
-                skinny_tn_kernel<TN_X, bf16><<<grid, kThreads, 0, ctx->stream>>>(
-                    static_cast<const bf16*>(X), static_cast<const bf16*>(L->sdUB), r, nullptr, nullptr, nullptr,
-                    x_part, N, in, x_rows_per, dA, 1, x_counters);
+                launch_k(ctx, true, skinny_tn_kernel<TN_X, bf16>, grid, dim3(kThreads), 0, static_cast<const bf16*>(X),
+                         static_cast<const bf16*>(L->sdUB), r, (const bf16*)nullptr, (const float*)nullptr,
+                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{});
             SA3K_LAUNCHED();
         } else {
             x_part = reduce_workspace(ctx, (size_t)x_S * R * in * sizeof(float));
@@ -955,19 +1077,21 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         }
     };
     auto x_sum = [&] {
-        if (x_counters) return;   // summed in-kernel
+        if (x_fused) return;   // summed in-kernel
         KernelScope ks(ctx, scope(ctx, L, "lin_bwd_reduce"));
         const int64_t stride = (sizeof(CT) == 2 ? (int64_t)32 : (int64_t)R) * in;
         sum_splits_kernel<<<(unsigned)ceil_div((int64_t)r * in, kThreads), kThreads, 0, ctx->stream>>>(
             x_part, stride, x_S, (int64_t)r * in, dA, 1);
         SA3K_LAUNCHED();
     };
-    if (early && !sdub_cols) {
+    if (!x_fused && !sdub_cols) {
         if (side) fork_fire(ctx);   // sdUB (merged: dU) and X are ready
         OnSide os(ctx, side);
         if (merged) sdub();
         x_partials();
     } else if (merged && !sdub_cols) {
+        if (side) fork_fire(ctx);   // dU is ready
+        OnSide os(ctx, side);
         sdub();
     }
     // 3. dX = dU W + sdUB A ; dora: dA += 2s B^T diag(gn) W + 2s^2 (B^T gn B) A as r extra rows
@@ -1003,17 +1127,13 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dora_da"));
     }
     // 4b. the partial sums into dA, after step 3
-    if (early) {
-        if (side) fork_fire(ctx);   // the dX GEMM has added its dA rows (and written sdUB)
-        {
-            OnSide os(ctx, side);
-            if (sdub_cols) x_partials();
-            x_sum();
-        }
-        if (side) side_join_unless_deferred(ctx);
-    } else {
-        x_partials();
+    if (side) fork_fire(ctx);   // the dX GEMM has added its dA rows (and written sdUB)
+    {
+        OnSide os(ctx, side);
+        if (x_fused || sdub_cols) x_partials();
+        x_sum();
     }
+    if (side) side_join_unless_deferred(ctx);
 }
 
 // ---------------------------------------------------------------- grouped adapter refresh

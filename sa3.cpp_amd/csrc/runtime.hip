@@ -78,6 +78,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_LIN_MERGE")) ctx->lin_merge = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_RANK_COLS")) ctx->rank_cols = std::atoi(e);
         if (const char* e = std::getenv("SA3K_MERGE_KN")) ctx->merge_kn = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_TN_FUSE")) ctx->tn_fuse = std::atoi(e);
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
@@ -93,9 +94,11 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
         sa3k_note_main(ctx);
-        SA3K_HIP(hipMalloc(&ctx->tile_counters, sizeof(int) * kMaxFixupTiles));
-        SA3K_HIP(hipMemsetAsync(ctx->tile_counters, 0, sizeof(int) * kMaxFixupTiles, ctx->stream));
-        sa3k_note_main(ctx);
+        for (int** c : {&ctx->tile_counters, &ctx->tile_counters_side}) {
+            SA3K_HIP(hipMalloc(c, sizeof(int) * kMaxFixupTiles));
+            SA3K_HIP(hipMemsetAsync(*c, 0, sizeof(int) * kMaxFixupTiles, ctx->stream));
+            sa3k_note_main(ctx);
+        }
         SA3K_HIP(hipMalloc(&ctx->skinny_counters, sizeof(int) * 2 * kSkinnyMaxTiles));
         SA3K_HIP(hipMemsetAsync(ctx->skinny_counters, 0, sizeof(int) * 2 * kSkinnyMaxTiles, ctx->stream));
         sa3k_note_main(ctx);
@@ -132,6 +135,7 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->block_tail_ev) (void)hipEventDestroy(ctx->block_tail_ev);
     if (ctx->zero_page) (void)hipFree(ctx->zero_page);
     if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
+    if (ctx->tile_counters_side) (void)hipFree(ctx->tile_counters_side);
     if (ctx->skinny_counters) (void)hipFree(ctx->skinny_counters);
     for (const ProfRecord& r : ctx->prof_pending) {
         (void)hipEventDestroy(r.start);
@@ -235,6 +239,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "lin_merge") ctx->lin_merge = value != 0;
         else if (n == "rank_cols") ctx->rank_cols = value;
         else if (n == "merge_kn") ctx->merge_kn = value != 0;
+        else if (n == "tn_fuse") ctx->tn_fuse = value;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

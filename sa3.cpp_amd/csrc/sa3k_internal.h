@@ -32,6 +32,11 @@ constexpr int kSideEvents = 64;
 // row tiles (32 rows each) of one skinny-product launch that may split K over workgroups
 constexpr int kSkinnyMaxTiles = 8192;
 
+// option tn_fuse: which split reductions their own last split to arrive sums (instead of a
+// separate launch): the block's modulation-gradient column sums, the adapted linears' dA sums, and
+// the adapted linears' dU column reduction together with its per-row step
+constexpr int kFuseColred = 1, kFuseXSum = 2, kFuseRows = 4;
+
 struct sa3k_ctx {
     int device = 0;
     // The stream launches go to: the context's main stream, or, while side work is being enqueued
@@ -86,6 +91,8 @@ struct sa3k_ctx {
     int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch):
                                           // 0 never, 1 always, 2 for small outputs only
     int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
+    int* tile_counters_side = nullptr;    // the same for launches on the second stream
+    int tn_fuse = kFuseColred | kFuseRows; // split reductions summed in-kernel (bits kFuse*)
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
                                           // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
@@ -181,11 +188,11 @@ inline void sa3k_note_main(sa3k_ctx* c) {
 }
 
 // ---- a second stream for independent chains of work (e.g. a column reduction beside the GEMM
-// that does not need it). Used only while launches go to the main stream, outside profiling
-// (per-kernel timing stays serial) and without in-kernel split reductions (their tile counters are
-// shared). Every function that forks joins before it returns, so no side work outlives a call.
+// that does not need it). Used only while launches go to the main stream and outside profiling
+// (per-kernel timing stays serial). Every function that forks joins before it returns, so no side
+// work outlives a call.
 inline bool side_usable(const sa3k_ctx* c) {
-    return c->use_side && c->side_stream && !c->prof_on && c->gemm_fixup == 0 && c->stream == c->main_stream;
+    return c->use_side && c->side_stream && !c->prof_on && c->stream == c->main_stream;
 }
 inline hipEvent_t side_event(sa3k_ctx* c) {
     hipEvent_t e = c->side_ev[c->side_ev_i];
@@ -315,10 +322,24 @@ constexpr int kMaxFixupTiles = 8192;
 // partial loads of the last workgroup serialize; 2 stays selectable, 0 is the default.)
 constexpr int64_t kSmallFixupElems = (int64_t)1 << 18;
 
+// The arrival counters of in-kernel split reductions launched on the current stream: one array
+// per stream, so reductions on the two streams never share a counter (launches on one stream run
+// one after another, and the last arrival resets each counter). Null on any other stream.
+inline int* stream_counters(const sa3k_ctx* c) {
+    if (c->stream == c->main_stream) return c->tile_counters;
+    if (c->stream == c->side_stream) return c->tile_counters_side;
+    return nullptr;
+}
 // whether a split reduction over an output of `elems` floats is done by the last split to arrive
 inline bool use_fixup(const sa3k_ctx* ctx, int64_t elems, int64_t tiles) {
-    if (tiles > kMaxFixupTiles) return false;
+    if (tiles > kMaxFixupTiles || !stream_counters(ctx)) return false;
     return ctx->gemm_fixup == 1 || (ctx->gemm_fixup == 2 && elems <= kSmallFixupElems);
+}
+// the counters of a reduction of kind `bit` over `tiles` column tiles summed by its last split to
+// arrive, or null: a separate launch sums the partials
+inline int* tn_counters(const sa3k_ctx* ctx, int64_t tiles, int bit) {
+    if (!(ctx->tn_fuse & bit) || tiles > kMaxFixupTiles) return nullptr;
+    return stream_counters(ctx);
 }
 
 // Split partial sums handed from one workgroup to another inside a launch ("the last split to
@@ -335,6 +356,40 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+// The split sums of NE elements of coherent partials: acc[i] = sum over z < S of the float at byte
+// offset off[i] + z * zstride of rs, added in z order from zero (the same sums as a sequential
+// loop over z), with device-coherent (sc1) buffer loads issued 8 splits x NE elements at a time so
+// the reading workgroup waits about S / 8 memory round trips, not S x NE. The caller gives every
+// element it stores a valid offset; the sums of the others are not used.
+constexpr int kSc1 = 16;   // buffer intrinsic cache policy: sc1 (device scope)
+template <int NE>
+__device__ __forceinline__ void coherent_split_sums(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[NE],
+                                                    uint32_t zstride, int S, float (&acc)[NE]) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) acc[i] = 0.f;
+    int z = 0;
+    for (; z + 8 <= S; z += 8) {
+        float v[NE][8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int i = 0; i < NE; ++i)
+                v[i][k] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rs, off[i] + (uint32_t)(z + k) * zstride, 0, kSc1));
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[i] += v[i][k];
+    }
+    for (; z < S; ++z) {
+        float v[NE];
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+            v[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off[i] + (uint32_t)z * zstride, 0, kSc1));
+#pragma unroll
+        for (int i = 0; i < NE; ++i) acc[i] += v[i];
+    }
+}
 // arrival of this workgroup on counter c of `expected` arrivals; true for the last one, which
 // also resets the counter. Every thread must call it (it contains workgroup barriers).
 __device__ __forceinline__ bool arrive_last(int* c, int expected, int* s_flag) {

@@ -213,14 +213,19 @@ def test_dit_side_stream_matches_one_stream(ctx):
             assert np.array_equal(a, b), f"stream schedule {sched} changes the results"
 
 
-def test_dit_in_kernel_reductions_match_separate_launches(ctx):
-    # every split reduction done by the last arriving workgroup (GEMM split-K, the column
-    # reductions, the modulation gradients) gives the separate-launch results bit for bit
+@pytest.mark.parametrize("side", [0, 1])
+def test_dit_in_kernel_reductions_match_separate_launches(ctx, side):
+    # every split reduction done by the last arriving workgroup (GEMM split-K under gemm_fixup; the
+    # modulation gradients, the adapted linears' dA sums and their dU column reductions with the
+    # rows step under tn_fuse bits 1, 2, 4) gives the separate-launch results bit for bit, on one
+    # stream and on two (each stream with its own arrival counters)
     cfg = dict(CFG, window=4)
     tensors, adapters, inputs = db.random_dit(45, cfg, "full")
     res = []
     try:
-        for fixup in (0, 1, 2):
+        ctx.set_option("side_stream", side)
+        for tn_fuse, fixup in ((0, 0), (1, 0), (7, 0), (0, 1), (7, 1), (0, 2)):
+            ctx.set_option("tn_fuse", tn_fuse)
             ctx.set_option("gemm_fixup", fixup)
             d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
             up, _ = upload_inputs(ctx, inputs)
@@ -229,6 +234,8 @@ def test_dit_in_kernel_reductions_match_separate_launches(ctx):
             d.destroy()
     finally:
         ctx.set_option("gemm_fixup", 0)
+        ctx.set_option("tn_fuse", 1)
+        ctx.set_option("side_stream", 1)
     for other in res[1:]:
         assert np.array_equal(res[0][0], other[0]) and np.array_equal(res[0][1], other[1])
 

@@ -272,3 +272,27 @@ def test_dx_k_major_operand(ctx, big):
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(kn[k], ref[k]) < 2e-2 and cosine(kn[k], ref[k]) >= 0.9999, (N, k)
             assert rel_err(kn[k], nk[k]) < 1e-5, (N, k)
+
+
+@pytest.mark.parametrize("merge", [True, False])
+@pytest.mark.parametrize("dora", [True, False])
+def test_fused_reductions_bit_identical(ctx, merge, dora):
+    """The column reduction of dU with the per-row step (dm, dB, the dA rows operand) and the dA
+    column reduction each summed by their own last split to arrive (option tn_fuse bits 4 and 2)
+    give the separate reduce / rows launches' results bit for bit (the same split order and
+    formulas), at the DiT's QKV shape and a ragged one."""
+    for N, in_, out_, r in ((2176, 1536, 4608, 32), (200, 192, 320, 8)):
+        X, dY, W, A, B = make_inputs(41, N, in_, out_, r)
+        Wh = W.astype(np.float16)
+        mag = (oracle.row_norms(Wh.astype(np.float32)) * 1.01).astype(np.float32) if dora else None
+        res = []
+        try:
+            for fuse in (0, 2, 4, 6):
+                ctx.set_option("tn_fuse", fuse)
+                res.append(run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 0.5, dora, mag, sa3k.PREC_BF16, reps=2,
+                                   merge=merge))
+        finally:
+            ctx.set_option("tn_fuse", 1)
+        for other in res[1:]:
+            for k in ("Y", "dX", "dA", "dB") + (("dm",) if dora else ()):
+                assert np.array_equal(res[0][k], other[k]), (N, k)
