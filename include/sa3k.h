@@ -126,13 +126,16 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 modulation-gradient column sums, 2 an adapted linear's dA sums, 4 an adapted
  *                 linear's dU column reduction with its per-row step (dm, dB, the dA rows operand)
  *                 (default 5)
+ *   "kv_stack"    1: a DiT set up from now on computes its blocks' context K/V projections (one
+ *                 shared input) as one product over their stacked merged weights, with the rank
+ *                 products as its extra columns; each block's backward stays its own (default 1)
  *   "merge_kn"    1: a merged linear's dX product reads W + s B A in its stored [out][in] layout as
  *                 a K-major operand (transposed by the LDS reads), so the refresh writes one bf16
  *                 copy; 0: the refresh also writes the transposed copy [in][out] and dX reads
  *                 that (default 1). It holds from a linear's next prepare (a DiT: its setup).
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny, gemm_big, gemm_splits, lin_merge, rank_cols and merge_kn, which change
- * the f32 summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big, gemm_splits, lin_merge, rank_cols, merge_kn and kv_stack, which
+ * change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

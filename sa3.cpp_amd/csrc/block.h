@@ -26,6 +26,9 @@ struct sa3k_block_ws {
     sa3k::bf16 *q1, *k1, *q2, *k2, *v; float* rq;
     sa3k::bf16* o; sa3k::bf16 *o1, *o2; float *l1, *l2; float* y; float* x1; float* rs_c; sa3k::bf16* hc;
     float* qf; float* kv; const float* ctxf; sa3k::bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck;
+    // when set, the block's context K/V projection was computed by a stacked product: its rows of
+    // kv_ld floats hold this block's 3 dim outputs (the block skips its own cross.kv forward)
+    const float* kv_ext = nullptr; int64_t kv_ld = 0;
     sa3k::bf16* oc; sa3k::bf16 *co1, *co2; float *cl1, *cl2; float* x2; float* rs_f; sa3k::bf16* fin; float* F;
     sa3k::bf16* g; float* yf;
     // scratch of the forward (yc) and the backward: may be shared by several workspaces that are

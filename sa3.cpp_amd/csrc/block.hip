@@ -378,12 +378,13 @@ struct PrepPart {
     int rope;
 };
 struct PrepArgs {
-    const float* in;      // [B*Sx][parts*dim]
+    const float* in;      // [B*Sx][ldin] (parts*dim used)
     int parts, Sx, H, dim, rope_dims;
     float eps;
     const float* tab;     // RoPE table [Sx][rope_dims] (parts with rope only)
     PrepPart p[5];
     float* rstd;          // [B*Sx][H][parts]
+    int64_t ldin;         // row stride of in (parts*dim when 0)
 };
 
 // 16 lanes per (row, head), lane j holding dims 4j..4j+3 (rope_dims % 8 == 0, so a rotation pair
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int item
     const int row = item / a.H, h = item - row * a.H;
     const int b = row / a.Sx, t = row - b * a.Sx;
     const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
-    const float* src = a.in + (int64_t)row * a.parts * a.dim + h * HD + d0;
+    const float* src = a.in + (int64_t)row * (a.ldin ? a.ldin : (int64_t)a.parts * a.dim) + h * HD + d0;
     float4 x[5];
 #pragma unroll
     for (int k = 0; k < 5; ++k)
@@ -444,7 +445,7 @@ struct PrepBwdPart {
     int rope;
 };
 struct PrepBwdArgs {
-    const float* in;      // forward input [B*Sx][parts*dim] (pre-norm values)
+    const float* in;      // forward input [B*Sx][ldin] (pre-norm values; parts*dim used)
     int parts, Sx, H, dim, rope_dims;
     const float* tab;
     PrepBwdPart p[5];
@@ -452,6 +453,7 @@ struct PrepBwdArgs {
     float* din;           // [B*Sx][parts*dim]
     bf16* du;             // instead of din: the input projection's dU [B*Sx][parts*dim]
     const float* dsc;     // its column scale (null: 1)
+    int64_t ldin;         // row stride of in (parts*dim when 0)
 };
 
 __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int items) {
@@ -462,12 +464,13 @@ __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int i
     const int b = row / a.Sx, t = row - b * a.Sx;
     const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
     const int64_t xo = (int64_t)row * a.parts * a.dim + h * HD + d0;
+    const int64_t xi = (int64_t)row * (a.ldin ? a.ldin : (int64_t)a.parts * a.dim) + h * HD + d0;
     float4 g[5], x[5];
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         if (k >= a.parts) break;
         g[k] = ld4(a.p[k].dy + ho);
-        if (a.p[k].gamma) x[k] = ld4(a.in + xo + (int64_t)k * a.dim);
+        if (a.p[k].gamma) x[k] = ld4(a.in + xi + (int64_t)k * a.dim);
     }
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
@@ -784,12 +787,14 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         arm();
         resnorm(x, w->y, 2, w->x1, b->cross_g, -1, w->hc, w->rs_c);
         chk(ctx, sa3k_lin_forward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, nullptr, w->qf));
-        chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
+        if (!w->kv_ext) chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
+        const float* kv = w->kv_ext ? w->kv_ext : w->kv;
+        const int64_t kv_ld = w->kv_ext ? w->kv_ld : 0;
         PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.qk_eps, nullptr,
                     {{w->cq1, b->cq_g, 0}, {w->cq2, b->cq_g, 0}, {}, {}, {}}, w->rcq};
         launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), pq, (int)(N * H));
-        PrepArgs pk{w->kv, 3, Ctx, H, D, c.rope_dims, c.qk_eps, nullptr,
-                    {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck};
+        PrepArgs pk{kv, 3, Ctx, H, D, c.rope_dims, c.qk_eps, nullptr,
+                    {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck, kv_ld};
         launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(NC * H)), pk, (int)(NC * H));
         arm();
         attn_forward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, B, H, S, Ctx, 0, scale, w->oc, w->co1, w->co2, w->cl1, w->cl2);
@@ -856,9 +861,9 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                        {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, nullptr,
                        lin_du(b->L[2]), lin_du_scale(b->L[2])};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bq, (int)(N * H));
-        PrepBwdArgs bk{w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
+        PrepBwdArgs bk{w->kv_ext ? w->kv_ext : w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
                        {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, nullptr,
-                       lin_du(b->L[3]), lin_du_scale(b->L[3])};
+                       lin_du(b->L[3]), lin_du_scale(b->L[3]), w->kv_ext ? w->kv_ld : 0};
         if (side_usable(ctx)) fork_arm(ctx);   // recorded by the next kernel, for the K/V projection
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(NC * H)), bk, (int)(NC * H));
         {   // the context K/V projection (Ctx tokens, small kernels) beside the query projection

@@ -271,6 +271,7 @@ struct sa3k_dit {
     bool dirty = true;
     int count = 0;
     LinGroup* group = nullptr;      // every adapted linear, refreshed together
+    LinStack* kvs = nullptr;        // the blocks' context K/V projections as one product (or null)
     // activations
     std::vector<sa3k_block_ws*> ws;
     std::vector<float*> xs;
@@ -353,6 +354,7 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
     for (hipGraphExec_t e : d->gexec)
         if (e) (void)hipGraphExecDestroy(e);
     lin_group_free(d->group);
+    lin_stack_free(d->kvs);
     for (float* p : {d->p, d->g, d->m, d->v})
         if (p) (void)hipFree(p);
     delete d;
@@ -472,6 +474,13 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     double* ls = dalloc<double>((size_t)B);
     d->bufs.push_back(ls);
     d->loss = ls;
+    if (ctx->kv_stack && c.depth > 1) {
+        // every block projects the same context to its cross-attention K/V: one product over the
+        // stacked merged weights (set up before the refresh group, which then writes into it)
+        std::vector<sa3k_lin*> kl;
+        for (sa3k_block* b : d->blocks) kl.push_back(b->L[3]);
+        d->kvs = lin_stack_create(ctx, kl.data(), (int)kl.size());
+    }
     {
         std::vector<sa3k_lin*> lins;
         std::vector<const float*> A, Bm, mag, bnsq;
@@ -539,6 +548,12 @@ void mlp_bwd(sa3k_ctx* ctx, sa3k_dit* d, int i0, const float* x, int64_t N, cons
     lin_bwd(ctx, d, i0, x, N, dh, dx, 0);
 }
 
+// block l's context K/V: its columns of the stacked product's output, or its own projection
+void bind_kv(sa3k_dit* d, sa3k_block_ws* w, int l) {
+    w->kv_ext = d->kvs ? lin_stack_y(d->kvs) + (int64_t)l * 3 * d->cfg.dim : nullptr;
+    w->kv_ld = d->kvs ? lin_stack_ld(d->kvs) : 0;
+}
+
 // head + blocks + tail forward: velocity in d->vel
 void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const float* cross, const float* glob) {
     const sa3k_dit_config& c = d->cfg;
@@ -559,6 +574,7 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
            d->gsum);
     mlp_fwd(ctx, d, H_GCE0, d->gsum, B, d->gce_h, d->gce_a, d->gcond);   // dim -> dim -> 6 dim
     mlp_fwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->context);
+    if (d->kvs) lin_stack_forward(ctx, d->kvs, d->context, NC);   // every block's context K/V
     // x path
     lin_fwd(ctx, d, H_PRE_CONV, x_t, NT, d->xp);
     launch(ctx, "dit_head", add_kernel, dim3(nblk(NT * c.io)), (const float*)d->xp, x_t, NT * c.io, d->xp);
@@ -567,6 +583,7 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
            c.mem_tokens, (int)D, d->xs[0]);
     // blocks
     for (int l = 0; l < c.depth; ++l) {
+        bind_kv(d, d->ws[d->tr.recompute ? 0 : l], l);
         block_forward(ctx, d->blocks[l], d->ws[d->tr.recompute ? 0 : l], d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         if (d->tr.recompute) side_join_since(ctx, forks0);
     }
@@ -610,6 +627,7 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
     float* dnext = d->dxb;
     for (int l = c.depth - 1; l >= 0; --l) {
         sa3k_block_ws* w = d->ws[d->tr.recompute ? 0 : l];
+        bind_kv(d, w, l);
         if (d->tr.recompute && l != c.depth - 1)   // the last block's activations are still in place
             block_forward(ctx, d->blocks[l], w, d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         float* dA[7];

@@ -44,6 +44,19 @@ bf16* lin_du(sa3k_lin* L);
 const float* lin_du_scale(const sa3k_lin* L);
 void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, float* dX, int dx_accumulate,
                      float* dA, float* dB, float* dm);
+// A stacked product: n bf16 merged adapted linears of one shape and rank that read the same input
+// (the DiT's per-block context K/V projections). Created before the linears are prepared, it moves
+// their W_eff, row scales d, A copies and the saved U / s X A^T into contiguous slabs, so that one
+// GEMM (lin_stack_forward) computes every member's forward: Y [N][n out] f32 (owned by the stack,
+// member i in columns i out .. (i+1) out - 1). Each member's backward then runs as usual on that
+// member (reading its slices of U and s X A^T); its own forward is refused. Null when the linears
+// are not eligible (or the merged refresh is off).
+struct LinStack;
+LinStack* lin_stack_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n);
+const float* lin_stack_forward(sa3k_ctx* ctx, LinStack* st, const float* X, int64_t N);
+int64_t lin_stack_ld(const LinStack* st);   // row stride of Y (n out)
+const float* lin_stack_y(const LinStack* st);   // Y (fixed for the stack's lifetime)
+void lin_stack_free(LinStack* st);
 // The B operand of X W^T (forward orientation) in g's precision: the bf16 working copy when the
 // weight has one and the precision is bf16, else the stored elements or Q8_0 planes, which the
 // GEMM decodes on their way into LDS.

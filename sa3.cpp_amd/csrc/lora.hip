@@ -58,6 +58,10 @@ struct sa3k_lin {
     void* A2x = nullptr;                // [r][r]   compute type: 2s^2 B^T diag(gn) B
     float* red = nullptr;               // [out][r] reduced dU^T Hc
     const char* tag = nullptr;          // role name for profiler scopes (lin_set_tag)
+    // a member of a stacked product (lin_stack_*): U and Hc are column slices of the stack's outputs
+    // with these row strides; the buffers named in `ext` belong to the stack
+    int64_t ldu = 0, ldh = 0;
+    unsigned ext = 0;
     // merged mode (bf16 precision): the products contract W_eff = W + s B A, refreshed by prepare
     int merged = 0;
     void* Wm = nullptr;                 // [out][in] bf16 W_eff
@@ -367,7 +371,9 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
                                                              const bf16* __restrict__ U, const float* __restrict__ d,
                                                              bf16* __restrict__ dU, float* __restrict__ part, int64_t N,
                                                              int64_t cols, int64_t rows_per, float* __restrict__ out,
-                                                             int accumulate, int* __restrict__ counters, RowsArgs rows) {
+                                                             int accumulate, int* __restrict__ counters, RowsArgs rows,
+                                                             int64_t ldu, int64_t ldp) {
+    // ldu / ldp: row strides of U and P in elements (the rows of a wider matrix); Q has `cols`
     __shared__ __attribute__((aligned(16))) char qt[2][TN_STEP * TN_QLD];
     __shared__ __attribute__((aligned(16))) char pt[2][TN_STEP * TN_PLD];
     __shared__ float red[TN_ROWS][TN_COLS + 1];
@@ -407,25 +413,26 @@ __global__ __launch_bounds__(kThreads) void skinny_tn_kernel(const QT* __restric
     constexpr bool kGd = MODE == TN_DY || MODE == TN_DU;   // the magnitude column sums gd
     const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<bf16*>(kGd && U ? U : static_cast<const bf16*>(nullptr)), (short)0,
-        (kGd && U) ? (int)(r1 * cols * 2) : 0, 0x00020000);
+        (kGd && U) ? (int)(r1 * ldu * 2) : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(P), (short)0,
-                                                                        (int)(r1 * r * 2), 0x00020000);
+                                                                        (int)(r1 * ldp * 2), 0x00020000);
     auto load = [&](int64_t n0, Regs& R) {
 #pragma unroll
         for (int h = 0; h < TN_H; ++h) {
             const int64_t n = n0 + lrow + TN_ROWS * h;
             const uint32_t e = col_ok ? (uint32_t)(n * cols + col) : 0u;   // element offset of the 8 columns
-            const uint32_t pe = a4 < r ? (uint32_t)(n * r + a4) : 0u;
+            const uint32_t eu = col_ok ? (uint32_t)(n * ldu + col) : 0u;   // the same in U
+            const uint32_t pe = a4 < r ? (uint32_t)(n * ldp + a4) : 0u;
             if constexpr (MODE == TN_DY || sizeof(QT) == 4) {
                 const uint32_t off = col_ok ? e * 4u : kOut;
                 R.ya[h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
                 R.yb[h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16u, 0, 0));
             }
             if constexpr (MODE == TN_DY) {
-                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? e * 2u : kOut, 0, 0));
+                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? eu * 2u : kOut, 0, 0));
             } else if constexpr (MODE == TN_DU) {
                 R.q[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, col_ok ? e * 2u : kOut, 0, 0));
-                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? e * 2u : kOut, 0, 0));
+                R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, col_ok ? eu * 2u : kOut, 0, 0));
             } else if constexpr (sizeof(QT) == 2) {
                 R.u[h] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, col_ok ? e * 2u : kOut, 0, 0));
             }
@@ -803,13 +810,19 @@ void free_weight(sa3k_weight* w) {
     delete w;
 }
 
+// buffers of a linear that a stacked product owns instead (sa3k_lin::ext)
+constexpr unsigned kExtAc = 1, kExtD = 2, kExtWm = 4, kExtU = 8, kExtHc = 16;
+
 void free_lin(sa3k_lin* L) {
     if (!L) return;
     if (L->solo) lin_group_free(L->solo);
-    for (void* p : {L->Xb, L->Ac, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq,
-                    (void*)L->d, L->Hc, L->U, L->dU, L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x,
-                    (void*)L->red, L->Wm, L->Wmt})
+    for (void* p : {L->Xb, L->At, L->Bc, L->Bt, (void*)L->Pt, (void*)L->G, (void*)L->BG, (void*)L->nsq, L->dU,
+                    L->sdUB, (void*)L->gd, (void*)L->gn, L->Ax, L->A2x, (void*)L->red, L->Wmt})
         if (p) (void)hipFree(p);
+    const std::pair<void*, unsigned> own[] = {{L->Ac, kExtAc}, {(void*)L->d, kExtD}, {L->Wm, kExtWm},
+                                              {L->U, kExtU}, {L->Hc, kExtHc}};
+    for (const auto& [p, bit] : own)
+        if (p && !(L->ext & bit)) (void)hipFree(p);
     delete L;
 }
 
@@ -838,6 +851,7 @@ WOp weight_operand(const sa3k_weight* W, bool bf, bool transposed) {
 
 template <class CT>
 void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* bias, float* Y) {
+    SA3K_REQUIRE(L->ext == 0, "a linear of a stacked product runs its forward through the stack");
     const sa3k_weight* W = L->W;
     const bool bf = L->prec == SA3K_PREC_BF16;
     // merged: Hc feeds only the backward's dB reduction, so it is computed beside the main product
@@ -938,6 +952,8 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         x_rows_per = ceil_div(N, x_S);
     }
     bool rows_fused = false;   // the rows step runs in the column reduction's last split
+    // row strides of the saved U and Hc (wider when a stacked product wrote them)
+    const int64_t ldu = L->ldu ? L->ldu : out, ldh = L->ldh ? L->ldh : r;
     // 1. dU = dY*d, gd, dU^T Hc (column reduction over tokens); the split partials rp[rS][rows][out]
     const float* rp = nullptr;
     int rS = 1;
@@ -945,7 +961,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     if constexpr (sizeof(CT) == 2) {
         // the skinny TN kernels address dY / X through 32-bit buffer offsets (with a few steps of
         // look-ahead past the last token row)
-        SA3K_REQUIRE((N + 4 * TN_STEP) * std::max(in, out) * 4 < ((int64_t)1 << 32),
+        SA3K_REQUIRE((N + 4 * TN_STEP) * std::max(std::max(in, out), ldu) * 4 < ((int64_t)1 << 32),
                      "tokens x features too large for one adapted-linear backward");
         // tn_fuse: the reduction's last split per column tile runs the rows step itself; else
         // (gemm_fixup) it sums the partials into L->red for the rows kernel, or that kernel sums them
@@ -967,12 +983,12 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
                 launch_k(ctx, true, skinny_tn_kernel<TN_DU, bf16>, grid, dim3(kThreads), 0,
                          static_cast<const bf16*>(L->dU), static_cast<const bf16*>(L->Hc), r,
                          static_cast<const bf16*>(L->dora ? L->U : nullptr), (const float*)(L->dora ? L->d : nullptr),
-                         (bf16*)nullptr, part, N, out, rows_per, L->red, 0, counters, ra);
+                         (bf16*)nullptr, part, N, out, rows_per, L->red, 0, counters, ra, ldu, ldh);
             else
                 launch_k(ctx, true, skinny_tn_kernel<TN_DY, float>, grid, dim3(kThreads), 0, dY,
                          static_cast<const bf16*>(L->Hc), r, static_cast<const bf16*>(L->dora ? L->U : nullptr),
                          (const float*)(L->dora ? L->d : nullptr), static_cast<bf16*>(L->dU), part, N, out, rows_per,
-                         L->red, 0, counters, ra);
+                         L->red, 0, counters, ra, ldu, ldh);
             SA3K_LAUNCHED();
         }
         // the rows kernel below sums the S partials (or, after the in-kernel reduction, reads the
@@ -1057,11 +1073,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
             if (x_src == SRC_F32)
                 launch_k(ctx, true, skinny_tn_kernel<TN_X, float>, grid, dim3(kThreads), 0, static_cast<const float*>(X),
                          static_cast<const bf16*>(L->sdUB), r, (const bf16*)nullptr, (const float*)nullptr,
-                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{});
+                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{}, (int64_t)in, (int64_t)r);
             else
                 launch_k(ctx, true, skinny_tn_kernel<TN_X, bf16>, grid, dim3(kThreads), 0, static_cast<const bf16*>(X),
                          static_cast<const bf16*>(L->sdUB), r, (const bf16*)nullptr, (const float*)nullptr,
-                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{});
+                         (bf16*)nullptr, x_part, N, in, x_rows_per, dA, 1, xc, RowsArgs{}, (int64_t)in, (int64_t)r);
             SA3K_LAUNCHED();
         } else {
             x_part = reduce_workspace(ctx, (size_t)x_S * R * in * sizeof(float));
@@ -1766,6 +1782,105 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
         SA3K_LAUNCHED();
     }
 }
+
+// ---------------------------------------------------------------- stacked products
+struct LinStack {
+    std::vector<sa3k_lin*> lins;
+    int64_t in = 0, out = 0, max_tokens = 0;
+    int r = 0;
+    void *Wm = nullptr, *Ac = nullptr, *U = nullptr, *H = nullptr, *Xb = nullptr;
+    float *d = nullptr, *Y = nullptr;
+};
+
+void lin_stack_free(LinStack* s) {
+    if (!s) return;
+    for (void* p : {s->Wm, s->Ac, s->U, s->H, s->Xb, (void*)s->d, (void*)s->Y})
+        if (p) (void)hipFree(p);
+    delete s;
+}
+
+LinStack* lin_stack_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n) {
+    SA3K_REQUIRE(n > 0 && lins, "empty stack");
+    // eligible: merged refresh on, bf16 adapted linears of one shape, rank and token budget, not yet
+    // prepared, stacked weights below 2 GiB (buffer descriptors); otherwise no stack (null)
+    if (!ctx->lin_merge) return nullptr;
+    const sa3k_lin* L0 = lins[0];
+    for (int i = 0; i < n; ++i) {
+        const sa3k_lin* L = lins[i];
+        if (L->prec != SA3K_PREC_BF16 || L->rank != L0->rank || L0->rank <= 0 || L->W->in != L0->W->in ||
+            L->W->out != L0->W->out || L->max_tokens != L0->max_tokens || L->ext != 0 || L->Wm || L->solo)
+            return nullptr;
+    }
+    if (L0->W->out % 8 != 0 || (int64_t)n * L0->W->out * L0->W->in * 2 >= ((int64_t)1 << 31)) return nullptr;
+    LinStack* st = new LinStack();
+    try {
+        st->in = L0->W->in;
+        st->out = L0->W->out;
+        st->r = L0->rank;
+        st->max_tokens = L0->max_tokens;
+        const int64_t cols = (int64_t)n * st->out, rcols = (int64_t)n * st->r;
+        st->Wm = dev_alloc<bf16>(cols * st->in);
+        st->Ac = dev_alloc<bf16>(rcols * st->in);
+        st->d = dev_alloc<float>(cols);
+        st->U = dev_alloc<bf16>(st->max_tokens * cols);
+        st->H = dev_alloc<bf16>(st->max_tokens * rcols);
+        st->Y = dev_alloc<float>(st->max_tokens * cols);
+        st->Xb = dev_alloc<bf16>(st->max_tokens * st->in);
+        for (int i = 0; i < n; ++i) {
+            sa3k_lin* L = lins[i];
+            for (void* p : {L->Ac, (void*)L->d, L->U, L->Hc})
+                if (p) SA3K_HIP(hipFree(p));
+            L->Ac = static_cast<bf16*>(st->Ac) + (int64_t)i * st->r * st->in;
+            L->d = st->d + (int64_t)i * st->out;
+            L->Wm = static_cast<bf16*>(st->Wm) + (int64_t)i * st->out * st->in;
+            L->U = static_cast<bf16*>(st->U) + (int64_t)i * st->out;
+            L->Hc = static_cast<bf16*>(st->H) + (int64_t)i * st->r;
+            L->ldu = cols;
+            L->ldh = rcols;
+            L->ext = kExtAc | kExtD | kExtWm | kExtU | kExtHc;
+            st->lins.push_back(L);
+        }
+    } catch (...) {
+        lin_stack_free(st);
+        throw;
+    }
+    return st;
+}
+
+const float* lin_stack_forward(sa3k_ctx* ctx, LinStack* st, const float* X, int64_t N) {
+    const int n = (int)st->lins.size();
+    const sa3k_lin* L0 = st->lins[0];
+    SA3K_REQUIRE(N > 0 && N <= st->max_tokens, "tokens exceed the stack's budget");
+    for (const sa3k_lin* L : st->lins)
+        SA3K_REQUIRE(L->merged && L->dora == L0->dora && L->s == L0->s,
+                     "stack members must be prepared merged, with one scale and adapter kind");
+    const int64_t cols = (int64_t)n * st->out, rcols = (int64_t)n * st->r;
+    {
+        const int64_t e = N * st->in;
+        KernelScope ks(ctx, "lin_stack_cvt_x");
+        launch_k(ctx, true, cvt_kernel<bf16>, dim3((unsigned)ceil_div(e, kThreads)), dim3(kThreads), 0, X,
+                 static_cast<bf16*>(st->Xb), e, 1.0f);
+        SA3K_LAUNCHED();
+    }
+    // Y_i = d_i (.) (X W_eff,i^T) for every member as one product over the stacked W_eff, with
+    // s X A_i^T of every member as the extra columns
+    GemmDesc g;
+    g.prec = SA3K_PREC_BF16; g.a_src = SRC_BF16; g.b_src = SRC_BF16;
+    g.A = st->Xb; g.lda = st->in;
+    g.B = st->Wm; g.ldb = st->in;
+    g.Nx = rcols; g.Bx = st->Ac; g.ldbx = st->in; g.alpha_x = L0->s; g.Cbn = static_cast<bf16*>(st->H); g.ldcn = rcols;
+    g.M = N; g.N = cols; g.K = st->in; g.alpha = 1.0f;
+    g.colscale = L0->dora ? st->d : nullptr;
+    g.C = st->Y; g.ldc = cols;
+    g.ldu = cols;
+    if (L0->dora) g.Ub = static_cast<bf16*>(st->U);
+    gemm_run(ctx, g, "lin_stack_fwd");
+    for (sa3k_lin* L : st->lins) L->saved_tokens = N;
+    return st->Y;
+}
+
+int64_t lin_stack_ld(const LinStack* st) { return (int64_t)st->lins.size() * st->out; }
+const float* lin_stack_y(const LinStack* st) { return st->Y; }
 
 }  // namespace sa3k
 

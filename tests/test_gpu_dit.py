@@ -213,6 +213,32 @@ def test_dit_side_stream_matches_one_stream(ctx):
             assert np.array_equal(a, b), f"stream schedule {sched} changes the results"
 
 
+@pytest.mark.parametrize("recompute", [0, 1])
+def test_dit_stacked_context_kv_matches_per_block(ctx, recompute):
+    # the blocks' context K/V projections computed as one product over their stacked merged weights
+    # (option kv_stack) give the per-block products' loss and gradients within f32 summation-order
+    # rounding, over two updates (refresh and AdamW between), resident and recomputed
+    cfg = dict(CFG, window=4)
+    tensors, adapters, inputs = db.random_dit(47, cfg, "full")
+    res = []
+    try:
+        for kv in (0, 1):
+            ctx.set_option("kv_stack", kv)
+            d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16, recompute=recompute)
+            up, _ = upload_inputs(ctx, inputs)
+            out = []
+            for step in (1, 2):
+                loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
+                out += [np.float64(loss), d.arena(1).numpy()]
+                d.apply_adamw(HP, step)
+            res.append(out)
+            d.destroy()
+    finally:
+        ctx.set_option("kv_stack", 1)
+    for a, b in zip(res[0], res[1]):
+        assert rel_err(np.atleast_1d(b), np.atleast_1d(a)) < 1e-4
+
+
 @pytest.mark.parametrize("side", [0, 1])
 def test_dit_in_kernel_reductions_match_separate_launches(ctx, side):
     # every split reduction done by the last arriving workgroup (GEMM split-K under gemm_fixup; the
