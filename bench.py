@@ -204,6 +204,71 @@ class LinearWorkload:
                           f"f32 mode (float accumulation, AVX2/FMA products, OpenMP)"}
 
 
+class ChainWorkload:
+    """Inference reuse: one forward of a composed adapter chain (build_functional_lora,
+    src/lora.h:372-622, and the chain branch of dit_lin, src/dit.h:108-117) over a frozen Q8_0 base
+    1536 -> 6144 at 2176 tokens: dora-rows r32 (strength 1), lora r16 (0.7), dora-rows r16 (0.5),
+    folded at create; a step is the chain's forward (X f32 -> bf16, the rank GEMM, the base GEMM with
+    the folded row scale and the stacked rank term). kind "q8": the base decoded from its Q8_0 blocks
+    between LDS and the MFMAs (no bf16 copy); "q8_copy": the same chain over the bf16 working copy."""
+
+    def __init__(self, ctx, kind):
+        sa3k = sys.modules["sa3k"]
+        oracle = _load("sa3_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        self.ctx, self.kind = ctx, kind
+        self.N, self.in_, self.out_ = 2176, 1536, 6144
+        self.dtype = "bf16"
+        self.specs = [(1, 32, 32.0, 1.0), (0, 16, 16.0, 0.7), (1, 16, 32.0, 0.5)]
+        g = rng(7)
+        W = g.normal(0, 0.02, (self.out_, self.in_)).astype(np.float32)
+        self.blocks = oracle.q8_0_quantize(W)
+        self.Wdec = oracle.q8_0_dequant(self.blocks, self.out_ * self.in_).reshape(self.out_, self.in_)
+        self.w = ctx.weight((self.blocks, self.in_, self.out_), sa3k.TYPE_Q8_0)
+        if kind == "q8":
+            self.w.drop_working_copy()
+        norms = np.sqrt((self.Wdec.astype(np.float64) ** 2).sum(1))
+        self.ads = []
+        for dora, r, alpha, strength in self.specs:
+            A = g.uniform(-1 / np.sqrt(self.in_), 1 / np.sqrt(self.in_), (r, self.in_)).astype(np.float32)
+            B = g.normal(0, 0.02, (self.out_, r)).astype(np.float32)
+            mag = (norms * (1.0 + 0.1 * g.standard_normal(self.out_))).astype(np.float32) if dora else None
+            self.ads.append((dora, r, alpha, strength, A, B, mag))
+        dev = [(d, r, a, st, ctx.upload(A), ctx.upload(B), ctx.upload(m) if m is not None else None)
+               for d, r, a, st, A, B, m in self.ads]
+        self.chain = ctx.lora_chain(self.w, dev, self.N)
+        self.X_host = g.normal(0, 1, (self.N, self.in_)).astype(np.float32)
+        self.X = ctx.upload(self.X_host)
+        self.Y = ctx.empty((self.N, self.out_))
+
+    def step(self):
+        self.chain.forward(self.X, self.N, self.Y)
+
+    def flops(self):
+        R = sum(r for _, r, _, _ in self.specs)
+        return 2.0 * self.N * self.in_ * self.out_ + 2.0 * self.N * self.in_ * R + 2.0 * self.N * R * self.out_
+
+    def config(self):
+        return {"workload": "lora_chain_q8_0_2176x1536x6144_3adapters" + ("" if self.kind == "q8" else "_bf16_copy"),
+                "tokens": self.N, "in": self.in_, "out": self.out_, "adapters": "dora r32, lora r16, dora r16",
+                "base": "q8_0 decoded in the GEMM" if self.kind == "q8" else "q8_0 via its bf16 working copy"}
+
+    def roofline(self, prof, steps):
+        return gemm_roofline(prof, steps)
+
+    def extra(self, ms_per_step):
+        return {"algorithmic_gflop_per_forward": round(self.flops() / 1e9, 2),
+                "tflops_whole_forward": round(self.flops() / (ms_per_step * 1e-3) / 1e12, 1)}
+
+    def cpu_baseline(self):
+        oracle = _load("sa3_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        n = 128
+        Xs = self.X_host[:n]
+        t, times = _median_time(lambda: oracle.chain_forward(Xs, self.Wdec, self.ads), runs=3)
+        return {"value": round(t * 1e3 * self.N / n, 1), "unit": "ms/forward", "cores": 1, "kind": "port",
+                "sample": f"the oracle's chain forward (double accumulation) on {n} of the {self.N} tokens, median of "
+                          f"{len(times)} after a warm-up ({t * 1e3:.1f} ms), scaled by {self.N}/{n}"}
+
+
 def _median_time(fn, runs=3):
     """one untimed warm-up call (it also maps the memory the later calls reuse), then the median of
     `runs` timed calls: (median seconds, [seconds])"""
@@ -496,7 +561,9 @@ WORKLOADS = {"adamw": AdamWWorkload,
              "lora_linear": lambda ctx: LinearWorkload(ctx, "lora_f32"),
              "block": BlockWorkload,
              "dit": DitWorkload,
-             "dit_recompute": lambda ctx: DitWorkload(ctx, recompute=True)}
+             "dit_recompute": lambda ctx: DitWorkload(ctx, recompute=True),
+             "chain_q8": lambda ctx: ChainWorkload(ctx, "q8"),
+             "chain_q8_copy": lambda ctx: ChainWorkload(ctx, "q8_copy")}
 DEFAULT = "dit"
 
 

@@ -87,6 +87,10 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 inside the producing kernel; 0: by a separate reduction launch; 2: in-kernel for
  *                 outputs of at most 2^18 floats, a separate launch for larger ones (default 0)
  *   "gemm_dma"    1: DMA-fed kernel for compute-type operands (default 1)
+ *   "gemm_dq"     1: bf16 products with an f16 or Q8_0 B operand (no extra rows or columns) run on the
+ *                 DMA-fed kernel, B staged in LDS as stored and decoded between LDS and the MFMAs;
+ *                 0: the kernel that decodes on the way into LDS (default 1; both decode to the same
+ *                 bf16 values, their tiles sum in different orders)
  *   "gemm_cfg"    DMA kernel tile configuration: 0 (default) 128 x 256 tiles for bf16 and
  *                 128 x 128 for f32; 1: 128 x 128; 4: 128 x 256 (3 stages); 7: 128 x 256 (2 stages)
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
@@ -134,8 +138,8 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 copy; 0: the refresh also writes the transposed copy [in][out] and dX reads
  *                 that (default 1). It holds from a linear's next prepare (a DiT: its setup).
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny, gemm_big, gemm_splits, lin_merge, rank_cols, merge_kn and kv_stack, which
- * change the f32 summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn and
+ * kv_stack, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

@@ -568,6 +568,22 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
         return;
     }
     const int ct_src = bf ? SRC_BF16 : SRC_F32;
+    // bf16 A with an f16 or Q8_0 B: the DMA-fed kernel stages B as stored (2 or 1 + 1/16 bytes per
+    // element) and decodes it between LDS and the MFMAs
+    auto a16 = [](const void* q, int64_t ld_bytes, int align) {
+        return (reinterpret_cast<uintptr_t>(q) % (uintptr_t)align) == 0 && ld_bytes % align == 0;
+    };
+    const bool dq = bf && ctx->gemm_dq && ctx->gemm_dma && d.a_src == SRC_BF16 &&
+                    (d.b_src == SRC_F16 || d.b_src == SRC_Q8) && d.Mx == 0 && d.Nx == 0 && !d.b_kn &&
+                    d.K % 64 == 0 && d.N % 8 == 0 && a16(d.A, d.lda * 2, 16) &&
+                    (d.b_src == SRC_F16 ? a16(d.B, d.ldb * 2, 16)
+                                        : a16(d.B, d.ldb, 16) && d.Bs && a16(d.Bs, d.ldbs * 2, 4));
+    if (dq) {
+        KernelScope ks(ctx, prof_name);
+        gemm_run_dma(ctx, d);
+        SA3K_LAUNCHED();
+        return;
+    }
     if (d.a_src == ct_src && d.b_src == ct_src && ctx->gemm_dma) {
         SA3K_REQUIRE((d.ldb * (bf ? 2 : 4)) % 16 == 0 && (d.Mx == 0 || (d.ldax * (bf ? 2 : 4)) % 16 == 0),
                      "GEMM operand rows must be 16-byte aligned");

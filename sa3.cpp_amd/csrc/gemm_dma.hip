@@ -52,6 +52,11 @@ struct DmaParams {
     bf16* Cbn; int64_t ldcn;
     uint32_t bx_bytes;
     int b_kn;   // B stored [K][ldb], N contiguous (GemmDesc::b_kn)
+    // main-segment B decoded on its way from LDS into the MFMA operands: bq 1 f16 elements, 2 Q8_0
+    // (int8 quants, ldb bytes per row, and f16 block scales Bs, ldbs per row); 0 bf16
+    int bq;
+    const void* Bs; int64_t ldbs;
+    uint32_t bs_bytes;
 };
 
 namespace {
@@ -106,6 +111,13 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
 // at dma16.
 __device__ __forceinline__ void dma16b(const u32x4& rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_addr), "v"(voff), "s"(rsrc),
+                 "s"(soff)
+                 : "memory");
+}
+
+// 4 bytes per lane into LDS at lds_addr + 4 lane
+__device__ __forceinline__ void dma4b(const u32x4& rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds_addr), "v"(voff), "s"(rsrc),
                  "s"(soff)
                  : "memory");
 }
@@ -247,7 +259,12 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
 // NW wave64s per workgroup (4 or 8): WMW of them along M, NW/WMW along N, each owning a
 // (BM/WMW) x (BN/(NW/WMW)) block of the tile. With 8 waves two share each SIMD, so one wave's
 // LDS reads and waits overlap the other's MFMAs inside a single workgroup.
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false>
+// Q8_0 B tile in LDS (BQ 2): BN rows of 64 quant bytes (four 16-byte chunks, XOR-swizzled by
+// qswz), then the rows' two f16 block scales (4 bytes per row, NW x 64 slots), then a dummy area for
+// the loads that pad a tile's DMA count to the bf16 tile's (so the ring's vmcnt accounting holds).
+__device__ __forceinline__ int qswz(int r) { return (r >> 1) & 3; }
+
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0>
 __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     constexpr int NT = NW * 64;
     constexpr int WNW = NW / WMW;
@@ -273,6 +290,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     static_assert(NA >= 1 && NB >= 1 && FM >= 1 && FN >= 1, "tile too small");
     static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * LPT < 64, "pipeline depth");
     static_assert(!KN || (BF16 && BN % 64 == 0), "a [K][N] B operand needs bf16 and whole 64-column sub-tiles");
+    static_assert(BQ == 0 || (BF16 && !KN), "decoded B operands are bf16-compute, [N][K] only");
+    constexpr int NBQ = BQ == 2 ? BN * 4 / NT : 0;             // Q8_0 quant chunks per thread per tile
+    static_assert(BQ != 2 || (NBQ >= 1 && NB - NBQ - 1 >= 0 && NW * 64 >= BN &&
+                              BN * 64 + NW * 256 + (NB - NBQ - 1) * NT * 16 <= BN * kRow),
+                  "Q8_0 tile layout does not fit the bf16 B region");
     // The stages are consecutive STAGE_BYTES regions of one LDS array, each always addressed at a
     // compile-time offset. Every LDS write of the K loop is an inline-asm DMA, so the compiler
     // inserts no waits of its own; the loop orders DMA and reads with vmcnt waits and barriers.
@@ -382,6 +404,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     // the 8 rows of B slot (q, wave) start at n0 + (q * NT + 64 wave) / 8: one source per slot
     // (N % 8 == 0), chosen on the scalar unit
     auto slot_bx = [&](int q) { return n0 + (q * NT + wave * 64) / 8 < p.Nt && n0 + (q * NT + wave * 64) / 8 >= p.N; };
+    // Q8_0: quant slot s = q NT + tid holds row s / 4, physical chunk s % 4 = logical chunk
+    // kc ^ qswz(row) (16 quant bytes); lane l of wave w loads row 64 w + l's two block scales
+    uint32_t qoff[BQ == 2 ? NBQ : 1] = {};
+    uint32_t soff_sc = 0;
+    u32x4 rs_bs = {};
+    if constexpr (BQ == 2) {
+#pragma unroll
+        for (int q = 0; q < NBQ; ++q) {
+            const int s = q * NT + tid, row = s >> 2, kc = (s & 3) ^ qswz(row);
+            int64_t gn = n0 + row;
+            if (gn >= p.N) gn = 0;   // clamped: this output column is never stored
+            qoff[q] = (uint32_t)(gn * p.ldb + kc * 16);
+        }
+        const int srow = wave * 64 + lane;
+        const int64_t gn = n0 + srow;
+        soff_sc = srow < BN && gn < p.N ? (uint32_t)(gn * p.ldbs * 2) : 0xFFFFFFF0u;
+        rs_bs = buffer_rsrc(p.Bs, p.bs_bytes);
+    }
 
     auto issue = [&](auto s_c, int t) {
         constexpr uint32_t so_lds = (uint32_t)((decltype(s_c)::value % STAGES) * STAGE_BYTES);
@@ -394,7 +434,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
                 for (int q = 0; q < NA; ++q) dma16(ag[q] + (int64_t)t * (BKE * EB), dst[q] + so_lds);
             }
-            if constexpr (KN) {   // always through the descriptor: the K tile is a row offset
+            if constexpr (BQ == 2) {   // quants, block scales, then the padding loads
+                const uint32_t kq = (uint32_t)(k0 + (int64_t)t * BKE);   // bytes into the quant rows
+#pragma unroll
+                for (int q = 0; q < NBQ; ++q) dma16b(rs_b, qoff[q], kq, dst[NA + q] + so_lds);
+                const uint32_t sc0 = lds_base + BM * kRow + BN * 64 + so_lds;
+                dma4b(rs_bs, soff_sc, kq / 16, sc0 + (uint32_t)wave * 256u);
+#pragma unroll
+                for (int q = 0; q < NB - NBQ - 1; ++q)
+                    dma16b(rs_bs, 0xFFFFFFF0u, 0u, sc0 + NW * 256 + (uint32_t)((q * NT + wave * 64) * 16));
+            } else if constexpr (KN) {   // always through the descriptor: the K tile is a row offset
                 const uint32_t sob = (uint32_t)((k0 + (int64_t)t * BKE) * p.ldb * 2);
 #pragma unroll
                 for (int q = 0; q < NB; ++q) dma16b(rs_b, boff[q], sob, dst[NA + q] + so_lds);
@@ -426,7 +475,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     auto frag = [&](const char* base, int row, int kc) {
         return base + row * kRow + ((kc ^ swz(row)) << 4);
     };
-    auto compute = [&](const char* As) {
+    // B fragment of lane (row n, K step ks, half g) decoded to bf16 from f16 (BQ 1) or Q8_0 (BQ 2):
+    // the same RNE of the exact decoded value as the weight's bf16 working copy
+    auto dq_frag = [&](const char* Bs, int n, int ks, int g, int kc) __attribute__((always_inline)) -> bf16x8 {
+        bf16x8 o;
+        if constexpr (BQ == 1) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 h = *reinterpret_cast<const h8*>(frag(Bs, n, kc));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (__bf16)(float)h[e];
+        } else if constexpr (BQ == 2) {
+            const uint2 qv = *reinterpret_cast<const uint2*>(Bs + n * 64 + ((ks ^ qswz(n)) << 4) + 8 * g);
+            const float sc = (float)*reinterpret_cast<const _Float16*>(Bs + BN * 64 + n * 4 + (ks >> 1) * 2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const unsigned w = e < 4 ? qv.x : qv.y;
+                const int q = (int)(signed char)(w >> (8 * (e & 3)));
+                o[e] = (__bf16)(sc * (float)q);
+            }
+        }
+        return o;
+    };
+    auto compute = [&](const char* As, bool deq) __attribute__((always_inline)) {
         const char* Bs = As + BM * kRow;
         if constexpr (BF16) {
             // 32x32x16: lane l holds row l%32, k = 8*(l/32) + e; four K steps of 16 per tile
@@ -447,6 +517,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
                         const char* sub = Bs + (nb >> 6) * (64 * kRow);
                         const int nl = (nb & 63) + 16 * ((lane >> 4) & 1), kb = 16 * ks + 8 * g;
                         bfr[ks][j] = cat44(ld_tr(sub, kb, nl, lane), ld_tr(sub, kb + 4, nl, lane));
+                    } else if (BQ != 0 && deq) {
+                        bfr[ks][j] = dq_frag(Bs, wn0 + 32 * j + r, ks, g, kc);
                     } else {
                         bfr[ks][j] = *reinterpret_cast<const bf16x8*>(frag(Bs, wn0 + 32 * j + r, kc));
                     }
@@ -522,7 +594,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             __asm__ volatile("s_barrier" ::: "memory");
             if (t + STAGES - 1 < T) issue(IC<decltype(s)::value + STAGES - 1>{}, t + STAGES - 1);
             if (p.prescale && t == Tm) scale_acc();
-            compute(lds + decltype(s)::value * STAGE_BYTES);
+            compute(lds + decltype(s)::value * STAGE_BYTES, t < Tm);
         });
     }
     if (p.prescale && !ext) scale_acc();   // a split without the second segment
@@ -856,7 +928,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     epilogue_elem(p, m, n, s);
 }
 
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false>
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
@@ -893,6 +965,15 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                          "a [K][N] B operand needs buffer-addressable operands");
         }
         p.bx_bytes = p.Nx > 0 ? extent(p.Nx, p.ldbx) : 0u;
+        if (BQ == 2) {   // int8 quants (ldb bytes per row) and f16 block scales (ldbs per row)
+            const int64_t qb = (p.N - 1) * p.ldb + p.K, sb = ((p.N - 1) * p.ldbs + p.K / 32) * 2;
+            p.b_bytes = qb < ((int64_t)1 << 31) ? (uint32_t)qb : 0u;
+            p.bs_bytes = sb < ((int64_t)1 << 31) ? (uint32_t)sb : 0u;
+            SA3K_REQUIRE(p.bs_bytes != 0, "Q8_0 scales beyond a buffer descriptor's reach");
+        }
+        if (BQ != 0)
+            SA3K_REQUIRE(p.a_bytes != 0 && p.b_bytes != 0 && p.Mx == 0 && p.Nx == 0,
+                         "a decoded B operand needs buffer-addressable operands and no extra rows or columns");
         // the staged epilogue stores 4 columns at once: rows and vectors must be 16-byte (f32) /
         // 8-byte (bf16) aligned
         auto ok = [](const void* q, int64_t ld, int align) {
@@ -913,9 +994,9 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         static const std::string name = std::string("gemm_dma<") + std::to_string(BM) + "," + std::to_string(BN) + "," +
                                         std::to_string(WMW) + "," + std::to_string(STAGES) +
                                         (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (KN ? ",kn" : "") +
-                                        (BF16 ? ",bf16>" : ",f32>");
+                                        (BQ == 1 ? ",f16b" : BQ == 2 ? ",q8b" : "") + (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN>, g,
+        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ>, g,
                  dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
@@ -1011,9 +1092,20 @@ void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
     return launch_dma<128, 256, 2, 3, true, 8, true>(ctx, p);
 }
 
+// B decoded from f16 / Q8_0 on its way into the MFMAs (bf16 A): the default tile and the short-K
+// small-grid tile of the bf16 dispatch
+template <int BQ>
+void dispatch_dma_dq(sa3k_ctx* ctx, const DmaParams& p) {
+    const int64_t tiles128 = ceil_div(p.M, 128) * ceil_div(p.N, 128);
+    if (tiles128 < 384 && p.K < 4096 && ctx->gemm_small == 2) return launch_dma<64, 128, 1, 3, true, 4, false, BQ>(ctx, p);
+    return launch_dma<128, 256, 2, 3, true, 8, false, BQ>(ctx, p);
+}
+
 template <bool BF16>
 void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if constexpr (BF16) {
+        if (p.bq == 1) return dispatch_dma_dq<1>(ctx, p);
+        if (p.bq == 2) return dispatch_dma_dq<2>(ctx, p);
         if (p.b_kn) return dispatch_dma_kn(ctx, p);
         if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.Nt > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
             // 256 x 256 tiles (one per CU) where they fill the chip about as evenly as 128 x 128 tiles
@@ -1103,6 +1195,9 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.Cbn = d.Cbn; p.ldcn = d.ldcn;
     p.bx_bytes = 0;
     p.b_kn = d.b_kn;
+    p.bq = d.b_src == SRC_F16 ? 1 : d.b_src == SRC_Q8 ? 2 : 0;
+    p.Bs = d.Bs; p.ldbs = d.ldbs;
+    p.bs_bytes = 0;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

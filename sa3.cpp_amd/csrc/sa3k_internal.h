@@ -75,6 +75,7 @@ struct sa3k_ctx {
     int gemm_pd = 1;                      // GEMM global-load prefetch depth (1 or 2 K tiles)
     int gemm_split = 1;                   // allow split-K
     int gemm_dma = 1;                     // use the DMA-fed kernel for compute-type operands
+    int gemm_dq = 1;                      // bf16 products with an f16 / Q8_0 B on the DMA-fed kernel (decoded from LDS)
     int gemm_cfg = 0;                     // DMA kernel tile configuration
     int gemm_nt_store = 1;                // GEMM outputs written with non-temporal stores
     int gemm_skinny = 1;                  // products with <= 32 output columns on the skinny kernel

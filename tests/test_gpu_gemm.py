@@ -178,3 +178,34 @@ def test_big_tile_gemm(ctx, M, N, K):
     assert np.array_equal(got, again), "not deterministic"
     assert rel_err(got, ref) < 1e-5
     assert max_rel_err(got, small) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(2176, 7680, 1536), (2176, 1536, 1536), (256, 6144, 1536), (96, 384, 256)])
+@pytest.mark.parametrize("btype", ["f16", "q8_0"])
+def test_gemm_decoded_b_on_dma_kernel(ctx, M, N, K, btype):
+    """bf16 A with an f16 or Q8_0 B on the DMA-fed kernel (option gemm_dq 1: B staged in LDS as
+    stored and decoded between LDS and the MFMAs) gives the same bits as the same kernel over the
+    decoded bf16 copy (the decode is the same RNE of the exact value), and the loader-decode kernel
+    (gemm_dq 0) within fp32 accumulation order; both within 1e-5 of the float64 product."""
+    r = rng(M + 3 * N + K)
+    A = bf16_bits(r.normal(0, 1, (M, K)).astype(np.float32))
+    W = r.normal(0, 0.02, (N, K)).astype(np.float32)
+    if btype == "f16":
+        Bop, sc, ldbs, bt = W.astype(np.float16), None, 0, sa3k.TYPE_F16
+        dec = Bop.astype(np.float32)
+    else:
+        q, sc, dec = q8_0_split(oracle.q8_0_quantize(W), N, K)
+        Bop, ldbs, bt = q, K // 32, sa3k.TYPE_Q8_0
+    try:
+        ctx.set_option("gemm_big", 0)
+        got = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, bt, B_scales=sc, ldbs=ldbs)
+        copy = run(ctx, A, bf16_bits(dec), M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, sa3k.TYPE_BF16)
+        ctx.set_option("gemm_dq", 0)
+        loader = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, bt, B_scales=sc, ldbs=ldbs)
+    finally:
+        ctx.set_option("gemm_dq", 1)
+        ctx.set_option("gemm_big", 1)
+    Af = (A.astype(np.uint32) << 16).view(np.float32)
+    ref = Af.astype(np.float64) @ bf16_round(dec).astype(np.float64).T
+    assert np.array_equal(got, copy)
+    assert rel_err(got, ref) < 1e-5 and rel_err(loader, ref) < 1e-5
