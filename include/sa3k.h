@@ -88,9 +88,10 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 outputs of at most 2^18 floats, a separate launch for larger ones (default 0)
  *   "gemm_dma"    1: DMA-fed kernel for compute-type operands (default 1)
  *   "gemm_dq"     1: bf16 products with an f16 or Q8_0 B operand (no extra rows or columns) run on the
- *                 DMA-fed kernel, B staged in LDS as stored and decoded between LDS and the MFMAs;
- *                 0: the kernel that decodes on the way into LDS (default 1; both decode to the same
- *                 bf16 values, their tiles sum in different orders)
+ *                 DMA-fed kernel, B staged in LDS as stored and decoded between LDS and the MFMAs
+ *                 (2: the same with 2 x 4 waves per tile instead of 1 x 8); 0: the kernel that
+ *                 decodes on the way into LDS (default 1; all decode to the same bf16 values, the
+ *                 last one's tiles sum in another order)
  *   "gemm_cfg"    DMA kernel tile configuration: 0 (default) 128 x 256 tiles for bf16 and
  *                 128 x 128 for f32; 1: 128 x 128; 4: 128 x 256 (3 stages); 7: 128 x 256 (2 stages)
  *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot

@@ -86,7 +86,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_GEMM_SPLIT")) ctx->gemm_split = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_GEMM_FIXUP")) ctx->gemm_fixup = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_DMA")) ctx->gemm_dma = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_GEMM_DQ")) ctx->gemm_dq = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_GEMM_DQ")) ctx->gemm_dq = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_SMALL")) ctx->gemm_small = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_NT")) ctx->gemm_nt_store = std::atoi(e) != 0;
@@ -229,7 +229,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         if (n == "gemm_split") ctx->gemm_split = value != 0;
         else if (n == "gemm_fixup") ctx->gemm_fixup = value;
         else if (n == "gemm_dma") ctx->gemm_dma = value != 0;
-        else if (n == "gemm_dq") ctx->gemm_dq = value != 0;
+        else if (n == "gemm_dq") ctx->gemm_dq = value;
         else if (n == "gemm_cfg") ctx->gemm_cfg = value;
         else if (n == "gemm_small") ctx->gemm_small = value;
         else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
