@@ -138,9 +138,12 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 a K-major operand (transposed by the LDS reads), so the refresh writes one bf16
  *                 copy; 0: the refresh also writes the transposed copy [in][out] and dX reads
  *                 that (default 1). It holds from a linear's next prepare (a DiT: its setup).
+ *   "attn_fwd32"  1: attention forwards over more than 128 keys run on 32x32x16 MFMA blocks with
+ *                 one branch per wave; 0: every forward on the 16x16x32 kernel that carries both
+ *                 branches per wave (default 1)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
- * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn and
- * kv_stack, which change the f32 summation order. Not to be changed while a graph is being captured. */
+ * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
+ * kv_stack and attn_fwd32, which change the f32 summation order. Not to be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a

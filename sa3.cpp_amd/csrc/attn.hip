@@ -37,6 +37,7 @@ namespace {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
 constexpr int kThreads = 256;
@@ -336,6 +337,193 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(FwdArgs a) {
             a.o[((int64_t)b * a.Sq + q) * (a.H * HD) + h * HD + d] = (bf16)(x1 - x2);
         }
     }
+}
+
+// Forward with one branch per wave, on 32x32x16 MFMA blocks: a workgroup takes 64 queries; waves 0
+// and 1 compute branch 1 for queries 0..31 and 32..63, waves 2 and 3 branch 2 for the same queries,
+// all from the same {K1, K2, V} tiles in LDS. Half the registers of a wave that carries both
+// branches, so three waves share each SIMD and hide each other's MFMA, LDS and exp latency.
+// Every product is computed transposed so that a lane owns one query throughout:
+//   S^T[k][q] = K Q^T (A = K rows from LDS, B = Q in registers) -> lane l holds query l % 32 and
+//               keys r(v) = 8 (v/4) + 4 (l/32) + v%4 of each 32-key half, v = 0..15;
+//   O^T[d][q] += V^T P^T (A = V columns read transposed from LDS, B = P^T) -> lane l holds its own
+//               query and dims 32 db + r(v), so the softmax rescale needs no lane exchange.
+// P^T's K order is the order the lane already holds: K step j of a half takes values v = 8j..8j+7,
+// i.e. keys 16j + 4 (l/32) + {0..3} and 16j + 8 + 4 (l/32) + {0..3}, and V^T is read in that order.
+// The running maximum m moves only when a block's maximum exceeds it by more than kLazy (log2
+// units), so the O rescale runs a few times per row instead of every block; the weights 2^(c s - m)
+// stay below 2^kLazy, and O / l and lse = m + log2 l are the same quantities as with the exact
+// maximum.
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+constexpr int QW = 32;          // queries per wave
+constexpr float kLazy = 8.f;    // weights stay below 2^8
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(kThreads) void attn_fwd32_kernel(FwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 3 * BLK * ROW];   // 2 stages x {K1, K2, V}
+    int qb, bh;
+    heavy_first(qb, bh);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int br = wave >> 1;                // branch of this wave
+    const int lane = threadIdx.x & 63, hl = lane >> 5, c32 = lane & 31;
+    const int64_t qoff = (int64_t)bh * a.Sq * HD, koff = (int64_t)bh * a.Sk * HD;
+    const int q0w = qb * BLK + (wave & 1) * QW;   // this wave's first query
+    const int q = q0w + c32;                      // this lane's query
+    const float c = a.scale * kLog2e;             // > 0 (checked by the host)
+    const Span sp = visible(q, a.Sk, a.window);
+
+    // Q as the B operand: query q, dims 16 ks + 8 (l/32) .. +7
+    const bf16* qsrc = br ? a.q2 : a.q1;
+    bf16x8 qf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (q < a.Sq) u = *reinterpret_cast<const uint4*>(qsrc + qoff + (int64_t)q * HD + ks * 16 + hl * 8);
+        qf[ks] = __builtin_bit_cast(bf16x8, u);
+    }
+    f32x16 o[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] = 0.f;
+    float m = -INFINITY, l = 0.f;   // scaled running maximum of query q; this lane's partial sum
+
+    // key blocks of the workgroup's 64 queries, and the keys this wave's 32 queries see
+    int kb_lo, kb_hi;
+    band_range(qb, a.Sk, a.window, kb_lo, kb_hi);
+    int wlo = 0, whi = a.Sk;
+    if (a.window > 0) {
+        const int half = a.window / 2;
+        wlo = max(0, q0w - half);
+        whi = min(a.Sk, q0w + QW - 1 + half + 1);
+    }
+    auto issue = [&](int st, int kb) {
+        char* t = lds + st * 3 * BLK * ROW;
+        tile_dma(a.k1 + koff, a.Sk, kb * BLK, t, threadIdx.x, wave);
+        tile_dma(a.k2 + koff, a.Sk, kb * BLK, t + BLK * ROW, threadIdx.x, wave);
+        tile_dma(a.v + koff, a.Sk, kb * BLK, t + 2 * BLK * ROW, threadIdx.x, wave);
+    };
+    if (kb_lo < kb_hi) issue(0, kb_lo);
+    for (int kb = kb_lo; kb < kb_hi; ++kb) {
+        const int st = (kb - kb_lo) & 1;
+        dma_wait_all();   // block kb landed; every wave is done with block kb-1 (the other stage)
+        if (kb + 1 < kb_hi) issue(st ^ 1, kb + 1);
+        const int kbase = kb * BLK;
+        if (q0w >= a.Sq || kbase >= whi || kbase + BLK <= wlo) continue;   // nothing of this block for this wave
+        const char* kt = lds + st * 3 * BLK * ROW + br * BLK * ROW;
+        const char* vt = lds + st * 3 * BLK * ROW + 2 * BLK * ROW;
+        // S^T per 32-key half h: keys 32 h + r(v), query q
+        f32x16 s[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[h][v] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) s[h] = mfma32(ld_row(kt, 32 * h + c32, 2 * ks + hl), qf[ks], s[h]);
+        }
+        // mask only blocks that cross a window edge or a sequence end for some query of the wave
+        const bool full = q0w + QW <= a.Sq && kbase + BLK <= a.Sk &&
+                          (a.window <= 0 || 2 * max(q0w + QW - 1 - kbase, kbase + BLK - 1 - q0w) <= a.window);
+        if (!full) {
+            const int rel = kbase + 4 * hl - sp.lo;   // key 32 h + r(v), less lo
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const bool ok = (unsigned)(rel + 32 * h + 8 * (v >> 2) + (v & 3)) < (unsigned)sp.n;
+                    s[h][v] = ok ? s[h][v] : -INFINITY;
+                }
+        }
+        // block maximum of the raw scores over this lane's 32 keys and the other 32 (lane ^ 32)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[h][v]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(mx > m + kLazy) != 0, 0)) {   // (uniform) a maximum moved far
+            const float mn = fmaxf(m, mx);
+            const float al = ex2(m - (mn == -INFINITY ? 0.f : mn));   // 0 when m was -inf
+            m = mn;
+            l *= al;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[db][v] *= al;
+        }
+        // weights 2^(c s - m), the exponent as one fma of the raw score; m = -inf only while every
+        // key so far is invisible, and then every weight is 0. l sums the weights as rounded to
+        // bf16, the values the P V product uses (two per dot2 instruction).
+        const float base = m == -INFINITY ? 0.f : m;
+        bf16x8 p[2][2];   // [half][K step]: values v = 8j .. 8j+7 of the half
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) p[h][v >> 3][v & 7] = (bf16)ex2(__builtin_fmaf(s[h][v], c, -base));
+        float ps[2] = {0.f, 0.f};
+        const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ps[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[h][j][2 * e], p[h][j][2 * e + 1]}, ones, ps[e & 1],
+                                                                false);
+        l += ps[0] + ps[1];
+        // O^T += V^T P^T: dims 32 db + lane % 32 (A rows), K step j of half h in the lane's key order
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const int k0 = 32 * h + 16 * j + 4 * hl, n0 = 32 * db + 16 * ((lane >> 4) & 1);
+                    o[db] = mfma32(cat44(ld_tr(vt, k0, n0, lane), ld_tr(vt, k0 + 8, n0, lane)), p[h][j], o[db]);
+                }
+    }
+    l += __shfl_xor(l, 32, 64);
+    const bool qok = q < a.Sq;
+    if (qok && hl == 0) (br ? a.lse2 : a.lse1)[(int64_t)bh * a.Sq + q] = m + log2f(l);
+    // normalised branch output; branch 2 hands its fp32 rows to branch 1 through LDS for O = O1 - O2
+    const float il = 1.0f / l;
+    bf16* ob = (br ? a.o2 : a.o1) + qoff + (int64_t)q * HD;
+    constexpr int YS = 68;   // floats per staged row (16-byte aligned, rows 4 banks apart)
+    float* y2s = reinterpret_cast<float*>(lds) + (size_t)((wave & 1) * QW + c32) * YS;
+    __syncthreads();   // every wave is done with the K/V stages
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+            const int d0 = 32 * db + 8 * vg + 4 * hl;   // dims d0 .. d0+3 = values v = 4 vg .. 4 vg + 3
+            float4 y;
+            y.x = o[db][4 * vg] * il;
+            y.y = o[db][4 * vg + 1] * il;
+            y.z = o[db][4 * vg + 2] * il;
+            y.w = o[db][4 * vg + 3] * il;
+            if (qok) *reinterpret_cast<bf16x4*>(ob + d0) = bf16x4{(bf16)y.x, (bf16)y.y, (bf16)y.z, (bf16)y.w};
+            if (br) *reinterpret_cast<float4*>(y2s + d0) = y;
+            o[db][4 * vg] = y.x;
+            o[db][4 * vg + 1] = y.y;
+            o[db][4 * vg + 2] = y.z;
+            o[db][4 * vg + 3] = y.w;
+        }
+    __syncthreads();
+    if (br || !qok) return;
+    const int b = bh / a.H, hh = bh % a.H;
+    bf16* od = a.o + ((int64_t)b * a.Sq + q) * (a.H * HD) + hh * HD;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+            const int d0 = 32 * db + 8 * vg + 4 * hl;
+            const float4 y2 = *reinterpret_cast<const float4*>(y2s + d0);
+            *reinterpret_cast<bf16x4*>(od + d0) =
+                bf16x4{(bf16)(o[db][4 * vg] - y2.x), (bf16)(o[db][4 * vg + 1] - y2.y), (bf16)(o[db][4 * vg + 2] - y2.z),
+                       (bf16)(o[db][4 * vg + 3] - y2.w)};
+        }
 }
 
 // ------------------------------------------------------------------------------------ backward
@@ -657,9 +845,15 @@ void attn_forward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2,
     SA3K_REQUIRE(B > 0 && H > 0 && Sq > 0 && Sk > 0, "attention extents must be positive");
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     FwdArgs a{q1, k1, q2, k2, v, H, Sq, Sk, window, scale, o, o1, o2, lse1, lse2};
-    dim3 grid((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H));
     KernelScope ks(ctx, Sq == Sk ? "attn_fwd" : "attn_fwd_cross");
-    launch_k(ctx, true, attn_fwd_kernel, grid, dim3(kThreads), 0, a);
+    // the branch-per-wave kernel pays a longer prologue and epilogue per workgroup and wins from
+    // about three key blocks per workgroup on (self-attention); short key sequences keep the other
+    if (ctx->attn_fwd32 && scale > 0.f && Sk > 2 * BLK) {
+        launch_k(ctx, true, attn_fwd32_kernel, dim3((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H)), dim3(kThreads),
+                 0, a);
+    } else {
+        launch_k(ctx, true, attn_fwd_kernel, dim3((unsigned)ceil_div(Sq, BLK), (unsigned)(B * H)), dim3(kThreads), 0, a);
+    }
     SA3K_LAUNCHED();
 }
 

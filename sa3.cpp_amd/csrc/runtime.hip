@@ -80,6 +80,7 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         if (const char* e = std::getenv("SA3K_MERGE_KN")) ctx->merge_kn = std::atoi(e) != 0;
         if (const char* e = std::getenv("SA3K_TN_FUSE")) ctx->tn_fuse = std::atoi(e);
         if (const char* e = std::getenv("SA3K_KV_STACK")) ctx->kv_stack = std::atoi(e) != 0;
+        if (const char* e = std::getenv("SA3K_ATTN_FWD32")) ctx->attn_fwd32 = std::atoi(e);
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
@@ -244,6 +245,7 @@ SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
         else if (n == "merge_kn") ctx->merge_kn = value != 0;
         else if (n == "tn_fuse") ctx->tn_fuse = value;
         else if (n == "kv_stack") ctx->kv_stack = value != 0;
+        else if (n == "attn_fwd32") ctx->attn_fwd32 = value;
         else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
     });
 }

@@ -95,6 +95,7 @@ struct sa3k_ctx {
     int* tile_counters_side = nullptr;    // the same for launches on the second stream
     int tn_fuse = kFuseColred | kFuseRows; // split reductions summed in-kernel (bits kFuse*)
     int kv_stack = 1;                     // a DiT's context K/V projections as one stacked product
+    int attn_fwd32 = 1;                   // attention forward on 32x32x16 MFMA blocks, 32 queries per wave
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
                                           // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream

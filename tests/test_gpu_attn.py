@@ -5,7 +5,7 @@ arithmetic (bf16 P in the PV / dS products, fp32 accumulation) against a double-
 restatement: outputs within 2e-2 normwise relative error and cosine >= 0.9999. Shapes cover the
 DiT block's self-attention (64 memory + T tokens), its cross-attention to the conditioning tokens,
 ragged lengths, the banded window at full size (batch 2, 24 heads, 1088 tokens, windows 0 and 256,
-forward and backward) and a single-key window (closed form: O = 0)."""
+forward and backward) a single-key window (closed form: O = 0) and both forward kernels on self-attention shapes."""
 import numpy as np
 import pytest
 
@@ -51,10 +51,33 @@ def test_attention_matches_oracle(ctx, B, H, Sq, Sk, window):
 
 
 def test_attention_single_key_window(ctx):
-    # window 1: every query sees only its own key, so both branches return V and O = 0
-    B, H, S = 1, 2, 96
+    # window 1: every query sees only its own key, so both branches return V and O = 0. Both forward
+    # kernels are exact here: the lone weight rounds to bf16 1.0 and l sums it as rounded (the
+    # 32x32 kernel) or is the fp32 weight 2^0 = 1 (the 16x16 kernel). 200 keys: past the length
+    # from which the 32x32 kernel serves self-attention.
+    B, H, S = 1, 2, 200
     r = rng(5)
     X = [ctx.upload(bf16_bits(r.normal(0, 1, (B * H, S, 64)).astype(np.float32))) for _ in range(5)]
-    o, o1, o2, l1, l2 = sa3k.attn_fwd(ctx, *X, B, H, S, S, window=1)
-    assert np.max(np.abs((o.numpy().astype(np.uint32) << 16).view(np.float32))) == 0.0
-    assert np.array_equal(o1.numpy(), X[4].numpy())
+    try:
+        for fwd32 in (0, 1):
+            ctx.set_option("attn_fwd32", fwd32)
+            o, o1, o2, l1, l2 = sa3k.attn_fwd(ctx, *X, B, H, S, S, window=1)
+            assert np.max(np.abs((o.numpy().astype(np.uint32) << 16).view(np.float32))) == 0.0, fwd32
+            assert np.array_equal(o1.numpy(), X[4].numpy()), fwd32
+            assert np.array_equal(o2.numpy(), X[4].numpy()), fwd32
+    finally:
+        ctx.set_option("attn_fwd32", 1)
+
+
+@pytest.mark.parametrize("fwd32", [0, 1])
+@pytest.mark.parametrize("B,H,Sq,Sk,window", [
+    (1, 2, 256, 256, 64), (1, 1, 130, 130, 16), (1, 3, 200, 200, 0), (1, 2, 300, 300, 7), (2, 24, 1088, 1088, 256),
+])
+def test_attention_forward_kernels(ctx, fwd32, B, H, Sq, Sk, window):
+    # the 16x16 forward (both branches per wave) and the 32x32 one (one branch per wave) on the
+    # self-attention shapes the 32x32 kernel serves, each against the oracle
+    ctx.set_option("attn_fwd32", fwd32)
+    try:
+        run(ctx, B, H, Sq, Sk, window, seed=7 * Sq + window, check_bwd=False)
+    finally:
+        ctx.set_option("attn_fwd32", 1)
