@@ -657,10 +657,12 @@ int64_t ctx_tn_wgs() {
 // CU overlap each other's memory latency; more share the CU's throughput. So a CU holding w of
 // them takes about rows x max(1, w / 2) token rows of streaming time (8 bytes per element: dY or X,
 // U, the dU store), and then each column tile's last split to arrive reads splits x rs x 64 partial
-// sums (rs rows of partials) at about a CU's streaming rate (environment SA3K_TN_RED scales that
-// term, for measurement). The split count minimising the sum is taken; it keeps the busiest CU's
-// load close to the average (576 workgroups over 256 CUs put 3 on some CUs and 2 on the rest). The
-// same count serves the separate reduce launches (option tn_fuse 0), so both give the same sums.
+// sums (rs rows of partials), weighted 4: the partials' round trip through memory and the last
+// split's wait cost more than their bytes at a CU's streaming rate (weights 2-6 measured equal on
+// the DiT update, 0.2 ms under weight 1; 10 and more slower; environment SA3K_TN_RED overrides it,
+// for measurement). The split count minimising the sum is taken; it keeps the busiest CU's load
+// close to the average (576 workgroups over 256 CUs put 3 on some CUs and 2 on the rest). The same
+// count serves the separate reduce launches (option tn_fuse 0), so both give the same sums.
 int64_t tn_rows_per(int64_t cols, int64_t N, int rs) {
     const int64_t tiles = ceil_div(cols, TN_COLS);
     if (const int64_t w = ctx_tn_wgs())
@@ -676,7 +678,7 @@ int64_t tn_rows_per(int64_t cols, int64_t N, int rs) {
         const double w = (double)ceil_div(wgs, kCUs);
         static const double red_scale = [] {
             const char* e = std::getenv("SA3K_TN_RED");
-            return e ? std::atof(e) : 1.0;
+            return e ? std::atof(e) : 4.0;
         }();
         const double red = red_scale * (double)splits * rs * TN_COLS * 4.0;
         const double cost = std::max(1.0, w / 2.0) * (double)rows * TN_COLS * 8.0 + red;
