@@ -167,16 +167,19 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
     const int64_t base = (int64_t)row * dim;
     const float* mv = modv ? modv + (int64_t)(row / S) * 6 * dim : nullptr;
     const float r = rstd[row];
-    float4 dg[V], xv[V];
+    // the residual gradient is loaded with the row's other operands (one memory round trip)
+    float4 dg[V], xv[V], dr[V];
     float dot = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
         const int c = 4 * (lane + 64 * k);
         dg[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         xv[k] = dg[k];
+        dr[k] = dg[k];
         if (c < dim) {
             dg[k] = ld4(dh + base + c);
             xv[k] = ld4(x + base + c);
+            dr[k] = ld4(dres + base + c);
         }
     }
 #pragma unroll
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
         const int c = 4 * (lane + 64 * k);
         if (c >= dim) continue;
         const float4 t = map4(dg[k], xv[k], [r, k3](float d, float xx) { return r * d - k3 * xx; });
-        const float4 o = map4(ld4(dres + base + c), t, [](float a, float b) { return a + b; });
+        const float4 o = map4(dr[k], t, [](float a, float b) { return a + b; });
         st4(dx + base + c, o);
         if (du_x) st_du4(du_x + base + c, o, dsc_x, c);
         if (g_part >= 0) {
