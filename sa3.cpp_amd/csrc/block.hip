@@ -390,18 +390,27 @@ struct PrepArgs {
     int64_t ldin;         // row stride of in (parts*dim when 0)
 };
 
-// 16 lanes per (row, head), lane j holding dims 4j..4j+3 (rope_dims % 8 == 0, so a rotation pair
-// (i, i + half) is the same component of lanes j and j + half/4). Rotates y in place; lanes past
-// rope_dims keep y. sign -1: the inverse rotation.
-__device__ inline void rope4(float4& y, int d0, int rope, const float* __restrict__ row_tab, float sign) {
+// NeoX RoPE over 16 lanes per (row, head), lane j holding dims 4j..4j+3 (rope_dims % 8 == 0, so a
+// rotation pair (i, i + half) is the same component of lanes j and j + half/4).
+// The table entries of this lane (cos, sin of its four dims; lanes past rope_dims get zeros and do
+// not use them).
+__device__ inline void rope_tab4(int d0, int rope, const float* __restrict__ row_tab, float4& cs, float4& sn) {
+    const int half = rope >> 1;
+    cs = sn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (d0 >= rope) return;
+    const int i = d0 < half ? d0 : d0 - half;
+    cs = ld4(row_tab + i);
+    sn = ld4(row_tab + half + i);
+}
+// Rotates y in place with the table entries of rope_tab4; lanes past rope_dims keep y. sign -1:
+// the inverse rotation.
+__device__ inline void rope4_cs(float4& y, int d0, int rope, const float4& cs, const float4& sn, float sign) {
     const int half = rope >> 1;
     const bool rot = d0 < rope, first = d0 < half;
     const int lane = threadIdx.x & 63;
     const int src = rot ? (first ? lane + (half >> 2) : lane - (half >> 2)) : lane;
     const float4 p = make_float4(__shfl(y.x, src, 64), __shfl(y.y, src, 64), __shfl(y.z, src, 64), __shfl(y.w, src, 64));
     if (!rot) return;
-    const int i = first ? d0 : d0 - half;
-    const float4 cs = ld4(row_tab + i), sn = ld4(row_tab + half + i);
     const float ys[4] = {y.x, y.y, y.z, y.w}, ps[4] = {p.x, p.y, p.z, p.w};
     const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sign * sn.x, sign * sn.y, sign * sn.z, sign * sn.w};
     float o[4];
@@ -424,10 +433,18 @@ __global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int item
     const int b = row / a.Sx, t = row - b * a.Sx;
     const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
     const float* src = a.in + (int64_t)row * (a.ldin ? a.ldin : (int64_t)a.parts * a.dim) + h * HD + d0;
-    float4 x[5];
+    // every load (inputs, norm weights, the token's RoPE row) before the first store, so the row
+    // costs one memory round trip
+    float4 x[5], gm[5], cs, sn;
+    bool any_rope = false;
 #pragma unroll
-    for (int k = 0; k < 5; ++k)
-        if (k < a.parts) x[k] = ld4(src + (int64_t)k * a.dim);
+    for (int k = 0; k < 5; ++k) {
+        if (k >= a.parts) break;
+        x[k] = ld4(src + (int64_t)k * a.dim);
+        gm[k] = a.p[k].gamma ? ld4(a.p[k].gamma + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        any_rope |= a.p[k].gamma && a.p[k].rope;
+    }
+    if (any_rope) rope_tab4(d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, cs, sn);
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         if (k >= a.parts) break;
@@ -435,8 +452,8 @@ __global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int item
         if (a.p[k].gamma) {
             const float r = 1.0f / sqrtf(group16_sum(dot4(y, y)) / HD + a.eps);
             if (d0 == 0) a.rstd[(int64_t)item * a.parts + k] = r;
-            y = map4(y, ld4(a.p[k].gamma + d0), [r](float v, float g) { return v * r * g; });
-            if (a.p[k].rope) rope4(y, d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, 1.0f);
+            y = map4(y, gm[k], [r](float v, float g) { return v * r * g; });
+            if (a.p[k].rope) rope4_cs(y, d0, a.rope_dims, cs, sn, 1.0f);
         }
         st4(a.p[k].out + ho, y);
     }
@@ -468,21 +485,31 @@ __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int i
     const int64_t ho = (((int64_t)b * a.H + h) * a.Sx + t) * HD + d0;
     const int64_t xo = (int64_t)row * a.parts * a.dim + h * HD + d0;
     const int64_t xi = (int64_t)row * (a.ldin ? a.ldin : (int64_t)a.parts * a.dim) + h * HD + d0;
-    float4 g[5], x[5];
+    // every load (gradients, inputs, norm weights and rstd, the token's RoPE row) before the first
+    // store, so the row costs one memory round trip
+    float4 g[5], x[5], gmv[5], cs, sn;
+    float rsv[5];
+    bool any_rope = false;
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         if (k >= a.parts) break;
         g[k] = ld4(a.p[k].dy + ho);
-        if (a.p[k].gamma) x[k] = ld4(a.in + xi + (int64_t)k * a.dim);
+        if (a.p[k].gamma) {
+            x[k] = ld4(a.in + xi + (int64_t)k * a.dim);
+            gmv[k] = ld4(a.p[k].gamma + d0);
+            rsv[k] = a.rstd[(int64_t)item * a.parts + k];
+            any_rope |= a.p[k].rope != 0;
+        }
     }
+    if (any_rope) rope_tab4(d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, cs, sn);
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         if (k >= a.parts) break;
         float4 gv = g[k];
         if (a.p[k].gamma) {
-            if (a.p[k].rope) rope4(gv, d0, a.rope_dims, a.tab + (int64_t)t * a.rope_dims, -1.0f);
-            const float4 gm = ld4(a.p[k].gamma + d0);
-            const float r = a.rstd[(int64_t)item * a.parts + k];
+            if (a.p[k].rope) rope4_cs(gv, d0, a.rope_dims, cs, sn, -1.0f);
+            const float4 gm = gmv[k];
+            const float r = rsv[k];
             const float dot = group16_sum(dot4(map4(gv, gm, [](float u, float w) { return u * w; }), x[k]));
             const float c3 = r * r * r * dot / HD;
             const float4 gg = map4(gv, gm, [r](float u, float w) { return r * u * w; });
