@@ -909,13 +909,21 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     const int64_t Mt = p.M + p.Mx;
     const int64_t plane = Mt * p.Nt;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    // the partials are loaded eight splits at a time (indices past the last split re-read it and
+    // are not added), so a thread waits about splits / 8 memory round trips; the sums are added
+    // in split order from zero either way
     if (p.vec_epi) {
         const int64_t e = idx * 4;
         if (e >= plane) return;
         float4 s = make_float4(0.f, 0.f, 0.f, 0.f);   // same sums as the element path
-        for (int z = 0; z < splits; ++z) {
-            const float4 v = *reinterpret_cast<const float4*>(p.ws + (int64_t)z * plane + e);
-            s = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
+        for (int z = 0; z < splits; z += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = *reinterpret_cast<const float4*>(p.ws + (int64_t)min(z + k, splits - 1) * plane + e);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (z + k < splits) s = make_float4(s.x + v[k].x, s.y + v[k].y, s.z + v[k].z, s.w + v[k].w);
         }
         const int64_t m = e / p.Nt, n = e - m * p.Nt;
         epilogue_vec4(p, m, n, s);
@@ -923,7 +931,14 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     }
     if (idx >= plane) return;
     float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += p.ws[(int64_t)z * plane + idx];
+    for (int z = 0; z < splits; z += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = p.ws[(int64_t)min(z + k, splits - 1) * plane + idx];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (z + k < splits) s += v[k];
+    }
     const int64_t m = idx / p.Nt, n = idx - m * p.Nt;
     epilogue_elem(p, m, n, s);
 }

@@ -715,8 +715,17 @@ __global__ __launch_bounds__(kThreads) void sum_splits_kernel(const float* __res
                                                               int64_t n, float* __restrict__ y, int accumulate) {
     const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (j >= n) return;
+    // eight splits' loads in flight at a time (past the last split: re-read, not added); the sums
+    // are added in split order from zero
     float s = 0.f;
-    for (int k = 0; k < S; ++k) s += part[(int64_t)k * stride + j];
+    for (int k0 = 0; k0 < S; k0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = part[(int64_t)min(k0 + k, S - 1) * stride + j];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k0 + k < S) s += v[k];
+    }
     y[j] = accumulate ? y[j] + s : s;
 }
 
