@@ -129,6 +129,19 @@ __global__ __launch_bounds__(kThreads) void resnorm_fwd_kernel(const float* __re
             st4(xo + base + c, v[k]);
         }
     }
+    // the norm weights and modulation rows are loaded before the row sum, not after it
+    float4 gw[V], sc[V], sh[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const int c = 4 * (lane + 64 * k);
+        gw[k] = sc[k] = sh[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c >= dim) continue;
+        gw[k] = ld4(gamma + c);
+        if (sc_part >= 0) {
+            sc[k] = ld4(mv + sc_part * dim + c);
+            sh[k] = ld4(mv + (sc_part + 1) * dim + c);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < V; ++k) ss += dot4(v[k], v[k]);
     ss = wave_sum(ss);
@@ -138,10 +151,10 @@ __global__ __launch_bounds__(kThreads) void resnorm_fwd_kernel(const float* __re
     for (int k = 0; k < V; ++k) {
         const int c = 4 * (lane + 64 * k);
         if (c >= dim) continue;
-        float4 o = map4(v[k], ld4(gamma + c), [r](float a, float g) { return a * r * g; });
+        float4 o = map4(v[k], gw[k], [r](float a, float g) { return a * r * g; });
         if (sc_part >= 0) {
-            o = map4(o, ld4(mv + sc_part * dim + c), [](float a, float s) { return a * (1.0f + s); });
-            o = map4(o, ld4(mv + (sc_part + 1) * dim + c), [](float a, float s) { return a + s; });
+            o = map4(o, sc[k], [](float a, float s) { return a * (1.0f + s); });
+            o = map4(o, sh[k], [](float a, float s) { return a + s; });
         }
         st4(h + base + c, o);
     }
