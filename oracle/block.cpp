@@ -7,6 +7,7 @@
 //   x1  = x + dit_lin(diff_attn(q,k,v,qd,kd)) * sigmoid(1 - g_a)              (src/dit.h:222-223)
 //   hc  = rms(x1) * cross_g; cq,cqd = rms_head(dit_lin(hc)); ck,ckd,cv from dit_lin(context)
 //   x2  = x1 + dit_lin(diff_attn(cq,ck,cv,cqd,ckd))                           (src/dit.h:226-242)
+//         [+ ladd: the inpaint local add, zero on the memory rows                (src/dit.h:244-254)]
 //   f   = rms(x2) * ff_g * (1 + sc_f) + sh_f; f = dit_lin(f) + b; f = val * silu(glu)
 //   out = x2 + (dit_lin(f) + b) * sigmoid(1 - g_f)                            (src/dit.h:257-265)
 // RoPE is ggml's NEOX mode on the first rope_dims of each head, positions 0..S-1, theta_i =
@@ -248,6 +249,8 @@ static void block_forward(const orc_block* p, const float* xin, const float* ctx
     const dvec yc = lin_fwd(mk(p, 4), f.oc, N);
     f.x2.resize((size_t)N * dim);
     for (size_t i = 0; i < f.x2.size(); ++i) f.x2[i] = f.x1[i] + yc[i];
+    if (p->ladd)
+        for (size_t i = 0; i < f.x2.size(); ++i) f.x2[i] += (double)p->ladd[i];
     // feed-forward
     rms_fwd(f.x2, N, dim, p->ff_g, eps, f.fn, f.rs_f);
     f.f_in.resize((size_t)N * dim);
@@ -322,6 +325,8 @@ void orc_block_bwd(const orc_block* p, const float* x, const float* ctxin, const
     dvec t;
     rms_bwd(f.x2, f.rs_f, N, dim, p->ff_g, dfn, t);
     for (size_t i = 0; i < dx2.size(); ++i) dx2[i] += t[i];
+    if (p->dladd)   // x2 = x1 + yc + ladd: the local add receives dx2
+        for (size_t i = 0; i < dx2.size(); ++i) p->dladd[i] = (float)dx2[i];
     // x2 = x1 + yc
     dvec dx1 = dx2;
     const dvec doc = lin_bwd(mk(p, 4), f.oc, N, dx2, dA[4], dB[4], dm[4]);

@@ -19,7 +19,8 @@ class OrcBlock(C.Structure):
                 ("ssg", C.c_void_p), ("pre_g", C.c_void_p), ("cross_g", C.c_void_p), ("ff_g", C.c_void_p),
                 ("sq_g", C.c_void_p), ("sk_g", C.c_void_p), ("cq_g", C.c_void_p), ("ck_g", C.c_void_p),
                 ("W", P7), ("bias", P7), ("A", P7), ("Bm", P7), ("mag", P7), ("bnsq", P7),
-                ("rank", C.c_int), ("dora", C.c_int), ("scale", C.c_float)]
+                ("rank", C.c_int), ("dora", C.c_int), ("scale", C.c_float),
+                ("ladd", C.c_void_p), ("dladd", C.c_void_p)]
 
 
 def _declare():

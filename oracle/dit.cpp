@@ -5,7 +5,9 @@
 //             glob) + te, gcond = mlp(gce, g), context = mlp(cond_embed, cross);
 //             x = dit_lin(pre_conv, x_t) + x_t; x = dit_lin(proj_in, x); x0 = [memory tokens; x]
 //             (mlp_silu, src/dit.h:269-274: lin -> silu -> lin, biases on time_embed and gce)
-//   blocks    orc_block_fwd / orc_block_bwd (block.cpp) for l = 0..depth-1
+//   blocks    orc_block_fwd / orc_block_bwd (block.cpp) for l = 0..depth-1; with inpaint local
+//             conditioning each block adds le = mlp(local, local_cond) (local.0 -> silu -> local.2,
+//             both with biases) to its T latent rows after the cross-attention (src/dit.h:244-254)
 //   dit_tail  (src/dit.h:316-325)  drop memory tokens, v = dit_lin(proj_out, x);
 //             v = dit_lin(post_conv, v) + v
 //   loss      sum((v - target)^2) / (io*T), or sum((v - target)^2 * w_frame) with a loss weight
@@ -103,10 +105,20 @@ void orc_expo_features(float t, float* out, int dim, float min_f, float max_f) {
 void orc_dit_loss(const orc_dit* p, const float* x_t, const float* target, const float* t, const float* cross,
                   const float* glob, const float* loss_weight, float* velocity, double* loss,
                   float* const* dA_blocks, float* const* dB_blocks, float* const* dm_blocks,
-                  float* const* dA_head, float* const* dB_head, float* const* dm_head) {
+                  float* const* dA_head, float* const* dB_head, float* const* dm_head,
+                  float* const* dA_local, float* const* dB_local, float* const* dm_local) {
     const int B = p->B, T = p->T, Ctx = p->Ctx, io = p->io, dim = p->dim, mem = p->mem, S = mem + T;
     const bool grad = dA_blocks != nullptr;
+    const bool local = p->local_dim > 0 && p->local && p->local_cond;
     auto hl = [&](int i) { return L{&p->head[i], p->rank, p->dora, p->scale}; };
+    auto ll = [&](int l, int k) { return L{&p->local[2 * l + k], p->rank, p->dora, p->scale}; };
+    std::vector<float*> dAl((size_t)2 * p->depth, nullptr), dBl = dAl, dml = dAl;
+    if (grad && local)
+        for (size_t i = 0; i < dAl.size(); ++i) {
+            dAl[i] = dA_local ? dA_local[i] : nullptr;
+            dBl[i] = dB_local ? dB_local[i] : nullptr;
+            dml[i] = dm_local ? dm_local[i] : nullptr;
+        }
     float* const* dAh = dA_head;
     float* const* dBh = dB_head;
     std::vector<float*> dmh_v(ORC_NHEAD, nullptr), dmb_v((size_t)7 * p->depth, nullptr);
@@ -133,14 +145,28 @@ void orc_dit_loss(const orc_dit* p, const float* x_t, const float* target, const
         std::vector<fvec> xs(p->depth + 1, fvec((size_t)S * dim));
         std::memcpy(xs[0].data(), p->memory_tokens, sizeof(float) * mem * dim);
         std::memcpy(xs[0].data() + (size_t)mem * dim, xi.data(), sizeof(float) * T * dim);
-        // ---- blocks
+        // ---- blocks (with the local conditioning's per-block MLP, added to the latent rows)
         std::vector<orc_block> bl(p->depth);
+        std::vector<Mlp> lm(local ? p->depth : 0);
+        std::vector<fvec> ladd(local ? p->depth : 0), dladd(local ? p->depth : 0);
+        fvec lc;
+        if (local) lc.assign(p->local_cond + (size_t)b * T * p->local_dim, p->local_cond + (size_t)(b + 1) * T * p->local_dim);
         for (int l = 0; l < p->depth; ++l) {
             bl[l] = p->blocks[l];
             bl[l].B = 1; bl[l].S = S; bl[l].Ctx = Ctx; bl[l].dim = dim; bl[l].heads = p->heads;
             bl[l].inner = p->inner; bl[l].rope_dims = p->rope_dims; bl[l].window = p->window;
             bl[l].rope_base = p->rope_base; bl[l].norm_eps = p->norm_eps; bl[l].qk_eps = p->qk_eps;
             bl[l].rank = p->rank; bl[l].dora = p->dora; bl[l].scale = p->scale;
+            bl[l].ladd = nullptr;
+            bl[l].dladd = nullptr;
+            if (local) {
+                lm[l] = mlp_fwd(ll(l, 0), ll(l, 1), lc, T);
+                ladd[l].assign((size_t)S * dim, 0.0f);
+                std::memcpy(ladd[l].data() + (size_t)mem * dim, lm[l].y.data(), sizeof(float) * T * dim);
+                dladd[l].resize((size_t)S * dim);
+                bl[l].ladd = ladd[l].data();
+                bl[l].dladd = dladd[l].data();
+            }
             orc_block_fwd(&bl[l], xs[l].data(), ce.y.data(), gc.y.data(), xs[l + 1].data());
         }
         // ---- tail
@@ -177,6 +203,11 @@ void orc_dit_loss(const orc_dit* p, const float* x_t, const float* target, const
                           dA_blocks + (size_t)l * 7, dB_blocks + (size_t)l * 7, dmb_v.data() + (size_t)l * 7);
             for (size_t i = 0; i < dctx.size(); ++i) dctx[i] += tc[i];
             for (size_t i = 0; i < dgc.size(); ++i) dgc[i] += tg[i];
+            if (local) {   // le enters the latent rows: its gradient is dladd there
+                const fvec dle(dladd[l].begin() + (size_t)mem * dim, dladd[l].end());
+                mlp_bwd(ll(l, 0), ll(l, 1), lm[l], lc, T, dle, nullptr, dAl.data(), dBl.data(), dml.data(), 2 * l,
+                        2 * l + 1);
+            }
             dx.swap(dxn);
         }
         // ---- head backward

@@ -4,6 +4,8 @@ the rest of oracle/.
 A model is a dict of float32 numpy arrays keyed by the reference's GGUF tensor names
 (dit.memory_tokens, dit.pre_conv.weight, dit.<l>.self.qkv.weight, dit.<l>.ssg, ...), adapters a
 dict weight name -> (A [r][in], B [out][r], magnitude [out] or None) for the selected targets.
+A config with local_dim > 0 adds the inpaint local-conditioning linears dit.<l>.local.{0,2}
+(weights and biases, src/dit.h:244-254); the step inputs then carry "local" [B][T][local_dim].
 """
 import ctypes as C
 
@@ -32,7 +34,8 @@ class OrcDit(C.Structure):
                                        "time_dim", "rope_dims", "window")] + \
                [(n, C.c_float) for n in ("rope_base", "norm_eps", "qk_eps", "time_min_freq", "time_max_freq")] + \
                [("blocks", C.c_void_p), ("head", OrcLin * 12), ("memory_tokens", C.c_void_p),
-                ("rank", C.c_int), ("dora", C.c_int), ("scale", C.c_float)]
+                ("rank", C.c_int), ("dora", C.c_int), ("scale", C.c_float),
+                ("local_dim", C.c_int), ("local", C.c_void_p), ("local_cond", C.c_void_p)]
 
 
 def tensor_shapes(cfg):
@@ -56,6 +59,11 @@ def tensor_shapes(cfg):
         for k, n in BLOCK_VECTORS.items():
             if k != "ssg":
                 s[p + n] = (d,) if k in ("pre_g", "cross_g", "ff_g") else (64,)
+        if cfg.get("local_dim", 0) > 0:
+            s[p + "local.0.weight"] = (d, cfg["local_dim"])
+            s[p + "local.0.bias"] = (d,)
+            s[p + "local.2.weight"] = (d, d)
+            s[p + "local.2.bias"] = (d,)
     return s
 
 
@@ -64,6 +72,8 @@ def target_names(cfg, scope="full"):
     names = [f"dit.{l}.{t}.weight" for l in range(cfg["depth"]) for t in BLOCK_TARGETS]
     if scope == "full":
         names += [f"dit.{t}.weight" for t in HEAD_TARGETS]
+        if cfg.get("local_dim", 0) > 0:   # "core" drops local.{0,2} (src/train_lora.h:85-89)
+            names += [f"dit.{l}.local.{k}.weight" for l in range(cfg["depth"]) for k in (0, 2)]
     return sorted(names)
 
 
@@ -96,6 +106,8 @@ def random_dit(seed, cfg, scope="full", w_sd=0.05, b_sd=0.05):
     inputs = dict(x_t=nd((B, T, cfg["io"]), 1.0), target=nd((B, T, cfg["io"]), 1.0),
                   t=g.uniform(0, 1, B).astype(np.float32), cross=nd((B, Ctx, cfg["cond_dim"]), 1.0),
                   glob=nd((B, cfg["cond_dim"]), 1.0))
+    if cfg.get("local_dim", 0) > 0:
+        inputs["local"] = nd((B, T, cfg["local_dim"]), 1.0)
     return tensors, adapters, inputs
 
 
@@ -127,7 +139,7 @@ def dit_loss(cfg, tensors, adapters, inputs, loss_weight=None, grad=True):
     L = lib()
     if not getattr(L, "_dit_declared", False):
         L.orc_dit_loss.restype = None
-        L.orc_dit_loss.argtypes = [C.POINTER(OrcDit)] + [C.c_void_p] * 14
+        L.orc_dit_loss.argtypes = [C.POINTER(OrcDit)] + [C.c_void_p] * 17
         L._dit_declared = True
     dora = int(cfg["dora"])
     depth = cfg["depth"]
@@ -166,6 +178,19 @@ def dit_loss(cfg, tensors, adapters, inputs, loss_weight=None, grad=True):
         st.head[i] = OrcLin(p(W), p(bias), p(ad[0]) if ad else None, p(ad[1]) if ad else None,
                             p(ad[2]) if (ad and dora) else None, p(bnsq_of(W)) if (ad and dora) else None,
                             W.shape[1], W.shape[0])
+    ldim = cfg.get("local_dim", 0)
+    lnames = [f"dit.{l}.local.{k}.weight" for l in range(depth) for k in (0, 2)] if ldim > 0 else []
+    locs = (OrcLin * max(len(lnames), 1))()
+    for i, wn in enumerate(lnames):
+        W = tensors[wn]
+        ad = adapters.get(wn)
+        locs[i] = OrcLin(p(W), p(tensors[wn[:-len("weight")] + "bias"]), p(ad[0]) if ad else None,
+                         p(ad[1]) if ad else None, p(ad[2]) if (ad and dora) else None,
+                         p(bnsq_of(W)) if (ad and dora) else None, W.shape[1], W.shape[0])
+    use_local = ldim > 0 and inputs.get("local") is not None
+    st.local_dim = ldim if use_local else 0
+    st.local = C.cast(locs, C.c_void_p) if use_local else None
+    st.local_cond = p(inputs["local"]) if use_local else None
     B = cfg["B"]
     loss = np.zeros(B, np.float64)
     vel = np.zeros((B, cfg["T"], cfg["io"]), np.float32)
@@ -178,8 +203,9 @@ def dit_loss(cfg, tensors, adapters, inputs, loss_weight=None, grad=True):
         hd = [f"dit.{t}.weight" for t in HEAD_TARGETS]
         pick = lambda names, j: arr([ptr(grads[n][j]) if n in grads else None for n in names])
         gargs = [pick(bl, 0), pick(bl, 1), pick(bl, 2), pick(hd, 0), pick(hd, 1), pick(hd, 2)]
+        gargs += [pick(lnames, 0), pick(lnames, 1), pick(lnames, 2)] if lnames else [None] * 3
     else:
-        gargs = [None] * 6
+        gargs = [None] * 9
     x, tg, t, cr, gl = (f32(inputs[k]) for k in ("x_t", "target", "t", "cross", "glob"))
     lw = f32(loss_weight) if loss_weight is not None else None
     L.orc_dit_loss(C.byref(st), x.ctypes.data, tg.ctypes.data, t.ctypes.data, cr.ctypes.data, gl.ctypes.data,

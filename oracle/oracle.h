@@ -119,6 +119,11 @@ typedef struct orc_block {
     const float* bnsq[7];
     int rank, dora;
     float scale;
+    /* inpaint local add (src/dit.h:244-254), NULL when absent: ladd [B][S][dim] is added to the
+     * residual after the cross-attention (memory rows hold zeros); the backward writes the
+     * gradient of that sum (the feed-forward input) to dladd [B][S][dim] when non-NULL */
+    const float* ladd;
+    float* dladd;
 } orc_block;
 /* the block's NEOX rotary (rope_dims of each 64-wide head vector, positions pos[j]), exported for tests */
 void orc_rope_neox(float* v, int n, int rope, const float* pos, float base);
@@ -143,15 +148,23 @@ typedef struct orc_dit {
     const float* memory_tokens;  /* [mem][dim] */
     int rank, dora;
     float scale;
+    /* inpaint local conditioning (src/dit.h:244-254): local [depth*2] = per block local.0
+     * (local_dim -> dim, bias) and local.2 (dim -> dim, bias); local_cond [B][T][local_dim]. Both
+     * NULL (or local_dim 0): no local add. The local linears' adapters follow the blocks' rules. */
+    int local_dim;
+    const orc_lin* local;
+    const float* local_cond;
 } orc_dit;
 /* Forward to the per-sample losses (loss [B]) and, if dA_* is non-NULL, the backward: adapter
- * gradients of sum_b loss_b ADDED to dA/dB/dm (blocks: [depth*7], head: [ORC_NHEAD], entries of
- * un-adapted linears ignored). x_t, target [B][T][io]; t [B]; cross [B][Ctx][cond_dim]; glob
+ * gradients of sum_b loss_b ADDED to dA/dB/dm (blocks: [depth*7], head: [ORC_NHEAD], local:
+ * [depth*2] (NULL arrays allowed when there is no local add), entries of un-adapted linears
+ * ignored). x_t, target [B][T][io]; t [B]; cross [B][Ctx][cond_dim]; glob
  * [B][cond_dim]; loss_weight [B][T] or NULL (uniform 1/(io*T)); velocity [B][T][io] nullable. */
 void orc_dit_loss(const orc_dit* p, const float* x_t, const float* target, const float* t, const float* cross,
                   const float* glob, const float* loss_weight, float* velocity, double* loss,
                   float* const* dA_blocks, float* const* dB_blocks, float* const* dm_blocks,
-                  float* const* dA_head, float* const* dB_head, float* const* dm_head);
+                  float* const* dA_head, float* const* dB_head, float* const* dm_head,
+                  float* const* dA_local, float* const* dB_local, float* const* dm_local);
 /* ExpoFourierFeatures of t into out[dim] (expo_features, src/sa3_pipeline.h:57-67) */
 void orc_expo_features(float t, float* out, int dim, float min_f, float max_f);
 

@@ -49,7 +49,7 @@ def attn(q, k, v, qd, kd, window):
     return br(q, k) - br(qd, kd)
 
 
-def block(cfg, w, A, Bm, mag, x, ctx, gc):
+def block(cfg, w, A, Bm, mag, x, ctx, gc, ladd=None):
     B, S, Ctx, dim, H, I = cfg["B"], cfg["S"], cfg["Ctx"], cfg["dim"], cfg["heads"], cfg["inner"]
     s = cfg["alpha"] / cfg["rank"]
     dora = cfg["dora"]
@@ -72,6 +72,8 @@ def block(cfg, w, A, Bm, mag, x, ctx, gc):
     ck, ckd = qn(hd(kv[..., :dim], Ctx), w["ck_g"], 0), qn(hd(kv[..., dim:2 * dim], Ctx), w["ck_g"], 0)
     cv = hd(kv[..., 2 * dim:], Ctx)
     x2 = x1 + L(4, attn(cq, ck, cv, cqd, ckd, 0).transpose(1, 2).reshape(B, S, dim))
+    if ladd is not None:   # inpaint local add after the cross-attention (src/dit.h:244-254)
+        x2 = x2 + ladd
     f = rms(x2, T(w["ff_g"]), 1e-5) * (1 + m[3]) + m[4]
     F = L(5, f)
     g = F[..., :I] * torch.nn.functional.silu(F[..., I:])

@@ -1,7 +1,9 @@
 """Write tests/golden/dit_autograd.npz: the whole DiT training loss (dit_head, dit_block x depth,
 dit_tail, src/dit.h:269-338; MSE src/train_dit.h:174-184) of a depth-2 model and every adapter
 gradient, from torch float64 autograd of a torch restatement that shares nothing with the
-oracle's hand-derived backward. Build-container only; the GPU tests never import torch.
+oracle's hand-derived backward; and tests/golden/dit_local_autograd.npz: the same for a model
+with the inpaint local conditioning (dit.<l>.local.{0,2}, src/dit.h:244-254) and its per-block
+MLP adapted in the full scope. Build-container only; the GPU tests never import torch.
 
 python tests/golden/make_dit_fixtures.py
 """
@@ -20,6 +22,9 @@ from make_block_fixtures import T, block, lin  # noqa: E402
 CFG = dict(B=2, T=12, Ctx=5, io=64, dim=128, heads=2, inner=128, depth=2, mem=4, cond_dim=64, time_dim=64,
            rope_dims=32, window=0, rank=8, alpha=16.0, dora=True)
 CASES = {"full_dora_dense": (41, "full", True, 0, False), "core_lora_band_weighted": (42, "core", False, 6, True)}
+# local_dim 65 = [mask | z * mask] over io 64 channels (src/train_inpaint.h:165-194)
+LOCAL_CASES = {"full_dora_local": (43, "full", True, 0, False, 65),
+               "core_lora_band_local_weighted": (44, "core", False, 6, True, 65)}
 
 
 def expo(t, dim, lo=0.5, hi=1e4):
@@ -59,6 +64,7 @@ def model_loss(cfg, tensors, ad, inputs, lw):
         gc = mlp("gce", g, True)                                      # [1, 6dim]
         ctx = mlp("cond_embed", T(inputs["cross"][b]), False)[None]   # [1, Ctx, dim]
         xin = T(inputs["x_t"][b])
+        lc = T(inputs["local"][b]) if cfg.get("local_dim", 0) > 0 else None
         x = L("dit.pre_conv.weight", xin) + xin
         x = L("dit.proj_in.weight", x)
         x = torch.cat([T(tensors["dit.memory_tokens"]), x], 0)[None]
@@ -72,7 +78,11 @@ def model_loss(cfg, tensors, ad, inputs, lw):
             Bm = [ad[p + t + ".weight"][1] for t in BLOCK_TARGETS]
             mg = [ad[p + t + ".weight"][2] for t in BLOCK_TARGETS]
             bc = dict(cfg, B=1, S=mem + Tn)
-            x = block(bc, w, A, Bm, mg, x, ctx, gc)
+            ladd = None
+            if lc is not None:   # le = local.2(silu(local.0(lc))), added to the latent rows only
+                le = mlp(f"{l}.local", lc, True)
+                ladd = torch.cat([torch.zeros(mem, dim, dtype=torch.float64), le], 0)[None]
+            x = block(bc, w, A, Bm, mg, x, ctx, gc, ladd)
         v = L("dit.proj_out.weight", x[0, mem:])
         v = L("dit.post_conv.weight", v) + v
         d2 = (v - T(inputs["target"][b])) ** 2
@@ -82,8 +92,8 @@ def model_loss(cfg, tensors, ad, inputs, lw):
     return total, np.array(losses)
 
 
-def case(seed, scope, dora, window, weighted):
-    cfg = dict(CFG, dora=dora, window=window)
+def case(seed, scope, dora, window, weighted, local_dim=0):
+    cfg = dict(CFG, dora=dora, window=window, local_dim=local_dim)
     tensors, adapters, inputs = random_dit(seed, cfg, scope)
     ad = {n: (T(a).requires_grad_(), T(b).requires_grad_(), T(m).requires_grad_() if m is not None else None)
           for n, (a, b, m) in adapters.items()}
@@ -110,6 +120,12 @@ def main():
         for k, v in case(*args).items():
             flat[f"{name}/{k}"] = v
     np.savez_compressed(os.path.join(HERE, "dit_autograd.npz"), **flat)
+    print("wrote", len(flat), "arrays")
+    flat = {}
+    for name, args in LOCAL_CASES.items():
+        for k, v in case(*args).items():
+            flat[f"{name}/{k}"] = v
+    np.savez_compressed(os.path.join(HERE, "dit_local_autograd.npz"), **flat)
     print("wrote", len(flat), "arrays")
 
 
