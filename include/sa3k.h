@@ -430,10 +430,13 @@ SA3K_API int sa3k_block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* ws
 /* ---------------------------------------------------------------- C4: the DiT training step */
 
 /* DitConfig (src/dit.h:20-46) of a differential DiT, plus the feed-forward inner width and the
- * self-attention window of this build (0 = dense, the reference). */
+ * self-attention window of this build (0 = dense, the reference). local_dim > 0 (dit.local_dim,
+ * src/dit.h:29-30; 257 in the inpaint model) adds each block's inpaint local-conditioning linears
+ * dit.<l>.local.0 [dim][local_dim] and dit.<l>.local.2 [dim][dim], with biases (src/dit.h:244-254). */
 typedef struct {
     int io, dim, depth, heads, head_dim, cond_dim, mem_tokens, rope_dims, time_dim, inner, window;
     float rope_base, norm_eps, qk_eps, time_min_freq, time_max_freq;
+    int local_dim;
 } sa3k_dit_config;
 
 /* The training setup: adapter family and scope (TrainLoraScope, src/train_lora.h:53-97), the
@@ -524,6 +527,15 @@ SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
  * the B per-sample losses; synchronises the stream. */
 SA3K_API int sa3k_dit_eval_loss(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* target, const float* t,
                                 const float* cross, const float* glob, const float* loss_weight, double* loss_out);
+/* Bind the inpaint local conditioning [B][T][local_dim] f32 (device; TrainInpaint::local,
+ * src/train_inpaint.h:155-194, set as TrainDitGraph::local by run_train_dit_accumulate,
+ * src/train_loop.h:239-242) for the following sa3k_dit_accumulate / sa3k_dit_eval_loss /
+ * sa3k_dit_forward calls: each block then adds local.2(silu(local.0(local))) to its T latent rows
+ * after the cross-attention (src/dit.h:244-254), and in the full scope the local linears' adapters
+ * receive gradients. NULL (the default) runs the model without the local add, as the reference's
+ * non-inpaint graph does (their adapters then get no gradient). The memory must stay valid and
+ * unchanged until the calls that use it have finished. */
+SA3K_API int sa3k_dit_set_local(sa3k_ctx* ctx, sa3k_dit* dit, const float* local);
 /* Forward only: velocity [B][T][io] (dit_forward, src/dit.h:327-338). */
 SA3K_API int sa3k_dit_forward(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* t, const float* cross,
                               const float* glob, float* velocity);

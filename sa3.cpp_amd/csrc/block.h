@@ -31,6 +31,10 @@ struct sa3k_block_ws {
     const float* kv_ext = nullptr; int64_t kv_ld = 0;
     sa3k::bf16* oc; sa3k::bf16 *co1, *co2; float *cl1, *cl2; float* x2; float* rs_f; sa3k::bf16* fin; float* F;
     sa3k::bf16* g; float* yf;
+    // inpaint local conditioning (src/dit.h:244-254), set by the caller per block or null: the
+    // forward adds ladd [B][ladd_T][dim] to the latent rows (the last ladd_T of each sample's S)
+    // after the cross-attention; the backward writes the gradient of that sum to dladd (same shape)
+    const float* ladd = nullptr; float* dladd = nullptr; int ladd_T = 0;
     // scratch of the forward (yc) and the backward: may be shared by several workspaces that are
     // used one at a time on the same stream
     float* yc;

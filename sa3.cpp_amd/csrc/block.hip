@@ -373,6 +373,26 @@ __global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __r
     }
 }
 
+// ---------------------------------------------------------------- inpaint local add (src/dit.h:244-254)
+// y[b][S - T + t] += le[b][t] (the T latent rows of each sample; the memory rows get nothing), and
+// its backward: dle[b][t] = dx[b][S - T + t]; 4 columns per thread (dim % 4 == 0)
+__global__ void local_add_kernel(const float* __restrict__ le, int S, int T, int dim, int n4, float* __restrict__ y) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n4) return;
+    const int q = dim / 4, row = i / q, b = row / T, t = row - b * T;
+    float4* dst = reinterpret_cast<float4*>(y + ((int64_t)b * S + (S - T) + t) * dim) + (i - row * q);
+    const float4 a = reinterpret_cast<const float4*>(le)[i], c = *dst;
+    *dst = make_float4(c.x + a.x, c.y + a.y, c.z + a.z, c.w + a.w);
+}
+
+__global__ void local_grad_kernel(const float* __restrict__ dx, int S, int T, int dim, int n4, float* __restrict__ dle) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n4) return;
+    const int q = dim / 4, row = i / q, b = row / T, t = row - b * T;
+    reinterpret_cast<float4*>(dle)[i] =
+        reinterpret_cast<const float4*>(dx + ((int64_t)b * S + (S - T) + t) * dim)[i - row * q];
+}
+
 // ---------------------------------------------------------------- q/k-norm + RoPE prep
 // RoPE table of one sequence length: tab[t][i] = cos(theta), tab[t][half + i] = sin(theta),
 // theta = t * base^(-2i/rope), i < half = rope/2 (pairs (i, i + half) of NEOX rotation)
@@ -842,6 +862,11 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         arm();
         attn_forward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, B, H, S, Ctx, 0, scale, w->oc, w->co1, w->co2, w->cl1, w->cl2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, nullptr, w->yc));
+        if (w->ladd) {   // inpaint local add: yc += [0; le] (x2 below then carries it)
+            SA3K_REQUIRE(w->ladd_T > 0 && w->ladd_T <= S, "local conditioning frames exceed the sequence");
+            const int n4 = (int)((int64_t)B * w->ladd_T * D / 4);
+            launch(ctx, "blk_local", local_add_kernel, dim3(nblk(n4)), w->ladd, S, w->ladd_T, D, n4, w->yc);
+        }
         // feed-forward: x2 = x1 + yc, fin = rms_norm(x2) * ff_g * (1 + sc_f) + sh_f
         arm();
         resnorm(w->x1, w->yc, -1, w->x2, b->ff_g, 3, w->fin, w->rs_f);
@@ -896,6 +921,12 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         lin_backward_du(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dfin, 0, dA[5], dB[5], dmt[5]);
         colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
         norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, b->L[4], nullptr);
+        if (w->dladd) {   // the local add's gradient: the latent rows of dx2
+            SA3K_REQUIRE(w->ladd_T > 0 && w->ladd_T <= S, "local conditioning frames exceed the sequence");
+            const int n4 = (int)((int64_t)B * w->ladd_T * D / 4);
+            launch(ctx, "blk_local", local_grad_kernel, dim3(nblk(n4)), (const float*)w->dx2, S, w->ladd_T, D, n4,
+                   w->dladd);
+        }
         // x2 = x1 + yc
         lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4]);
         attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,

@@ -214,6 +214,38 @@ __global__ void mse_sum_kernel(const double* __restrict__ part, int nch, int B, 
     loss[b] = s;
 }
 
+// ---------------------------------------------------------------- inpaint local conditioning
+// local.0 takes local_dim inputs (1 + io: the mask and the masked latents, src/train_inpaint.h:
+// 165-194), which the MFMA products take in whole 64-column steps: its weight, its A and its input
+// are kept with kp = local_dim rounded up to 64 columns, the extra columns zero. They add exact
+// zeros to every product, and their dA columns are zero (dA = (s B^T dU)^T X plus DoRA terms in
+// W_eff, all of which vanish on a zero column).
+template <class E>
+__global__ void pad_cols_kernel(const E* __restrict__ src, int64_t rows, int64_t cols, int64_t ld, E* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= rows * ld) return;
+    const int64_t r = i / ld, c = i - r * ld;
+    dst[i] = c < cols ? src[r * cols + c] : E(0);
+}
+
+// A of block y's local.0 from the arena ([rank][cols] at off[y]) into dst[y] ([rank][ld])
+__global__ void pad_a_kernel(const float* __restrict__ p, const int64_t* __restrict__ off, int rank, int cols, int ld,
+                             float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= (int64_t)rank * ld) return;
+    const int64_t r = i / ld, c = i - r * ld;
+    dst[(int64_t)blockIdx.y * rank * ld + i] = c < cols ? p[off[blockIdx.y] + r * cols + c] : 0.0f;
+}
+
+// g[rank][cols] += src[rank][ld] over the first cols columns; src is cleared for the next backward
+__global__ void fold_a_kernel(float* __restrict__ src, int rank, int cols, int ld, float* __restrict__ g) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= (int64_t)rank * ld) return;
+    const int64_t r = i / ld, c = i - r * ld;
+    if (c < cols) g[r * cols + c] += src[i];
+    src[i] = 0.0f;
+}
+
 // ---------------------------------------------------------------- model description
 enum HeadIdx { H_PRE_CONV, H_PROJ_IN, H_TIME0, H_TIME2, H_GLOBAL0, H_GLOBAL2, H_GCE0, H_GCE2, H_COND0, H_COND2,
                H_PROJ_OUT, H_POST_CONV, H_N };
@@ -221,6 +253,7 @@ const char* const kHeadNames[H_N] = {"pre_conv", "proj_in", "time_embed.0", "tim
                                      "global_embed.2", "gce.0", "gce.2", "cond_embed.0", "cond_embed.2", "proj_out",
                                      "post_conv"};
 const char* const kBlockTargets[7] = {"self.qkv", "self.out", "cross.q", "cross.kv", "cross.out", "ff.proj", "ff.out"};
+const char* const kLocalNames[2] = {"local.0", "local.2"};
 const char* const kBlockVecs[8] = {"ssg", "pre_norm.gamma", "cross_norm.gamma", "ff_norm.gamma", "self.q_norm.gamma",
                                    "self.k_norm.gamma", "cross.q_norm.gamma", "cross.k_norm.gamma"};
 
@@ -242,6 +275,7 @@ struct Target {
     int64_t in = 0, out = 0, off_a = -1, off_b = -1, off_m = -1;
     sa3k_lin* lin = nullptr;
     const float* bnsq = nullptr;
+    const float* a_src = nullptr;   // the A the adapted linear reads when it is not the arena's (padded)
 };
 
 }  // namespace
@@ -272,6 +306,22 @@ struct sa3k_dit {
     int count = 0;
     LinGroup* group = nullptr;      // every adapted linear, refreshed together
     LinStack* kvs = nullptr;        // the blocks' context K/V projections as one product (or null)
+    // inpaint local conditioning (cfg.local_dim > 0): per block local.0 (local_dim -> dim, its
+    // input padded to kp columns) and local.2 (dim -> dim), both with biases, adapted in the full
+    // scope; index 2 l + k
+    int kp = 0;
+    std::vector<sa3k_weight*> lw;
+    std::vector<sa3k_lin*> ll;
+    std::vector<float*> lbnsq;
+    std::vector<const float*> lbias;
+    std::vector<int> local_target;  // index into targets or -1
+    float* lA = nullptr;            // [depth][rank][kp] local.0's A, the arena's rows padded
+    float* ldA = nullptr;           // [rank][kp] local.0's dA of one backward, padded
+    int64_t* lA_off = nullptr;      // [depth] arena offsets of local.0's A
+    const float* local_in = nullptr;  // bound conditioning [B][T][local_dim] (device) or null
+    float* lc = nullptr;            // [B*T][kp] the padded conditioning of the current step
+    std::vector<float*> lh, la, le;   // [depth] x [B*T][dim]: local.0 output, its silu, local.2 output
+    float *dle = nullptr, *dla = nullptr, *dlh = nullptr;   // [B*T][dim] backward scratch
     // activations
     std::vector<sa3k_block_ws*> ws;
     std::vector<float*> xs;
@@ -285,7 +335,7 @@ struct sa3k_dit {
     // second-stream branches one after another, the eager step runs them beside the main stream.
     bool use_graph = false, warm = false;
     hipGraphExec_t gexec[2] = {nullptr, nullptr};
-    const void* gkey[2][6] = {};
+    const void* gkey[2][7] = {};
 };
 
 namespace {
@@ -331,6 +381,14 @@ void describe(sa3k_dit* d) {
         add_tensor(d, p + "ssg", 6 * D, 1, 2);
         for (int k = 1; k < 8; ++k) add_tensor(d, p + kBlockVecs[k], k <= 3 ? D : 64, 1, 3);
     }
+    if (c.local_dim > 0)
+        for (int l = 0; l < c.depth; ++l) {
+            const std::string p = "dit." + std::to_string(l) + ".";
+            add_tensor(d, p + "local.0.weight", D, c.local_dim, 0);
+            add_tensor(d, p + "local.0.bias", D, 1, 1);
+            add_tensor(d, p + "local.2.weight", D, D, 0);
+            add_tensor(d, p + "local.2.bias", D, 1, 1);
+        }
 }
 
 Tensor& tensor(sa3k_dit* d, const std::string& name) {
@@ -347,6 +405,11 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
         if (d->hl[i]) sa3k_lin_destroy(ctx, d->hl[i]);
         if (d->hw[i]) sa3k_weight_destroy(ctx, d->hw[i]);
         if (d->hbnsq[i]) (void)hipFree(d->hbnsq[i]);
+    }
+    for (size_t i = 0; i < d->ll.size(); ++i) {
+        if (d->ll[i]) sa3k_lin_destroy(ctx, d->ll[i]);
+        if (d->lw[i]) sa3k_weight_destroy(ctx, d->lw[i]);
+        if (d->lbnsq[i]) (void)hipFree(d->lbnsq[i]);
     }
     for (Tensor& t : d->tensors)
         if (t.raw) (void)hipFree(t.raw);
@@ -411,17 +474,62 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         auto it = d->index.find(std::string("dit.") + kHeadNames[i] + ".bias");
         d->hbias[i] = it != d->index.end() ? static_cast<const float*>(d->tensors[it->second].raw) : nullptr;
     }
+    // inpaint local conditioning: local.0 over kp padded input columns, local.2; adapters in the
+    // full scope (the core scope drops local.{0,2}, src/train_lora.h:85-89)
+    if (c.local_dim > 0) {
+        d->kp = (int)ceil_div(c.local_dim, 64) * 64;
+        const int r = tr.scope == SA3K_SCOPE_FULL ? tr.rank : 0;
+        const size_t nl = (size_t)2 * c.depth;
+        d->lw.assign(nl, nullptr); d->ll.assign(nl, nullptr); d->lbnsq.assign(nl, nullptr); d->lbias.assign(nl, nullptr);
+        for (int l = 0; l < c.depth; ++l)
+            for (int k = 0; k < 2; ++k) {
+                const size_t i = (size_t)2 * l + k;
+                const std::string stem = "dit." + std::to_string(l) + "." + kLocalNames[k];
+                Tensor& t = tensor(d, stem + ".weight");
+                const void* src = t.raw;
+                void* padded = nullptr;
+                int64_t in = t.cols;
+                if (k == 0 && d->kp != t.cols) {
+                    const int64_t n = t.rows * d->kp;
+                    if (d->wtype == SA3K_TYPE_F32) {
+                        padded = dalloc<float>((size_t)n);
+                        launch(ctx, "dit_local", pad_cols_kernel<uint32_t>, dim3(nblk(n)), (const uint32_t*)t.raw,
+                               t.rows, t.cols, (int64_t)d->kp, (uint32_t*)padded);
+                    } else {
+                        padded = dalloc<uint16_t>((size_t)n);
+                        launch(ctx, "dit_local", pad_cols_kernel<uint16_t>, dim3(nblk(n)), (const uint16_t*)t.raw,
+                               t.rows, t.cols, (int64_t)d->kp, (uint16_t*)padded);
+                    }
+                    src = padded;
+                    in = d->kp;
+                }
+                const int rc = sa3k_weight_create(ctx, d->wtype, in, t.rows, src, 1, &d->lw[i]);
+                if (padded) {
+                    (void)hipStreamSynchronize(ctx->stream);
+                    (void)hipFree(padded);
+                }
+                chk(ctx, rc);
+                chk(ctx, sa3k_lin_create(ctx, d->lw[i], r, SA3K_PREC_BF16, NT, &d->ll[i]));
+                lin_set_tag(d->ll[i], "local");
+                if (r && tr.dora) {   // base_norm_sq over the stored local_dim columns (eps counts them)
+                    d->lbnsq[i] = dalloc<float>((size_t)t.rows);
+                    chk(ctx, sa3k_row_norms(ctx, d->wtype, t.cols, t.rows, t.raw, 1, 1e-12f, d->lbnsq[i]));
+                }
+                d->lbias[i] = static_cast<const float*>(tensor(d, stem + ".bias").raw);
+            }
+    }
     d->memtok = static_cast<const float*>(tensor(d, "dit.memory_tokens").raw);
     SA3K_HIP(hipStreamSynchronize(ctx->stream));
     // the weights and the block vectors now live in the sa3k_weight / sa3k_block objects; the head
-    // biases and the memory tokens are read in place
+    // and local biases and the memory tokens are read in place, and local.0's stored (unpadded)
+    // weight stays for its row norms over local_dim columns
     for (Tensor& t : d->tensors)
-        if (t.kind == 0 || t.kind == 2 || t.kind == 3) {
+        if ((t.kind == 0 || t.kind == 2 || t.kind == 3) && t.name.find(".local.0.weight") == std::string::npos) {
             (void)hipFree(t.raw);
             t.raw = nullptr;
         }
     // adapter targets in the reference's order (sorted weight names)
-    struct Ref { std::string name; sa3k_lin* lin; const float* bnsq; int64_t in, out; int head; int block; };
+    struct Ref { std::string name; sa3k_lin* lin; const float* bnsq; int64_t in, out; int head; int block; int local; };
     std::vector<Ref> refs;
     const int64_t outs[7] = {5 * (int64_t)c.dim, c.dim, 2 * (int64_t)c.dim, 3 * (int64_t)c.dim, c.dim,
                              2 * (int64_t)c.inner, c.dim};
@@ -429,15 +537,21 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     for (int l = 0; l < c.depth; ++l)
         for (int t = 0; t < 7; ++t)
             refs.push_back({"dit." + std::to_string(l) + "." + kBlockTargets[t] + ".weight", d->blocks[l]->L[t],
-                            d->blocks[l]->bnsq[t], ins[t], outs[t], -1, l * 7 + t});
+                            d->blocks[l]->bnsq[t], ins[t], outs[t], -1, l * 7 + t, -1});
     if (tr.scope == SA3K_SCOPE_FULL)
         for (int i = 0; i < H_N; ++i) {
             const Tensor& t = tensor(d, std::string("dit.") + kHeadNames[i] + ".weight");
-            refs.push_back({t.name, d->hl[i], d->hbnsq[i], t.cols, t.rows, i, -1});
+            refs.push_back({t.name, d->hl[i], d->hbnsq[i], t.cols, t.rows, i, -1, -1});
+        }
+    if (tr.scope == SA3K_SCOPE_FULL)
+        for (size_t i = 0; i < d->ll.size(); ++i) {   // the arena keeps local.0's A at local_dim columns
+            const Tensor& t = tensor(d, "dit." + std::to_string(i / 2) + "." + kLocalNames[i % 2] + ".weight");
+            refs.push_back({t.name, d->ll[i], d->lbnsq[i], t.cols, t.rows, -1, -1, (int)i});
         }
     std::sort(refs.begin(), refs.end(), [](const Ref& a, const Ref& b) { return a.name < b.name; });
     for (int i = 0; i < H_N; ++i) d->head_target[i] = -1;
     d->block_target.assign((size_t)c.depth * 7, -1);
+    d->local_target.assign(d->ll.size(), -1);
     int64_t off = 0;
     for (const Ref& r : refs) {
         Target t;
@@ -447,6 +561,7 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         if (tr.dora) { t.off_m = off; off += r.out; }
         if (r.head >= 0) d->head_target[r.head] = (int)d->targets.size();
         if (r.block >= 0) d->block_target[r.block] = (int)d->targets.size();
+        if (r.local >= 0) d->local_target[r.local] = (int)d->targets.size();
         d->targets.push_back(t);
     }
     d->n_params = off;
@@ -467,6 +582,31 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     d->dxi = fbuf(d, NT * D); d->dxp = fbuf(d, NT * io);
     d->da = fbuf(d, 6 * B * D); d->dh = fbuf(d, 6 * B * D); d->dg = fbuf(d, B * D);
     d->dca = fbuf(d, NC * D); d->dch = fbuf(d, NC * D);
+    if (c.local_dim > 0) {
+        d->lc = fbuf(d, (size_t)NT * d->kp);
+        for (int l = 0; l < c.depth; ++l) {
+            d->lh.push_back(fbuf(d, NT * D));
+            d->la.push_back(fbuf(d, NT * D));
+            d->le.push_back(fbuf(d, NT * D));
+        }
+        if (tr.scope == SA3K_SCOPE_FULL) {
+            d->dle = fbuf(d, NT * D); d->dla = fbuf(d, NT * D); d->dlh = fbuf(d, NT * D);
+            d->lA = fbuf(d, (size_t)c.depth * tr.rank * d->kp);
+            d->ldA = fbuf(d, (size_t)tr.rank * d->kp);
+            fill(ctx, d->ldA, (int64_t)tr.rank * d->kp, 0.0f);
+            std::vector<int64_t> offs((size_t)c.depth);
+            for (int l = 0; l < c.depth; ++l) {
+                Target& t0 = d->targets[d->local_target[(size_t)2 * l]];
+                offs[l] = t0.off_a;
+                t0.a_src = d->lA + (int64_t)l * tr.rank * d->kp;
+            }
+            int64_t* od = dalloc<int64_t>(offs.size());
+            d->bufs.push_back(od);
+            SA3K_HIP(hipMemcpyAsync(od, offs.data(), offs.size() * sizeof(int64_t), hipMemcpyHostToDevice, ctx->stream));
+            sa3k_note_main(ctx);
+            d->lA_off = od;
+        }
+    }
     d->loss_chunks = (int)std::min<int64_t>(64, ceil_div(T, 16));
     double* lp = dalloc<double>((size_t)B * d->loss_chunks);
     d->bufs.push_back(lp);
@@ -486,7 +626,7 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         std::vector<const float*> A, Bm, mag, bnsq;
         for (const Target& t : d->targets) {
             lins.push_back(t.lin);
-            A.push_back(d->p + t.off_a);
+            A.push_back(t.a_src ? t.a_src : d->p + t.off_a);
             Bm.push_back(d->p + t.off_b);
             mag.push_back(tr.dora ? d->p + t.off_m : nullptr);
             bnsq.push_back(tr.dora ? t.bnsq : nullptr);
@@ -496,6 +636,9 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         for (int i = 0; i < H_N; ++i)
             if (d->head_target[i] < 0)
                 chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
+        for (size_t i = 0; i < d->ll.size(); ++i)
+            if (d->local_target[i] < 0)
+                chk(ctx, sa3k_lin_prepare(ctx, d->ll[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
     }
     const int nws = tr.recompute ? 1 : c.depth;
     for (int l = 0; l < nws; ++l) d->ws.push_back(block_ws_build(bc, B, S, Ctx, l == 0 ? nullptr : d->ws[0]));
@@ -507,6 +650,9 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
 void prepare(sa3k_ctx* ctx, sa3k_dit* d) {
     if (!d->dirty) return;
     KernelScope ks(ctx, "dit_prepare");
+    if (d->lA)   // local.0's A at kp columns for its padded product
+        launch(ctx, "dit_local", pad_a_kernel, dim3(nblk((int64_t)d->tr.rank * d->kp), (unsigned)d->cfg.depth),
+               (const float*)d->p, (const int64_t*)d->lA_off, d->tr.rank, d->cfg.local_dim, d->kp, d->lA);
     lin_group_prepare(ctx, d->group);
     d->dirty = false;
 }
@@ -554,6 +700,50 @@ void bind_kv(sa3k_dit* d, sa3k_block_ws* w, int l) {
     w->kv_ld = d->kvs ? lin_stack_ld(d->kvs) : 0;
 }
 
+// block l's inpaint local add: its MLP's output when conditioning is bound, and the gradient
+// buffer when the local linears carry adapters
+void bind_local(sa3k_dit* d, sa3k_block_ws* w, int l) {
+    const bool on = d->local_in != nullptr;
+    w->ladd = on ? d->le[l] : nullptr;
+    w->dladd = on && d->dle && (d->local_target[(size_t)2 * l] >= 0 || d->local_target[(size_t)2 * l + 1] >= 0)
+                   ? d->dle : nullptr;
+    w->ladd_T = d->tr.frames;
+}
+
+// le = local.2(silu(local.0(local_cond))), both with biases (src/dit.h:246-249)
+void local_fwd(sa3k_ctx* ctx, sa3k_dit* d, int l) {
+    const int64_t NT = (int64_t)d->tr.batch * d->tr.frames, n = NT * d->cfg.dim;
+    chk(ctx, sa3k_lin_forward(ctx, d->ll[(size_t)2 * l], SA3K_TYPE_F32, d->lc, NT, d->lbias[(size_t)2 * l], d->lh[l]));
+    launch(ctx, "dit_local", silu_kernel, dim3(nblk(n)), (const float*)d->lh[l], n, d->la[l]);
+    chk(ctx, sa3k_lin_forward(ctx, d->ll[(size_t)2 * l + 1], SA3K_TYPE_F32, d->la[l], NT, d->lbias[(size_t)2 * l + 1],
+                              d->le[l]));
+}
+
+// the local MLP's backward from dle (written by block l's backward): adapter gradients only (the
+// conditioning is data); local.0's dA comes out at kp columns and is folded into the arena
+void local_bwd(sa3k_ctx* ctx, sa3k_dit* d, int l) {
+    const int64_t NT = (int64_t)d->tr.batch * d->tr.frames, n = NT * d->cfg.dim;
+    auto grads = [&](size_t i, float** dA, float** dB, float** dm) {
+        const int ti = d->local_target[i];
+        *dA = *dB = *dm = nullptr;
+        if (ti < 0) return;
+        const Target& tg = d->targets[ti];
+        *dA = d->g + tg.off_a;
+        *dB = d->g + tg.off_b;
+        *dm = d->tr.dora ? d->g + tg.off_m : nullptr;
+    };
+    float *dA, *dB, *dm;
+    grads((size_t)2 * l + 1, &dA, &dB, &dm);
+    chk(ctx, sa3k_lin_backward(ctx, d->ll[(size_t)2 * l + 1], SA3K_TYPE_F32, d->la[l], NT, d->dle, d->dla, 0, dA, dB,
+                               dm));
+    if (d->local_target[(size_t)2 * l] < 0) return;
+    launch(ctx, "dit_local", silu_bwd_kernel, dim3(nblk(n)), (const float*)d->dla, (const float*)d->lh[l], n, d->dlh);
+    grads((size_t)2 * l, &dA, &dB, &dm);
+    chk(ctx, sa3k_lin_backward(ctx, d->ll[(size_t)2 * l], SA3K_TYPE_F32, d->lc, NT, d->dlh, nullptr, 0, d->ldA, dB, dm));
+    launch(ctx, "dit_local", fold_a_kernel, dim3(nblk((int64_t)d->tr.rank * d->kp)), d->ldA, d->tr.rank,
+           d->cfg.local_dim, d->kp, dA);
+}
+
 // head + blocks + tail forward: velocity in d->vel
 void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const float* cross, const float* glob) {
     const sa3k_dit_config& c = d->cfg;
@@ -581,9 +771,14 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     lin_fwd(ctx, d, H_PROJ_IN, d->xp, NT, d->xi);
     launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B, T,
            c.mem_tokens, (int)D, d->xs[0]);
+    if (d->local_in)   // the inpaint conditioning, zero-padded to local.0's kp input columns
+        launch(ctx, "dit_local", pad_cols_kernel<float>, dim3(nblk(NT * d->kp)), d->local_in, NT,
+               (int64_t)c.local_dim, (int64_t)d->kp, d->lc);
     // blocks
     for (int l = 0; l < c.depth; ++l) {
         bind_kv(d, d->ws[d->tr.recompute ? 0 : l], l);
+        bind_local(d, d->ws[d->tr.recompute ? 0 : l], l);
+        if (d->local_in) local_fwd(ctx, d, l);
         block_forward(ctx, d->blocks[l], d->ws[d->tr.recompute ? 0 : l], d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         if (d->tr.recompute) side_join_since(ctx, forks0);
     }
@@ -628,6 +823,7 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
     for (int l = c.depth - 1; l >= 0; --l) {
         sa3k_block_ws* w = d->ws[d->tr.recompute ? 0 : l];
         bind_kv(d, w, l);
+        bind_local(d, w, l);
         if (d->tr.recompute && l != c.depth - 1)   // the last block's activations are still in place
             block_forward(ctx, d->blocks[l], w, d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         float* dA[7];
@@ -642,6 +838,7 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
         // resident activations: a block's last second-stream work may run on beside the next block
         block_backward(ctx, d->blocks[l], w, dcur, dnext, d->dctx, d->dgcond, dA, dB, d->tr.dora ? dm : nullptr,
                        ctx->late_join && !d->tr.recompute);
+        if (w->dladd) local_bwd(ctx, d, l);
         std::swap(dcur, dnext);
     }
     if (side_usable(ctx)) side_join(ctx);   // the head reads dgcond; AdamW reads every dA
@@ -689,7 +886,7 @@ bool capture(sa3k_ctx* ctx, sa3k_dit* d, int gi, const void* const* key, const f
     const hipError_t e = hipGraphInstantiate(&d->gexec[gi], g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     SA3K_HIP(e);
-    for (int k = 0; k < 6; ++k) d->gkey[gi][k] = key[k];
+    for (int k = 0; k < 7; ++k) d->gkey[gi][k] = key[k];
     return true;
 }
 
@@ -700,9 +897,9 @@ void accumulate(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* targe
     bool launched = false;
     if (graph) {
         const int gi = d->dirty ? 1 : 0;
-        const void* key[6] = {x_t, target, t, cross, glob, lw};
+        const void* key[7] = {x_t, target, t, cross, glob, lw, d->local_in};
         bool have = d->gexec[gi] != nullptr;
-        for (int k = 0; k < 6 && have; ++k) have = d->gkey[gi][k] == key[k];
+        for (int k = 0; k < 7 && have; ++k) have = d->gkey[gi][k] == key[k];
         if (!have) have = capture(ctx, d, gi, key, x_t, target, t, cross, glob, lw);
         if (have) {
             SA3K_HIP(hipGraphLaunch(d->gexec[gi], ctx->stream));
@@ -737,6 +934,7 @@ SA3K_API int sa3k_dit_create(sa3k_ctx* ctx, const sa3k_dit_config* cfg, int weig
                      "depth / mem_tokens / time_dim");
         for (int v : {cfg->io, cfg->dim, cfg->cond_dim, cfg->time_dim, cfg->inner})
             SA3K_REQUIRE(v > 0 && v % 64 == 0, "io, dim, cond_dim, time_dim and inner must be multiples of 64");
+        SA3K_REQUIRE(cfg->local_dim >= 0, "local_dim must be 0 (no inpaint conditioning) or positive");
         sa3k_dit* d = new sa3k_dit();
         d->cfg = *cfg;
         d->wtype = weight_type;
@@ -818,22 +1016,21 @@ SA3K_API int sa3k_dit_weight_row_norms(sa3k_ctx* ctx, sa3k_dit* dit, const char*
         SA3K_REQUIRE(dit && name && out && (mode == 0 || mode == 1), "bad arguments");
         Tensor& t = tensor(dit, name);
         SA3K_REQUIRE(t.kind == 0, "not a 2-D weight: " + t.name);
-        const sa3k_weight* w = nullptr;
-        if (dit->ready) {   // the built weight objects (the raw storage is released at setup)
-            for (int l = 0; l < dit->cfg.depth && !w; ++l)
-                for (int k = 0; k < 7; ++k)
-                    if (t.name == "dit." + std::to_string(l) + "." + kBlockTargets[k] + ".weight") w = dit->blocks[l]->W[k];
-            for (int h = 0; h < H_N && !w; ++h)
-                if (t.name == std::string("dit.") + kHeadNames[h] + ".weight") w = dit->hw[h];
-            SA3K_REQUIRE(w != nullptr, "weight not found: " + t.name);
-            chk(ctx, mode == 0 ? sa3k_weight_row_norms(ctx, w, out) : sa3k_weight_row_norm_sq(ctx, w, eps, out));
+        if (t.raw) {   // the stored tensor (before setup; local.0 keeps it, its built weight is padded)
+            chk(ctx, sa3k_row_norms(ctx, t.type, t.cols, t.rows, t.raw, mode, eps, out));
             return;
         }
-        sa3k_weight* tmp = nullptr;   // a temporary weight object over the raw tensor
-        chk(ctx, sa3k_weight_create(ctx, t.type, t.cols, t.rows, t.raw, 1, &tmp));
-        const int rc = mode == 0 ? sa3k_weight_row_norms(ctx, tmp, out) : sa3k_weight_row_norm_sq(ctx, tmp, eps, out);
-        chk(ctx, sa3k_weight_destroy(ctx, tmp));
-        chk(ctx, rc);
+        // after setup: the built weight objects (the raw storage is released at setup)
+        const sa3k_weight* w = nullptr;
+        for (int l = 0; l < dit->cfg.depth && !w; ++l)
+            for (int k = 0; k < 7; ++k)
+                if (t.name == "dit." + std::to_string(l) + "." + kBlockTargets[k] + ".weight") w = dit->blocks[l]->W[k];
+        for (int h = 0; h < H_N && !w; ++h)
+            if (t.name == std::string("dit.") + kHeadNames[h] + ".weight") w = dit->hw[h];
+        for (size_t k = 0; k < dit->lw.size() && !w; ++k)
+            if (t.name == "dit." + std::to_string(k / 2) + "." + kLocalNames[k % 2] + ".weight") w = dit->lw[k];
+        SA3K_REQUIRE(w != nullptr, "weight not found: " + t.name);
+        chk(ctx, mode == 0 ? sa3k_weight_row_norms(ctx, w, out) : sa3k_weight_row_norm_sq(ctx, w, eps, out));
     });
 }
 
@@ -901,6 +1098,8 @@ SA3K_API int sa3k_dit_adapters_init(sa3k_ctx* ctx, sa3k_dit* dit, uint64_t seed,
                         if (dit->block_target[(size_t)l * 7 + k] == (int)i) w = dit->blocks[l]->W[k];
                 for (int h = 0; h < H_N && !w; ++h)
                     if (dit->head_target[h] == (int)i) w = dit->hw[h];
+                for (size_t k = 0; k < dit->ll.size() && !w; ++k)   // local.0 padded: zero columns add nothing
+                    if (dit->local_target[k] == (int)i) w = dit->lw[k];
                 SA3K_REQUIRE(w != nullptr, "target without a weight");
                 chk(ctx, sa3k_weight_row_norms(ctx, w, dit->p + t.off_m));
             }
@@ -940,6 +1139,14 @@ SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw
         fill(ctx, dit->g, dit->n_params, 0.0f);
         dit->count = 0;
         dit->dirty = true;
+    });
+}
+
+SA3K_API int sa3k_dit_set_local(sa3k_ctx* ctx, sa3k_dit* dit, const float* local) {
+    return sa3k_guard(ctx, "sa3k_dit_set_local", [&] {
+        SA3K_REQUIRE(dit && dit->ready, "the model is not set up");
+        SA3K_REQUIRE(!local || dit->cfg.local_dim > 0, "the model has no local-conditioning linears (local_dim 0)");
+        dit->local_in = local;
     });
 }
 

@@ -38,15 +38,16 @@ public:
             err = "only the differential DiT (medium family) is implemented";
             return false;
         }
-        if (c.local_dim != 0) {
-            err = "inpainting local conditioning is not implemented";
+        if (c.local_dim < 0) {
+            err = "dit.local_dim must be 0 (no inpaint conditioning) or positive";
             return false;
         }
         ctx_ = sa3k_default_ctx(err);
         if (!ctx_) return false;
         cfg_ = c;
         sa3k_dit_config kc{c.io, c.dim, c.depth, c.heads, c.head_dim, c.cond_dim, c.mem_tokens, c.rot, c.time_dim,
-                           c.inner, c.window, c.rope_base, c.norm_eps, c.qk_eps, c.time_min_freq, c.time_max_freq};
+                           c.inner, c.window, c.rope_base, c.norm_eps, c.qk_eps, c.time_min_freq, c.time_max_freq,
+                           c.local_dim};
         if (sa3k_dit_create(ctx_, &kc, weight_type, &dit_) != SA3K_OK) return sa3k_fail(ctx_, err);
         int n = 0;
         if (sa3k_dit_tensor_count(ctx_, dit_, &n) != SA3K_OK) return sa3k_fail(ctx_, err);

@@ -41,6 +41,10 @@ struct DitDeviceStep {
     int64_t n_params = 0;
     std::vector<Slot> slots;   // aligned with TrainLoraState::params
     DeviceF32 x, target, t, cross, global;
+    // inpaint graphs (src/train_dit.h:83-87): the local conditioning [frames][local_dim] and the
+    // per-frame loss weight [frames] of the last sample
+    bool inpaint = false;
+    DeviceF32 local, loss_weight;
 };
 
 // Set `dit` up for one sample of `frames` latent frames and `ctx_len` context tokens with the
@@ -53,8 +57,8 @@ inline bool setup_dit_step(DitModel& dit, const DitConfig& dc, const TrainLoraSt
         err = "invalid DiT training graph dimensions";
         return false;
     }
-    if (inpaint) {
-        err = "inpainting training graphs are not implemented";
+    if (inpaint && dc.local_dim <= 0) {
+        err = "inpainting requested but DiT has no local-cond weights (dit.local_dim <= 0)";
         return false;
     }
     if (cond_dim != dc.cond_dim) {
@@ -103,6 +107,10 @@ inline bool setup_dit_step(DitModel& dit, const DitConfig& dc, const TrainLoraSt
         sa3k_dit_arena(ctx, dit.handle(), 1, &out.grads, nullptr) != SA3K_OK)
         return sa3k_fail(ctx, err);
     const size_t nx = (size_t)dc.io * frames;
+    out.inpaint = inpaint;
+    if (inpaint && !(out.local.alloc(ctx, (size_t)dc.local_dim * frames, err) &&
+                     out.loss_weight.alloc(ctx, (size_t)frames, err)))
+        return false;
     return out.x.alloc(ctx, nx, err) && out.target.alloc(ctx, nx, err) && out.t.alloc(ctx, 1, err) &&
            out.cross.alloc(ctx, (size_t)cond_dim * ctx_len, err) && out.global.alloc(ctx, (size_t)cond_dim, err);
 }

@@ -207,6 +207,27 @@ inline bool upload_step_inputs(DitDeviceStep& st, const TrainDiffusionSample& sa
            st.global.upload(cond.global.data(), (size_t)st.cond_dim, 0, err);
 }
 
+// An inpaint sample's local conditioning and loss weight (src/train_loop.h:239-242). The reference's
+// weight is [frames][io] with one value per frame (build_train_inpaint broadcasts it over the
+// channels); the device loss takes that per-frame value.
+inline bool upload_inpaint(DitDeviceStep& st, const TrainInpaint& in, const DitConfig& dc, std::string& err) {
+    const size_t F = (size_t)st.frames, io = (size_t)dc.io;
+    if (in.local.size() != (size_t)dc.local_dim * F || in.loss_weight.size() != io * F) {
+        err = "inpaint inputs do not match the graph's dimensions";
+        return false;
+    }
+    std::vector<float> w(F);
+    for (size_t t = 0; t < F; ++t) {
+        w[t] = in.loss_weight[t * io];
+        for (size_t c = 1; c < io; ++c)
+            if (in.loss_weight[t * io + c] != w[t]) {
+                err = "inpaint loss weights must be constant over a frame's channels";
+                return false;
+            }
+    }
+    return st.local.upload(in.local.data(), in.local.size(), 0, err) && st.loss_weight.upload(w.data(), F, 0, err);
+}
+
 // One sample through the model in whichever schedule it was set up with: forward, velocity MSE,
 // backward; this call's gradients are read back and added into accum target by target, in the
 // order of `visit` (count += 1).
@@ -218,21 +239,21 @@ inline bool accumulate_step(DitDeviceStep& st, const TrainLoraState& lora, Train
         err = "training step inputs are empty";
         return false;
     }
-    // the device DiT has no local-conditioning input (dit.local.*): like the reference's graph built
-    // without one, it answers an inpaint sample with the reference's mismatch error
-    if (inpaint != nullptr) {
+    if (st.inpaint != (inpaint != nullptr)) {
         err = "inpaint graph/sample mismatch (local-cond present in one but not the other)";
         return false;
     }
     if (!upload_step_inputs(st, sample, cond, dc, "training step inputs are empty", err)) return false;
+    if (inpaint && !upload_inpaint(st, *inpaint, dc, err)) return false;
     if (!upload_train_lora_state(lora, st, err)) return false;
     sa3k_ctx* ctx = st.model->ctx();
     // this call's gradients alone, then added into the host accumulator like the reference reads
     // them back from its graphs (train_accum_read_subset)
     if (sa3k_memset(ctx, st.grads, 0, (size_t)st.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
     double loss = 0.0;
-    if (sa3k_dit_accumulate(ctx, st.model->handle(), st.x.get(), st.target.get(), st.t.get(), st.cross.get(),
-                            st.global.get(), nullptr, &loss) != SA3K_OK)
+    if (sa3k_dit_set_local(ctx, st.model->handle(), st.inpaint ? st.local.get() : nullptr) != SA3K_OK ||
+        sa3k_dit_accumulate(ctx, st.model->handle(), st.x.get(), st.target.get(), st.t.get(), st.cross.get(),
+                            st.global.get(), st.inpaint ? st.loss_weight.get() : nullptr, &loss) != SA3K_OK)
         return sa3k_fail(ctx, err);
     loss_out = (float)loss;
     std::vector<float> g((size_t)st.n_params);
@@ -309,8 +330,12 @@ inline bool run_eval_dit_loss(detail::DitDeviceStep& graph, const TrainLoraState
     if (!upload_train_lora_state(lora, graph, err)) return false;
     sa3k_ctx* ctx = graph.model->ctx();
     double loss = 0.0;
-    if (sa3k_dit_eval_loss(ctx, graph.model->handle(), graph.x.get(), graph.target.get(), graph.t.get(),
-                           graph.cross.get(), graph.global.get(), nullptr, &loss) != SA3K_OK)
+    // an inpaint graph evaluates with its last sample's local conditioning and loss weight, as the
+    // reference's graph keeps its input tensors
+    if (sa3k_dit_set_local(ctx, graph.model->handle(), graph.inpaint ? graph.local.get() : nullptr) != SA3K_OK ||
+        sa3k_dit_eval_loss(ctx, graph.model->handle(), graph.x.get(), graph.target.get(), graph.t.get(),
+                           graph.cross.get(), graph.global.get(), graph.inpaint ? graph.loss_weight.get() : nullptr,
+                           &loss) != SA3K_OK)
         return sa3k_fail(ctx, err);
     loss_out = (float)loss;
     return true;

@@ -52,7 +52,8 @@ BLOCK_VECTORS = ("ssg", "pre_g", "cross_g", "ff_g", "sq_g", "sk_g", "cq_g", "ck_
 class DitConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("io", "dim", "depth", "heads", "head_dim", "cond_dim", "mem_tokens", "rope_dims",
                                        "time_dim", "inner", "window")] + \
-               [(n, C.c_float) for n in ("rope_base", "norm_eps", "qk_eps", "time_min_freq", "time_max_freq")]
+               [(n, C.c_float) for n in ("rope_base", "norm_eps", "qk_eps", "time_min_freq", "time_max_freq")] + \
+               [("local_dim", C.c_int)]
 
 
 class DitTrain(C.Structure):
@@ -63,9 +64,9 @@ class DitTrain(C.Structure):
 SCOPE_CORE, SCOPE_FULL = 0, 1
 
 
-def dit_config(io, dim, depth, heads, cond_dim, mem_tokens, time_dim, inner, window=0, rope_dims=32):
+def dit_config(io, dim, depth, heads, cond_dim, mem_tokens, time_dim, inner, window=0, rope_dims=32, local_dim=0):
     return DitConfig(io, dim, depth, heads, 64, cond_dim, mem_tokens, rope_dims, time_dim, inner, window,
-                     1e4, 1e-5, 1e-6, 0.5, 1e4)
+                     1e4, 1e-5, 1e-6, 0.5, 1e4, local_dim)
 
 
 def block_target_dims(dim, inner):
@@ -144,6 +145,7 @@ def _declare(lib):
         "sa3k_dit_forward": (I, [P, P, P, P, P, P, P]),
         "sa3k_dit_eval_loss": (I, [P, P, P, P, P, P, P, P, C.POINTER(D)]),
         "sa3k_dit_set_graphs": (I, [P, P, I]),
+        "sa3k_dit_set_local": (I, [P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -579,6 +581,11 @@ class Dit:
 
     def set_graphs(self, on):
         self.ctx.check(self.ctx.lib.sa3k_dit_set_graphs(self.ctx.h, self.h, int(on)))
+
+    def set_local(self, local):
+        """bind the inpaint local conditioning [B][T][local_dim] (device buffer) or None"""
+        self._local = local   # keeps the buffer alive while bound
+        self.ctx.check(self.ctx.lib.sa3k_dit_set_local(self.ctx.h, self.h, local.ptr if local is not None else None))
 
     def forward(self, x_t, t, cross, glob, velocity):
         self.ctx.check(self.ctx.lib.sa3k_dit_forward(self.ctx.h, self.h, x_t.ptr, t.ptr, cross.ptr, glob.ptr,

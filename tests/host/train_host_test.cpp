@@ -315,7 +315,7 @@ static void test_gpu() {
         const sa3::TrainInpaint ip = sa3::build_train_inpaint(z, mask, dc.io, frames, dc.io + 1, 1.0f);
         expect(!sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss0, err, &ip) &&
                    err.find("inpaint graph/sample mismatch") == 0,
-               "inpaint sample rejected (no local-conditioning input)");
+               "inpaint sample rejected by a graph built without local conditioning");
     }
     expect(sa3::run_train_dit_accumulate(graph, st, accum, s, c, dc, loss0, err), "accumulate 1");
     const sa3::TrainLoraGradAccum once = accum;
@@ -386,6 +386,56 @@ static void test_gpu() {
                   s_step.params[i].magnitude == s_mono.params[i].magnitude;
         expect(upd, "updated adapters equal across schedules and run_train_dit_step");
         sa3::free_train_dit_ckpt(ck);
+    }
+
+    // ---- inpainting (src/train_dit.h:59-87, src/train_loop.h:212-256): a model with the local
+    // conditioning linears (local_dim = 1 + io), its full scope (9 per block + 12), an inpaint
+    // sample through the monolithic and the checkpointed graphs (bitwise equal), the mismatch rules
+    {
+        sa3::DitConfig di = dc;
+        di.local_dim = dc.io + 1;
+        sa3::TrainDitGraph ig;
+        expect(!sa3::build_train_dit_forward_graph(dit, dc, st, frames, dc.cond_dim, ctx_len, ig, err, true) &&
+                   err == "inpainting requested but DiT has no local-cond weights (dit.local_dim <= 0)",
+               "inpaint graph on a model without local weights rejected");
+        sa3::DitModel m1, m2;
+        expect(m1.create(di, SA3K_TYPE_F16, err) && m1.init_random(21, 0.05f, err), "inpaint model");
+        expect(m2.create(di, SA3K_TYPE_F16, err) && m2.init_random(21, 0.05f, err), "inpaint model 2");
+        sa3::TrainLoraScope sfull, score;
+        score.name = "core";
+        const std::vector<sa3::TrainLoraTarget> it = sa3::enumerate_train_lora_targets(m1, sfull);
+        expect(it.size() == 2 * 9 + 12, "full scope with local linears: 9 per block + 12");
+        expect(sa3::enumerate_train_lora_targets(m1, score).size() == 14, "core scope drops local.{0,2}");
+        sa3::TrainLoraState ist;
+        expect(sa3::init_train_lora_state(m1, it, "dora-rows", 8, 16.0f, 9, ist, err), "init inpaint state");
+        for (sa3::TrainLoraParam& p : ist.params)
+            for (float& b : p.lora_B) b = 0.01f * nd(rng);
+        std::mt19937_64 mrng(6);
+        sa3::InpaintMaskType ty;
+        const std::vector<float> mask = sa3::generate_inpaint_mask(frames, frames, {0.1, 0.8, 0.1}, mrng, ty);
+        const sa3::TrainInpaint ip = sa3::build_train_inpaint(z, mask, dc.io, frames, di.local_dim, 1.0f);
+        sa3::TrainDitCkpt ick;
+        expect(sa3::build_train_dit_forward_graph(m1, di, ist, frames, dc.cond_dim, ctx_len, ig, err, true),
+               "inpaint graph");
+        expect(sa3::build_train_dit_ckpt(m2, di, ist, frames, dc.cond_dim, ctx_len, ick, err, true), "inpaint ckpt");
+        sa3::TrainLoraGradAccum a1, a2;
+        float l1 = 0.0f, l2 = 0.0f, le = 0.0f;
+        expect(!sa3::run_train_dit_accumulate(ig, ist, a1, s, c, dc, l1, err) &&
+                   err.find("inpaint graph/sample mismatch") == 0,
+               "inpaint graph without its sample rejected");
+        expect(sa3::run_train_dit_accumulate(ig, ist, a1, s, c, di, l1, err, &ip), "inpaint accumulate");
+        expect(sa3::run_train_dit_accumulate_ckpt(ick, ist, a2, s, c, di, l2, err, &ip), "inpaint accumulate ckpt");
+        expect(std::isfinite(l1) && l1 > 0.0f && l1 == l2, "inpaint loss finite, equal across schedules");
+        expect(sa3::run_eval_dit_loss(ig, ist, s, c, di, le, err) && le == l1, "inpaint eval loss == accumulate loss");
+        bool same = a1.A.size() == a2.A.size(), local_live = false;
+        for (size_t i = 0; same && i < a1.A.size(); ++i) {
+            same = a1.A[i] == a2.A[i] && a1.B[i] == a2.B[i] && a1.mag[i] == a2.mag[i];
+            if (it[i].weight_name.find(".local.") != std::string::npos)
+                for (float g : a1.A[i]) local_live = local_live || g != 0.0f;
+        }
+        expect(same, "inpaint gradients: checkpointed == monolithic bit for bit");
+        expect(local_live, "local-conditioning adapters receive gradients");
+        sa3::free_train_dit_ckpt(ick);
     }
 
     // the C ABI's arena path on the same state: gradients of two accumulate calls, then one
