@@ -1097,7 +1097,8 @@ void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
         const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.N, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
         const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
         const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return launch_big(ctx, p);
+        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && p.K >= 8192))
+            return launch_big(ctx, p);
     }
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, true, 4, true>(ctx, p);
     if (p.N <= 64) return launch_dma<128, 64, 4, 4, true, 4, true>(ctx, p);
@@ -1135,7 +1136,8 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
             const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.Nt, 128);
             const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
             const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-            if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return launch_big(ctx, p);
+            if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && p.K >= 8192))
+                return launch_big(ctx, p);
         }
     }
     const int64_t Mt = p.M + p.Mx;
