@@ -433,17 +433,20 @@ class DitWorkload:
     clip + AdamW over the 43.4M-parameter arena. dim 1536, 24 heads x 64, FFN 6144, io 64, batch 2 x
     (64 memory + 1024 latent) tokens, self-attention window 256, 128 context tokens of 768, f16 base
     ~ N(0, 0.02) (random init on the device); x_t, target ~ N(0,1), t ~ U(0,1). Every block keeps
-    its activations (no recompute; the checkpointed schedule is --recompute)."""
+    its activations (no recompute; the checkpointed schedule is --recompute). local_dim > 0 adds each
+    block's inpaint local-conditioning MLP (local.0 local_dim -> 1536, SiLU, local.2 1536 -> 1536, both
+    adapted: 228 targets) with a bound [B][T][local_dim] conditioning ~ N(0,1)."""
     dtype = "bf16"
 
-    def __init__(self, ctx, recompute=False, B=2, T=1024, Ctx=128, depth=24, window=256, r=32):
+    def __init__(self, ctx, recompute=False, B=2, T=1024, Ctx=128, depth=24, window=256, r=32, local_dim=0):
         sa3k = sys.modules["sa3k"]
         self.ctx, self.B, self.T, self.Ctx, self.depth, self.window, self.r = ctx, B, T, Ctx, depth, window, r
         self.dim, self.heads, self.inner, self.io, self.cond_dim, self.time_dim, self.mem = 1536, 24, 6144, 64, 768, 256, 64
-        self.recompute = recompute
-        self.name = f"dit_update_{depth}x1536_b{B}_t{T}_w{window}_dora_r{r}" + ("_recompute" if recompute else "")
+        self.recompute, self.local_dim = recompute, local_dim
+        self.name = f"dit_update_{depth}x1536_b{B}_t{T}_w{window}_dora_r{r}" + ("_recompute" if recompute else "") + \
+            (f"_inpaint_local{local_dim}" if local_dim else "")
         cfg = sa3k.dit_config(self.io, self.dim, depth, self.heads, self.cond_dim, self.mem, self.time_dim,
-                              self.inner, window)
+                              self.inner, window, local_dim=local_dim)
         self.d = sa3k.Dit(ctx, cfg, sa3k.TYPE_F16)
         self.d.init_random(1234, 0.02)
         self.d.setup(r, 32.0, True, sa3k.SCOPE_FULL, B, T, Ctx, recompute)
@@ -455,7 +458,11 @@ class DitWorkload:
                          t=g.uniform(0, 1, B).astype(np.float32),
                          cr=g.normal(0, 1, (B, Ctx, self.cond_dim)).astype(np.float32),
                          gl=g.normal(0, 1, (B, self.cond_dim)).astype(np.float32))
+        if local_dim:
+            self.host["lc"] = g.normal(0, 1, (B, T, local_dim)).astype(np.float32)
         self.dev = {k: ctx.upload(v) for k, v in self.host.items()}
+        if local_dim:
+            self.d.set_local(self.dev["lc"])
         self.hp = (1e-4, 0.9, 0.999, 1e-8, 0.01, 1.0)
         self.k = 0
 
@@ -469,13 +476,19 @@ class DitWorkload:
         S = self.mem + self.T
         f, b = block_flops(self.B, S, self.Ctx, self.dim, self.inner, self.r, self.window)
         hf, hb = dit_head_flops(self.B, self.T, self.Ctx, self.io, self.dim, self.cond_dim, self.time_dim, self.r)
+        if self.local_dim:   # the local MLP's base products: forward both, backward local.2's dX
+            n = self.B * self.T
+            hf += self.depth * 2 * n * self.dim * (self.local_dim + self.dim)
+            hb += self.depth * 2 * n * self.dim * self.dim
         return self.depth * f + hf, self.depth * b + hb
 
     def config(self):
         return {"workload": self.name, "blocks": self.depth, "batch": self.B, "frames": self.T,
                 "memory_tokens": self.mem, "context_tokens": self.Ctx, "io": self.io, "dim": self.dim,
                 "heads": self.heads, "ffn_inner": self.inner, "window": self.window, "rank": self.r,
-                "adapter": "dora-rows", "scope": "full (180 targets)", "base": "f16",
+                "adapter": "dora-rows", "base": "f16",
+                "scope": f"full ({(9 if self.local_dim else 7) * self.depth + 12} targets)",
+                **({"local_dim": self.local_dim} if self.local_dim else {}),
                 "adapter_params": self.n, "schedule": "checkpointed recompute" if self.recompute else "resident"}
 
     def roofline(self, prof, steps):
@@ -562,6 +575,7 @@ WORKLOADS = {"adamw": AdamWWorkload,
              "block": BlockWorkload,
              "dit": DitWorkload,
              "dit_recompute": lambda ctx: DitWorkload(ctx, recompute=True),
+             "dit_inpaint": lambda ctx: DitWorkload(ctx, local_dim=257),
              "chain_q8": lambda ctx: ChainWorkload(ctx, "q8"),
              "chain_q8_copy": lambda ctx: ChainWorkload(ctx, "q8_copy")}
 DEFAULT = "dit"

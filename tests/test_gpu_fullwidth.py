@@ -64,16 +64,22 @@ def test_block_full_width_vs_oracle(ctx, window):
     print(f"worst normwise error {e:.3e} ({what}), lowest cosine {min(x[1] for x in worst):.7f}")
 
 
-def test_dit_depth1_full_width_vs_oracle(ctx):
+@pytest.mark.parametrize("local_dim", [0, 257])
+def test_dit_depth1_full_width_vs_oracle(ctx, local_dim):
+    # local_dim 257: the reference's inpaint model ([mask | z * mask] over its 256 latent channels),
+    # local.0's input padded to 320 columns on the device, the local linears adapted (full scope)
     cfg = dict(B=2, T=72, Ctx=128, io=64, dim=1536, heads=24, inner=6144, depth=1, mem=64, cond_dim=768,
-               time_dim=256, rope_dims=32, window=256, rank=32, alpha=32.0, dora=True)
-    print("full-width depth-1 DiT vs oracle: T 72, Ctx 128, window 256, DoRA r32 full scope", flush=True)
+               time_dim=256, rope_dims=32, window=256, rank=32, alpha=32.0, dora=True, local_dim=local_dim)
+    print(f"full-width depth-1 DiT vs oracle: T 72, Ctx 128, window 256, DoRA r32 full scope, local_dim {local_dim}",
+          flush=True)
     tensors, adapters, inputs = db.random_dit(53, cfg, "full", w_sd=0.02, b_sd=0.01)
     tensors = {k: (v.astype(np.float16).astype(np.float32) if k.endswith(".weight") else v)
                for k, v in tensors.items()}
     d = make_gpu(ctx, cfg, tensors, adapters, "full", sa3k.TYPE_F16)
     try:
         up, _ = upload_inputs(ctx, inputs)
+        if local_dim:
+            d.set_local(up["local"])
         loss = d.accumulate(up["x_t"], up["target"], up["t"], up["cross"], up["glob"])
         vel = ctx.empty((cfg["B"], cfg["T"], cfg["io"]))
         d.forward(up["x_t"], up["t"], up["cross"], up["glob"], vel)
@@ -82,7 +88,7 @@ def test_dit_depth1_full_width_vs_oracle(ctx):
         assert np.allclose(loss, ref_loss, rtol=1e-3), (loss, ref_loss)
         worst = []
         check(vel.numpy(), ref_vel, "velocity", worst)
-        assert len(ref) == 19
+        assert len(ref) == (21 if local_dim else 19)
         for n, (dA, dB, dm) in ref.items():
             check(got[n][0], dA, f"dA {n}", worst)
             check(got[n][1], dB, f"dB {n}", worst)
