@@ -321,7 +321,9 @@ struct sa3k_dit {
     const float* local_in = nullptr;  // bound conditioning [B][T][local_dim] (device) or null
     float* lc = nullptr;            // [B*T][kp] the padded conditioning of the current step
     std::vector<float*> lh, la, le;   // [depth] x [B*T][dim]: local.0 output, its silu, local.2 output
-    float *dle = nullptr, *dla = nullptr, *dlh = nullptr;   // [B*T][dim] backward scratch
+    std::vector<float*> dle;        // [depth] x [B*T][dim]: each block's local-add gradient
+    float *dla = nullptr, *dlh = nullptr;   // [B*T][dim] backward scratch
+    std::vector<hipEvent_t> lev;    // [depth] block l's local MLP output is ready (second stream)
     // activations
     std::vector<sa3k_block_ws*> ws;
     std::vector<float*> xs;
@@ -406,6 +408,8 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
         if (d->hw[i]) sa3k_weight_destroy(ctx, d->hw[i]);
         if (d->hbnsq[i]) (void)hipFree(d->hbnsq[i]);
     }
+    for (hipEvent_t e : d->lev)
+        if (e) (void)hipEventDestroy(e);
     for (size_t i = 0; i < d->ll.size(); ++i) {
         if (d->ll[i]) sa3k_lin_destroy(ctx, d->ll[i]);
         if (d->lw[i]) sa3k_weight_destroy(ctx, d->lw[i]);
@@ -583,6 +587,8 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     d->da = fbuf(d, 6 * B * D); d->dh = fbuf(d, 6 * B * D); d->dg = fbuf(d, B * D);
     d->dca = fbuf(d, NC * D); d->dch = fbuf(d, NC * D);
     if (c.local_dim > 0) {
+        d->lev.assign((size_t)c.depth, nullptr);
+        for (hipEvent_t& e : d->lev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         d->lc = fbuf(d, (size_t)NT * d->kp);
         for (int l = 0; l < c.depth; ++l) {
             d->lh.push_back(fbuf(d, NT * D));
@@ -590,7 +596,8 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
             d->le.push_back(fbuf(d, NT * D));
         }
         if (tr.scope == SA3K_SCOPE_FULL) {
-            d->dle = fbuf(d, NT * D); d->dla = fbuf(d, NT * D); d->dlh = fbuf(d, NT * D);
+            for (int l = 0; l < c.depth; ++l) d->dle.push_back(fbuf(d, NT * D));
+            d->dla = fbuf(d, NT * D); d->dlh = fbuf(d, NT * D);
             d->lA = fbuf(d, (size_t)c.depth * tr.rank * d->kp);
             d->ldA = fbuf(d, (size_t)tr.rank * d->kp);
             fill(ctx, d->ldA, (int64_t)tr.rank * d->kp, 0.0f);
@@ -705,8 +712,9 @@ void bind_kv(sa3k_dit* d, sa3k_block_ws* w, int l) {
 void bind_local(sa3k_dit* d, sa3k_block_ws* w, int l) {
     const bool on = d->local_in != nullptr;
     w->ladd = on ? d->le[l] : nullptr;
-    w->dladd = on && d->dle && (d->local_target[(size_t)2 * l] >= 0 || d->local_target[(size_t)2 * l + 1] >= 0)
-                   ? d->dle : nullptr;
+    w->dladd = on && !d->dle.empty() &&
+                       (d->local_target[(size_t)2 * l] >= 0 || d->local_target[(size_t)2 * l + 1] >= 0)
+                   ? d->dle[l] : nullptr;
     w->ladd_T = d->tr.frames;
 }
 
@@ -719,7 +727,7 @@ void local_fwd(sa3k_ctx* ctx, sa3k_dit* d, int l) {
                               d->le[l]));
 }
 
-// the local MLP's backward from dle (written by block l's backward): adapter gradients only (the
+// the local MLP's backward from dle[l] (written by block l's backward): adapter gradients only (the
 // conditioning is data); local.0's dA comes out at kp columns and is folded into the arena
 void local_bwd(sa3k_ctx* ctx, sa3k_dit* d, int l) {
     const int64_t NT = (int64_t)d->tr.batch * d->tr.frames, n = NT * d->cfg.dim;
@@ -734,7 +742,7 @@ void local_bwd(sa3k_ctx* ctx, sa3k_dit* d, int l) {
     };
     float *dA, *dB, *dm;
     grads((size_t)2 * l + 1, &dA, &dB, &dm);
-    chk(ctx, sa3k_lin_backward(ctx, d->ll[(size_t)2 * l + 1], SA3K_TYPE_F32, d->la[l], NT, d->dle, d->dla, 0, dA, dB,
+    chk(ctx, sa3k_lin_backward(ctx, d->ll[(size_t)2 * l + 1], SA3K_TYPE_F32, d->la[l], NT, d->dle[l], d->dla, 0, dA, dB,
                                dm));
     if (d->local_target[(size_t)2 * l] < 0) return;
     launch(ctx, "dit_local", silu_bwd_kernel, dim3(nblk(n)), (const float*)d->dla, (const float*)d->lh[l], n, d->dlh);
@@ -771,14 +779,25 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     lin_fwd(ctx, d, H_PROJ_IN, d->xp, NT, d->xi);
     launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B, T,
            c.mem_tokens, (int)D, d->xs[0]);
-    if (d->local_in)   // the inpaint conditioning, zero-padded to local.0's kp input columns
+    // the inpaint conditioning, zero-padded to local.0's kp input columns; every block's local MLP
+    // depends on it alone, so all of them run up front on the second stream and block l waits for
+    // its own MLP only
+    const bool local_side = d->local_in && side_usable(ctx);
+    if (d->local_in) {
         launch(ctx, "dit_local", pad_cols_kernel<float>, dim3(nblk(NT * d->kp)), d->local_in, NT,
                (int64_t)c.local_dim, (int64_t)d->kp, d->lc);
+        if (local_side) side_fork(ctx);
+        OnSide os(ctx, local_side);
+        for (int l = 0; l < c.depth; ++l) {
+            local_fwd(ctx, d, l);
+            if (local_side) SA3K_HIP(hipEventRecord(d->lev[l], ctx->side_stream));
+        }
+    }
     // blocks
     for (int l = 0; l < c.depth; ++l) {
         bind_kv(d, d->ws[d->tr.recompute ? 0 : l], l);
         bind_local(d, d->ws[d->tr.recompute ? 0 : l], l);
-        if (d->local_in) local_fwd(ctx, d, l);
+        if (local_side) SA3K_HIP(hipStreamWaitEvent(ctx->main_stream, d->lev[l], 0));
         block_forward(ctx, d->blocks[l], d->ws[d->tr.recompute ? 0 : l], d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         if (d->tr.recompute) side_join_since(ctx, forks0);
     }
@@ -838,7 +857,12 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
         // resident activations: a block's last second-stream work may run on beside the next block
         block_backward(ctx, d->blocks[l], w, dcur, dnext, d->dctx, d->dgcond, dA, dB, d->tr.dora ? dm : nullptr,
                        ctx->late_join && !d->tr.recompute);
-        if (w->dladd) local_bwd(ctx, d, l);
+        if (w->dladd) {   // reads block l's own buffers only: beside the next blocks on the second stream
+            const bool side = side_usable(ctx);
+            if (side) side_fork(ctx);
+            OnSide os(ctx, side);
+            local_bwd(ctx, d, l);
+        }
         std::swap(dcur, dnext);
     }
     if (side_usable(ctx)) side_join(ctx);   // the head reads dgcond; AdamW reads every dA
