@@ -233,7 +233,7 @@ SA3K_API int sa3k_gemm_nt(sa3k_ctx* ctx, int prec, int a_type, const void* A, in
  * tight serving loops, harnesses that forbid hipMalloc). No reference counterpart: ggml allocates
  * its graphs up front (src/train_ckpt.h), and this entry point serves those callers instead.
  * Same arguments, kernels and results (bit for bit) as sa3k_gemm_nt, but the split-K partial sums
- * go to a fixed 32 MiB scratch array in device memory that the library's code object carries (one
+ * go to a fixed 64 MiB scratch array in device memory that the library's code object carries (one
  * copy per GPU, held until the process ends), and the call never allocates. Every split plan the
  * dispatch chooses by itself fits; a plan that would need more (only possible when the
  * "gemm_splits" option forces a split count) fails with SA3K_ERR_INVALID before anything is

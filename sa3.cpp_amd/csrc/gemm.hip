@@ -40,12 +40,12 @@ struct KParams {
 }  // namespace
 
 // Scratch of sa3k_gemm_nt_noalloc: the split-K partial sums of one GEMM, in device memory that
-// the code object itself carries (no hipMalloc at any call). 32 MiB covers every split plan the
+// the code object itself carries (no hipMalloc at any call). 64 MiB covers every split plan the
 // dispatch chooses by itself: a GEMM splits only while its tiles fill fewer than the chip's
-// resident slots (512 for 128 x 128 tiles, 256 for 128 x 256 ones; 256 x 256 tiles are taken only
-// for grids of at least 200 tiles and then never split), so splits x tiles x tile floats <= 2^23.
-// Every GPU that loads the library holds its own copy until the process ends.
-constexpr size_t kNoAllocScratchFloats = (size_t)1 << 23;
+// resident slots (512 for 128 x 128 tiles, 256 for 128 x 256 and 256 x 256 ones), so splits x
+// tiles x tile floats <= 256 x 65536 = 2^24. Every GPU that loads the library holds its own copy
+// until the process ends.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 24;
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 namespace {

@@ -1187,7 +1187,8 @@ int64_t dma_rounds(const sa3k_ctx* ctx, int64_t Mt, int64_t Nt, int64_t K) {
         const int64_t t256 = ceil_div(Mt, 256) * ceil_div(Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
         const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
         const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02)) return rounds(t256, 256, true);
+        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && K >= 8192))
+            return rounds(t256, 256, true);
     }
     if (Mt <= 32 || Nt <= 64) return 1;
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);

@@ -79,7 +79,8 @@ struct sa3k_ctx {
     int gemm_cfg = 0;                     // DMA kernel tile configuration
     int gemm_nt_store = 1;                // GEMM outputs written with non-temporal stores
     int gemm_skinny = 1;                  // products with <= 32 output columns on the skinny kernel
-    int gemm_big = 1;                     // 256 x 256 bf16 tiles: 0 never, 1 where they fill the chip, 2 always
+    int gemm_big = 3;                     // 256 x 256 bf16 tiles: 0 never, 1 where they fill the chip, 2 always,
+                                          // 3 as 1 plus every product with K >= 8192 (split over K)
     int gemm_splits = 0;                  // > 0: split-K count of DMA GEMMs that split (for measurement)
     int gemm_small = 2;                   // tile configuration for small grids (0: the default tile + split-K)
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)

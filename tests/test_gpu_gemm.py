@@ -174,7 +174,7 @@ def test_big_tile_gemm(ctx, M, N, K):
         ctx.set_option("gemm_big", 0)
         small = run(ctx, *args, bias=bias, colscale=cs)
     finally:
-        ctx.set_option("gemm_big", 1)
+        ctx.set_option("gemm_big", 3)
     assert np.array_equal(got, again), "not deterministic"
     assert rel_err(got, ref) < 1e-5
     assert max_rel_err(got, small) < 1e-5
@@ -204,7 +204,7 @@ def test_gemm_decoded_b_on_dma_kernel(ctx, M, N, K, btype):
         loader = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, bt, B_scales=sc, ldbs=ldbs)
     finally:
         ctx.set_option("gemm_dq", 1)
-        ctx.set_option("gemm_big", 1)
+        ctx.set_option("gemm_big", 3)
     Af = (A.astype(np.uint32) << 16).view(np.float32)
     ref = Af.astype(np.float64) @ bf16_round(dec).astype(np.float64).T
     assert np.array_equal(got, copy)

@@ -143,7 +143,7 @@ def test_dora_linear_big_tiles(ctx, N, in_, out_, r, merge):
         ctx.set_option("gemm_big", 0)
         small = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16, merge=merge)
     finally:
-        ctx.set_option("gemm_big", 1)
+        ctx.set_option("gemm_big", 3)
     ref = run_oracle(X, dY, Wdec, A, B, 1.5, True, mag)
     for k in ("Y", "dX", "dA", "dB", "dm"):
         assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
@@ -267,7 +267,7 @@ def test_dx_k_major_operand(ctx, big):
             nk = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
         finally:
             ctx.set_option("merge_kn", 1)
-            ctx.set_option("gemm_big", 1)
+            ctx.set_option("gemm_big", 3)
         ref = run_oracle(X, dY, Wdec, A, B, 1.25, True, mag)
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(kn[k], ref[k]) < 2e-2 and cosine(kn[k], ref[k]) >= 0.9999, (N, k)

@@ -78,7 +78,7 @@ def test_noalloc_without_split(ctx):
 
 
 def test_noalloc_rejects_plan_beyond_scratch(ctx):
-    # a forced split count whose partials exceed the 32 MiB array: a clear error before any launch,
+    # a forced split count whose partials exceed the 64 MiB array: a clear error before any launch,
     # after which the entry point and the context keep working
     r = rng(5)
     M = N = 1024
@@ -86,7 +86,7 @@ def test_noalloc_rejects_plan_beyond_scratch(ctx):
     A, at, B, bt, _, _, prec = _inputs(r, M, N, K, "bf16-dma")
     dA, dB = ctx.upload(A), ctx.upload(B)
     dC = ctx.zeros((M, N))
-    ctx.set_option("gemm_splits", 16)   # 16 x 1024 x 1024 floats = 64 MiB of partials
+    ctx.set_option("gemm_splits", 32)   # 32 x 1024 x 1024 floats = 128 MiB of partials
     try:
         print("gemm_nt_noalloc forced split beyond the scratch (host-side rejection)", flush=True)
         with pytest.raises(sa3k.Sa3kError) as e:
