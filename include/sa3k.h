@@ -528,7 +528,7 @@ SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
 SA3K_API int sa3k_dit_eval_loss(sa3k_ctx* ctx, sa3k_dit* dit, const float* x_t, const float* target, const float* t,
                                 const float* cross, const float* glob, const float* loss_weight, double* loss_out);
 /* Bind the inpaint local conditioning [B][T][local_dim] f32 (device; TrainInpaint::local,
- * src/train_inpaint.h:155-194, set as TrainDitGraph::local by run_train_dit_accumulate,
+ * src/train_inpaint.h:145-194, set as TrainDitGraph::local by run_train_dit_accumulate,
  * src/train_loop.h:239-242) for the following sa3k_dit_accumulate / sa3k_dit_eval_loss /
  * sa3k_dit_forward calls: each block then adds local.2(silu(local.0(local))) to its T latent rows
  * after the cross-attention (src/dit.h:244-254), and in the full scope the local linears' adapters
