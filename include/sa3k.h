@@ -141,10 +141,22 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *   "attn_fwd32"  1: attention forwards over more than 128 keys run on 32x32x16 MFMA blocks with
  *                 one branch per wave; 0: every forward on the 16x16x32 kernel that carries both
  *                 branches per wave (default 1)
+ *   "head_f32"    1: a DiT's twelve head / tail linears (pre_conv, proj_in, the time, global,
+ *                 gce and cond embeddings, proj_out, post_conv) compute on f32 MFMA when the base
+ *                 is f32 or f16, each refreshed by its own two-segment prepare; 0: bf16 like the
+ *                 blocks (default 1). It holds from a DiT's setup.
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
- * kv_stack and attn_fwd32, which change the f32 summation order. Not to be changed while a graph is being captured. */
+ * kv_stack, attn_fwd32 and head_f32, which change the rounding or the f32 summation order. Not to
+ * be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
+
+/* The current value of an option (the names of sa3k_set_option). No reference counterpart: the
+ * tests use it to run with, and to restore, the shipped defaults. */
+SA3K_API int sa3k_get_option(sa3k_ctx* ctx, const char* name, int* value);
+
+/* The name of option `index` (0, 1, ...), NULL past the last one. No reference counterpart. */
+SA3K_API const char* sa3k_option_name(int index);
 
 /* Stream timer: sa3k_timer_start records an event on the context stream, sa3k_timer_stop records a
  * second one, synchronises and returns the elapsed milliseconds between them. */

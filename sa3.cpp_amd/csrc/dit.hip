@@ -295,6 +295,7 @@ struct sa3k_dit {
     sa3k_lin* hl[H_N] = {};
     float* hbnsq[H_N] = {};
     const float* hbias[H_N] = {};
+    bool hf32[H_N] = {};            // head linear i computes in f32 (refreshed by its own prepare)
     const float* memtok = nullptr;
     // adapters
     std::vector<Target> targets;    // sorted by name
@@ -469,7 +470,13 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         Tensor& t = tensor(d, std::string("dit.") + kHeadNames[i] + ".weight");
         chk(ctx, sa3k_weight_create(ctx, d->wtype, t.cols, t.rows, t.raw, 1, &d->hw[i]));
         const int r = tr.scope == SA3K_SCOPE_FULL ? tr.rank : 0;
-        chk(ctx, sa3k_lin_create(ctx, d->hw[i], r, SA3K_PREC_BF16, head_tokens[i], &d->hl[i]));
+        // The head and tail sit at both ends of every gradient chain: the conditioning linears see
+        // B or B*Ctx tokens (nothing averages their rounding) and feed every block's modulation,
+        // and proj_in / proj_out carry the whole residual stream's gradient. They run on f32 MFMA
+        // (a fraction of a percent of the update's work) over an f32 or f16 base.
+        d->hf32[i] = ctx->head_f32 && (d->wtype == SA3K_TYPE_F32 || d->wtype == SA3K_TYPE_F16);
+        chk(ctx, sa3k_lin_create(ctx, d->hw[i], r, d->hf32[i] ? SA3K_PREC_F32 : SA3K_PREC_BF16, head_tokens[i],
+                                 &d->hl[i]));
         lin_set_tag(d->hl[i], "head");
         if (r && tr.dora) {
             d->hbnsq[i] = dalloc<float>((size_t)t.rows);
@@ -631,7 +638,12 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
     {
         std::vector<sa3k_lin*> lins;
         std::vector<const float*> A, Bm, mag, bnsq;
-        for (const Target& t : d->targets) {
+        std::vector<bool> f32_lin(d->targets.size(), false);
+        for (int i = 0; i < H_N; ++i)
+            if (d->head_target[i] >= 0 && d->hf32[i]) f32_lin[(size_t)d->head_target[i]] = true;
+        for (size_t k = 0; k < d->targets.size(); ++k) {
+            const Target& t = d->targets[k];
+            if (f32_lin[k]) continue;   // refreshed by prepare() on their own
             lins.push_back(t.lin);
             A.push_back(t.a_src ? t.a_src : d->p + t.off_a);
             Bm.push_back(d->p + t.off_b);
@@ -661,6 +673,13 @@ void prepare(sa3k_ctx* ctx, sa3k_dit* d) {
         launch(ctx, "dit_local", pad_a_kernel, dim3(nblk((int64_t)d->tr.rank * d->kp), (unsigned)d->cfg.depth),
                (const float*)d->p, (const int64_t*)d->lA_off, d->tr.rank, d->cfg.local_dim, d->kp, d->lA);
     lin_group_prepare(ctx, d->group);
+    for (int i = 0; i < H_N; ++i) {   // the f32 head linears: their two-segment refresh
+        if (!d->hf32[i] || d->head_target[i] < 0) continue;
+        const Target& t = d->targets[(size_t)d->head_target[i]];
+        const bool dora = d->tr.dora != 0;
+        chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], d->p + t.off_a, d->p + t.off_b, d->scale, dora ? 1 : 0,
+                                  dora ? d->p + t.off_m : nullptr, dora ? t.bnsq : nullptr));
+    }
     d->dirty = false;
 }
 

@@ -223,31 +223,58 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
     });
 }
 
+}  // extern "C"
+
+namespace {
+// Every tunable of a context, by name: sa3k_set_option / sa3k_get_option / sa3k_option_name.
+struct OptionDef {
+    const char* name;
+    int sa3k_ctx::*field;
+    bool flag;   // stored as 0 / 1
+};
+const OptionDef kOptions[] = {
+    {"gemm_split", &sa3k_ctx::gemm_split, true},   {"gemm_fixup", &sa3k_ctx::gemm_fixup, false},
+    {"gemm_dma", &sa3k_ctx::gemm_dma, true},       {"gemm_dq", &sa3k_ctx::gemm_dq, false},
+    {"gemm_cfg", &sa3k_ctx::gemm_cfg, false},      {"gemm_small", &sa3k_ctx::gemm_small, false},
+    {"gemm_nt_store", &sa3k_ctx::gemm_nt_store, true}, {"gemm_skinny", &sa3k_ctx::gemm_skinny, true},
+    {"gemm_big", &sa3k_ctx::gemm_big, false},      {"gemm_splits", &sa3k_ctx::gemm_splits, false},
+    {"side_stream", &sa3k_ctx::use_side, true},    {"fork_tail", &sa3k_ctx::fork_tail, true},
+    {"late_join", &sa3k_ctx::late_join, true},     {"lin_merge", &sa3k_ctx::lin_merge, true},
+    {"rank_cols", &sa3k_ctx::rank_cols, false},    {"merge_kn", &sa3k_ctx::merge_kn, true},
+    {"tn_fuse", &sa3k_ctx::tn_fuse, false},        {"kv_stack", &sa3k_ctx::kv_stack, true},
+    {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
+};
+constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
+
+const OptionDef& find_option(const char* name) {
+    SA3K_REQUIRE(name != nullptr, "null option name");
+    for (const OptionDef& o : kOptions)
+        if (std::strcmp(o.name, name) == 0) return o;
+    sa3k_throw(SA3K_ERR_INVALID, std::string("unknown option ") + name);
+    return kOptions[0];   // not reached
+}
+}  // namespace
+
+extern "C" {
+
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
     return sa3k_guard(ctx, "sa3k_set_option", [&] {
-        SA3K_REQUIRE(name != nullptr, "null option name");
-        const std::string n(name);
-        if (n == "gemm_split") ctx->gemm_split = value != 0;
-        else if (n == "gemm_fixup") ctx->gemm_fixup = value;
-        else if (n == "gemm_dma") ctx->gemm_dma = value != 0;
-        else if (n == "gemm_dq") ctx->gemm_dq = value;
-        else if (n == "gemm_cfg") ctx->gemm_cfg = value;
-        else if (n == "gemm_small") ctx->gemm_small = value;
-        else if (n == "gemm_nt_store") ctx->gemm_nt_store = value != 0;
-        else if (n == "gemm_skinny") ctx->gemm_skinny = value != 0;
-        else if (n == "gemm_big") ctx->gemm_big = value;
-        else if (n == "gemm_splits") ctx->gemm_splits = std::max(0, value);
-        else if (n == "side_stream") ctx->use_side = value != 0;
-        else if (n == "fork_tail") ctx->fork_tail = value != 0;
-        else if (n == "late_join") ctx->late_join = value != 0;
-        else if (n == "lin_merge") ctx->lin_merge = value != 0;
-        else if (n == "rank_cols") ctx->rank_cols = value;
-        else if (n == "merge_kn") ctx->merge_kn = value != 0;
-        else if (n == "tn_fuse") ctx->tn_fuse = value;
-        else if (n == "kv_stack") ctx->kv_stack = value != 0;
-        else if (n == "attn_fwd32") ctx->attn_fwd32 = value;
-        else sa3k_throw(SA3K_ERR_INVALID, "unknown option " + n);
+        const OptionDef& o = find_option(name);
+        int v = o.flag ? (value != 0) : value;
+        if (o.field == &sa3k_ctx::gemm_splits) v = std::max(0, v);
+        ctx->*o.field = v;
     });
+}
+
+SA3K_API int sa3k_get_option(sa3k_ctx* ctx, const char* name, int* value) {
+    return sa3k_guard(ctx, "sa3k_get_option", [&] {
+        SA3K_REQUIRE(value != nullptr, "value is null");
+        *value = ctx->*find_option(name).field;
+    });
+}
+
+SA3K_API const char* sa3k_option_name(int index) {
+    return index >= 0 && index < kNumOptions ? kOptions[index].name : nullptr;
 }
 
 SA3K_API int sa3k_timer_start(sa3k_ctx* ctx) {

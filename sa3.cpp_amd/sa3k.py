@@ -89,6 +89,8 @@ def _declare(lib):
         "sa3k_memset": (I, [P, P, I, C.c_size_t]),
         "sa3k_sync": (I, [P]),
         "sa3k_set_option": (I, [P, C.c_char_p, I]),
+        "sa3k_get_option": (I, [P, C.c_char_p, C.POINTER(I)]),
+        "sa3k_option_name": (C.c_char_p, [I]),
         "sa3k_timer_start": (I, [P]),
         "sa3k_timer_stop": (I, [P, C.POINTER(F)]),
         "sa3k_profile_enable": (I, [P, I]),
@@ -270,6 +272,25 @@ class Context:
 
     def set_option(self, name, value):
         self.check(self.lib.sa3k_set_option(self.h, name.encode(), int(value)))
+
+    def get_option(self, name):
+        v = C.c_int()
+        self.check(self.lib.sa3k_get_option(self.h, name.encode(), C.byref(v)))
+        return v.value
+
+    def options(self):
+        """{name: value} of every option of this context"""
+        names = []
+        while True:
+            n = self.lib.sa3k_option_name(len(names))
+            if not n:
+                break
+            names.append(n.decode())
+        return {n: self.get_option(n) for n in names}
+
+    def set_options(self, opts):
+        for n, v in opts.items():
+            self.set_option(n, v)
 
     def timer_start(self):
         self.check(self.lib.sa3k_timer_start(self.h))

@@ -30,8 +30,26 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def ctx():
     c = sa3k.Context(0)
+    c.defaults = c.options()   # the shipped option values, as a fresh context has them
     yield c
     c.close()
+
+
+@pytest.fixture(autouse=True)
+def _restore_options(request):
+    """After every test that used the GPU context, put every option back to its shipped default,
+    so that no test runs with a value another test left behind."""
+    yield
+    if "ctx" in request.fixturenames:
+        c = request.getfixturevalue("ctx")
+        c.set_options(c.defaults)
+
+
+def assert_shipped_options(c):
+    """the context runs the shipped configuration: every option at its default"""
+    now = c.options()
+    diff = {k: (now[k], v) for k, v in c.defaults.items() if now[k] != v}
+    assert not diff, f"options differ from the defaults (now, default): {diff}"
 
 
 def rng(seed):

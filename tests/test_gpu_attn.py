@@ -66,7 +66,7 @@ def test_attention_single_key_window(ctx):
             assert np.array_equal(o1.numpy(), X[4].numpy()), fwd32
             assert np.array_equal(o2.numpy(), X[4].numpy()), fwd32
     finally:
-        ctx.set_option("attn_fwd32", 1)
+        ctx.set_options(ctx.defaults)
 
 
 @pytest.mark.parametrize("fwd32", [0, 1])
@@ -80,4 +80,4 @@ def test_attention_forward_kernels(ctx, fwd32, B, H, Sq, Sk, window):
     try:
         run(ctx, B, H, Sq, Sk, window, seed=7 * Sq + window, check_bwd=False)
     finally:
-        ctx.set_option("attn_fwd32", 1)
+        ctx.set_options(ctx.defaults)

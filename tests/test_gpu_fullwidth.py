@@ -16,7 +16,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import ROOT, cosine, rel_err, rng, sa3k
+from conftest import ROOT, assert_shipped_options, cosine, rel_err, rng, sa3k
 from test_gpu_block import GpuBlock, run_gpu, to_f16_grid
 from test_gpu_dit import grads_by_target, make_gpu, upload_inputs
 
@@ -37,6 +37,7 @@ def check(got, ref, what, worst):
 
 @pytest.mark.parametrize("window", [256, 0])
 def test_block_full_width_vs_oracle(ctx, window):
+    assert_shipped_options(ctx)   # the shipped configuration: every option at its default
     B, S, Ctx = 2, 64 + 72, 128
     print(f"full-width block vs oracle: window {window}, B {B}, S {S}, Ctx {Ctx}", flush=True)
     cfg, w, x, cx, gc = bb.random_block(51 + window, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
@@ -68,6 +69,7 @@ def test_block_full_width_vs_oracle(ctx, window):
 def test_dit_depth1_full_width_vs_oracle(ctx, local_dim):
     # local_dim 257: the reference's inpaint model ([mask | z * mask] over its 256 latent channels),
     # local.0's input padded to 320 columns on the device, the local linears adapted (full scope)
+    assert_shipped_options(ctx)   # the shipped configuration: every option at its default
     cfg = dict(B=2, T=72, Ctx=128, io=64, dim=1536, heads=24, inner=6144, depth=1, mem=64, cond_dim=768,
                time_dim=256, rope_dims=32, window=256, rank=32, alpha=32.0, dora=True, local_dim=local_dim)
     print(f"full-width depth-1 DiT vs oracle: T 72, Ctx 128, window 256, DoRA r32 full scope, local_dim {local_dim}",

@@ -127,7 +127,7 @@ def test_split_k_fixup_matches_separate_reduction(ctx, M, N, K):
                 assert np.array_equal(res, out[fixup]), "not deterministic"
             out[fixup] = res
     finally:
-        ctx.set_option("gemm_fixup", 0)
+        ctx.set_options(ctx.defaults)
     assert np.array_equal(out[0], out[1]) and np.array_equal(out[0], out[2])
 
 
@@ -148,7 +148,7 @@ def test_skinny_gemm(ctx, M, N, K):
         ctx.set_option("gemm_skinny", 0)
         tiled = run(ctx, *args)
     finally:
-        ctx.set_option("gemm_skinny", 1)
+        ctx.set_options(ctx.defaults)
     assert np.array_equal(got, again), "not deterministic"
     assert rel_err(got, ref) < 1e-5
     assert rel_err(tiled, ref) < 1e-5
@@ -174,7 +174,7 @@ def test_big_tile_gemm(ctx, M, N, K):
         ctx.set_option("gemm_big", 0)
         small = run(ctx, *args, bias=bias, colscale=cs)
     finally:
-        ctx.set_option("gemm_big", 3)
+        ctx.set_options(ctx.defaults)
     assert np.array_equal(got, again), "not deterministic"
     assert rel_err(got, ref) < 1e-5
     assert max_rel_err(got, small) < 1e-5
@@ -203,8 +203,7 @@ def test_gemm_decoded_b_on_dma_kernel(ctx, M, N, K, btype):
         ctx.set_option("gemm_dq", 0)
         loader = run(ctx, A, Bop, M, N, K, sa3k.PREC_BF16, sa3k.TYPE_BF16, bt, B_scales=sc, ldbs=ldbs)
     finally:
-        ctx.set_option("gemm_dq", 1)
-        ctx.set_option("gemm_big", 3)
+        ctx.set_options(ctx.defaults)
     Af = (A.astype(np.uint32) << 16).view(np.float32)
     ref = Af.astype(np.float64) @ bf16_round(dec).astype(np.float64).T
     assert np.array_equal(got, copy)

@@ -48,7 +48,7 @@ def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1,
     try:
         lin.prepare(dA_, dB_, s, dora, dmag, bnsq)
     finally:
-        ctx.set_option("lin_merge", 1)
+        ctx.set_options(ctx.defaults)
     dX_, dY_ = ctx.upload(X), ctx.upload(dY)
     Y = ctx.empty((N, out_))
     gX, gA, gB, gm = ctx.empty((N, in_)), ctx.zeros((r, in_)), ctx.zeros((out_, r)), ctx.zeros(out_)
@@ -143,7 +143,7 @@ def test_dora_linear_big_tiles(ctx, N, in_, out_, r, merge):
         ctx.set_option("gemm_big", 0)
         small = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.5, True, mag, sa3k.PREC_BF16, merge=merge)
     finally:
-        ctx.set_option("gemm_big", 3)
+        ctx.set_options(ctx.defaults)
     ref = run_oracle(X, dY, Wdec, A, B, 1.5, True, mag)
     for k in ("Y", "dX", "dA", "dB", "dm"):
         assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, k
@@ -238,8 +238,7 @@ def test_rank_products_as_extra_columns(ctx, cols):
             ctx.set_option("rank_cols", 0)
             sep = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
         finally:
-            ctx.set_option("rank_cols", 1)
-            ctx.set_option("merge_kn", 1)
+            ctx.set_options(ctx.defaults)
         ref = run_oracle(X, dY, Wdec, A, B, 1.0, True, mag)
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, (N, k)
@@ -266,8 +265,7 @@ def test_dx_k_major_operand(ctx, big):
             ctx.set_option("merge_kn", 0)
             nk = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
         finally:
-            ctx.set_option("merge_kn", 1)
-            ctx.set_option("gemm_big", 3)
+            ctx.set_options(ctx.defaults)
         ref = run_oracle(X, dY, Wdec, A, B, 1.25, True, mag)
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(kn[k], ref[k]) < 2e-2 and cosine(kn[k], ref[k]) >= 0.9999, (N, k)
@@ -292,7 +290,7 @@ def test_fused_reductions_bit_identical(ctx, merge, dora):
                 res.append(run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 0.5, dora, mag, sa3k.PREC_BF16, reps=2,
                                    merge=merge))
         finally:
-            ctx.set_option("tn_fuse", 1)
+            ctx.set_options(ctx.defaults)
         for other in res[1:]:
             for k in ("Y", "dX", "dA", "dB") + (("dm",) if dora else ()):
                 assert np.array_equal(res[0][k], other[k]), (N, k)

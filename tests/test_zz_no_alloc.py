@@ -93,6 +93,6 @@ def test_noalloc_rejects_plan_beyond_scratch(ctx):
             ctx.gemm_nt(dA, dB, M, N, K, prec=prec, a_type=at, b_type=bt, C=dC, noalloc=True)
         assert e.value.code == 1 and "scratch" in str(e.value)
     finally:
-        ctx.set_option("gemm_splits", 0)
+        ctx.set_options(ctx.defaults)
     ref, got = _pair(ctx, r, 256, 256, 4096, "bf16-dma", False)
     assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
