@@ -296,6 +296,7 @@ struct sa3k_dit {
     float* hbnsq[H_N] = {};
     const float* hbias[H_N] = {};
     bool hf32[H_N] = {};            // head linear i computes in f32 (refreshed by its own prepare)
+    bool group_pending = false;     // the grouped refresh is running on the second stream
     const float* memtok = nullptr;
     // adapters
     std::vector<Target> targets;    // sorted by name
@@ -305,7 +306,8 @@ struct sa3k_dit {
     int64_t n_params = 0;
     bool dirty = true;
     int count = 0;
-    LinGroup* group = nullptr;      // every adapted linear, refreshed together
+    LinGroup* group = nullptr;      // every adapted bf16 linear, refreshed together
+    LinGroup* hgroup = nullptr;     // the adapted f32 head / tail linears, refreshed together
     LinStack* kvs = nullptr;        // the blocks' context K/V projections as one product (or null)
     // inpaint local conditioning (cfg.local_dim > 0): per block local.0 (local_dim -> dim, its
     // input padded to kp columns) and local.2 (dim -> dim), both with biases, adapted in the full
@@ -422,6 +424,7 @@ void free_dit(sa3k_ctx* ctx, sa3k_dit* d) {
     for (hipGraphExec_t e : d->gexec)
         if (e) (void)hipGraphExecDestroy(e);
     lin_group_free(d->group);
+    lin_group_free(d->hgroup);
     lin_stack_free(d->kvs);
     for (float* p : {d->p, d->g, d->m, d->v})
         if (p) (void)hipFree(p);
@@ -641,17 +644,22 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
         std::vector<bool> f32_lin(d->targets.size(), false);
         for (int i = 0; i < H_N; ++i)
             if (d->head_target[i] >= 0 && d->hf32[i]) f32_lin[(size_t)d->head_target[i]] = true;
+        std::vector<sa3k_lin*> hlins;
+        std::vector<const float*> hA, hBm, hmag, hbnsq;
         for (size_t k = 0; k < d->targets.size(); ++k) {
             const Target& t = d->targets[k];
-            if (f32_lin[k]) continue;   // refreshed by prepare() on their own
-            lins.push_back(t.lin);
-            A.push_back(t.a_src ? t.a_src : d->p + t.off_a);
-            Bm.push_back(d->p + t.off_b);
-            mag.push_back(tr.dora ? d->p + t.off_m : nullptr);
-            bnsq.push_back(tr.dora ? t.bnsq : nullptr);
+            const bool f32 = f32_lin[k];   // the f32 head linears form a group of their own
+            (f32 ? hlins : lins).push_back(t.lin);
+            (f32 ? hA : A).push_back(t.a_src ? t.a_src : d->p + t.off_a);
+            (f32 ? hBm : Bm).push_back(d->p + t.off_b);
+            (f32 ? hmag : mag).push_back(tr.dora ? d->p + t.off_m : nullptr);
+            (f32 ? hbnsq : bnsq).push_back(tr.dora ? t.bnsq : nullptr);
         }
         d->group = lin_group_create(ctx, lins.data(), (int)lins.size(), A.data(), Bm.data(), mag.data(), bnsq.data(),
                                     d->scale, tr.dora);
+        if (!hlins.empty())
+            d->hgroup = lin_group_create(ctx, hlins.data(), (int)hlins.size(), hA.data(), hBm.data(), hmag.data(),
+                                         hbnsq.data(), d->scale, tr.dora);
         for (int i = 0; i < H_N; ++i)
             if (d->head_target[i] < 0)
                 chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
@@ -669,18 +677,29 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
 void prepare(sa3k_ctx* ctx, sa3k_dit* d) {
     if (!d->dirty) return;
     KernelScope ks(ctx, "dit_prepare");
-    if (d->lA)   // local.0's A at kp columns for its padded product
-        launch(ctx, "dit_local", pad_a_kernel, dim3(nblk((int64_t)d->tr.rank * d->kp), (unsigned)d->cfg.depth),
-               (const float*)d->p, (const int64_t*)d->lA_off, d->tr.rank, d->cfg.local_dim, d->kp, d->lA);
-    lin_group_prepare(ctx, d->group);
-    for (int i = 0; i < H_N; ++i) {   // the f32 head linears: their two-segment refresh
-        if (!d->hf32[i] || d->head_target[i] < 0) continue;
-        const Target& t = d->targets[(size_t)d->head_target[i]];
-        const bool dora = d->tr.dora != 0;
-        chk(ctx, sa3k_lin_prepare(ctx, d->hl[i], d->p + t.off_a, d->p + t.off_b, d->scale, dora ? 1 : 0,
-                                  dora ? d->p + t.off_m : nullptr, dora ? t.bnsq : nullptr));
+    // The grouped bf16 refresh streams every block weight (HBM-bound, the whole chip); the f32 head
+    // linears' refresh is a few short launches. With both, the bf16 group goes to the second stream
+    // and the heads' refresh and forwards run beside it on the main stream; forward() joins before
+    // the first product that reads a member of the bf16 group.
+    const bool side = d->hgroup && side_usable(ctx);
+    if (side) side_fork(ctx);
+    {
+        OnSide os(ctx, side);
+        if (d->lA)   // local.0's A at kp columns for its padded product
+            launch(ctx, "dit_local", pad_a_kernel, dim3(nblk((int64_t)d->tr.rank * d->kp), (unsigned)d->cfg.depth),
+                   (const float*)d->p, (const int64_t*)d->lA_off, d->tr.rank, d->cfg.local_dim, d->kp, d->lA);
+        lin_group_prepare(ctx, d->group);
     }
+    d->group_pending = side;
+    if (d->hgroup) lin_group_prepare(ctx, d->hgroup);   // the f32 head linears: two-segment refresh
     d->dirty = false;
+}
+
+// the main stream waits for the grouped refresh when prepare() left it on the second stream
+void join_group(sa3k_ctx* ctx, sa3k_dit* d) {
+    if (!d->group_pending) return;
+    side_join(ctx);
+    d->group_pending = false;
 }
 
 void lin_fwd(sa3k_ctx* ctx, sa3k_dit* d, int i, const float* X, int64_t N, float* Y) {
@@ -713,8 +732,9 @@ void mlp_fwd(sa3k_ctx* ctx, sa3k_dit* d, int i0, const float* x, int64_t N, floa
 void mlp_bwd(sa3k_ctx* ctx, sa3k_dit* d, int i0, const float* x, int64_t N, const float* h, const float* a,
              const float* dy, float* dx) {
     const int64_t n = N * d->cfg.dim;
-    float* da = N == d->tr.batch ? d->da : d->dca;
-    float* dh = N == d->tr.batch ? d->dh : d->dch;
+    // the context MLP has scratch of its own: its backward runs beside the modulation chain's
+    float* da = i0 == H_COND0 ? d->dca : d->da;
+    float* dh = i0 == H_COND0 ? d->dch : d->dh;
     lin_bwd(ctx, d, i0 + 1, a, N, dy, da, 0);
     launch(ctx, "dit_silu", silu_bwd_kernel, dim3(nblk(n)), (const float*)da, h, n, dh);
     lin_bwd(ctx, d, i0, x, N, dh, dx, 0);
@@ -791,13 +811,14 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
            d->gsum);
     mlp_fwd(ctx, d, H_GCE0, d->gsum, B, d->gce_h, d->gce_a, d->gcond);   // dim -> dim -> 6 dim
     mlp_fwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->context);
-    if (d->kvs) lin_stack_forward(ctx, d->kvs, d->context, NC);   // every block's context K/V
     // x path
     lin_fwd(ctx, d, H_PRE_CONV, x_t, NT, d->xp);
     launch(ctx, "dit_head", add_kernel, dim3(nblk(NT * c.io)), (const float*)d->xp, x_t, NT * c.io, d->xp);
     lin_fwd(ctx, d, H_PROJ_IN, d->xp, NT, d->xi);
     launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B, T,
            c.mem_tokens, (int)D, d->xs[0]);
+    join_group(ctx, d);   // every product from here on reads a member of the grouped refresh
+    if (d->kvs) lin_stack_forward(ctx, d->kvs, d->context, NC);   // every block's context K/V
     // the inpaint conditioning, zero-padded to local.0's kp input columns; every block's local MLP
     // depends on it alone, so all of them run up front on the second stream and block l waits for
     // its own MLP only
@@ -886,20 +907,30 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
     }
     if (side_usable(ctx)) side_join(ctx);   // the head reads dgcond; AdamW reads every dA
     ctx->block_tail_pending = false;
-    // head backward (only adapter gradients are wanted: the inputs are data)
+    // head backward (only adapter gradients are wanted: the inputs are data). Three independent
+    // chains of short launches: the modulation chain (gcond = gce(ge + te)) on the second stream,
+    // the x path and the context MLP on the main stream beside it (their own forks held back).
     if (d->tr.scope == SA3K_SCOPE_FULL) {
-        launch(ctx, "dit_head", gather_frames_kernel, dim3(nblk(NT * D)), (const float*)dcur, B, T, c.mem_tokens, (int)D,
-               d->dxi);
-        lin_bwd(ctx, d, H_PROJ_IN, d->xp, NT, d->dxi, d->dxp, 0);
-        lin_bwd(ctx, d, H_PRE_CONV, x_t, NT, d->dxp, nullptr, 0);
-        // gcond = gce(ge + te)
-        lin_bwd(ctx, d, H_GCE2, d->gce_a, B, d->dgcond, d->da, 0);
-        launch(ctx, "dit_silu", silu_bwd_kernel, dim3(nblk(B * D)), (const float*)d->da, (const float*)d->gce_h,
-               (int64_t)B * D, d->dh);
-        lin_bwd(ctx, d, H_GCE0, d->gsum, B, d->dh, d->dg, 0);
-        mlp_bwd(ctx, d, H_GLOBAL0, glob, B, d->ge_h, d->ge_a, d->dg, nullptr);
-        mlp_bwd(ctx, d, H_TIME0, d->tf, B, d->te_h, d->te_a, d->dg, nullptr);
-        mlp_bwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->dctx, nullptr);
+        const bool two = side_usable(ctx);
+        if (two) side_fork(ctx);   // dgcond, dctx and the first block's dx are complete
+        {
+            OnSide os(ctx, two);
+            lin_bwd(ctx, d, H_GCE2, d->gce_a, B, d->dgcond, d->da, 0);
+            launch(ctx, "dit_silu", silu_bwd_kernel, dim3(nblk(B * D)), (const float*)d->da, (const float*)d->gce_h,
+                   (int64_t)B * D, d->dh);
+            lin_bwd(ctx, d, H_GCE0, d->gsum, B, d->dh, d->dg, 0);
+            mlp_bwd(ctx, d, H_GLOBAL0, glob, B, d->ge_h, d->ge_a, d->dg, nullptr);
+            mlp_bwd(ctx, d, H_TIME0, d->tf, B, d->te_h, d->te_a, d->dg, nullptr);
+        }
+        {
+            SideHeld hold(ctx, two);
+            launch(ctx, "dit_head", gather_frames_kernel, dim3(nblk(NT * D)), (const float*)dcur, B, T, c.mem_tokens,
+                   (int)D, d->dxi);
+            lin_bwd(ctx, d, H_PROJ_IN, d->xp, NT, d->dxi, d->dxp, 0);
+            lin_bwd(ctx, d, H_PRE_CONV, x_t, NT, d->dxp, nullptr, 0);
+            mlp_bwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->dctx, nullptr);
+        }
+        if (two) side_join(ctx);   // AdamW reads every gradient
     }
 }
 

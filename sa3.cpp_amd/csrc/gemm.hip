@@ -466,9 +466,12 @@ void launch(sa3k_ctx* ctx, KParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.N, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
     const int KT = (int)(p.K / (BF16 ? 64 : 32));
-    // split K when the output tiles cannot fill the chip twice over (2 workgroups per CU resident)
+    // split K when the output tiles cannot fill the chip twice over (2 workgroups per CU resident);
+    // a product with a handful of output tiles (a few tokens against a long K: the DiT's conditioning
+    // linears) splits further, so its B operand streams through many workgroups
     int splits = 1;
-    if (ctx->gemm_split && tiles < 512 && KT >= 8) splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, 512 / tiles)});
+    const int64_t max_splits = tiles <= 32 ? 64 : 16;
+    if (ctx->gemm_split && tiles < 512 && KT >= 8) splits = (int)std::min<int64_t>({max_splits, KT / 4, std::max<int64_t>(1, 512 / tiles)});
     p.kps = (KT + splits - 1) / std::max(splits, 1);
     if (p.kps == 0) p.kps = 1;
     splits = std::max(1, (KT + p.kps - 1) / p.kps);
@@ -500,6 +503,7 @@ void launch(sa3k_ctx* ctx, KParams p) {
 template <int ASRC, int BSRC, bool BF16>
 void launch_tiles(sa3k_ctx* ctx, const KParams& p) {
     if (p.M + p.Mx <= 32) launch<32, 128, 1, ASRC, BSRC, BF16>(ctx, p);
+    else if (p.M + p.Mx <= 64 && p.N > 64) launch<64, 128, 2, ASRC, BSRC, BF16>(ctx, p);
     else if (p.N <= 32) launch<128, 32, 4, ASRC, BSRC, BF16>(ctx, p);
     else if (p.N <= 64) launch<128, 64, 4, ASRC, BSRC, BF16>(ctx, p);
     else launch<128, 128, 2, ASRC, BSRC, BF16>(ctx, p);

@@ -1176,7 +1176,8 @@ constexpr int kTermRows = 64;                 // DoRA rows per block (8 passes o
 
 struct PrepDesc {
     const float *A, *B, *mag, *bnsq;   // adapter (device) [r][in], [out][r], [out], [out]
-    bf16 *Ac, *At, *Bc, *Bt;           // compute-type copies [r][in], [in][r], [out][r], [r][out]
+    void *Ac, *At, *Bc, *Bt;           // compute-type copies [r][in], [in][r], [out][r], [r][out]
+                                       // (bf16, or f32 in a group of f32-precision linears)
     const bf16* W;                     // bf16 working copy of the base [out][in]
     float *Pt, *G, *BG, *nsq, *d;
     int in, out;
@@ -1193,10 +1194,15 @@ struct PrepDesc {
 // (all r rows) for its first ceil(in/64) blocks, then rows [64t, 64t + 64) of B (all r columns).
 // The copies in the source layout are written as read; the transposed copies go through LDS so
 // every store is a contiguous row (a direct transposed store touches one cache segment per value).
+template <class CT>
 __global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc* __restrict__ ds,
                                                                  const int* __restrict__ block_member, int r) {
     const PrepDesc& q = ds[block_member[blockIdx.x]];
-    __shared__ bf16 tile[64][34];   // [tile index][rank], padded
+    __shared__ CT tile[64][34];   // [tile index][rank], padded
+    CT* const Ac = static_cast<CT*>(q.Ac);
+    CT* const At = static_cast<CT*>(q.At);
+    CT* const Bc = static_cast<CT*>(q.Bc);
+    CT* const Bt = static_cast<CT*>(q.Bt);
     const int t = blockIdx.x - q.blk0[kStageConvert];
     const int a_tiles = (q.in + 63) / 64;
     const bool is_a = t < a_tiles;
@@ -1210,10 +1216,10 @@ __global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc*
         const int64_t idx = base + j;
         if (a >= r || idx >= extent) continue;
         const float v = is_a ? q.A[(int64_t)a * q.in + idx] : q.B[idx * r + a];
-        const bf16 b = (bf16)v;
+        const CT b = (CT)v;
         tile[j][a] = b;
-        if (is_a) q.Ac[(int64_t)a * q.in + idx] = b;
-        else q.Bc[idx * r + a] = b;
+        if (is_a) Ac[(int64_t)a * q.in + idx] = b;
+        else Bc[idx * r + a] = b;
     }
     __syncthreads();
     // transposed stores: At [in][r] (rows of r ranks), Bt [r][out] (rows of 64 indices)
@@ -1223,8 +1229,8 @@ __global__ __launch_bounds__(kThreads) void group_convert_kernel(const PrepDesc*
         else { a = e / 64; j = e % 64; }
         const int64_t idx = base + j;
         if (a >= r || idx >= extent) continue;
-        if (is_a) q.At[idx * r + a] = tile[j][a];
-        else q.Bt[(int64_t)a * q.out + idx] = tile[j][a];
+        if (is_a) At[idx * r + a] = tile[j][a];
+        else Bt[(int64_t)a * q.out + idx] = tile[j][a];
     }
 }
 
@@ -1359,6 +1365,83 @@ __global__ __launch_bounds__(kThreads) void group_gram_sum_kernel(const PrepDesc
         for (int c = 0; c < chunks; ++c) sum += part[(int64_t)(q.blk0[kStageGram] + c) * 1024 + e];
         q.G[a * r + b] = (float)sum;
     }
+}
+
+// P^T[a][o] = sum_i A[a][i] W[o][i] in f32 for the members of an f32-precision group (the DiT's
+// head / tail linears), from the stored base (f32 or f16, decoded exactly to f32): one block per
+// kPtRowsF32 = 64 rows o of one member, the K loop in 64-wide chunks staged in LDS (W rows as f32,
+// A's r x 64 slice); wave w owns ranks 8w..8w+7 of all 64 rows, lane l row l, so the A reads are
+// wave-uniform broadcasts and the W reads fall into distinct banks (row pitch 65). Each sum runs
+// over i in order: deterministic. The input dimension is a multiple of 64 (checked on the host).
+constexpr int kPtRowsF32 = 64;
+template <int WT>
+__global__ __launch_bounds__(kThreads) void group_pt_f32_kernel(const PrepDesc* __restrict__ ds,
+                                                                const int* __restrict__ block_member, int r) {
+    const PrepDesc& q = ds[block_member[blockIdx.x]];
+    if (q.wtype != WT) return;   // another launch serves this member's element type
+    __shared__ float ws[kPtRowsF32][65];
+    __shared__ float as[32][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t o0 = (int64_t)(blockIdx.x - q.blk0[kStagePt]) * kPtRowsF32;
+    const int in = q.in;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int k0 = 0; k0 < in; k0 += 64) {
+        // W rows o0 .. o0 + 63, columns k0 .. k0 + 63: 16 columns per thread (rows past out: zeros)
+        {
+            const int row = tid >> 2, c0 = (tid & 3) * 16;
+            const int64_t o = o0 + row;
+            float v[16];
+            if (o < q.out) {
+                if (WT == SA3K_TYPE_F32) {
+                    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(q.Wsrc) + o * in + k0 + c0);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float4 f = src[u];
+                        v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
+                    }
+                } else {
+                    const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(q.Wsrc) + o * in + k0 + c0);
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint4 h = src[u];
+                        const uint32_t w4[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            v[8 * u + 2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[e] & 0xffffu));
+                            v[8 * u + 2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[e] >> 16));
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) ws[row][c0 + e] = v[e];
+        }
+        // A[:, k0 .. k0 + 63]: 8 columns per thread (ranks past r: zeros)
+        {
+            const int a = tid >> 3, c0 = (tid & 7) * 8;
+            const float* A = static_cast<const float*>(q.A);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) as[a][c0 + e] = a < r ? A[(int64_t)a * in + k0 + c0 + e] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < 64; ++k) {
+            const float w = ws[lane][k];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += w * as[8 * wave + j][k];
+        }
+        __syncthreads();
+    }
+    const int64_t o = o0 + lane;
+    if (o >= q.out) return;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (8 * wave + j < r) q.Pt[(int64_t)(8 * wave + j) * q.out + o] = acc[j];
 }
 
 // nsq, d and BG = B G for kTermRows rows of one member per block (G staged in LDS once per block)
@@ -1505,7 +1588,7 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
     // delta's A operand: the rank entries 8g.. of B row o (this wave's 16 rows), loop-invariant
     const int64_t ob = min(o0 + 16 * wave + l16, out - 1);
     const bf16x8 zero8 = {};
-    const bf16x8 bop = 8 * g < r ? __builtin_bit_cast(bf16x8, ldg16(q.Bc + ob * r + (8 * g < r ? 8 * g : 0))) : zero8;
+    const bf16x8 bop = 8 * g < r ? __builtin_bit_cast(bf16x8, ldg16(static_cast<const bf16*>(q.Bc) + ob * r + (8 * g < r ? 8 * g : 0))) : zero8;
     double nacc[4] = {0.0, 0.0, 0.0, 0.0};   // rows 16 wave + 4g + v, this lane's columns
     f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
     const uint32_t wbytes = (uint32_t)(out * in * 2);   // < 2^31 (checked when the group is built)
@@ -1643,6 +1726,7 @@ struct LinGroup {
     int* block_member[kStages] = {};   // per stage: the member of every block
     int blocks[kStages] = {};
     int n = 0, r = 0, dora = 0, merged = 0;
+    int f32 = 0;   // members compute in f32: f32 copies, P on the VALU from the stored base
     float s = 1.0f;
 };
 
@@ -1663,21 +1747,28 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
         g->r = lins[0]->rank;
         g->dora = dora ? 1 : 0;
         g->s = scale;
-        g->merged = ctx->lin_merge ? 1 : 0;
+        // f32-precision members: the two-segment refresh with f32 copies and an f32 P
+        g->f32 = lins[0]->prec == SA3K_PREC_F32 ? 1 : 0;
+        g->merged = ctx->lin_merge && !g->f32 ? 1 : 0;
         std::vector<PrepDesc> h(n);
         std::vector<int> bm[kStages];
         for (int i = 0; i < n; ++i) {
             sa3k_lin* L = lins[i];
-            SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && (g->merged || L->W->wb) && L->rank == g->r && g->r > 0,
-                         "a linear group needs bf16 linears of one rank (with bf16 working copies unless merged)");
+            SA3K_REQUIRE(L->prec == lins[0]->prec && L->rank == g->r && g->r > 0,
+                         "a linear group needs linears of one precision and rank");
+            if (g->f32)
+                SA3K_REQUIRE((L->W->type == SA3K_TYPE_F32 || L->W->type == SA3K_TYPE_F16) && L->W->in % 64 == 0,
+                             "an f32 linear group needs f32 / f16 bases with inputs a multiple of 64");
+            else
+                SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && (g->merged || L->W->wb),
+                             "a bf16 linear group needs bf16 working copies unless merged");
             SA3K_REQUIRE(A[i] && B[i] && (!dora || (mag[i] && bnsq[i])), "missing adapter pointer");
             const int64_t in = L->W->in, out = L->W->out;
             SA3K_REQUIRE(out % 64 == 0 || out % 16 == 0, "group output dimension must be a multiple of 16");
             SA3K_REQUIRE((int64_t)out * in * 2 < ((int64_t)1 << 31), "group member weight above 2 GiB");
             PrepDesc& q = h[i];
             q.A = A[i]; q.B = B[i]; q.mag = dora ? mag[i] : nullptr; q.bnsq = dora ? bnsq[i] : nullptr;
-            q.Ac = static_cast<bf16*>(L->Ac); q.At = static_cast<bf16*>(L->At);
-            q.Bc = static_cast<bf16*>(L->Bc); q.Bt = static_cast<bf16*>(L->Bt);
+            q.Ac = L->Ac; q.At = L->At; q.Bc = L->Bc; q.Bt = L->Bt;
             q.W = static_cast<const bf16*>(L->W->wb);
             q.Pt = L->Pt; q.G = L->G; q.BG = L->BG; q.nsq = L->nsq; q.d = L->d;
             q.in = (int)in; q.out = (int)out;
@@ -1695,7 +1786,8 @@ LinGroup* lin_group_create(sa3k_ctx* ctx, sa3k_lin* const* lins, int n, const fl
                 q.Wm = static_cast<bf16*>(L->Wm);
                 q.Wmt = static_cast<bf16*>(L->Wmt);
             }
-            const int64_t per_stage[kStages] = {ceil_div(in, 64) + ceil_div(out, 64), ceil_div(out, kPtRows),
+            const int64_t per_stage[kStages] = {ceil_div(in, 64) + ceil_div(out, 64),
+                                                ceil_div(out, g->f32 ? kPtRowsF32 : kPtRows),
                                                 ceil_div(in, kGramCols), ceil_div(out, kTermRows),
                                                 ceil_div(out, kMergeRows)};
             for (int st = 0; st < kStages; ++st) {
@@ -1746,8 +1838,9 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
     }
     {
         KernelScope ks(ctx, "group_convert");
-        group_convert_kernel<<<(unsigned)g->blocks[kStageConvert], kThreads, 0, ctx->stream>>>(
-            g->dev, g->block_member[kStageConvert], g->r);
+        auto* kern = g->f32 ? group_convert_kernel<float> : group_convert_kernel<bf16>;
+        kern<<<(unsigned)g->blocks[kStageConvert], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStageConvert],
+                                                                            g->r);
         SA3K_LAUNCHED();
     }
     if (g->merged) {
@@ -1773,9 +1866,25 @@ void lin_group_prepare(sa3k_ctx* ctx, LinGroup* g) {
         double flops = 0.0;
         for (sa3k_lin* L : g->lins) flops += 2.0 * g->r * (double)L->W->in * (double)L->W->out;
         KernelScope ks(ctx, "group_pt", flops);
-        auto* kern = g->r > 16 ? group_pt_kernel<true> : group_pt_kernel<false>;
-        kern<<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStagePt], g->r);
-        SA3K_LAUNCHED();
+        if (g->f32) {
+            // one launch per stored element type present (blocks of other members exit at once)
+            bool has32 = false, has16 = false;
+            for (sa3k_lin* L : g->lins) (L->W->type == SA3K_TYPE_F32 ? has32 : has16) = true;
+            if (has32) {
+                group_pt_f32_kernel<SA3K_TYPE_F32><<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(
+                    g->dev, g->block_member[kStagePt], g->r);
+                SA3K_LAUNCHED();
+            }
+            if (has16) {
+                group_pt_f32_kernel<SA3K_TYPE_F16><<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(
+                    g->dev, g->block_member[kStagePt], g->r);
+                SA3K_LAUNCHED();
+            }
+        } else {
+            auto* kern = g->r > 16 ? group_pt_kernel<true> : group_pt_kernel<false>;
+            kern<<<(unsigned)g->blocks[kStagePt], kThreads, 0, ctx->stream>>>(g->dev, g->block_member[kStagePt], g->r);
+            SA3K_LAUNCHED();
+        }
     }
     {
         KernelScope ks(ctx, "group_gram");

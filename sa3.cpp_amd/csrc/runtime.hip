@@ -3,8 +3,10 @@
 #include "gemm.h"
 
 #include <algorithm>
+#include <cctype>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 
 namespace {
 constexpr int kAdamwMaxBlocks = 2048;
@@ -44,6 +46,45 @@ void prof_collect(sa3k_ctx* ctx) {
     ctx->prof_pending.clear();
 }
 
+namespace {
+// Every tunable of a context, by name: sa3k_set_option / sa3k_get_option / sa3k_option_name.
+struct OptionDef {
+    const char* name;
+    int sa3k_ctx::*field;
+    bool flag;   // stored as 0 / 1
+};
+const OptionDef kOptions[] = {
+    {"gemm_split", &sa3k_ctx::gemm_split, true},   {"gemm_fixup", &sa3k_ctx::gemm_fixup, false},
+    {"gemm_dma", &sa3k_ctx::gemm_dma, true},       {"gemm_dq", &sa3k_ctx::gemm_dq, false},
+    {"gemm_cfg", &sa3k_ctx::gemm_cfg, false},      {"gemm_small", &sa3k_ctx::gemm_small, false},
+    {"gemm_nt_store", &sa3k_ctx::gemm_nt_store, true}, {"gemm_skinny", &sa3k_ctx::gemm_skinny, true},
+    {"gemm_big", &sa3k_ctx::gemm_big, false},      {"gemm_splits", &sa3k_ctx::gemm_splits, false},
+    {"side_stream", &sa3k_ctx::use_side, true},    {"fork_tail", &sa3k_ctx::fork_tail, true},
+    {"late_join", &sa3k_ctx::late_join, true},     {"lin_merge", &sa3k_ctx::lin_merge, true},
+    {"rank_cols", &sa3k_ctx::rank_cols, false},    {"merge_kn", &sa3k_ctx::merge_kn, true},
+    {"tn_fuse", &sa3k_ctx::tn_fuse, false},        {"kv_stack", &sa3k_ctx::kv_stack, true},
+    {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
+};
+constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
+
+// SA3K_<NAME> in the environment overrides option <name> at context creation (A/B measurements)
+void options_from_env(sa3k_ctx* ctx) {
+    for (const OptionDef& o : kOptions) {
+        std::string env = "SA3K_";
+        for (const char* p = o.name; *p; ++p) env += (char)std::toupper((unsigned char)*p);
+        if (const char* e = std::getenv(env.c_str())) ctx->*o.field = o.flag ? (std::atoi(e) != 0) : std::atoi(e);
+    }
+}
+
+const OptionDef& find_option(const char* name) {
+    SA3K_REQUIRE(name != nullptr, "null option name");
+    for (const OptionDef& o : kOptions)
+        if (std::strcmp(o.name, name) == 0) return o;
+    sa3k_throw(SA3K_ERR_INVALID, std::string("unknown option ") + name);
+    return kOptions[0];   // not reached
+}
+}  // namespace
+
 extern "C" {
 
 SA3K_API const char* sa3k_version(void) { return "sa3k 0.1 gfx950"; }
@@ -72,27 +113,10 @@ SA3K_API sa3k_ctx* sa3k_create(int device, char* err, int err_len) {
         SA3K_HIP(hipStreamCreateWithFlags(&ctx->quick_stream, hipStreamNonBlocking));
         for (hipEvent_t& e : ctx->side_ev) SA3K_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         SA3K_HIP(hipEventCreateWithFlags(&ctx->block_tail_ev, hipEventDisableTiming));
-        if (const char* e = std::getenv("SA3K_SIDE_STREAM")) ctx->use_side = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_FORK_TAIL")) ctx->fork_tail = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_LATE_JOIN")) ctx->late_join = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_LIN_MERGE")) ctx->lin_merge = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_RANK_COLS")) ctx->rank_cols = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_MERGE_KN")) ctx->merge_kn = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_TN_FUSE")) ctx->tn_fuse = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_KV_STACK")) ctx->kv_stack = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_ATTN_FWD32")) ctx->attn_fwd32 = std::atoi(e);
+        options_from_env(ctx);
         SA3K_HIP(hipEventCreate(&ctx->ev_start));
         SA3K_HIP(hipEventCreate(&ctx->ev_stop));
         if (const char* e = std::getenv("SA3K_GEMM_PD")) ctx->gemm_pd = std::atoi(e) == 2 ? 2 : 1;
-        if (const char* e = std::getenv("SA3K_GEMM_SPLIT")) ctx->gemm_split = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_GEMM_FIXUP")) ctx->gemm_fixup = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_GEMM_DMA")) ctx->gemm_dma = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_GEMM_DQ")) ctx->gemm_dq = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_GEMM_CFG")) ctx->gemm_cfg = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_GEMM_SMALL")) ctx->gemm_small = std::atoi(e);
-        if (const char* e = std::getenv("SA3K_GEMM_NT")) ctx->gemm_nt_store = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_GEMM_SKINNY")) ctx->gemm_skinny = std::atoi(e) != 0;
-        if (const char* e = std::getenv("SA3K_GEMM_BIG")) ctx->gemm_big = std::atoi(e);
         if (const char* e = std::getenv("SA3K_GEMM_WGPCU")) ctx->gemm_wg_per_cu = std::max(1, std::atoi(e));
         SA3K_HIP(hipMalloc(&ctx->zero_page, 256));
         SA3K_HIP(hipMemsetAsync(ctx->zero_page, 0, 256, ctx->stream));
@@ -223,39 +247,6 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx) {
     });
 }
 
-}  // extern "C"
-
-namespace {
-// Every tunable of a context, by name: sa3k_set_option / sa3k_get_option / sa3k_option_name.
-struct OptionDef {
-    const char* name;
-    int sa3k_ctx::*field;
-    bool flag;   // stored as 0 / 1
-};
-const OptionDef kOptions[] = {
-    {"gemm_split", &sa3k_ctx::gemm_split, true},   {"gemm_fixup", &sa3k_ctx::gemm_fixup, false},
-    {"gemm_dma", &sa3k_ctx::gemm_dma, true},       {"gemm_dq", &sa3k_ctx::gemm_dq, false},
-    {"gemm_cfg", &sa3k_ctx::gemm_cfg, false},      {"gemm_small", &sa3k_ctx::gemm_small, false},
-    {"gemm_nt_store", &sa3k_ctx::gemm_nt_store, true}, {"gemm_skinny", &sa3k_ctx::gemm_skinny, true},
-    {"gemm_big", &sa3k_ctx::gemm_big, false},      {"gemm_splits", &sa3k_ctx::gemm_splits, false},
-    {"side_stream", &sa3k_ctx::use_side, true},    {"fork_tail", &sa3k_ctx::fork_tail, true},
-    {"late_join", &sa3k_ctx::late_join, true},     {"lin_merge", &sa3k_ctx::lin_merge, true},
-    {"rank_cols", &sa3k_ctx::rank_cols, false},    {"merge_kn", &sa3k_ctx::merge_kn, true},
-    {"tn_fuse", &sa3k_ctx::tn_fuse, false},        {"kv_stack", &sa3k_ctx::kv_stack, true},
-    {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
-};
-constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
-
-const OptionDef& find_option(const char* name) {
-    SA3K_REQUIRE(name != nullptr, "null option name");
-    for (const OptionDef& o : kOptions)
-        if (std::strcmp(o.name, name) == 0) return o;
-    sa3k_throw(SA3K_ERR_INVALID, std::string("unknown option ") + name);
-    return kOptions[0];   // not reached
-}
-}  // namespace
-
-extern "C" {
 
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value) {
     return sa3k_guard(ctx, "sa3k_set_option", [&] {

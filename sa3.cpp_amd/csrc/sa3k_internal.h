@@ -48,6 +48,7 @@ struct sa3k_ctx {
     hipEvent_t side_ev[kSideEvents] = {};   // fork/join events, reused round-robin
     int side_ev_i = 0;
     int use_side = 1;                      // run independent chains on the second stream
+    int side_held = 0;                     // > 0: the second stream is taken by a caller's own chain
     int side_defer = 0;                    // >0: a caller joins the second stream (callees need not)
     int fork_tail = 1;                     // forks recorded by the producer kernel's completion (fork_arm)
     int late_join = 1;                     // a DiT block's last second-stream work may overlap the next block
@@ -197,7 +198,7 @@ inline void sa3k_note_main(sa3k_ctx* c) {
 // (per-kernel timing stays serial). Every function that forks joins before it returns, so no side
 // work outlives a call.
 inline bool side_usable(const sa3k_ctx* c) {
-    return c->use_side && c->side_stream && !c->prof_on && c->stream == c->main_stream;
+    return c->use_side && !c->side_held && c->side_stream && !c->prof_on && c->stream == c->main_stream;
 }
 inline hipEvent_t side_event(sa3k_ctx* c) {
     hipEvent_t e = c->side_ev[c->side_ev_i];
@@ -305,6 +306,20 @@ struct OnQuick {
     }
     OnQuick(const OnQuick&) = delete;
     OnQuick& operator=(const OnQuick&) = delete;
+};
+// while held, functions on the main stream fork nothing (a caller runs its own chain on the second
+// stream beside them)
+struct SideHeld {
+    sa3k_ctx* c;
+    bool on;
+    SideHeld(sa3k_ctx* ctx, bool enable) : c(ctx), on(enable) {
+        if (on) ++c->side_held;
+    }
+    ~SideHeld() {
+        if (on) --c->side_held;
+    }
+    SideHeld(const SideHeld&) = delete;
+    SideHeld& operator=(const SideHeld&) = delete;
 };
 // launches inside the scope go to the second stream (when `on`)
 struct OnSide {
