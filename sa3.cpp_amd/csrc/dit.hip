@@ -681,7 +681,7 @@ void prepare(sa3k_ctx* ctx, sa3k_dit* d) {
     // linears' refresh is a few short launches. With both, the bf16 group goes to the second stream
     // and the heads' refresh and forwards run beside it on the main stream; forward() joins before
     // the first product that reads a member of the bf16 group.
-    const bool side = d->hgroup && side_usable(ctx);
+    const bool side = d->hgroup && ctx->prep_side && side_usable(ctx);
     if (side) side_fork(ctx);
     {
         OnSide os(ctx, side);

@@ -98,6 +98,7 @@ struct sa3k_ctx {
     int tn_fuse = kFuseColred | kFuseRows; // split reductions summed in-kernel (bits kFuse*)
     int kv_stack = 1;                     // a DiT's context K/V projections as one stacked product
     int attn_fwd32 = 1;                   // attention forward on 32x32x16 MFMA blocks, 32 queries per wave
+    int prep_side = 1;                    // a DiT's bf16 group refresh on the second stream beside the f32 heads'
     int head_f32 = 1;                     // a DiT's head / tail linears on f32 MFMA (f32 / f16 bases)
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
                                           // one half per stream, zero between launches
