@@ -438,13 +438,14 @@ class DitWorkload:
     adapted: 228 targets) with a bound [B][T][local_dim] conditioning ~ N(0,1)."""
     dtype = "bf16"
 
-    def __init__(self, ctx, recompute=False, B=2, T=1024, Ctx=128, depth=24, window=256, r=32, local_dim=0):
+    def __init__(self, ctx, recompute=False, B=2, T=1024, Ctx=128, depth=24, window=256, r=32, local_dim=0, micro=1):
         sa3k = sys.modules["sa3k"]
         self.ctx, self.B, self.T, self.Ctx, self.depth, self.window, self.r = ctx, B, T, Ctx, depth, window, r
+        self.micro = micro   # accumulate calls (micro-batches of B samples) per optimizer update
         self.dim, self.heads, self.inner, self.io, self.cond_dim, self.time_dim, self.mem = 1536, 24, 6144, 64, 768, 256, 64
         self.recompute, self.local_dim = recompute, local_dim
         self.name = f"dit_update_{depth}x1536_b{B}_t{T}_w{window}_dora_r{r}" + ("_recompute" if recompute else "") + \
-            (f"_inpaint_local{local_dim}" if local_dim else "")
+            (f"_inpaint_local{local_dim}" if local_dim else "") + (f"_x{micro}" if micro > 1 else "")
         cfg = sa3k.dit_config(self.io, self.dim, depth, self.heads, self.cond_dim, self.mem, self.time_dim,
                               self.inner, window, local_dim=local_dim)
         self.d = sa3k.Dit(ctx, cfg, sa3k.TYPE_F16)
@@ -469,7 +470,8 @@ class DitWorkload:
     def step(self):
         self.k += 1
         v = self.dev
-        self.d.accumulate(v["x"], v["tg"], v["t"], v["cr"], v["gl"], want_loss=False)
+        for _ in range(self.micro):
+            self.d.accumulate(v["x"], v["tg"], v["t"], v["cr"], v["gl"], want_loss=False)
         self.d.apply_adamw(self.hp, self.k)
 
     def flops(self):
@@ -480,7 +482,7 @@ class DitWorkload:
             n = self.B * self.T
             hf += self.depth * 2 * n * self.dim * (self.local_dim + self.dim)
             hb += self.depth * 2 * n * self.dim * self.dim
-        return self.depth * f + hf, self.depth * b + hb
+        return self.micro * (self.depth * f + hf), self.micro * (self.depth * b + hb)
 
     def config(self):
         return {"workload": self.name, "blocks": self.depth, "batch": self.B, "frames": self.T,
@@ -489,7 +491,8 @@ class DitWorkload:
                 "adapter": "dora-rows", "base": "f16",
                 "scope": f"full ({(9 if self.local_dim else 7) * self.depth + 12} targets)",
                 **({"local_dim": self.local_dim} if self.local_dim else {}),
-                "adapter_params": self.n, "schedule": "checkpointed recompute" if self.recompute else "resident"}
+                "adapter_params": self.n, "schedule": "checkpointed recompute" if self.recompute else "resident",
+                **({"micro_batches_per_update": self.micro} if self.micro > 1 else {})}
 
     def roofline(self, prof, steps):
         return gemm_roofline(prof, steps)
@@ -530,13 +533,86 @@ class DitWorkload:
         with sys.modules["oracle"].f32_mode():
             t_b, tb = _median_time(lambda: bb.block_bwd(cfg, w, x, ctx, gc, dout), runs=3)
             t_h, th = _median_time(lambda: db.dit_loss(hcfg, tensors, adapters, inputs), runs=3)
-        value = t_h + self.depth * t_b
-        return {"value": round(value * 1e3, 1), "unit": "ms/update (forward + backward, no AdamW)",
+        # the clip + AdamW of the reference's loop (the oracle's literal transcription, one core) over
+        # an 8M-parameter slice of the arena, scaled to its size
+        oracle = sys.modules["sa3_oracle"] if "sa3_oracle" in sys.modules else \
+            _load("sa3_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        ns = 8_000_000
+        pa, ga = g.normal(0, 0.05, ns).astype(np.float32), g.normal(0, 1e-3, ns).astype(np.float32)
+        z = np.zeros(ns, np.float32)
+        t_a, ta = _median_time(lambda: oracle.apply_accumulated_adamw(pa, ga, z, z, *self.hp, 1, 1), runs=3)
+        t_adamw = t_a / ns * self.n
+        value = t_h + self.depth * t_b + t_adamw
+        return {"value": round(value * 1e3, 1), "unit": "ms/update (forward + backward + clip/AdamW)",
                 "cores": bb.lib().orc_num_threads(), "kind": "port",
                 "sample": f"the oracle in its f32 mode (float accumulation, AVX2/FMA products, OpenMP): one "
                           f"full-size block fwd+bwd (B {self.B}, S {S}), median of {len(tb)} after a warm-up "
                           f"= {t_b:.2f} s ({', '.join(f'{v:.2f}' for v in tb)}); head + tail (depth-0 DiT "
-                          f"loss+grad, T {self.T}) median {t_h:.2f} s; update = head/tail + {self.depth} x block"}
+                          f"loss+grad, T {self.T}) median {t_h:.2f} s; clip + AdamW (one core) over an "
+                          f"{ns}-param slice, median {t_a:.3f} s, scaled to the {self.n}-param arena "
+                          f"= {t_adamw:.3f} s; update = head/tail + {self.depth} x block + AdamW"}
+
+
+class MirrorWorkload:
+    """The reference trainer's default update (tools/sa3-train.cpp:574-714) through the C++ host
+    mirror of its interface (sa3.cpp_amd/host/sa3/*.h, driven by host/mirror_bench.cpp in
+    libsa3mirror.so): the same 24-block model and full-scope dora-rows r32 adapters as `dit`
+    (adapters from init_train_lora_state), build_train_dit_ckpt (which keeps every block's
+    activations when they fit), then per update two samples of 1024 frames, one per
+    run_train_dit_accumulate_ckpt call as the reference runs them, and train_apply_accumulated_adamw.
+    device_resident: the adapters, the gradient window and the moments stay on the device (this
+    build's mode); otherwise the reference's per-sample upload / gradient read-back and the host
+    AdamW vectors (round trips through PCIe). Timed by the wall clock: every call synchronises."""
+    dtype = "bf16"
+    wall_timed = True
+
+    def __init__(self, ctx, device_resident=True, micro=2, frames=1024):
+        import ctypes as C
+        self.C = C
+        self.lib = C.CDLL(os.path.join(ROOT, "sa3.cpp_amd", "libsa3mirror.so"))
+        self.lib.sa3m_create.restype = C.c_void_p
+        self.lib.sa3m_create.argtypes = [C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int]
+        self.lib.sa3m_update.argtypes = [C.c_void_p, C.c_char_p, C.c_int]
+        self.lib.sa3m_info.argtypes = [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_longlong),
+                                       C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        self.lib.sa3m_destroy.argtypes = [C.c_void_p]
+        self.err = C.create_string_buffer(1024)
+        self.h = self.lib.sa3m_create(int(device_resident), micro, frames, self.err, 1024)
+        if not self.h:
+            raise RuntimeError("mirror setup: " + self.err.value.decode())
+        self.device_resident, self.micro, self.frames = device_resident, micro, frames
+        self.name = f"dit_update_mirror_24x1536_{micro}x1_t{frames}_w256_dora_r32" + \
+            ("" if device_resident else "_roundtrip")
+
+    def step(self):
+        if self.lib.sa3m_update(self.h, self.err, 1024) != 0:
+            raise RuntimeError("mirror update: " + self.err.value.decode())
+
+    def info(self):
+        C = self.C
+        rc, n, loss, norm = C.c_int(), C.c_longlong(), C.c_double(), C.c_double()
+        self.lib.sa3m_info(self.h, C.byref(rc), C.byref(n), C.byref(loss), C.byref(norm))
+        return rc.value, n.value, loss.value, norm.value
+
+    def config(self):
+        rc, n, _, _ = self.info()
+        return {"workload": self.name, "blocks": 24, "samples_per_update": self.micro, "batch_per_call": 1,
+                "frames": self.frames, "memory_tokens": 64, "context_tokens": 128, "io": 64, "dim": 1536,
+                "heads": 24, "ffn_inner": 6144, "window": 256, "rank": 32, "adapter": "dora-rows", "base": "f16",
+                "scope": "full (180 targets)", "adapter_params": n,
+                "path": "host mirror (train_loop.h) " + ("device-resident" if self.device_resident else
+                                                         "per-sample round trips"),
+                "schedule": "checkpointed recompute" if rc else "resident"}
+
+    def roofline(self, prof, steps):
+        return None
+
+    def extra(self, ms_per_step):
+        _, _, loss, norm = self.info()
+        return {"last_mean_loss": round(loss, 6), "last_grad_norm": round(norm, 6)}
+
+    def cpu_baseline(self):
+        return None
 
 
 def measured_traffic(kernel):
@@ -576,9 +652,31 @@ WORKLOADS = {"adamw": AdamWWorkload,
              "dit": DitWorkload,
              "dit_recompute": lambda ctx: DitWorkload(ctx, recompute=True),
              "dit_inpaint": lambda ctx: DitWorkload(ctx, local_dim=257),
+             "dit_inpaint_recompute": lambda ctx: DitWorkload(ctx, recompute=True, local_dim=257),
+             "dit_b1x2": lambda ctx: DitWorkload(ctx, B=1, micro=2),
+             "dit_mirror": lambda ctx: MirrorWorkload(ctx, device_resident=True),
+             "dit_mirror_roundtrip": lambda ctx: MirrorWorkload(ctx, device_resident=False),
              "chain_q8": lambda ctx: ChainWorkload(ctx, "q8"),
              "chain_q8_copy": lambda ctx: ChainWorkload(ctx, "q8_copy")}
 DEFAULT = "dit"
+WALL_TIMED = {"dit_mirror", "dit_mirror_roundtrip"}
+
+
+class _WallClock:
+    """Stands in for the library context in main() for a workload that runs on a context of its own
+    (timed by the wall clock)."""
+
+    def sync(self):
+        pass
+
+    def timer_start(self):
+        pass
+
+    def timer_stop(self):
+        return 0.0
+
+    def close(self):
+        pass
 
 
 def main():
@@ -598,7 +696,9 @@ def main():
         sys.exit(2)
 
     sa3k = _load("sa3k", os.path.join(ROOT, "sa3.cpp_amd", "sa3k.py"))
-    ctx = sa3k.Context(0)
+    # the mirror workloads run on the host mirror's own context; a second context here would share
+    # the process's hardware queues with its streams
+    ctx = _WallClock() if a.workload in WALL_TIMED else sa3k.Context(0)
     if a.copy_bytes > 0:
         src, dst = ctx.empty(a.copy_bytes // 4, np.float32), ctx.empty(a.copy_bytes // 4, np.float32)
         for _ in range(5):
@@ -626,18 +726,22 @@ def main():
     ms_total = ctx.timer_stop()
     wall = time.perf_counter() - t0
     ms_per_step = ms_total / a.steps
+    if getattr(wl, "wall_timed", False):   # work on another context's streams: the wall clock
+        ms_per_step = wall * 1e3 / a.steps
     log(f"{ms_per_step:.4f} ms/step (wall {wall * 1e3 / a.steps:.4f} ms/step)")
-    # profiled pass: the same K steps again with a HIP event pair around every kernel launch on the
-    # library's stream (launched eagerly), for the per-kernel averages and the roofline
-    ctx.profile(True)
-    ctx.profile_reset()
-    ctx.timer_start()
-    for _ in range(a.steps):
-        wl.step()
-    ms_prof = ctx.timer_stop() / a.steps
-    prof = ctx.profile_report(with_work=True)
-    ctx.profile(False)
-    log(f"profiled pass {ms_prof:.4f} ms/step; kernels: {prof}")
+    prof, ms_prof = {}, None
+    if not getattr(wl, "wall_timed", False):
+        # profiled pass: the same K steps again with a HIP event pair around every kernel launch on
+        # the library's stream (launched eagerly), for the per-kernel averages and the roofline
+        ctx.profile(True)
+        ctx.profile_reset()
+        ctx.timer_start()
+        for _ in range(a.steps):
+            wl.step()
+        ms_prof = ctx.timer_stop() / a.steps
+        prof = ctx.profile_report(with_work=True)
+        ctx.profile(False)
+        log(f"profiled pass {ms_prof:.4f} ms/step; kernels: {prof}")
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -650,7 +754,7 @@ def main():
         "data": "synthetic (seeded Philox normals; random-init weights)", "config": wl.config(),
         "roofline": wl.roofline(prof, a.steps), "cpu_baseline": cpu,
         "kernels_ms": {k: round(v[1] / max(v[0], 1), 5) for k, v in prof.items()},
-        "profiled_pass_ms_per_step": round(ms_prof, 5),
+        "profiled_pass_ms_per_step": round(ms_prof, 5) if ms_prof is not None else None,
     }
     out.update(wl.extra(ms_per_step))
     print(json.dumps(out), flush=True)

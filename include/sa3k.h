@@ -80,6 +80,12 @@ SA3K_API int sa3k_download(sa3k_ctx* ctx, void* dst_host, const void* src_dev, s
 SA3K_API int sa3k_copy_d2d(sa3k_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes);
 SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst_dev, int value, size_t bytes);
 SA3K_API int sa3k_sync(sa3k_ctx* ctx);
+/* Free and total device memory of the context's GPU (hipMemGetInfo). No reference counterpart:
+ * the host mirror's build_train_dit_ckpt uses it to choose the schedule that fits. */
+SA3K_API int sa3k_device_memory(sa3k_ctx* ctx, size_t* free_bytes, size_t* total_bytes);
+/* dst[i] += src[i] in f32 for n device floats (16-byte aligned): train_accum_add
+ * (src/train_loop.h:75-78) on the device, the host mirror's device-resident gradient accumulator. */
+SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, int64_t n);
 
 /* Implementation knobs of a context (no reference counterpart; for tests and measurement):
  *   "gemm_split"  1: split K when a GEMM's output tiles cannot fill the chip (default 1)
@@ -101,8 +107,9 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 products s X A^T and s dU B) run on a kernel that splits K across the waves of
  *                 one workgroup instead of over workgroups (default 1)
  *   "gemm_big"    bf16 products on 256 x 256 tiles (8 waves, one workgroup per CU): 0 never,
- *                 1 where they fill the chip about as evenly as 128 x 128 tiles (default), 2 always
- *                 (when operand extents and output alignment allow)
+ *                 1 where they fill the chip about as evenly as 128 x 256 tiles, 2 always (when
+ *                 operand extents and output alignment allow), 3 as 1 plus every product with
+ *                 K >= 8192, split over K (default 3)
  *   "gemm_splits" > 0: the split-K count of DMA-fed GEMMs that split, in place of the one chosen
  *                 from the grid (clamped to the number of K tiles; default 0: chosen)
  *   "side_stream" 1: independent kernels of a backward pass (column reductions, attention dQ, the
@@ -145,9 +152,12 @@ SA3K_API int sa3k_sync(sa3k_ctx* ctx);
  *                 gce and cond embeddings, proj_out, post_conv) compute on f32 MFMA when the base
  *                 is f32 or f16, each refreshed by its own two-segment prepare; 0: bf16 like the
  *                 blocks (default 1). It holds from a DiT's setup.
+ *   "prep_side"   1: with f32 head linears, a DiT's bf16 group refresh runs on the second stream
+ *                 beside the heads' refresh and forward on the main one (default 1)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
- * kv_stack, attn_fwd32 and head_f32, which change the rounding or the f32 summation order. Not to
+ * kv_stack, attn_fwd32 and head_f32, which change the rounding or the f32 summation order
+ * (prep_side changes only the stream a refresh runs on). Not to
  * be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 
@@ -501,6 +511,12 @@ SA3K_API int sa3k_dit_setup(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_dit_train* 
  * end to end (the order train_apply_accumulated_adamw visits them, src/train_loop.h:181-207).
  * which: 0 parameters, 1 accumulated gradients, 2 AdamW first moments, 3 second moments. */
 SA3K_API int sa3k_dit_arena(sa3k_ctx* ctx, sa3k_dit* dit, int which, float** ptr, int64_t* n);
+/* The device memory the resident schedule (recompute = 0) takes beyond the checkpointed one
+ * (recompute = 1) for this model and micro-batch shape: depth - 1 more block workspaces. Valid
+ * before sa3k_dit_setup. No reference counterpart: build_train_dit_ckpt (src/train_ckpt.h:143-474)
+ * of the host mirror picks the resident schedule when it fits (both give the same results bit for
+ * bit). */
+SA3K_API int sa3k_dit_resident_bytes(sa3k_ctx* ctx, const sa3k_dit* dit, const sa3k_dit_train* train, size_t* bytes);
 SA3K_API int sa3k_dit_target_count(sa3k_ctx* ctx, const sa3k_dit* dit, int* count);
 SA3K_API int sa3k_dit_target_info(sa3k_ctx* ctx, const sa3k_dit* dit, int i, char* name, int name_len,
                                   int64_t* in, int64_t* out, int64_t* off_a, int64_t* off_b, int64_t* off_m);

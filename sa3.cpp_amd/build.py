@@ -3,7 +3,8 @@
 Usage: python sa3.cpp_amd/build.py [-j N]
 Each .hip file is compiled to an object under sa3.cpp_amd/_build/ and linked into
 sa3.cpp_amd/libsa3k.so. The host-side mirror of the reference trainer headers (host/) is
-header-only and is compiled by its users.
+header-only and is compiled by its users; its benchmark driver host/mirror_bench.cpp is built into
+sa3.cpp_amd/libsa3mirror.so.
 """
 import argparse
 import os
@@ -70,7 +71,24 @@ def build(jobs=8, verbose=False):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
+    build_mirror_bench()
     return LIB
+
+
+MIRROR_SRC = os.path.join(HERE, "host", "mirror_bench.cpp")
+MIRROR_LIB = os.path.join(HERE, "libsa3mirror.so")
+
+
+def build_mirror_bench():
+    """libsa3mirror.so: the host mirror's default training sequence for bench.py (host C++ only)."""
+    tmp = MIRROR_LIB + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-shared", "-fPIC", "-Wall", "-Wextra", "-Werror",
+           "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "host"), MIRROR_SRC, "-o", tmp,
+           "-L", HERE, "-lsa3k", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("mirror bench build failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp, MIRROR_LIB)
 
 
 if __name__ == "__main__":

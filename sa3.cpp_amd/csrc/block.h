@@ -55,7 +55,9 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
                         int64_t max_tokens, int64_t max_ctx);
 void block_free(sa3k_ctx* ctx, sa3k_block* b);
 // share_scratch: take the forward/backward scratch of another workspace of the same shape
-sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share_scratch);
+// count_bytes (optional): allocate nothing, add the bytes the workspace would take and return null
+sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share_scratch,
+                              size_t* count_bytes = nullptr);
 void block_ws_free(sa3k_block_ws* w);
 void block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
                    const float* const* mag, float scale, int dora);

@@ -685,7 +685,8 @@ void block_ws_free(sa3k_block_ws* w) {
     delete w;
 }
 
-sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share) {
+sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share,
+                              size_t* count_bytes) {
     SA3K_REQUIRE(B > 0 && S > 0 && Ctx > 0, "bad workspace shape");
     SA3K_REQUIRE(!share || (share->B == B && share->S == S && share->Ctx == Ctx && share->dim == cfg.dim &&
                             share->inner == cfg.inner && share->H == cfg.heads),
@@ -695,8 +696,15 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
     try {
         const size_t N = (size_t)B * S, NC = (size_t)B * Ctx, D = cfg.dim, I = cfg.inner, H = cfg.heads;
         const size_t BHS = (size_t)B * H * S * HD, BHC = (size_t)B * H * Ctx * HD, BHq = (size_t)B * H * S;
-        auto F32 = [&](size_t n) { float* p = dalloc<float>(n); w->allocs.push_back(p); return p; };
-        auto B16 = [&](size_t n) { bf16* p = dalloc<bf16>(n); w->allocs.push_back(p); return p; };
+        // count_bytes: only add up the bytes the workspace would allocate (every pointer stays null)
+        auto F32 = [&](size_t n) -> float* {
+            if (count_bytes) { *count_bytes += n * sizeof(float); return nullptr; }
+            float* p = dalloc<float>(n); w->allocs.push_back(p); return p;
+        };
+        auto B16 = [&](size_t n) -> bf16* {
+            if (count_bytes) { *count_bytes += n * sizeof(bf16); return nullptr; }
+            bf16* p = dalloc<bf16>(n); w->allocs.push_back(p); return p;
+        };
         w->x = nullptr; w->ctxf = nullptr; w->dssg = nullptr;
         w->modv = F32((size_t)B * 6 * D);
         w->rs_a = F32(N); w->h = B16(N * D); w->qkv = F32(N * 5 * D);
@@ -736,6 +744,10 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
     } catch (...) {
         block_ws_free(w);
         throw;
+    }
+    if (count_bytes) {
+        block_ws_free(w);
+        return nullptr;
     }
     return w;
 }

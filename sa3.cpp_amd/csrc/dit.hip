@@ -1115,6 +1115,25 @@ SA3K_API int sa3k_dit_setup(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_dit_train* 
     });
 }
 
+SA3K_API int sa3k_dit_resident_bytes(sa3k_ctx* ctx, const sa3k_dit* dit, const sa3k_dit_train* train,
+                                     size_t* bytes) {
+    return sa3k_guard(ctx, "sa3k_dit_resident_bytes", [&] {
+        SA3K_REQUIRE(dit && train && bytes, "null pointer");
+        SA3K_REQUIRE(train->batch > 0 && train->frames > 0 && train->ctx_tokens > 0, "batch / frames / ctx_tokens");
+        const sa3k_dit_config& c = dit->cfg;
+        const sa3k_block_config bc{c.dim, c.heads, c.head_dim, c.inner, c.rope_dims, c.window, c.rope_base,
+                                   c.norm_eps, c.qk_eps};
+        // the resident schedule keeps depth workspaces where the recompute schedule keeps one; every
+        // workspace after the first shares its backward scratch with the first
+        sa3k_block_ws shape{};
+        shape.B = train->batch; shape.S = c.mem_tokens + train->frames; shape.Ctx = train->ctx_tokens;
+        shape.dim = c.dim; shape.inner = c.inner; shape.H = c.heads;
+        size_t per = 0;
+        block_ws_build(bc, shape.B, shape.S, shape.Ctx, &shape, &per);
+        *bytes = per * (size_t)(c.depth - 1);
+    });
+}
+
 SA3K_API int sa3k_dit_arena(sa3k_ctx* ctx, sa3k_dit* dit, int which, float** ptr, int64_t* n) {
     return sa3k_guard(ctx, "sa3k_dit_arena", [&] {
         SA3K_REQUIRE(dit && dit->ready, "the model is not set up");

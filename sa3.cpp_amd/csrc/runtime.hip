@@ -86,6 +86,29 @@ const OptionDef& find_option(const char* name) {
 }
 }  // namespace
 
+namespace {
+// dst += src element by element in f32 (the reference's train_accum_add, src/train_loop.h:75-78)
+__global__ __launch_bounds__(256) void vec_add_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                      int64_t n) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        float4 a = *reinterpret_cast<const float4*>(dst + i);
+        const float4 b = *reinterpret_cast<const float4*>(src + i);
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        *reinterpret_cast<float4*>(dst + i) = a;
+    } else {
+        for (int64_t k = i; k < n; ++k) dst[k] += src[k];
+    }
+}
+
+void vec_add(sa3k_ctx* ctx, float* dst, const float* src, int64_t n) {
+    const bool al = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
+    SA3K_REQUIRE(al, "sa3k_vec_add needs 16-byte aligned buffers");
+    vec_add_kernel<<<(unsigned)ceil_div(ceil_div(n, 4), 256), 256, 0, ctx->stream>>>(dst, src, n);
+    SA3K_LAUNCHED();
+}
+}  // namespace
+
 extern "C" {
 
 SA3K_API const char* sa3k_version(void) { return "sa3k 0.1 gfx950"; }
@@ -237,6 +260,21 @@ SA3K_API int sa3k_memset(sa3k_ctx* ctx, void* dst, int value, size_t bytes) {
         SA3K_REQUIRE(dst, "null pointer");
         SA3K_HIP(hipMemsetAsync(dst, value, bytes, ctx->stream));
         sa3k_note_main(ctx);
+    });
+}
+
+SA3K_API int sa3k_device_memory(sa3k_ctx* ctx, size_t* free_bytes, size_t* total_bytes) {
+    return sa3k_guard(ctx, "sa3k_device_memory", [&] {
+        SA3K_REQUIRE(free_bytes && total_bytes, "null pointer");
+        SA3K_HIP(hipMemGetInfo(free_bytes, total_bytes));
+    });
+}
+
+SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst, const float* src, int64_t n) {
+    return sa3k_guard(ctx, "sa3k_vec_add", [&] {
+        SA3K_REQUIRE(n >= 0 && (n == 0 || (dst && src)), "null pointer or negative length");
+        if (!n) return;
+        vec_add(ctx, dst, src, n);
     });
 }
 

@@ -23,7 +23,11 @@
 
 namespace sa3 {
 
-inline bool write_train_lora_gguf(const TrainLoraState& state, const std::string& out_path, std::string& err) {
+inline bool write_train_lora_gguf(const TrainLoraState& state_in, const std::string& out_path, std::string& err) {
+    TrainLoraState synced;   // device-resident training: the newest values, read from the device
+    const TrainLoraState* view = nullptr;
+    if (!train_lora_host_view(state_in, synced, view, err)) return false;
+    const TrainLoraState& state = *view;
     if (state.rank <= 0 || state.params.empty()) {
         err = "cannot write empty LoRA checkpoint";
         return false;

@@ -15,6 +15,7 @@
 
 #include "train_dit.h"
 
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -34,12 +35,19 @@ inline int train_ckpt_segment(const std::string& stem, int depth) {
 
 struct TrainDitCkpt : detail::DitDeviceStep {
     int depth = 0;
+    // the device schedule build_train_dit_ckpt chose: 1 recompute every block before its backward
+    // (the reference's), 0 keep every block's activations (when they fit; the same results bit for
+    // bit, one forward per block less)
+    int recompute = 1;
     std::vector<size_t> tail_param_idx;                // targets of the tail graph (T)
     std::vector<std::vector<size_t>> block_param_idx;  // per block l: the targets of B_l
     std::vector<size_t> head_param_idx;                // targets of the head graph (H)
 };
 
-inline void free_train_dit_ckpt(TrainDitCkpt& ck) { ck = TrainDitCkpt{}; }
+inline void free_train_dit_ckpt(TrainDitCkpt& ck) {
+    detail::release_device_step(ck);
+    ck = TrainDitCkpt{};
+}
 
 // build_train_dit_ckpt (src/train_ckpt.h:143-474): set `dit` up in the checkpointed schedule for
 // one sample of `frames` frames and `ctx_len` context tokens with the adapters of `lora`, and group
@@ -47,11 +55,27 @@ inline void free_train_dit_ckpt(TrainDitCkpt& ck) { ck = TrainDitCkpt{}; }
 inline bool build_train_dit_ckpt(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames,
                                  int cond_dim, int ctx_len, TrainDitCkpt& out, std::string& err, bool inpaint = false) {
     free_train_dit_ckpt(out);
-    if (!detail::setup_dit_step(dit, dc, lora, frames, cond_dim, ctx_len, 1, out, err, inpaint)) {
+    // The reference checkpoints to fit 8 GB GPUs. The activations of every block are kept when they
+    // fit the device with room to spare (a quarter more plus 16 GiB for the weights' working copies,
+    // the arenas and the shared scratch): the recompute forward is then skipped.
+    int recompute = 1;
+    {
+        sa3k_ctx* ctx = dit.ctx();
+        const bool dora = lora.adapter_type == "dora-rows";
+        sa3k_dit_train tr{lora.rank, lora.alpha, dora ? 1 : 0, SA3K_SCOPE_FULL, 1, frames, ctx_len, 0};
+        size_t need = 0, free_b = 0, total_b = 0;
+        if (frames > 0 && ctx_len > 0 && sa3k_dit_resident_bytes(ctx, dit.handle(), &tr, &need) == SA3K_OK &&
+            sa3k_device_memory(ctx, &free_b, &total_b) == SA3K_OK && free_b > need + need / 4 + ((size_t)16 << 30))
+            recompute = 0;
+        // SA3K_CKPT_RECOMPUTE=1 keeps the reference's checkpointed schedule, 0 forces the resident one
+        if (const char* e = std::getenv("SA3K_CKPT_RECOMPUTE")) recompute = std::atoi(e) != 0 ? 1 : 0;
+    }
+    if (!detail::setup_dit_step(dit, dc, lora, frames, cond_dim, ctx_len, recompute, out, err, inpaint)) {
         free_train_dit_ckpt(out);
         return false;
     }
     out.depth = dc.depth;
+    out.recompute = recompute;
     out.block_param_idx.assign((size_t)dc.depth, {});
     for (size_t i = 0; i < lora.params.size(); ++i) {
         const int seg = train_ckpt_segment(lora.params[i].target.stem, dc.depth);

@@ -11,6 +11,7 @@
 #include "train_diffusion.h"
 #include "train_lora.h"
 
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -45,6 +46,22 @@ struct DitDeviceStep {
     // per-frame loss weight [frames] of the last sample
     bool inpaint = false;
     DeviceF32 local, loss_weight;
+    // Device-resident training (this build; set device_resident before the first step). The
+    // reference uploads the adapters and reads every gradient back per sample, and runs AdamW on
+    // host vectors (src/train_loop.h:42-73, :173-211). In this mode the adapter values, the
+    // gradient sums of the accumulation window and the AdamW moments stay in the model's arenas
+    // between calls: run_train_dit_accumulate[_ckpt] uploads a state only when the arena does not
+    // already hold it and adds the sample's gradients into a device accumulator (f32, as
+    // train_accum_add does on the host), train_apply_accumulated_adamw updates the arena in place,
+    // and the host vectors are refreshed by train_state_to_host and read through by the checkpoint
+    // writers (TrainLoraState::device_newer). Same values bit for bit as the round-trip path.
+    bool device_resident = false;
+    const void* held = nullptr;       // the TrainLoraState whose values the params arena holds
+    uint64_t held_edits = 0;          // its host_edits at the upload
+    DeviceF32 acc;                    // the accumulation window's gradient sums
+    void* newer_state = nullptr;      // a TrainLoraState / TrainLoopState newer here than on the host
+    void* newer_loop = nullptr;
+    bool (*release)(DitDeviceStep& step, std::string& err) = nullptr;   // copies those back
 };
 
 // Set `dit` up for one sample of `frames` latent frames and `ctx_len` context tokens with the
@@ -120,7 +137,19 @@ inline bool setup_dit_step(DitModel& dit, const DitConfig& dc, const TrainLoraSt
 // The monolithic training graph (src/train_dit.h:30-48): every block keeps its forward activations.
 struct TrainDitGraph : detail::DitDeviceStep {};
 
-inline void free_train_dit_graph(TrainDitGraph& g) { g = TrainDitGraph{}; }
+namespace detail {
+// Before a graph goes away: the values only it holds (device-resident training) go back to the
+// host state and loop objects.
+inline void release_device_step(DitDeviceStep& g) {
+    std::string err;
+    if (g.release && !g.release(g, err)) throw std::runtime_error("freeing a device-resident training graph: " + err);
+}
+}  // namespace detail
+
+inline void free_train_dit_graph(TrainDitGraph& g) {
+    detail::release_device_step(g);
+    g = TrainDitGraph{};
+}
 
 // build_train_dit_forward_graph (src/train_dit.h:57-218): the model's adapters are those of `lora`.
 inline bool build_train_dit_forward_graph(DitModel& dit, const DitConfig& dc, const TrainLoraState& lora, int frames,

@@ -29,6 +29,11 @@ struct TrainLoopState {
     std::vector<TrainAdamWTensorState> mag_state;
     std::vector<TrainAdamWTensorState> mag_r_state;
     std::vector<TrainAdamWTensorState> mag_c_state;
+    // This build only: set while a device-resident training graph holds newer AdamW moments than
+    // these host vectors (TrainLoraState::device_newer has the rules); device_read fills a loop
+    // state with them.
+    const void* device_newer = nullptr;
+    bool (*device_read)(const void* graph, TrainLoopState& into, std::string& err) = nullptr;
 };
 
 struct TrainLoraGradAccum {
@@ -39,7 +44,23 @@ struct TrainLoraGradAccum {
     std::vector<std::vector<float>> mag;
     std::vector<std::vector<float>> mag_r;
     std::vector<std::vector<float>> mag_c;
+    // This build only: the device-resident training graph whose accumulator holds this window's
+    // sums (the host vectors then stay empty)
+    const void* device = nullptr;
 };
+
+// The values of `loop` as host vectors: `loop` itself, or (device-newer) a copy filled from the
+// device into `tmp`.
+inline bool train_loop_host_view(const TrainLoopState& loop, TrainLoopState& tmp, const TrainLoopState*& view,
+                                 std::string& err) {
+    view = &loop;
+    if (!loop.device_newer) return true;
+    tmp = loop;
+    tmp.device_newer = nullptr;
+    if (!loop.device_read || !loop.device_read(loop.device_newer, tmp, err)) return false;
+    view = &tmp;
+    return true;
+}
 
 inline void train_accum_add(std::vector<float>& dst, const std::vector<float>& grad) {
     if (dst.empty()) dst.assign(grad.size(), 0.0f);
@@ -64,12 +85,138 @@ inline size_t total_size(const std::vector<std::vector<float>*>& v) {
     return n;
 }
 
+// ---- device-resident training (DitDeviceStep::device_resident)
+
+// the params arena in the state layout of the graph's slots
+inline bool read_state_from(const DitDeviceStep& st, TrainLoraState& into, std::string& err) {
+    if (into.params.size() != st.slots.size()) {
+        err = "adapter state does not match the training graph's targets";
+        return false;
+    }
+    sa3k_ctx* ctx = st.model->ctx();
+    for (size_t i = 0; i < st.slots.size(); ++i) {
+        const DitDeviceStep::Slot& sl = st.slots[i];
+        TrainLoraParam& q = into.params[i];
+        q.lora_A.resize((size_t)sl.n_a);
+        q.lora_B.resize((size_t)sl.n_b);
+        if (sl.off_m >= 0) q.magnitude.resize((size_t)sl.n_m);
+        if (sa3k_download(ctx, q.lora_A.data(), st.params + sl.off_a, (size_t)sl.n_a * 4) != SA3K_OK ||
+            sa3k_download(ctx, q.lora_B.data(), st.params + sl.off_b, (size_t)sl.n_b * 4) != SA3K_OK ||
+            (sl.off_m >= 0 &&
+             sa3k_download(ctx, q.magnitude.data(), st.params + sl.off_m, (size_t)sl.n_m * 4) != SA3K_OK))
+            return sa3k_fail(ctx, err);
+    }
+    return true;
+}
+
+// the moment arenas (m, v) of the graph and their slots' vectors in a loop state
+inline bool moment_arenas(const DitDeviceStep& st, float** m, float** v, std::string& err) {
+    sa3k_ctx* ctx = st.model->ctx();
+    if (sa3k_dit_arena(ctx, st.model->handle(), 2, m, nullptr) != SA3K_OK ||
+        sa3k_dit_arena(ctx, st.model->handle(), 3, v, nullptr) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    return true;
+}
+
+inline bool read_loop_from(const DitDeviceStep& st, TrainLoopState& into, std::string& err) {
+    float *m = nullptr, *v = nullptr;
+    if (!moment_arenas(st, &m, &v, err)) return false;
+    sa3k_ctx* ctx = st.model->ctx();
+    const size_t np = st.slots.size();
+    for (auto* x : {&into.A_state, &into.B_state, &into.mag_state}) x->resize(np);
+    for (size_t i = 0; i < np; ++i) {
+        const DitDeviceStep::Slot& sl = st.slots[i];
+        const struct { TrainAdamWTensorState* s; int64_t off, n; } parts[3] = {
+            {&into.A_state[i], sl.off_a, sl.n_a}, {&into.B_state[i], sl.off_b, sl.n_b}, {&into.mag_state[i], sl.off_m, sl.n_m}};
+        for (const auto& p : parts) {
+            if (p.off < 0) continue;
+            p.s->m.resize((size_t)p.n);
+            p.s->v.resize((size_t)p.n);
+            if (sa3k_download(ctx, p.s->m.data(), m + p.off, (size_t)p.n * 4) != SA3K_OK ||
+                sa3k_download(ctx, p.s->v.data(), v + p.off, (size_t)p.n * 4) != SA3K_OK)
+                return sa3k_fail(ctx, err);
+        }
+    }
+    return true;
+}
+
+// a loop's host moments into the graph's moment arenas (zeros where a vector is missing, as the
+// round-trip path starts them)
+inline bool write_loop_to(const DitDeviceStep& st, const TrainLoopState& loop, std::string& err) {
+    float *m = nullptr, *v = nullptr;
+    if (!moment_arenas(st, &m, &v, err)) return false;
+    sa3k_ctx* ctx = st.model->ctx();
+    if (sa3k_memset(ctx, m, 0, (size_t)st.n_params * 4) != SA3K_OK ||
+        sa3k_memset(ctx, v, 0, (size_t)st.n_params * 4) != SA3K_OK)
+        return sa3k_fail(ctx, err);
+    const size_t np = st.slots.size();
+    for (size_t i = 0; i < np; ++i) {
+        const DitDeviceStep::Slot& sl = st.slots[i];
+        const struct { const std::vector<TrainAdamWTensorState>* s; int64_t off, n; } parts[3] = {
+            {&loop.A_state, sl.off_a, sl.n_a}, {&loop.B_state, sl.off_b, sl.n_b}, {&loop.mag_state, sl.off_m, sl.n_m}};
+        for (const auto& p : parts) {
+            if (p.off < 0 || i >= p.s->size()) continue;
+            const TrainAdamWTensorState& ts = (*p.s)[i];
+            if (ts.m.size() == (size_t)p.n && sa3k_upload(ctx, m + p.off, ts.m.data(), (size_t)p.n * 4) != SA3K_OK)
+                return sa3k_fail(ctx, err);
+            if (ts.v.size() == (size_t)p.n && sa3k_upload(ctx, v + p.off, ts.v.data(), (size_t)p.n * 4) != SA3K_OK)
+                return sa3k_fail(ctx, err);
+        }
+    }
+    return true;
+}
+
+inline bool read_state_cb(const void* g, TrainLoraState& into, std::string& err) {
+    return read_state_from(*static_cast<const DitDeviceStep*>(g), into, err);
+}
+inline bool read_loop_cb(const void* g, TrainLoopState& into, std::string& err) {
+    return read_loop_from(*static_cast<const DitDeviceStep*>(g), into, err);
+}
+
+// the graph goes away: the state and loop whose newest values it holds get them back
+inline bool release_cb(DitDeviceStep& st, std::string& err) {
+    if (auto* s = static_cast<TrainLoraState*>(st.newer_state); s && s->device_newer == &st) {
+        if (!read_state_from(st, *s, err)) return false;
+        s->device_newer = nullptr;
+    }
+    if (auto* l = static_cast<TrainLoopState*>(st.newer_loop); l && l->device_newer == &st) {
+        if (!read_loop_from(st, *l, err)) return false;
+        l->device_newer = nullptr;
+    }
+    st.newer_state = st.newer_loop = nullptr;
+    return true;
+}
+
 }  // namespace detail
+
+// This build only: copy the newest values of a device-resident training run back into the host
+// vectors of `lora` (and `loop`, when given). A no-op for values the host already holds.
+inline bool train_state_to_host(TrainLoraState& lora, TrainLoopState* loop, std::string& err) {
+    if (lora.device_newer) {
+        if (!lora.device_read || !lora.device_read(lora.device_newer, lora, err)) return false;
+        lora.device_newer = nullptr;
+    }
+    if (loop && loop->device_newer) {
+        if (!loop->device_read || !loop->device_read(loop->device_newer, *loop, err)) return false;
+        loop->device_newer = nullptr;
+    }
+    return true;
+}
 
 // train_average_and_clip (src/train_loop.h:147-171): mean over the window (count > 1), then scale
 // every vector so the global L2 norm is <= grad_clip; grad_norm_out gets the pre-clip norm.
 inline void train_average_and_clip(TrainLoraGradAccum& accum, const TrainAdamWParams& hp,
                                    double* grad_norm_out = nullptr) {
+    if (accum.device) {   // device-resident: the window's sums are on the device
+        auto& st = *static_cast<detail::DitDeviceStep*>(const_cast<void*>(accum.device));
+        sa3k_ctx* ctx = st.model->ctx();
+        double norm = 0.0;
+        if (sa3k_average_and_clip(ctx, st.acc.get(), st.n_params, accum.count > 0 ? accum.count : 1, hp.grad_clip,
+                                  &norm) != SA3K_OK)
+            throw std::runtime_error(std::string("train_average_and_clip: ") + sa3k_last_error(ctx));
+        if (grad_norm_out) *grad_norm_out = norm;
+        return;
+    }
     auto vecs = detail::accum_vectors(accum);
     const size_t n = detail::total_size(vecs);
     std::string err;
@@ -101,6 +248,42 @@ inline bool train_apply_accumulated_adamw(TrainLoraState& state, TrainLoraGradAc
                                           double* grad_norm_out = nullptr) {
     if (accum.count <= 0) {
         err = "cannot apply empty gradient batch";
+        return false;
+    }
+    if (accum.device) {   // device-resident: AdamW over the graph's arenas, in place
+        auto& st = *static_cast<detail::DitDeviceStep*>(const_cast<void*>(accum.device));
+        sa3k_ctx* ctx = st.model->ctx();
+        if (st.held != &state) {
+            err = "the accumulator's training graph holds another adapter state";
+            return false;
+        }
+        if (loop.device_newer && loop.device_newer != &st) {
+            err = "the loop state's moments are newer on another training graph (train_state_to_host first)";
+            return false;
+        }
+        if (loop.device_newer != &st && !detail::write_loop_to(st, loop, err)) return false;
+        float *m = nullptr, *v = nullptr;
+        if (!detail::moment_arenas(st, &m, &v, err)) return false;
+        loop.step += 1;
+        sa3k_adamw_params p{hp.learning_rate, hp.beta1, hp.beta2, hp.eps, hp.weight_decay, hp.grad_clip};
+        double norm = 0.0;
+        if (sa3k_adamw_clip(ctx, st.params, st.acc.get(), m, v, st.n_params, &p, loop.step, accum.count, &norm) !=
+                SA3K_OK ||
+            sa3k_dit_adapters_changed(ctx, st.model->handle()) != SA3K_OK)
+            return sa3k_fail(ctx, err);
+        if (grad_norm_out) *grad_norm_out = norm;
+        state.device_newer = &st;
+        state.device_read = detail::read_state_cb;
+        loop.device_newer = &st;
+        loop.device_read = detail::read_loop_cb;
+        st.newer_state = &state;
+        st.newer_loop = &loop;
+        st.release = detail::release_cb;
+        train_clear_accum(accum);
+        return true;
+    }
+    if (state.device_newer || loop.device_newer) {
+        err = "adapter or optimizer state is newer on a device-resident training graph (train_state_to_host first)";
         return false;
     }
     loop.step += 1;
@@ -163,6 +346,11 @@ inline bool train_apply_accumulated_adamw(TrainLoraState& state, TrainLoraGradAc
 
 // upload_train_lora_state (src/train_loop.h:42-60): the host adapters into the graph's arena
 inline bool upload_train_lora_state(const TrainLoraState& state, detail::DitDeviceStep& graph, std::string& err) {
+    if (state.device_newer) {   // device-resident training: its newest values are on a device
+        if (state.device_newer == &graph) return true;
+        err = "adapter state is newer on another training graph's device (train_state_to_host first)";
+        return false;
+    }
     if (state.params.size() != graph.slots.size()) {
         err = "adapter state does not match the training graph's targets";
         return false;
@@ -183,8 +371,21 @@ inline bool upload_train_lora_state(const TrainLoraState& state, detail::DitDevi
             return sa3k_fail(ctx, err);
     }
     if (sa3k_dit_adapters_changed(ctx, graph.model->handle()) != SA3K_OK) return sa3k_fail(ctx, err);
+    graph.held = &state;
+    graph.held_edits = state.host_edits;
     return true;
 }
+
+namespace detail {
+// The state's values into the graph's arena: every call on the round-trip path (the reference's
+// per-sample upload); once in device-resident mode, while the arena holds them.
+inline bool ensure_state(DitDeviceStep& st, const TrainLoraState& lora, std::string& err) {
+    if (st.device_resident && st.held == &lora && st.held_edits == lora.host_edits &&
+        (!lora.device_newer || lora.device_newer == &st))
+        return true;
+    return upload_train_lora_state(lora, st, err);
+}
+}  // namespace detail
 
 namespace detail {
 
@@ -245,8 +446,31 @@ inline bool accumulate_step(DitDeviceStep& st, const TrainLoraState& lora, Train
     }
     if (!upload_step_inputs(st, sample, cond, dc, "training step inputs are empty", err)) return false;
     if (inpaint && !upload_inpaint(st, *inpaint, dc, err)) return false;
-    if (!upload_train_lora_state(lora, st, err)) return false;
+    if (!ensure_state(st, lora, err)) return false;
     sa3k_ctx* ctx = st.model->ctx();
+    if (st.device_resident) {
+        // this sample's gradients into the graph's gradient arena, then added into the window's
+        // device accumulator (0 + g1 + g2 ... in f32, as train_accum_add sums them on the host)
+        if (accum.device != &st && (accum.device || accum.count > 0)) {
+            err = "the accumulator holds sums of another graph or of the host path";
+            return false;
+        }
+        if (!st.acc.get() && !st.acc.alloc(ctx, (size_t)st.n_params, err)) return false;
+        if (!accum.device && sa3k_memset(ctx, st.acc.get(), 0, (size_t)st.n_params * 4) != SA3K_OK)
+            return sa3k_fail(ctx, err);
+        if (sa3k_memset(ctx, st.grads, 0, (size_t)st.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
+        double loss = 0.0;
+        if (sa3k_dit_set_local(ctx, st.model->handle(), st.inpaint ? st.local.get() : nullptr) != SA3K_OK ||
+            sa3k_dit_accumulate(ctx, st.model->handle(), st.x.get(), st.target.get(), st.t.get(), st.cross.get(),
+                                st.global.get(), st.inpaint ? st.loss_weight.get() : nullptr, &loss) != SA3K_OK ||
+            sa3k_vec_add(ctx, st.acc.get(), st.grads, st.n_params) != SA3K_OK)
+            return sa3k_fail(ctx, err);
+        loss_out = (float)loss;
+        accum.device = &st;
+        accum.count += 1;
+        (void)visit;   // the device accumulator keeps the arena's target order
+        return true;
+    }
     // this call's gradients alone, then added into the host accumulator like the reference reads
     // them back from its graphs (train_accum_read_subset)
     if (sa3k_memset(ctx, st.grads, 0, (size_t)st.n_params * 4) != SA3K_OK) return sa3k_fail(ctx, err);
@@ -327,7 +551,7 @@ inline bool run_eval_dit_loss(detail::DitDeviceStep& graph, const TrainLoraState
                               const TrainDiffusionSample& sample, const TrainConditioning& cond, const DitConfig& dc,
                               float& loss_out, std::string& err) {
     if (!detail::upload_step_inputs(graph, sample, cond, dc, "evaluation inputs are empty", err)) return false;
-    if (!upload_train_lora_state(lora, graph, err)) return false;
+    if (!detail::ensure_state(graph, lora, err)) return false;
     sa3k_ctx* ctx = graph.model->ctx();
     double loss = 0.0;
     // an inpaint graph evaluates with its last sample's local conditioning and loss weight, as the

@@ -40,7 +40,31 @@ struct TrainLoraState {
     int rank = 0;
     float alpha = 1.0f;
     std::vector<TrainLoraParam> params;
+    // This build only (no reference counterpart): set while a training graph in device-resident
+    // mode (train_dit.h) holds newer values of `params` than these host vectors, i.e. after an
+    // AdamW update that ran there; device_read copies them into a state of the same layout.
+    // train_state_to_host (train_loop.h) refreshes the vectors; the checkpoint writers read through
+    // train_lora_host_view. Host code must not change `params` while this is set.
+    const void* device_newer = nullptr;
+    bool (*device_read)(const void* graph, TrainLoraState& into, std::string& err) = nullptr;
+    // Bumped by the functions of this build that change the host vectors of an existing state
+    // (train_restore_adapter_values): a device-resident graph holding an older edit uploads again.
+    // Code that changes the vectors itself calls upload_train_lora_state.
+    uint64_t host_edits = 0;
 };
+
+// The values of `s` as host vectors: `s` itself, or (device-newer) a copy filled from the device
+// into `tmp`.
+inline bool train_lora_host_view(const TrainLoraState& s, TrainLoraState& tmp, const TrainLoraState*& view,
+                                 std::string& err) {
+    view = &s;
+    if (!s.device_newer) return true;
+    tmp = s;
+    tmp.device_newer = nullptr;
+    if (!s.device_read || !s.device_read(s.device_newer, tmp, err)) return false;
+    view = &tmp;
+    return true;
+}
 
 // Which weights get an adapter (src/train_lora.h:53-97): "full" = every 2-D dit.*.weight, "core" =
 // the 7 per-block projections (dit.<N>.*, no local.*); include/exclude are substring filters.

@@ -163,6 +163,8 @@ inline bool train_restore_adapter_values(TrainLoraState& expected, const TrainLo
             *parts[k].first = *parts[k].second;
         }
     }
+    expected.device_newer = nullptr;   // the restored values are the newest; a holding graph uploads them
+    expected.host_edits += 1;
     return true;
 }
 
@@ -271,8 +273,17 @@ inline bool state_u64(const gguf::Reader& g, const char* key, uint64_t& out, std
 }  // namespace detail
 
 // write_train_state_gguf (src/train_resume.h:336-381)
-inline bool write_train_state_gguf(const TrainLoraState& lora, const TrainLoopState& loop,
+inline bool write_train_state_gguf(const TrainLoraState& lora_in, const TrainLoopState& loop_in,
                                    const TrainResumeProgress& progress, const std::string& out_path, std::string& err) {
+    // device-resident training: the newest values, read from the device
+    TrainLoraState lora_synced;
+    TrainLoopState loop_synced;
+    const TrainLoraState* lv = nullptr;
+    const TrainLoopState* pv = nullptr;
+    if (!train_lora_host_view(lora_in, lora_synced, lv, err) || !train_loop_host_view(loop_in, loop_synced, pv, err))
+        return false;
+    const TrainLoraState& lora = *lv;
+    const TrainLoopState& loop = *pv;
     if (loop.step <= 0 || progress.order.empty() || progress.next_sample > progress.order.size()) {
         err = "cannot write invalid trainer continuation state";
         return false;

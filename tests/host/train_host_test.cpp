@@ -11,6 +11,7 @@
 #include <cmath>
 #include <filesystem>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <random>
 #include <string>
@@ -436,6 +437,119 @@ static void test_gpu() {
         expect(same, "inpaint gradients: checkpointed == monolithic bit for bit");
         expect(local_live, "local-conditioning adapters receive gradients");
         sa3::free_train_dit_ckpt(ick);
+    }
+
+    // ---- device-resident training (TrainDitCkpt::device_resident): the reference's default
+    // sequence (build_train_dit_ckpt -> per-sample run_train_dit_accumulate_ckpt -> AdamW over
+    // the window) with the adapters, the accumulator and the moments kept on the device, against
+    // the round-trip path on a second model with the same weights: the same losses, pre-clip norms,
+    // adapters and moments bit for bit over three updates of two samples each; the checkpoint pair
+    // written from the device-resident state (read through, no explicit sync) is the same bytes;
+    // freeing the graph hands the newest values back to the host state
+    {
+        sa3::DitModel ma, mb;
+        expect(ma.create(dc, SA3K_TYPE_F16, err) && ma.init_random(31, 0.05f, err) && mb.create(dc, SA3K_TYPE_F16, err) &&
+                   mb.init_random(31, 0.05f, err),
+               "resident: two models");
+        sa3::TrainLoraState sa, sb;
+        expect(sa3::init_train_lora_state(ma, targets, "dora-rows", 8, 16.0f, 13, sa, err), "resident: init");
+        for (sa3::TrainLoraParam& q : sa.params)
+            for (float& b : q.lora_B) b = 0.01f * nd(rng);
+        sb = sa;
+        sa3::TrainDitCkpt ca, cb;
+        expect(sa3::build_train_dit_ckpt(ma, dc, sa, frames, dc.cond_dim, ctx_len, ca, err) &&
+                   sa3::build_train_dit_ckpt(mb, dc, sb, frames, dc.cond_dim, ctx_len, cb, err),
+               "resident: build ckpt graphs");
+        expect(ca.recompute == 0 && cb.recompute == 0, "the activations fit: the resident schedule is chosen");
+        cb.device_resident = true;
+        std::vector<sa3::TrainDiffusionSample> samples(2);
+        for (int k = 0; k < 2; ++k) {
+            std::vector<float> zz((size_t)dc.io * frames);
+            for (float& x : zz) x = nd(rng);
+            expect(sampler.sample_at(zz, sampler.draw_t(), samples[(size_t)k], err), "resident: sample");
+        }
+        sa3::TrainLoopState la, lb;
+        bool same = true;
+        for (int step = 0; step < 3; ++step) {
+            sa3::TrainLoraGradAccum aa, ab;
+            for (const sa3::TrainDiffusionSample& smp : samples) {
+                float lossa = 0.0f, lossb = 0.0f;
+                expect(sa3::run_train_dit_accumulate_ckpt(ca, sa, aa, smp, c, dc, lossa, err) &&
+                           sa3::run_train_dit_accumulate_ckpt(cb, sb, ab, smp, c, dc, lossb, err),
+                       "resident: accumulate");
+                same = same && lossa == lossb;
+            }
+            expect(ab.device == &cb && ab.A.empty() && ab.count == 2, "resident: the window's sums stay on the device");
+            double na = 0.0, nb = 0.0;
+            expect(sa3::train_apply_accumulated_adamw(sa, aa, la, hp, err, &na) &&
+                       sa3::train_apply_accumulated_adamw(sb, ab, lb, hp, err, &nb),
+                   "resident: adamw");
+            same = same && na == nb && la.step == lb.step && sb.device_newer == &cb;
+        }
+        expect(same, "resident: losses, norms and steps equal the round-trip path");
+        // checkpoint pair from the device-resident state, read through without an explicit sync
+        sa3::TrainResumeProgress prog;
+        prog.order = {0, 1};
+        prog.next_sample = 1;
+        const std::string p_ad = "resident_pair.gguf", p_st = "resident_pair.state.gguf";
+        auto bytes = [](const std::string& f) {
+            std::FILE* h = std::fopen(f.c_str(), "rb");
+            std::vector<char> v;
+            if (!h) return v;
+            char buf[65536];
+            size_t k;
+            while ((k = std::fread(buf, 1, sizeof buf, h)) > 0) v.insert(v.end(), buf, buf + k);
+            std::fclose(h);
+            return v;
+        };
+        std::vector<char> files[2][2];
+        for (int k = 0; k < 2; ++k) {
+            std::remove(p_ad.c_str());
+            std::remove(p_st.c_str());
+            expect(k == 0 ? sa3::write_train_checkpoint_pair(sa, la, prog, p_ad, p_st, err)
+                          : sa3::write_train_checkpoint_pair(sb, lb, prog, p_ad, p_st, err),
+                   "resident: checkpoint pair");
+            files[k][0] = bytes(p_ad);
+            files[k][1] = bytes(p_st);
+        }
+        std::remove(p_ad.c_str());
+        std::remove(p_st.c_str());
+        expect(!files[0][1].empty() && files[0][0] == files[1][0] && files[0][1] == files[1][1],
+               "resident: the same adapter and trainer-state files");
+        expect(sb.device_newer == &cb && sb.params[0].lora_A != sa.params[0].lora_A,
+               "resident: the host vectors are stale until synced");
+        sa3::free_train_dit_ckpt(cb);   // hands the newest values back to sb and lb
+        bool eq = sb.device_newer == nullptr && lb.device_newer == nullptr && sa.params.size() == sb.params.size();
+        for (size_t i = 0; eq && i < sa.params.size(); ++i)
+            eq = sa.params[i].lora_A == sb.params[i].lora_A && sa.params[i].lora_B == sb.params[i].lora_B &&
+                 sa.params[i].magnitude == sb.params[i].magnitude && la.A_state[i].m == lb.A_state[i].m &&
+                 la.A_state[i].v == lb.A_state[i].v && la.B_state[i].m == lb.B_state[i].m &&
+                 la.mag_state[i].v == lb.mag_state[i].v;
+        expect(eq, "resident: adapters and moments equal the round-trip path bit for bit");
+        sa3::free_train_dit_ckpt(ca);
+        // the reference's checkpointed schedule on request, bitwise equal to the resident one
+        setenv("SA3K_CKPT_RECOMPUTE", "1", 1);
+        sa3::DitModel mc;
+        sa3::TrainDitCkpt cc;
+        expect(mc.create(dc, SA3K_TYPE_F16, err) && mc.init_random(31, 0.05f, err) &&
+                   sa3::build_train_dit_ckpt(mc, dc, sa, frames, dc.cond_dim, ctx_len, cc, err) && cc.recompute == 1,
+               "recompute schedule on request");
+        unsetenv("SA3K_CKPT_RECOMPUTE");
+        sa3::DitModel md;
+        sa3::TrainDitCkpt cd;
+        expect(md.create(dc, SA3K_TYPE_F16, err) && md.init_random(31, 0.05f, err) &&
+                   sa3::build_train_dit_ckpt(md, dc, sa, frames, dc.cond_dim, ctx_len, cd, err) && cd.recompute == 0,
+               "resident schedule again");
+        sa3::TrainLoraGradAccum ac, ad;
+        float lc = 0.0f, ld = 0.0f;
+        expect(sa3::run_train_dit_accumulate_ckpt(cc, sa, ac, samples[0], c, dc, lc, err) &&
+                   sa3::run_train_dit_accumulate_ckpt(cd, sa, ad, samples[0], c, dc, ld, err),
+               "accumulate on both schedules");
+        bool bit = lc == ld && ac.A.size() == ad.A.size();
+        for (size_t i = 0; bit && i < ac.A.size(); ++i) bit = ac.A[i] == ad.A[i] && ac.B[i] == ad.B[i] && ac.mag[i] == ad.mag[i];
+        expect(bit, "checkpointed == resident schedule, bit for bit");
+        sa3::free_train_dit_ckpt(cc);
+        sa3::free_train_dit_ckpt(cd);
     }
 
     // the C ABI's arena path on the same state: gradients of two accumulate calls, then one
