@@ -348,9 +348,10 @@ typedef struct {
 
 typedef struct sa3k_lora_chain sa3k_lora_chain;
 
-/* build_functional_lora (src/lora.h:372-622) for one target: up to 8 adapters applied in order over
+/* build_functional_lora (src/lora.h:372-622) for one target: up to 32 adapters applied in order over
  * the frozen base W (f32 / f16 / bf16 / Q8_0, which is never dequantised into HBM), whose active
- * ranks add up to at most 64. Folds every dora-rows row scale into constants once, in double
+ * ranks add up to at most 512 (up to 64 the rank term rides on the base product as its second
+ * segment, above that it is a GEMM of its own accumulating into Y). Folds every dora-rows row scale into constants once, in double
  * precision: base_scale c0 [out] and the row-scaled B'_k, so that the chain's output equals merging
  * the adapters into W one after another (apply_loras, src/lora.h:111-143). Scratch for up to
  * max_tokens rows. The adapter pointers are read during this call only. */

@@ -16,7 +16,8 @@
 // The forward is two GEMMs: H = X [s_1 A_1; ...; s_M A_M]^T (every residual's rank-r input at once),
 // then the base product over the stored weight (bf16 working copy, or f16 / Q8_0 decoded on its way
 // into LDS) with c0 applied to its accumulators before the rank segment H [B'_1 .. B'_M]^T is added
-// (the GEMM's prescale mode), and the bias.
+// (the GEMM's prescale mode), and the bias. A total rank above one K tile (64) adds the rank term
+// as a third GEMM accumulating into the output instead of as the base product's second segment.
 #include "lora.h"
 
 #include <cmath>
@@ -27,8 +28,9 @@ using namespace sa3k;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxChain = 8;     // adapters in one chain
-constexpr int kMaxRank = 64;     // total rank of the active adapters (one K tile of the rank segment)
+constexpr int kMaxChain = 32;    // adapters in one chain
+constexpr int kMaxRank = 512;    // total rank of the active adapters
+constexpr int kSegRank = 64;     // up to this total rank the rank term rides on the base product
 
 struct ChainArgs {
     int n;                       // active adapters
@@ -102,12 +104,15 @@ __global__ __launch_bounds__(kThreads) void chain_stack_a_kernel(ChainArgs c, in
     Ac[idx] = (bf16)v;
 }
 
-// One workgroup per output row o: nsq0, P[a] = W[o] . A_row(a), then the chain walk.
+// One workgroup per output row o: nsq0, P[a] = W[o] . A_row(a), the per-adapter terms T2_k and
+// G_kl (one thread each), then the chain walk (one thread) and the folded row (all threads).
 __global__ __launch_bounds__(kThreads) void chain_fold_kernel(sa3k_weight w, ChainArgs c, const double* __restrict__ gram,
                                                               int Rp, float* __restrict__ c0, float* __restrict__ Bp,
                                                               bf16* __restrict__ Bc) {
     __shared__ double sh[kThreads / 64];
     __shared__ double P[kMaxRank];
+    __shared__ double T2[kMaxChain], G[kMaxChain][kMaxChain], g[kMaxChain];
+    __shared__ double bsh;
     const int64_t o = blockIdx.x, in = w.in;
     double nsq0 = 0.0;
     for (int64_t i = threadIdx.x; i < in; i += kThreads) {
@@ -123,17 +128,16 @@ __global__ __launch_bounds__(kThreads) void chain_fold_kernel(sa3k_weight w, Cha
         if (threadIdx.x == 0) P[a] = s;
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    // chain walk (M <= 8 adapters, R <= 64): per-row quantities in double
-    double T2[kMaxChain], G[kMaxChain][kMaxChain], g[kMaxChain];
-    for (int k = 0; k < c.n; ++k) {
-        double t = 0.0;
-        for (int j = 0; j < c.rank[k]; ++j) t += P[c.col0[k] + j] * (double)c.B[k][o * c.rank[k] + j];
-        T2[k] = t;
-        g[k] = 1.0;
-    }
-    for (int k = 0; k < c.n; ++k)
-        for (int l = 0; l < c.n; ++l) {
+    // per-row quantities in double: T2_k = P_k . B_k[o], G_kl = B_k[o] . (gram_kl B_l[o])
+    for (int t = threadIdx.x; t < c.n * (c.n + 1); t += kThreads) {
+        if (t < c.n) {
+            const int k = t;
+            double v = 0.0;
+            for (int j = 0; j < c.rank[k]; ++j) v += P[c.col0[k] + j] * (double)c.B[k][o * c.rank[k] + j];
+            T2[k] = v;
+            g[k] = 1.0;
+        } else {
+            const int k = (t - c.n) / c.n, l = (t - c.n) % c.n;
             double acc = 0.0;
             for (int j = 0; j < c.rank[k]; ++j) {
                 const double* gr = gram + (int64_t)(c.col0[k] + j) * c.R + c.col0[l];
@@ -143,25 +147,34 @@ __global__ __launch_bounds__(kThreads) void chain_fold_kernel(sa3k_weight w, Cha
             }
             G[k][l] = acc;
         }
-    double b = 1.0;
-    for (int j = 0; j < c.n; ++j) {
-        if (!c.dora[j]) continue;
-        double nsq = b * b * nsq0;
-        for (int k = 0; k <= j; ++k) nsq += 2.0 * (double)c.scale[k] * g[k] * b * T2[k];
-        for (int k = 0; k <= j; ++k)
-            for (int l = 0; l <= j; ++l) nsq += (double)c.scale[k] * c.scale[l] * g[k] * g[l] * G[k][l];
-        const double d = (double)c.mag[j][o] / sqrt(nsq);
-        b *= d;
-        for (int k = 0; k <= j; ++k) g[k] *= d;
     }
-    c0[o] = (float)b;
-    for (int k = 0; k < c.n; ++k)
-        for (int j = 0; j < c.rank[k]; ++j) {
-            const float v = (float)(g[k] * (double)c.B[k][o * c.rank[k] + j]);
-            Bp[o * c.R + c.col0[k] + j] = v;
-            Bc[o * Rp + c.col0[k] + j] = (bf16)v;
+    __syncthreads();
+    if (threadIdx.x == 0) {   // the walk: each dora-rows adapter rescales the base and every residual so far
+        double b = 1.0;
+        for (int j = 0; j < c.n; ++j) {
+            if (!c.dora[j]) continue;
+            double nsq = b * b * nsq0;
+            for (int k = 0; k <= j; ++k) nsq += 2.0 * (double)c.scale[k] * g[k] * b * T2[k];
+            for (int k = 0; k <= j; ++k)
+                for (int l = 0; l <= j; ++l) nsq += (double)c.scale[k] * c.scale[l] * g[k] * g[l] * G[k][l];
+            const double d = (double)c.mag[j][o] / sqrt(nsq);
+            b *= d;
+            for (int k = 0; k <= j; ++k) g[k] *= d;
         }
-    for (int j = c.R; j < Rp; ++j) Bc[o * Rp + j] = (bf16)0.0f;
+        bsh = b;
+        c0[o] = (float)b;
+    }
+    __syncthreads();
+    for (int a = threadIdx.x; a < Rp; a += kThreads) {
+        if (a < c.R) {
+            const int k = adapter_of(c, a), j = a - c.col0[k];
+            const float v = (float)(g[k] * (double)c.B[k][o * c.rank[k] + j]);
+            Bp[o * c.R + a] = v;
+            Bc[o * Rp + a] = (bf16)v;
+        } else {
+            Bc[o * Rp + a] = (bf16)0.0f;
+        }
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void chain_cvt_kernel(const float* __restrict__ x, bf16* __restrict__ y, int64_t n) {
@@ -207,7 +220,7 @@ SA3K_API int sa3k_lora_chain_create(sa3k_ctx* ctx, const sa3k_weight* W, int n_a
                                     const sa3k_chain_adapter* adapters, int64_t max_tokens, sa3k_lora_chain** out) {
     return sa3k_guard(ctx, "sa3k_lora_chain_create", [&] {
         SA3K_REQUIRE(W && out && (n_adapters == 0 || adapters), "null pointer");
-        SA3K_REQUIRE(n_adapters >= 0 && n_adapters <= kMaxChain, "a chain holds at most 8 adapters");
+        SA3K_REQUIRE(n_adapters >= 0 && n_adapters <= kMaxChain, "a chain holds at most 32 adapters");
         SA3K_REQUIRE(max_tokens > 0, "max_tokens must be positive");
         *out = nullptr;
         ChainArgs a{};
@@ -227,12 +240,14 @@ SA3K_API int sa3k_lora_chain_create(sa3k_ctx* ctx, const sa3k_weight* W, int n_a
             dora = dora || x.dora;
             ++a.n;
         }
-        SA3K_REQUIRE(a.R <= kMaxRank, "the active adapters' ranks add up to more than 64");
+        SA3K_REQUIRE(a.R <= kMaxRank, "the active adapters' ranks add up to more than 512");
         sa3k_lora_chain* c = new sa3k_lora_chain();
         c->W = W;
         c->max_tokens = max_tokens;
         c->R = a.R;
-        c->Rp = (int)ceil_div(a.R, 8) * 8;
+        // a rank segment of the base product takes up to one K tile (8-column steps); a longer rank
+        // term is its own GEMM, whose K runs in whole 64-column tiles
+        c->Rp = a.R <= kSegRank ? (int)ceil_div(a.R, 8) * 8 : (int)ceil_div(a.R, 64) * 64;
         c->dora = dora;
         try {
             const int64_t in = W->in, outd = W->out;
@@ -317,16 +332,27 @@ SA3K_API int sa3k_lora_chain_forward(sa3k_ctx* ctx, sa3k_lora_chain* chain, int 
         weight_fwd_operand(W, g);
         g.A = xb; g.lda = W->in;
         g.M = N; g.N = W->out; g.K = W->in;
-        if (chain->R > 0) {
+        const bool seg = chain->R > 0 && chain->Rp <= kSegRank;
+        if (seg) {
             g.A2 = chain->Hc; g.lda2 = chain->Rp; g.B2 = chain->Bc; g.ldb2 = chain->Rp; g.K2 = chain->Rp;
             if (chain->dora) {
                 g.colscale = chain->c0;
                 g.prescale = 1;
             }
+        } else if (chain->R > 0 && chain->dora) {
+            g.colscale = chain->c0;   // y = c0 (.) (W x) + bias, the rank term added below
         }
         g.bias = bias;
         g.C = Y; g.ldc = W->out;
         gemm_run(ctx, g, "chain_main");
+        if (chain->R > 0 && !seg) {   // y += H [B'_1 .. B'_M]^T
+            GemmDesc r;
+            r.prec = SA3K_PREC_BF16; r.a_src = SRC_BF16; r.b_src = SRC_BF16;
+            r.A = chain->Hc; r.lda = chain->Rp; r.B = chain->Bc; r.ldb = chain->Rp;
+            r.M = N; r.N = W->out; r.K = chain->Rp;
+            r.C = Y; r.ldc = W->out; r.accumulate = 1;
+            gemm_run(ctx, r, "chain_rank");
+        }
     });
 }
 

@@ -11,7 +11,9 @@ tests/test_oracle_chain.py).
   0.9999), and the two base paths within 1e-5 of each other;
 * lora-only, dora-only and mixed chains, ranks that are not multiples of 8, a zero-strength adapter
   (the identity), an empty chain (a plain mul_mat), a bias; order matters for two dora adapters;
-* chains beyond the limits (9 adapters, total rank over 64) are rejected.
+* long chains past the rank segment of the base product (10 adapters, total rank 128; 32 adapters,
+  total rank 512: the rank term as a GEMM of its own), against the oracle on both base paths;
+* chains beyond the limits (33 adapters, total rank over 512) are rejected.
 """
 import numpy as np
 import pytest
@@ -64,6 +66,9 @@ def run_chain(ctx, w, dev, X, bias=None, decode=False):
 
 CHAINS = {
     "dora_lora_dora": [(1, 32, 32.0, 1.0), (0, 16, 16.0, 1.7), (1, 16, 32.0, 0.6)],
+    # 10 adapters, total rank 128 (past one K tile: the rank term is its own GEMM)
+    "ten_mixed_r128": [(k % 3 == 0, 16 if k < 6 else 8, 16.0, 0.5 + 0.1 * k) for k in range(10)] +
+                      [(0, 8, 8.0, 0.0)],
     "lora_r2_r3": [(0, 2, 4.0, 1.0), (0, 3, 6.0, 1.7)],
     "dora_zero_strength": [(1, 8, 16.0, 1.0), (1, 24, 8.0, 0.0), (0, 8, 8.0, 1.0)],
     "empty": [(1, 16, 16.0, 0.0)],
@@ -121,17 +126,38 @@ def test_chain_order_matters(ctx):
     assert rel_err(ab, ba) > 5 * max(rel_err(ab, ref_ab), rel_err(ba, ref_ba))
 
 
+def test_chain_32_adapters_rank_512(ctx):
+    # the longest chain: 32 adapters (every fourth dora-rows) of rank 16, total rank 512
+    g = rng(313)
+    in_, out_, N = 512, 1024, 128
+    w, Wdec = make_weight(ctx, g, out_, in_, sa3k.TYPE_Q8_0)
+    ads = adapters_for(g, Wdec, [(k % 4 == 1, 16, 16.0, 0.3) for k in range(32)])
+    X = g.normal(0, 1, (N, in_)).astype(np.float32)
+    try:
+        y, (c0, Bp) = run_chain(ctx, w, to_device(ctx, ads), X)
+    finally:
+        w.destroy()
+    ref = oracle.chain_forward(X, Wdec, ads)
+    e, c = rel_err(y, ref), cosine(y, ref)
+    assert e <= 2e-2 and c >= 0.9999, f"rel {e:.3e} cos {c:.6f}"
+    rc0, rBp, _ = oracle.chain_fold(Wdec, ads)
+    assert np.max(np.abs(c0 - rc0) / np.abs(rc0)) < 1e-5
+    assert rel_err(Bp, rBp) < 1e-5 and Bp.shape == (out_, 512)
+
+
 def test_chain_limits(ctx):
     g = rng(312)
     w, Wdec = make_weight(ctx, g, 256, 128, sa3k.TYPE_F16)
     try:
-        nine = to_device(ctx, adapters_for(g, Wdec, [(0, 8, 8.0, 1.0)] * 9))
+        many = to_device(ctx, adapters_for(g, Wdec, [(0, 8, 8.0, 1.0)] * 33))
         with pytest.raises(sa3k.Sa3kError):
-            ctx.lora_chain(w, nine, 64)
-        wide = to_device(ctx, adapters_for(g, Wdec, [(0, 32, 8.0, 1.0), (1, 40, 8.0, 1.0)]))
+            ctx.lora_chain(w, many, 64)
+        wide = to_device(ctx, adapters_for(g, Wdec, [(0, 256, 8.0, 1.0), (1, 264, 8.0, 1.0)]))
         with pytest.raises(sa3k.Sa3kError):
             ctx.lora_chain(w, wide, 64)
-        ok = ctx.lora_chain(w, wide[:1], 64)   # 32 alone fits
+        ok = ctx.lora_chain(w, wide[:1], 64)   # 256 alone fits
+        ok.destroy()
+        ok = ctx.lora_chain(w, many[:32], 64)   # 32 adapters of rank 8 fit
         ok.destroy()
     finally:
         w.destroy()
