@@ -154,10 +154,14 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 blocks (default 1). It holds from a DiT's setup.
  *   "prep_side"   1: with f32 head linears, a DiT's bf16 group refresh runs on the second stream
  *                 beside the heads' refresh and forward on the main one (default 1)
+ *   "epi_fuse"    1: a block's FFN SwiGLU val * silu(glu) is written by the up-projection's GEMM
+ *                 epilogue (each 256-column output tile holds matching val and glu columns) where
+ *                 the chosen tiles allow it (no split over K); 0: by its own kernel (default 1)
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
  * kv_stack, attn_fwd32 and head_f32, which change the rounding or the f32 summation order
- * (prep_side changes only the stream a refresh runs on). Not to
+ * (prep_side changes only the stream a refresh runs on; epi_fuse only where SwiGLU is computed).
+ * Not to
  * be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);
 

@@ -345,7 +345,7 @@ __global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int n4, bf
     if (i4 >= n4) return;
     const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
     const float* f = F + (int64_t)row * 2 * I + c;
-    st4(g + e, map4(ld4(f), ld4(f + I), [](float val, float glu) { return val * glu * sigmoidf_(glu); }));
+    st4(g + e, map4(ld4(f), ld4(f + I), [](float val, float glu) { return val * glu * swiglu_sigmoid(glu); }));
 }
 
 // dF (du: written as the FFN up-projection's dU, scale over its 2I columns)
@@ -882,9 +882,11 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         // feed-forward: x2 = x1 + yc, fin = rms_norm(x2) * ff_g * (1 + sc_f) + sh_f
         arm();
         resnorm(w->x1, w->yc, -1, w->x2, b->ff_g, 3, w->fin, w->rs_f);
-        chk(ctx, sa3k_lin_forward(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, b->bias[5], w->F));
-        arm();
-        launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->F, I, (int)(N * I / 4), w->g);
+        // g = val * silu(glu): from the up-projection's epilogue where its tiles allow, else here
+        if (!lin_forward_swiglu(ctx, b->L[5], w->fin, N, b->bias[5], w->F, w->g)) {
+            arm();
+            launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->F, I, (int)(N * I / 4), w->g);
+        }
         chk(ctx, sa3k_lin_forward(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, b->bias[6], w->yf));
         launch(ctx, "blk_gate", gate_res_kernel, dim3(nblk(N * D / 4)), (const float*)w->x2, (const float*)w->yf, mv, 5,
                S, D, (int)(N * D / 4), out);

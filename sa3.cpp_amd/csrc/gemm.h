@@ -88,6 +88,15 @@ struct GemmDesc {
     // 1: colscale multiplies the main segment A . B^T only, before the second segment is added
     // (C = colscale (.) (A B^T) + A2 B2^T); needs colscale, no extra rows and no U / Ub copies
     int prescale = 0;
+    // Paired SwiGLU epilogue (the DiT FFN up-projection, src/dit.h:259-264): the N = 2 sw_half
+    // output columns are [val | glu]. Where the chosen tiles allow it (bf16 256-column tiles, no
+    // split over K, the staged epilogue), a tile holds columns [c, c + 128) of both halves and also
+    // writes sw_g [M][sw_ldg] = bf16(val * glu * sigmoid(glu)) from its final values; *sw_done is
+    // set then (else the caller applies SwiGLU itself). C, U and every other output are unchanged.
+    int64_t sw_half = 0;
+    bf16* sw_g = nullptr;
+    int64_t sw_ldg = 0;
+    int* sw_done = nullptr;
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

@@ -57,6 +57,11 @@ struct DmaParams {
     int bq;
     const void* Bs; int64_t ldbs;
     uint32_t bs_bytes;
+    // paired SwiGLU epilogue (GemmDesc::sw_*): 256-column tiles below 2 sw_half hold columns
+    // [128 t, 128 t + 128) of both halves; 0: off
+    int64_t sw_half;
+    bf16* sw_g; int64_t sw_ldg;
+    int* sw_done;   // host-side: set to 1 by the launcher that keeps the pairing
 };
 
 namespace {
@@ -203,23 +208,52 @@ __device__ __forceinline__ void st_out(bool nt, uint2* p, uint2 v) {
     else *p = v;
 }
 
+// Column factors of four consecutive main columns n..n+3 (colscale where the epilogue applies it,
+// bias; 1 and 0 otherwise or past N). The staged epilogue loads them once per thread: a thread's
+// columns stay the same over every row it stores.
+struct EpiCols {
+    float4 cs, bs;
+};
+__device__ inline EpiCols epi_cols(const DmaParams& p, int64_t n) {
+    EpiCols k{make_float4(1.0f, 1.0f, 1.0f, 1.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
+    if (n < p.N) {
+        if (p.colscale && !p.prescale) k.cs = *reinterpret_cast<const float4*>(p.colscale + n);
+        if (p.bias) k.bs = *reinterpret_cast<const float4*>(p.bias + n);
+    }
+    return k;
+}
+// Wait for the loads of k here, ahead of the output stores. A use of k after stores were issued
+// would wait on the vector-memory counter, which the stores count too (in order), so every row's
+// epilogue would wait for the previous row's stores to complete.
+__device__ __forceinline__ void epi_cols_ready(const EpiCols& k) {
+    asm volatile("" ::"v"(k.cs.x), "v"(k.cs.y), "v"(k.cs.z), "v"(k.cs.w), "v"(k.bs.x), "v"(k.bs.y), "v"(k.bs.z),
+                 "v"(k.bs.w));
+}
+// colscale, then bias, on x = alpha (A B^T + ...) of main rows
+__device__ inline float4 epi_scale(const DmaParams& p, float4 x, const EpiCols& k) {
+    if (p.colscale && !p.prescale) x = make_float4(x.x * k.cs.x, x.y * k.cs.y, x.z * k.cs.z, x.w * k.cs.w);
+    if (p.bias) x = make_float4(x.x + k.bs.x, x.y + k.bs.y, x.z + k.bs.z, x.w + k.bs.w);
+    return x;
+}
+
 // Epilogue of four consecutive columns n..n+3 of row m (host-checked: 16-byte aligned rows, N a
-// multiple of 4), same operations and order as epilogue_elem.
-__device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a) {
+// multiple of 4), same operations and order as epilogue_elem; k = epi_cols(p, n). Returns the
+// main-row value before accumulation into C (unspecified for extra rows and columns).
+__device__ inline float4 epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a, const EpiCols& k) {
     if (n >= p.N) {   // four extra columns (N % 4 == 0)
         if (m < p.M) {
             const bf16 b[4] = {(bf16)(p.alpha_x * a.x), (bf16)(p.alpha_x * a.y), (bf16)(p.alpha_x * a.z),
                                (bf16)(p.alpha_x * a.w)};
             *reinterpret_cast<uint2*>(p.Cbn + m * p.ldcn + (n - p.N)) = __builtin_bit_cast(uint2, b);
         }
-        return;
+        return a;
     }
     float4 x = make_float4(p.alpha * a.x, p.alpha * a.y, p.alpha * a.z, p.alpha * a.w);
     if (m >= p.M) {
         if (p.Cbx) {
             bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
             *reinterpret_cast<uint2*>(p.Cbx + (m - p.M) * p.ldcx + n) = __builtin_bit_cast(uint2, b);
-            return;
+            return x;
         }
         float4* cx = reinterpret_cast<float4*>(p.Cx + (m - p.M) * p.ldcx + n);
         if (p.accumulate_x) {
@@ -227,21 +261,15 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
             x = make_float4(o.x + x.x, o.y + x.y, o.z + x.z, o.w + x.w);
         }
         *cx = x;
-        return;
+        return x;
     }
     if (p.U) st_out(p.nt_store, reinterpret_cast<float4*>(p.U + m * p.ldu + n), x);
     if (p.Ub) {
         bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
         st_out(p.nt_store, reinterpret_cast<uint2*>(p.Ub + m * p.ldu + n), __builtin_bit_cast(uint2, b));
     }
-    if (p.colscale && !p.prescale) {
-        const float4 c = *reinterpret_cast<const float4*>(p.colscale + n);
-        x = make_float4(x.x * c.x, x.y * c.y, x.z * c.z, x.w * c.w);
-    }
-    if (p.bias) {
-        const float4 c = *reinterpret_cast<const float4*>(p.bias + n);
-        x = make_float4(x.x + c.x, x.y + c.y, x.z + c.z, x.w + c.w);
-    }
+    x = epi_scale(p, x, k);
+    const float4 v = x;
     if (p.C) {
         float4* c = reinterpret_cast<float4*>(p.C + m * p.ldc + n);
         if (p.accumulate) {
@@ -254,6 +282,51 @@ __device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, f
         bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
         st_out(p.nt_store, reinterpret_cast<uint2*>(p.Cb + m * p.ldcb + n), __builtin_bit_cast(uint2, b));
     }
+    return v;
+}
+__device__ inline void epilogue_vec4(const DmaParams& p, int64_t m, int64_t n, float4 a) {
+    epilogue_vec4(p, m, n, a, epi_cols(p, n));
+}
+
+// Output column of local column c of the 256-column tile tn: with the paired SwiGLU epilogue,
+// columns [0, 128) of a tile below 2 sw_half are val columns 128 tn + c and [128, 256) the matching
+// glu columns sw_half + 128 tn + c - 128; otherwise (and for the extra-column tile past 2 sw_half)
+// 256 tn + c.
+__device__ __forceinline__ int64_t tile_col(const DmaParams& p, int64_t n0, int c) {
+    if (p.sw_half > 0 && n0 < 2 * p.sw_half) {
+        const int64_t h0 = n0 >> 1;
+        return c < 128 ? h0 + c : p.sw_half + h0 + (c - 128);
+    }
+    return n0 + c;
+}
+
+// tile_col for a tile BN columns wide: only 256-column tiles are ever paired
+template <int BN>
+__device__ __forceinline__ int64_t tile_col_bn(const DmaParams& p, int64_t n0, int c) {
+    if constexpr (BN == 256) return tile_col(p, n0, c);
+    else return n0 + c;
+}
+
+__device__ __forceinline__ void st_out(bool nt, unsigned* p, unsigned v) {
+    if (nt) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+// Paired SwiGLU tile (GemmDesc::sw_half): lane l < 32 of a wave holds the val chunk (columns nv ..
+// nv + 3) of its row's epilogue value, lane l + 32 the glu chunk (sw_half + nv ..); the two swap
+// values and each writes two of the four g = bf16(val * glu * sigmoid(glu)), the lower lane columns
+// nv, nv + 1, the upper one nv + 2, nv + 3. Called by all 64 lanes of a wave with one row m.
+__device__ inline void swiglu_pair_store(const DmaParams& p, int64_t m, int64_t nq, bool lo, float4 mine) {
+    float4 other;
+    other.x = __shfl_xor(mine.x, 32);
+    other.y = __shfl_xor(mine.y, 32);
+    other.z = __shfl_xor(mine.z, 32);
+    other.w = __shfl_xor(mine.w, 32);
+    const float4 v = lo ? mine : other, u = lo ? other : mine;
+    const float v0 = lo ? v.x : v.z, v1 = lo ? v.y : v.w, u0 = lo ? u.x : u.z, u1 = lo ? u.y : u.w;
+    const bf16 o[2] = {(bf16)(v0 * u0 * swiglu_sigmoid(u0)), (bf16)(v1 * u1 * swiglu_sigmoid(u1))};
+    const int64_t col = lo ? nq : nq - p.sw_half + 2;
+    st_out(p.nt_store, reinterpret_cast<unsigned*>(p.sw_g + m * p.sw_ldg + col), __builtin_bit_cast(unsigned, o));
 }
 
 // NW wave64s per workgroup (4 or 8): WMW of them along M, NW/WMW along N, each owning a
@@ -359,7 +432,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
-        int64_t gn = n0 + row;
+        int64_t gn = tile_col_bn<BN>(p, n0, row);
         if (gn >= p.Nt) gn = 0;
         bg[q] = gn < p.N ? static_cast<const char*>(p.B) + (gn * p.ldb + k0 + kc * CE) * EB
                          : static_cast<const char*>(p.Bx) + ((gn - p.N) * p.ldbx + k0 + kc * CE) * EB;
@@ -385,7 +458,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
-        int64_t gn = n0 + row;
+        int64_t gn = tile_col_bn<BN>(p, n0, row);
         if (gn >= p.Nt) gn = 0;
         boff[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * CE) * EB) : (uint32_t)(((gn - p.N) * p.ldbx + kc * CE) * EB);
     }
@@ -403,7 +476,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     }
     // the 8 rows of B slot (q, wave) start at n0 + (q * NT + 64 wave) / 8: one source per slot
     // (N % 8 == 0), chosen on the scalar unit
-    auto slot_bx = [&](int q) { return n0 + (q * NT + wave * 64) / 8 < p.Nt && n0 + (q * NT + wave * 64) / 8 >= p.N; };
+    unsigned bx_mask = 0;   // bit q: slot q's rows are extra columns (fixed over the K loop)
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        const int64_t r0 = tile_col_bn<BN>(p, n0, (q * NT + wave * 64) / 8);
+        if (r0 < p.Nt && r0 >= p.N) bx_mask |= 1u << q;
+    }
+    auto slot_bx = [&](int q) { return ((bx_mask >> q) & 1u) != 0; };
     // Q8_0: quant slot s = q NT + tid holds row s / 4, physical chunk s % 4 = logical chunk
     // kc ^ qswz(row) (16 quant bytes); lane l of wave w loads row 64 w + l's two block scales
     uint32_t qoff[BQ == 2 ? NBQ : 1] = {};
@@ -648,7 +727,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 
     // Staged epilogue: the waves owning rows [rb, rb + ER) of the tile write their accumulators to
     // LDS (row-major, padded rows), then every thread stores 16-byte row chunks: whole cache lines
-    // per wave instead of one scattered element per lane and register.
+    // per wave instead of one scattered element per lane and register. A thread's chunk column cq
+    // is the same in every row (NT is a multiple of the chunks per row), so its column factors are
+    // loaded once, ahead of the output stores. A paired SwiGLU tile's val-column threads also read
+    // the matching glu chunk 128 columns on and write g.
+    constexpr int CPR = BN / 4;   // 16-byte chunks per row
+    static_assert(NT % CPR == 0, "a thread's chunk column must not change between rows");
+    const int cq = (tid % CPR) * 4;
+    const int64_t nq = tile_col_bn<BN>(p, n0, cq);
+    const EpiCols kq = epi_cols(p, nq);
+    const bool sw_tile = BN == 256 && p.sw_half > 0 && n0 < 2 * p.sw_half;   // workgroup-uniform
+    epi_cols_ready(kq);
     float* st = reinterpret_cast<float*>(lds);
     __syncthreads();   // every wave is done reading the last K tile
 #pragma unroll
@@ -664,14 +753,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        constexpr int CPR = BN / 4;   // 16-byte chunks per row
         for (int e = tid; e < ER * CPR; e += NT) {
-            const int r = e / CPR, c = (e % CPR) * 4;
-            const int64_t m = m0 + rb + r, n = n0 + c;
-            if (m >= Mt || n >= p.Nt) continue;
-            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + c);
-            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + n) = a;
-            else epilogue_vec4(p, m, n, a);
+            const int r = e / CPR;
+            const int64_t m = m0 + rb + r;
+            if (m >= Mt || nq >= p.Nt) continue;
+            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + cq);
+            if (p.ws) {
+                *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + nq) = a;
+                continue;
+            }
+            const float4 v = epilogue_vec4(p, m, nq, a, kq);
+            if (sw_tile && m < p.M) swiglu_pair_store(p, m, nq, cq < 128, v);   // a wave holds one row
         }
         if (rb + ER < BM) __syncthreads();
     }
@@ -761,15 +853,21 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
         const int s = q * NT + tid, row = s >> 3, kc = (s & 7) ^ swz(row);
-        int64_t gn = n0 + row;
+        int64_t gn = tile_col(p, n0, row);
         if (gn >= p.Nt) gn = p.Nt - 1;
         bo.off[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * 8) * 2) : (uint32_t)(((gn - p.N) * p.ldbx + kc * 8) * 2);
         b2o.off[q] = kc * 8 < p.K2 && gn < p.N ? (uint32_t)((gn * p.ldb2 + kc * 8) * 2) : kNoData;
     }
-    auto slot_bx = [&](int q) {   // wave-uniform: slot q's B rows are extra columns (N % 8 == 0)
-        const int64_t r0 = min(n0 + 64 * q + 8 * wave, p.Nt - 1);
-        return r0 >= p.N;
-    };
+    // wave-uniform, fixed over the K loop: bit q set when slot q's B rows are extra columns (N % 8
+    // == 0), resp. its A rows extra rows (M % 8 == 0)
+    unsigned bx_mask = 0, x_mask = 0;
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        if (min(tile_col(p, n0, 64 * q + 8 * wave), p.Nt - 1) >= p.N) bx_mask |= 1u << q;
+#pragma unroll
+    for (int q = 0; q < NA; ++q)
+        if (min(m0 + 64 * q + 8 * wave, Mt - 1) >= p.M) x_mask |= 1u << q;
+    auto slot_bx = [&](int q) { return ((bx_mask >> q) & 1u) != 0; };
     if constexpr (KN) {
         // [K][N] B: slot s of the B region is sub-tile s / 512 (64 columns), row k = (s % 512) / 8 of
         // the K tile, logical chunk (s % 8) ^ swz(k); columns past N read a valid column
@@ -781,10 +879,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
             bo.off[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
         }
     }
-    auto slot_x = [&](int q) {   // wave-uniform: slot q's rows are extra rows
-        const int64_t r0 = min(m0 + 64 * q + 8 * wave, Mt - 1);
-        return r0 >= p.M;
-    };
+    auto slot_x = [&](int q) { return ((x_mask >> q) & 1u) != 0; };
 
     auto issue = [&](auto s_c, int t) {
         constexpr uint32_t so_lds = (uint32_t)((decltype(s_c)::value % STAGES) * STAGE_BYTES);
@@ -873,8 +968,16 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
         });
     }
 
-    // staged epilogue only (the host routes outputs that do not allow 16-byte stores elsewhere)
+    // staged epilogue only (the host routes outputs that do not allow 16-byte stores elsewhere);
+    // fixed chunk column per thread as in gemm_dma_kernel
     auto out_row = [&](int v) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); };
+    constexpr int CPR = BN / 4;
+    static_assert(NT % CPR == 0, "a thread's chunk column must not change between rows");
+    const int cq = (tid % CPR) * 4;
+    const int64_t nq = tile_col(p, n0, cq);
+    const EpiCols kq = epi_cols(p, nq);
+    const bool sw_tile = p.sw_half > 0 && n0 < 2 * p.sw_half;   // workgroup-uniform
+    epi_cols_ready(kq);
     float* st = reinterpret_cast<float*>(lds);
     __syncthreads();
 #pragma unroll
@@ -890,14 +993,17 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        constexpr int CPR = BN / 4;
         for (int e = tid; e < ER * CPR; e += NT) {
-            const int r = e / CPR, c = (e % CPR) * 4;
-            const int64_t m = m0 + rb + r, n = n0 + c;
-            if (m >= Mt || n >= p.Nt) continue;
-            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + c);
-            if (p.ws) *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + n) = a;
-            else epilogue_vec4(p, m, n, a);
+            const int r = e / CPR;
+            const int64_t m = m0 + rb + r;
+            if (m >= Mt || nq >= p.Nt) continue;
+            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + cq);
+            if (p.ws) {
+                *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + nq) = a;
+                continue;
+            }
+            const float4 v = epilogue_vec4(p, m, nq, a, kq);
+            if (sw_tile && m < p.M) swiglu_pair_store(p, m, nq, cq < 128, v);   // a wave holds one row
         }
         if (rb + ER < BM) __syncthreads();
     }
@@ -941,6 +1047,22 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     }
     const int64_t m = idx / p.Nt, n = idx - m * p.Nt;
     epilogue_elem(p, m, n, s);
+}
+
+// Keep the paired SwiGLU epilogue only where the launch computes each tile's final values in one
+// workgroup and stores them through the staged epilogue: 256-column tiles, no split over K, a
+// [N][K] bf16 B, N = 2 sw_half a multiple of 256 (every tile below N is paired), no extra rows and
+// no accumulation into C. Otherwise sw_half is cleared and *sw_done left alone.
+void settle_swiglu(DmaParams& p, int bn, int splits, bool kn, int bq) {
+    if (p.sw_half <= 0) return;
+    const bool ok = bn == 256 && splits == 1 && !kn && bq == 0 && p.vec_epi && !p.accumulate && p.Mx == 0 &&
+                    p.N == 2 * p.sw_half && p.N % 256 == 0 && p.sw_g && p.sw_ldg % 4 == 0 &&
+                    (uintptr_t)p.sw_g % 8 == 0;
+    if (!ok) {
+        p.sw_half = 0;
+        return;
+    }
+    if (p.sw_done) *p.sw_done = 1;
 }
 
 template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0>
@@ -999,6 +1121,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                     ok(p.Ub, p.ldu, 8) && ok(p.Cb, p.ldcb, 8) && ok(p.Cx, p.ldcx, 16) && ok(p.Cbx, p.ldcx, 8) &&
                     ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
+    settle_swiglu(p, BN, splits, KN, BQ);
     if (splits > 1) {
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
         if (use_fixup(ctx, (p.M + p.Mx) * p.Nt, tiles)) p.counters = stream_counters(ctx);
@@ -1073,6 +1196,7 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     if (p.b_kn) p.b_bytes = (uint32_t)(p.K * p.ldb * 2);   // the whole [K][ldb] operand (big_ok: < 2 GiB)
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
+    settle_swiglu(p, BN, splits, p.b_kn != 0, 0);
     if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
     {
         KernelScope ks(ctx, p.b_kn ? "gemm_big<256,256,kn,bf16>" : "gemm_big<256,256,bf16>",
@@ -1220,6 +1344,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.bq = d.b_src == SRC_F16 ? 1 : d.b_src == SRC_Q8 ? 2 : 0;
     p.Bs = d.Bs; p.ldbs = d.ldbs;
     p.bs_bytes = 0;
+    p.sw_half = d.sw_half; p.sw_g = d.sw_g; p.sw_ldg = d.sw_ldg; p.sw_done = d.sw_done;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

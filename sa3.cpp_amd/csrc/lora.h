@@ -57,6 +57,10 @@ const float* lin_stack_forward(sa3k_ctx* ctx, LinStack* st, const float* X, int6
 int64_t lin_stack_ld(const LinStack* st);   // row stride of Y (n out)
 const float* lin_stack_y(const LinStack* st);   // Y (fixed for the stack's lifetime)
 void lin_stack_free(LinStack* st);
+// sa3k_lin_forward of a bf16 FFN up-projection (Y = [val | glu], bf16 X) that also writes the
+// SwiGLU g = bf16(val * silu(glu)) [N][out / 2] from its GEMM epilogue when the option epi_fuse is
+// on and the chosen kernel allows it. Returns whether it did; if not, the caller computes g from Y.
+bool lin_forward_swiglu(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, const float* bias, float* Y, bf16* g);
 // The B operand of X W^T (forward orientation) in g's precision: the bf16 working copy when the
 // weight has one and the precision is bf16, else the stored elements or Q8_0 planes, which the
 // GEMM decodes on their way into LDS.

@@ -100,6 +100,7 @@ struct sa3k_ctx {
     int attn_fwd32 = 1;                   // attention forward on 32x32x16 MFMA blocks, 32 queries per wave
     int prep_side = 1;                    // a DiT's bf16 group refresh on the second stream beside the f32 heads'
     int head_f32 = 1;                     // a DiT's head / tail linears on f32 MFMA (f32 / f16 bases)
+    int epi_fuse = 1;                     // FFN SwiGLU in the up-projection's GEMM epilogue where its tiles allow
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
                                           // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream
@@ -361,6 +362,13 @@ inline bool use_fixup(const sa3k_ctx* ctx, int64_t elems, int64_t tiles) {
 inline int* tn_counters(const sa3k_ctx* ctx, int64_t tiles, int bit) {
     if (!(ctx->tn_fuse & bit) || tiles > kMaxFixupTiles) return nullptr;
     return stream_counters(ctx);
+}
+
+// The FFN SwiGLU's gate sigmoid(z) = 1 / (1 + e^-z) on the hardware exp2 and reciprocal (within a
+// few ulp of the correctly rounded value). The up-projection's GEMM epilogue and the separate
+// SwiGLU kernel both use it, so the two paths give the same bits.
+__device__ __forceinline__ float swiglu_sigmoid(float z) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * z));
 }
 
 // Split partial sums handed from one workgroup to another inside a launch ("the last split to

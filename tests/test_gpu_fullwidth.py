@@ -99,3 +99,39 @@ def test_dit_depth1_full_width_vs_oracle(ctx, local_dim):
         print(f"worst normwise error {e:.3e} ({what}), lowest cosine {min(x[1] for x in worst):.7f}")
     finally:
         d.destroy()
+
+
+@pytest.mark.parametrize("S", [64 + 960, 64 + 1024])
+def test_block_swiglu_epilogue_bitwise(ctx, S):
+    """The FFN SwiGLU written by the up-projection's GEMM epilogue (option epi_fuse) against the
+    separate SwiGLU kernel, at the benchmark's width: 2 x 1024 tokens take the 128 x 256 DMA tiles
+    without a split over K, 2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles. Both orders
+    of evaluation are the same per element, so every output and gradient agrees bit for bit; the
+    profile shows the SwiGLU kernel only in the backward when fused."""
+    assert_shipped_options(ctx)
+    B, Ctx = 2, 128
+    print(f"swiglu epilogue: B {B}, S {S}, Ctx {Ctx}", flush=True)
+    cfg, w, x, cx, gc = bb.random_block(61, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
+                                        alpha=32.0, dora=True, window=256, w_sd=0.02, b_sd=0.01)
+    dout = rng(62).normal(0, 1e-2, x.shape).astype(np.float32)
+    gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
+    res, swiglu_launches = {}, {}
+    try:
+        for fuse in (1, 0):
+            ctx.set_option("epi_fuse", fuse)
+            ctx.profile(True)
+            ctx.profile_reset()
+            res[fuse] = run_gpu(ctx, gb, x, cx, gc, dout)
+            rep = ctx.profile_report()
+            ctx.profile(False)
+            swiglu_launches[fuse] = sum(v[0] for k, v in rep.items() if k.startswith("blk_swiglu"))
+    finally:
+        ctx.profile(False)
+        ctx.set_options(ctx.defaults)
+        gb.destroy()
+    assert swiglu_launches == {1: 1, 0: 2}, swiglu_launches
+    for k in ("out", "dx", "dctx", "dgcond"):
+        assert np.array_equal(res[1][k], res[0][k]), k
+    for k in ("dA", "dB", "dm"):
+        for t in range(7):
+            assert np.array_equal(res[1][k][t], res[0][k][t]), f"{k}[{t}]"
