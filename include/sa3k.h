@@ -154,13 +154,21 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 blocks (default 1). It holds from a DiT's setup.
  *   "prep_side"   1: with f32 head linears, a DiT's bf16 group refresh runs on the second stream
  *                 beside the heads' refresh and forward on the main one (default 1)
- *   "epi_fuse"    1: a block's FFN SwiGLU val * silu(glu) is written by the up-projection's GEMM
- *                 epilogue (each 256-column output tile holds matching val and glu columns) where
- *                 the chosen tiles allow it (no split over K); 0: by its own kernel (default 1)
+ *   "epi_fuse"    bit 0: a block's FFN SwiGLU val * silu(glu) is written by the up-projection's
+ *                 GEMM epilogue (each 256-column output tile holds matching val and glu columns);
+ *                 bit 1: the per-head q/k RMS norm, RoPE and head-major bf16 layout of the
+ *                 attention inputs come out of the QKV and cross-query projections' epilogues; each
+ *                 where the chosen tiles allow it (no split over K), else by its own kernel
+ *                 (default 3)
+ *   "act_bf16"    bit 0: a block's backward reads a bf16 copy of the FFN up-projection's output
+ *                 (written by its epilogue) instead of the f32 output, which then is forward
+ *                 scratch; bit 1: likewise for the QKV and cross-query outputs (default 1). It
+ *                 holds for workspaces built from now on (a DiT: from its setup).
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
- * kv_stack, attn_fwd32 and head_f32, which change the rounding or the f32 summation order
- * (prep_side changes only the stream a refresh runs on; epi_fuse only where SwiGLU is computed).
+ * kv_stack, attn_fwd32, head_f32 and act_bf16, which change the rounding or the f32 summation order
+ * (prep_side changes only the stream a refresh runs on; epi_fuse only which kernel computes
+ * SwiGLU and the head preparation).
  * Not to
  * be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);

@@ -21,16 +21,21 @@ struct sa3k_block {
 
 struct sa3k_block_ws {
     int B = 0, S = 0, Ctx = 0, dim = 0, H = 0, inner = 0;
-    // forward activations (read again by the backward)
-    float* modv; const float* x; float* rs_a; sa3k::bf16* h; float* qkv;
+    // forward activations (read again by the backward). With act_bf16 bit 0 (bit 1) the f32
+    // output F of the FFN up-projection (qkv and qf of the QKV and cross-query projections) is
+    // forward scratch, written only where the separate SwiGLU (head-preparation) kernel needs it,
+    // and the backward reads its bf16 copy Fb (qkvb, qfb), which the projection's epilogue always
+    // writes; otherwise the copy is null and the backward reads the f32 output.
+    int act_bf16 = 0;
+    float* modv; const float* x; float* rs_a; sa3k::bf16* h; float* qkv; sa3k::bf16* qkvb;
     sa3k::bf16 *q1, *k1, *q2, *k2, *v; float* rq;
     sa3k::bf16* o; sa3k::bf16 *o1, *o2; float *l1, *l2; float* y; float* x1; float* rs_c; sa3k::bf16* hc;
-    float* qf; float* kv; const float* ctxf; sa3k::bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck;
+    float* qf; sa3k::bf16* qfb; float* kv; const float* ctxf; sa3k::bf16 *cq1, *ck1, *cq2, *ck2, *cv; float *rcq, *rck;
     // when set, the block's context K/V projection was computed by a stacked product: its rows of
     // kv_ld floats hold this block's 3 dim outputs (the block skips its own cross.kv forward)
     const float* kv_ext = nullptr; int64_t kv_ld = 0;
     sa3k::bf16* oc; sa3k::bf16 *co1, *co2; float *cl1, *cl2; float* x2; float* rs_f; sa3k::bf16* fin; float* F;
-    sa3k::bf16* g; float* yf;
+    sa3k::bf16* Fb; sa3k::bf16* g; float* yf;
     // inpaint local conditioning (src/dit.h:244-254), set by the caller per block or null: the
     // forward adds ladd [B][ladd_T][dim] to the latent rows (the last ladd_T of each sample's S)
     // after the cross-attention; the backward writes the gradient of that sum to dladd (same shape)
@@ -55,9 +60,12 @@ sa3k_block* block_build(sa3k_ctx* ctx, const sa3k_block_config& cfg, int weight_
                         int64_t max_tokens, int64_t max_ctx);
 void block_free(sa3k_ctx* ctx, sa3k_block* b);
 // share_scratch: take the forward/backward scratch of another workspace of the same shape
+// act_bf16 (the option of that name): bit 0 keeps a bf16 copy of the FFN up-projection's output for
+// the backward (the f32 output becomes forward scratch), bit 1 likewise for the QKV and
+// cross-query outputs
 // count_bytes (optional): allocate nothing, add the bytes the workspace would take and return null
 sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share_scratch,
-                              size_t* count_bytes = nullptr);
+                              int act_bf16, size_t* count_bytes = nullptr);
 void block_ws_free(sa3k_block_ws* w);
 void block_prepare(sa3k_ctx* ctx, sa3k_block* b, const float* const* A, const float* const* Bm,
                    const float* const* mag, float scale, int dora);

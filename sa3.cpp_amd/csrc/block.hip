@@ -14,6 +14,7 @@
 // recomputes block l into a shared one right before its backward (the gradient-checkpointed
 // schedule of src/train_ckpt.h:386-431).
 #include "block.h"
+#include "headprep.h"
 #include "lora.h"
 
 #include <cmath>
@@ -64,6 +65,12 @@ __global__ void modv_kernel(const float* __restrict__ ssg, const float* __restri
 typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
 
 __device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ inline float4 ld4b(const bf16* p) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+__device__ inline float4 ldx4(const float* p) { return ld4(p); }
+__device__ inline float4 ldx4(const bf16* p) { return ld4b(p); }
 // An adapted linear's dU = bf16(scale (.) dY) for four consecutive output columns c..c+3 (scale
 // null: 1), written by the kernel that produces dY instead of dY itself (lin_du / lin_backward_du)
 __device__ inline void st_du4(bf16* p, float4 v, const float* scale, int64_t c) {
@@ -348,14 +355,15 @@ __global__ void swiglu_fwd_kernel(const float* __restrict__ F, int I, int n4, bf
     st4(g + e, map4(ld4(f), ld4(f + I), [](float val, float glu) { return val * glu * swiglu_sigmoid(glu); }));
 }
 
-// dF (du: written as the FFN up-projection's dU, scale over its 2I columns)
-__global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const float* __restrict__ F, int I, int n4,
+// dF from F or its bf16 copy (du: written as the FFN up-projection's dU, scale over its 2I columns)
+template <class FT>
+__global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const FT* __restrict__ F, int I, int n4,
                                   float* __restrict__ dF, bf16* __restrict__ du, const float* __restrict__ dsc) {
     const int i4 = blockIdx.x * kThreads + threadIdx.x;
     if (i4 >= n4) return;
     const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
     const int64_t o = (int64_t)row * 2 * I + c;
-    const float4 val = ld4(F + o), glu = ld4(F + o + I), d = ld4(dg + e);
+    const float4 val = ldx4(F + o), glu = ldx4(F + o + I), d = ld4(dg + e);
     float dv[4], dgl[4];
     const float vs[4] = {val.x, val.y, val.z, val.w}, gs[4] = {glu.x, glu.y, glu.z, glu.w}, ds[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
@@ -423,40 +431,6 @@ struct PrepArgs {
     int64_t ldin;         // row stride of in (parts*dim when 0)
 };
 
-// NeoX RoPE over 16 lanes per (row, head), lane j holding dims 4j..4j+3 (rope_dims % 8 == 0, so a
-// rotation pair (i, i + half) is the same component of lanes j and j + half/4).
-// The table entries of this lane (cos, sin of its four dims; lanes past rope_dims get zeros and do
-// not use them).
-__device__ inline void rope_tab4(int d0, int rope, const float* __restrict__ row_tab, float4& cs, float4& sn) {
-    const int half = rope >> 1;
-    cs = sn = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (d0 >= rope) return;
-    const int i = d0 < half ? d0 : d0 - half;
-    cs = ld4(row_tab + i);
-    sn = ld4(row_tab + half + i);
-}
-// Rotates y in place with the table entries of rope_tab4; lanes past rope_dims keep y. sign -1:
-// the inverse rotation.
-__device__ inline void rope4_cs(float4& y, int d0, int rope, const float4& cs, const float4& sn, float sign) {
-    const int half = rope >> 1;
-    const bool rot = d0 < rope, first = d0 < half;
-    const int lane = threadIdx.x & 63;
-    const int src = rot ? (first ? lane + (half >> 2) : lane - (half >> 2)) : lane;
-    const float4 p = make_float4(__shfl(y.x, src, 64), __shfl(y.y, src, 64), __shfl(y.z, src, 64), __shfl(y.w, src, 64));
-    if (!rot) return;
-    const float ys[4] = {y.x, y.y, y.z, y.w}, ps[4] = {p.x, p.y, p.z, p.w};
-    const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sign * sn.x, sign * sn.y, sign * sn.z, sign * sn.w};
-    float o[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) o[u] = first ? ys[u] * cc[u] - ps[u] * ss[u] : ps[u] * ss[u] + ys[u] * cc[u];
-    y = make_float4(o[0], o[1], o[2], o[3]);
-}
-
-__device__ inline float group16_sum(float v) {
-    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 16);
-    return v;
-}
-
 // items = rows * H (< 2^31); every part's loads are issued before any is used
 __global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int items) {
     const int item = blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
@@ -483,10 +457,8 @@ __global__ __launch_bounds__(kThreads) void prep_fwd_kernel(PrepArgs a, int item
         if (k >= a.parts) break;
         float4 y = x[k];
         if (a.p[k].gamma) {
-            const float r = 1.0f / sqrtf(group16_sum(dot4(y, y)) / HD + a.eps);
+            const float r = head_norm_rope4(y, gm[k], a.p[k].rope != 0, d0, a.rope_dims, a.eps, cs, sn);
             if (d0 == 0) a.rstd[(int64_t)item * a.parts + k] = r;
-            y = map4(y, gm[k], [r](float v, float g) { return v * r * g; });
-            if (a.p[k].rope) rope4_cs(y, d0, a.rope_dims, cs, sn, 1.0f);
         }
         st4(a.p[k].out + ho, y);
     }
@@ -507,6 +479,7 @@ struct PrepBwdArgs {
     bf16* du;             // instead of din: the input projection's dU [B*Sx][parts*dim]
     const float* dsc;     // its column scale (null: 1)
     int64_t ldin;         // row stride of in (parts*dim when 0)
+    const bf16* inb;      // instead of in: its bf16 copy [B*Sx][parts*dim]
 };
 
 __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int items) {
@@ -528,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void prep_bwd_kernel(PrepBwdArgs a, int i
         if (k >= a.parts) break;
         g[k] = ld4(a.p[k].dy + ho);
         if (a.p[k].gamma) {
-            x[k] = ld4(a.in + xi + (int64_t)k * a.dim);
+            x[k] = a.inb ? ld4b(a.inb + xi + (int64_t)k * a.dim) : ld4(a.in + xi + (int64_t)k * a.dim);
             gmv[k] = ld4(a.p[k].gamma + d0);
             rsv[k] = a.rstd[(int64_t)item * a.parts + k];
             any_rope |= a.p[k].rope != 0;
@@ -686,12 +659,14 @@ void block_ws_free(sa3k_block_ws* w) {
 }
 
 sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ctx, const sa3k_block_ws* share,
-                              size_t* count_bytes) {
+                              int act_bf16, size_t* count_bytes) {
     SA3K_REQUIRE(B > 0 && S > 0 && Ctx > 0, "bad workspace shape");
     SA3K_REQUIRE(!share || (share->B == B && share->S == S && share->Ctx == Ctx && share->dim == cfg.dim &&
                             share->inner == cfg.inner && share->H == cfg.heads),
                  "shared scratch comes from a workspace of another shape");
+    SA3K_REQUIRE(!share || share->act_bf16 == act_bf16, "shared scratch comes from a workspace of another layout");
     sa3k_block_ws* w = new sa3k_block_ws();
+    w->act_bf16 = act_bf16;
     w->B = B; w->S = S; w->Ctx = Ctx; w->dim = cfg.dim; w->H = cfg.heads; w->inner = cfg.inner;
     try {
         const size_t N = (size_t)B * S, NC = (size_t)B * Ctx, D = cfg.dim, I = cfg.inner, H = cfg.heads;
@@ -707,16 +682,23 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
         };
         w->x = nullptr; w->ctxf = nullptr; w->dssg = nullptr;
         w->modv = F32((size_t)B * 6 * D);
-        w->rs_a = F32(N); w->h = B16(N * D); w->qkv = F32(N * 5 * D);
+        const bool fcopy = (act_bf16 & 1) != 0, qcopy = (act_bf16 & 2) != 0;
+        w->rs_a = F32(N); w->h = B16(N * D);
+        w->qkvb = qcopy ? B16(N * 5 * D) : nullptr;
+        w->qkv = qcopy ? nullptr : F32(N * 5 * D);
         w->q1 = B16(BHS); w->k1 = B16(BHS); w->q2 = B16(BHS); w->k2 = B16(BHS); w->v = B16(BHS);
         w->rq = F32(N * H * 5);
         w->o = B16(N * D); w->o1 = B16(BHS); w->o2 = B16(BHS); w->l1 = F32(BHq); w->l2 = F32(BHq);
-        w->y = F32(N * D); w->x1 = F32(N * D); w->rs_c = F32(N); w->hc = B16(N * D); w->qf = F32(N * 2 * D);
+        w->y = F32(N * D); w->x1 = F32(N * D); w->rs_c = F32(N); w->hc = B16(N * D);
+        w->qfb = qcopy ? B16(N * 2 * D) : nullptr;
+        w->qf = qcopy ? nullptr : F32(N * 2 * D);
         w->kv = F32(NC * 3 * D);
         w->cq1 = B16(BHS); w->cq2 = B16(BHS); w->ck1 = B16(BHC); w->ck2 = B16(BHC); w->cv = B16(BHC);
         w->rcq = F32(N * H * 2); w->rck = F32(NC * H * 3);
         w->oc = B16(N * D); w->co1 = B16(BHS); w->co2 = B16(BHS); w->cl1 = F32(BHq); w->cl2 = F32(BHq);
-        w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D); w->F = F32(N * 2 * I);
+        w->x2 = F32(N * D); w->rs_f = F32(N); w->fin = B16(N * D);
+        w->Fb = fcopy ? B16(N * 2 * I) : nullptr;
+        w->F = fcopy ? nullptr : F32(N * 2 * I);
         w->g = B16(N * I); w->yf = F32(N * D);
         w->rope_tab = F32((size_t)S * HD);
         w->part_chunks = (int)std::max<int64_t>(1, std::min<int64_t>(32, ceil_div(S, 32)));
@@ -724,6 +706,12 @@ sa3k_block_ws* block_ws_build(const sa3k_block_config& cfg, int B, int S, int Ct
         // block's backward (resident activations, late join) writes the shared scratch: per workspace
         w->dfin = F32(N * D);
         w->dx1 = F32(N * D);
+        // the f32 outputs that only the forward reads: shared scratch like the backward's
+        if (qcopy) {
+            w->qkv = share ? share->qkv : F32(N * 5 * D);
+            w->qf = share ? share->qf : F32(N * 2 * D);
+        }
+        if (fcopy) w->F = share ? share->F : F32(N * 2 * I);
         if (share) {
             w->yc = share->yc;
             w->dg = share->dg; w->dx2 = share->dx2; w->doc = share->doc; w->dhc = share->dhc;
@@ -792,7 +780,7 @@ SA3K_API int sa3k_block_ws_create(sa3k_ctx* ctx, const sa3k_block_config* cfg, i
                                   sa3k_block_ws** out) {
     return sa3k_guard(ctx, "sa3k_block_ws_create", [&] {
         SA3K_REQUIRE(cfg && out, "null pointer");
-        *out = block_ws_build(*cfg, B, S, Ctx, nullptr);
+        *out = block_ws_build(*cfg, B, S, Ctx, nullptr, ctx->act_bf16);
     });
 }
 
@@ -850,24 +838,32 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         // self attention
         arm();
         resnorm(x, nullptr, -1, nullptr, b->pre_g, 0, w->h, w->rs_a);
-        chk(ctx, sa3k_lin_forward(ctx, b->L[0], SA3K_TYPE_BF16, w->h, N, nullptr, w->qkv));
-        PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.qk_eps, w->rope_tab,
-                    {{w->q1, b->sq_g, 1}, {w->k1, b->sk_g, 1}, {w->v, nullptr, 0}, {w->q2, b->sq_g, 1}, {w->k2, b->sk_g, 1}},
-                    w->rq};
-        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), ps, (int)(N * H));
+        // q|k|v|qd|kd heads: normed, rotated and head-major from the projection's epilogue where its
+        // tiles allow, else by the prep kernel
+        const HeadPrep hs{5, S, H, D, c.rope_dims, c.qk_eps, w->rope_tab, {w->q1, w->k1, w->v, w->q2, w->k2},
+                          {b->sq_g, b->sk_g, nullptr, b->sq_g, b->sk_g}, {1, 1, 0, 1, 1}, w->rq};
+        if (!lin_forward_headprep(ctx, b->L[0], w->h, N, w->qkv, w->qkvb, hs)) {
+            PrepArgs ps{w->qkv, 5, S, H, D, c.rope_dims, c.qk_eps, w->rope_tab,
+                        {{w->q1, b->sq_g, 1}, {w->k1, b->sk_g, 1}, {w->v, nullptr, 0}, {w->q2, b->sq_g, 1}, {w->k2, b->sk_g, 1}},
+                        w->rq};
+            launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), ps, (int)(N * H));
+        }
         arm();
         attn_forward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, B, H, S, S, c.window, scale, w->o, w->o1, w->o2, w->l1, w->l2);
         chk(ctx, sa3k_lin_forward(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, nullptr, w->y));
         // cross attention: x1 = x + y * sigmoid(1 - g_a), hc = rms_norm(x1) * cross_g
         arm();
         resnorm(x, w->y, 2, w->x1, b->cross_g, -1, w->hc, w->rs_c);
-        chk(ctx, sa3k_lin_forward(ctx, b->L[2], SA3K_TYPE_BF16, w->hc, N, nullptr, w->qf));
+        const HeadPrep hq{2, S, H, D, c.rope_dims, c.qk_eps, nullptr, {w->cq1, w->cq2}, {b->cq_g, b->cq_g}, {0, 0}, w->rcq};
+        const bool q_done = lin_forward_headprep(ctx, b->L[2], w->hc, N, w->qf, w->qfb, hq);
         if (!w->kv_ext) chk(ctx, sa3k_lin_forward(ctx, b->L[3], SA3K_TYPE_F32, context, NC, nullptr, w->kv));
         const float* kv = w->kv_ext ? w->kv_ext : w->kv;
         const int64_t kv_ld = w->kv_ext ? w->kv_ld : 0;
-        PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.qk_eps, nullptr,
-                    {{w->cq1, b->cq_g, 0}, {w->cq2, b->cq_g, 0}, {}, {}, {}}, w->rcq};
-        launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), pq, (int)(N * H));
+        if (!q_done) {
+            PrepArgs pq{w->qf, 2, S, H, D, c.rope_dims, c.qk_eps, nullptr,
+                        {{w->cq1, b->cq_g, 0}, {w->cq2, b->cq_g, 0}, {}, {}, {}}, w->rcq};
+            launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(N * H)), pq, (int)(N * H));
+        }
         PrepArgs pk{kv, 3, Ctx, H, D, c.rope_dims, c.qk_eps, nullptr,
                     {{w->ck1, b->ck_g, 0}, {w->ck2, b->ck_g, 0}, {w->cv, nullptr, 0}, {}, {}}, w->rck, kv_ld};
         launch(ctx, "blk_prep_fwd", prep_fwd_kernel, dim3(ngroup16_blk(NC * H)), pk, (int)(NC * H));
@@ -883,7 +879,7 @@ void sa3k::block_forward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const f
         arm();
         resnorm(w->x1, w->yc, -1, w->x2, b->ff_g, 3, w->fin, w->rs_f);
         // g = val * silu(glu): from the up-projection's epilogue where its tiles allow, else here
-        if (!lin_forward_swiglu(ctx, b->L[5], w->fin, N, b->bias[5], w->F, w->g)) {
+        if (!lin_forward_swiglu(ctx, b->L[5], w->fin, N, b->bias[5], w->F, w->Fb, w->g)) {
             arm();
             launch(ctx, "blk_swiglu", swiglu_fwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->F, I, (int)(N * I / 4), w->g);
         }
@@ -930,8 +926,12 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                (float*)nullptr, lin_du(b->L[6]), lin_du_scale(b->L[6]));
         colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
         lin_backward_du(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dg, 0, dA[6], dB[6], dmt[6]);
-        launch(ctx, "blk_swiglu", swiglu_bwd_kernel, dim3(nblk(N * I / 4)), (const float*)w->dg, (const float*)w->F, I,
-               (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
+        if (w->Fb)
+            launch(ctx, "blk_swiglu", swiglu_bwd_kernel<bf16>, dim3(nblk(N * I / 4)), (const float*)w->dg,
+                   (const bf16*)w->Fb, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
+        else
+            launch(ctx, "blk_swiglu", swiglu_bwd_kernel<float>, dim3(nblk(N * I / 4)), (const float*)w->dg,
+                   (const float*)w->F, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
         lin_backward_du(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dfin, 0, dA[5], dB[5], dmt[5]);
         colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
         norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, b->L[4], nullptr);
@@ -947,7 +947,7 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
         PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, nullptr,
                        {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, nullptr,
-                       lin_du(b->L[2]), lin_du_scale(b->L[2])};
+                       lin_du(b->L[2]), lin_du_scale(b->L[2]), 0, w->qfb};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bq, (int)(N * H));
         PrepBwdArgs bk{w->kv_ext ? w->kv_ext : w->kv, 3, Ctx, H, D, c.rope_dims, nullptr,
                        {{w->dk1, b->ck_g, 0}, {w->dk2, b->ck_g, 0}, {w->dv, nullptr, 0}, {}, {}}, w->rck, nullptr,
@@ -971,7 +971,7 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
         PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, w->rope_tab,
                        {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
-                       w->rq, nullptr, lin_du(b->L[0]), lin_du_scale(b->L[0])};
+                       w->rq, nullptr, lin_du(b->L[0]), lin_du_scale(b->L[0]), 0, w->qkvb};
         launch(ctx, "blk_prep_bwd", prep_bwd_kernel, dim3(ngroup16_blk(N * H)), bs, (int)(N * H));
         // the previous block's last second-stream work (late_join) reads w->dh, written next
         if (ctx->block_tail_pending) {

@@ -668,7 +668,8 @@ void setup(sa3k_ctx* ctx, sa3k_dit* d, const sa3k_dit_train& tr) {
                 chk(ctx, sa3k_lin_prepare(ctx, d->ll[i], nullptr, nullptr, d->scale, 0, nullptr, nullptr));
     }
     const int nws = tr.recompute ? 1 : c.depth;
-    for (int l = 0; l < nws; ++l) d->ws.push_back(block_ws_build(bc, B, S, Ctx, l == 0 ? nullptr : d->ws[0]));
+    for (int l = 0; l < nws; ++l)
+        d->ws.push_back(block_ws_build(bc, B, S, Ctx, l == 0 ? nullptr : d->ws[0], ctx->act_bf16));
     SA3K_HIP(hipStreamSynchronize(ctx->stream));
     d->ready = true;
     d->dirty = true;
@@ -1129,7 +1130,8 @@ SA3K_API int sa3k_dit_resident_bytes(sa3k_ctx* ctx, const sa3k_dit* dit, const s
         shape.B = train->batch; shape.S = c.mem_tokens + train->frames; shape.Ctx = train->ctx_tokens;
         shape.dim = c.dim; shape.inner = c.inner; shape.H = c.heads;
         size_t per = 0;
-        block_ws_build(bc, shape.B, shape.S, shape.Ctx, &shape, &per);
+        shape.act_bf16 = ctx->act_bf16;
+        block_ws_build(bc, shape.B, shape.S, shape.Ctx, &shape, ctx->act_bf16, &per);
         *bytes = per * (size_t)(c.depth - 1);
     });
 }

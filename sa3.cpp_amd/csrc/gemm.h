@@ -33,6 +33,22 @@ typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
 enum SrcType { SRC_BF16 = 0, SRC_F16 = 1, SRC_F32 = 2, SRC_Q8 = 3, SRC_Q8T = 4 };
 
+// Per-head q/k preparation in a GEMM epilogue (the DiT's attention inputs, src/dit.h:207-217): the
+// N = parts x dim output columns are parts k = 0 .. parts - 1 of dim columns each. Each 64-column
+// head slice h of part k, taken as C receives it, is RMS-normed with the gain gamma[k] (null:
+// copied as is), rotated by NeoX RoPE over rope_dims dims when rope[k] (table tab [Sx][rope_dims]:
+// the half-pair cosines, then the sines), and stored bf16 to out[k] [B][H][Sx][64] (row m = b Sx +
+// t); the norm's 1/rms goes to rstd[(m H + h) parts + k].
+struct HeadPrep {
+    int parts = 0, Sx = 0, H = 0, dim = 0, rope_dims = 0;
+    float eps = 0.0f;
+    const float* tab = nullptr;
+    bf16* out[5] = {};
+    const float* gamma[5] = {};
+    int rope[5] = {};
+    float* rstd = nullptr;
+};
+
 struct GemmDesc {
     int prec = SA3K_PREC_BF16;   // compute type
     int a_src = SRC_BF16;        // SRC_BF16 or SRC_F32
@@ -97,6 +113,15 @@ struct GemmDesc {
     bf16* sw_g = nullptr;
     int64_t sw_ldg = 0;
     int* sw_done = nullptr;
+    // Per-head q/k preparation (HeadPrep; parts 0: off) where the chosen tiles allow it (bf16
+    // 128 x 256 tiles, no split over K, the staged epilogue, dim a multiple of 256); *hp_done is
+    // set then (else the caller prepares the heads itself). C and every other output unchanged.
+    HeadPrep hp;
+    int* hp_done = nullptr;
+    // 1: C is written only where neither the SwiGLU nor the head preparation epilogue applies (the
+    // callers that keep a bf16 copy Cb for later passes need the f32 C only for their own
+    // separate SwiGLU / head preparation kernels)
+    int c_unfused_only = 0;
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

@@ -12,6 +12,7 @@
 // Rows past M+Mx / N are clamped to a valid row (their results are never stored); K chunks past
 // K2 in the second segment read a zero page, since they feed valid outputs.
 #include "gemm.h"
+#include "headprep.h"
 
 #include <algorithm>
 
@@ -62,6 +63,9 @@ struct DmaParams {
     int64_t sw_half;
     bf16* sw_g; int64_t sw_ldg;
     int* sw_done;   // host-side: set to 1 by the launcher that keeps the pairing
+    HeadPrep hp;    // per-head q/k preparation (GemmDesc::hp), head-prep instantiations only
+    int* hp_done;   // host-side, like sw_done
+    int c_unfused_only;   // host-side (GemmDesc::c_unfused_only)
 };
 
 namespace {
@@ -315,8 +319,8 @@ __device__ __forceinline__ void st_out(bool nt, unsigned* p, unsigned v) {
 // Paired SwiGLU tile (GemmDesc::sw_half): lane l < 32 of a wave holds the val chunk (columns nv ..
 // nv + 3) of its row's epilogue value, lane l + 32 the glu chunk (sw_half + nv ..); the two swap
 // values and each writes two of the four g = bf16(val * glu * sigmoid(glu)), the lower lane columns
-// nv, nv + 1, the upper one nv + 2, nv + 3. Called by all 64 lanes of a wave with one row m.
-__device__ inline void swiglu_pair_store(const DmaParams& p, int64_t m, int64_t nq, bool lo, float4 mine) {
+// nv, nv + 1, the upper one nv + 2, nv + 3 (at gp). Called by all 64 lanes of a wave with one row.
+__device__ inline void swiglu_pair_store(const DmaParams& p, bf16* gp, bool lo, float4 mine) {
     float4 other;
     other.x = __shfl_xor(mine.x, 32);
     other.y = __shfl_xor(mine.y, 32);
@@ -325,8 +329,47 @@ __device__ inline void swiglu_pair_store(const DmaParams& p, int64_t m, int64_t 
     const float4 v = lo ? mine : other, u = lo ? other : mine;
     const float v0 = lo ? v.x : v.z, v1 = lo ? v.y : v.w, u0 = lo ? u.x : u.z, u1 = lo ? u.y : u.w;
     const bf16 o[2] = {(bf16)(v0 * u0 * swiglu_sigmoid(u0)), (bf16)(v1 * u1 * swiglu_sigmoid(u1))};
-    const int64_t col = lo ? nq : nq - p.sw_half + 2;
-    st_out(p.nt_store, reinterpret_cast<unsigned*>(p.sw_g + m * p.sw_ldg + col), __builtin_bit_cast(unsigned, o));
+    st_out(p.nt_store, reinterpret_cast<unsigned*>(gp), __builtin_bit_cast(unsigned, o));
+}
+
+// Main-row, main-column outputs of one staged-epilogue thread, addressed by per-lane pointers at
+// the thread's first row of a pass; a later row adds a wave-uniform row offset (no per-row 64-bit
+// index products, and the output bases and strides do not stay live in scalar registers).
+struct EpiRow {
+    float* C; bf16* Cb; float* U; bf16* Ub;
+};
+__device__ inline EpiRow epi_row(const DmaParams& p, int64_t m, int64_t n) {
+    EpiRow r;
+    r.C = p.C ? p.C + m * p.ldc + n : nullptr;
+    r.Cb = p.Cb ? p.Cb + m * p.ldcb + n : nullptr;
+    r.U = p.U ? p.U + m * p.ldu + n : nullptr;
+    r.Ub = p.Ub ? p.Ub + m * p.ldu + n : nullptr;
+    return r;
+}
+// epilogue_vec4 for a main row and main columns, dr rows past the pointers of r; returns the value
+// before accumulation into C
+__device__ inline float4 epilogue_main4(const DmaParams& p, const EpiRow& r, int dr, float4 a, const EpiCols& k) {
+    float4 x = make_float4(p.alpha * a.x, p.alpha * a.y, p.alpha * a.z, p.alpha * a.w);
+    if (r.U) st_out(p.nt_store, reinterpret_cast<float4*>(r.U + (int64_t)dr * p.ldu), x);
+    if (r.Ub) {
+        bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
+        st_out(p.nt_store, reinterpret_cast<uint2*>(r.Ub + (int64_t)dr * p.ldu), __builtin_bit_cast(uint2, b));
+    }
+    x = epi_scale(p, x, k);
+    const float4 v = x;
+    if (r.C) {
+        float4* c = reinterpret_cast<float4*>(r.C + (int64_t)dr * p.ldc);
+        if (p.accumulate) {
+            const float4 o = *c;
+            x = make_float4(o.x + x.x, o.y + x.y, o.z + x.z, o.w + x.w);
+        }
+        st_out(p.nt_store, c, x);
+    }
+    if (r.Cb) {
+        bf16 b[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
+        st_out(p.nt_store, reinterpret_cast<uint2*>(r.Cb + (int64_t)dr * p.ldcb), __builtin_bit_cast(uint2, b));
+    }
+    return v;
 }
 
 // NW wave64s per workgroup (4 or 8): WMW of them along M, NW/WMW along N, each owning a
@@ -337,7 +380,98 @@ __device__ inline void swiglu_pair_store(const DmaParams& p, int64_t m, int64_t 
 // the loads that pad a tile's DMA count to the bf16 tile's (so the ring's vmcnt accounting holds).
 __device__ __forceinline__ int qswz(int r) { return (r >> 1) & 3; }
 
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0>
+// Output stores of the per-head q/k preparation: row m, output column nq (a multiple of 4 below N)
+// with its 16-lane head group; k the tile's part; tab_row the token's RoPE table row (LDS).
+struct HeadPrepLane {
+    int k;                // part of the tile's columns
+    const float* gamma;   // part k's gain (null: copied)
+    bf16* out;            // part k's head-major output
+    bool rope;
+    float4 g;             // this lane's four gains
+};
+__device__ inline HeadPrepLane head_prep_lane(const DmaParams& p, int64_t n0, int64_t nq) {
+    HeadPrepLane l{(int)(n0 / p.hp.dim), nullptr, nullptr, false, make_float4(0.f, 0.f, 0.f, 0.f)};
+#pragma unroll
+    for (int i = 0; i < 5; ++i)   // selects, no dynamic index into the kernel arguments
+        if (i == l.k) {
+            l.gamma = p.hp.gamma[i];
+            l.out = p.hp.out[i];
+            l.rope = p.hp.rope[i] != 0 && p.hp.gamma[i] != nullptr;
+        }
+    if (l.gamma) l.g = *reinterpret_cast<const float4*>(l.gamma + (nq & (kHeadDim - 1)));
+    return l;
+}
+// Row m = b Sx + t (wave-uniform; host-checked: m H parts < 2^31) of a head-prep tile; outp is this
+// lane's head output at row (b, t) = (0, 0), rsp its rstd at row 0.
+__device__ inline void head_prep_store(const DmaParams& p, const HeadPrepLane& l, int m, int b, int t, int64_t nq,
+                                       float4 y, const float* tab_row, bf16* outp, float* rsp) {
+    const int d0 = (int)(nq & (kHeadDim - 1));
+    if (l.gamma) {
+        float4 cs = make_float4(0.f, 0.f, 0.f, 0.f), sn = cs;
+        if (l.rope) rope_tab4(d0, p.hp.rope_dims, tab_row, cs, sn);
+        const float r = head_norm_rope4(y, l.g, l.rope, d0, p.hp.rope_dims, p.hp.eps, cs, sn);
+        if (d0 == 0) rsp[m * p.hp.H * p.hp.parts] = r;
+    }
+    const bf16 o[4] = {(bf16)y.x, (bf16)y.y, (bf16)y.z, (bf16)y.w};
+    *reinterpret_cast<uint2*>(outp + ((int64_t)b * p.hp.H * p.hp.Sx + t) * kHeadDim) = __builtin_bit_cast(uint2, o);
+}
+
+// The store phase of one staged-epilogue pass over tile rows [rb, rb + ER) (staged in st, EROW
+// floats per row): thread tid stores chunk column cq (output column nq, column factors kq) of tile
+// rows tid / CPR + i NT / CPR. With 256-column tiles a wave holds one row, which the paired SwiGLU
+// and the head preparation rely on.
+template <int BN, int NT, int ER, int EROW, bool HP>
+__device__ inline void staged_store(const DmaParams& p, const float* st, int64_t m0, int64_t n0, int rb, int64_t Mt,
+                                    int z, int tid, int cq, int64_t nq, const EpiCols& kq, bool sw_tile, bool hp_tile,
+                                    const HeadPrepLane& hl, const float* tabs) {
+    constexpr int CPR = BN / 4, RS = NT / CPR, IT = ER * CPR / NT;
+    static_assert(NT % CPR == 0 && (ER * CPR) % NT == 0, "a thread's chunk column must not change between rows");
+    // the thread's first row: with one row per wave, a wave-uniform value
+    const int r0 = CPR == 64 ? __builtin_amdgcn_readfirstlane(tid / CPR) : tid / CPR;
+    const int64_t mf = m0 + rb + r0;
+    const bool main_col = nq < p.N;
+    const EpiRow er = epi_row(p, main_col && mf < p.M ? mf : 0, main_col ? nq : 0);
+    const bool lo = cq < 128;
+    bf16* gp = nullptr;
+    if (BN == 256 && sw_tile) gp = p.sw_g + mf * p.sw_ldg + (lo ? nq : nq - p.sw_half + 2);
+    [[maybe_unused]] int hb = 0, ht = 0;
+    [[maybe_unused]] bf16* outp = nullptr;
+    [[maybe_unused]] float* rsp = nullptr;
+    if constexpr (HP) {
+        if (hp_tile) {
+            hb = (int)mf / p.hp.Sx;
+            ht = (int)mf - hb * p.hp.Sx;
+            const int h = (int)(nq - (int64_t)hl.k * p.hp.dim) >> 6;   // kHeadDim = 64
+            outp = hl.out + (int64_t)h * p.hp.Sx * kHeadDim + (nq & (kHeadDim - 1));
+            rsp = p.hp.rstd + (int64_t)h * p.hp.parts + hl.k;
+        }
+    }
+    for (int it = 0; it < IT; ++it) {
+        const int r = r0 + it * RS, dr = it * RS;
+        const int64_t m = mf + dr;
+        if constexpr (HP) {
+            if (it) {
+                ht += RS;
+                while (ht >= p.hp.Sx) { ht -= p.hp.Sx; ++hb; }
+            }
+        }
+        if (m >= Mt || nq >= p.Nt) continue;
+        const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + cq);
+        if (p.ws) {
+            *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + nq) = a;
+            continue;
+        }
+        const bool main_row = m < p.M;
+        const float4 v = main_row && main_col ? epilogue_main4(p, er, dr, a, kq) : epilogue_vec4(p, m, nq, a, kq);
+        if (BN == 256 && sw_tile && main_row) swiglu_pair_store(p, gp + (int64_t)dr * p.sw_ldg, lo, v);
+        if constexpr (HP)
+            if (hp_tile && main_row) head_prep_store(p, hl, (int)m, hb, ht, nq, v, tabs + (rb + r) * p.hp.rope_dims, outp, rsp);
+    }
+}
+
+// HP: the per-head q/k preparation instantiation (128 x 256 bf16 tiles): the staged epilogue takes
+// the tile in two passes of 64 rows and keeps the tile rows' RoPE table rows in LDS past them.
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false>
 __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     constexpr int NT = NW * 64;
     constexpr int WNW = NW / WMW;
@@ -358,8 +492,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     // writes fall into different banks
     constexpr int EROW = BN + 8;
     constexpr int ER_FIT = (STAGES * STAGE_BYTES) / (EROW * 4);
-    constexpr int ER = (ER_FIT >= BM ? BM : (ER_FIT / WTM) * WTM);
+    constexpr int ER = HP ? WTM : (ER_FIT >= BM ? BM : (ER_FIT / WTM) * WTM);
     static_assert(ER >= WTM, "epilogue staging does not fit");
+    static_assert(!HP || (BF16 && BN == 256 && !KN && BQ == 0 && NT % 64 == 0 &&
+                          (ER * EROW + BM * kHeadDim) * 4 <= STAGES * STAGE_BYTES),
+                  "head preparation needs bf16 256-column tiles and room for the RoPE rows");
     static_assert(NA >= 1 && NB >= 1 && FM >= 1 && FN >= 1, "tile too small");
     static_assert(STAGES >= 2 && STAGES <= 4 && (STAGES - 1) * LPT < 64, "pipeline depth");
     static_assert(!KN || (BF16 && BN % 64 == 0), "a [K][N] B operand needs bf16 and whole 64-column sub-tiles");
@@ -740,6 +877,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     epi_cols_ready(kq);
     float* st = reinterpret_cast<float*>(lds);
     __syncthreads();   // every wave is done reading the last K tile
+    // head preparation (workgroup-uniform: every main-column tile lies inside one part): this
+    // lane's gains, and the tile rows' RoPE table rows staged past the accumulator rows, loaded
+    // ahead of the output stores
+    const bool hp_tile = HP && n0 < p.N;
+    HeadPrepLane hl{};
+    float* tabs = st + ER * EROW;
+    if constexpr (HP) {
+        if (hp_tile) {
+            hl = head_prep_lane(p, n0, nq);
+            if (hl.rope) {
+                const int R4 = p.hp.rope_dims / 4;
+                for (int i = tid; i < BM * R4; i += NT) {
+                    const int r = i / R4, c = i - r * R4;
+                    const int64_t m = min(m0 + r, p.M - 1);
+                    const unsigned t = (unsigned)m % (unsigned)p.hp.Sx;
+                    *reinterpret_cast<float4*>(tabs + r * p.hp.rope_dims + 4 * c) =
+                        *reinterpret_cast<const float4*>(p.hp.tab + t * p.hp.rope_dims + 4 * c);
+                }
+            }
+            asm volatile("" ::"v"(hl.g.x), "v"(hl.g.y), "v"(hl.g.z), "v"(hl.g.w));   // loaded before the stores
+        }
+    }
 #pragma unroll
     for (int rb = 0; rb < BM; rb += ER) {
         if (wm0 >= rb && wm0 < rb + ER) {
@@ -753,18 +912,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        for (int e = tid; e < ER * CPR; e += NT) {
-            const int r = e / CPR;
-            const int64_t m = m0 + rb + r;
-            if (m >= Mt || nq >= p.Nt) continue;
-            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + cq);
-            if (p.ws) {
-                *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + nq) = a;
-                continue;
-            }
-            const float4 v = epilogue_vec4(p, m, nq, a, kq);
-            if (sw_tile && m < p.M) swiglu_pair_store(p, m, nq, cq < 128, v);   // a wave holds one row
-        }
+        staged_store<BN, NT, ER, EROW, HP>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, hp_tile, hl, tabs);
         if (rb + ER < BM) __syncthreads();
     }
 }
@@ -993,18 +1141,8 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        for (int e = tid; e < ER * CPR; e += NT) {
-            const int r = e / CPR;
-            const int64_t m = m0 + rb + r;
-            if (m >= Mt || nq >= p.Nt) continue;
-            const float4 a = *reinterpret_cast<const float4*>(st + r * EROW + cq);
-            if (p.ws) {
-                *reinterpret_cast<float4*>(p.ws + (int64_t)z * Mt * p.Nt + m * p.Nt + nq) = a;
-                continue;
-            }
-            const float4 v = epilogue_vec4(p, m, nq, a, kq);
-            if (sw_tile && m < p.M) swiglu_pair_store(p, m, nq, cq < 128, v);   // a wave holds one row
-        }
+        staged_store<BN, NT, ER, EROW, false>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, false,
+                                              HeadPrepLane{}, nullptr);
         if (rb + ER < BM) __syncthreads();
     }
 }
@@ -1063,9 +1201,28 @@ void settle_swiglu(DmaParams& p, int bn, int splits, bool kn, int bq) {
         return;
     }
     if (p.sw_done) *p.sw_done = 1;
+    if (p.c_unfused_only) p.C = nullptr;
 }
 
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0>
+// Whether the per-head q/k preparation fits this launch: one workgroup per tile (no split over K),
+// the staged epilogue, no extra rows, no accumulation, N = parts x dim with dim = H x 64 a multiple
+// of 256 (so each 256-column tile lies in one part), M = B x Sx, RoPE dims a multiple of 8.
+bool headprep_ok(const DmaParams& p, int splits) {
+    const HeadPrep& h = p.hp;
+    if (h.parts <= 0 || h.parts > 5 || splits != 1 || !p.vec_epi || p.accumulate || p.Mx != 0) return false;
+    if (h.dim % 256 != 0 || h.H * kHeadDim != h.dim || p.N != (int64_t)h.parts * h.dim) return false;
+    if (h.Sx <= 0 || p.M % h.Sx != 0 || p.M * h.H * h.parts >= ((int64_t)1 << 31)) return false;
+    for (int k = 0; k < h.parts; ++k) {
+        if (!h.out[k] || (uintptr_t)h.out[k] % 8 != 0) return false;
+        if (h.gamma[k] && ((uintptr_t)h.gamma[k] % 16 != 0 || !h.rstd)) return false;
+        if (h.gamma[k] && h.rope[k] &&
+            (!h.tab || h.rope_dims <= 0 || h.rope_dims > kHeadDim || h.rope_dims % 8 != 0 || (uintptr_t)h.tab % 16 != 0))
+            return false;
+    }
+    return true;
+}
+
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
@@ -1122,6 +1279,14 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                     ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
     settle_swiglu(p, BN, splits, KN, BQ);
+    if constexpr (HP) {
+        if (!headprep_ok(p, splits)) {   // the caller prepares the heads: the plain instantiation
+            p.hp.parts = 0;
+            return launch_dma<BM, BN, WMW, STAGES, BF16, NW, KN, BQ, false>(ctx, p);
+        }
+        if (p.hp_done) *p.hp_done = 1;
+        if (p.c_unfused_only) p.C = nullptr;
+    }
     if (splits > 1) {
         p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
         if (use_fixup(ctx, (p.M + p.Mx) * p.Nt, tiles)) p.counters = stream_counters(ctx);
@@ -1132,9 +1297,10 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
         static const std::string name = std::string("gemm_dma<") + std::to_string(BM) + "," + std::to_string(BN) + "," +
                                         std::to_string(WMW) + "," + std::to_string(STAGES) +
                                         (NW != 4 ? ",w" + std::to_string(NW) : std::string()) + (KN ? ",kn" : "") +
-                                        (BQ == 1 ? ",f16b" : BQ == 2 ? ",q8b" : "") + (BF16 ? ",bf16>" : ",f32>");
+                                        (BQ == 1 ? ",f16b" : BQ == 2 ? ",q8b" : "") + (HP ? ",hp" : "") +
+                                        (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ>, g,
+        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ, HP>, g,
                  dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
@@ -1248,6 +1414,9 @@ void dispatch_dma_dq(sa3k_ctx* ctx, const DmaParams& p) {
 template <bool BF16>
 void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if constexpr (BF16) {
+        // per-head q/k preparation: 128 x 256 tiles, the default for the attention projections
+        // (falls back to the plain instantiation where headprep_ok refuses)
+        if (p.hp.parts > 0 && p.bq == 0 && !p.b_kn) return launch_dma<128, 256, 2, 3, true, 8, false, 0, true>(ctx, p);
         if (p.bq == 1) return dispatch_dma_dq<1>(ctx, p);
         if (p.bq == 2) return dispatch_dma_dq<2>(ctx, p);
         if (p.b_kn) return dispatch_dma_kn(ctx, p);
@@ -1345,6 +1514,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.Bs = d.Bs; p.ldbs = d.ldbs;
     p.bs_bytes = 0;
     p.sw_half = d.sw_half; p.sw_g = d.sw_g; p.sw_ldg = d.sw_ldg; p.sw_done = d.sw_done;
+    p.hp = d.hp; p.hp_done = d.hp_done; p.c_unfused_only = d.c_unfused_only;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

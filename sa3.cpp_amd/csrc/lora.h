@@ -58,9 +58,18 @@ int64_t lin_stack_ld(const LinStack* st);   // row stride of Y (n out)
 const float* lin_stack_y(const LinStack* st);   // Y (fixed for the stack's lifetime)
 void lin_stack_free(LinStack* st);
 // sa3k_lin_forward of a bf16 FFN up-projection (Y = [val | glu], bf16 X) that also writes the
-// SwiGLU g = bf16(val * silu(glu)) [N][out / 2] from its GEMM epilogue when the option epi_fuse is
-// on and the chosen kernel allows it. Returns whether it did; if not, the caller computes g from Y.
-bool lin_forward_swiglu(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, const float* bias, float* Y, bf16* g);
+// SwiGLU g = bf16(val * silu(glu)) [N][out / 2] from its GEMM epilogue when the option epi_fuse has
+// bit 0 set and the chosen kernel allows it, and returns whether it did (if not, the caller computes
+// g from Y). Yb (optional): a bf16 copy of Y, with Y then written only where g is not fused.
+bool lin_forward_swiglu(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, const float* bias, float* Y, bf16* Yb,
+                        bf16* g);
+// sa3k_lin_forward of an attention projection (no bias, bf16 X) that also prepares its heads (the
+// per-head q/k RMS norm, RoPE and head-major bf16 outputs of HeadPrep) from its GEMM epilogue when
+// bit 1 of the option epi_fuse is set and the chosen kernel allows it, and returns whether it did
+// (if not, the caller prepares them from Y). Yb (optional): a bf16 copy of Y, with Y then written
+// only where the heads are not prepared in the epilogue.
+bool lin_forward_headprep(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, float* Y, bf16* Yb,
+                          const HeadPrep& hp);
 // The B operand of X W^T (forward orientation) in g's precision: the bf16 working copy when the
 // weight has one and the precision is bf16, else the stored elements or Q8_0 planes, which the
 // GEMM decodes on their way into LDS.

@@ -860,11 +860,19 @@ WOp weight_operand(const sa3k_weight* W, bool bf, bool transposed) {
     return WOp{src_of_weight(W->type, false), W->w, W->ws, W->in, W->in / 32};
 }
 
-// sw_g: also write the FFN SwiGLU g = bf16(val * silu(glu)) of Y = [val | glu] from the GEMM
-// epilogue where the chosen kernel allows it (*sw_done set to 1 then)
+// Epilogue work of the main product beyond Y: sw_g, the FFN SwiGLU g = bf16(val * silu(glu)) of Y =
+// [val | glu], or hp, the attention heads prepared from Y, where the chosen kernel allows it (*done
+// set to 1 then); Yb, a bf16 copy of Y, with Y itself written only where that work is not done.
+struct LinEpi {
+    bf16* sw_g = nullptr;
+    const HeadPrep* hp = nullptr;
+    bf16* Yb = nullptr;
+    int* done = nullptr;
+};
+
 template <class CT>
 void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* bias, float* Y,
-                   bf16* sw_g = nullptr, int* sw_done = nullptr) {
+                   const LinEpi* epi = nullptr) {
     SA3K_REQUIRE(L->ext == 0, "a linear of a stacked product runs its forward through the stack");
     const sa3k_weight* W = L->W;
     const bool bf = L->prec == SA3K_PREC_BF16;
@@ -913,7 +921,13 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
     g.C = Y; g.ldc = W->out;
     g.ldu = W->out;
     if (L->dora) { if (bf) g.Ub = static_cast<bf16*>(L->U); else g.U = static_cast<float*>(L->U); }
-    if (sw_g && W->out % 2 == 0) { g.sw_half = W->out / 2; g.sw_g = sw_g; g.sw_ldg = W->out / 2; g.sw_done = sw_done; }
+    if (epi) {
+        if (epi->sw_g && W->out % 2 == 0) {
+            g.sw_half = W->out / 2; g.sw_g = epi->sw_g; g.sw_ldg = W->out / 2; g.sw_done = epi->done;
+        }
+        if (epi->hp) { g.hp = *epi->hp; g.hp_done = epi->done; }
+        if (epi->Yb) { g.Cb = epi->Yb; g.ldcb = W->out; g.c_unfused_only = 1; }
+    }
     gemm_run(ctx, g, scope(ctx, L, "lin_fwd_main"));
     if (side) side_join_unless_deferred(ctx);
     L->saved_tokens = N;
@@ -2246,15 +2260,36 @@ SA3K_API int sa3k_lin_forward(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void
 }  // extern "C"
 
 // sa3k_lin_forward of the FFN up-projection (bf16 activations) that also writes g = bf16(val *
-// silu(glu)) of Y = [val | glu] from its GEMM epilogue when the option epi_fuse is on and the
-// chosen kernel allows it; returns whether it did (else the caller applies SwiGLU to Y itself)
+// silu(glu)) of Y = [val | glu] from its GEMM epilogue when bit 0 of the option epi_fuse is set and
+// the chosen kernel allows it; returns whether it did (else the caller applies SwiGLU to Y itself)
 bool sa3k::lin_forward_swiglu(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, const float* bias, float* Y,
-                              bf16* g) {
+                              bf16* Yb, bf16* g) {
     SA3K_REQUIRE(L && X && Y && g, "null pointer");
     SA3K_REQUIRE(N > 0 && N <= L->max_tokens, "token count exceeds the linear's max_tokens");
     SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && L->ext == 0, "the fused SwiGLU needs a bf16 linear outside a stack");
     int done = 0;
-    lin_forward_t<bf16>(ctx, L, SRC_BF16, X, N, bias, Y, ctx->epi_fuse ? g : nullptr, &done);
+    LinEpi e;
+    e.sw_g = (ctx->epi_fuse & 1) ? g : nullptr;
+    e.Yb = Yb;
+    e.done = &done;
+    lin_forward_t<bf16>(ctx, L, SRC_BF16, X, N, bias, Y, &e);
+    return done != 0;
+}
+
+// sa3k_lin_forward of an attention projection (bf16 activations) that also prepares the heads
+// (HeadPrep) from its GEMM epilogue when bit 1 of the option epi_fuse is set and the chosen kernel
+// allows it; returns whether it did (else the caller prepares them from Y)
+bool sa3k::lin_forward_headprep(sa3k_ctx* ctx, sa3k_lin* L, const bf16* X, int64_t N, float* Y, bf16* Yb,
+                                const HeadPrep& hp) {
+    SA3K_REQUIRE(L && X && Y, "null pointer");
+    SA3K_REQUIRE(N > 0 && N <= L->max_tokens, "token count exceeds the linear's max_tokens");
+    SA3K_REQUIRE(L->prec == SA3K_PREC_BF16 && L->ext == 0, "the head preparation needs a bf16 linear outside a stack");
+    int done = 0;
+    LinEpi e;
+    e.hp = (ctx->epi_fuse & 2) ? &hp : nullptr;
+    e.Yb = Yb;
+    e.done = &done;
+    lin_forward_t<bf16>(ctx, L, SRC_BF16, X, N, nullptr, Y, &e);
     return done != 0;
 }
 

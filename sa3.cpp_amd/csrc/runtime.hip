@@ -64,7 +64,8 @@ const OptionDef kOptions[] = {
     {"rank_cols", &sa3k_ctx::rank_cols, false},    {"merge_kn", &sa3k_ctx::merge_kn, true},
     {"tn_fuse", &sa3k_ctx::tn_fuse, false},        {"kv_stack", &sa3k_ctx::kv_stack, true},
     {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
-    {"prep_side", &sa3k_ctx::prep_side, true},     {"epi_fuse", &sa3k_ctx::epi_fuse, true},
+    {"prep_side", &sa3k_ctx::prep_side, true},     {"epi_fuse", &sa3k_ctx::epi_fuse, false},
+    {"act_bf16", &sa3k_ctx::act_bf16, false},
 };
 constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
 

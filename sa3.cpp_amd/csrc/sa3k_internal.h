@@ -100,7 +100,8 @@ struct sa3k_ctx {
     int attn_fwd32 = 1;                   // attention forward on 32x32x16 MFMA blocks, 32 queries per wave
     int prep_side = 1;                    // a DiT's bf16 group refresh on the second stream beside the f32 heads'
     int head_f32 = 1;                     // a DiT's head / tail linears on f32 MFMA (f32 / f16 bases)
-    int epi_fuse = 1;                     // FFN SwiGLU in the up-projection's GEMM epilogue where its tiles allow
+    int epi_fuse = 3;                     // in GEMM epilogues where the tiles allow: 1 the FFN SwiGLU, 2 q/k head prep
+    int act_bf16 = 1;                     // block backward reads bf16 copies: 1 of the FFN up output, 2 of qkv / qf
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,
                                           // one half per stream, zero between launches
     bool capturing = false;               // a HIP graph capture is recording the stream

@@ -177,10 +177,12 @@ def test_block_full_size_properties(ctx):
         assert np.array_equal(r3["out"], r1["out"])
         for k in ("dx", "dctx", "dgcond", "g"):
             assert np.array_equal(r3[k], 2 * r1[k]), f"{k} not homogeneous in dout"
-        # batch independence: sample 1 alone gives the rows of sample 1 inside the batch (up to the
-        # f32 summation order of a different split-K choice for half the rows)
+        # batch independence: sample 1 alone gives the rows of sample 1 inside the batch, up to the
+        # f32 summation order of different tile and split-K choices at 1088 rows, which the block's
+        # bf16 roundings of its activations turn into one-ulp bf16 flips (measured 1.06e-3 normwise;
+        # mixing the samples would differ at order 1)
         r4 = run_full(ctx, blk, c, params, x[1:], cx[1:], gc[1:], None)
-        assert rel_err(r4["out"][0] - x[1], r1["out"][1] - x[1]) < 1e-3
+        assert rel_err(r4["out"][0] - x[1], r1["out"][1] - x[1]) < 2e-3
         # window locality: move token j of sample 0; rows farther than window/2 are unchanged
         j = 600
         xp = x.copy()

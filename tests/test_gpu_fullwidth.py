@@ -102,36 +102,85 @@ def test_dit_depth1_full_width_vs_oracle(ctx, local_dim):
 
 
 @pytest.mark.parametrize("S", [64 + 960, 64 + 1024])
-def test_block_swiglu_epilogue_bitwise(ctx, S):
-    """The FFN SwiGLU written by the up-projection's GEMM epilogue (option epi_fuse) against the
-    separate SwiGLU kernel, at the benchmark's width: 2 x 1024 tokens take the 128 x 256 DMA tiles
-    without a split over K, 2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles. Both orders
-    of evaluation are the same per element, so every output and gradient agrees bit for bit; the
-    profile shows the SwiGLU kernel only in the backward when fused."""
+def test_block_epilogue_fusions_bitwise(ctx, S):
+    """The GEMM-epilogue fusions (option epi_fuse) against their separate kernels at the benchmark's
+    width: the FFN SwiGLU from the up-projection's epilogue (bit 0) and the per-head q/k RMS norm,
+    RoPE and head-major bf16 outputs from the QKV and cross-query projections' epilogues (bit 1).
+    2 x 1024 tokens take the 128 x 256 DMA tiles without a split over K for every fused product,
+    2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles for the up-projection. Each fused
+    path evaluates the same expressions per element, so every output and gradient agrees bit for
+    bit; the profile shows which separate kernels ran (SwiGLU: forward + backward unfused, backward
+    only fused; head prep: self + cross query + context K/V unfused, context K/V only fused)."""
     assert_shipped_options(ctx)
     B, Ctx = 2, 128
-    print(f"swiglu epilogue: B {B}, S {S}, Ctx {Ctx}", flush=True)
+    print(f"epilogue fusions: B {B}, S {S}, Ctx {Ctx}", flush=True)
     cfg, w, x, cx, gc = bb.random_block(61, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
                                         alpha=32.0, dora=True, window=256, w_sd=0.02, b_sd=0.01)
     dout = rng(62).normal(0, 1e-2, x.shape).astype(np.float32)
     gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
-    res, swiglu_launches = {}, {}
+    res, launches = {}, {}
     try:
-        for fuse in (1, 0):
+        for fuse in (3, 0, 1, 2):
             ctx.set_option("epi_fuse", fuse)
             ctx.profile(True)
             ctx.profile_reset()
             res[fuse] = run_gpu(ctx, gb, x, cx, gc, dout)
             rep = ctx.profile_report()
             ctx.profile(False)
-            swiglu_launches[fuse] = sum(v[0] for k, v in rep.items() if k.startswith("blk_swiglu"))
+            launches[fuse] = tuple(sum(v[0] for k, v in rep.items() if k.startswith(n))
+                                   for n in ("blk_swiglu", "blk_prep_fwd"))
     finally:
         ctx.profile(False)
         ctx.set_options(ctx.defaults)
         gb.destroy()
-    assert swiglu_launches == {1: 1, 0: 2}, swiglu_launches
-    for k in ("out", "dx", "dctx", "dgcond"):
-        assert np.array_equal(res[1][k], res[0][k]), k
-    for k in ("dA", "dB", "dm"):
-        for t in range(7):
-            assert np.array_equal(res[1][k][t], res[0][k][t]), f"{k}[{t}]"
+    assert launches == {3: (1, 1), 0: (2, 3), 1: (1, 3), 2: (2, 1)}, launches
+    for fuse in (0, 1, 2):
+        for k in ("out", "dx", "dctx", "dgcond"):
+            assert np.array_equal(res[3][k], res[fuse][k]), (fuse, k)
+        for k in ("dA", "dB", "dm"):
+            for t in range(7):
+                assert np.array_equal(res[3][k][t], res[fuse][k][t]), (fuse, f"{k}[{t}]")
+
+
+@pytest.mark.parametrize("act_bf16", [1, 3])
+def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
+    """The fused epilogues against the oracle directly: the full-width block at 2 x 136 tokens with
+    the split over K and the small-grid tile switched off, so that the up-projection, QKV and
+    cross-query products take unsplit 128 x 256 tiles and the fusions apply (shipped, these small
+    grids take split or 64 x 128 tiles and the separate kernels, which the other full-width tests
+    cover); the backward reading the bf16 copy of the FFN up-projection's output (act_bf16 1, the
+    default) and also those of the QKV and cross-query outputs (3)."""
+    B, S, Ctx = 2, 64 + 72, 128
+    cfg, w, x, cx, gc = bb.random_block(71, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
+                                        alpha=32.0, dora=True, window=256, w_sd=0.02, b_sd=0.01)
+    w["W"] = [to_f16_grid(W) for W in w["W"]]
+    w["bnsq"] = [((W.astype(np.float64) ** 2).sum(1) + W.shape[1] * 1e-12).astype(np.float32) for W in w["W"]]
+    dout = rng(72).normal(0, 1e-2, x.shape).astype(np.float32)
+    gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
+    try:
+        ctx.set_option("gemm_split", 0)
+        ctx.set_option("gemm_small", 0)
+        ctx.set_option("act_bf16", act_bf16)
+        ctx.profile(True)
+        ctx.profile_reset()
+        got = run_gpu(ctx, gb, x, cx, gc, dout)
+        rep = ctx.profile_report()
+    finally:
+        ctx.profile(False)
+        ctx.set_options(ctx.defaults)
+        gb.destroy()
+    n = tuple(sum(v[0] for k, v in rep.items() if k.startswith(p)) for p in ("blk_swiglu", "blk_prep_fwd"))
+    assert n == (1, 1), n   # SwiGLU backward and the context K/V prep only
+    ref_out = bb.block_fwd(cfg, w, x, cx, gc)
+    ref = bb.block_bwd(cfg, w, x, cx, gc, dout)
+    worst = []
+    check(got["out"] - x, ref_out - x, "out - x", worst)
+    check(got["dx"] - dout, ref["dx"] - dout, "dx - dout", worst)
+    check(got["dctx"], ref["dctx"], "dcontext", worst)
+    check(got["dgcond"], ref["dgcond"], "dgcond", worst)
+    for t in range(7):
+        check(got["dA"][t], ref["dA"][t], f"dA[{t}]", worst)
+        check(got["dB"][t], ref["dB"][t], f"dB[{t}]", worst)
+        check(got["dm"][t], ref["dm"][t], f"dm[{t}]", worst)
+    e, c, what = max(worst)
+    print(f"worst normwise error {e:.3e} ({what}), lowest cosine {min(x[1] for x in worst):.7f}")
