@@ -635,7 +635,7 @@ def gemm_roofline(prof, steps):
     """Roofline of the GEMM kernel instantiation with the largest total time. The library counts
     each launch's algorithmic flops, 2 (M + extra rows) N (K + rank extension), at launch time, so
     achieved = counted flops / measured time = flops per launch / average launch duration."""
-    cands = {k: v for k, v in prof.items() if k.startswith(("gemm_dma<", "gemm_decode<")) and v[2] > 0}
+    cands = {k: v for k, v in prof.items() if k.startswith(("gemm_dma<", "gemm_big<", "gemm_decode<")) and v[2] > 0}
     k = max(cands, key=lambda n: cands[n][1])
     cnt, ms, work = cands[k]
     peak = BF16_PEAK_TFLOPS if k.endswith("bf16>") else FP32_MFMA_PEAK_TFLOPS

@@ -160,6 +160,9 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 attention inputs come out of the QKV and cross-query projections' epilogues; each
  *                 where the chosen tiles allow it (no split over K), else by its own kernel
  *                 (default 3)
+ *   "gemm_prio"   1: the DMA GEMMs raise their waves' priority over the MFMA clusters of the K
+ *                 loop, so a wave that has its operands keeps issuing while the others read
+ *                 (default 1)
  *   "act_bf16"    bit 0: a block's backward reads a bf16 copy of the FFN up-projection's output
  *                 (written by its epilogue) instead of the f32 output, which then is forward
  *                 scratch; bit 1: likewise for the QKV and cross-query outputs (default 1). It

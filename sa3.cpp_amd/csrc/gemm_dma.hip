@@ -66,6 +66,7 @@ struct DmaParams {
     HeadPrep hp;    // per-head q/k preparation (GemmDesc::hp), head-prep instantiations only
     int* hp_done;   // host-side, like sw_done
     int c_unfused_only;   // host-side (GemmDesc::c_unfused_only)
+    int prio;             // raise the wave priority over the MFMA clusters of the K loop
 };
 
 namespace {
@@ -743,6 +744,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             // keep the reads ahead of the MFMAs (the LDS counter tracks at most 15 reads, so the
             // first half's MFMAs can start with the second half's reads still outstanding)
             __builtin_amdgcn_sched_barrier(0);
+            if (p.prio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
@@ -752,6 +754,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], bfr[ks][j], acc[i][j], 0, 0, 0);
                 if (ks == 1) __builtin_amdgcn_sched_barrier(0);
             }
+            if (p.prio) __builtin_amdgcn_s_setprio(0);
         } else {
             // 16x16x4 f32: lane l holds row l%16; a 16-byte chunk feeds four K steps
             const int r = lane & 15, g = lane >> 4;
@@ -1094,6 +1097,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
         load(0, 0);
         load(1, 1);
         __builtin_amdgcn_sched_barrier(0);
+        if (p.prio) __builtin_amdgcn_s_setprio(1);
         mma(0);
         load(2, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -1102,6 +1106,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
         __builtin_amdgcn_sched_barrier(0);
         mma(0);
         mma(1);
+        if (p.prio) __builtin_amdgcn_s_setprio(0);
     };
 
     if (T > 0) issue(IC<0>{}, 0);
@@ -1515,6 +1520,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.bs_bytes = 0;
     p.sw_half = d.sw_half; p.sw_g = d.sw_g; p.sw_ldg = d.sw_ldg; p.sw_done = d.sw_done;
     p.hp = d.hp; p.hp_done = d.hp_done; p.c_unfused_only = d.c_unfused_only;
+    p.prio = ctx->gemm_prio;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);
 }

@@ -65,7 +65,7 @@ const OptionDef kOptions[] = {
     {"tn_fuse", &sa3k_ctx::tn_fuse, false},        {"kv_stack", &sa3k_ctx::kv_stack, true},
     {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
     {"prep_side", &sa3k_ctx::prep_side, true},     {"epi_fuse", &sa3k_ctx::epi_fuse, false},
-    {"act_bf16", &sa3k_ctx::act_bf16, false},
+    {"act_bf16", &sa3k_ctx::act_bf16, false},     {"gemm_prio", &sa3k_ctx::gemm_prio, true},
 };
 constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
 
