@@ -137,6 +137,11 @@ bool gemm_skinny_ok(const sa3k_ctx* ctx, const GemmDesc& d);
 void gemm_run_skinny(sa3k_ctx* ctx, const GemmDesc& d);
 // split-K partial-sum workspace owned by the context (grows on demand)
 float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes);
+// The most f32 partial sums a split plan of the dispatch's own choosing writes: it splits only
+// while splits x tiles <= the launch's resident workgroup slots, and every tile family keeps slots x
+// tile area <= 2^24 (512 x 128 x 128, 256 x 128 x 256, 256 x 256 x 256; checked at compile time
+// per instantiation). Forced splits (option gemm_splits) or slot counts (gemm_wg_per_cu) may exceed it.
+constexpr int64_t kMaxSplitFloats = (int64_t)1 << 24;
 // Look up this device's copy of the allocation-free entry point's scratch array (once per
 // device, with the context's device current) and keep its address in the context.
 void gemm_noalloc_setup(sa3k_ctx* ctx);

@@ -43,9 +43,10 @@ struct KParams {
 // the code object itself carries (no hipMalloc at any call). 64 MiB covers every split plan the
 // dispatch chooses by itself: a GEMM splits only while its tiles fill fewer than the chip's
 // resident slots (512 for 128 x 128 tiles, 256 for 128 x 256 and 256 x 256 ones), so splits x
-// tiles x tile floats <= 256 x 65536 = 2^24. Every GPU that loads the library holds its own copy
-// until the process ends.
+// tiles x tile floats <= 256 x 65536 = 2^24 (kMaxSplitFloats; the launchers check both factors).
+// Every GPU that loads the library holds its own copy until the process ends.
 constexpr size_t kNoAllocScratchFloats = (size_t)1 << 24;
+static_assert((int64_t)kNoAllocScratchFloats >= kMaxSplitFloats, "the scratch must hold every automatic split plan");
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 namespace {

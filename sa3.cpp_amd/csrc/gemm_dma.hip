@@ -1192,6 +1192,39 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_splitk_reduce(DmaParams p, 
     epilogue_elem(p, m, n, s);
 }
 
+// The split over K of a launch of `tiles` tiles with `slots` resident workgroups and KT K tiles,
+// one rule for the launchers and for dma_rounds: split only when there are K tiles to spare (below
+// 16, e.g. the 256-token context projection with K = 768, the split partials and their reduction
+// launch cost more than the idle slots: 256 x 4608 x 768 measured 10.6 us unsplit, 16.9 us in 3
+// splits), into at most 16 and at most slots / tiles parts, so splits x tiles <= slots; option
+// gemm_splits forces a count. Returns the splits actually used (every split gets a whole share).
+int split_count(const sa3k_ctx* ctx, int64_t tiles, int64_t slots, int KT, int* kps) {
+    int splits = 1;
+    if (ctx->gemm_split && tiles < slots && KT >= 16)
+        splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
+    if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
+    const int per = std::max(1, (KT + splits - 1) / splits);
+    if (kps) *kps = per;
+    splits = std::max(1, (KT + per - 1) / per);
+    // the bound the allocation-free entry point's scratch is sized by (kMaxSplitFloats)
+    SA3K_REQUIRE(splits == 1 || ctx->gemm_splits > 0 || (int64_t)splits * tiles <= slots,
+                 "GEMM split plan exceeds the resident slots");
+    return splits;
+}
+
+// Whether a bf16 product of Mt x Nt x K takes the 256 x 256 tiles (one workgroup per CU): where
+// they fill the chip about as evenly as 128 x 128 tiles (two per CU) do, or with option gemm_big 3
+// for K >= 8192 (they need no split over K there, or fewer), always with gemm_big 2. Measured on
+// MI355X at 2176 rows: FFN up-projection 2176 x 12288 x 1536 107 vs 111 us, 2176 x 6144 x 1536 52
+// vs 56 us, 8192^3 877 vs 1057 us; the 2176 x 7680 QKV projection (270 tiles) 98 vs 62 us.
+bool use_big_tiles(const sa3k_ctx* ctx, int64_t Mt, int64_t Nt, int64_t K) {
+    if (ctx->gemm_big == 0 || Mt <= 32 || Nt <= 64) return false;
+    const int64_t t256 = ceil_div(Mt, 256) * ceil_div(Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
+    const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
+    const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
+    return ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && K >= 8192);
+}
+
 // Keep the paired SwiGLU epilogue only where the launch computes each tile's final values in one
 // workgroup and stores them through the staged epilogue: 256-column tiles, no split over K, a
 // [N][K] bf16 B, N = 2 sw_half a multiple of 256 (every tile below N is paired), no extra rows and
@@ -1232,19 +1265,13 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
     const int KT = (int)(p.K / (BF16 ? 64 : 32));
-    int splits = 1;
     // resident workgroups per CU: as many as the 160 KiB of LDS hold (or the context's override)
     constexpr int kLdsBytes = STAGES * (BM + BN) * kRow + 64;
     const int wg_per_cu = ctx->gemm_wg_per_cu > 0 ? ctx->gemm_wg_per_cu : std::max(1, (160 * 1024) / kLdsBytes);
     const int64_t slots = (int64_t)256 * wg_per_cu;
-    // split K only when there are K tiles to spare: below 16 (the 256-token context projection,
-    // K = 768) the split partials and their reduction launch cost more than the idle slots (measured
-    // on MI355X: 256 x 4608 x 768 10.6 us unsplit, 16.9 us in 3 splits)
-    if (ctx->gemm_split && tiles < slots && KT >= 16)
-        splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
-    if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
-    p.kps = std::max(1, (KT + splits - 1) / splits);
-    splits = std::max(1, (KT + p.kps - 1) / p.kps);
+    static_assert((int64_t)256 * std::max(1, (160 * 1024) / kLdsBytes) * BM * BN <= kMaxSplitFloats,
+                  "split partials of this tile family exceed kMaxSplitFloats");
+    const int splits = split_count(ctx, tiles, slots, KT, &p.kps);
     p.ws = nullptr;
     p.counters = nullptr;
     {
@@ -1350,13 +1377,9 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
     const int KT = (int)(p.K / 64);
-    int splits = 1;
     const int64_t slots = 256;   // one workgroup per CU (128 KiB of LDS)
-    if (ctx->gemm_split && tiles < slots && KT >= 16)
-        splits = (int)std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
-    if (ctx->gemm_splits > 0 && ctx->gemm_split) splits = std::min(ctx->gemm_splits, std::max(1, KT));
-    p.kps = std::max(1, (KT + splits - 1) / splits);
-    splits = std::max(1, (KT + p.kps - 1) / p.kps);
+    static_assert((int64_t)256 * 256 * 256 <= kMaxSplitFloats, "256 x 256 split partials exceed kMaxSplitFloats");
+    const int splits = split_count(ctx, tiles, slots, KT, &p.kps);
     p.ws = nullptr;
     p.counters = nullptr;
     auto extent = [&](int64_t rows, int64_t ld) -> uint32_t { return rows > 0 ? (uint32_t)(((rows - 1) * ld + p.K) * 2) : 0u; };
@@ -1388,13 +1411,7 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
 // [K][N] B operands (bf16): the tiles of the default dispatch that have whole 64-column sub-tiles
 void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
     const int64_t Mt = p.M + p.Mx;
-    if (ctx->gemm_big != 0 && Mt > 32 && p.N > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
-        const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.N, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
-        const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
-        const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && p.K >= 8192))
-            return launch_big(ctx, p);
-    }
+    if (use_big_tiles(ctx, Mt, p.N, p.K) && big_ok(ctx, p) && vec_epi_ok(p)) return launch_big(ctx, p);
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, true, 4, true>(ctx, p);
     if (p.N <= 64) return launch_dma<128, 64, 4, 4, true, 4, true>(ctx, p);
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
@@ -1425,18 +1442,7 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
         if (p.bq == 1) return dispatch_dma_dq<1>(ctx, p);
         if (p.bq == 2) return dispatch_dma_dq<2>(ctx, p);
         if (p.b_kn) return dispatch_dma_kn(ctx, p);
-        if (ctx->gemm_big != 0 && p.M + p.Mx > 32 && p.Nt > 64 && big_ok(ctx, p) && vec_epi_ok(p)) {
-            // 256 x 256 tiles (one per CU) where they fill the chip about as evenly as 128 x 128 tiles
-            // (two per CU) do and need no split over K; measured on MI355X at 2176 rows: FFN
-            // up-projection 2176 x 12288 x 1536 107 vs 111 us, 2176 x 6144 x 1536 52 vs 56 us,
-            // 8192^3 877 vs 1057 us; the 2176 x 7680 QKV projection (270 tiles) 98 vs 62 us.
-            const int64_t Mt = p.M + p.Mx;
-            const int64_t t256 = ceil_div(Mt, 256) * ceil_div(p.Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(p.Nt, 128);
-            const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
-            const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-            if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && p.K >= 8192))
-                return launch_big(ctx, p);
-        }
+        if (use_big_tiles(ctx, p.M + p.Mx, p.Nt, p.K) && big_ok(ctx, p) && vec_epi_ok(p)) return launch_big(ctx, p);
     }
     const int64_t Mt = p.M + p.Mx;
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, BF16>(ctx, p);
@@ -1473,26 +1479,16 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
 // Rounds of resident workgroups a bf16 DMA GEMM of Mt x Nt x K takes under the dispatch above
 // (the tile and split choices, ignoring operand alignment): splits x tiles / slots, rounded up.
 int64_t dma_rounds(const sa3k_ctx* ctx, int64_t Mt, int64_t Nt, int64_t K) {
-    const int64_t KT = K / 64;
-    auto rounds = [&](int64_t tiles, int64_t slots, bool may_split) {
-        int64_t splits = 1;
-        if (may_split && ctx->gemm_split && tiles < slots && KT >= 16)
-            splits = std::min<int64_t>({(int64_t)16, KT / 4, std::max<int64_t>(1, slots / tiles)});
-        splits = std::max<int64_t>(1, ceil_div(KT, std::max<int64_t>(1, ceil_div(KT, splits))));
-        return ceil_div(tiles * splits, slots);
+    const int KT = (int)(K / 64);
+    auto rounds = [&](int64_t tiles, int64_t slots) {
+        return ceil_div(tiles * split_count(ctx, tiles, slots, KT, nullptr), slots);
     };
-    if (ctx->gemm_big != 0 && Mt > 32 && Nt > 64) {
-        const int64_t t256 = ceil_div(Mt, 256) * ceil_div(Nt, 256), t128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
-        const double q256 = (double)t256 / (double)(ceil_div(t256, 256) * 256);
-        const double q128 = (double)t128 / (double)(ceil_div(t128, 512) * 512);
-        if (ctx->gemm_big == 2 || (t256 >= 200 && q256 >= q128 - 0.02) || (ctx->gemm_big == 3 && K >= 8192))
-            return rounds(t256, 256, true);
-    }
+    if (use_big_tiles(ctx, Mt, Nt, K)) return rounds(ceil_div(Mt, 256) * ceil_div(Nt, 256), 256);
     if (Mt <= 32 || Nt <= 64) return 1;
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
-    if (tiles128 < 384 && K < 4096 && ctx->gemm_small == 2) return rounds(ceil_div(Mt, 64) * ceil_div(Nt, 128), 512, true);
-    if (ctx->gemm_cfg == 1) return rounds(tiles128, 512, true);
-    return rounds(ceil_div(Mt, 128) * ceil_div(Nt, 256), 256, true);
+    if (tiles128 < 384 && K < 4096 && ctx->gemm_small == 2) return rounds(ceil_div(Mt, 64) * ceil_div(Nt, 128), 512);
+    if (ctx->gemm_cfg == 1) return rounds(tiles128, 512);
+    return rounds(ceil_div(Mt, 128) * ceil_div(Nt, 256), 256);
 }
 
 }  // namespace
