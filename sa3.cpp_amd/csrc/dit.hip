@@ -821,23 +821,28 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     join_group(ctx, d);   // every product from here on reads a member of the grouped refresh
     if (d->kvs) lin_stack_forward(ctx, d->kvs, d->context, NC);   // every block's context K/V
     // the inpaint conditioning, zero-padded to local.0's kp input columns; every block's local MLP
-    // depends on it alone, so all of them run up front on the second stream and block l waits for
-    // its own MLP only
+    // depends on it alone, so they run on the second stream and block l waits for its own MLP only:
+    // all of them up front, or under recompute, where every block joins the second stream at its
+    // end, one block ahead (block l's MLP beside block l - 1)
     const bool local_side = d->local_in && side_usable(ctx);
-    if (d->local_in) {
-        launch(ctx, "dit_local", pad_cols_kernel<float>, dim3(nblk(NT * d->kp)), d->local_in, NT,
-               (int64_t)c.local_dim, (int64_t)d->kp, d->lc);
+    auto local_ahead = [&](int l0, int l1) {
         if (local_side) side_fork(ctx);
         OnSide os(ctx, local_side);
-        for (int l = 0; l < c.depth; ++l) {
+        for (int l = l0; l < l1; ++l) {
             local_fwd(ctx, d, l);
             if (local_side) SA3K_HIP(hipEventRecord(d->lev[l], ctx->side_stream));
         }
+    };
+    if (d->local_in) {
+        launch(ctx, "dit_local", pad_cols_kernel<float>, dim3(nblk(NT * d->kp)), d->local_in, NT,
+               (int64_t)c.local_dim, (int64_t)d->kp, d->lc);
+        local_ahead(0, d->tr.recompute ? 1 : c.depth);
     }
     // blocks
     for (int l = 0; l < c.depth; ++l) {
         bind_kv(d, d->ws[d->tr.recompute ? 0 : l], l);
         bind_local(d, d->ws[d->tr.recompute ? 0 : l], l);
+        if (d->local_in && d->tr.recompute && l + 1 < c.depth) local_ahead(l + 1, l + 2);
         if (local_side) SA3K_HIP(hipStreamWaitEvent(ctx->main_stream, d->lev[l], 0));
         block_forward(ctx, d->blocks[l], d->ws[d->tr.recompute ? 0 : l], d->xs[l], d->context, d->gcond, d->xs[l + 1]);
         if (d->tr.recompute) side_join_since(ctx, forks0);
@@ -880,12 +885,24 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
     fill(ctx, d->dgcond, 6 * B * D, 0.0f);
     float* dcur = d->dxa;
     float* dnext = d->dxb;
+    // a block's local MLP backward reads block l's own buffers only, so it runs on the second stream
+    // beside the next blocks; under recompute it is enqueued after the next block's recomputed
+    // forward, whose join at its end would otherwise wait for it
+    auto local_back = [&](int l) {
+        const bool side = side_usable(ctx);
+        if (side) side_fork(ctx);
+        OnSide os(ctx, side);
+        local_bwd(ctx, d, l);
+    };
+    int local_pending = -1;
     for (int l = c.depth - 1; l >= 0; --l) {
         sa3k_block_ws* w = d->ws[d->tr.recompute ? 0 : l];
         bind_kv(d, w, l);
         bind_local(d, w, l);
         if (d->tr.recompute && l != c.depth - 1)   // the last block's activations are still in place
             block_forward(ctx, d->blocks[l], w, d->xs[l], d->context, d->gcond, d->xs[l + 1]);
+        if (local_pending >= 0) local_back(local_pending);
+        local_pending = -1;
         float* dA[7];
         float* dB[7];
         float* dm[7];
@@ -898,14 +915,13 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
         // resident activations: a block's last second-stream work may run on beside the next block
         block_backward(ctx, d->blocks[l], w, dcur, dnext, d->dctx, d->dgcond, dA, dB, d->tr.dora ? dm : nullptr,
                        ctx->late_join && !d->tr.recompute);
-        if (w->dladd) {   // reads block l's own buffers only: beside the next blocks on the second stream
-            const bool side = side_usable(ctx);
-            if (side) side_fork(ctx);
-            OnSide os(ctx, side);
-            local_bwd(ctx, d, l);
+        if (w->dladd) {
+            if (d->tr.recompute) local_pending = l;
+            else local_back(l);
         }
         std::swap(dcur, dnext);
     }
+    if (local_pending >= 0) local_back(local_pending);
     if (side_usable(ctx)) side_join(ctx);   // the head reads dgcond; AdamW reads every dA
     ctx->block_tail_pending = false;
     // head backward (only adapter gradients are wanted: the inputs are data). Three independent
