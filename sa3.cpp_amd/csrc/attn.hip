@@ -46,14 +46,18 @@ constexpr int BLK = 64;         // queries / keys per block
 constexpr int ROW = 128;        // bytes per [row][64] bf16 LDS row (swizzled, unpadded)
 constexpr float kLog2e = 1.4426950408889634f;
 
-// XOR swizzle of the eight 16-byte chunks of a 128-byte LDS row. MFMA operand reads (lane l reads
-// chunk 4s + l/16 of row l%16 of a 16-row group) are bank-conflict-free with it on gfx950: rows r
-// and r^1 sit in different bank halves, and the chunk XOR is a bit permutation of (r>>1)&7 such that
-// every group of lanes the LDS serves in one pass covers each bank once (the previous (r&7)^(r>>3&1)
-// left 2-way conflicts: 3.2 extra cycles per ds_read_b128 on the SQ_LDS_BANK_CONFLICT counter).
+// XOR swizzle of the eight 16-byte chunks of a 128-byte LDS row: rows r and r^1 sit in different
+// bank halves, and the chunk XOR is a linear map of a = (r>>1)&7, s = (a2, a1^a2, a0) as bits
+// (s0, s1, s2). Every read pattern of these kernels is bank-conflict-free with it on gfx950: the
+// ds_read_b128 row reads (lane l: chunk c + l/16 of row l%16, or chunk c + l/32 of row l%32) and the
+// ds_read_b64_tr_b16 reads of four or eight consecutive rows per 16 lanes (ld_tr below). Measured
+// with SQ_LDS_BANK_CONFLICT over every invertible map of a: 32 of the 168 serve all four patterns
+// in one pass per lane group; the bit permutation (a0, a2, a1) used before cost 2 extra cycles per
+// transposed read, (r&7)^(r>>3&1) before it 3.2 per row read. (The kernels are latency-bound: the
+// conflict-free map made the forwards 1-2% faster and left the backward within noise.)
 __device__ __forceinline__ int swz(int r) {
     const int a = (r >> 1) & 7;
-    return (a & 1) | ((a & 2) << 1) | ((a & 4) >> 1);
+    return ((a >> 2) & 1) | ((((a >> 1) ^ (a >> 2)) & 1) << 1) | ((a & 1) << 2);
 }
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {

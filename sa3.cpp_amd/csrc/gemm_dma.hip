@@ -77,10 +77,14 @@ constexpr int kRow = 128;   // LDS bytes per tile row
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // XOR swizzle of the eight 16-byte chunks of a 128-byte LDS row. MFMA operand reads (lane l reads
-// chunk 4s + l/16 of row l%16 of a 16-row group) are bank-conflict-free with it on gfx950: rows r
-// and r^1 sit in different bank halves, and the chunk XOR is a bit permutation of (r>>1)&7 such that
-// every group of lanes the LDS serves in one pass covers each bank once (the previous (r&7)^(r>>3&1)
-// left 2-way conflicts: 3.2 extra cycles per ds_read_b128 on the SQ_LDS_BANK_CONFLICT counter).
+// chunk 2s + l/32 of row l%32, or chunk 4s + l/16 of row l%16) are bank-conflict-free with it on
+// gfx950: rows r and r^1 sit in different bank halves, and the chunk XOR is a bit permutation of
+// (r>>1)&7 such that every group of lanes the LDS serves in one pass covers each bank once (the
+// previous (r&7)^(r>>3&1) left 2-way conflicts: 3.2 extra cycles per ds_read_b128 on the
+// SQ_LDS_BANK_CONFLICT counter). The transposed reads of a [K][N] B operand (ld_tr) still meet
+// 2-way conflicts (2 extra cycles per read); the linear map (a2, a1^a2, a0) of a = (r>>1)&7 serves
+// them in one pass too, but measured no faster on these kernels (the 128 x 256 products without
+// transposed reads 1-2% slower, the [K][N] ones within 1%), so the permutation stays.
 __device__ __forceinline__ int swz(int r) {
     const int a = (r >> 1) & 7;
     return (a & 1) | ((a & 2) << 1) | ((a & 4) >> 1);
