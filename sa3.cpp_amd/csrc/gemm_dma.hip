@@ -517,8 +517,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
 
     const int64_t Mt = p.M + p.Mx;
     const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.Nt + BN - 1) / BN);
-    const int nwg = gridDim.x;
-    const int bid = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+    // This workgroup's item (split z, tile bid). Dispatch deals workgroups out to the 8 XCDs
+    // round-robin in linear order (x fastest), so XCD c runs the linear ids L with L % 8 == c; it
+    // takes the contiguous run [c T/8, (c+1) T/8) of the T items in (split, raster) order, so the
+    // tiles of one split's K range that share A rows and B panels run on one XCD and share its L2.
+    const int nwg = gridDim.x;   // tiles rounded up to a multiple of 8
+    const int L = blockIdx.x + nwg * blockIdx.y;
+    const int item = (L & 7) * ((nwg * (int)gridDim.y) >> 3) + (L >> 3);
+    const int z = __builtin_amdgcn_readfirstlane(item / nwg);   // uniform: scalar operands derive from it
+    const int bid = __builtin_amdgcn_readfirstlane(item - z * nwg);
     if (bid >= tiles_m * tiles_n) return;
     constexpr int G = 8;
     const int per_group = G * tiles_n;
@@ -534,7 +541,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     const int wm0 = (wave % WMW) * WTM, wn0 = (wave / WMW) * WTN;
 
     const int KT = (int)(p.K / BKE);
-    const int z = blockIdx.y;
     const int kt0 = z * p.kps;
     const int Tm = max(0, min(KT, kt0 + p.kps) - kt0);
     const bool ext = p.K2 > 0 && z == (int)gridDim.y - 1;
@@ -956,8 +962,15 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
 
     const int64_t Mt = p.M + p.Mx;
     const int tiles_m = (int)((Mt + BM - 1) / BM), tiles_n = (int)((p.Nt + BN - 1) / BN);
-    const int nwg = gridDim.x;
-    const int bid = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+    // This workgroup's item (split z, tile bid). Dispatch deals workgroups out to the 8 XCDs
+    // round-robin in linear order (x fastest), so XCD c runs the linear ids L with L % 8 == c; it
+    // takes the contiguous run [c T/8, (c+1) T/8) of the T items in (split, raster) order, so the
+    // tiles of one split's K range that share A rows and B panels run on one XCD and share its L2.
+    const int nwg = gridDim.x;   // tiles rounded up to a multiple of 8
+    const int L = blockIdx.x + nwg * blockIdx.y;
+    const int item = (L & 7) * ((nwg * (int)gridDim.y) >> 3) + (L >> 3);
+    const int z = __builtin_amdgcn_readfirstlane(item / nwg);   // uniform: scalar operands derive from it
+    const int bid = __builtin_amdgcn_readfirstlane(item - z * nwg);
     if (bid >= tiles_m * tiles_n) return;
     constexpr int G = 8;
     const int per_group = G * tiles_n;
@@ -973,7 +986,6 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     const int wm0 = (wave % WMW) * WTM, wn0 = (wave / WMW) * WTN;
 
     const int KT = (int)(p.K / 64);
-    const int z = blockIdx.y;
     const int kt0 = z * p.kps;
     const int Tm = max(0, min(KT, kt0 + p.kps) - kt0);
     const bool ext = p.K2 > 0 && z == (int)gridDim.y - 1;
