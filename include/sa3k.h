@@ -562,9 +562,14 @@ SA3K_API int sa3k_dit_apply_adamw(sa3k_ctx* ctx, sa3k_dit* dit, const sa3k_adamw
  * turns it on): the first call runs eagerly, the next captures the step for its input pointers
  * (with and without the adapter refresh), later calls with the same pointers replay it. Results
  * are identical to the eager path. While profiling is on the step always runs eagerly. The eager
- * step is as fast on MI355X (launches hide behind the kernels) and runs the second stream's kernels
- * (option "side_stream") concurrently, which a replay of the graph does not. */
+ * step is faster on MI355X (launches hide behind the kernels, and the second stream's kernels,
+ * option "side_stream", run beside the main stream's, which a replay of the graph overlaps less):
+ * 34.2 against 38.5 ms per update at the DiT's benchmark size. */
 SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on);
+/* Whether the accumulate step replays captured graphs: 1 after sa3k_dit_set_graphs(on = 1) until a
+ * capture fails (the step then runs eagerly from that call on). No reference counterpart: the
+ * tests use it to check that the graph path ran. */
+SA3K_API int sa3k_dit_get_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int* on);
 /* run_eval_dit_loss (src/train_loop.h:455-476): the forward and the per-sample velocity MSE of
  * sa3k_dit_accumulate (same kernels, so the same losses bit for bit) without the backward; the
  * gradient arena and the accumulated sample count are untouched. loss_out (host, required) receives

@@ -962,10 +962,18 @@ bool capture(sa3k_ctx* ctx, sa3k_dit* d, int gi, const void* const* key, const f
     hipGraph_t g = nullptr;
     SA3K_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
+    ctx->tail_ev = nullptr;   // a fork armed before the capture would wait on uncaptured work
     try {
         accumulate_body(ctx, d, x_t, target, t, cross, glob, lw);
     } catch (...) {
         ctx->capturing = false;
+        // bring the other streams back into the capture (best effort: a stream that never joined
+        // it refuses), so that ending it leaves no stream capturing
+        for (hipStream_t st : {ctx->side_stream, ctx->quick_stream}) {
+            if (!st) continue;
+            hipEvent_t e = side_event(ctx);
+            if (hipEventRecord(e, st) == hipSuccess) (void)hipStreamWaitEvent(ctx->stream, e, 0);
+        }
         (void)hipStreamEndCapture(ctx->stream, &g);
         if (g) (void)hipGraphDestroy(g);
         (void)hipGetLastError();
@@ -1270,6 +1278,13 @@ SA3K_API int sa3k_dit_set_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int on) {
                 SA3K_HIP(hipGraphExecDestroy(e));
                 e = nullptr;
             }
+    });
+}
+
+SA3K_API int sa3k_dit_get_graphs(sa3k_ctx* ctx, sa3k_dit* dit, int* on) {
+    return sa3k_guard(ctx, "sa3k_dit_get_graphs", [&] {
+        SA3K_REQUIRE(dit && on, "null pointer");
+        *on = dit->use_graph ? 1 : 0;
     });
 }
 

@@ -242,8 +242,10 @@ inline void launch_k(sa3k_ctx* c, bool last, void (*kernel)(KArgs...), dim3 grid
         kernel<<<grid, block, shmem, c->stream>>>(args...);
     }
 }
+// Under a graph capture the fork records its own event: the completion event of a launch through
+// hipExtLaunchKernelGGL is not part of the capture, and a captured stream may not wait on it.
 inline void fork_arm(sa3k_ctx* c) {
-    if (!c->fork_tail) return;
+    if (!c->fork_tail || c->capturing) return;
     c->tail_ev = side_event(c);
     c->tail_seq = ~(uint64_t)0;
 }

@@ -147,6 +147,7 @@ def _declare(lib):
         "sa3k_dit_forward": (I, [P, P, P, P, P, P, P]),
         "sa3k_dit_eval_loss": (I, [P, P, P, P, P, P, P, P, C.POINTER(D)]),
         "sa3k_dit_set_graphs": (I, [P, P, I]),
+        "sa3k_dit_get_graphs": (I, [P, P, P]),
         "sa3k_dit_set_local": (I, [P, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -602,6 +603,12 @@ class Dit:
 
     def set_graphs(self, on):
         self.ctx.check(self.ctx.lib.sa3k_dit_set_graphs(self.ctx.h, self.h, int(on)))
+
+    def graphs(self):
+        """whether the accumulate step replays captured graphs (0 once a capture has failed)"""
+        on = C.c_int(0)
+        self.ctx.check(self.ctx.lib.sa3k_dit_get_graphs(self.ctx.h, self.h, C.byref(on)))
+        return on.value
 
     def set_local(self, local):
         """bind the inpaint local conditioning [B][T][local_dim] (device buffer) or None"""
