@@ -83,7 +83,7 @@ struct sa3k_ctx {
     int gemm_big = 3;                     // 256 x 256 bf16 tiles: 0 never, 1 where they fill the chip, 2 always,
                                           // 3 as 1 plus every product with K >= 8192 (split over K)
     int gemm_splits = 0;                  // > 0: split-K count of DMA GEMMs that split (for measurement)
-    int gemm_small = 2;                   // tile configuration for small grids (0: the default tile + split-K)
+    int gemm_small = 4;                   // tile configuration for small grids (0: the default tile + split-K)
     int gemm_prio = 1;                    // DMA GEMMs: wave priority 1 over the MFMA clusters of the K loop
     int gemm_wg_per_cu = 0;               // resident workgroups per CU assumed by the split choice (0: from LDS use)
     void* red_ws = nullptr;              // column-reduction partial sums (grows on demand)
