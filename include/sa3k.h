@@ -100,9 +100,10 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 last one's tiles sum in another order)
  *   "gemm_cfg"    DMA kernel tile configuration: 0 (default) 128 x 256 tiles for bf16 and
  *                 128 x 128 for f32; 1: 128 x 128; 4: 128 x 256 (3 stages); 7: 128 x 256 (2 stages)
- *   "gemm_small"  DMA kernel tile configuration for GEMMs with a short K whose default tiles cannot
- *                 fill the chip (default 4: bf16 128x128 tiles of eight waves, f32 and decoded B
- *                 64x128; 2: 64x128 tiles; 0: the default tile, split over K)
+ *   "gemm_small"  DMA kernel tile configuration for GEMMs whose 128x128 grid cannot fill the chip
+ *                 (default 4: bf16 128x128 tiles of eight waves at any K, f32 and decoded B 64x128
+ *                 below K 2048 / 4096; 2: 64x128 tiles below those K; 0: the default tile, split
+ *                 over K)
  *   "gemm_nt_store" 1: GEMM outputs are written with non-temporal stores (default 1)
  *   "gemm_skinny" 1: bf16 products with at most 32 output columns and a plain epilogue (the rank
  *                 products s X A^T and s dU B) run on a kernel that splits K across the waves of

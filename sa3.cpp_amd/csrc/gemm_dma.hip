@@ -1432,7 +1432,7 @@ void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
     if (p.N <= 64) return launch_dma<128, 64, 4, 4, true, 4, true>(ctx, p);
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.N, 128);
     if (tiles128 < 384 && p.K < 4096 && ctx->gemm_small == 2) return launch_dma<64, 128, 1, 3, true, 4, true>(ctx, p);
-    if (tiles128 < 384 && p.K < 4096 && ctx->gemm_small == 4) return launch_dma<128, 128, 2, 3, true, 8, true>(ctx, p);
+    if (tiles128 < 384 && ctx->gemm_small == 4) return launch_dma<128, 128, 2, 3, true, 8, true>(ctx, p);
     if (ctx->gemm_cfg == 1) return launch_dma<128, 128, 2, 2, true, 4, true>(ctx, p);
     return launch_dma<128, 256, 2, 3, true, 8, true>(ctx, p);
 }
@@ -1467,20 +1467,20 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if (Mt <= 32) return launch_dma<32, 128, 1, 4, BF16>(ctx, p);
     if (p.Nt <= 32) return launch_dma<128, 32, 4, 4, BF16>(ctx, p);
     if (p.Nt <= 64) return launch_dma<128, 64, 4, 4, BF16>(ctx, p);
-    // Grids of 128x128 tiles that leave a quarter of the two-per-CU slots idle: with a short K no
-    // split, on 128 x 128 tiles with eight waves in one workgroup per CU (three stages, 96 KiB) for
-    // bf16, 64 x 128 tiles for f32 (measured on MI355X, 2176 x 1536 x 1536 bf16: 21.4 us, against
-    // 23.6 us on 64 x 128 tiles and 31.1 us on the default tile split over K; 34.56 against
-    // 35.16 ms per DiT update); with a long K (>= 4096) the default tile split over K stays faster.
+    // Grids of 128x128 tiles that leave a quarter of the two-per-CU slots idle. bf16: no split, on
+    // 128 x 128 tiles with eight waves in one workgroup per CU (three stages, 96 KiB), at any K
+    // (measured on MI355X: 2176 x 1536 x 1536 21.4 us against 23.6 us on 64 x 128 tiles and 31.1 us
+    // on the default tile split over K; 2176 x 1536 x 6144 67.7 against 71.1 us split over K; the
+    // DiT update 34.56 against 35.16 ms with the short-K products alone, then 33.66 against 33.97 ms
+    // with the long-K ones too). f32 with a short K: 64 x 128 tiles, no split.
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(p.Nt, 128);
+    if constexpr (BF16)
+        if (tiles128 < 384 && ctx->gemm_small == 4) return launch_dma<128, 128, 2, 3, true, 8>(ctx, p);
     if (tiles128 < 384 && p.K < (BF16 ? 4096 : 2048)) {
         switch (ctx->gemm_small) {
             case 1: return launch_dma<64, 128, 2, 2, BF16>(ctx, p);
-            case 2: return launch_dma<64, 128, 1, 3, BF16>(ctx, p);
+            case 2: case 4: return launch_dma<64, 128, 1, 3, BF16>(ctx, p);
             case 3: return launch_dma<128, 64, 2, 2, BF16>(ctx, p);
-            case 4:
-                if constexpr (BF16) return launch_dma<128, 128, 2, 3, true, 8>(ctx, p);
-                else return launch_dma<64, 128, 1, 3, false>(ctx, p);
             default: break;
         }
     }
@@ -1511,7 +1511,7 @@ int64_t dma_rounds(const sa3k_ctx* ctx, int64_t Mt, int64_t Nt, int64_t K) {
     if (Mt <= 32 || Nt <= 64) return 1;
     const int64_t tiles128 = ceil_div(Mt, 128) * ceil_div(Nt, 128);
     if (tiles128 < 384 && K < 4096 && ctx->gemm_small == 2) return rounds(ceil_div(Mt, 64) * ceil_div(Nt, 128), 512);
-    if (tiles128 < 384 && K < 4096 && ctx->gemm_small == 4) return rounds(tiles128, 256);
+    if (tiles128 < 384 && ctx->gemm_small == 4) return rounds(tiles128, 256);
     if (ctx->gemm_cfg == 1) return rounds(tiles128, 512);
     return rounds(ceil_div(Mt, 128) * ceil_div(Nt, 256), 256);
 }
