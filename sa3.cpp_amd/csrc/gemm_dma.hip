@@ -1434,7 +1434,8 @@ void dispatch_dma_kn(sa3k_ctx* ctx, const DmaParams& p) {
     if (tiles128 < 384 && p.K < 4096 && ctx->gemm_small == 2) return launch_dma<64, 128, 1, 3, true, 4, true>(ctx, p);
     if (tiles128 < 384 && ctx->gemm_small == 4) return launch_dma<128, 128, 2, 3, true, 8, true>(ctx, p);
     if (ctx->gemm_cfg == 1) return launch_dma<128, 128, 2, 2, true, 4, true>(ctx, p);
-    return launch_dma<128, 256, 2, 3, true, 8, true>(ctx, p);
+    if (ctx->gemm_cfg == 4) return launch_dma<128, 256, 2, 3, true, 8, true>(ctx, p);
+    return launch_dma<128, 256, 2, 3, true, 16, true>(ctx, p);
 }
 
 // B decoded from f16 / Q8_0 on its way into the MFMAs (bf16 A): the short-K small-grid tile of the
@@ -1457,7 +1458,10 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
     if constexpr (BF16) {
         // per-head q/k preparation: 128 x 256 tiles, the default for the attention projections
         // (falls back to the plain instantiation where headprep_ok refuses)
-        if (p.hp.parts > 0 && p.bq == 0 && !p.b_kn) return launch_dma<128, 256, 2, 3, true, 8, false, 0, true>(ctx, p);
+        if (p.hp.parts > 0 && p.bq == 0 && !p.b_kn) {
+            if (ctx->gemm_cfg == 4) return launch_dma<128, 256, 2, 3, true, 8, false, 0, true>(ctx, p);
+            return launch_dma<128, 256, 2, 3, true, 16, false, 0, true>(ctx, p);
+        }
         if (p.bq == 1) return dispatch_dma_dq<1>(ctx, p);
         if (p.bq == 2) return dispatch_dma_dq<2>(ctx, p);
         if (p.b_kn) return dispatch_dma_kn(ctx, p);
@@ -1484,19 +1488,21 @@ void dispatch_dma(sa3k_ctx* ctx, const DmaParams& p) {
             default: break;
         }
     }
-    // bf16: 128 x 256 tiles, 8 waves of 64 x 64, three stages in 144 KiB of LDS (one workgroup per
-    // CU). Against two 128 x 128 workgroups per CU they move a quarter fewer operand bytes per flop
-    // through the CU's vector-memory path, which the MFMA rate otherwise saturates; measured on
-    // MI355X at 2176 rows: QKV 2176 x 7680 x 1536 58.2 vs 64.7 us, 2176 x 3072 x 1536 27.4 vs
+    // bf16: 128 x 256 tiles, three stages in 144 KiB of LDS (one workgroup per CU), 16 waves of
+    // 64 x 32 (four per SIMD, to hide the DMA and LDS latency behind each other's MFMAs). Against
+    // two 128 x 128 workgroups per CU the tile moves a quarter fewer operand bytes per flop through
+    // the CU's vector-memory path, which the MFMA rate otherwise saturates (measured on MI355X at
+    // 2176 rows, 8 waves: QKV 2176 x 7680 x 1536 58.2 vs 64.7 us, 2176 x 3072 x 1536 27.4 vs
     // 31.0 us, the split-K products 2176 x 1536 x 6144 / 7680 / 12288 53.4 / 63.5 / 93.5 vs
-    // 59.4 / 70.7 / 102.2 us.
+    // 59.4 / 70.7 / 102.2 us); 16 waves against 8 (option gemm_cfg 4): 2176 x 7680 x 1536 with f32
+    // output 76.7 vs 86.6 us, the DiT update 34.57 vs 35.00 ms.
     switch (ctx->gemm_cfg) {
         case 1: return launch_dma<128, 128, 2, 2, BF16>(ctx, p);    // 64 KiB LDS: two workgroups per CU
         case 4: return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);
         case 7: return launch_dma<128, 256, 2, 2, BF16, 8>(ctx, p);
         default:
-            if constexpr (BF16) return launch_dma<128, 256, 2, 3, BF16, 8>(ctx, p);
-            else return launch_dma<128, 128, 2, 2, BF16>(ctx, p);
+            if constexpr (BF16) return launch_dma<128, 256, 2, 3, true, 16>(ctx, p);
+            else return launch_dma<128, 128, 2, 2, false>(ctx, p);
     }
 }
 
