@@ -99,7 +99,8 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 decodes on the way into LDS (default 1; all decode to the same bf16 values, the
  *                 last one's tiles sum in another order)
  *   "gemm_cfg"    DMA kernel tile configuration: 0 (default) 128 x 256 tiles of 16 waves for bf16
- *                 and 128 x 128 for f32; 1: 128 x 128; 4: 128 x 256 of 8 waves (3 stages);
+ *                 (and 16-wave 256 x 256 tiles where those are taken) and 128 x 128 for f32;
+ *                 1: 128 x 128; 4: 128 x 256 and 256 x 256 of 8 waves (3 / 2 stages);
  *                 7: 128 x 256 of 8 waves (2 stages)
  *   "gemm_small"  DMA kernel tile configuration for GEMMs whose 128x128 grid cannot fill the chip
  *                 (default 4: bf16 128x128 tiles of eight waves at any K, f32 and decoded B 64x128

@@ -946,12 +946,13 @@ struct BigSeg {
     uint32_t off[4];
 };
 
-template <bool KN>
-__global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
-    constexpr int BM = 256, BN = 256, NW = 8, NT = 512, WMW = 4;
-    constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW);   // 64 x 128
-    constexpr int FM = WTM / 32, FN = WTN / 32;             // 2 x 4 MFMA blocks
-    constexpr int NA = BM * 8 / NT, NB = BN * 8 / NT;       // 4 + 4 DMA chunks per thread and tile
+template <bool KN, int NW = 8>
+__global__ __launch_bounds__(NW * 64) void gemm_big_kernel(DmaParams p) {
+    constexpr int BM = 256, BN = 256, NT = NW * 64, WMW = 4;
+    constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW);   // 64 x 128 (8 waves), 64 x 64 (16)
+    constexpr int FM = WTM / 32, FN = WTN / 32;             // MFMA blocks per wave
+    constexpr int NA = BM * 8 / NT, NB = BN * 8 / NT;       // DMA chunks per thread and tile
+    constexpr int RPQ = NT / 8;                             // tile rows per DMA slot q
     constexpr int LPT = NA + NB;
     constexpr int STAGES = 2;
     constexpr int STAGE_BYTES = (BM + BN) * kRow;           // 64 KiB
@@ -1004,7 +1005,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     constexpr uint32_t kNoData = 0xFFFFFFF0u;   // past every extent: loads zeros
 
     // per-thread DMA sources: slot s = q * NT + tid of the A (B) region, row s / 8, chunk kc. The 8
-    // rows of slot (q, wave) start at m0 + 64 q + 8 wave, so their source is decided from
+    // rows of slot (q, wave) start at m0 + (NT / 8) q + 8 wave, so their source is decided from
     // wave-uniform values (M % 8 == 0 when there are extra rows).
     BigSeg ao, a2o, bo, b2o;
 #pragma unroll
@@ -1030,10 +1031,10 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(DmaParams p) {
     unsigned bx_mask = 0, x_mask = 0;
 #pragma unroll
     for (int q = 0; q < NB; ++q)
-        if (min(tile_col(p, n0, 64 * q + 8 * wave), p.Nt - 1) >= p.N) bx_mask |= 1u << q;
+        if (min(tile_col(p, n0, RPQ * q + 8 * wave), p.Nt - 1) >= p.N) bx_mask |= 1u << q;
 #pragma unroll
     for (int q = 0; q < NA; ++q)
-        if (min(m0 + 64 * q + 8 * wave, Mt - 1) >= p.M) x_mask |= 1u << q;
+        if (min(m0 + RPQ * q + 8 * wave, Mt - 1) >= p.M) x_mask |= 1u << q;
     auto slot_bx = [&](int q) { return ((bx_mask >> q) & 1u) != 0; };
     if constexpr (KN) {
         // [K][N] B: slot s of the B region is sub-tile s / 512 (64 columns), row k = (s % 512) / 8 of
@@ -1411,8 +1412,16 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     {
         KernelScope ks(ctx, p.b_kn ? "gemm_big<256,256,kn,bf16>" : "gemm_big<256,256,bf16>",
                        2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true>, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
-        else launch_k(ctx, splits == 1, gemm_big_kernel<false>, dim3((unsigned)grid, (unsigned)splits), dim3(512), 0, p);
+        // 16 waves of 64 x 64 (four per SIMD); option gemm_cfg 4: 8 waves of 64 x 128 (the DiT update
+        // 32.90 against 33.08 ms on one box)
+        const dim3 g((unsigned)grid, (unsigned)splits);
+        if (ctx->gemm_cfg == 4) {
+            if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true, 8>, g, dim3(512), 0, p);
+            else launch_k(ctx, splits == 1, gemm_big_kernel<false, 8>, g, dim3(512), 0, p);
+        } else {
+            if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true, 16>, g, dim3(1024), 0, p);
+            else launch_k(ctx, splits == 1, gemm_big_kernel<false, 16>, g, dim3(1024), 0, p);
+        }
         SA3K_LAUNCHED();
     }
     if (splits > 1) {
