@@ -44,11 +44,12 @@ def run_gpu(ctx, X, dY, Wop, wtype, A, B, s, dora, mag, prec, bias=None, reps=1,
     dA_, dB_ = ctx.upload(A), ctx.upload(B)
     dmag = ctx.upload(mag) if dora else None
     bnsq = w.row_norm_sq(1e-12) if dora else None
+    prev = ctx.options()   # the caller's settings hold for the products below
     ctx.set_option("lin_merge", 1 if merge else 0)
     try:
         lin.prepare(dA_, dB_, s, dora, dmag, bnsq)
     finally:
-        ctx.set_options(ctx.defaults)
+        ctx.set_options(prev)
     dX_, dY_ = ctx.upload(X), ctx.upload(dY)
     Y = ctx.empty((N, out_))
     gX, gA, gB, gm = ctx.empty((N, in_)), ctx.zeros((r, in_)), ctx.zeros((out_, r)), ctx.zeros(out_)
@@ -243,6 +244,33 @@ def test_rank_products_as_extra_columns(ctx, cols):
         for k in ("Y", "dX", "dA", "dB", "dm"):
             assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, (N, k)
             assert rel_err(got[k], sep[k]) < 1e-4, (N, k)
+
+
+@pytest.mark.parametrize("opts", [dict(gemm_cfg=4), dict(gemm_cfg=1), dict(gemm_small=2), dict(gemm_small=0)])
+def test_tile_configurations(ctx, opts):
+    """The tile families the options select (gemm_cfg 4: 128 x 256 and 256 x 256 workgroups of 8
+    waves instead of 16; gemm_cfg 1: 128 x 128 tiles; gemm_small 2 / 0: 64 x 128 tiles or the default
+    tile split over K for the small grids instead of 8-wave 128 x 128) give the default's results up
+    to the summation order, on a merged DoRA linear's forward ([N][K] B operand) and dX ([K][N])
+    products at the DiT's shapes, and stay within the oracle's bar. The bound between the two runs
+    is 1e-3: the rank product s X A^T and the DoRA rows reach dA / dB through bf16 roundings, where
+    an f32 difference in the last place flips a bf16 value now and then (5.7e-5 seen on dB)."""
+    for N, in_, out_, r in ((2176, 1536, 1536, 32), (2176, 1536, 6144, 32), (2176, 6144, 1536, 32)):
+        X, dY, W, A, B = make_inputs(37, N, in_, out_, r)
+        Wh = W.astype(np.float16)
+        Wdec = Wh.astype(np.float32)
+        mag = (oracle.row_norms(Wdec) * 0.97).astype(np.float32)
+        base = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
+        try:
+            for k, v in opts.items():
+                ctx.set_option(k, v)
+            got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.25, True, mag, sa3k.PREC_BF16)
+        finally:
+            ctx.set_options(ctx.defaults)
+        ref = run_oracle(X, dY, Wdec, A, B, 1.25, True, mag)
+        for k in ("Y", "dX", "dA", "dB", "dm"):
+            assert rel_err(got[k], base[k]) < 1e-3, (N, in_, out_, k)
+            assert rel_err(got[k], ref[k]) < 2e-2 and cosine(got[k], ref[k]) >= 0.9999, (N, in_, out_, k)
 
 
 @pytest.mark.parametrize("big", [0, 1, 2])
