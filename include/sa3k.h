@@ -136,7 +136,7 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *   "rank_cols"   bit 0: a merged linear's rank product s X A^T rides on its forward product as r
  *                 extra output columns where they cost it no extra round of workgroups (default 1);
  *                 bit 1: likewise s dU B on its dX product (default 0: measured slower on MI355X
- *                 than the separate product beside it; needs merge_kn 0)
+ *                 than the separate product beside it; with merge_kn 1 it needs in % 64 == 0)
  *   "tn_fuse"     bit mask of split reductions summed by their own last split to arrive instead of
  *                 a separate launch (each stream has its own arrival counters): 1 the block's
  *                 modulation-gradient column sums, 2 an adapted linear's dA sums, 4 an adapted

@@ -559,8 +559,10 @@ void gemm_run(sa3k_ctx* ctx, const GemmDesc& d, const char* prof_name) {
     SA3K_REQUIRE(!d.prescale || (d.colscale && d.Mx == 0 && !d.U && !d.Ub),
                  "GEMM prescale needs colscale and no extra rows or pre-scale copies");
     SA3K_REQUIRE(!d.b_kn || (bf && d.a_src == SRC_BF16 && d.b_src == SRC_BF16 && ctx->gemm_dma && d.K2 == 0 &&
-                             d.Nx == 0 && !d.prescale && d.N % 8 == 0 && d.ldb >= d.N && (d.ldb * 2) % 16 == 0),
-                 "a [K][N] B operand needs bf16 operands on the DMA kernel, no second segment or extra columns");
+                             !d.prescale && d.N % 8 == 0 && d.ldb >= d.N && (d.ldb * 2) % 16 == 0 &&
+                             (d.Nx == 0 || (d.N % 64 == 0 && d.ldbx >= d.Nx))),
+                 "a [K][N] B operand needs bf16 operands on the DMA kernel, no second segment, and extra "
+                 "columns ([K][Nx], row pitch ldbx) only beside N % 64 == 0");
     SA3K_REQUIRE(d.Nx >= 0, "negative extra columns");
     SA3K_REQUIRE(d.Nx == 0 || (bf && d.a_src == SRC_BF16 && d.b_src == SRC_BF16 && ctx->gemm_dma && d.K2 == 0 &&
                                !d.prescale && d.N % 8 == 0 && d.Nx % 8 == 0 && d.Bx && al16(d.Bx) &&

@@ -610,25 +610,36 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
         if (gn >= p.Nt) gn = 0;
         boff[q] = gn < p.N ? (uint32_t)((gn * p.ldb + kc * CE) * EB) : (uint32_t)(((gn - p.N) * p.ldbx + kc * CE) * EB);
     }
-    if constexpr (KN) {
-        // [K][N] B: slot s of the B region is sub-tile s / 512, row k = (s % 512) / 8 of the K tile,
-        // logical chunk (s % 8) ^ swz(k): 8 columns at n0 + 64 (s / 512) + 8 chunk (columns past N
-        // read a valid column; their results are never stored). The K tile moves in soff.
-#pragma unroll
-        for (int q = 0; q < NB; ++q) {
-            const int s = q * NT + tid, t = s >> 9, k = (s & 511) >> 3, kc = (s & 7) ^ swz(k);
-            int64_t gn = n0 + 64 * t + 8 * kc;
-            if (gn + 8 > p.N) gn = p.N - 8;
-            boff[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
-        }
-    }
     // the 8 rows of B slot (q, wave) start at n0 + (q * NT + 64 wave) / 8: one source per slot
     // (N % 8 == 0), chosen on the scalar unit
     unsigned bx_mask = 0;   // bit q: slot q's rows are extra columns (fixed over the K loop)
+    if constexpr (KN) {
+        // [K][N] B: slot s of the B region is sub-tile s / 512, row k = (s % 512) / 8 of the K tile,
+        // logical chunk (s % 8) ^ swz(k): 8 columns at n0 + 64 (s / 512) + 8 chunk (columns past N
+        // read a valid column; their results are never stored). The K tile moves in soff. A wave's
+        // slot q lies in one sub-tile; with extra columns (N % 64 == 0) a sub-tile at or past N reads
+        // them from Bx, [K][Nx] with row pitch ldbx.
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-        const int64_t r0 = tile_col_bn<BN>(p, n0, (q * NT + wave * 64) / 8);
-        if (r0 < p.Nt && r0 >= p.N) bx_mask |= 1u << q;
+        for (int q = 0; q < NB; ++q) {
+            const int s = q * NT + tid, t = s >> 9, k = (s & 511) >> 3, kc = (s & 7) ^ swz(k);
+            const bool extra = p.Nx > 0 && n0 + 64 * ((q * NT + wave * 64) >> 9) >= p.N;   // wave-uniform
+            int64_t gn = n0 + 64 * t + 8 * kc;
+            if (extra) {
+                bx_mask |= 1u << q;
+                int64_t gx = gn - p.N;
+                if (gx + 8 > p.Nx) gx = p.Nx - 8;
+                boff[q] = (uint32_t)(((int64_t)k * p.ldbx + gx) * 2);
+            } else {
+                if (gn + 8 > p.N) gn = p.N - 8;
+                boff[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            const int64_t r0 = tile_col_bn<BN>(p, n0, (q * NT + wave * 64) / 8);
+            if (r0 < p.Nt && r0 >= p.N) bx_mask |= 1u << q;
+        }
     }
     auto slot_bx = [&](int q) { return ((bx_mask >> q) & 1u) != 0; };
     // Q8_0: quant slot s = q NT + tid holds row s / 4, physical chunk s % 4 = logical chunk
@@ -672,8 +683,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
                     dma16b(rs_bs, 0xFFFFFFF0u, 0u, sc0 + NW * 256 + (uint32_t)((q * NT + wave * 64) * 16));
             } else if constexpr (KN) {   // always through the descriptor: the K tile is a row offset
                 const uint32_t sob = (uint32_t)((k0 + (int64_t)t * BKE) * p.ldb * 2);
+                const uint32_t sobx = (uint32_t)((k0 + (int64_t)t * BKE) * p.ldbx * 2);
 #pragma unroll
-                for (int q = 0; q < NB; ++q) dma16b(rs_b, boff[q], sob, dst[NA + q] + so_lds);
+                for (int q = 0; q < NB; ++q)
+                    dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), boff[q], slot_bx(q) ? sobx : sob, dst[NA + q] + so_lds);
             } else if (a_src != 0) {
 #pragma unroll
                 for (int q = 0; q < NB; ++q) dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), boff[q], so, dst[NA + q] + so_lds);
@@ -1038,13 +1051,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_big_kernel(DmaParams p) {
     auto slot_bx = [&](int q) { return ((bx_mask >> q) & 1u) != 0; };
     if constexpr (KN) {
         // [K][N] B: slot s of the B region is sub-tile s / 512 (64 columns), row k = (s % 512) / 8 of
-        // the K tile, logical chunk (s % 8) ^ swz(k); columns past N read a valid column
+        // the K tile, logical chunk (s % 8) ^ swz(k); columns past N read a valid column. A wave's
+        // slot q lies in one sub-tile; with extra columns (N % 64 == 0) a sub-tile at or past N reads
+        // them from Bx, [K][Nx] with row pitch ldbx.
+        bx_mask = 0;
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
             const int s = q * NT + tid, t = s >> 9, k = (s & 511) >> 3, kc = (s & 7) ^ swz(k);
+            const bool extra = p.Nx > 0 && n0 + 64 * ((q * NT + wave * 64) >> 9) >= p.N;   // wave-uniform
             int64_t gn = n0 + 64 * t + 8 * kc;
-            if (gn + 8 > p.N) gn = p.N - 8;
-            bo.off[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
+            if (extra) {
+                bx_mask |= 1u << q;
+                int64_t gx = gn - p.N;
+                if (gx + 8 > p.Nx) gx = p.Nx - 8;
+                bo.off[q] = (uint32_t)(((int64_t)k * p.ldbx + gx) * 2);
+            } else {
+                if (gn + 8 > p.N) gn = p.N - 8;
+                bo.off[q] = (uint32_t)(((int64_t)k * p.ldb + gn) * 2);
+            }
         }
     }
     auto slot_x = [&](int q) { return ((x_mask >> q) & 1u) != 0; };
@@ -1058,8 +1082,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_big_kernel(DmaParams p) {
             for (int q = 0; q < NA; ++q) dma16b(slot_x(q) ? rs_ax : rs_a, ao.off[q], so, dst0 + q * NT * 16);
             if constexpr (KN) {   // the K tile is a row offset of the [K][N] operand
                 const uint32_t sob = (uint32_t)(((int64_t)kt0 + t) * 64 * p.ldb * 2);
+                const uint32_t sobx = (uint32_t)(((int64_t)kt0 + t) * 64 * p.ldbx * 2);
 #pragma unroll
-                for (int q = 0; q < NB; ++q) dma16b(rs_b, bo.off[q], sob, dst0 + BM * kRow + q * NT * 16);
+                for (int q = 0; q < NB; ++q)
+                    dma16b(pick_rsrc(slot_bx(q), rs_bx, rs_b), bo.off[q], slot_bx(q) ? sobx : sob,
+                           dst0 + BM * kRow + q * NT * 16);
             } else {
 #pragma unroll
                 for (int q = 0; q < NB; ++q)
@@ -1308,6 +1335,12 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                          "a [K][N] B operand needs buffer-addressable operands");
         }
         p.bx_bytes = p.Nx > 0 ? extent(p.Nx, p.ldbx) : 0u;
+        if (KN && p.Nx > 0) {   // [K][Nx] extra columns, whole 64-column sub-tiles of the main ones
+            SA3K_REQUIRE(p.N % 64 == 0 && p.Nx % 8 == 0 && p.Nx <= p.ldbx, "[K][N] extra columns need N % 64 == 0");
+            const int64_t b = ((p.K - 1) * p.ldbx + p.Nx) * 2;
+            p.bx_bytes = b < ((int64_t)1 << 32) ? (uint32_t)b : 0u;
+            SA3K_REQUIRE(p.bx_bytes != 0, "[K][N] extra columns beyond a buffer descriptor's reach");
+        }
         if (BQ == 2) {   // int8 quants (ldb bytes per row) and f16 block scales (ldbs per row)
             const int64_t qb = (p.N - 1) * p.ldb + p.K, sb = ((p.N - 1) * p.ldbs + p.K / 32) * 2;
             p.b_bytes = qb < ((int64_t)1 << 31) ? (uint32_t)qb : 0u;
@@ -1371,6 +1404,7 @@ bool big_ok(const sa3k_ctx* ctx, const DmaParams& p) {
     if (extent(p.M, p.lda, p.K) >= lim || extent(p.N, p.ldb, p.K) >= lim) return false;
     if (p.b_kn && p.K * p.ldb * 2 >= lim) return false;
     if (p.Nx > 0 && (p.N % 8 != 0 || extent(p.Nx, p.ldbx, p.K) >= lim)) return false;
+    if (p.b_kn && p.Nx > 0 && (p.N % 64 != 0 || p.Nx % 8 != 0 || (p.K - 1) * p.ldbx * 2 + p.Nx * 2 >= lim)) return false;
     if (p.Mx > 0 && (p.M % 8 != 0 || extent(p.Mx, p.ldax, p.K) >= lim)) return false;
     if (p.K2 > 0 && (extent(p.M, p.lda2, p.K2) >= lim || extent(p.N, p.ldb2, p.K2) >= lim ||
                      (p.Mx > 0 && extent(p.Mx, p.lda2x, p.K2) >= lim)))
@@ -1405,6 +1439,10 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     p.b_bytes = extent(p.N, p.ldb);
     p.bx_bytes = extent(p.Nx, p.ldbx);
     if (p.b_kn) p.b_bytes = (uint32_t)(p.K * p.ldb * 2);   // the whole [K][ldb] operand (big_ok: < 2 GiB)
+    if (p.b_kn && p.Nx > 0) {   // [K][Nx] extra columns (big_ok: N % 64 == 0, within reach)
+        SA3K_REQUIRE(p.N % 64 == 0 && p.Nx % 8 == 0 && p.Nx <= p.ldbx, "[K][N] extra columns need N % 64 == 0");
+        p.bx_bytes = (uint32_t)(((p.K - 1) * p.ldbx + p.Nx) * 2);
+    }
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
     settle_swiglu(p, BN, splits, p.b_kn != 0, 0);

@@ -1081,7 +1081,9 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
     if (!merged) sdub();
     // merged: sdUB = s dU B as r extra output columns of the dX GEMM (B rows from B^T) when they cost
     // it no extra round of workgroups; the dA partials then follow that GEMM
-    const bool sdub_cols = merged && dX && L->Wmt && (ctx->rank_cols & 2) &&
+    // (with W_eff read as a [K][N] operand the extra columns read B itself, [out][r], as a [K][Nx]
+    // operand: whole 64-column sub-tiles of dX's columns, in % 64 == 0)
+    const bool sdub_cols = merged && dX && (L->Wmt || (in % 64 == 0 && r % 8 == 0)) && (ctx->rank_cols & 2) &&
                            gemm_extra_cols_free(ctx, N + (L->dora ? r : 0), in, out, r);
     // 4a. dA += sdUB^T X: the column-reduction partials only need sdUB and X, so they run before
     //     (on the second stream: beside) the dX GEMM; their sum is added to dA after the GEMM's
@@ -1153,7 +1155,11 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.prec = L->prec; g.a_src = bf ? SRC_BF16 : SRC_F32; g.b_src = wt.src;
         g.A = L->dU; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds; g.b_kn = kn;
         if (!merged) { g.A2 = L->sdUB; g.lda2 = r; g.B2 = L->At; g.ldb2 = r; g.K2 = r; }
-        if (sdub_cols) { g.Nx = r; g.Bx = L->Bt; g.ldbx = out; g.alpha_x = L->s; g.Cbn = static_cast<bf16*>(L->sdUB); g.ldcn = r; }
+        if (sdub_cols) {
+            g.Nx = r; g.alpha_x = L->s; g.Cbn = static_cast<bf16*>(L->sdUB); g.ldcn = r;
+            if (kn) { g.Bx = L->Bc; g.ldbx = r; }   // B [out][r]: K rows of r columns
+            else { g.Bx = L->Bt; g.ldbx = out; }    // B^T [r][out]: r rows of K
+        }
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
         if (L->dora) {

@@ -220,20 +220,22 @@ def test_merged_refresh_terms(ctx, wt, r):
         assert rel_err(got[k], seg[k]) < 1e-2, k
 
 
+@pytest.mark.parametrize("kn", [0, 1])
 @pytest.mark.parametrize("cols", [0, 1, 2, 3])
-def test_rank_products_as_extra_columns(ctx, cols):
+def test_rank_products_as_extra_columns(ctx, cols, kn):
     """Merged DoRA linear with s X A^T (bit 0) and s dU B (bit 1) as extra output columns of the
-    forward / dX products (option rank_cols), at the DiT's 2176-token shape (the 256 x 256, 128 x 256
-    and split-K tilings all carry them) and a ragged one: within the bf16 bar of the oracle, and
-    within bf16 rounding of the separate products. The dX product's columns need the transposed
-    merged copy, so these runs keep it (merge_kn 0)."""
+    forward / dX products (option rank_cols), at the DiT's 2176-token shape (the 256 x 256, 128 x 256,
+    128 x 128 and split-K tilings all carry them) and a ragged one: within the bf16 bar of the
+    oracle, and within bf16 rounding of the separate products. The dX product reads the transposed
+    merged copy (merge_kn 0, s dU B from B^T [r][out]) or W + s B A itself as a [K][N] operand
+    (merge_kn 1, s dU B from B [out][r] as [K][Nx] extra columns)."""
     for N, in_, out_, r in ((2176, 1536, 6144, 32), (2176, 6144, 1536, 32), (120, 192, 320, 16)):
         X, dY, W, A, B = make_inputs(21, N, in_, out_, r)
         Wh = W.astype(np.float16)
         Wdec = Wh.astype(np.float32)
         mag = (oracle.row_norms(Wdec) * 1.02).astype(np.float32)
         try:
-            ctx.set_option("merge_kn", 0)
+            ctx.set_option("merge_kn", kn)
             ctx.set_option("rank_cols", cols)
             got = run_gpu(ctx, X, dY, Wh, sa3k.TYPE_F16, A, B, 1.0, True, mag, sa3k.PREC_BF16)
             ctx.set_option("rank_cols", 0)
