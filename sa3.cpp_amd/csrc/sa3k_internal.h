@@ -392,7 +392,7 @@ __device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(
 // The split sums of NE elements of coherent partials: acc[i] = sum over z < S of the float at byte
 // offset off[i] + z * zstride of rs, added in z order from zero (the same sums as a sequential
 // loop over z), with device-coherent (sc1) buffer loads issued 8 splits x NE elements at a time so
-// the reading workgroup waits about S / 8 memory round trips, not S x NE. The caller gives every
+// the reading workgroup waits about ceil(S / 8) memory round trips, not S x NE. The caller gives every
 // element it stores a valid offset; the sums of the others are not used.
 constexpr int kSc1 = 16;   // buffer intrinsic cache policy: sc1 (device scope)
 template <int NE>
@@ -414,13 +414,21 @@ __device__ __forceinline__ void coherent_split_sums(__amdgpu_buffer_rsrc_t rs, c
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[i] += v[i][k];
     }
-    for (; z < S; ++z) {
-        float v[NE];
+    if (z < S) {   // the last S % 8 splits: also in one batch (a loop over them waited once per split)
+        const int n = S - z;
+        float v[NE][8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < n)
+#pragma unroll
+                for (int i = 0; i < NE; ++i)
+                    v[i][k] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rs, off[i] + (uint32_t)(z + k) * zstride, 0, kSc1));
 #pragma unroll
         for (int i = 0; i < NE; ++i)
-            v[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off[i] + (uint32_t)z * zstride, 0, kSc1));
 #pragma unroll
-        for (int i = 0; i < NE; ++i) acc[i] += v[i];
+            for (int k = 0; k < 8; ++k)
+                if (k < n) acc[i] += v[i][k];
     }
 }
 // arrival of this workgroup on counter c of `expected` arrivals; true for the last one, which
