@@ -158,6 +158,9 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 blocks (default 1). It holds from a DiT's setup.
  *   "prep_side"   1: with f32 head linears, a DiT's bf16 group refresh runs on the second stream
  *                 beside the heads' refresh and forward on the main one (default 1)
+ *   "head_quick"  1: a DiT's context MLP and x path (pre_conv, proj_in) run on a third stream of
+ *                 the context beside the modulation chain in the forward, and the context MLP's
+ *                 backward beside the x path's (default 1; off while a profiler scope is open)
  *   "epi_fuse"    bit 0: a block's FFN SwiGLU val * silu(glu) is written by the up-projection's
  *                 GEMM epilogue (each 256-column output tile holds matching val and glu columns);
  *                 bit 1: the per-head q/k RMS norm, RoPE and head-major bf16 layout of the
@@ -174,7 +177,7 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  * Every setting gives results identical to the defaults bit for bit except gemm_split, gemm_cfg,
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
  * kv_stack, attn_fwd32, head_f32 and act_bf16, which change the rounding or the f32 summation order
- * (prep_side changes only the stream a refresh runs on; epi_fuse only which kernel computes
+ * (prep_side and head_quick change only the stream work runs on; epi_fuse only which kernel computes
  * SwiGLU and the head preparation).
  * Not to
  * be changed while a graph is being captured. */

@@ -803,7 +803,21 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     const bool join_here = ctx->side_defer == 0;
     const uint64_t forks0 = ctx->side_forks;
     SideDeferScope defer(ctx);
-    // conditioning
+    // The head: three chains of short dependent launches that meet at the first block. The context
+    // MLP and the x path run on the third stream beside the modulation chain (gcond = gce(ge + te))
+    // on the main stream; both wait on little but memory latency, the more so beside the grouped
+    // refresh, so two chains in flight take about as long as the longer one.
+    const bool quick = ctx->head_quick && side_usable(ctx);
+    if (quick) quick_fork(ctx);   // the head linears' refresh is complete
+    {
+        OnQuick oq(ctx, quick);
+        mlp_fwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->context);
+        lin_fwd(ctx, d, H_PRE_CONV, x_t, NT, d->xp);
+        launch(ctx, "dit_head", add_kernel, dim3(nblk(NT * c.io)), (const float*)d->xp, x_t, NT * c.io, d->xp);
+        lin_fwd(ctx, d, H_PROJ_IN, d->xp, NT, d->xi);
+        launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B,
+               T, c.mem_tokens, (int)D, d->xs[0]);
+    }
     launch(ctx, "dit_head", expo_kernel, dim3(nblk((int64_t)B * (c.time_dim / 2))), t, B, c.time_dim,
            logf(c.time_min_freq), logf(c.time_max_freq), d->tf);
     mlp_fwd(ctx, d, H_TIME0, d->tf, B, d->te_h, d->te_a, d->te);
@@ -811,13 +825,7 @@ void forward(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* t, const
     launch(ctx, "dit_head", add_kernel, dim3(nblk(B * D)), (const float*)d->ge, (const float*)d->te, (int64_t)B * D,
            d->gsum);
     mlp_fwd(ctx, d, H_GCE0, d->gsum, B, d->gce_h, d->gce_a, d->gcond);   // dim -> dim -> 6 dim
-    mlp_fwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->context);
-    // x path
-    lin_fwd(ctx, d, H_PRE_CONV, x_t, NT, d->xp);
-    launch(ctx, "dit_head", add_kernel, dim3(nblk(NT * c.io)), (const float*)d->xp, x_t, NT * c.io, d->xp);
-    lin_fwd(ctx, d, H_PROJ_IN, d->xp, NT, d->xi);
-    launch(ctx, "dit_head", concat_mem_kernel, dim3(nblk((int64_t)B * S * D)), d->memtok, (const float*)d->xi, B, T,
-           c.mem_tokens, (int)D, d->xs[0]);
+    if (quick) quick_join(ctx);
     join_group(ctx, d);   // every product from here on reads a member of the grouped refresh
     if (d->kvs) lin_stack_forward(ctx, d->kvs, d->context, NC);   // every block's context K/V
     // the inpaint conditioning, zero-padded to local.0's kp input columns; every block's local MLP
@@ -941,11 +949,18 @@ void accumulate_body(sa3k_ctx* ctx, sa3k_dit* d, const float* x_t, const float* 
         }
         {
             SideHeld hold(ctx, two);
+            // the context MLP on the third stream beside the x path
+            const bool quick = two && ctx->head_quick;
+            if (quick) quick_fork(ctx);
+            {
+                OnQuick oq(ctx, quick);
+                mlp_bwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->dctx, nullptr);
+            }
             launch(ctx, "dit_head", gather_frames_kernel, dim3(nblk(NT * D)), (const float*)dcur, B, T, c.mem_tokens,
                    (int)D, d->dxi);
             lin_bwd(ctx, d, H_PROJ_IN, d->xp, NT, d->dxi, d->dxp, 0);
             lin_bwd(ctx, d, H_PRE_CONV, x_t, NT, d->dxp, nullptr, 0);
-            mlp_bwd(ctx, d, H_COND0, cross, NC, d->ce_h, d->ce_a, d->dctx, nullptr);
+            if (quick) quick_join(ctx);
         }
         if (two) side_join(ctx);   // AdamW reads every gradient
     }

@@ -80,10 +80,10 @@ float* gemm_workspace_bytes(sa3k_ctx* ctx, size_t bytes) {
                                              std::to_string(ctx->ws_fixed_bytes) + " bytes available");
         return ctx->ws_fixed;
     }
-    // one workspace per stream: work on the second stream runs beside the main stream's
-    const bool side = ctx->stream == ctx->side_stream;
-    void*& ws = side ? ctx->gemm_ws_side : ctx->gemm_ws;
-    size_t& have = side ? ctx->gemm_ws_side_bytes : ctx->gemm_ws_bytes;
+    // one workspace per stream: work on the second and third streams runs beside the main stream's
+    const bool side = ctx->stream == ctx->side_stream, quick = ctx->stream == ctx->quick_stream;
+    void*& ws = side ? ctx->gemm_ws_side : quick ? ctx->gemm_ws_quick : ctx->gemm_ws;
+    size_t& have = side ? ctx->gemm_ws_side_bytes : quick ? ctx->gemm_ws_quick_bytes : ctx->gemm_ws_bytes;
     if (bytes > have) {
         SA3K_REQUIRE(!ctx->capturing, "the split-K workspace cannot grow while a graph is being captured");
         if (ws) {

@@ -244,6 +244,31 @@ __global__ __launch_bounds__(kThreads) void dora_terms_kernel(const float* __res
 template <class CT>
 __device__ inline float ld_ct(const CT* p, int64_t i) { return (float)p[i]; }
 
+// Stage rows [nb, nb + cnt) of a [tokens][r] rank matrix into sh[64][R] (rows past cnt and ranks
+// past r read as 0). Every thread's loads are issued before the first LDS write: one memory round
+// trip per 64-row chunk.
+template <class CT, int R>
+__device__ inline void stage_rank_rows(float (*sh)[R], const CT* __restrict__ P, int64_t nb, int cnt, int r) {
+    constexpr int kPer = 64 * R / kThreads;
+    static_assert(64 * R % kThreads == 0, "whole staging rounds");
+    float v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int k = threadIdx.x + j * kThreads, row = k / R, a = k % R;
+        v[j] = (row < cnt && a < r) ? ld_ct(P, (nb + row) * r + a) : 0.f;
+    }
+    __syncthreads();   // the previous chunk's readers are done
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int k = threadIdx.x + j * kThreads;
+        sh[k / R][k % R] = v[j];
+    }
+    __syncthreads();
+}
+
+// token rows whose loads one thread issues before their sums (one memory round trip per batch)
+constexpr int kColBatch = 32;
+
 // Rows [r0, r1) of dY: dU = dY*d (stored, compute type), partial gd = sum dY*U and
 // partial (dU^T Hc)[o][a] = sum_n dU[n][o] Hc[n][a]. One thread per column o.
 template <class CT, int R>
@@ -260,21 +285,28 @@ __global__ __launch_bounds__(kThreads) void colred_dy_kernel(const float* __rest
     for (int a = 0; a < R; ++a) acc[a] = 0.f;
     for (int64_t nb = r0; nb < r1; nb += 64) {
         const int cnt = (int)min((int64_t)64, r1 - nb);
-        __syncthreads();
-        for (int k = threadIdx.x; k < cnt * R; k += kThreads) {
-            const int row = k / R, a = k - row * R;
-            hs[row][a] = a < r ? ld_ct(Hc, (nb + row) * r + a) : 0.f;
-        }
-        __syncthreads();
+        stage_rank_rows<CT, R>(hs, Hc, nb, cnt, r);
         if (o < out) {
-            for (int row = 0; row < cnt; ++row) {
-                const int64_t n = nb + row;
-                const float y = dY[n * out + o];
-                const float du = y * dd;
-                if (U) gd += y * ld_ct(U, n * out + o);
-                dU[n * out + o] = (CT)du;
+            // the sums keep the row order
+            for (int row0 = 0; row0 < cnt; row0 += kColBatch) {
+                float y[kColBatch], u[kColBatch];
 #pragma unroll
-                for (int a = 0; a < R; ++a) acc[a] += du * hs[row][a];
+                for (int k = 0; k < kColBatch; ++k) {
+                    const int64_t n = nb + min(row0 + k, cnt - 1);
+                    y[k] = dY[n * out + o];
+                    u[k] = U ? ld_ct(U, n * out + o) : 0.f;
+                }
+#pragma unroll
+                for (int k = 0; k < kColBatch; ++k) {
+                    const int row = row0 + k;
+                    if (row < cnt) {
+                        const float du = y[k] * dd;
+                        if (U) gd += y[k] * u[k];
+                        dU[(nb + row) * out + o] = (CT)du;
+#pragma unroll
+                        for (int a = 0; a < R; ++a) acc[a] += du * hs[row][a];
+                    }
+                }
             }
         }
     }
@@ -299,17 +331,20 @@ __global__ __launch_bounds__(kThreads) void colred_x_kernel(const XT* __restrict
     for (int a = 0; a < R; ++a) acc[a] = 0.f;
     for (int64_t nb = r0; nb < r1; nb += 64) {
         const int cnt = (int)min((int64_t)64, r1 - nb);
-        __syncthreads();
-        for (int k = threadIdx.x; k < cnt * R; k += kThreads) {
-            const int row = k / R, a = k - row * R;
-            gs[row][a] = a < r ? ld_ct(Gm, (nb + row) * r + a) : 0.f;
-        }
-        __syncthreads();
+        stage_rank_rows<CT, R>(gs, Gm, nb, cnt, r);
         if (i < in) {
-            for (int row = 0; row < cnt; ++row) {
-                const float x = (float)X[(nb + row) * in + i];
+            for (int row0 = 0; row0 < cnt; row0 += kColBatch) {
+                float x[kColBatch];
 #pragma unroll
-                for (int a = 0; a < R; ++a) acc[a] += x * gs[row][a];
+                for (int k = 0; k < kColBatch; ++k) x[k] = (float)X[(nb + min(row0 + k, cnt - 1)) * in + i];
+#pragma unroll
+                for (int k = 0; k < kColBatch; ++k) {
+                    const int row = row0 + k;
+                    if (row < cnt) {
+#pragma unroll
+                        for (int a = 0; a < R; ++a) acc[a] += x[k] * gs[row][a];
+                    }
+                }
             }
         }
     }
@@ -693,9 +728,10 @@ int64_t tn_rows_per(int64_t cols, int64_t N, int rs) {
 // partial sums of the column reductions: one buffer per context, shared by every linear (used
 // in turn on the context stream); it grows outside graph capture only
 float* reduce_workspace(sa3k_ctx* ctx, size_t bytes) {
-    const bool side = ctx->stream == ctx->side_stream;   // one workspace per stream
-    void*& ws = side ? ctx->red_ws_side : ctx->red_ws;
-    size_t& have = side ? ctx->red_ws_side_bytes : ctx->red_ws_bytes;
+    // one workspace per stream
+    const bool side = ctx->stream == ctx->side_stream, quick = ctx->stream == ctx->quick_stream;
+    void*& ws = side ? ctx->red_ws_side : quick ? ctx->red_ws_quick : ctx->red_ws;
+    size_t& have = side ? ctx->red_ws_side_bytes : quick ? ctx->red_ws_quick_bytes : ctx->red_ws_bytes;
     if (bytes > have) {
         SA3K_REQUIRE(!ctx->capturing, "the reduction workspace cannot grow while a graph is being captured");
         if (ws) {
@@ -1643,6 +1679,16 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
         }
         if (c + 1 < nc) load(i0 + 64);   // the next chunk in flight
         __syncthreads();   // the chunk is staged; the previous chunk's W_eff tiles are consumed
+        // The P product's A operands (this chunk's A rows) are read before the second barrier: a
+        // wave past that barrier may already be writing the next chunk's A rows into acs.
+        bf16x8 pa[2][2] = {};
+        if (dora) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                pa[ks][0] = *reinterpret_cast<const bf16x8*>(acs + l16 * CP + (32 * ks + 8 * g) * 2);
+                if (hi) pa[ks][1] = *reinterpret_cast<const bf16x8*>(acs + (16 + l16) * CP + (32 * ks + 8 * g) * 2);
+            }
+        }
         // W_eff at (row 16 wave + 4g + v, column 16j + l16)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1667,12 +1713,8 @@ __global__ __launch_bounds__(kThreads) void group_merge_kernel(const PrepDesc* _
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&et[16 * wave + l16][32 * ks + 8 * g]);
-                const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(acs + l16 * CP + (32 * ks + 8 * g) * 2);
-                p0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, a0, p0, 0, 0, 0);
-                if (hi) {
-                    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(acs + (16 + l16) * CP + (32 * ks + 8 * g) * 2);
-                    p1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, a1, p1, 0, 0, 0);
-                }
+                p0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, pa[ks][0], p0, 0, 0, 0);
+                if (hi) p1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, pa[ks][1], p1, 0, 0, 0);
             }
         }
         {   // 32 contiguous bytes of a W_eff row and of a W_eff^T row per thread, after every load.

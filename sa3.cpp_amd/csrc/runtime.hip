@@ -66,6 +66,7 @@ const OptionDef kOptions[] = {
     {"attn_fwd32", &sa3k_ctx::attn_fwd32, false},  {"head_f32", &sa3k_ctx::head_f32, true},
     {"prep_side", &sa3k_ctx::prep_side, true},     {"epi_fuse", &sa3k_ctx::epi_fuse, false},
     {"act_bf16", &sa3k_ctx::act_bf16, false},     {"gemm_prio", &sa3k_ctx::gemm_prio, true},
+    {"head_quick", &sa3k_ctx::head_quick, true},
 };
 constexpr int kNumOptions = (int)(sizeof(kOptions) / sizeof(kOptions[0]));
 
@@ -182,6 +183,8 @@ SA3K_API void sa3k_destroy(sa3k_ctx* ctx) {
     if (ctx->red_ws) (void)hipFree(ctx->red_ws);
     if (ctx->gemm_ws_side) (void)hipFree(ctx->gemm_ws_side);
     if (ctx->red_ws_side) (void)hipFree(ctx->red_ws_side);
+    if (ctx->gemm_ws_quick) (void)hipFree(ctx->gemm_ws_quick);
+    if (ctx->red_ws_quick) (void)hipFree(ctx->red_ws_quick);
     for (hipEvent_t e : ctx->side_ev)
         if (e) (void)hipEventDestroy(e);
     if (ctx->block_tail_ev) (void)hipEventDestroy(ctx->block_tail_ev);

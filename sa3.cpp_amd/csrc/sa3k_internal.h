@@ -92,6 +92,10 @@ struct sa3k_ctx {
     size_t gemm_ws_side_bytes = 0;
     void* red_ws_side = nullptr;
     size_t red_ws_side_bytes = 0;
+    void* gemm_ws_quick = nullptr;       // and on the third stream
+    size_t gemm_ws_quick_bytes = 0;
+    void* red_ws_quick = nullptr;
+    size_t red_ws_quick_bytes = 0;
     int gemm_fixup = 0;                   // split partials summed by the last split (no reduce launch):
                                           // 0 never, 1 always, 2 for small outputs only
     int* tile_counters = nullptr;         // [kMaxFixupTiles] arrival counters, zero between launches
@@ -101,6 +105,7 @@ struct sa3k_ctx {
     int attn_fwd32 = 1;                   // attention forward on 32x32x16 MFMA blocks, 32 queries per wave
     int prep_side = 1;                    // a DiT's bf16 group refresh on the second stream beside the f32 heads'
     int head_f32 = 1;                     // a DiT's head / tail linears on f32 MFMA (f32 / f16 bases)
+    int head_quick = 1;                   // a DiT's head chains partly on the third stream
     int epi_fuse = 3;                     // in GEMM epilogues where the tiles allow: 1 the FFN SwiGLU, 2 q/k head prep
     int act_bf16 = 1;                     // block backward reads bf16 copies: 1 of the FFN up output, 2 of qkv / qf
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,

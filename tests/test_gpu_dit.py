@@ -282,12 +282,14 @@ def test_dit_side_stream_matches_one_stream(ctx, local_dim):
     # the backward kernels forked to the context's second stream give the one-stream results bit for
     # bit, over two updates (adapter refresh and AdamW in between): with forks recorded by the
     # producer kernels or by separate event records, and with each block's last second-stream work
-    # joined at the block's end or overlapping the next block (two blocks); with the inpaint local
-    # conditioning, the local MLPs' forwards and backwards on the second stream too
+    # joined at the block's end or overlapping the next block (two blocks); with the head's context
+    # MLP and x path on the third stream or not; with the inpaint local conditioning, the local
+    # MLPs' forwards and backwards on the second stream too
     cfg = dict(CFG, window=5, local_dim=local_dim)
     tensors, adapters, inputs = db.random_dit(46, cfg, "full")
-    schedules = [dict(side_stream=0), dict(side_stream=1, fork_tail=0, late_join=0),
-                 dict(side_stream=1, fork_tail=1, late_join=0), dict(side_stream=1, fork_tail=1, late_join=1)]
+    schedules = [dict(side_stream=0), dict(side_stream=1, fork_tail=0, late_join=0, head_quick=0),
+                 dict(side_stream=1, fork_tail=1, late_join=0, head_quick=1),
+                 dict(side_stream=1, fork_tail=1, late_join=1, head_quick=1)]
     res = []
     try:
         for sched in schedules:
