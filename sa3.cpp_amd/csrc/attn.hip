@@ -23,6 +23,7 @@
 // sequence read as zeros. Two LDS stages: the DMA of block i+1 runs while block i is computed.
 //
 // window > 0 keeps keys with |q - k| <= window/2 (self-attention only); 0 is dense.
+#include "headprep.h"
 #include "sa3k_internal.h"
 
 #include <algorithm>
@@ -532,39 +533,26 @@ __global__ __launch_bounds__(kThreads) void attn_fwd32_kernel(FwdArgs a) {
 
 // ------------------------------------------------------------------------------------ backward
 // Dn_i[bh][q] = sum_d dO[b][q][h][d] * O_i[bh][q][d]; dOh[bh][q][d] = bf16(dO) (head-major).
-// Eight lanes per (bh, q), 8 dims each (32-byte dO, 16-byte O_i loads), the dot products summed
-// over the eight lanes by butterfly shuffles.
+// Sixteen lanes per (bh, q), 4 dims each (16-byte dO, 8-byte O_i loads), the dot products summed
+// over the 16 lanes by group16_sum: the same arithmetic as the epilogue of the product that
+// computes dO (the GEMM's attention dO epilogue), which writes these outputs itself where its
+// tiles allow.
 __global__ __launch_bounds__(kThreads) void attn_bwd_dot_kernel(const float* __restrict__ dO, const bf16* __restrict__ o1,
                                                                 const bf16* __restrict__ o2, int BH, int H, int Sq,
                                                                 bf16* __restrict__ dOh, float* __restrict__ dn1,
                                                                 float* __restrict__ dn2) {
-    const unsigned item = (blockIdx.x * kThreads + threadIdx.x) >> 3;
-    const int d0 = (threadIdx.x & 7) * 8;
-    const bool ok = item < (unsigned)BH * (unsigned)Sq;
-    float s1 = 0.f, s2 = 0.f;
-    if (ok) {
-        const unsigned bh = item / (unsigned)Sq, q = item - bh * (unsigned)Sq;
-        const unsigned b = bh / (unsigned)H, h = bh - b * (unsigned)H;
-        const float* src = dO + ((int64_t)b * Sq + q) * (H * HD) + h * HD + d0;
-        const float4 xa = *reinterpret_cast<const float4*>(src), xb = *reinterpret_cast<const float4*>(src + 4);
-        const int64_t idx = (int64_t)item * HD + d0;
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(o1 + idx), a2 = *reinterpret_cast<const bf16x8*>(o2 + idx);
-        const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        bf16x8 xo;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            xo[j] = (bf16)x[j];
-            s1 += x[j] * (float)a1[j];
-            s2 += x[j] * (float)a2[j];
-        }
-        *reinterpret_cast<bf16x8*>(dOh + idx) = xo;
-    }
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        s1 += __shfl_xor(s1, off, 64);
-        s2 += __shfl_xor(s2, off, 64);
-    }
-    if (ok && (threadIdx.x & 7) == 0) {
+    const unsigned item = (blockIdx.x * kThreads + threadIdx.x) >> 4;
+    const int d0 = (threadIdx.x & 15) * 4;
+    if (item >= (unsigned)BH * (unsigned)Sq) return;   // uniform over the item's 16 lanes
+    const unsigned bh = item / (unsigned)Sq, q = item - bh * (unsigned)Sq;
+    const unsigned b = bh / (unsigned)H, h = bh - b * (unsigned)H;
+    const float4 x = *reinterpret_cast<const float4*>(dO + ((int64_t)b * Sq + q) * (H * HD) + h * HD + d0);
+    const int64_t idx = (int64_t)item * HD + d0;
+    const uint2 a1 = *reinterpret_cast<const uint2*>(o1 + idx), a2 = *reinterpret_cast<const uint2*>(o2 + idx);
+    const bf16 xo[4] = {(bf16)x.x, (bf16)x.y, (bf16)x.z, (bf16)x.w};
+    *reinterpret_cast<uint2*>(dOh + idx) = __builtin_bit_cast(uint2, xo);
+    const float s1 = sa3k::group16_sum(sa3k::dot4_bf16(x, a1)), s2 = sa3k::group16_sum(sa3k::dot4_bf16(x, a2));
+    if (d0 == 0) {
         dn1[item] = s1;
         dn2[item] = s2;
     }
@@ -865,19 +853,20 @@ void attn_forward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2,
 void attn_backward(sa3k_ctx* ctx, const bf16* q1, const bf16* k1, const bf16* q2, const bf16* k2, const bf16* v,
                    const bf16* o1, const bf16* o2, const float* lse1, const float* lse2, const float* dO,
                    int B, int H, int Sq, int Sk, int window, float scale, bf16* dOh, float* dn1, float* dn2,
-                   float* dq1, float* dk1, float* dq2, float* dk2, float* dv) {
+                   float* dq1, float* dk1, float* dq2, float* dk2, float* dv, bool dot_done) {
     SA3K_REQUIRE(window == 0 || Sq == Sk, "a window needs self-attention (Sq == Sk)");
     const int BH = B * H;
     // dQ (third stream) and dK/dV (main stream) only share inputs: they run side by side once the
-    // row dots are done (the dot kernel records the fork event)
+    // row dots are done (the dot kernel records the fork event). dot_done: the product that
+    // computed dO has written dOh and the row dots (dO itself is not read).
     const bool side = side_usable(ctx);
-    if (side) fork_arm(ctx);
-    {
+    if (!dot_done) {
+        if (side) fork_arm(ctx);
         KernelScope ks(ctx, Sq == Sk ? "attn_bwd_dot" : "attn_bwd_dot_cross");
         const int64_t items = (int64_t)BH * Sq;
-        SA3K_REQUIRE(items * 8 < ((int64_t)1 << 32), "too many (batch, head, query) rows for one attention call");
-        launch_k(ctx, true, attn_bwd_dot_kernel, dim3((unsigned)ceil_div(items * 8, kThreads)), dim3(kThreads), 0, dO,
-                 o1, o2, BH, H, Sq, dOh, dn1, dn2);
+        SA3K_REQUIRE(items * 16 < ((int64_t)1 << 32), "too many (batch, head, query) rows for one attention call");
+        launch_k(ctx, true, attn_bwd_dot_kernel, dim3((unsigned)ceil_div(items * 16, kThreads)), dim3(kThreads), 0,
+                 dO, o1, o2, BH, H, Sq, dOh, dn1, dn2);
         SA3K_LAUNCHED();
     }
     BwdArgs a{q1, k1, q2, k2, v, dOh, lse1, lse2, dn1, dn2, Sq, Sk, window, scale, dq1, dq2, dk1, dk2, dv, 1, nullptr};
@@ -937,7 +926,7 @@ SA3K_API int sa3k_diff_attn_bwd(sa3k_ctx* ctx, const void* q1, const void* k1, c
         const int64_t n = (int64_t)B * H * Sq;
         sa3k::attn_backward(ctx, (const bf16*)q1, (const bf16*)k1, (const bf16*)q2, (const bf16*)k2, (const bf16*)v,
                             (const bf16*)o1, (const bf16*)o2, lse1, lse2, dO, B, H, Sq, Sk, window, scale,
-                            (bf16*)scratch_dOh, scratch_dn, scratch_dn + n, dq1, dk1, dq2, dk2, dv);
+                            (bf16*)scratch_dOh, scratch_dn, scratch_dn + n, dq1, dk1, dq2, dk2, dv, false);
     });
 }
 

@@ -28,7 +28,7 @@ void attn_forward(sa3k_ctx*, const bf16*, const bf16*, const bf16*, const bf16*,
                   float, bf16*, bf16*, bf16*, float*, float*);
 void attn_backward(sa3k_ctx*, const bf16*, const bf16*, const bf16*, const bf16*, const bf16*, const bf16*,
                    const bf16*, const float*, const float*, const float*, int, int, int, int, int, float, bf16*,
-                   float*, float*, float*, float*, float*, float*, float*);
+                   float*, float*, float*, float*, float*, float*, float*, bool);
 }
 
 namespace {
@@ -942,9 +942,14 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
                    w->dladd);
         }
         // x2 = x1 + yc
-        lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4]);
+        // the out-projections' dX products write the attention backward's dOh and row dots from
+        // their epilogues where their tiles allow (epi_fuse bit 2; dO itself is then not written)
+        int dot_done = 0;
+        const AttnDot adc{w->co1, w->co2, w->dOh, w->dn, w->dn + nq, H, S};
+        lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4],
+                        (ctx->epi_fuse & 4) ? &adc : nullptr, &dot_done);
         attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,
-                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
+                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv, dot_done != 0);
         PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, nullptr,
                        {{w->dq1, b->cq_g, 0}, {w->dq2, b->cq_g, 0}, {}, {}, {}}, w->rcq, nullptr,
                        lin_du(b->L[2]), lin_du_scale(b->L[2]), 0, w->qfb};
@@ -966,9 +971,12 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         if (side_usable(ctx)) fork_arm(ctx);
         norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, nullptr, b->L[1]);
         colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
-        lin_backward_du(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dob, 0, dA[1], dB[1], dmt[1]);
+        dot_done = 0;
+        const AttnDot ads{w->o1, w->o2, w->dOh, w->dn, w->dn + nq, H, S};
+        lin_backward_du(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dob, 0, dA[1], dB[1], dmt[1],
+                        (ctx->epi_fuse & 4) ? &ads : nullptr, &dot_done);
         attn_backward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, w->o1, w->o2, w->l1, w->l2, w->dob, B, H, S, S, c.window,
-                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv);
+                      scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv, dot_done != 0);
         PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, w->rope_tab,
                        {{w->dq1, b->sq_g, 1}, {w->dk1, b->sk_g, 1}, {w->dv, nullptr, 0}, {w->dq2, b->sq_g, 1}, {w->dk2, b->sk_g, 1}},
                        w->rq, nullptr, lin_du(b->L[0]), lin_du_scale(b->L[0]), 0, w->qkvb};

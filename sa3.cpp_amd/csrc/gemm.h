@@ -49,6 +49,19 @@ struct HeadPrep {
     float* rstd = nullptr;
 };
 
+// The attention backward's inputs from the product that computes dO = the gradient of the attention
+// output (rows b Sq + t, columns h 64 + d): dOh [B][H][Sq][64] = bf16(dO) and the row dots
+// dn1/dn2 [B][H][Sq] = sum_d dO . o1/o2 over each head's 64 dims, o1/o2 [B][H][Sq][64] the two
+// branch outputs of the forward.
+struct AttnDot {
+    const bf16* o1 = nullptr;
+    const bf16* o2 = nullptr;
+    bf16* doh = nullptr;
+    float* dn1 = nullptr;
+    float* dn2 = nullptr;
+    int H = 0, Sq = 0;
+};
+
 struct GemmDesc {
     int prec = SA3K_PREC_BF16;   // compute type
     int a_src = SRC_BF16;        // SRC_BF16 or SRC_F32
@@ -122,6 +135,12 @@ struct GemmDesc {
     // callers that keep a bf16 copy Cb for later passes need the f32 C only for their own
     // separate SwiGLU / head preparation kernels)
     int c_unfused_only = 0;
+    // The attention dO epilogue (AttnDot; doh null: off) where the chosen tiles allow it (the bf16
+    // DMA kernel's staged epilogue with tiles of 64 or more columns, no split over K, no
+    // accumulation, N = H 64, M = B Sq): the outputs of AttnDot are written in place of C (C is not
+    // written) and *ad_done is set; else C is written and the caller computes them from it.
+    AttnDot ad;
+    int* ad_done = nullptr;
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

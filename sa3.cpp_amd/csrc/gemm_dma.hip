@@ -67,6 +67,8 @@ struct DmaParams {
     int* hp_done;   // host-side, like sw_done
     int c_unfused_only;   // host-side (GemmDesc::c_unfused_only)
     int prio;             // raise the wave priority over the MFMA clusters of the K loop
+    AttnDot ad;           // the attention dO epilogue (GemmDesc::ad; doh null: off)
+    int* ad_done;         // host-side, like sw_done
 };
 
 namespace {
@@ -421,6 +423,25 @@ __device__ inline void head_prep_store(const DmaParams& p, const HeadPrepLane& l
     *reinterpret_cast<uint2*>(outp + ((int64_t)b * p.hp.H * p.hp.Sx + t) * kHeadDim) = __builtin_bit_cast(uint2, o);
 }
 
+// The attention dO epilogue at row m (main rows), output column nq (a multiple of 4 below N) with
+// final values v: the bf16 head-major copy and, summed over the head's aligned 16-lane group (every
+// lane of which takes this path: rows and 64-column heads are uniform over it), the row dots.
+__device__ inline void attn_dot_store(const DmaParams& p, int64_t m, int64_t nq, const float4& v) {
+    const unsigned sq = (unsigned)p.ad.Sq, b = (unsigned)m / sq, t = (unsigned)m - b * sq;
+    const int d0 = (int)(nq & (kHeadDim - 1));
+    const int64_t row = ((int64_t)b * p.ad.H + (nq >> 6)) * sq + t;   // kHeadDim = 64
+    const int64_t idx = row * kHeadDim + d0;
+    const uint2 a1 = *reinterpret_cast<const uint2*>(p.ad.o1 + idx);
+    const uint2 a2 = *reinterpret_cast<const uint2*>(p.ad.o2 + idx);
+    const bf16 o[4] = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
+    *reinterpret_cast<uint2*>(p.ad.doh + idx) = __builtin_bit_cast(uint2, o);
+    const float s1 = group16_sum(dot4_bf16(v, a1)), s2 = group16_sum(dot4_bf16(v, a2));
+    if (d0 == 0) {
+        p.ad.dn1[row] = s1;
+        p.ad.dn2[row] = s2;
+    }
+}
+
 // The store phase of one staged-epilogue pass over tile rows [rb, rb + ER) (staged in st, EROW
 // floats per row): thread tid stores chunk column cq (output column nq, column factors kq) of tile
 // rows tid / CPR + i NT / CPR. With 256-column tiles a wave holds one row, which the paired SwiGLU
@@ -471,6 +492,7 @@ __device__ inline void staged_store(const DmaParams& p, const float* st, int64_t
         if (BN == 256 && sw_tile && main_row) swiglu_pair_store(p, gp + (int64_t)dr * p.sw_ldg, lo, v);
         if constexpr (HP)
             if (hp_tile && main_row) head_prep_store(p, hl, (int)m, hb, ht, nq, v, tabs + (rb + r) * p.hp.rope_dims, outp, rsp);
+        if (p.ad.doh && main_row && main_col) attn_dot_store(p, m, nq, v);
     }
 }
 
@@ -1304,6 +1326,18 @@ bool headprep_ok(const DmaParams& p, int splits) {
     return true;
 }
 
+// Whether the attention dO epilogue fits this launch: one workgroup per tile, the staged epilogue
+// with whole heads in each 16-lane group of a row (tiles of 64 or more columns), no accumulation,
+// N = H x 64, M = B x Sq, 8-byte aligned bf16 rows.
+bool attn_dot_ok(const DmaParams& p, int splits, int bn) {
+    const AttnDot& a = p.ad;
+    if (!a.doh || splits != 1 || !p.vec_epi || p.accumulate || bn < 64) return false;
+    if (a.H <= 0 || a.Sq <= 0 || p.N != (int64_t)a.H * kHeadDim || p.M % a.Sq != 0 || p.M >= ((int64_t)1 << 31))
+        return false;
+    return a.o1 && a.o2 && a.dn1 && a.dn2 && (uintptr_t)a.doh % 8 == 0 && (uintptr_t)a.o1 % 8 == 0 &&
+           (uintptr_t)a.o2 % 8 == 0;
+}
+
 template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
@@ -1361,6 +1395,14 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                     ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
     settle_swiglu(p, BN, splits, KN, BQ);
+    if (p.ad.doh) {
+        if (attn_dot_ok(p, splits, BN)) {   // the epilogue writes the attention inputs instead of C
+            if (p.ad_done) *p.ad_done = 1;
+            p.C = nullptr;
+        } else {
+            p.ad.doh = nullptr;   // the caller computes them from C
+        }
+    }
     if constexpr (HP) {
         if (!headprep_ok(p, splits)) {   // the caller prepares the heads: the plain instantiation
             p.hp.parts = 0;
@@ -1424,6 +1466,7 @@ bool vec_epi_ok(const DmaParams& p) {
 }
 
 void launch_big(sa3k_ctx* ctx, DmaParams p) {
+    p.ad.doh = nullptr;   // the attention dO epilogue: the DMA kernel's only
     constexpr int BM = 256, BN = 256;
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
@@ -1594,6 +1637,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.bs_bytes = 0;
     p.sw_half = d.sw_half; p.sw_g = d.sw_g; p.sw_ldg = d.sw_ldg; p.sw_done = d.sw_done;
     p.hp = d.hp; p.hp_done = d.hp_done; p.c_unfused_only = d.c_unfused_only;
+    p.ad = d.ad; p.ad_done = d.ad_done;
     p.prio = ctx->gemm_prio;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);

@@ -43,6 +43,9 @@ __device__ inline void rope_tab4(int d0, int rope, const float* row_tab, float4&
 // Rotates y in place with the table entries of rope_tab4; lanes past rope_dims keep y. sign -1:
 // the inverse rotation. Every lane of the wave takes part (the partner values come by shuffle).
 __device__ inline void rope4_cs(float4& y, int d0, int rope, const float4& cs, const float4& sn, float sign) {
+    // explicit fused multiply-adds, no contraction left to the compiler: the prep kernels and the
+    // projection epilogues compile this in different code and must round alike
+#pragma clang fp contract(off)
     const int half = rope >> 1;
     const bool rot = d0 < rope, first = d0 < half;
     const int lane = threadIdx.x & 63;
@@ -53,8 +56,23 @@ __device__ inline void rope4_cs(float4& y, int d0, int rope, const float4& cs, c
     const float cc[4] = {cs.x, cs.y, cs.z, cs.w}, ss[4] = {sign * sn.x, sign * sn.y, sign * sn.z, sign * sn.w};
     float o[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) o[u] = first ? ys[u] * cc[u] - ps[u] * ss[u] : ps[u] * ss[u] + ys[u] * cc[u];
+    for (int u = 0; u < 4; ++u)
+        o[u] = first ? __builtin_fmaf(ys[u], cc[u], -(ps[u] * ss[u])) : __builtin_fmaf(ps[u], ss[u], ys[u] * cc[u]);
     y = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// The attention backward's row dot over a head, this lane's share: y . o for four f32 values y and
+// four bf16 values o, in a fixed order (one product, then three fused multiply-adds). The separate
+// dot kernel and the dX product's epilogue both sum a head's 16 shares with group16_sum, so the two
+// paths give the same bits.
+__device__ inline float dot4_bf16(const float4& y, uint2 o) {
+#pragma clang fp contract(off)
+    typedef __bf16 b4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+    const b4 b = __builtin_bit_cast(b4, o);
+    float s = y.x * (float)b[0];
+    s = __builtin_fmaf(y.y, (float)b[1], s);
+    s = __builtin_fmaf(y.z, (float)b[2], s);
+    return __builtin_fmaf(y.w, (float)b[3], s);
 }
 
 // y: this lane's four values of the head as the projection produced them. Normalises them in
@@ -62,7 +80,8 @@ __device__ inline void rope4_cs(float4& y, int d0, int rope, const float4& cs, c
 // reciprocal square root), rotates them when rope is set, and returns r.
 __device__ inline float head_norm_rope4(float4& y, const float4& gm, bool rope, int d0, int rope_dims, float eps,
                                         const float4& cs, const float4& sn) {
-    const float ss = y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+#pragma clang fp contract(off)   // as in rope4_cs: every fused multiply-add written out
+    const float ss = __builtin_fmaf(y.w, y.w, __builtin_fmaf(y.z, y.z, __builtin_fmaf(y.y, y.y, y.x * y.x)));
     const float r = __builtin_amdgcn_rsqf(group16_sum(ss) / kHeadDim + eps);
     y = make_float4(y.x * r * gm.x, y.y * r * gm.y, y.z * r * gm.z, y.w * r * gm.w);
     if (rope) rope4_cs(y, d0, rope_dims, cs, sn, 1.0f);

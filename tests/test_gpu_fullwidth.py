@@ -104,13 +104,16 @@ def test_dit_depth1_full_width_vs_oracle(ctx, local_dim):
 @pytest.mark.parametrize("S", [64 + 960, 64 + 1024])
 def test_block_epilogue_fusions_bitwise(ctx, S):
     """The GEMM-epilogue fusions (option epi_fuse) against their separate kernels at the benchmark's
-    width: the FFN SwiGLU from the up-projection's epilogue (bit 0) and the per-head q/k RMS norm,
-    RoPE and head-major bf16 outputs from the QKV and cross-query projections' epilogues (bit 1).
-    2 x 1024 tokens take the 128 x 256 DMA tiles without a split over K for every fused product,
-    2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles for the up-projection. Each fused
-    path evaluates the same expressions per element, so every output and gradient agrees bit for
-    bit; the profile shows which separate kernels ran (SwiGLU: forward + backward unfused, backward
-    only fused; head prep: self + cross query + context K/V unfused, context K/V only fused)."""
+    width: the FFN SwiGLU from the up-projection's epilogue (bit 0), the per-head q/k RMS norm,
+    RoPE and head-major bf16 outputs from the QKV and cross-query projections' epilogues (bit 1),
+    and the attention backward's head-major bf16 dO and row dots from the two out-projections' dX
+    epilogues (bit 2). 2 x 1024 tokens take the 128 x 256 DMA tiles without a split over K for the
+    forward products, 2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles for the
+    up-projection; the dX products take the small-grid 128 x 128 tiles. Each fused path evaluates the
+    same expressions per element, so every output and gradient agrees bit for bit; the profile
+    shows which separate kernels ran (SwiGLU: forward + backward unfused, backward only fused; head
+    prep: self + cross query + context K/V unfused, context K/V only fused; attention dots: self +
+    cross unfused, none fused)."""
     assert_shipped_options(ctx)
     B, Ctx = 2, 128
     print(f"epilogue fusions: B {B}, S {S}, Ctx {Ctx}", flush=True)
@@ -120,7 +123,7 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
     gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
     res, launches = {}, {}
     try:
-        for fuse in (3, 0, 1, 2):
+        for fuse in (7, 0, 1, 2, 3, 4):
             ctx.set_option("epi_fuse", fuse)
             ctx.profile(True)
             ctx.profile_reset()
@@ -128,25 +131,26 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
             rep = ctx.profile_report()
             ctx.profile(False)
             launches[fuse] = tuple(sum(v[0] for k, v in rep.items() if k.startswith(n))
-                                   for n in ("blk_swiglu", "blk_prep_fwd"))
+                                   for n in ("blk_swiglu", "blk_prep_fwd", "attn_bwd_dot"))
     finally:
         ctx.profile(False)
         ctx.set_options(ctx.defaults)
         gb.destroy()
-    assert launches == {3: (1, 1), 0: (2, 3), 1: (1, 3), 2: (2, 1)}, launches
-    for fuse in (0, 1, 2):
+    assert launches == {7: (1, 1, 0), 0: (2, 3, 2), 1: (1, 3, 2), 2: (2, 1, 2), 3: (1, 1, 2), 4: (2, 3, 0)}, launches
+    for fuse in (0, 1, 2, 3, 4):
         for k in ("out", "dx", "dctx", "dgcond"):
-            assert np.array_equal(res[3][k], res[fuse][k]), (fuse, k)
+            assert np.array_equal(res[7][k], res[fuse][k]), (fuse, k)
         for k in ("dA", "dB", "dm"):
             for t in range(7):
-                assert np.array_equal(res[3][k][t], res[fuse][k][t]), (fuse, f"{k}[{t}]")
+                assert np.array_equal(res[7][k][t], res[fuse][k][t]), (fuse, f"{k}[{t}]")
 
 
 @pytest.mark.parametrize("act_bf16", [1, 3])
 def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
     """The fused epilogues against the oracle directly: the full-width block at 2 x 136 tokens with
     the split over K and the small-grid tile switched off, so that the up-projection, QKV and
-    cross-query products take unsplit 128 x 256 tiles and the fusions apply (shipped, these small
+    cross-query products and the out-projections' dX products take unsplit 128 x 256 tiles and the
+    fusions apply (shipped, these small
     grids take split or 64 x 128 tiles and the separate kernels, which the other full-width tests
     cover); the backward reading the bf16 copy of the FFN up-projection's output (act_bf16 1, the
     default) and also those of the QKV and cross-query outputs (3)."""
@@ -169,8 +173,9 @@ def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
         ctx.profile(False)
         ctx.set_options(ctx.defaults)
         gb.destroy()
-    n = tuple(sum(v[0] for k, v in rep.items() if k.startswith(p)) for p in ("blk_swiglu", "blk_prep_fwd"))
-    assert n == (1, 1), n   # SwiGLU backward and the context K/V prep only
+    n = tuple(sum(v[0] for k, v in rep.items() if k.startswith(p))
+              for p in ("blk_swiglu", "blk_prep_fwd", "attn_bwd_dot"))
+    assert n == (1, 1, 0), n   # SwiGLU backward and the context K/V prep only; no attention dot kernel
     ref_out = bb.block_fwd(cfg, w, x, cx, gc)
     ref = bb.block_bwd(cfg, w, x, cx, gc, dout)
     worst = []
