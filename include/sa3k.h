@@ -166,9 +166,11 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 bit 1: the per-head q/k RMS norm, RoPE and head-major bf16 layout of the
  *                 attention inputs come out of the QKV and cross-query projections' epilogues;
  *                 bit 2: the attention backward's head-major bf16 dO and per-head row dots come
- *                 out of the out-projections' dX epilogues (the f32 dO is then not written); each
- *                 where the chosen tiles allow it (no split over K), else by its own kernel
- *                 (default 7)
+ *                 out of the out-projections' dX epilogues (the f32 dO is then not written);
+ *                 bit 3: the SwiGLU backward (the up-projection's bf16 dU) comes out of the FFN
+ *                 down-projection's dX epilogue, with act_bf16 bit 0 (the f32 dG is then not
+ *                 written); each where the chosen tiles allow it (no split over K), else by its
+ *                 own kernel (default 15)
  *   "gemm_prio"   1: the DMA GEMMs raise their waves' priority over the MFMA clusters of the K
  *                 loop, so a wave that has its operands keeps issuing while the others read
  *                 (default 1)
@@ -180,7 +182,7 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  * gemm_small, gemm_skinny, gemm_big, gemm_splits, gemm_dq, lin_merge, rank_cols, merge_kn,
  * kv_stack, attn_fwd32, head_f32 and act_bf16, which change the rounding or the f32 summation order
  * (prep_side and head_quick change only the stream work runs on; epi_fuse only which kernel computes
- * SwiGLU, the head preparation and the attention row dots).
+ * SwiGLU and its backward, the head preparation and the attention row dots).
  * Not to
  * be changed while a graph is being captured. */
 SA3K_API int sa3k_set_option(sa3k_ctx* ctx, const char* name, int value);

@@ -364,20 +364,14 @@ __global__ void swiglu_bwd_kernel(const float* __restrict__ dg, const FT* __rest
     const unsigned e = 4u * (unsigned)i4, row = e / (unsigned)I, c = e - row * (unsigned)I;
     const int64_t o = (int64_t)row * 2 * I + c;
     const float4 val = ldx4(F + o), glu = ldx4(F + o + I), d = ld4(dg + e);
-    float dv[4], dgl[4];
-    const float vs[4] = {val.x, val.y, val.z, val.w}, gs[4] = {glu.x, glu.y, glu.z, glu.w}, ds[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const float sg = sigmoidf_(gs[u]);
-        dv[u] = ds[u] * gs[u] * sg;
-        dgl[u] = ds[u] * vs[u] * (sg + gs[u] * sg * (1.0f - sg));
-    }
+    float4 dv, dgl;
+    swiglu_bwd4(val, glu, d, dv, dgl);   // the same function as the down-projection's dX epilogue
     if (du) {
-        st_du4(du + o, make_float4(dv[0], dv[1], dv[2], dv[3]), dsc, c);
-        st_du4(du + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]), dsc, (int64_t)I + c);
+        store_du4(du + o, dv, dsc, c);
+        store_du4(du + o + I, dgl, dsc, (int64_t)I + c);
     } else {
-        st4(dF + o, make_float4(dv[0], dv[1], dv[2], dv[3]));
-        st4(dF + o + I, make_float4(dgl[0], dgl[1], dgl[2], dgl[3]));
+        st4(dF + o, dv);
+        st4(dF + o + I, dgl);
     }
 }
 
@@ -925,13 +919,25 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         launch(ctx, "blk_gate", gate_bwd_kernel, dim3(nblk(N * D / 4)), dout, mv, 5, S, D, (int)(N * D / 4),
                (float*)nullptr, lin_du(b->L[6]), lin_du_scale(b->L[6]));
         colred(ctx, w, 1, dout, w->yf, nullptr, nullptr, 5, 5);
-        lin_backward_du(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dg, 0, dA[6], dB[6], dmt[6]);
-        if (w->Fb)
-            launch(ctx, "blk_swiglu", swiglu_bwd_kernel<bf16>, dim3(nblk(N * I / 4)), (const float*)w->dg,
-                   (const bf16*)w->Fb, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
-        else
-            launch(ctx, "blk_swiglu", swiglu_bwd_kernel<float>, dim3(nblk(N * I / 4)), (const float*)w->dg,
-                   (const float*)w->F, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]), lin_du_scale(b->L[5]));
+        // the FFN down-projection's dX product writes the up-projection's dU (the SwiGLU backward)
+        // from its epilogue where its tiles allow (epi_fuse bit 3; dG itself is then not written)
+        int sw_done = 0;
+        DxEpi se;
+        if ((ctx->epi_fuse & 8) && w->Fb) {
+            se.sb = SwiBwd{w->Fb, lin_du(b->L[5]), lin_du_scale(b->L[5]), I};
+            se.done = &sw_done;
+        }
+        lin_backward_du(ctx, b->L[6], SA3K_TYPE_BF16, w->g, N, w->dg, 0, dA[6], dB[6], dmt[6], &se);
+        if (!sw_done) {
+            if (w->Fb)
+                launch(ctx, "blk_swiglu", swiglu_bwd_kernel<bf16>, dim3(nblk(N * I / 4)), (const float*)w->dg,
+                       (const bf16*)w->Fb, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]),
+                       lin_du_scale(b->L[5]));
+            else
+                launch(ctx, "blk_swiglu", swiglu_bwd_kernel<float>, dim3(nblk(N * I / 4)), (const float*)w->dg,
+                       (const float*)w->F, I, (int)(N * I / 4), (float*)nullptr, lin_du(b->L[5]),
+                       lin_du_scale(b->L[5]));
+        }
         lin_backward_du(ctx, b->L[5], SA3K_TYPE_BF16, w->fin, N, w->dfin, 0, dA[5], dB[5], dmt[5]);
         colred(ctx, w, 0, w->dfin, w->x2, w->rs_f, b->ff_g, 0, 3);
         norm_bwd(w->dfin, w->x2, w->rs_f, b->ff_g, 3, dout, w->dx2, -1, b->L[4], nullptr);
@@ -945,9 +951,12 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         // the out-projections' dX products write the attention backward's dOh and row dots from
         // their epilogues where their tiles allow (epi_fuse bit 2; dO itself is then not written)
         int dot_done = 0;
-        const AttnDot adc{w->co1, w->co2, w->dOh, w->dn, w->dn + nq, H, S};
-        lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4],
-                        (ctx->epi_fuse & 4) ? &adc : nullptr, &dot_done);
+        DxEpi adc;
+        if (ctx->epi_fuse & 4) {
+            adc.ad = AttnDot{w->co1, w->co2, w->dOh, w->dn, w->dn + nq, H, S};
+            adc.done = &dot_done;
+        }
+        lin_backward_du(ctx, b->L[4], SA3K_TYPE_BF16, w->oc, N, w->doc, 0, dA[4], dB[4], dmt[4], &adc);
         attn_backward(ctx, w->cq1, w->ck1, w->cq2, w->ck2, w->cv, w->co1, w->co2, w->cl1, w->cl2, w->doc, B, H, S, Ctx, 0,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv, dot_done != 0);
         PrepBwdArgs bq{w->qf, 2, S, H, D, c.rope_dims, nullptr,
@@ -972,9 +981,12 @@ void sa3k::block_backward(sa3k_ctx* ctx, sa3k_block* b, sa3k_block_ws* w, const 
         norm_bwd(w->dhc, w->x1, w->rs_c, b->cross_g, -1, w->dx2, w->dx1, 2, nullptr, b->L[1]);
         colred(ctx, w, 1, w->dx1, w->y, nullptr, nullptr, 2, 2);
         dot_done = 0;
-        const AttnDot ads{w->o1, w->o2, w->dOh, w->dn, w->dn + nq, H, S};
-        lin_backward_du(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dob, 0, dA[1], dB[1], dmt[1],
-                        (ctx->epi_fuse & 4) ? &ads : nullptr, &dot_done);
+        DxEpi ads;
+        if (ctx->epi_fuse & 4) {
+            ads.ad = AttnDot{w->o1, w->o2, w->dOh, w->dn, w->dn + nq, H, S};
+            ads.done = &dot_done;
+        }
+        lin_backward_du(ctx, b->L[1], SA3K_TYPE_BF16, w->o, N, w->dob, 0, dA[1], dB[1], dmt[1], &ads);
         attn_backward(ctx, w->q1, w->k1, w->q2, w->k2, w->v, w->o1, w->o2, w->l1, w->l2, w->dob, B, H, S, S, c.window,
                       scale, w->dOh, w->dn, w->dn + nq, w->dq1, w->dk1, w->dq2, w->dk2, w->dv, dot_done != 0);
         PrepBwdArgs bs{w->qkv, 5, S, H, D, c.rope_dims, w->rope_tab,

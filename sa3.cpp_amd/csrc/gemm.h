@@ -62,6 +62,16 @@ struct AttnDot {
     int H = 0, Sq = 0;
 };
 
+// The SwiGLU backward of the FFN (src/dit.h:259-264) from the product that computes dG, the gradient
+// of g = val * silu(glu) ([M][I]): with F = [val | glu] ([M][2 I] bf16), du [M][2 I] = bf16(dsc (.)
+// [d val | d glu]) (dsc null: 1), the up-projection's output gradient as its backward reads it.
+struct SwiBwd {
+    const bf16* F = nullptr;
+    bf16* du = nullptr;
+    const float* dsc = nullptr;
+    int64_t I = 0;
+};
+
 struct GemmDesc {
     int prec = SA3K_PREC_BF16;   // compute type
     int a_src = SRC_BF16;        // SRC_BF16 or SRC_F32
@@ -135,12 +145,14 @@ struct GemmDesc {
     // callers that keep a bf16 copy Cb for later passes need the f32 C only for their own
     // separate SwiGLU / head preparation kernels)
     int c_unfused_only = 0;
-    // The attention dO epilogue (AttnDot; doh null: off) where the chosen tiles allow it (the bf16
-    // DMA kernel's staged epilogue with tiles of 64 or more columns, no split over K, no
-    // accumulation, N = H 64, M = B Sq): the outputs of AttnDot are written in place of C (C is not
-    // written) and *ad_done is set; else C is written and the caller computes them from it.
+    // Backward epilogues that write what the consumer of C needs in place of C: the attention dO
+    // epilogue (AttnDot; doh null: off; N = H 64, M = B Sq) and the SwiGLU backward (SwiBwd; du
+    // null: off; N = I), where the chosen tiles allow it (the bf16 DMA kernels' staged epilogues, no
+    // split over K, no accumulation; the attention dots on tiles of 64 or more columns). C is then
+    // not written and *bwd_done is set; else C is written and the caller computes them from it.
     AttnDot ad;
-    int* ad_done = nullptr;
+    SwiBwd sb;
+    int* bwd_done = nullptr;
 };
 
 // Enqueue one GEMM on the context stream (validates shapes, picks the kernel and tile

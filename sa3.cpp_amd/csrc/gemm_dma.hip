@@ -68,7 +68,8 @@ struct DmaParams {
     int c_unfused_only;   // host-side (GemmDesc::c_unfused_only)
     int prio;             // raise the wave priority over the MFMA clusters of the K loop
     AttnDot ad;           // the attention dO epilogue (GemmDesc::ad; doh null: off)
-    int* ad_done;         // host-side, like sw_done
+    SwiBwd sb;            // the SwiGLU backward epilogue (GemmDesc::sb; du null: off)
+    int* bwd_done;        // host-side, like sw_done
 };
 
 namespace {
@@ -442,6 +443,18 @@ __device__ inline void attn_dot_store(const DmaParams& p, int64_t m, int64_t nq,
     }
 }
 
+// The SwiGLU backward epilogue at row m (main rows), output column nq (a multiple of 4 below N = I)
+// with final values v = dG: both halves of the up-projection's dU from the bf16 [val | glu] row.
+__device__ inline void swiglu_bwd_store(const DmaParams& p, int64_t m, int64_t nq, const float4& v) {
+    const int64_t o = m * 2 * p.sb.I + nq;
+    const float4 val = bf16x4_to_f4(*reinterpret_cast<const uint2*>(p.sb.F + o));
+    const float4 glu = bf16x4_to_f4(*reinterpret_cast<const uint2*>(p.sb.F + o + p.sb.I));
+    float4 dv, dgl;
+    swiglu_bwd4(val, glu, v, dv, dgl);
+    store_du4(p.sb.du + o, dv, p.sb.dsc, nq);
+    store_du4(p.sb.du + o + p.sb.I, dgl, p.sb.dsc, p.sb.I + nq);
+}
+
 // The store phase of one staged-epilogue pass over tile rows [rb, rb + ER) (staged in st, EROW
 // floats per row): thread tid stores chunk column cq (output column nq, column factors kq) of tile
 // rows tid / CPR + i NT / CPR. With 256-column tiles a wave holds one row, which the paired SwiGLU
@@ -493,6 +506,7 @@ __device__ inline void staged_store(const DmaParams& p, const float* st, int64_t
         if constexpr (HP)
             if (hp_tile && main_row) head_prep_store(p, hl, (int)m, hb, ht, nq, v, tabs + (rb + r) * p.hp.rope_dims, outp, rsp);
         if (p.ad.doh && main_row && main_col) attn_dot_store(p, m, nq, v);
+        if (p.sb.du && main_row && main_col) swiglu_bwd_store(p, m, nq, v);
     }
 }
 
@@ -1337,6 +1351,24 @@ bool attn_dot_ok(const DmaParams& p, int splits, int bn) {
     return a.o1 && a.o2 && a.dn1 && a.dn2 && (uintptr_t)a.doh % 8 == 0 && (uintptr_t)a.o1 % 8 == 0 &&
            (uintptr_t)a.o2 % 8 == 0;
 }
+// Whether the SwiGLU backward epilogue fits: one workgroup per tile, the staged epilogue, no
+// accumulation, N = I (a multiple of 4), 8-byte aligned bf16 rows, a 16-byte aligned row scale.
+bool swiglu_bwd_ok(const DmaParams& p, int splits) {
+    const SwiBwd& b = p.sb;
+    if (!b.du || !b.F || splits != 1 || !p.vec_epi || p.accumulate || p.N != b.I || b.I % 4 != 0) return false;
+    return (uintptr_t)b.F % 8 == 0 && (uintptr_t)b.du % 8 == 0 && (!b.dsc || (uintptr_t)b.dsc % 16 == 0);
+}
+// Keep the backward epilogues this launch can run (then C is not written and *bwd_done is set);
+// switch the others off, so that C is written for the caller's own kernels.
+void settle_bwd_epilogues(DmaParams& p, int splits, int bn) {
+    if (!p.ad.doh && !p.sb.du) return;
+    if (p.ad.doh && !attn_dot_ok(p, splits, bn)) p.ad.doh = nullptr;
+    if (p.sb.du && !swiglu_bwd_ok(p, splits)) p.sb.du = nullptr;
+    if (p.ad.doh || p.sb.du) {
+        if (p.bwd_done) *p.bwd_done = 1;
+        p.C = nullptr;
+    }
+}
 
 template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false>
 void launch_dma(sa3k_ctx* ctx, DmaParams p) {
@@ -1395,14 +1427,7 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                     ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
     settle_swiglu(p, BN, splits, KN, BQ);
-    if (p.ad.doh) {
-        if (attn_dot_ok(p, splits, BN)) {   // the epilogue writes the attention inputs instead of C
-            if (p.ad_done) *p.ad_done = 1;
-            p.C = nullptr;
-        } else {
-            p.ad.doh = nullptr;   // the caller computes them from C
-        }
-    }
+    settle_bwd_epilogues(p, splits, BN);
     if constexpr (HP) {
         if (!headprep_ok(p, splits)) {   // the caller prepares the heads: the plain instantiation
             p.hp.parts = 0;
@@ -1466,7 +1491,6 @@ bool vec_epi_ok(const DmaParams& p) {
 }
 
 void launch_big(sa3k_ctx* ctx, DmaParams p) {
-    p.ad.doh = nullptr;   // the attention dO epilogue: the DMA kernel's only
     constexpr int BM = 256, BN = 256;
     const int64_t tiles = ceil_div(p.M + p.Mx, BM) * ceil_div(p.Nt, BN);
     const int64_t grid = ceil_div(tiles, 8) * 8;
@@ -1489,6 +1513,7 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
     settle_swiglu(p, BN, splits, p.b_kn != 0, 0);
+    settle_bwd_epilogues(p, splits, BN);
     if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
     {
         KernelScope ks(ctx, p.b_kn ? "gemm_big<256,256,kn,bf16>" : "gemm_big<256,256,bf16>",
@@ -1637,7 +1662,7 @@ void gemm_run_dma(sa3k_ctx* ctx, const GemmDesc& d) {
     p.bs_bytes = 0;
     p.sw_half = d.sw_half; p.sw_g = d.sw_g; p.sw_ldg = d.sw_ldg; p.sw_done = d.sw_done;
     p.hp = d.hp; p.hp_done = d.hp_done; p.c_unfused_only = d.c_unfused_only;
-    p.ad = d.ad; p.ad_done = d.ad_done;
+    p.ad = d.ad; p.sb = d.sb; p.bwd_done = d.bwd_done;
     p.prio = ctx->gemm_prio;
     if (d.prec == SA3K_PREC_BF16) dispatch_dma<true>(ctx, p);
     else dispatch_dma<false>(ctx, p);

@@ -1,8 +1,8 @@
-// Per-head preparation of the DiT's attention inputs (src/dit.h:207-217, src/nn.h:40-59): RMS
-// norm over a head's 64 dims with a per-dim gain, then NeoX RoPE over its first rope_dims dims.
-// 16 lanes work on one (row, head), lane j holding dims 4j..4j+3. The block's prep kernels and the
-// projection GEMM's epilogue both compute through these functions, so the two paths give the same
-// bits.
+// Element math that a separate kernel and a GEMM epilogue both compute (each through the functions
+// here, so the two paths give the same bits): the per-head preparation of the DiT's attention
+// inputs (src/dit.h:207-217, src/nn.h:40-59: RMS norm over a head's 64 dims with a per-dim gain,
+// then NeoX RoPE over its first rope_dims dims; 16 lanes work on one (row, head), lane j holding
+// dims 4j..4j+3), the attention backward's row dots and the FFN SwiGLU backward.
 #pragma once
 
 #include "sa3k_internal.h"
@@ -73,6 +73,40 @@ __device__ inline float dot4_bf16(const float4& y, uint2 o) {
     s = __builtin_fmaf(y.y, (float)b[1], s);
     s = __builtin_fmaf(y.z, (float)b[2], s);
     return __builtin_fmaf(y.w, (float)b[3], s);
+}
+
+// The FFN SwiGLU backward of four columns (src/dit.h:259-264): g = val * glu * s(glu) with the
+// sigmoid s(z) = 1 / (1 + e^-z) on the library exp, so d val = d * glu * s and d glu = d * val *
+// (s + glu * s * (1 - s)); no contraction. The block's swiglu_bwd kernel and the FFN
+// down-projection's dX epilogue both compute through this function and store_du4.
+__device__ inline void swiglu_bwd4(const float4& val, const float4& glu, const float4& d, float4& dv, float4& dgl) {
+#pragma clang fp contract(off)
+    const float vs[4] = {val.x, val.y, val.z, val.w}, gs[4] = {glu.x, glu.y, glu.z, glu.w};
+    const float ds[4] = {d.x, d.y, d.z, d.w};
+    float a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float sg = 1.0f / (1.0f + expf(-gs[u]));
+        a[u] = ds[u] * gs[u] * sg;
+        b[u] = ds[u] * vs[u] * (sg + gs[u] * sg * (1.0f - sg));
+    }
+    dv = make_float4(a[0], a[1], a[2], a[3]);
+    dgl = make_float4(b[0], b[1], b[2], b[3]);
+}
+// bf16(v (.) scale[c .. c + 3]) (scale null: v) at p: an adapted linear's dU as its producer writes it
+__device__ inline void store_du4(__bf16* p, float4 v, const float* scale, int64_t c) {
+    if (scale) {
+        const float4 s = *reinterpret_cast<const float4*>(scale + c);
+        v = make_float4(v.x * s.x, v.y * s.y, v.z * s.z, v.w * s.w);
+    }
+    const __bf16 b[4] = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    *reinterpret_cast<uint2*>(p) = __builtin_bit_cast(uint2, b);
+}
+// four bf16 values as floats
+__device__ inline float4 bf16x4_to_f4(uint2 u) {
+    typedef __bf16 b4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+    const b4 b = __builtin_bit_cast(b4, u);
+    return make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
 }
 
 // y: this lane's four values of the head as the projection produced them. Normalises them in

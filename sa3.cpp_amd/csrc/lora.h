@@ -42,9 +42,15 @@ void lin_set_tag(sa3k_lin* l, const char* tag);
 // lin_backward_du, which is sa3k_lin_backward on that dU (the f32 dY is never materialised).
 bf16* lin_du(sa3k_lin* L);
 const float* lin_du_scale(const sa3k_lin* L);
-// ad: the dX product's attention dO epilogue (GemmDesc::ad; null: off), *ad_done set where it ran.
+// Backward epilogues of the dX product that write what consumes dX in place of dX (GemmDesc::ad,
+// GemmDesc::sb): *done is set where the chosen kernel ran them (dX is then not written).
+struct DxEpi {
+    AttnDot ad;
+    SwiBwd sb;
+    int* done = nullptr;
+};
 void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, float* dX, int dx_accumulate,
-                     float* dA, float* dB, float* dm, const AttnDot* ad = nullptr, int* ad_done = nullptr);
+                     float* dA, float* dB, float* dm, const DxEpi* epi = nullptr);
 // A stacked product: n bf16 merged adapted linears of one shape and rank that read the same input
 // (the DiT's per-block context K/V projections). Created before the linears are prepared, it moves
 // their W_eff, row scales d, A copies and the saved U / s X A^T into contiguous slabs, so that one

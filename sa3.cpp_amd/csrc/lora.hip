@@ -973,8 +973,7 @@ void lin_forward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t
 // DoRA) into L->dU itself (bf16 precision only)
 template <class CT, int R>
 void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_t N, const float* dY, float* dX,
-                    int dx_acc, float* dA, float* dB, float* dm, const AttnDot* ad = nullptr,
-                    int* ad_done = nullptr) {
+                    int dx_acc, float* dA, float* dB, float* dm, const DxEpi* epi = nullptr) {
     const sa3k_weight* W = L->W;
     const bool bf = L->prec == SA3K_PREC_BF16;
     const int64_t in = W->in, out = W->out;
@@ -998,7 +997,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         g.A = dyc; g.lda = out; g.B = wt.p; g.ldb = wt.ld; g.Bs = wt.s; g.ldbs = wt.lds;
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
-        if (ad) { g.ad = *ad; g.ad_done = ad_done; }
+        if (epi) { g.ad = epi->ad; g.sb = epi->sb; g.bwd_done = epi->done; }
         gemm_run(ctx, g, scope(ctx, L, "lin_bwd_dx"));
         return;
     }
@@ -1200,7 +1199,7 @@ void lin_backward_t(sa3k_ctx* ctx, sa3k_lin* L, int x_src, const void* X, int64_
         }
         g.M = N; g.N = in; g.K = out; g.alpha = 1.0f;
         g.C = dX; g.ldc = in; g.accumulate = dx_acc;
-        if (ad) { g.ad = *ad; g.ad_done = ad_done; }
+        if (epi) { g.ad = epi->ad; g.sb = epi->sb; g.bwd_done = epi->done; }
         if (L->dora) {
             g.Mx = r; g.Ax = L->Ax; g.ldax = out;
             if (!merged) { g.A2x = L->A2x; g.lda2x = r; }
@@ -1767,7 +1766,7 @@ bf16* lin_du(sa3k_lin* L) { return static_cast<bf16*>(L->dU); }
 const float* lin_du_scale(const sa3k_lin* L) { return L->rank > 0 && L->dora ? L->d : nullptr; }
 
 void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int64_t N, float* dX, int dx_accumulate,
-                     float* dA, float* dB, float* dm, const AttnDot* ad, int* ad_done) {
+                     float* dA, float* dB, float* dm, const DxEpi* epi) {
     SA3K_REQUIRE(L && X, "null pointer");
     SA3K_REQUIRE(L->prec == SA3K_PREC_BF16, "a precomputed dU needs a bf16-precision linear");
     SA3K_REQUIRE(N == L->saved_tokens, "backward must follow a forward over the same tokens");
@@ -1775,8 +1774,8 @@ void lin_backward_du(sa3k_ctx* ctx, sa3k_lin* L, int x_type, const void* X, int6
     SA3K_REQUIRE(!L->dora || dm, "dora needs a magnitude gradient buffer");
     SA3K_REQUIRE(x_type == SA3K_TYPE_F32 || x_type == SA3K_TYPE_BF16, "activation type must be f32 or bf16");
     const int xs = x_type == SA3K_TYPE_F32 ? SRC_F32 : SRC_BF16;
-    if (L->rank <= 16) lin_backward_t<bf16, 16>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm, ad, ad_done);
-    else lin_backward_t<bf16, 32>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm, ad, ad_done);
+    if (L->rank <= 16) lin_backward_t<bf16, 16>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm, epi);
+    else lin_backward_t<bf16, 32>(ctx, L, xs, X, N, nullptr, dX, dx_accumulate, dA, dB, dm, epi);
 }
 
 void weight_fwd_operand(const sa3k_weight* W, GemmDesc& g) {

@@ -106,14 +106,16 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
     """The GEMM-epilogue fusions (option epi_fuse) against their separate kernels at the benchmark's
     width: the FFN SwiGLU from the up-projection's epilogue (bit 0), the per-head q/k RMS norm,
     RoPE and head-major bf16 outputs from the QKV and cross-query projections' epilogues (bit 1),
-    and the attention backward's head-major bf16 dO and row dots from the two out-projections' dX
-    epilogues (bit 2). 2 x 1024 tokens take the 128 x 256 DMA tiles without a split over K for the
+    the attention backward's head-major bf16 dO and row dots from the two out-projections' dX
+    epilogues (bit 2) and the SwiGLU backward (the up-projection's dU) from the down-projection's dX
+    epilogue (bit 3). 2 x 1024 tokens take the 128 x 256 DMA tiles without a split over K for the
     forward products, 2 x 1088 (the benchmark's 2176 tokens) the 256 x 256 tiles for the
-    up-projection; the dX products take the small-grid 128 x 128 tiles. Each fused path evaluates the
-    same expressions per element, so every output and gradient agrees bit for bit; the profile
-    shows which separate kernels ran (SwiGLU: forward + backward unfused, backward only fused; head
-    prep: self + cross query + context K/V unfused, context K/V only fused; attention dots: self +
-    cross unfused, none fused)."""
+    up-projection; the out-projections' dX products take the small-grid 128 x 128 tiles, the
+    down-projection's the 256 x 256 ones. Each fused path evaluates the same expressions per
+    element, so every output and gradient agrees bit for bit; the profile shows which separate
+    kernels ran (SwiGLU: one forward and one backward launch, each unless fused; head prep: self +
+    cross query + context K/V unfused, context K/V only fused; attention dots: self + cross unfused,
+    none fused)."""
     assert_shipped_options(ctx)
     B, Ctx = 2, 128
     print(f"epilogue fusions: B {B}, S {S}, Ctx {Ctx}", flush=True)
@@ -123,7 +125,7 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
     gb = GpuBlock(ctx, cfg, w, sa3k.TYPE_F16, B * S, B * Ctx)
     res, launches = {}, {}
     try:
-        for fuse in (7, 0, 1, 2, 3, 4):
+        for fuse in (15, 0, 1, 2, 3, 4, 8):
             ctx.set_option("epi_fuse", fuse)
             ctx.profile(True)
             ctx.profile_reset()
@@ -136,21 +138,22 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
         ctx.profile(False)
         ctx.set_options(ctx.defaults)
         gb.destroy()
-    assert launches == {7: (1, 1, 0), 0: (2, 3, 2), 1: (1, 3, 2), 2: (2, 1, 2), 3: (1, 1, 2), 4: (2, 3, 0)}, launches
-    for fuse in (0, 1, 2, 3, 4):
+    want = {f: ((0 if f & 1 else 1) + (0 if f & 8 else 1), 1 if f & 2 else 3, 0 if f & 4 else 2) for f in launches}
+    assert launches == want, launches
+    for fuse in (0, 1, 2, 3, 4, 8):
         for k in ("out", "dx", "dctx", "dgcond"):
-            assert np.array_equal(res[7][k], res[fuse][k]), (fuse, k)
+            assert np.array_equal(res[15][k], res[fuse][k]), (fuse, k)
         for k in ("dA", "dB", "dm"):
             for t in range(7):
-                assert np.array_equal(res[7][k][t], res[fuse][k][t]), (fuse, f"{k}[{t}]")
+                assert np.array_equal(res[15][k][t], res[fuse][k][t]), (fuse, f"{k}[{t}]")
 
 
 @pytest.mark.parametrize("act_bf16", [1, 3])
 def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
     """The fused epilogues against the oracle directly: the full-width block at 2 x 136 tokens with
     the split over K and the small-grid tile switched off, so that the up-projection, QKV and
-    cross-query products and the out-projections' dX products take unsplit 128 x 256 tiles and the
-    fusions apply (shipped, these small
+    cross-query products and the out- and down-projections' dX products take unsplit 128 x 256 tiles
+    and the fusions apply (shipped, these small
     grids take split or 64 x 128 tiles and the separate kernels, which the other full-width tests
     cover); the backward reading the bf16 copy of the FFN up-projection's output (act_bf16 1, the
     default) and also those of the QKV and cross-query outputs (3)."""
@@ -175,7 +178,7 @@ def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
         gb.destroy()
     n = tuple(sum(v[0] for k, v in rep.items() if k.startswith(p))
               for p in ("blk_swiglu", "blk_prep_fwd", "attn_bwd_dot"))
-    assert n == (1, 1, 0), n   # SwiGLU backward and the context K/V prep only; no attention dot kernel
+    assert n == (0, 1, 0), n   # the context K/V prep only: no SwiGLU or attention dot kernel
     ref_out = bb.block_fwd(cfg, w, x, cx, gc)
     ref = bb.block_bwd(cfg, w, x, cx, gc, dout)
     worst = []
