@@ -170,7 +170,9 @@ SA3K_API int sa3k_vec_add(sa3k_ctx* ctx, float* dst_dev, const float* src_dev, i
  *                 bit 3: the SwiGLU backward (the up-projection's bf16 dU) comes out of the FFN
  *                 down-projection's dX epilogue, with act_bf16 bit 0 (the f32 dG is then not
  *                 written); each where the chosen tiles allow it (no split over K), else by its
- *                 own kernel (default 15)
+ *                 own kernel (default 3: measured on MI355X, the DiT update with bits 2 / 2 and 3
+ *                 takes 32.20 / 32.34 ms against 32.14 ms, the epilogue's extra loads stalling a
+ *                 tile's whole workgroup where the separate kernels stream at full occupancy)
  *   "gemm_prio"   1: the DMA GEMMs raise their waves' priority over the MFMA clusters of the K
  *                 loop, so a wave that has its operands keeps issuing while the others read
  *                 (default 1)

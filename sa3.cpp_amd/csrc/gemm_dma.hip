@@ -459,7 +459,7 @@ __device__ inline void swiglu_bwd_store(const DmaParams& p, int64_t m, int64_t n
 // floats per row): thread tid stores chunk column cq (output column nq, column factors kq) of tile
 // rows tid / CPR + i NT / CPR. With 256-column tiles a wave holds one row, which the paired SwiGLU
 // and the head preparation rely on.
-template <int BN, int NT, int ER, int EROW, bool HP>
+template <int BN, int NT, int ER, int EROW, bool HP, bool XE = false>
 __device__ inline void staged_store(const DmaParams& p, const float* st, int64_t m0, int64_t n0, int rb, int64_t Mt,
                                     int z, int tid, int cq, int64_t nq, const EpiCols& kq, bool sw_tile, bool hp_tile,
                                     const HeadPrepLane& hl, const float* tabs) {
@@ -505,14 +505,19 @@ __device__ inline void staged_store(const DmaParams& p, const float* st, int64_t
         if (BN == 256 && sw_tile && main_row) swiglu_pair_store(p, gp + (int64_t)dr * p.sw_ldg, lo, v);
         if constexpr (HP)
             if (hp_tile && main_row) head_prep_store(p, hl, (int)m, hb, ht, nq, v, tabs + (rb + r) * p.hp.rope_dims, outp, rsp);
-        if (p.ad.doh && main_row && main_col) attn_dot_store(p, m, nq, v);
-        if (p.sb.du && main_row && main_col) swiglu_bwd_store(p, m, nq, v);
+        if constexpr (XE) {   // the backward epilogues: their own instantiations (register use)
+            if (p.ad.doh && main_row && main_col) attn_dot_store(p, m, nq, v);
+            if (p.sb.du && main_row && main_col) swiglu_bwd_store(p, m, nq, v);
+        }
     }
 }
 
 // HP: the per-head q/k preparation instantiation (128 x 256 bf16 tiles): the staged epilogue takes
 // the tile in two passes of 64 rows and keeps the tile rows' RoPE table rows in LDS past them.
-template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false>
+// XE: the instantiation that also runs the backward epilogues (DmaParams::ad / sb); the others do
+// not carry their code, which costs registers.
+template <int BM, int BN, int WMW, int STAGES, bool BF16, int NW = 4, bool KN = false, int BQ = 0, bool HP = false,
+          bool XE = false>
 __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
     constexpr int NT = NW * 64;
     constexpr int WNW = NW / WMW;
@@ -974,7 +979,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_dma_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        staged_store<BN, NT, ER, EROW, HP>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, hp_tile, hl, tabs);
+        staged_store<BN, NT, ER, EROW, HP, XE>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, hp_tile, hl, tabs);
         if (rb + ER < BM) __syncthreads();
     }
 }
@@ -995,7 +1000,7 @@ struct BigSeg {
     uint32_t off[4];
 };
 
-template <bool KN, int NW = 8>
+template <bool KN, int NW = 8, bool XE = false>   // XE: as for gemm_dma_kernel
 __global__ __launch_bounds__(NW * 64) void gemm_big_kernel(DmaParams p) {
     constexpr int BM = 256, BN = 256, NT = NW * 64, WMW = 4;
     constexpr int WTM = BM / WMW, WTN = BN / (NW / WMW);   // 64 x 128 (8 waves), 64 x 64 (16)
@@ -1226,7 +1231,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_big_kernel(DmaParams p) {
             }
         }
         __syncthreads();
-        staged_store<BN, NT, ER, EROW, false>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, false,
+        staged_store<BN, NT, ER, EROW, false, XE>(p, st, m0, n0, rb, Mt, z, tid, cq, nq, kq, sw_tile, false,
                                               HeadPrepLane{}, nullptr);
         if (rb + ER < BM) __syncthreads();
     }
@@ -1427,6 +1432,12 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                     ok(p.colscale, 4, 16) && ok(p.bias, 4, 16) && ok(p.Cbn, p.ldcn, 8);
     }
     settle_swiglu(p, BN, splits, KN, BQ);
+    // the backward epilogues: only on the bf16 [K][N] instantiations (the merged dX products)
+    constexpr bool kXE = BF16 && KN && BQ == 0 && !HP;
+    if (!kXE) {
+        p.ad.doh = nullptr;
+        p.sb.du = nullptr;
+    }
     settle_bwd_epilogues(p, splits, BN);
     if constexpr (HP) {
         if (!headprep_ok(p, splits)) {   // the caller prepares the heads: the plain instantiation
@@ -1449,8 +1460,10 @@ void launch_dma(sa3k_ctx* ctx, DmaParams p) {
                                         (BQ == 1 ? ",f16b" : BQ == 2 ? ",q8b" : "") + (HP ? ",hp" : "") +
                                         (BF16 ? ",bf16>" : ",f32>");
         KernelScope ks(ctx, name.c_str(), 2.0 * (double)(p.M + p.Mx) * (double)p.Nt * (double)(p.K + p.K2));
-        launch_k(ctx, !(splits > 1 && !p.counters), gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ, HP>, g,
-                 dim3(NW * 64), 0, p);
+        auto kern = gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ, HP>;
+        if constexpr (kXE)
+            if (p.ad.doh || p.sb.du) kern = gemm_dma_kernel<BM, BN, WMW, STAGES, BF16, NW, KN, BQ, HP, true>;
+        launch_k(ctx, !(splits > 1 && !p.counters), kern, g, dim3(NW * 64), 0, p);
         SA3K_LAUNCHED();
     }
     if (splits > 1 && !p.counters) {
@@ -1513,7 +1526,12 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
     p.nt_store = ctx->gemm_nt_store;
     p.vec_epi = 1;
     settle_swiglu(p, BN, splits, p.b_kn != 0, 0);
+    if (!p.b_kn) {   // the backward epilogues: [K][N] instantiations only, as in launch_dma
+        p.ad.doh = nullptr;
+        p.sb.du = nullptr;
+    }
     settle_bwd_epilogues(p, splits, BN);
+    const bool xe = p.ad.doh || p.sb.du;
     if (splits > 1) p.ws = gemm_workspace_bytes(ctx, (size_t)splits * (size_t)(p.M + p.Mx) * (size_t)p.Nt * sizeof(float));
     {
         KernelScope ks(ctx, p.b_kn ? "gemm_big<256,256,kn,bf16>" : "gemm_big<256,256,bf16>",
@@ -1522,10 +1540,12 @@ void launch_big(sa3k_ctx* ctx, DmaParams p) {
         // 32.90 against 33.08 ms on one box)
         const dim3 g((unsigned)grid, (unsigned)splits);
         if (ctx->gemm_cfg == 4) {
-            if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true, 8>, g, dim3(512), 0, p);
+            if (p.b_kn) launch_k(ctx, splits == 1, xe ? gemm_big_kernel<true, 8, true> : gemm_big_kernel<true, 8>, g,
+                                 dim3(512), 0, p);
             else launch_k(ctx, splits == 1, gemm_big_kernel<false, 8>, g, dim3(512), 0, p);
         } else {
-            if (p.b_kn) launch_k(ctx, splits == 1, gemm_big_kernel<true, 16>, g, dim3(1024), 0, p);
+            if (p.b_kn) launch_k(ctx, splits == 1, xe ? gemm_big_kernel<true, 16, true> : gemm_big_kernel<true, 16>, g,
+                                 dim3(1024), 0, p);
             else launch_k(ctx, splits == 1, gemm_big_kernel<false, 16>, g, dim3(1024), 0, p);
         }
         SA3K_LAUNCHED();

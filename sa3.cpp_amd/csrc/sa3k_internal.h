@@ -106,7 +106,7 @@ struct sa3k_ctx {
     int prep_side = 1;                    // a DiT's bf16 group refresh on the second stream beside the f32 heads'
     int head_f32 = 1;                     // a DiT's head / tail linears on f32 MFMA (f32 / f16 bases)
     int head_quick = 1;                   // a DiT's head chains partly on the third stream
-    int epi_fuse = 15;                    // in GEMM epilogues where the tiles allow: 1 the FFN SwiGLU, 2 q/k head prep,
+    int epi_fuse = 3;                     // in GEMM epilogues where the tiles allow: 1 the FFN SwiGLU, 2 q/k head prep,
                                           // 4 the attention backward's dOh and row dots, 8 the SwiGLU backward
     int act_bf16 = 1;                     // block backward reads bf16 copies: 1 of the FFN up output, 2 of qkv / qf
     int* skinny_counters = nullptr;       // [2][kSkinnyMaxTiles] the skinny product's split arrivals,

@@ -151,12 +151,12 @@ def test_block_epilogue_fusions_bitwise(ctx, S):
 @pytest.mark.parametrize("act_bf16", [1, 3])
 def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
     """The fused epilogues against the oracle directly: the full-width block at 2 x 136 tokens with
-    the split over K and the small-grid tile switched off, so that the up-projection, QKV and
-    cross-query products and the out- and down-projections' dX products take unsplit 128 x 256 tiles
-    and the fusions apply (shipped, these small
-    grids take split or 64 x 128 tiles and the separate kernels, which the other full-width tests
-    cover); the backward reading the bf16 copy of the FFN up-projection's output (act_bf16 1, the
-    default) and also those of the QKV and cross-query outputs (3)."""
+    every epilogue fusion on (epi_fuse 15) and the split over K and the small-grid tile switched
+    off, so that the up-projection, QKV and cross-query products and the out- and down-projections'
+    dX products take unsplit 128 x 256 tiles and the fusions apply (shipped, these small grids take
+    split or 64 x 128 tiles and the separate kernels, which the other full-width tests cover); the
+    backward reading the bf16 copy of the FFN up-projection's output (act_bf16 1, the default) and
+    also those of the QKV and cross-query outputs (3)."""
     B, S, Ctx = 2, 64 + 72, 128
     cfg, w, x, cx, gc = bb.random_block(71, B=B, S=S, Ctx=Ctx, dim=1536, heads=24, inner=6144, rank=32,
                                         alpha=32.0, dora=True, window=256, w_sd=0.02, b_sd=0.01)
@@ -168,6 +168,7 @@ def test_block_fused_epilogues_vs_oracle(ctx, act_bf16):
         ctx.set_option("gemm_split", 0)
         ctx.set_option("gemm_small", 0)
         ctx.set_option("act_bf16", act_bf16)
+        ctx.set_option("epi_fuse", 15)   # every epilogue fusion, the backward ones included
         ctx.profile(True)
         ctx.profile_reset()
         got = run_gpu(ctx, gb, x, cx, gc, dout)
