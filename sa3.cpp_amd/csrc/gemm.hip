@@ -456,8 +456,18 @@ __global__ __launch_bounds__(kThreads) void gemm_splitk_reduce(KParams p, int sp
     const int64_t Mt = p.M + p.Mx;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= Mt * p.N) return;
+    // eight splits' partials loaded per memory round trip (indices past the last split re-read it
+    // and are not added); the sums are added in split order from zero
+    const int64_t plane = Mt * p.N;
     float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += p.ws[(int64_t)z * Mt * p.N + idx];
+    for (int z = 0; z < splits; z += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = p.ws[(int64_t)min(z + k, splits - 1) * plane + idx];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (z + k < splits) s += v[k];
+    }
     const int64_t m = idx / p.N, n = idx - m * p.N;
     epilogue_elem(p, m, n, s);
 }
