@@ -713,12 +713,22 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_sum(BwdArgs a, int64_t
     float4 s[3];
 #pragma unroll
     for (int o = 0; o < 3; ++o) s[o] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int z = 0; z < a.qsplit; ++z)
+    // four splits' partials loaded per memory round trip (indices past the last split re-read it and
+    // are not added); the sums are added in split order from zero
+    for (int z = 0; z < a.qsplit; z += 4) {
+        float4 v[4][3];
 #pragma unroll
-        for (int o = 0; o < 3; ++o) {
-            const float4 v = *reinterpret_cast<const float4*>(a.part + ((int64_t)z * 3 + o) * plane + i);
-            s[o] = make_float4(s[o].x + v.x, s[o].y + v.y, s[o].z + v.z, s[o].w + v.w);
-        }
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int o = 0; o < 3; ++o)
+                v[k][o] = *reinterpret_cast<const float4*>(a.part + ((int64_t)min(z + k, a.qsplit - 1) * 3 + o) * plane + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (z + k < a.qsplit)
+#pragma unroll
+                for (int o = 0; o < 3; ++o)
+                    s[o] = make_float4(s[o].x + v[k][o].x, s[o].y + v[k][o].y, s[o].z + v[k][o].z, s[o].w + v[k][o].w);
+    }
     *reinterpret_cast<float4*>(a.dv + i) = s[0];
     *reinterpret_cast<float4*>(a.dk1 + i) = make_float4(a.scale * s[1].x, a.scale * s[1].y, a.scale * s[1].z, a.scale * s[1].w);
     *reinterpret_cast<float4*>(a.dk2 + i) = make_float4(a.scale * s[2].x, a.scale * s[2].y, a.scale * s[2].z, a.scale * s[2].w);
